@@ -1,0 +1,197 @@
+"""Talker decode benchmark on one MI355X: frames/s of the 0.6B-shaped int8 talker at batch 1, KV 512.
+
+    python bench.py [--steps K] [--warmup W] [--workload talker06b|talker17b] [--no-cpu]
+
+A step is one greedy decode run of 64 frames starting at KV length 512 (positions 512..575 are rewritten on
+every step, so every step does identical work): each frame is one replay of the captured HIP graph
+(embed -> 28 x [rms_gemv qkv, attention, gemv o, rms_gemv gate/up, gemv down] -> rmsnorm -> codec head ->
+argmax). Weights are seeded random-init of the real architecture, int8 per output channel with bf16 scales
+(``i8row``); the KV cache is bf16. Inputs are resident in HBM before timing starts.
+
+Prints one JSON line with the metric, the roofline of the dominant kernel (algorithmic bytes per launch over
+its average duration, timed with HIP events on the launch stream) and the CPU oracle timed on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0
+
+
+def algorithmic_bytes(s, T: int, wd: str = "i8row") -> dict:
+    """HBM bytes one frame must move at attended length T (all layers), by kernel kind.
+    int8 weights 1 B each + bf16 scale per row; K+V read 2 x nkv x T x 128 x 2 B; K+V append; head; embedding row."""
+    wb = {"i8row": 1, "i8g32": 1, "bf16": 2, "f32": 4}[wd]
+
+    def mat(N, K):
+        b = N * K * wb
+        if wd == "i8row":
+            b += 2 * N
+        elif wd == "i8g32":
+            b += 2 * N * K // 32
+        return b
+
+    H, I, nq, nkv, hd = s.hidden, s.inter, s.nq, s.nkv, s.head_dim
+    per = {"qkv": mat((nq + 2 * nkv) * hd, H), "o": mat(H, nq * hd), "gu": mat(2 * I, H), "down": mat(H, I),
+           "attn": 2 * nkv * T * hd * 2 + 2 * nkv * hd * 2}
+    frame = s.n_layers * sum(per.values()) + mat(s.vocab, H) + 2 * H
+    return {"per_layer": per, "frame": frame, "head": mat(s.vocab, H)}
+
+
+def time_kernels(eng, reps: int = 200) -> dict:
+    """Average duration of each launch kind of one layer, timed with HIP events on the launch stream."""
+    import torch
+
+    P = eng.T
+    L = P.layers[0]
+    calls = {
+        "qkv": lambda: eng._rms_gemv(eng.ht, L["in_norm"], P.eps, L["qkv"], eng.qkv_t, False),
+        "attn": lambda: eng._attn(P, L, eng.qkv_t, eng.tk[0], eng.tv[0], eng.pos, -1, eng.att_t),
+        "o": lambda: eng._gemv(eng.att_t, L["o"], None, eng.act_t[: P.H], False),
+        "gu": lambda: eng._rms_gemv(eng.ht, L["post_norm"], P.eps, L["gu"], eng.act_t, True),
+        "down": lambda: eng._gemv(eng.act_t, L["down"], None, eng.ph32, False),
+    }
+    out = {}
+    for name, fn in calls.items():
+        for _ in range(10):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) * 1e3 / reps  # us
+    return out
+
+
+def cpu_baseline(name: str, seed: int, budget_s: float = 15.0) -> dict:
+    """The numpy oracle on this host's cores: frames of the same workload until ~budget_s of frame time."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+
+    from oracle.workload import talker_oracle
+    from sokutou_amd import synthetic as syn
+
+    spec = syn.WORKLOADS[name]
+    orc, tok, s = talker_oracle(name, seed, "i8row")
+    pos = spec["kv"]
+    token = tok
+    for f in range(2):  # warm-up frames
+        token, _ = orc.step(token, pos + f)
+    times = []
+    t_start = time.perf_counter()
+    f = 2
+    while f < spec["frames"] and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        token, _ = orc.step(token, pos + f)
+        times.append(time.perf_counter() - t0)
+        f += 1
+    med = float(np.median(times))
+    threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    return {"value": round(1.0 / med, 3), "unit": "frames/s", "cores": int(threads), "kind": "port",
+            "sample": f"{len(times)} frames (positions {pos + 2}..{pos + 1 + len(times)}) of the same workload after 2 "
+                      f"warm-up frames, median frame time {med * 1e3:.1f} ms; numpy fp32 over dequantised int8 weights",
+            "host_cpus": os.cpu_count()}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="talker06b", choices=["talker06b", "talker17b"])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the talker decode step at batch 1 runs on a single MI355X "
+              "(how it would shard is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from sokutou_amd import synthetic as syn
+
+    dev = torch.device("cuda:0")
+    name = args.workload
+    spec = syn.WORKLOADS[name]
+    frames = spec["frames"]
+    t0 = time.perf_counter()
+    eng, tok = syn.make_engine(name, seed=args.seed, wd="i8row", device=dev)
+    eng.capture()
+    setup_s = time.perf_counter() - t0
+    s = syn.workload_shape(name)
+    pos0 = spec["kv"]
+
+    def step():
+        eng.reset(pos0, tok)
+        for _ in range(frames):
+            eng.graph.replay()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt * 1e3 / args.steps
+    fps = frames * args.steps / dt
+
+    # correctness of the measured path: one more step, codes against the oracle fixture when present
+    eng.reset(pos0, tok)
+    codes = []
+    for _ in range(frames):
+        eng.graph.replay()
+        codes.append(int(eng.next_id0.item()))
+    gold = ROOT / "tests" / "golden" / f"{name}_seed{args.seed}.json"
+    parity = None
+    if gold.exists():
+        parity = codes == json.loads(gold.read_text())["codes"]
+
+    # bytes per frame summed over the attended lengths of the 64 frames
+    ab = [algorithmic_bytes(s, pos0 + 1 + f) for f in range(frames)]
+    frame_bytes = sum(a["frame"] for a in ab) / frames
+    frame_gbs = frame_bytes * fps / 1e9
+    kt = time_kernels(eng)
+    per = ab[0]["per_layer"]
+    per_frame_us = {k: kt[k] * s.n_layers for k in kt}
+    dom = max(per_frame_us, key=per_frame_us.get)
+    achieved = per[dom] / (kt[dom] * 1e-6) / 1e9
+    res = {
+        "metric": "talker decode frames/sec (0.6B int8, bs1, KV 512); achieved HBM GB/s vs peak" if name == "talker06b"
+        else "talker decode frames/sec (1.7B int8, bs1, KV 1024)",
+        "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 weights x fp32 accumulate (bf16 KV cache)", "data": "synthetic",
+        "config": {"workload": f"{name}: {s.n_layers} layers, hidden {s.hidden}, {s.nq}q/{s.nkv}kv heads x 128, "
+                               f"intermediate {s.inter}, codec vocab {s.vocab}, i8row weights, batch 1, KV {pos0}, "
+                               f"{frames} greedy frames per step", "batch": 1, "kv_start": pos0, "frames_per_step": frames,
+                   "weights": "i8row", "engine": "Qwen3Kernels, one HIP graph per frame"},
+        "roofline": {"bound": "hbm", "kernel": f"{dom} (sk_{'rms_gemv' if dom in ('qkv', 'gu') else 'attn' if dom == 'attn' else 'gemv'})",
+                     "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_launch": per[dom], "avg_launch_us": round(kt[dom], 3)},
+        "frame": {"us_per_frame": round(1e6 / fps, 2), "us_per_layer": round(1e6 / fps / s.n_layers, 3),
+                  "algorithmic_bytes_per_frame": int(frame_bytes), "effective_GBs": round(frame_gbs, 1),
+                  "frac_of_peak": round(frame_gbs / PEAK_HBM_GBS, 4), "kernel_us_per_frame": {k: round(v, 1) for k, v in per_frame_us.items()}},
+        "parity_codes_match_oracle": parity, "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(name, args.seed)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,106 @@
+/* sokutou_amd: C-ABI of the MI355X (gfx950) Qwen3-TTS talker decode step.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t passed as `void*` (torch's
+ * `torch.cuda.current_stream().cuda_stream`), enqueues its kernels on that stream and returns immediately:
+ * no host synchronisation, no host reads of device memory and no allocation, so every call can be captured in
+ * a HIP graph. The caller owns every buffer. Return value: SK_OK (0) or a negative SK_E* code; the message of
+ * the last failure on the calling thread is `sk_last_error()`.
+ *
+ * Each function names the reference kernel it replaces (paths relative to the Soyomi66/sokutou repository).
+ * In the reference those are `extern "C" __global__` CUDA kernels launched through CuPy with a grid, a block
+ * and a tuple of raw pointers (`Qwen3Kernels._launch`, qwen3/kernels.py:575-577); here the launch shape is
+ * chosen inside the library and the call takes only the kernel's own arguments.
+ */
+#ifndef SOKUTOU_AMD_H
+#define SOKUTOU_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------------------------------------- */
+#define SK_OK 0
+#define SK_EINVAL (-1)       /* bad shape, format or null pointer (the reference's asserts)                */
+#define SK_ELAUNCH (-2)      /* the HIP launch failed                                                       */
+#define SK_EUNSUPPORTED (-3) /* a feature this build does not provide                                       */
+#define SK_EWORKSPACE (-4)   /* workspace too small                                                          */
+#define SK_EDEVICE (-5)      /* not a gfx950 device                                                          */
+
+/* ---- weight formats (`wd` of _Lin, qwen3/kernels.py:434-444, plus per-channel int8) -------------------- */
+#define SK_WD_I8ROW 0 /* int8 [N,K] + bf16 scale per output row                                          */
+#define SK_WD_I8G32 1 /* int8 [N,K] + fp16 scale per 32 consecutive K elements ([N, K/32])               */
+#define SK_WD_BF16 2  /* bf16 [N,K]                                                                       */
+#define SK_WD_F32 3   /* fp32 [N,K]                                                                       */
+
+/* ---- cache / embedding element types (the reference's ct_t: bf16, or f32 under ACT_F32) --------------- */
+#define SK_CT_BF16 0
+#define SK_CT_F32 1
+
+#define SK_MAX_K 8192 /* largest GEMV input length (1.7B down projection is 6144)                         */
+#define SK_MAX_V 4096 /* largest sampler vocabulary (qwen3/sampler.py:162)                               */
+
+/* Library and device checks. sk_device_check returns SK_OK when the current HIP device is gfx950 (the
+ * reference's sm_80 gate, qwen3/kernels.py:492-493). */
+const char* sk_version(void);
+const char* sk_last_error(void);
+int sk_device_check(void);
+
+/* out = W · (h ⊙ nw) · rsqrt(mean(h²) + eps). With swiglu != 0 the rows of W are interleaved gate/up and
+ * out[n] = silu(row 2n) · row 2n+1 (N/2 outputs). K % 512 == 0, K <= SK_MAX_K.
+ * policy 1 streams the weights with nontemporal loads (read once per frame), 0 uses ordinary loads.
+ * Replaces rms_gemv(h, nw, eps, W, S, out, N, K, swiglu, split, policy) (qwen3/kernels.py:271-275). */
+int sk_rms_gemv(const float* h, const float* nw, float eps, const void* W, const uint16_t* S, float* out, int N, int K,
+                int swiglu, int wd, int policy, void* stream);
+
+/* out = W · x (+ bias) (+ out when accumulate != 0). bias may be NULL.
+ * Replaces gemv(x, W, S, bias, out, N, K, accumulate, split, policy) (qwen3/kernels.py:301-305). */
+int sk_gemv(const float* x, const void* W, const uint16_t* S, const float* bias, float* out, int N, int K,
+            int accumulate, int wd, int policy, void* stream);
+
+/* out = h · rsqrt(mean(h²) + eps) · nw over K elements.
+ * Replaces rmsnorm(h, nw, eps, out, K) (qwen3/kernels.py:313-319). */
+int sk_rmsnorm(const float* h, const float* nw, float eps, float* out, int K, void* stream);
+
+/* out[i] = float(table[idx[0] * dim + i]); idx is a device int64.
+ * Replaces embed(table, idx, out, dim) (qwen3/kernels.py:322-326). */
+int sk_embed(const void* table, const int64_t* idx, float* out, int dim, int ct, void* stream);
+
+/* out[i] = Σ_g tabs[g][codes[g] * dim + i] + pad[i]; tabs is a device array of G table addresses.
+ * Replaces talker_in(tabs, codes, pad, out, dim, G) (qwen3/kernels.py:329-336). */
+int sk_talker_in(const uint64_t* tabs, const int64_t* codes, const void* pad, float* out, int dim, int G, int ct,
+                 void* stream);
+
+/* Bytes of scratch that sk_attn needs for nkv kv heads and caches of max_len positions (split-K partials and
+ * per-head arrival counters). The counters must be zero before the first call; sk_attn leaves them zero. */
+int64_t sk_attn_workspace_size(int nq, int nkv, int max_len);
+
+/* One-token GQA decode attention. qkv is [nq·128 | nkv·128 | nkv·128] fp32; for each kv head: per-head RMSNorm
+ * of k (weight kn) and q (weight qn), rotate-half RoPE from rope[pos] = [cos 64 | sin 64], K and V stored at
+ * position pos of Kc/Vc ([nkv][max_len][128], element type ct), q scaled by 1/sqrt(128), softmax over positions
+ * 0..pos, out = [nq·128] fp32. pos = (pos_ptr ? *pos_ptr : 0) + pos_add, read on the device. nq == 2·nkv.
+ * The cache length is split across blocks and merged with a log-sum-exp (online softmax) combine.
+ * Replaces attn(qkv, qn, kn, eps, rope, Kc, Vc, pos_ptr, pos_add, max_len, nq, nkv, out)
+ * (qwen3/kernels.py:341-414). */
+int sk_attn(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc, void* Vc,
+            const int64_t* pos_ptr, int pos_add, int max_len, int nq, int nkv, float* out, void* workspace,
+            int64_t workspace_bytes, int ct, void* stream);
+
+/* One sampling step over V <= SK_MAX_V fp32 logits, writing the chosen id to out[0] (int64).
+ * talker != 0 applies the talker processor first (repetition penalty on seen, suppressed ids, EOS blocked while
+ * ngen < min_new) and then updates the device state: id0 = id, seen[id] = 1, ngen += 1, pos += 1.
+ * do_sample == 0 is greedy argmax with the lowest index winning ties. seen / suppress are bool (1 byte) arrays,
+ * NULL when unused; seed / counter are device uint64 (used only when sampling).
+ * Replaces sample(logits, V, inv_temp, top_k, do_sample, seen, rep_pen, suppress, ngen, min_new, eos, seed,
+ * counter, out, talker, id0, pos) (qwen3/sampler.py:37-159). This build implements the greedy path
+ * (do_sample == 0); do_sample != 0 returns SK_EUNSUPPORTED. */
+int sk_sample(const float* logits, int V, float inv_temp, int top_k, int do_sample, uint8_t* seen, float rep_pen,
+              const uint8_t* suppress, int64_t* ngen, int min_new, int eos, const uint64_t* seed, uint64_t* counter,
+              int64_t* out, int talker, int64_t* id0, int64_t* pos, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOKUTOU_AMD_H */

@@ -1,0 +1,61 @@
+"""Builds the oracle for a named synthetic workload (TEST INFRASTRUCTURE ONLY, see oracle/__init__.py).
+
+The weights, prior cache and start token come from ``sokutou_amd.synthetic`` (the shared seeded input
+generator); quantisation, packing and all arithmetic are the oracle's own (oracle/talker.py), so the GPU path
+and the oracle meet only at the raw fp32 inputs.
+"""
+
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+
+from sokutou_amd import synthetic as syn
+
+from . import talker as O
+
+
+def pack_layer(w: dict, wd: str) -> dict:
+    """q/k/v rows concatenated, gate/up rows interleaved (row 2n gate n, 2n+1 up n) as the reference's _Stack
+    does (qwen3/kernels.py:462-469), each quantised with the oracle's quantiser and dequantised to fp32."""
+    gu = np.stack([w["gate"], w["up"]], axis=1).reshape(-1, w["gate"].shape[1])
+    return {"qkv": O.quantize(np.concatenate([w["q"], w["k"], w["v"]]), wd)[2], "o": O.quantize(w["o"], wd)[2],
+            "gu": O.quantize(gu, wd)[2], "down": O.quantize(w["down"], wd)[2], "in_norm": w["in_norm"],
+            "post_norm": w["post_norm"], "qn": w["q_norm"], "kn": w["k_norm"]}
+
+
+def talker_oracle(name: str, seed: int = 0, wd: str = "i8row", max_len: int | None = None,
+                  cache_bf16: bool = True, digests: dict | None = None):
+    """Returns (TalkerOracle, start token, shape) for ``name`` with the prior cache loaded.
+    When ``digests`` is a dict it receives SHA-256 digests of the generated inputs."""
+    spec = syn.WORKLOADS[name]
+    s = syn.workload_shape(name)
+    T = spec["kv"]
+    max_len = max_len or (T + spec.get("frames", 1) + 1)
+    layers = []
+    K = np.zeros((s.n_layers, s.nkv, max_len, 128), np.float32)
+    V = np.zeros_like(K)
+    all_h = hashlib.sha256()
+    for i in range(s.n_layers):
+        w = syn.layer_weights(seed, i, s)
+        for k in sorted(w):
+            d = syn.sha256(w[k])
+            all_h.update(d.encode())
+            if digests is not None and i == 0:
+                digests[f"layer0.{k}"] = d
+        layers.append(pack_layer(w, wd))
+        k, v = syn.kv_prefill(seed, i, s, T)
+        K[i, :, :T] = k
+        V[i, :, :T] = v
+        if digests is not None and i == 0:
+            digests["layer0.kcache"] = syn.sha256(k)
+            digests["layer0.vcache"] = syn.sha256(v)
+    f = syn.final_weights(seed, s)
+    if digests is not None:
+        digests["all_layers"] = all_h.hexdigest()
+        for k in sorted(f):
+            digests[f"final.{k}"] = syn.sha256(f[k])
+    weights = {"layers": layers, "norm": f["norm"], "head": O.quantize(f["head"], wd)[2], "emb": f["emb"],
+               "rope": O.rope_table(syn.inv_freq(s), max_len), "eps": s.eps, "nq": s.nq, "nkv": s.nkv}
+    return O.TalkerOracle(weights, K, V, cache_bf16), syn.start_token(seed, s), s

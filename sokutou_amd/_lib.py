@@ -1,0 +1,87 @@
+"""ctypes binding of ``libsokutou_amd.so`` (the C-ABI declared in ``include/sokutou_amd.h``).
+
+torch is imported before the library is opened: torch bundles its own HIP runtime with the same soname
+(``libamdhip64.so.7``), so the dynamic loader resolves the library against that one runtime and the stream
+handles torch hands out (``torch.cuda.current_stream().cuda_stream``) are valid inside the library.
+There is no fallback: if the library is missing, every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_int64, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  (must be loaded first, see above)
+
+LIB_PATH = Path(__file__).resolve().parent / "libsokutou_amd.so"
+HEADER = Path(__file__).resolve().parent.parent / "include" / "sokutou_amd.h"
+
+SK_OK, SK_EINVAL, SK_ELAUNCH, SK_EUNSUPPORTED, SK_EWORKSPACE, SK_EDEVICE = 0, -1, -2, -3, -4, -5
+WD = {"i8row": 0, "i8g32": 1, "bf16": 2, "f32": 3}
+CT = {"bf16": 0, "f32": 1}
+
+_P = c_void_p
+_SIGS = {
+    "sk_version": (ctypes.c_char_p, []),
+    "sk_last_error": (ctypes.c_char_p, []),
+    "sk_device_check": (c_int, []),
+    "sk_rms_gemv": (c_int, [_P, _P, c_float, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P]),
+    "sk_gemv": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P]),
+    "sk_rmsnorm": (c_int, [_P, _P, c_float, _P, c_int, _P]),
+    "sk_embed": (c_int, [_P, _P, _P, c_int, c_int, _P]),
+    "sk_talker_in": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P]),
+    "sk_attn_workspace_size": (c_int64, [c_int, c_int, c_int]),
+    "sk_attn": (c_int, [_P, _P, _P, c_float, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, _P, c_int64, c_int, _P]),
+    "sk_sample": (c_int, [_P, c_int, c_float, c_int, c_int, _P, c_float, _P, _P, c_int, c_int, _P, _P, _P, c_int, _P,
+                          _P, _P]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Opens the library once and declares every signature."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python -m sokutou_amd.build` (hipcc, gfx950)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, name: str) -> None:
+    """Raises the Python error matching an SK_* status (ValueError where the reference asserts)."""
+    if rc == SK_OK:
+        return
+    msg = f"{name}: {load().sk_last_error().decode(errors='replace')}"
+    if rc in (SK_EINVAL, SK_EWORKSPACE):
+        raise ValueError(msg)
+    if rc == SK_EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for None); tensors must be contiguous, as in the reference's _ptr
+    (qwen3/kernels.py:418-422)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return t.data_ptr()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args), name)

@@ -1,0 +1,150 @@
+// Device helpers shared by the gfx950 kernels of the talker decode step.
+// Wave64 throughout: reductions use DPP row operations, never 32-lane shuffles.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SK_HD 128          // head_dim (fixed by the model family; the reference asserts it, qwen3/kernels.py:457)
+#define SK_WAVE 64
+
+typedef uint16_t bf16_t;
+
+// ---- weight formats (the `wd` names of _Lin) -------------------------------------------------------------
+enum SkWd { SK_WD_I8ROW = 0, SK_WD_I8G32 = 1, SK_WD_BF16 = 2, SK_WD_F32 = 3 };
+// ---- KV-cache / embedding element type ------------------------------------------------------------------
+enum SkCt { SK_CT_BF16 = 0, SK_CT_F32 = 1 };
+
+// ---- scalar conversions ----------------------------------------------------------------------------------
+__device__ __forceinline__ float bf2f(uint32_t u16) { return __uint_as_float(u16 << 16); }
+// fp32 -> bf16, round to nearest even, NaN -> 0x7fc0 (same rule as torch's conversion)
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+__device__ __forceinline__ float h2f(uint16_t h) {
+  _Float16 x;
+  __builtin_memcpy(&x, &h, 2);
+  return (float)x;
+}
+template <int CT> struct Cache;
+template <> struct Cache<SK_CT_BF16> {
+  typedef bf16_t T;
+  static __device__ __forceinline__ float ld(T v) { return bf2f(v); }
+  static __device__ __forceinline__ T st(float f) { return f2bf(f); }
+  static __device__ __forceinline__ float rnd(float f) { return bf2f(f2bf(f)); }
+};
+template <> struct Cache<SK_CT_F32> {
+  typedef float T;
+  static __device__ __forceinline__ float ld(T v) { return v; }
+  static __device__ __forceinline__ T st(float f) { return f; }
+  static __device__ __forceinline__ float rnd(float f) { return f; }
+};
+
+// ---- DPP wave reductions ---------------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
+}
+// Sum within each row of 16 lanes; every lane of the row receives it.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x124>(v);  // row_ror:4
+  v += dpp<0x128>(v);  // row_ror:8
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x124>(v));
+  v = fmaxf(v, dpp<0x128>(v));
+  return v;
+}
+// Full wave64 sum, returned uniform (via lane 63).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  v += dpp<0x142, 0xA>(v);  // row_bcast:15
+  v += dpp<0x143, 0xC>(v);  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  // combine the four 16-lane rows through scalar reads of one lane per row
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// ---- 16-byte weight chunk dot products -------------------------------------------------------------------
+// A 16-byte chunk holds 16 int8, 8 bf16 or 4 fp32 weights; xp points at the matching fp32 inputs.
+__device__ __forceinline__ float dot_i8x16(uint4 v, const float* __restrict__ xp) {
+  float a0 = 0.f, a1 = 0.f;
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float4 x = *(const float4*)(xp + 4 * i);
+    float t = (float)(int8_t)(w[i]) * x.x;
+    t = __builtin_fmaf((float)(int8_t)(w[i] >> 8), x.y, t);
+    t = __builtin_fmaf((float)(int8_t)(w[i] >> 16), x.z, t);
+    t = __builtin_fmaf((float)(int8_t)(w[i] >> 24), x.w, t);
+    if (i & 1) a1 += t; else a0 += t;
+  }
+  return a0 + a1;
+}
+__device__ __forceinline__ float dot_bf16x8(uint4 v, const float* __restrict__ xp) {
+  float4 a = *(const float4*)xp, b = *(const float4*)(xp + 4);
+  float t = bf2f(v.x & 0xffffu) * a.x;
+  t = __builtin_fmaf(bf2f(v.x >> 16), a.y, t);
+  t = __builtin_fmaf(bf2f(v.y & 0xffffu), a.z, t);
+  t = __builtin_fmaf(bf2f(v.y >> 16), a.w, t);
+  t = __builtin_fmaf(bf2f(v.z & 0xffffu), b.x, t);
+  t = __builtin_fmaf(bf2f(v.z >> 16), b.y, t);
+  t = __builtin_fmaf(bf2f(v.w & 0xffffu), b.z, t);
+  t = __builtin_fmaf(bf2f(v.w >> 16), b.w, t);
+  return t;
+}
+__device__ __forceinline__ float dot_f32x4(uint4 v, const float* __restrict__ xp) {
+  float4 a = *(const float4*)xp;
+  float t = __uint_as_float(v.x) * a.x;
+  t = __builtin_fmaf(__uint_as_float(v.y), a.y, t);
+  t = __builtin_fmaf(__uint_as_float(v.z), a.z, t);
+  t = __builtin_fmaf(__uint_as_float(v.w), a.w, t);
+  return t;
+}
+
+// Elements per 16-byte chunk for a weight format.
+template <int WD> struct WdInfo;
+template <> struct WdInfo<SK_WD_I8ROW> { static constexpr int E = 16, BYTES = 1; };
+template <> struct WdInfo<SK_WD_I8G32> { static constexpr int E = 16, BYTES = 1; };
+template <> struct WdInfo<SK_WD_BF16> { static constexpr int E = 8, BYTES = 2; };
+template <> struct WdInfo<SK_WD_F32> { static constexpr int E = 4, BYTES = 4; };
+
+// Dot of chunk c of row `row` (K elements) with xp; applies group scales for i8g32 inside.
+template <int WD>
+__device__ __forceinline__ float chunk_dot(uint4 v, const float* __restrict__ xp, const uint16_t* __restrict__ S,
+                                           int row, int K, int c) {
+  if constexpr (WD == SK_WD_I8ROW) return dot_i8x16(v, xp);
+  else if constexpr (WD == SK_WD_I8G32) return h2f(S[(size_t)row * (K >> 5) + (c >> 1)]) * dot_i8x16(v, xp);
+  else if constexpr (WD == SK_WD_BF16) return dot_bf16x8(v, xp);
+  else return dot_f32x4(v, xp);
+}
+// Row-level scale applied after the dot (i8row only).
+template <int WD>
+__device__ __forceinline__ float row_scale(const uint16_t* __restrict__ S, int row) {
+  if constexpr (WD == SK_WD_I8ROW) return bf2f(S[row]);
+  else return 1.f;
+}
+
+// ---- streaming loads -------------------------------------------------------------------------------------
+// Weights are read once per frame: nontemporal hint keeps them from displacing reused lines in L2/MALL.
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 r = __builtin_nontemporal_load((const u32x4*)p);
+  return make_uint4(r.x, r.y, r.z, r.w);
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }

@@ -1,0 +1,286 @@
+"""The talker decode engine on hand-written gfx950 kernels, behind the reference's ``Qwen3Kernels`` surface.
+
+Mirrors qwen3/kernels.py: ``_Lin`` (425-447) packs one [N, K] matrix, ``_Stack`` (450-480) packs a decoder
+stack, ``Qwen3Kernels`` (483-754) composes the frame. One decoder layer is five launches on the caller's stream:
+
+  1. sk_rms_gemv(qkv)          RMSNorm fused into the q/k/v projection
+  2. sk_attn                   q/k RMSNorm, RoPE, KV append, split-K GQA attention with log-sum-exp merge
+  3. sk_gemv(o, accumulate)    output projection added into the fp32 residual
+  4. sk_rms_gemv(gu, swiglu)   RMSNorm fused into gate/up (rows interleaved), silu(gate) * up
+  5. sk_gemv(down, accumulate) down projection added into the residual
+
+The frame (talker half of qwen3/kernels.py:676-685) is embed(id0) -> 28 layers -> sk_rmsnorm -> codec head ->
+sk_sample, and is recorded once as a HIP graph. Weight formats: ``i8row`` (int8 + bf16 scale per output row,
+the primary format), ``i8g32`` (the reference's int8 + fp16 per-32 scale), ``bf16`` and ``f32``.
+"""
+
+from __future__ import annotations
+
+import time
+
+import torch
+
+from . import _lib
+from .fast import Qwen3Fast, Sampling, _sample
+from .sampler import FusedSampler
+
+HD = 128
+
+
+class _Lin:
+    """One matrix [N, K] in the kernels' format. ``wd``: ``i8row`` int8 + bf16 scale per row
+    (s = bf16(max(max|w|/127, 1e-12)), q = clamp(round_half_even(w/s), +-127)); ``i8g32`` int8 + fp16 scale per
+    32 K elements (qwen3/kernels.py:438-442); ``bf16``; ``f32``. ``pol`` 1 streams the weights past the caches
+    (read once per frame), 0 keeps them cacheable; ``split`` is kept for interface parity (always 1)."""
+
+    def __init__(self, w: torch.Tensor, wd: str):
+        dev = w.device
+        # quantise on the CPU: its fp32 division is correctly rounded, so the int8 values are reproducible
+        # bit for bit on any host (a GPU division can land on the other side of a .5 tie)
+        w = w.detach().to("cpu").contiguous()
+        self.N, self.K = w.shape
+        self.pol = 0
+        self.split = 1
+        self.wd = wd
+        if self.K % 512 != 0:
+            raise ValueError(f"K={self.K} must be a multiple of 512")
+        if wd == "bf16":
+            self.w, self.s = w.to(torch.bfloat16).contiguous(), None
+        elif wd == "f32":
+            self.w, self.s = w.float().contiguous(), None
+        elif wd == "i8row":
+            wf = w.float()
+            sc = (wf.abs().amax(1) / 127).clamp_min(1e-12).to(torch.bfloat16)
+            q = torch.round(wf / sc.float()[:, None])
+            q = torch.nan_to_num(q, nan=0.0).clamp(-127, 127).to(torch.int8)
+            self.w, self.s = q.contiguous(), sc.view(torch.int16).contiguous()
+        elif wd == "i8g32":
+            g = w.float().view(self.N, self.K // 32, 32)
+            sc = (g.abs().amax(2) / 127).clamp_min(1e-12).half()
+            q = torch.round(g / sc.float()[..., None])
+            q = torch.nan_to_num(q, nan=0.0, posinf=127.0, neginf=-127.0).clamp(-127, 127).to(torch.int8)
+            self.w, self.s = q.view(self.N, self.K).contiguous(), sc.view(torch.int16).contiguous()
+        else:
+            raise ValueError(wd)
+        self.w = self.w.to(dev)
+        self.s = None if self.s is None else self.s.to(dev)
+
+    @property
+    def wd_code(self) -> int:
+        return _lib.WD[self.wd]
+
+    def bytes(self) -> int:
+        return self.w.numel() * self.w.element_size() + (0 if self.s is None else self.s.numel() * 2)
+
+    def dequant(self) -> torch.Tensor:
+        """fp32 [N, K] weights the kernels effectively multiply with (for checks)."""
+        if self.wd in ("bf16", "f32"):
+            return self.w.float()
+        if self.wd == "i8row":
+            return self.w.float() * self.s.view(torch.bfloat16).float()[:, None]
+        s = self.s.view(torch.float16).float()
+        return (self.w.float().view(self.N, self.K // 32, 32) * s[..., None]).view(self.N, self.K)
+
+
+class _Stack:
+    """Decoder layers in kernel form (qwen3/kernels.py:450-480): q/k/v rows concatenated into ``qkv``, gate/up
+    rows interleaved (row 2n gate n, row 2n+1 up n) into ``gu``, norm weights fp32, and the RoPE table
+    [max_len][cos 64 | sin 64] from ``pos * inv_freq`` in fp32."""
+
+    def __init__(self, model, wd: str, max_len: int):
+        cfg = model.config
+        self.H, self.I = int(cfg.hidden_size), int(cfg.intermediate_size)
+        self.nq, self.nkv = int(cfg.num_attention_heads), int(cfg.num_key_value_heads)
+        if int(cfg.head_dim) != HD or self.nq != 2 * self.nkv:
+            raise ValueError("only head_dim 128 with two q heads per kv head is supported")
+        self.eps = float(cfg.rms_norm_eps)
+        self.layers = []
+        for layer in model.layers:
+            a, m = layer.self_attn, layer.mlp
+            gu = torch.stack([m.gate_proj.weight, m.up_proj.weight], dim=1).reshape(2 * self.I, self.H)
+            self.layers.append({
+                "in_norm": layer.input_layernorm.weight.float().contiguous(),
+                "qkv": _Lin(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], dim=0), wd),
+                "qn": a.q_norm.weight.float().contiguous(), "kn": a.k_norm.weight.float().contiguous(),
+                "o": _Lin(a.o_proj.weight, wd),
+                "post_norm": layer.post_attention_layernorm.weight.float().contiguous(),
+                "gu": _Lin(gu, wd), "down": _Lin(m.down_proj.weight, wd),
+            })
+            if getattr(a.q_proj, "bias", None) is not None or getattr(a.o_proj, "bias", None) is not None:
+                raise ValueError("attention biases are not supported")
+        self.norm = model.norm.weight.float().contiguous()
+        inv = model.rotary_emb.inv_freq.float()
+        if inv.numel() != HD // 2 or float(model.rotary_emb.attention_scaling) != 1.0:
+            raise ValueError("only default 1-D RoPE (64 frequencies, scaling 1) is supported")
+        f = torch.arange(max_len, device=inv.device, dtype=torch.float32)[:, None] * inv[None, :]
+        self.rope = torch.cat([f.cos(), f.sin()], dim=1).contiguous()
+        self.max_len = max_len
+
+    def bytes(self) -> int:
+        return sum(L[k].bytes() for L in self.layers for k in ("qkv", "o", "gu", "down"))
+
+
+class Qwen3Kernels(Qwen3Fast):
+    """The talker frame on the sokutou_amd kernels (qwen3/kernels.py:483-754 surface).
+
+    Constructor arguments as the reference; ``wd`` adds ``i8row``. ``l2_keep_mb`` and ``cp_pair`` are accepted
+    for interface parity: the talker's weights are always streamed (policy 1), and the code predictor is not
+    part of this engine yet. ``suppress_tail`` (default 1024, as the reference) sets how many trailing ids the
+    processor suppresses; 0 disables suppression.
+    """
+
+    def __init__(self, tts, sampling: Sampling | None = None, max_cache: int = 1024, wd: str = "bf16",
+                 graphs: bool = True, sampler: str = "fused", l2_keep_mb: float | None = None,
+                 cp_pair: bool | None = None, suppress_tail: int = 1024):
+        super().__init__(tts, sampling, max_cache=max_cache, compile=False, graphs=graphs, suppress_tail=suppress_tail)
+        if sampler not in ("fused", "torch"):
+            raise ValueError(sampler)
+        if wd not in _lib.WD:
+            raise ValueError(wd)
+        L = _lib.load()
+        if self.device.type != "cuda":
+            raise RuntimeError("Qwen3Kernels runs on a HIP device")
+        with torch.cuda.device(self.device):
+            _lib.check(L.sk_device_check(), "sk_device_check")
+        if self.cp is not None:
+            raise NotImplementedError("the code predictor (15 sub-steps per frame) is not part of this engine yet")
+        t0 = time.perf_counter()
+        self.wd = wd
+        self.ct = "f32" if wd == "f32" else "bf16"
+        cdt = torch.float32 if self.ct == "f32" else torch.bfloat16
+        self.cp_pair = bool(cp_pair) if cp_pair is not None else True
+        self.l2_keep_mb = l2_keep_mb if l2_keep_mb is not None else 0.0
+        dev = self.device
+        with torch.no_grad():
+            self.T = _Stack(self.talker.model, wd, max_cache)
+            self.codec_head = _Lin(self.talker.codec_head.weight, wd)
+            self.temb = self.talker.get_input_embeddings().weight.to(cdt).contiguous()
+        for Ly in self.T.layers:
+            for m in ("qkv", "o", "gu", "down"):
+                Ly[m].pol = 1
+        self.codec_head.pol = 1
+        self.l2_kept_bytes = 0
+        self.kernel_compile_sec = time.perf_counter() - t0
+        self.sampler = sampler
+        self.fs = FusedSampler(dev) if sampler == "fused" else None
+        P = self.T
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.ph32 = torch.zeros(P.H, **f32)
+        self.ht = torch.zeros(P.H, **f32)
+        self.qkv_t = torch.zeros((P.nq + 2 * P.nkv) * HD, **f32)
+        self.att_t = torch.zeros(P.nq * HD, **f32)
+        self.act_t = torch.zeros(P.I, **f32)
+        self.logit_t = torch.zeros((1, self.V), **f32)
+        # talker KV cache [layer][kv head][position][128]
+        self.kc = torch.zeros((len(P.layers), P.nkv, max_cache, HD), dtype=cdt, device=dev)
+        self.vc = torch.zeros_like(self.kc)
+        self.tk = list(self.kc.unbind(0))
+        self.tv = list(self.vc.unbind(0))
+        nbytes = int(L.sk_attn_workspace_size(P.nq, P.nkv, max_cache))
+        self.attn_ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        self.trace: list[torch.Tensor] | None = None
+
+    # --- launches -----------------------------------------------------------------------------------------
+    def _rms_gemv(self, h, nw, eps, lin: _Lin, out, swiglu: bool) -> None:
+        p = _lib.ptr
+        _lib.call("sk_rms_gemv", p(h), p(nw), float(eps), p(lin.w), p(lin.s), p(out), lin.N, lin.K, int(swiglu),
+                  lin.wd_code, lin.pol, _lib.stream())
+
+    def _gemv(self, x, lin: _Lin, bias, out, accumulate: bool) -> None:
+        p = _lib.ptr
+        _lib.call("sk_gemv", p(x), p(lin.w), p(lin.s), p(bias), p(out), lin.N, lin.K, int(accumulate), lin.wd_code,
+                  lin.pol, _lib.stream())
+
+    def _attn(self, P: _Stack, L: dict, qkv, kc, vc, pos_ptr, pos_add: int, out) -> None:
+        p = _lib.ptr
+        _lib.call("sk_attn", p(qkv), p(L["qn"]), p(L["kn"]), float(P.eps), p(P.rope), p(kc), p(vc), p(pos_ptr),
+                  int(pos_add), P.max_len, P.nq, P.nkv, p(out), p(self.attn_ws), self.attn_ws.numel(),
+                  _lib.CT[self.ct], _lib.stream())
+
+    def _embed(self, table, idx, out) -> None:
+        p = _lib.ptr
+        _lib.call("sk_embed", p(table), p(idx), p(out), out.numel(), _lib.CT[self.ct], _lib.stream())
+
+    def _rmsnorm(self, h, nw, eps, out) -> None:
+        p = _lib.ptr
+        _lib.call("sk_rmsnorm", p(h), p(nw), float(eps), p(out), h.numel(), _lib.stream())
+
+    def _layers(self, P: _Stack, h, qkv, att, act, kcache, vcache, pos_ptr, pos_add: int) -> None:
+        """One decoder stack on the fp32 residual ``h`` (qwen3/kernels.py:619-627)."""
+        for i, L in enumerate(P.layers):
+            self._rms_gemv(h, L["in_norm"], P.eps, L["qkv"], qkv, False)
+            self._attn(P, L, qkv, kcache[i], vcache[i], pos_ptr, pos_add, att)
+            self._gemv(att, L["o"], None, h, True)
+            self._rms_gemv(h, L["post_norm"], P.eps, L["gu"], act, True)
+            self._gemv(act, L["down"], None, h, True)
+            if self.trace is not None:
+                self.trace.append(h.clone())
+
+    # --- one frame ----------------------------------------------------------------------------------------
+    def _talker(self) -> None:
+        """embed(id0) -> layers -> final RMSNorm -> codec head (logits in ``logit_t``)."""
+        P = self.T
+        self._embed(self.temb, self.id0, self.ht)
+        self._layers(P, self.ht, self.qkv_t, self.att_t, self.act_t, self.tk, self.tv, self.pos, 0)
+        self._rmsnorm(self.ht, P.norm, P.eps, self.ph32)
+        self._gemv(self.ph32, self.codec_head, None, self.logit_t, False)
+
+    def _frame(self) -> None:
+        s = self.s
+        self.codes[:, :1].copy_(self.id0)
+        self._talker()
+        if self.fs is not None:
+            # processor and the state update (next_id0, id0, seen, ngen, pos) happen inside the kernel
+            self.fs(self.logit_t.view(-1), self.next_id0, s.do_sample, s.temperature, s.top_k,
+                    talker=dict(seen=self.seen, rep_pen=s.repetition_penalty,
+                                suppress=self.suppress if self.suppress_tail else None, ngen=self.ngen,
+                                min_new=s.min_new_tokens, eos=self.eos, id0=self.id0, pos=self.pos))
+            return
+        nxt = _sample(self._process(self.logit_t), s.do_sample, s.temperature, s.top_k)
+        self.next_id0.copy_(nxt)
+        self.seen.scatter_(1, nxt, True)
+        self.ngen.add_(1)
+        self.pos.add_(1)
+        self.id0.copy_(nxt)
+
+    # --- prompt state -------------------------------------------------------------------------------------
+    def load_kv(self, K: torch.Tensor, V: torch.Tensor) -> None:
+        """Copies prior cache contents [layers, nkv, T, 128] into positions [0, T) (a prefilled prompt)."""
+        T = K.shape[2]
+        if T > self.max_cache:
+            raise ValueError("prefill longer than the cache")
+        self.kc[:, :, :T].copy_(K.to(self.kc.dtype))
+        self.vc[:, :, :T].copy_(V.to(self.vc.dtype))
+
+    def reset(self, pos: int, token: int) -> None:
+        """Frame state right after a prompt of ``pos`` tokens whose first sampled code is ``token``
+        (what the reference's _prefill_body leaves, qwen3/fast.py:253-263)."""
+        self.id0.fill_(int(token))
+        self.next_id0.fill_(int(token))
+        self.seen.zero_()
+        self.seen[0, int(token)] = True
+        self.ngen.fill_(1)
+        self.pos.fill_(int(pos))
+
+    def _start(self, kw: dict) -> int:
+        if "inputs_embeds" in kw:
+            raise NotImplementedError("prompt prefill through Hugging Face modules is not part of this engine")
+        L = int(kw["prefill_len"])
+        self.reset(L, int(kw["first_token"]))
+        return L
+
+    @torch.no_grad()
+    def layer_trace(self, token: int, pos: int) -> list[torch.Tensor]:
+        """Runs one talker step eagerly and returns the residual after every layer, then the logits."""
+        self.id0.fill_(int(token))
+        self.pos.fill_(int(pos))
+        self.trace = []
+        try:
+            self._talker()
+            out = self.trace + [self.logit_t.clone()]
+        finally:
+            self.trace = None
+        return out
+
+    def weight_bytes(self) -> dict:
+        return {"talker": self.T.bytes() + self.codec_head.bytes(), "code_predictor": 0, "cp_heads": 0}

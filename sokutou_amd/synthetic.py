@@ -1,0 +1,218 @@
+"""Seeded synthetic Qwen3-TTS talker: random-init weights of the real architecture, shaped like the Hugging Face
+modules that ``_Stack`` reads (qwen3/kernels.py:450-480), so the engine can be built without qwen-tts or a
+network fetch.
+
+Value distributions (fixed so that every run, the oracle and the GPU path see identical inputs):
+  * projection weights  N(0, 0.02), drawn in float64 by numpy ``default_rng`` and stored as float32;
+  * RMSNorm weights     1 + 0.1 * N(0, 1), float32 (the reference's bench uses the same form,
+                        qwen3/gemv2_bench.py:109);
+  * embedding table     N(0, 0.02) rounded to bf16, shape [vocab, hidden];
+  * prior K/V cache     N(0, 1) rounded to bf16;
+  * eps 1e-6, RoPE theta 1e6, head_dim 128, GQA with two q heads per kv head.
+Each tensor has its own stream, ``SeedSequence([seed, layer + 1, tag])``, so any one layer can be regenerated
+alone and the draw order never matters.
+"""
+
+from __future__ import annotations
+
+import hashlib
+from dataclasses import dataclass, replace
+from types import SimpleNamespace
+
+import numpy as np
+import torch
+
+_TAGS = {"q": 1, "k": 2, "v": 3, "o": 4, "gate": 5, "up": 6, "down": 7, "in_norm": 8, "post_norm": 9, "q_norm": 10,
+         "k_norm": 11, "norm": 12, "head": 13, "emb": 14, "kcache": 15, "vcache": 16, "h": 17, "token": 18}
+
+
+@dataclass(frozen=True)
+class TalkerShape:
+    """Talker architecture. Defaults are the 0.6B talker (hidden 1024, 28 layers, 16 q / 8 kv heads,
+    head_dim 128, intermediate 3072, codec vocabulary 3072)."""
+    hidden: int = 1024
+    n_layers: int = 28
+    nq: int = 16
+    nkv: int = 8
+    head_dim: int = 128
+    inter: int = 3072
+    vocab: int = 3072
+    eps: float = 1e-6
+    theta: float = 1e6
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.nq + 2 * self.nkv) * self.head_dim
+
+
+SHAPES = {
+    "0.6b": TalkerShape(),
+    "1.7b": TalkerShape(hidden=2048, inter=6144),
+    "tiny": TalkerShape(hidden=512, n_layers=2, nq=4, nkv=2, inter=1024, vocab=512),
+}
+
+
+def shape(name: str, **over) -> TalkerShape:
+    return replace(SHAPES[name], **over)
+
+
+def _rng(seed: int, layer: int, tag: str) -> np.random.Generator:
+    return np.random.default_rng(np.random.SeedSequence([int(seed), int(layer) + 1, _TAGS[tag]]))
+
+
+def normal(seed: int, layer: int, tag: str, shp, std: float = 1.0, mean: float = 0.0) -> np.ndarray:
+    """float64 N(mean, std) draw, returned as float32."""
+    x = _rng(seed, layer, tag).standard_normal(shp, dtype=np.float64)
+    return (mean + std * x).astype(np.float32)
+
+
+def bf16_values(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to bf16 (nearest even) and return them as float32."""
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def inv_freq(s: TalkerShape) -> np.ndarray:
+    """RoPE inverse frequencies computed in float32 exactly as Hugging Face's default rotary embedding does
+    (``1 / theta ** (arange(0, hd, 2) / hd)``)."""
+    e = torch.arange(0, s.head_dim, 2, dtype=torch.int64).to(torch.float32) / s.head_dim
+    return (1.0 / (s.theta ** e)).numpy().astype(np.float32)
+
+
+def layer_weights(seed: int, i: int, s: TalkerShape) -> dict:
+    """fp32 weights of decoder layer ``i`` in Hugging Face layout ([out, in])."""
+    H, I, hd = s.hidden, s.inter, s.head_dim
+    std = 0.02
+    return {
+        "q": normal(seed, i, "q", (s.nq * hd, H), std), "k": normal(seed, i, "k", (s.nkv * hd, H), std),
+        "v": normal(seed, i, "v", (s.nkv * hd, H), std), "o": normal(seed, i, "o", (H, s.nq * hd), std),
+        "gate": normal(seed, i, "gate", (I, H), std), "up": normal(seed, i, "up", (I, H), std),
+        "down": normal(seed, i, "down", (H, I), std),
+        "in_norm": normal(seed, i, "in_norm", (H,), 0.1, 1.0), "post_norm": normal(seed, i, "post_norm", (H,), 0.1, 1.0),
+        "q_norm": normal(seed, i, "q_norm", (hd,), 0.1, 1.0), "k_norm": normal(seed, i, "k_norm", (hd,), 0.1, 1.0),
+    }
+
+
+def final_weights(seed: int, s: TalkerShape) -> dict:
+    L = s.n_layers
+    return {"norm": normal(seed, L, "norm", (s.hidden,), 0.1, 1.0),
+            "head": normal(seed, L, "head", (s.vocab, s.hidden), 0.02),
+            "emb": bf16_values(normal(seed, L, "emb", (s.vocab, s.hidden), 0.02))}
+
+
+def kv_prefill(seed: int, i: int, s: TalkerShape, T: int) -> tuple[np.ndarray, np.ndarray]:
+    """Prior K/V for layer ``i``: [nkv, T, 128] N(0,1) rounded to bf16 (as float32 values)."""
+    k = bf16_values(normal(seed, i, "kcache", (s.nkv, T, s.head_dim)))
+    v = bf16_values(normal(seed, i, "vcache", (s.nkv, T, s.head_dim)))
+    return k, v
+
+
+def input_hidden(seed: int, s: TalkerShape) -> np.ndarray:
+    """A single-layer input activation h ~ N(0,1) rounded to bf16 (as float32)."""
+    return bf16_values(normal(seed, 0, "h", (s.hidden,)))
+
+
+def start_token(seed: int, s: TalkerShape) -> int:
+    return int(_rng(seed, 0, "token").integers(0, s.vocab))
+
+
+def sha256(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+# ---------------------------------------------------------------------------------------------------------
+# Hugging Face-shaped stand-ins (duck-typed attributes read by _Stack / Qwen3Kernels)
+# ---------------------------------------------------------------------------------------------------------
+def _p(x: np.ndarray, device, dtype=torch.float32) -> SimpleNamespace:
+    return SimpleNamespace(weight=torch.from_numpy(np.ascontiguousarray(x)).to(device=device, dtype=dtype), bias=None)
+
+
+class _Rotary:
+    def __init__(self, inv: np.ndarray, device):
+        self.inv_freq = torch.from_numpy(inv).to(device)
+        self.attention_scaling = 1.0
+
+
+def make_talker(seed: int, s: TalkerShape, device="cpu", layers: list[dict] | None = None,
+                final: dict | None = None) -> SimpleNamespace:
+    """A talker object with the attributes the engine reads: ``model.layers[i].self_attn.{q,k,v,o}_proj``,
+    ``q_norm``/``k_norm``, ``mlp.{gate,up,down}_proj``, ``input_layernorm``, ``post_attention_layernorm``,
+    ``model.norm``, ``model.rotary_emb``, ``codec_head`` and ``get_input_embeddings()`` (bf16 table).
+    ``code_predictor`` is None: the synthetic frame feeds the talker its own embedding row."""
+    layers = layers if layers is not None else [layer_weights(seed, i, s) for i in range(s.n_layers)]
+    final = final if final is not None else final_weights(seed, s)
+    hl = []
+    for w in layers:
+        attn = SimpleNamespace(q_proj=_p(w["q"], device), k_proj=_p(w["k"], device), v_proj=_p(w["v"], device),
+                               o_proj=_p(w["o"], device), q_norm=_p(w["q_norm"], device), k_norm=_p(w["k_norm"], device))
+        mlp = SimpleNamespace(gate_proj=_p(w["gate"], device), up_proj=_p(w["up"], device), down_proj=_p(w["down"], device))
+        hl.append(SimpleNamespace(self_attn=attn, mlp=mlp, input_layernorm=_p(w["in_norm"], device),
+                                  post_attention_layernorm=_p(w["post_norm"], device)))
+    cfg = SimpleNamespace(hidden_size=s.hidden, intermediate_size=s.inter, num_attention_heads=s.nq,
+                          num_key_value_heads=s.nkv, head_dim=s.head_dim, rms_norm_eps=s.eps, rope_theta=s.theta,
+                          num_hidden_layers=s.n_layers, vocab_size=s.vocab)
+    model = SimpleNamespace(config=cfg, layers=hl, norm=_p(final["norm"], device),
+                            rotary_emb=_Rotary(inv_freq(s), device))
+    emb = SimpleNamespace(weight=torch.from_numpy(final["emb"]).to(device=device, dtype=torch.bfloat16))
+    talker = SimpleNamespace(model=model, config=cfg, codec_head=_p(final["head"], device), code_predictor=None,
+                             device=torch.device(device), dtype=torch.bfloat16)
+    talker.get_input_embeddings = lambda: emb
+    return talker
+
+
+def make_tts(seed: int, s: TalkerShape, device="cpu", eos: int | None = None, **kw) -> SimpleNamespace:
+    """A ``tts`` object as ``Qwen3Fast.__init__`` reads it (qwen3/fast.py:77-90): ``tts.model.talker`` and
+    ``tts.model.config.talker_config`` with ``num_code_groups``, ``vocab_size`` and ``codec_eos_token_id``."""
+    talker = make_talker(seed, s, device, **kw)
+    # the 12 Hz codec's EOS id is 2150 in a 3072-entry vocabulary (qwen3/check_sampler.py:42)
+    eos = (2150 if s.vocab > 2150 else s.vocab - 1) if eos is None else eos
+    tc = SimpleNamespace(num_code_groups=1, vocab_size=s.vocab, hidden_size=s.hidden, codec_eos_token_id=eos)
+    model = SimpleNamespace(talker=talker, config=SimpleNamespace(talker_config=tc))
+    return SimpleNamespace(model=model)
+
+
+# ---------------------------------------------------------------------------------------------------------
+# named workloads
+# ---------------------------------------------------------------------------------------------------------
+WORKLOADS = {
+    # single 0.6B-shaped decoder layer, one token, 256 prior positions (T = 257)
+    "layer06b": dict(shape="0.6b", n_layers=1, kv=256),
+    # 0.6B-shaped talker: 28 layers + final norm + 3072-way codec head, KV 512, 64 greedy frames
+    "talker06b": dict(shape="0.6b", n_layers=28, kv=512, frames=64),
+    # 1.7B-shaped talker: hidden 2048, intermediate 6144, KV 1024, 64 greedy frames
+    "talker17b": dict(shape="1.7b", n_layers=28, kv=1024, frames=64),
+    # tiny two-layer model for quick checks
+    "tiny": dict(shape="tiny", n_layers=2, kv=24, frames=8),
+}
+
+
+def workload_shape(name: str) -> TalkerShape:
+    w = WORKLOADS[name]
+    return shape(w["shape"], n_layers=w["n_layers"])
+
+
+def make_engine(name: str, seed: int = 0, wd: str = "i8row", device="cuda", graphs: bool = True,
+                max_cache: int | None = None, frames: int | None = None):
+    """Builds a Qwen3Kernels engine over the seeded synthetic talker of workload ``name`` with the prior KV
+    cache loaded and the frame state set at position ``kv``. Greedy decoding without the processor (plain
+    argmax over the whole codec vocabulary). Returns (engine, start token)."""
+    from .fast import Sampling
+    from .kernels import Qwen3Kernels
+
+    w = WORKLOADS[name]
+    s = workload_shape(name)
+    frames = w.get("frames", 1) if frames is None else frames
+    max_cache = max_cache or (w["kv"] + frames + 1)
+    tts = make_tts(seed, s, device=device)
+    eng = Qwen3Kernels(tts, Sampling.greedy(processor=False), max_cache=max_cache, wd=wd, graphs=graphs,
+                       sampler="fused", suppress_tail=0)
+    tts.model.talker = None  # the fp32 source weights are no longer needed once packed
+    eng.talker = None
+    del tts
+    dt = eng.kc.dtype
+    for i in range(s.n_layers):
+        k, v = kv_prefill(seed, i, s, w["kv"])
+        eng.kc[i, :, :w["kv"]].copy_(torch.from_numpy(k).to(dt))
+        eng.vc[i, :, :w["kv"]].copy_(torch.from_numpy(v).to(dt))
+    tok = start_token(seed, s)
+    eng.reset(w["kv"], tok)
+    return eng, tok

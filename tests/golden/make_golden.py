@@ -1,0 +1,125 @@
+"""Writes the golden fixtures in this directory from the CPU oracle and, for the single layer, from
+transformers' Qwen3DecoderLayer (an independent implementation of the same layer).
+
+    python tests/golden/make_golden.py [--only NAME]
+
+Fixtures are data: inputs (by seed and SHA-256 digest of every generated tensor), expected outputs and the
+numbers needed to judge argmax robustness (top-1/top-2 logit margins).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parent.parent))
+
+from oracle import talker as O  # noqa: E402
+from oracle.workload import pack_layer, talker_oracle  # noqa: E402
+from sokutou_amd import synthetic as syn  # noqa: E402
+
+
+def layer06b(seed: int = 0) -> None:
+    """One 0.6B-shaped layer, one token at position 256 over 256 prior positions, i8row weights."""
+    s = syn.workload_shape("layer06b")
+    T = syn.WORKLOADS["layer06b"]["kv"]
+    w = syn.layer_weights(seed, 0, s)
+    L = pack_layer(w, "i8row")
+    k, v = syn.kv_prefill(seed, 0, s, T)
+    h = syn.input_hidden(seed, s)
+    rope = O.rope_table(syn.inv_freq(s), T + 1)
+    res = {}
+    for bf in (True, False):
+        Kc = np.zeros((s.nkv, T + 1, 128), np.float32)
+        Vc = np.zeros_like(Kc)
+        Kc[:, :T], Vc[:, :T] = k, v
+        out = O.decoder_layer(h, L, s.eps, rope, Kc, Vc, T, s.nq, s.nkv, cache_bf16=bf)
+        res[bf] = (out, Kc[:, T].copy(), Vc[:, T].copy())
+    # transformers, f32 cache, the same dequantised weights
+    from transformers import DynamicCache, Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3DecoderLayer, Qwen3RotaryEmbedding
+
+    cfg = Qwen3Config(hidden_size=s.hidden, intermediate_size=s.inter, num_attention_heads=s.nq,
+                      num_key_value_heads=s.nkv, head_dim=128, rms_norm_eps=s.eps, num_hidden_layers=1,
+                      rope_parameters={"rope_type": "default", "rope_theta": s.theta})
+    cfg._attn_implementation = "eager"
+    hf = Qwen3DecoderLayer(cfg, 0).float().eval()
+    H, I = s.hidden, s.inter
+    qd = s.nq * 128
+    kd = s.nkv * 128
+    with torch.no_grad():
+        a, m = hf.self_attn, hf.mlp
+        a.q_proj.weight.copy_(torch.from_numpy(L["qkv"][:qd]))
+        a.k_proj.weight.copy_(torch.from_numpy(L["qkv"][qd:qd + kd]))
+        a.v_proj.weight.copy_(torch.from_numpy(L["qkv"][qd + kd:]))
+        a.o_proj.weight.copy_(torch.from_numpy(L["o"]))
+        m.gate_proj.weight.copy_(torch.from_numpy(L["gu"][0::2]))
+        m.up_proj.weight.copy_(torch.from_numpy(L["gu"][1::2]))
+        m.down_proj.weight.copy_(torch.from_numpy(L["down"]))
+        a.q_norm.weight.copy_(torch.from_numpy(w["q_norm"]))
+        a.k_norm.weight.copy_(torch.from_numpy(w["k_norm"]))
+        hf.input_layernorm.weight.copy_(torch.from_numpy(w["in_norm"]))
+        hf.post_attention_layernorm.weight.copy_(torch.from_numpy(w["post_norm"]))
+        cache = DynamicCache()
+        cache.update(torch.from_numpy(k[None].copy()), torch.from_numpy(v[None].copy()), 0)
+        x = torch.from_numpy(h)[None, None]
+        pid = torch.tensor([[T]])
+        cs = Qwen3RotaryEmbedding(cfg)(x, pid)
+        ref = hf(x, position_ids=pid, past_key_values=cache, use_cache=True, position_embeddings=cs)[0, 0].numpy()
+    dig = {k2: syn.sha256(v2) for k2, v2 in sorted(w.items())}
+    dig.update(kcache=syn.sha256(k), vcache=syn.sha256(v), h=syn.sha256(h))
+    np.savez_compressed(HERE / "layer06b_seed0.npz", h=h, out=res[True][0], k_new=res[True][1], v_new=res[True][2],
+                        out_f32cache=res[False][0], out_transformers_f32cache=ref)
+    meta = {"workload": "layer06b", "seed": seed, "wd": "i8row", "pos": T, "digests": dig,
+            "oracle_vs_transformers_f32cache_max_rel": float(np.max(np.abs(res[False][0] - ref)) / np.max(np.abs(ref)))}
+    (HERE / "layer06b_seed0.json").write_text(json.dumps(meta, indent=1))
+    print("layer06b", meta["oracle_vs_transformers_f32cache_max_rel"])
+
+
+def talker(name: str, seed: int, wd: str = "i8row") -> None:
+    """Greedy frames of a whole talker: codes, margins, per-layer residuals of frame 0, logits of frames 0 and
+    the last one."""
+    spec = syn.WORKLOADS[name]
+    frames = spec["frames"]
+    t0 = time.time()
+    dig: dict = {}
+    orc, tok, s = talker_oracle(name, seed, wd, digests=dig)
+    t1 = time.time()
+    layer_out: list = []
+    pos0 = spec["kv"]
+    codes, margins, logits = [], [], []
+    token = tok
+    for f in range(frames):
+        token_next, lg = orc.step(token, pos0 + f, layer_out if f == 0 else None)
+        top = np.sort(lg)[-2:]
+        margins.append(float(top[1] - top[0]))
+        if f in (0, frames - 1):
+            logits.append(lg)
+        codes.append(token_next)
+        token = token_next
+    t2 = time.time()
+    np.savez_compressed(HERE / f"{name}_seed{seed}.npz", layer_out0=np.stack(layer_out), logits_first=logits[0],
+                        logits_last=logits[-1])
+    meta = {"workload": name, "seed": seed, "wd": wd, "start_token": tok, "start_pos": pos0, "frames": frames,
+            "codes": codes, "margins": margins, "digests": dig,
+            "oracle_seconds": {"build": round(t1 - t0, 1), "frames": round(t2 - t1, 1)}}
+    (HERE / f"{name}_seed{seed}.json").write_text(json.dumps(meta, indent=1))
+    print(name, "codes", codes[:12], "... min margin", min(margins), meta["oracle_seconds"])
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only", default=None)
+    a = ap.parse_args()
+    jobs = {"layer06b": lambda: layer06b(0), "tiny": lambda: talker("tiny", 1), "talker06b": lambda: talker("talker06b", 0),
+            "talker17b": lambda: talker("talker17b", 0)}
+    for n, fn in jobs.items():
+        if a.only in (None, n):
+            fn()

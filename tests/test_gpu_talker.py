@@ -1,0 +1,121 @@
+"""Talker-level parity on the GPU: one 0.6B layer against the golden single-layer fixture, the full 0.6B talker
+(28 layers, KV 512) against the oracle's 64 greedy codes and per-layer residuals, and graph replay against
+eager execution."""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from sokutou_amd import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+TOL = 1e-2  # per-layer max relative error, max|a - b| / max|b|
+
+
+def rel_err(a, b) -> float:
+    a = a.detach().cpu().numpy() if isinstance(a, torch.Tensor) else a
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+def _fixture(name):
+    meta = json.loads((GOLD / f"{name}.json").read_text())
+    return meta, np.load(GOLD / f"{name}.npz")
+
+
+def _check_inputs(meta, seed, s):
+    """The generator still produces the fixture's inputs (catches drift of numpy or the seeding scheme)."""
+    w = syn.layer_weights(seed, 0, s)
+    for k, v in w.items():
+        key = f"layer0.{k}" if "all_layers" in meta["digests"] else k
+        assert syn.sha256(v) == meta["digests"][key], k
+
+
+def test_single_layer_06b(gpu):
+    print("layer06b: 0.6B layer, pos 256", flush=True)
+    meta, gold = _fixture("layer06b_seed0")
+    s = syn.workload_shape("layer06b")
+    _check_inputs(meta, 0, s)
+    eng, _ = syn.make_engine("layer06b", seed=0, wd="i8row", device=gpu, frames=1)
+    h = torch.from_numpy(gold["h"]).to(gpu)
+    eng.ht.copy_(h)
+    eng.pos.fill_(meta["pos"])
+    with torch.no_grad():
+        P = eng.T
+        eng._layers(P, eng.ht, eng.qkv_t, eng.att_t, eng.act_t, eng.tk, eng.tv, eng.pos, 0)
+    torch.cuda.synchronize()
+    err = rel_err(eng.ht, gold["out"])
+    print(f"layer06b max rel err {err:.3e}", flush=True)
+    assert err < TOL
+    assert err < 1e-5  # fp32 accumulation: far inside the tolerance
+    kn = eng.kc[0, :, meta["pos"]].float().cpu().numpy()
+    vn = eng.vc[0, :, meta["pos"]].float().cpu().numpy()
+    assert np.mean(kn != gold["k_new"]) < 0.02
+    np.testing.assert_array_equal(vn, gold["v_new"])
+
+
+@pytest.mark.parametrize("name,seed", [("tiny", 1), ("talker06b", 0)])
+def test_greedy_frames_match_oracle(gpu, name, seed):
+    print(f"{name}: greedy frames against the oracle fixture", flush=True)
+    meta, gold = _fixture(f"{name}_seed{seed}")
+    s = syn.workload_shape(name)
+    _check_inputs(meta, seed, s)
+    eng, tok = syn.make_engine(name, seed=seed, wd=meta["wd"], device=gpu)
+    assert tok == meta["start_token"]
+    # frame 0 eagerly, layer by layer
+    trace = eng.layer_trace(tok, meta["start_pos"])
+    errs = [rel_err(trace[i], gold["layer_out0"][i]) for i in range(s.n_layers)]
+    print(f"{name} per-layer max rel err: max {max(errs):.3e}", flush=True)
+    assert max(errs) < TOL
+    assert rel_err(trace[-1].view(-1), gold["logits_first"]) < TOL
+    # all frames through the captured graph
+    eng.reset(meta["start_pos"], tok)
+    eng.capture()
+    codes = []
+    for _ in range(meta["frames"]):
+        eng.graph.replay()
+        codes.append(int(eng.next_id0.item()))
+    assert codes == meta["codes"], (codes, meta["codes"])
+    assert int(eng.pos.item()) == meta["start_pos"] + meta["frames"]
+    assert rel_err(eng.logit_t.view(-1), gold["logits_last"]) < TOL
+
+
+def test_graph_replay_equals_eager(gpu):
+    print("tiny: graph replay vs eager", flush=True)
+    eng, tok = syn.make_engine("tiny", seed=3, device=gpu)
+    pos0 = syn.WORKLOADS["tiny"]["kv"]
+    kc0, vc0 = eng.kc.clone(), eng.vc.clone()
+    eager = []
+    for _ in range(6):
+        eng._frame()
+        eager.append((int(eng.next_id0.item()), eng.logit_t.clone()))
+    eng.kc.copy_(kc0)
+    eng.vc.copy_(vc0)
+    eng.reset(pos0, tok)
+    eng.capture()
+    for i in range(6):
+        eng.graph.replay()
+        torch.cuda.synchronize()
+        assert int(eng.next_id0.item()) == eager[i][0]
+        assert torch.equal(eng.logit_t, eager[i][1])
+
+
+def test_generate_codes_loop(gpu):
+    """The host frame loop (qwen3/fast.py:221-249 semantics): stops at the frame cap, counts cache limits."""
+    eng, tok = syn.make_engine("tiny", seed=1, device=gpu)
+    eng.capture()
+    from sokutou_amd.fast import Sampling
+
+    kw = {"prefill_len": syn.WORKLOADS["tiny"]["kv"], "first_token": tok, "do_sample": False, "subtalker_dosample": False,
+          "repetition_penalty": 1.0, "min_new_tokens": 0}
+    assert Sampling.from_kwargs(kw) == eng.s
+    codes = eng.generate_codes(kw, max_frames=5)
+    meta = json.loads((GOLD / "tiny_seed1.json").read_text())
+    assert codes.shape == (5, 1)
+    assert codes[:, 0].tolist() == [tok] + meta["codes"][:4]
+    assert eng.stats["frame_limited"] and not eng.stats["stopped"]
+    with pytest.raises(ValueError):
+        eng.generate_codes(dict(kw, top_p=0.5))

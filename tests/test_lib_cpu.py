@@ -1,0 +1,63 @@
+"""The C-ABI library loads on a machine without a GPU, exports every function declared in
+include/sokutou_amd.h, and rejects bad shapes before launching anything. No kernel is launched here."""
+
+import ctypes
+import re
+
+import pytest
+
+from sokutou_amd import _lib
+
+
+def _declared():
+    text = _lib.HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    names = _declared()
+    assert "sk_attn" in names and "sk_rms_gemv" in names
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) <= set(_lib._SIGS), "every declared entry point has a ctypes signature"
+
+
+def test_version_string():
+    assert b"gfx950" in _lib.load().sk_version()
+
+
+def test_workspace_size():
+    L = _lib.load()
+    assert L.sk_attn_workspace_size(16, 8, 1024) >= 8 * 2 * 32 * 130 * 4 + 8 * 4
+    assert L.sk_attn_workspace_size(16, 8, 16) > 0
+    assert L.sk_attn_workspace_size(16, 0, 16) == 0
+
+
+@pytest.mark.parametrize("N,K", [(64, 1000), (0, 1024), (64, 16384)])
+def test_gemv_rejects_bad_shapes_without_launching(N, K):
+    L = _lib.load()
+    dummy = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc = L.sk_gemv(dummy, dummy, dummy, None, dummy, N, K, 0, 0, 1, None)
+    assert rc == _lib.SK_EINVAL
+    assert b"sk_gemv" in L.sk_last_error()
+    with pytest.raises(ValueError):
+        _lib.check(rc, "sk_gemv")
+
+
+def test_attn_rejects_bad_head_ratio():
+    L = _lib.load()
+    d = ctypes.c_void_p(256)
+    rc = L.sk_attn(d, d, d, 1e-6, d, d, d, None, 0, 64, 12, 8, d, d, 1 << 20, 0, None)
+    assert rc == _lib.SK_EINVAL
+
+
+def test_sample_rejects_large_vocab_and_sampling():
+    L = _lib.load()
+    d = ctypes.c_void_p(256)
+    assert L.sk_sample(d, 5000, 1.0, 0, 0, None, 1.0, None, None, 0, -1, None, None, d, 0, None, None, None) == _lib.SK_EINVAL
+    rc = L.sk_sample(d, 100, 1.0, 50, 1, None, 1.0, None, None, 0, -1, d, d, d, 0, None, None, None)
+    assert rc == _lib.SK_EUNSUPPORTED
+    with pytest.raises(NotImplementedError):
+        _lib.check(rc, "sk_sample")

@@ -1,0 +1,294 @@
+"""Pins the CPU oracle (oracle/talker.py) against independent references: torch's bf16 conversion, brute-force
+loops, float64 closed forms and transformers' Qwen3 layer (a library implementation of the same architecture).
+CPU only."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import talker as O
+from sokutou_amd import synthetic as syn
+
+F32 = np.float32
+
+
+# ---- bf16 storage rounding ----------------------------------------------------------------------------------
+def test_bf16_matches_torch_on_all_classes():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(100000).astype(F32) * F32(3.0),
+        rng.standard_normal(1000).astype(F32) * F32(1e-38),  # subnormals
+        np.array([0.0, -0.0, np.inf, -np.inf, 1.0, -1.0, 3.4e38, -3.4e38, 1e-45], dtype=F32),
+        # exact ties between two bf16 values, both parities of the kept bit
+        (np.arange(1, 2000, dtype=np.uint32) << 16 | 0x8000).view(F32),
+    ])
+    got = O.bf16_bits(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_bf16_nan_rule():
+    x = np.array([np.nan, -np.nan], dtype=F32)
+    x = np.concatenate([x, np.array([0x7F800001, 0xFFC00001, 0x7FFFFFFF], dtype=np.uint32).view(F32)])
+    assert np.all(O.bf16_bits(x) == 0x7FC0)
+
+
+# ---- quantisation -------------------------------------------------------------------------------------------
+def _brute_rowwise(w):
+    N, K = w.shape
+    q = np.zeros((N, K), np.int8)
+    s_bits = np.zeros(N, np.uint16)
+    for n in range(N):
+        amax = F32(0)
+        for k in range(K):
+            amax = max(amax, abs(w[n, k]))
+        s = F32(max(F32(amax / F32(127)), F32(1e-12)))
+        sb = int(torch.tensor([float(s)], dtype=torch.float32).to(torch.bfloat16).view(torch.int16).item()) & 0xFFFF
+        s_bits[n] = sb
+        sv = np.array([sb << 16], np.uint32).view(F32)[0]
+        for k in range(K):
+            r = F32(w[n, k] / sv)
+            # round half to even by hand
+            f = np.floor(r)
+            d = r - f
+            v = f + 1 if d > 0.5 or (d == 0.5 and int(f) % 2 == 1) else f
+            q[n, k] = int(min(127, max(-127, v)))
+    return q, s_bits
+
+
+def test_quantize_rowwise_brute_force():
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((6, 64)) * 0.02).astype(F32)
+    w[1] = 0.0  # all-zero row -> scale clamps to 1e-12, q = 0
+    w[2, :4] = [F32(127 * 0.001), F32(-0.0005), F32(0.0015), F32(0.0025)]  # ties after division
+    q, s = O.quantize_rowwise(w)
+    qb, sb = _brute_rowwise(w)
+    assert np.array_equal(s, sb)
+    assert np.array_equal(q, qb)
+    assert np.all(q[1] == 0)
+
+
+def test_quantize_rowwise_ties_round_to_even():
+    # scale exactly 1.0 (max 127): w/s lands on .5 ties
+    w = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5] + [0.0] * 56], dtype=F32)
+    q, s = O.quantize_rowwise(w)
+    assert O.bf16_to_f32(s)[0] == 1.0
+    assert list(q[0, :8]) == [127, 0, 2, 2, 0, -2, -2, 4]
+
+
+def test_quantize_rowwise_clamps_when_scale_rounds_down():
+    # max|w|/127 rounds down in bf16 -> the max element exceeds 127 * s and clamps to 127
+    amax = F32(1.0) + F32(2 ** -12)
+    w = np.zeros((1, 512), F32)
+    w[0, 0] = amax
+    w[0, 1] = -amax
+    q, s = O.quantize_rowwise(w)
+    assert q[0, 0] == 127 and q[0, 1] == -127
+
+
+def test_quantize_g32_matches_brute_force():
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal((4, 128)) * 0.05).astype(F32)
+    w[0, :32] = 0.0  # zero group -> fp16 scale underflows to 0, defined q = 0
+    q, s = O.quantize_g32(w)
+    for n in range(4):
+        for gi in range(4):
+            g = w[n, 32 * gi:32 * gi + 32]
+            sc = np.float16(max(F32(np.abs(g).max() / F32(127)), F32(1e-12)))
+            assert s[n, gi] == np.array([sc], np.float16).view(np.uint16)[0]
+            for k in range(32):
+                if float(sc) == 0.0:
+                    expect = 0
+                else:
+                    expect = int(np.clip(np.rint(F32(g[k] / F32(sc))), -127, 127))
+                assert q[n, 32 * gi + k] == expect
+    assert np.all(q[0, :32] == 0)
+
+
+@pytest.mark.parametrize("wd", ["i8row", "i8g32", "bf16", "f32"])
+def test_lin_quantisation_matches_oracle_bit_exact(wd):
+    from sokutou_amd.kernels import _Lin
+
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((64, 1024)) * 0.02).astype(F32)
+    w[5] = 0.0
+    lin = _Lin(torch.from_numpy(w), wd)
+    qo, so, deq = O.quantize(w, wd)
+    if wd in ("i8row", "i8g32"):
+        assert np.array_equal(lin.w.numpy(), qo)
+        assert np.array_equal(lin.s.numpy().view(np.uint16), so)
+    elif wd == "bf16":
+        assert np.array_equal(lin.w.view(torch.int16).numpy().view(np.uint16), qo)
+    else:
+        assert np.array_equal(lin.w.numpy(), qo)
+    assert np.array_equal(lin.dequant().numpy(), deq)
+
+
+def test_dequant_exact_in_fp32():
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((8, 512)) * 0.02).astype(F32)
+    q, s = O.quantize_rowwise(w)
+    d64 = q.astype(np.float64) * O.bf16_to_f32(s).astype(np.float64)[:, None]
+    assert np.array_equal(O.dequant_rowwise(q, s).astype(np.float64), d64)
+
+
+# ---- RoPE table, norms, GEMV ----------------------------------------------------------------------------------
+def test_rope_table_closed_form_and_hf_inv_freq():
+    from transformers import Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RotaryEmbedding
+
+    s = syn.shape("0.6b")
+    inv = syn.inv_freq(s)
+    cfg = Qwen3Config(hidden_size=1024, num_attention_heads=16, num_key_value_heads=8, head_dim=128,
+                      rope_parameters={"rope_type": "default", "rope_theta": 1e6})
+    hf_inv, scaling = Qwen3RotaryEmbedding.compute_default_rope_parameters(cfg)
+    assert scaling == 1.0 and np.array_equal(hf_inv.numpy(), inv)
+    tab = O.rope_table(inv, 600)
+    f = (np.arange(600, dtype=F32)[:, None] * inv[None, :]).astype(np.float64)
+    assert np.array_equal(tab[:, :64], np.cos(f).astype(F32))
+    assert np.array_equal(tab[:, 64:], np.sin(f).astype(F32))
+    # the engine's torch table agrees to 2 ulp
+    ft = torch.arange(600, dtype=torch.float32)[:, None] * torch.from_numpy(inv)[None, :]
+    tt = torch.cat([ft.cos(), ft.sin()], 1).numpy()
+    assert np.max(np.abs(tt - tab)) <= 2 * np.spacing(F32(1.0))
+
+
+def test_rmsnorm_and_rms_gemv_against_float64():
+    rng = np.random.default_rng(5)
+    K, N = 512, 64
+    h = rng.standard_normal(K).astype(F32)
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(F32)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(F32)
+    h64, nw64, W64 = h.astype(np.float64), nw.astype(np.float64), W.astype(np.float64)
+    inv = 1 / np.sqrt(np.mean(h64 ** 2) + 1e-6)
+    np.testing.assert_allclose(O.rmsnorm(h, nw, 1e-6), h64 * inv * nw64, rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(O.rms_gemv(h, nw, 1e-6, W), W64 @ (h64 * nw64) * inv, rtol=1e-5, atol=1e-6)
+    y = W64 @ (h64 * nw64) * inv
+    g, u = y[0::2], y[1::2]
+    np.testing.assert_allclose(O.rms_gemv(h, nw, 1e-6, W, swiglu=True), g / (1 + np.exp(-g)) * u, rtol=1e-5, atol=1e-6)
+    x = rng.standard_normal(K).astype(F32)
+    b = rng.standard_normal(N).astype(F32)
+    acc = rng.standard_normal(N).astype(F32)
+    np.testing.assert_allclose(O.gemv(x, W, b, acc), W64 @ x + b + acc, rtol=1e-5, atol=1e-6)
+
+
+# ---- attention ----------------------------------------------------------------------------------------------
+def _rand_attn_inputs(seed, nq=4, nkv=2, T=9, max_len=16):
+    rng = np.random.default_rng(seed)
+    qkv = rng.standard_normal((nq + 2 * nkv) * 128).astype(F32)
+    qn = (1 + 0.1 * rng.standard_normal(128)).astype(F32)
+    kn = (1 + 0.1 * rng.standard_normal(128)).astype(F32)
+    Kc = O.bf16_round(rng.standard_normal((nkv, max_len, 128)).astype(F32))
+    Vc = O.bf16_round(rng.standard_normal((nkv, max_len, 128)).astype(F32))
+    rope = O.rope_table(syn.inv_freq(syn.shape("tiny")), max_len)
+    return qkv, qn, kn, Kc, Vc, rope
+
+
+def test_attention_single_position_returns_v():
+    qkv, qn, kn, Kc, Vc, rope = _rand_attn_inputs(6)
+    out = O.attention(qkv, qn, kn, 1e-6, rope, Kc, Vc, 0, 4, 2).reshape(4, 128)
+    v = O.bf16_round(qkv[(4 + 2) * 128:].reshape(2, 128))
+    for h in range(4):
+        np.testing.assert_array_equal(out[h], v[h // 2])
+    # the new K was stored rounded at position 0
+    assert np.array_equal(Kc[:, 0], O.bf16_round(Kc[:, 0]))
+
+
+def test_attention_uniform_keys_average_values():
+    qkv, qn, kn, Kc, Vc, rope = _rand_attn_inputs(7, T=9)
+    pos = 8
+    k = qkv[4 * 128:6 * 128].reshape(2, 128)
+    # make every prior key equal to the (normalised, rotated, rounded) new key -> all scores equal
+    kk = O._rot(O._head_norm(k, kn, 1e-6), rope[pos, :64], rope[pos, 64:])
+    Kc[:, :pos] = O.bf16_round(kk)[:, None, :]
+    out = O.attention(qkv, qn, kn, 1e-6, rope, Kc, Vc, pos, 4, 2).reshape(4, 128)
+    for h in range(4):
+        np.testing.assert_allclose(out[h], Vc[h // 2, :pos + 1].mean(0), rtol=1e-5, atol=1e-6)
+
+
+def _hf_layer(s, w):
+    from transformers import Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3DecoderLayer, Qwen3RotaryEmbedding
+
+    cfg = Qwen3Config(hidden_size=s.hidden, intermediate_size=s.inter, num_attention_heads=s.nq,
+                      num_key_value_heads=s.nkv, head_dim=s.head_dim, rms_norm_eps=s.eps, num_hidden_layers=1,
+                      rope_parameters={"rope_type": "default", "rope_theta": s.theta}, attention_bias=False)
+    cfg._attn_implementation = "eager"
+    layer = Qwen3DecoderLayer(cfg, 0).float().eval()
+    a, m = layer.self_attn, layer.mlp
+    with torch.no_grad():
+        for mod, key in ((a.q_proj, "q"), (a.k_proj, "k"), (a.v_proj, "v"), (a.o_proj, "o"), (m.gate_proj, "gate"),
+                         (m.up_proj, "up"), (m.down_proj, "down"), (a.q_norm, "q_norm"), (a.k_norm, "k_norm"),
+                         (layer.input_layernorm, "in_norm"), (layer.post_attention_layernorm, "post_norm")):
+            mod.weight.copy_(torch.from_numpy(w[key]))
+    return layer, Qwen3RotaryEmbedding(cfg)
+
+
+def _oracle_layer_weights(w):
+    gu = np.stack([w["gate"], w["up"]], axis=1).reshape(-1, w["gate"].shape[1])
+    return {"qkv": np.concatenate([w["q"], w["k"], w["v"]]), "o": w["o"], "gu": gu, "down": w["down"],
+            "in_norm": w["in_norm"], "post_norm": w["post_norm"], "qn": w["q_norm"], "kn": w["k_norm"]}
+
+
+@pytest.mark.parametrize("T", [1, 5, 33])
+def test_decoder_layer_matches_transformers(T):
+    """f32 cache (the reference's ACT_F32 mode): the oracle layer equals transformers' Qwen3DecoderLayer
+    (eager attention) fed the same prior K/V, to fp32 rounding."""
+    from transformers import DynamicCache
+
+    s = syn.shape("tiny")
+    w = syn.layer_weights(11, 0, s)
+    layer, rot = _hf_layer(s, w)
+    rng = np.random.default_rng(12)
+    pos = T - 1
+    max_len = 40
+    Kp = rng.standard_normal((s.nkv, max_len, 128)).astype(F32)
+    Vp = rng.standard_normal((s.nkv, max_len, 128)).astype(F32)
+    h = rng.standard_normal(s.hidden).astype(F32)
+    rope = O.rope_table(syn.inv_freq(s), max_len)
+    Kc, Vc = Kp.copy(), Vp.copy()
+    ours = O.decoder_layer(h, _oracle_layer_weights(w), s.eps, rope, Kc, Vc, pos, s.nq, s.nkv, cache_bf16=False)
+    cache = DynamicCache()
+    if pos > 0:
+        cache.update(torch.from_numpy(Kp[None, :, :pos].copy()), torch.from_numpy(Vp[None, :, :pos].copy()), 0)
+    x = torch.from_numpy(h)[None, None, :]
+    pid = torch.tensor([[pos]])
+    with torch.no_grad():
+        cos, sin = rot(x, pid)
+        ref = layer(x, attention_mask=None, position_ids=pid, past_key_values=cache, use_cache=True,
+                    position_embeddings=(cos, sin))[0, 0].numpy()
+    err = np.max(np.abs(ours - ref)) / np.max(np.abs(ref))
+    assert err < 2e-6, err
+    # and the stored key/value of the new position equal transformers' cache entries
+    kh, vh = cache.layers[0].keys[0, :, pos].numpy(), cache.layers[0].values[0, :, pos].numpy()
+    np.testing.assert_allclose(Kc[:, pos], kh, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(Vc[:, pos], vh, rtol=1e-5, atol=1e-6)
+
+
+# ---- processor and argmax -----------------------------------------------------------------------------------
+def test_argmax_first_rules():
+    assert O.argmax_first(np.array([1, 3, 3, 2], F32)) == 1
+    assert O.argmax_first(np.array([np.nan, 1, np.nan, 1], F32)) == 1
+    assert O.argmax_first(np.full(5, -np.inf, F32)) == 0
+    assert O.argmax_first(np.full(5, np.nan, F32)) == 0
+    assert O.argmax_first(np.array([-np.inf, -5, -np.inf], F32)) == 1
+
+
+def test_process_logits_matches_torch_processor():
+    rng = np.random.default_rng(13)
+    V, eos = 3072, 2150
+    for trial in range(50):
+        lg = (rng.standard_normal(V) * 3).astype(F32)
+        seen = rng.random(V) < 0.05
+        sup = np.zeros(V, bool)
+        sup[V - 1024:] = True
+        sup[eos] = False
+        ngen = trial % 4
+        ours = O.process_logits(lg, seen, 1.05, sup, ngen, 2, eos)
+        t = torch.from_numpy(lg)[None]
+        ts = torch.from_numpy(seen)[None]
+        ref = torch.where(ts, torch.where(t < 0, t * 1.05, t / 1.05), t).masked_fill(torch.from_numpy(sup)[None], -np.inf)
+        if ngen < 2:
+            ref[0, eos] = -np.inf
+        np.testing.assert_array_equal(ours, ref[0].numpy())
+        assert O.argmax_first(ours) == int(torch.argmax(ref))
