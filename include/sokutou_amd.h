@@ -99,6 +99,72 @@ int sk_sample(const float* logits, int V, float inv_temp, int top_k, int do_samp
               const uint8_t* suppress, int64_t* ngen, int min_new, int eos, const uint64_t* seed, uint64_t* counter,
               int64_t* out, int talker, int64_t* id0, int64_t* pos, void* stream);
 
+/* ---- whole frames in one launch ------------------------------------------------------------------------- */
+
+/* One decoder layer's device pointers (i8row weights: int8 [N,K] + bf16 scale per row). kc/vc are this
+ * layer's caches [nkv][max_len][128] bf16. */
+typedef struct sk_layer_desc {
+  const void* qkv_w;        /* [(nq + 2 nkv) * 128, H], q rows then k rows then v rows */
+  const uint16_t* qkv_s;
+  const void* o_w;          /* [H, nq * 128] */
+  const uint16_t* o_s;
+  const void* gu_w;         /* [2 I, H], row 2n gate n, row 2n + 1 up n */
+  const uint16_t* gu_s;
+  const void* down_w;       /* [H, I] */
+  const uint16_t* down_s;
+  const float* in_norm;     /* [H] */
+  const float* post_norm;   /* [H] */
+  const float* qn;          /* [128] */
+  const float* kn;          /* [128] */
+  void* kc;
+  void* vc;
+} sk_layer_desc;
+
+/* A talker and its frame state, all device pointers. `layers` is a device array of n_layers descriptors.
+ * id0 / pos / next_id0 / ngen / seen are the reference's frame state (qwen3/fast.py:99-106); out (optional)
+ * receives the id chosen in each frame; logits (optional) the raw logits of the last frame; layer_out (optional,
+ * [n_layers][H]) the residual after every layer of the last frame. */
+typedef struct sk_talker_desc {
+  int n_layers, hidden, inter, nq, nkv, vocab, max_len, wd, ct;
+  float eps;
+  const sk_layer_desc* layers;
+  const float* norm;        /* final RMSNorm weight [H] */
+  const void* head_w;       /* codec head [vocab, H] */
+  const uint16_t* head_s;
+  const void* emb;          /* input embedding table [vocab, H] bf16 */
+  const float* rope;        /* [max_len][cos 64 | sin 64] */
+  int64_t* id0;
+  int64_t* pos;
+  int64_t* next_id0;
+  int64_t* out;
+  uint8_t* seen;
+  int64_t* ngen;
+  const uint8_t* suppress;
+  float rep_pen;
+  int min_new;
+  int eos;
+  int talker_processor;     /* 1: repetition penalty / suppression / EOS block before the argmax */
+  float* logits;
+  float* layer_out;
+  void* workspace;
+  int64_t workspace_bytes;
+} sk_talker_desc;
+
+/* Bytes of workspace sk_talker_frames needs. It must be zero before the first call and must be zeroed again
+ * after a call that reported an error (its first 4 bytes hold the error code, 0 when healthy). */
+int64_t sk_talker_workspace_size(int hidden, int inter);
+
+/* n_frames greedy talker frames in ONE launch: for each frame, embedding row of id0 -> n_layers decoder layers
+ * -> final RMSNorm -> codec head -> (processor) -> argmax -> next id, with the frame state advanced on the
+ * device exactly as the fused sampler advances it (id0, next_id0, seen, ngen, pos += 1 per frame).
+ * 256 persistent workgroups (one per CU, grouped by XCD: kv head x on XCD x) exchange activations through the
+ * workspace. Supports the 0.6B (H 1024, I 3072) and 1.7B (H 2048, I 6144) talkers: 16 q / 8 kv heads, vocab
+ * 3072, i8row weights, bf16 cache, max_len <= 2048, a 256-CU device.
+ * Replaces, for greedy decoding, the talker half of Qwen3Kernels._frame (qwen3/kernels.py:676-685): talker_in /
+ * embed, _layers (rms_gemv, attn, gemv, rms_gemv, gemv per layer, qwen3/kernels.py:619-627), rmsnorm, gemv
+ * (codec_head) and sample (qwen3/sampler.py:37-159 with do_sample = 0). */
+int sk_talker_frames(const sk_talker_desc* desc, int n_frames, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

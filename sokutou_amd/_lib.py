@@ -37,6 +37,28 @@ _SIGS = {
                           _P, _P]),
 }
 
+
+
+class SkLayerDesc(ctypes.Structure):
+    """Mirror of ``sk_layer_desc`` (include/sokutou_amd.h)."""
+    _fields_ = [(n, c_void_p) for n in ("qkv_w", "qkv_s", "o_w", "o_s", "gu_w", "gu_s", "down_w", "down_s", "in_norm",
+                                        "post_norm", "qn", "kn", "kc", "vc")]
+
+
+class SkTalkerDesc(ctypes.Structure):
+    """Mirror of ``sk_talker_desc`` (include/sokutou_amd.h)."""
+    _fields_ = [("n_layers", c_int), ("hidden", c_int), ("inter", c_int), ("nq", c_int), ("nkv", c_int),
+                ("vocab", c_int), ("max_len", c_int), ("wd", c_int), ("ct", c_int), ("eps", c_float),
+                ("layers", c_void_p), ("norm", c_void_p), ("head_w", c_void_p), ("head_s", c_void_p), ("emb", c_void_p),
+                ("rope", c_void_p), ("id0", c_void_p), ("pos", c_void_p), ("next_id0", c_void_p), ("out", c_void_p),
+                ("seen", c_void_p), ("ngen", c_void_p), ("suppress", c_void_p), ("rep_pen", c_float),
+                ("min_new", c_int), ("eos", c_int), ("talker_processor", c_int), ("logits", c_void_p),
+                ("layer_out", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_int64)]
+
+
+_SIGS["sk_talker_workspace_size"] = (c_int64, [c_int, c_int])
+_SIGS["sk_talker_frames"] = (c_int, [ctypes.POINTER(SkTalkerDesc), c_int, _P])
+
 _lib = None
 
 

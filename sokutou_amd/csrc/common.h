@@ -148,3 +148,27 @@ __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
+
+// ---- device-coherent scalar accesses (sc1: visible to every XCD without an L2 writeback/invalidate) -------
+__device__ __forceinline__ float ld_dev(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// ---- buffer accesses with an explicit cache policy ----------------------------------------------------------
+// `base` must be uniform across the wave (it becomes the SGPR buffer resource); per-lane offsets are in bytes.
+// kPolDev (sc1) makes a load or store coherent at device scope, across all XCDs, without any L2 writeback or
+// invalidate instruction.
+constexpr int kPolDev = 16;
+constexpr int kPolStream = 2;  // nt
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7fffffff, 0x00020000);
+}
+template <int POL = kPolDev>
+__device__ __forceinline__ float buf_ldf(const void* base, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(base), off, 0, POL));
+}
+template <int POL = kPolDev>
+__device__ __forceinline__ void buf_stf(void* base, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), make_rsrc(base), off, 0, POL);
+}

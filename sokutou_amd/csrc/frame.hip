@@ -1,0 +1,784 @@
+// Persistent talker decode kernel: whole frames (28 layers + final norm + codec head + greedy pick + next
+// embedding) in one launch of 256 workgroups, one per CU.
+//
+// It computes what the five per-layer launches of the reference compute (qwen3/kernels.py:619-627, frame order
+// 676-685, with `embed` feeding the next token as in qwen3/kernels.py:642), but as a dataflow over the whole chip:
+//
+//  * XCD-aware placement. The talker has 8 kv heads and MI355X has 8 XCDs: kv head x is owned by the 32 workgroups
+//    of XCD x. Each workgroup learns its XCD from the hardware XCC_ID register and a dense rank 0..31 from an
+//    arrival counter (the block -> XCD assignment is round-robin with a start that moves between dispatches).
+//  * Stages of a layer, each a set of rows of one projection per workgroup:
+//      S1 qkv     rows of head x (q of heads 2x, 2x+1, k and v of head x), 16 per workgroup
+//      S2 attn    positions [t0, t1) of head x (the cache length split 32 ways), both q heads; unnormalised
+//                 partial (m, l, o) per workgroup; the owner of `pos` appends K/V to the cache
+//      S3 merge   dims [8r, 8r+8) of heads 2x, 2x+1: log-sum-exp merge of the 32 partials
+//      S4 o       H/256 rows of the output projection, added to the residual
+//      S5 gu      2I/256 interleaved gate/up rows with RMSNorm, silu(g)*u
+//      S6 down    H/256 rows of the down projection, added to the residual
+//    then per frame: head rows (with the talker processor) and a local argmax, and every workgroup reduces the
+//    256 candidates itself and loads the next embedding row.
+//  * Exchanges use 8-byte cells {value, epoch} written and read with device-coherent (sc1) accesses: a consumer
+//    polls the cells it needs until all carry the producer's epoch. A 64-bit aligned store is single-copy atomic,
+//    so data and readiness arrive together and no fence, flag or L2 writeback is needed.
+//  * Wave roles. Waves 0..W-1 compute; wave W (the control wave) does all polling and copies inputs into LDS.
+//    The compute waves issue only weight and K/V loads: as soon as a stage's registers are consumed, the same
+//    registers are reloaded with that stage's weights of the next layer, so the HBM stream runs a full layer
+//    ahead of the dependency chain. The hardware waits for loads in issue order per wave, which is why polling
+//    (whose completion time is unknown) lives in a wave that has no prefetches queued.
+//  * Every wait is bounded. A timeout or an inconsistent placement sets an error word in the workspace; every
+//    poll also watches that word, so all workgroups leave promptly and the host reports the error.
+//
+// Numerics are those of the per-op kernels: fp32 residual and accumulation, bf16 K/V cache written round to
+// nearest even, per-row bf16 weight scales applied after the dot, RMSNorm scale applied after the dot.
+#include "common.h"
+#include "internal.h"
+
+namespace {
+
+constexpr int kXcd = 8, kPerXcd = 32, kWG = kXcd * kPerXcd;
+constexpr int kChunks = kPerXcd;           // attention split of the cache length per head
+constexpr int kPartN = 4 + 2 * SK_HD;      // m0 l0 m1 l1 o0[128] o1[128]
+constexpr int kNQ = 16, kNKV = 8, kQKV = (kNQ + 2 * kNKV) * SK_HD, kQ = kNQ * SK_HD;
+constexpr int kV = 3072;                   // codec vocabulary
+constexpr int kHeadRows = kV / kWG;        // 12
+constexpr uint32_t kSpinLimit = 1u << 19;
+constexpr float kInvSqrtHd = 0.08838834764831845f;
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11)) & 0xfu; }
+
+// ---- exchange cells ------------------------------------------------------------------------------------------
+__device__ __forceinline__ void put(void* cells, uint32_t idx, float v, uint32_t e) {
+  u32x2 x = {__float_as_uint(v), e};
+  __builtin_amdgcn_raw_buffer_store_b64(x, make_rsrc(cells), idx * 8u, 0, kPolDev);
+}
+__device__ __forceinline__ u32x4 get2(const void* cells, uint32_t idx) {  // cells idx, idx+1
+  return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(cells), idx * 8u, 0, kPolDev);
+}
+__device__ __forceinline__ uint32_t ld_u32_dev(const void* base, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(base), off, 0, kPolDev);
+}
+__device__ __forceinline__ void st_u32_dev(void* base, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, make_rsrc(base), off, 0, kPolDev);
+}
+
+// Workgroup barrier that does not wait for outstanding global loads (the compute waves keep their weight
+// prefetches in flight across it); it only makes this wave's LDS writes visible first.
+__device__ __forceinline__ void wg_sync() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt untouched
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// ---- layout of the workspace (bytes) -------------------------------------------------------------------------
+struct Ws {
+  // control words
+  static constexpr uint32_t kErr = 0, kTick = 4, kLaunch = 8, kDiag = 16, kCensus = 64;  // census: 8 counters
+  static constexpr uint32_t kCells = 256;
+};
+
+struct Layout {
+  uint32_t e1, e2, e3, e4, e5, e6, e7, total;  // cell offsets (in cells) from the cell base
+  __host__ __device__ Layout(int H, int I) {
+    e1 = 0;                                    // qkv        [8][512]
+    e2 = e1 + kNKV * 512;                      // partials   [8][32][260]
+    e3 = e2 + kNKV * kChunks * kPartN;         // att        [2048]
+    e4 = e3 + kQ;                              // h after o  [H]
+    e5 = e4 + H;                               // act        [I]
+    e6 = e5 + I;                               // h after down [H]
+    e7 = e6 + H;                               // candidates [256][2]
+    total = e7 + kWG * 2;
+  }
+};
+
+}  // namespace
+
+// Descriptor layouts shared with the host (declared in sokutou_amd.h).
+static_assert(sizeof(sk_layer_desc) == 14 * sizeof(void*), "sk_layer_desc layout");
+
+namespace {
+
+// Order-preserving key of (value, index): larger value wins, then the lower index.
+__device__ __forceinline__ uint64_t pick_key(float v, int i) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)k << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+}
+
+template <int H, int I, int W>
+struct Cfg {
+  static constexpr int R_O = H / kWG, R_GU = 2 * I / kWG, R_D = H / kWG;
+  static constexpr int RW_QKV = 16 / W;                       // rows per compute wave
+  static constexpr int RW_O = (R_O + W - 1) / W, RW_GU = R_GU / W, RW_D = (R_D + W - 1) / W;
+  static constexpr int RW_HEAD = (kHeadRows + W - 1) / W;
+  static constexpr int CH = H / 1024, CQ = kQ / 1024, CI = I / 1024;  // 16-byte chunks per lane per row
+  static constexpr int KVL = 2;                                // K (and V) loads per lane
+  static constexpr int kMaxChunk = 4 * W * KVL;                // positions per attention workgroup: 32 / 64
+  static constexpr int kMaxLen = kMaxChunk * kChunks;          // 1024 / 2048
+  static_assert(16 % W == 0 && R_GU % W == 0 && R_GU % 2 == 0, "row split");
+};
+
+// LDS of the frame kernel
+template <int H, int I, int W>
+struct Lds {
+  static constexpr int XS = I > kQ ? I : kQ;
+  float hin[H];        // residual entering the layer (S1; read back by S4), or the final residual (head)
+  float hmid[H];       // residual after the o projection (S5; read back by S6)
+  float xs[2][XS];     // staged GEMV inputs, alternating so the control wave can fill the next stage's input
+                       // while the compute waves still read the current one: [0] S1/S5/head, [1] S4/S6
+  float qkv[512];      // S2: q0 | q1 | k | v of this workgroup's head
+  float qs[2][SK_HD];  // normalised, rotated, scaled q
+  float kn[SK_HD], vn[SK_HD];
+  float sc[2][Cfg<H, I, W>::kMaxChunk];
+  float red[32];
+  float opart[W][4][16][17];
+  float mrg[kChunks][10];  // S3 inputs per chunk: m, l, o[8] of one q head
+  float inv;
+  uint64_t cand[W];
+  int flags[8];
+  int64_t tok;
+};
+
+// Records a timeout: error code, then frame and layer of the stage that gave up (diagnostic words of the workspace).
+struct Ctx;
+__device__ void fail(const Ctx& c, uint32_t code, int f, int l);
+
+// ---- control wave: poll cells into LDS ---------------------------------------------------------------------
+// Waits until cells [idx0, idx0 + n) (n even, idx0 even) all carry epoch e, copying the values to dst.
+// Returns false on timeout or when the global error word is set.
+template <int MAXB>
+__device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, float* dst, void* ws, int lane,
+                           const Ctx& c, uint32_t code, int f, int l) {
+  for (uint32_t spin = 0;; spin++) {
+    bool ok = true;
+    for (int base = 0; base < n; base += 128 * MAXB) {
+      u32x4 q[MAXB];
+#pragma unroll
+      for (int b = 0; b < MAXB; b++) {
+        const int i = base + 128 * b + 2 * lane;
+        if (i < n) q[b] = get2(cells, idx0 + i);
+      }
+#pragma unroll
+      for (int b = 0; b < MAXB; b++) {
+        const int i = base + 128 * b + 2 * lane;
+        if (i < n) {
+          ok &= q[b].y == e && q[b].w == e;
+          dst[i] = __uint_as_float(q[b].x);
+          dst[i + 1] = __uint_as_float(q[b].z);
+        }
+      }
+    }
+    if (__all(ok)) return true;
+    if ((spin & 63) == 63) {
+      if (ld_u32_dev(ws, Ws::kErr) != 0) return false;
+      if (spin > kSpinLimit) {
+        if (lane == 0) fail(c, code, f, l);
+        return false;
+      }
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// ---- compute-wave GEMV pieces ------------------------------------------------------------------------------
+// A wave owns RW consecutive rows starting at row0 (wave-uniform); lane reads chunk lane + 64 c of each row.
+template <int RW, int C>
+__device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], const int8_t* W, int row0, int nvalid, int K, int lane) {
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const int row = r < nvalid ? row0 + r : row0;
+    const uint4* p = (const uint4*)(W + (size_t)row * K);
+#pragma unroll
+    for (int c = 0; c < C; c++) w[r][c] = ld_stream(p + lane + 64 * c);
+  }
+}
+// y[r] = (row r) . xs, reduced over the wave (uniform result), without the row scale
+template <int RW, int C>
+__device__ __forceinline__ void dot_rows(const uint4 (&w)[RW][C], const float* xs, int lane, float (&y)[RW]) {
+  float acc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; r++) acc[r] = 0.f;
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+    const float* xp = xs + 16 * (lane + 64 * c);
+#pragma unroll
+    for (int r = 0; r < RW; r++) acc[r] += dot_i8x16(w[r][c], xp);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; r++) y[r] = wave_sum(acc[r]);
+}
+__device__ __forceinline__ float row_scale_u(const uint16_t* S, int row) {
+  return bf2f(S[__builtin_amdgcn_readfirstlane(row)]);
+}
+
+// Position bookkeeping of a frame for this workgroup's attention chunk.
+struct Chunk {
+  int T, pos, t0, n;
+  __device__ Chunk(int pos_, int r) {
+    pos = pos_;
+    T = pos + 1;
+    const int ch = (T + kChunks - 1) / kChunks;
+    t0 = r * ch;
+    const int t1 = min(T, t0 + ch);
+    n = t1 > t0 ? t1 - t0 : 0;
+  }
+  __device__ bool has_pos() const { return n > 0 && t0 <= pos && pos < t0 + n; }
+};
+
+template <int W, int KVL>
+__device__ __forceinline__ void load_kv(uint4 (&kr)[KVL], uint4 (&vr)[KVL], const bf16_t* Kh, const bf16_t* Vh,
+                                        const Chunk& ck, int w, int g, int sl) {
+#pragma unroll
+  for (int i = 0; i < KVL; i++) {
+    const int jj = 4 * W * i + 4 * w + g;
+    if (jj < ck.n && ck.t0 + jj != ck.pos) {
+      const uint32_t off = (uint32_t)((ck.t0 + jj) * SK_HD + 8 * sl) * 2u;
+      kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(Kh), off, 0, kPolDev));
+      vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(Vh), off, 0, kPolDev));
+    } else {
+      kr[i] = make_uint4(0, 0, 0, 0);
+      vr[i] = make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void unpack8(uint4 a, float* o) {
+  o[0] = bf2f(a.x & 0xffffu); o[1] = bf2f(a.x >> 16); o[2] = bf2f(a.y & 0xffffu); o[3] = bf2f(a.y >> 16);
+  o[4] = bf2f(a.z & 0xffffu); o[5] = bf2f(a.z >> 16); o[6] = bf2f(a.w & 0xffffu); o[7] = bf2f(a.w >> 16);
+}
+
+// Everything a role function needs about this workgroup and launch.
+struct Ctx {
+  sk_talker_desc d;
+  void* ws;
+  char* cells;
+  uint32_t x;     // XCD = kv head
+  int r, g;       // rank in the XCD, global workgroup index
+  uint32_t base, tpf;
+  int pos0, n_frames, L;
+  __device__ uint32_t tick(int f, int l, int s) const {
+    return base + 1u + (uint32_t)f * tpf + (uint32_t)l * 8u + (uint32_t)s;
+  }
+  __device__ const bf16_t* kh(const sk_layer_desc& Ly) const { return (const bf16_t*)Ly.kc + (size_t)x * d.max_len * SK_HD; }
+  __device__ const bf16_t* vh(const sk_layer_desc& Ly) const { return (const bf16_t*)Ly.vc + (size_t)x * d.max_len * SK_HD; }
+};
+
+__device__ void fail(const Ctx& c, uint32_t code, int f, int l) {
+  st_u32_dev(c.ws, Ws::kDiag, code);
+  st_u32_dev(c.ws, Ws::kDiag + 4, (uint32_t)f);
+  st_u32_dev(c.ws, Ws::kDiag + 8, (uint32_t)l);
+  st_u32_dev(c.ws, Ws::kDiag + 12, (uint32_t)c.g);
+  __builtin_amdgcn_s_waitcnt(0);
+  st_u32_dev(c.ws, Ws::kErr, code);
+}
+
+// Barriers of the attention stage after its input has arrived (both roles execute the same count).
+__device__ __forceinline__ int attn_barriers(const Chunk& ck) { return 4 + (ck.n > 0 ? 4 : 0); }
+
+// ================================================================================================================
+// Control wave
+// ================================================================================================================
+template <int H, int I, int W>
+__device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
+  const Layout LY(H, I);
+  const float eps = c.d.eps;
+  const bf16_t* emb = (const bf16_t*)c.d.emb;
+  int64_t tok = c.d.id0[0];
+  for (int f = 0; f < c.n_frames; f++) {
+    const int pos = c.pos0 + f;
+    const Chunk ck(pos, c.r);
+    for (int l = 0; l < c.L; l++) {
+      const sk_layer_desc& Ly = c.d.layers[l];
+      // S1 input: embedding row (layer 0) or the previous layer's residual, times the input norm
+      bool ok = true;
+      if (l == 0) {
+        for (int i = lane; i < H; i += 64) S.hin[i] = bf2f(emb[(size_t)tok * H + i]);
+      } else {
+        ok = poll_cells<8>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
+      }
+      float ss = 0.f;
+      for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
+      ss = wave_sum(ss);
+      for (int i = lane; i < H; i += 64) S.xs[0][i] = S.hin[i] * Ly.in_norm[i];
+      if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[0] = !ok; }
+      wg_sync();
+      if (!ok) return;
+      // S2 input: this head's q/k/v
+      ok = poll_cells<4>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
+      if (lane == 0) S.flags[1] = !ok;
+      wg_sync();
+      if (!ok) return;
+      for (int b = 0; b < attn_barriers(ck); b++) wg_sync();
+      // S3: merge of the 32 chunk partials for q head 2x + r/16, dims [8 (r % 16), 8 (r % 16) + 8)
+      {
+        const uint32_t e = c.tick(f, l, 1);
+        const int mh = c.r >> 4, md0 = 8 * (c.r & 15);
+        for (uint32_t spin = 0;; spin++) {
+          bool good = true;
+          // per chunk 5 cell pairs: (m, l) of head mh, then 4 pairs of its o slice
+          for (int it = lane; it < kChunks * 5; it += 64) {
+            const int ch = it / 5, k = it % 5;
+            const uint32_t pb = LY.e2 + (c.x * kChunks + ch) * kPartN;
+            const uint32_t idx = k == 0 ? pb + 2 * mh : pb + 4 + mh * SK_HD + md0 + 2 * (k - 1);
+            const u32x4 q = get2(c.cells, idx);
+            good &= q.y == e && q.w == e;
+            S.mrg[ch][2 * k] = __uint_as_float(q.x);
+            S.mrg[ch][2 * k + 1] = __uint_as_float(q.z);
+          }
+          if (__all(good)) break;
+          if ((spin & 63) == 63) {
+            if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
+            if (spin > kSpinLimit) { if (lane == 0) fail(c, 13u, f, l); ok = false; break; }
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+        if (ok && lane < 8) {
+          float M = -INFINITY;
+          for (int ch = 0; ch < kChunks; ch++) M = fmaxf(M, S.mrg[ch][0]);
+          float Lw = 0.f, O = 0.f;
+          for (int ch = 0; ch < kChunks; ch++) {
+            const float mc = S.mrg[ch][0];
+            if (mc == -INFINITY) continue;
+            const float fct = expf(mc - M);
+            Lw = __builtin_fmaf(fct, S.mrg[ch][1], Lw);
+            O = __builtin_fmaf(fct, S.mrg[ch][2 + lane], O);
+          }
+          put(c.cells, LY.e3 + (2 * c.x + mh) * SK_HD + md0 + lane, Lw > 0.f ? O / Lw : 0.f, c.tick(f, l, 2));
+        }
+      }
+      // S4 input: the whole attention output
+      ok = ok && poll_cells<16>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
+      if (lane == 0) S.flags[2] = !ok;
+      wg_sync();
+      if (!ok) return;
+      // S5 input: residual after o, times the post-attention norm
+      ok = poll_cells<8>(c.cells, LY.e4, H, c.tick(f, l, 3), S.hmid, c.ws, lane, c, 15u, f, l);
+      ss = 0.f;
+      for (int i = lane; i < H; i += 64) { const float v = S.hmid[i]; ss += v * v; }
+      ss = wave_sum(ss);
+      for (int i = lane; i < H; i += 64) S.xs[0][i] = S.hmid[i] * Ly.post_norm[i];
+      if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[3] = !ok; }
+      wg_sync();
+      if (!ok) return;
+      // S6 input: the whole SwiGLU activation
+      ok = poll_cells<16>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+      if (lane == 0) S.flags[4] = !ok;
+      wg_sync();
+      if (!ok) return;
+    }
+    // head input: final residual times the final norm
+    bool ok = poll_cells<8>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
+    float ss = 0.f;
+    for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
+    ss = wave_sum(ss);
+    for (int i = lane; i < H; i += 64) S.xs[0][i] = S.hin[i] * c.d.norm[i];
+    if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[5] = !ok; }
+    wg_sync();
+    if (!ok) return;
+    wg_sync();  // candidates of the compute waves are in S.cand
+    if (lane == 0) {
+      uint64_t best = 0;
+      for (int i = 0; i < W; i++) best = S.cand[i] > best ? S.cand[i] : best;
+      const uint32_t e = c.tick(f, c.L, 0);
+      put(c.cells, LY.e7 + 2 * c.g, __uint_as_float((uint32_t)(best >> 32)), e);
+      put(c.cells, LY.e7 + 2 * c.g + 1, __uint_as_float((uint32_t)best), e);
+    }
+    // pick: reduce the 256 candidates
+    {
+      const uint32_t e = c.tick(f, c.L, 0);
+      uint64_t best = 0;
+      for (uint32_t spin = 0;; spin++) {
+        bool good = true;
+        best = 0;
+        for (int it = lane; it < kWG; it += 64) {
+          const u32x4 q = get2(c.cells, LY.e7 + 2 * it);
+          good &= q.y == e && q.w == e;
+          const uint64_t k = ((uint64_t)q.x << 32) | q.z;
+          best = k > best ? k : best;
+        }
+        if (__all(good)) break;
+        if ((spin & 63) == 63) {
+          if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
+          if (spin > kSpinLimit) { if (lane == 0) fail(c, 18u, f, c.L); ok = false; break; }
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t b = __shfl_xor(best, o);
+        best = b > best ? b : best;
+      }
+      tok = best ? (int64_t)(0xffffffffu - (uint32_t)best) : 0;
+      if (lane == 0) { S.tok = tok; S.flags[6] = !ok; }
+    }
+    wg_sync();
+    if (!ok) return;
+    if (c.g == 0 && lane == 0) {
+      // device-side frame state, as the sampler leaves it (qwen3/sampler.py:147-156)
+      if (c.d.out) c.d.out[f] = tok;
+      if (c.d.seen) {
+        // read back by later frames of this launch through device-coherent loads
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)1, make_rsrc(c.d.seen), (uint32_t)tok, 0, kPolDev);
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+    }
+  }
+  if (c.g == 0 && lane == 0) {
+    if (ld_u32_dev(c.ws, Ws::kErr) == 0) {
+      c.d.id0[0] = tok;
+      if (c.d.next_id0) c.d.next_id0[0] = tok;
+      c.d.pos[0] = c.pos0 + c.n_frames;
+      if (c.d.ngen) c.d.ngen[0] += c.n_frames;
+    }
+  }
+}
+
+// ================================================================================================================
+// Compute waves
+// ================================================================================================================
+template <int H, int I, int W>
+__device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int lane) {
+  using C = Cfg<H, I, W>;
+  const Layout LY(H, I);
+  const float eps = c.d.eps;
+  const int ag = lane >> 4, asl = lane & 15;
+  const int x = (int)c.x, r = c.r, g = c.g;
+  // S1 rows: 512 rows of head x (q of heads 2x, 2x+1, then k and v of head x), 16 per workgroup
+  int qkv_row0;
+  if (r < 16) qkv_row0 = 256 * x + 16 * r;
+  else if (r < 24) qkv_row0 = kQ + 128 * x + 16 * (r - 16);
+  else qkv_row0 = kQ + kNKV * 128 + 128 * x + 16 * (r - 24);
+  const int q_w0 = qkv_row0 + C::RW_QKV * cw;
+  const int o_w0 = C::R_O * g + C::RW_O * cw, o_wn = max(0, min(C::RW_O, C::R_O - C::RW_O * cw));
+  const int gu_w0 = C::R_GU * g + C::RW_GU * cw;
+  const int d_w0 = C::R_D * g + C::RW_D * cw, d_wn = max(0, min(C::RW_D, C::R_D - C::RW_D * cw));
+  const int h_w0 = kHeadRows * g + C::RW_HEAD * cw, h_wn = max(0, min(C::RW_HEAD, kHeadRows - C::RW_HEAD * cw));
+  // the attention thread mapping uses the first 256 compute threads: head p = t / 128, dim dd = t % 128
+  const int p = tid >> 7, dd = tid & 127;
+  const bool att_thread = tid < 256;
+
+  uint4 wq[C::RW_QKV][C::CH], wo[C::RW_O][C::CQ], wg[C::RW_GU][C::CH], wd[C::RW_D][C::CI];
+  uint4 kr[C::KVL], vr[C::KVL];
+  {
+    const sk_layer_desc& L0 = c.d.layers[0];
+    load_rows<C::RW_QKV, C::CH>(wq, (const int8_t*)L0.qkv_w, q_w0, C::RW_QKV, H, lane);
+    load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), Chunk(c.pos0, r), cw, ag, asl);
+    load_rows<C::RW_O, C::CQ>(wo, (const int8_t*)L0.o_w, o_w0, o_wn, kQ, lane);
+    load_rows<C::RW_GU, C::CH>(wg, (const int8_t*)L0.gu_w, gu_w0, C::RW_GU, H, lane);
+    load_rows<C::RW_D, C::CI>(wd, (const int8_t*)L0.down_w, d_w0, d_wn, I, lane);
+  }
+  const bool block_eos0 = c.d.talker_processor && c.d.ngen;
+  for (int f = 0; f < c.n_frames; f++) {
+    const int pos = c.pos0 + f;
+    const Chunk ck(pos, r);
+    for (int l = 0; l < c.L; l++) {
+      const sk_layer_desc& Ly = c.d.layers[l];
+      const bool last_layer = l == c.L - 1;
+      const sk_layer_desc& Ln = c.d.layers[last_layer ? 0 : l + 1];
+      const bool more = !last_layer || f + 1 < c.n_frames;
+      // ---- S1: qkv rows -----------------------------------------------------------------------------------
+      wg_sync();
+      if (S.flags[0]) return;
+      {
+        float y[C::RW_QKV];
+        dot_rows<C::RW_QKV, C::CH>(wq, S.xs[0], lane, y);
+        const float inv = S.inv;
+        if (lane == 0) {
+#pragma unroll
+          for (int i = 0; i < C::RW_QKV; i++)
+            put(c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r + C::RW_QKV * cw + i,
+                y[i] * row_scale_u(Ly.qkv_s, q_w0 + i) * inv, c.tick(f, l, 0));
+        }
+        if (more) load_rows<C::RW_QKV, C::CH>(wq, (const int8_t*)Ln.qkv_w, q_w0, C::RW_QKV, H, lane);
+      }
+      // ---- S2: attention over this workgroup's chunk ----------------------------------------------------
+      wg_sync();
+      if (S.flags[1]) return;
+      {
+        const bool has_pos = ck.has_pos();
+        float qv = 0.f, kv = 0.f, cs = 0.f, sn = 0.f;
+        if (att_thread) {
+          cs = c.d.rope[(size_t)pos * SK_HD + (dd & 63)];
+          sn = c.d.rope[(size_t)pos * SK_HD + 64 + (dd & 63)];
+          qv = S.qkv[p * SK_HD + dd];
+          kv = S.qkv[256 + p * SK_HD + dd];  // p 0: k, p 1: v
+        }
+        const float sqv = wave_sum(qv * qv), skv = wave_sum(kv * kv);
+        if (att_thread && lane == 0) { S.red[cw] = sqv; S.red[4 + cw] = skv; }
+        wg_sync();  // attention barrier 1
+        if (att_thread) {
+          S.qs[p][dd] = qv * rsqrtf((S.red[2 * p] + S.red[2 * p + 1]) / SK_HD + eps) * Ly.qn[dd];
+          if (p == 0) S.kn[dd] = kv * rsqrtf((S.red[4] + S.red[5]) / SK_HD + eps) * Ly.kn[dd];
+          else S.vn[dd] = bf2f(f2bf(kv));
+        }
+        wg_sync();  // 2
+        float qr = 0.f, krot = 0.f;
+        if (att_thread) {
+          qr = (S.qs[p][dd] * cs + (dd < 64 ? -S.qs[p][dd + 64] : S.qs[p][dd - 64]) * sn) * kInvSqrtHd;
+          if (p == 0) krot = bf2f(f2bf(S.kn[dd] * cs + (dd < 64 ? -S.kn[dd + 64] : S.kn[dd - 64]) * sn));
+        }
+        wg_sync();  // 3
+        if (att_thread) {
+          S.qs[p][dd] = qr;
+          if (p == 0) S.kn[dd] = krot;
+          if (has_pos) {
+            // append the new K/V at pos (device-coherent: later frames read it from other workgroups)
+            const uint32_t off = (uint32_t)(pos * SK_HD + dd) * 2u;
+            if (p == 0) __builtin_amdgcn_raw_buffer_store_b16(f2bf(krot), make_rsrc(c.kh(Ly)), off, 0, kPolDev);
+            else __builtin_amdgcn_raw_buffer_store_b16(f2bf(S.vn[dd]), make_rsrc(c.vh(Ly)), off, 0, kPolDev);
+          }
+        }
+        wg_sync();  // 4
+        float m = -INFINITY, lsum = 0.f, o = 0.f;
+        if (ck.n > 0) {
+          {
+            float q0[8], q1[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) { q0[e] = S.qs[0][8 * asl + e]; q1[e] = S.qs[1][8 * asl + e]; }
+#pragma unroll
+            for (int i = 0; i < C::KVL; i++) {
+              const int jj = 4 * W * i + 4 * cw + ag;
+              float k8[8];
+              if (jj < ck.n && ck.t0 + jj == pos) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) k8[e] = S.kn[8 * asl + e];
+              } else {
+                unpack8(kr[i], k8);
+              }
+              float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+              for (int e = 0; e < 8; e++) { s0 = __builtin_fmaf(q0[e], k8[e], s0); s1 = __builtin_fmaf(q1[e], k8[e], s1); }
+              s0 = row16_sum(s0);
+              s1 = row16_sum(s1);
+              if (asl == 0 && jj < ck.n) { S.sc[0][jj] = s0; S.sc[1][jj] = s1; }
+            }
+          }
+          wg_sync();  // 5
+          const float sv = (att_thread && dd < ck.n) ? S.sc[p][dd] : -INFINITY;
+          const float mx = wave_max(sv);
+          if (att_thread && lane == 0) S.red[8 + cw] = mx;
+          wg_sync();  // 6
+          const float mp = att_thread ? fmaxf(S.red[8 + 2 * p], S.red[8 + 2 * p + 1]) : 0.f;
+          const float ev = (att_thread && dd < ck.n) ? expf(sv - mp) : 0.f;
+          const float se = wave_sum(ev);
+          if (att_thread && dd < ck.n) S.sc[p][dd] = ev;
+          if (att_thread && lane == 0) S.red[12 + cw] = se;
+          wg_sync();  // 7
+          {
+            float a0[8], a1[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) { a0[e] = 0.f; a1[e] = 0.f; }
+#pragma unroll
+            for (int i = 0; i < C::KVL; i++) {
+              const int jj = 4 * W * i + 4 * cw + ag;
+              if (jj < ck.n) {
+                float v8[8];
+                if (ck.t0 + jj == pos) {
+#pragma unroll
+                  for (int e = 0; e < 8; e++) v8[e] = S.vn[8 * asl + e];
+                } else {
+                  unpack8(vr[i], v8);
+                }
+                const float e0 = S.sc[0][jj], e1 = S.sc[1][jj];
+#pragma unroll
+                for (int e = 0; e < 8; e++) { a0[e] = __builtin_fmaf(e0, v8[e], a0[e]); a1[e] = __builtin_fmaf(e1, v8[e], a1[e]); }
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) { S.opart[cw][ag][asl][e] = a0[e]; S.opart[cw][ag][asl][8 + e] = a1[e]; }
+          }
+          wg_sync();  // 8
+          if (att_thread) {
+            m = mp;
+            lsum = S.red[12 + 2 * p] + S.red[12 + 2 * p + 1];
+            for (int ww = 0; ww < W; ww++)
+#pragma unroll
+              for (int gg = 0; gg < 4; gg++) o += S.opart[ww][gg][dd >> 3][p * 8 + (dd & 7)];
+          }
+        }
+        // publish the partial: [m0 l0 m1 l1 | o0[128] | o1[128]]
+        if (att_thread) {
+          const uint32_t pb = LY.e2 + ((uint32_t)x * kChunks + r) * kPartN;
+          const uint32_t e = c.tick(f, l, 1);
+          if (dd == 0) { put(c.cells, pb + 2 * p, m, e); put(c.cells, pb + 2 * p + 1, lsum, e); }
+          put(c.cells, pb + 4 + p * SK_HD + dd, o, e);
+        }
+        if (more) load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), Chunk(last_layer ? pos + 1 : pos, r), cw, ag, asl);
+      }
+      // ---- S4: o projection rows, added to the layer's input residual ------------------------------------
+      wg_sync();
+      if (S.flags[2]) return;
+      {
+        float y[C::RW_O];
+        dot_rows<C::RW_O, C::CQ>(wo, S.xs[1], lane, y);
+        if (lane == 0) {
+#pragma unroll
+          for (int i = 0; i < C::RW_O; i++)
+            if (i < o_wn)
+              put(c.cells, LY.e4 + o_w0 + i, S.hin[o_w0 + i] + y[i] * row_scale_u(Ly.o_s, o_w0 + i), c.tick(f, l, 3));
+        }
+        if (more) load_rows<C::RW_O, C::CQ>(wo, (const int8_t*)Ln.o_w, o_w0, o_wn, kQ, lane);
+      }
+      // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
+      wg_sync();
+      if (S.flags[3]) return;
+      {
+        float y[C::RW_GU];
+        dot_rows<C::RW_GU, C::CH>(wg, S.xs[0], lane, y);
+        const float inv = S.inv;
+        if (lane == 0) {
+#pragma unroll
+          for (int i = 0; i < C::RW_GU; i += 2)
+            put(c.cells, LY.e5 + (gu_w0 + i) / 2,
+                silu_mul(y[i] * row_scale_u(Ly.gu_s, gu_w0 + i) * inv, y[i + 1] * row_scale_u(Ly.gu_s, gu_w0 + i + 1) * inv),
+                c.tick(f, l, 4));
+        }
+        if (more) load_rows<C::RW_GU, C::CH>(wg, (const int8_t*)Ln.gu_w, gu_w0, C::RW_GU, H, lane);
+      }
+      // ---- S6: down rows, added to the residual after o --------------------------------------------------
+      wg_sync();
+      if (S.flags[4]) return;
+      {
+        float y[C::RW_D];
+        dot_rows<C::RW_D, C::CI>(wd, S.xs[1], lane, y);
+        if (lane == 0) {
+#pragma unroll
+          for (int i = 0; i < C::RW_D; i++) {
+            if (i < d_wn) {
+              const float hv = S.hmid[d_w0 + i] + y[i] * row_scale_u(Ly.down_s, d_w0 + i);
+              put(c.cells, LY.e6 + d_w0 + i, hv, c.tick(f, l, 5));
+              if (c.d.layer_out && f == c.n_frames - 1) c.d.layer_out[(size_t)l * H + d_w0 + i] = hv;
+            }
+          }
+        }
+        if (more) load_rows<C::RW_D, C::CI>(wd, (const int8_t*)Ln.down_w, d_w0, d_wn, I, lane);
+      }
+    }
+    // ---- head rows (loaded now; the final residual is a full layer away), processor, local argmax ----------
+    uint4 wh[C::RW_HEAD][C::CH];
+    load_rows<C::RW_HEAD, C::CH>(wh, (const int8_t*)c.d.head_w, h_w0, h_wn, H, lane);
+    wg_sync();
+    if (S.flags[5]) return;
+    {
+      float y[C::RW_HEAD];
+      dot_rows<C::RW_HEAD, C::CH>(wh, S.xs[0], lane, y);
+      const float inv = S.inv;
+      const bool block_eos = block_eos0 && (c.d.ngen[0] + f) < c.d.min_new;
+      uint64_t best = 0;
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < C::RW_HEAD; i++) {
+          if (i >= h_wn) break;
+          const int row = h_w0 + i;
+          float v = y[i] * row_scale_u(c.d.head_s, row) * inv;
+          if (c.d.logits && f == c.n_frames - 1) c.d.logits[row] = v;
+          if (c.d.talker_processor) {
+            if (c.d.seen && ((ld_u32_dev(c.d.seen, (uint32_t)row & ~3u) >> (8 * (row & 3))) & 0xffu))
+              v = v < 0.f ? v * c.d.rep_pen : v / c.d.rep_pen;
+            if (c.d.suppress && c.d.suppress[row]) v = -INFINITY;
+            if (block_eos && row == c.d.eos) v = -INFINITY;
+          }
+          if (v == v) { const uint64_t k = pick_key(v, row); best = k > best ? k : best; }
+        }
+        S.cand[cw] = best;
+      }
+    }
+    wg_sync();  // candidates ready for the control wave
+    wg_sync();  // pick done
+    if (S.flags[6]) return;
+  }
+}
+
+template <int H, int I, int W>
+__global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n_frames) {
+  extern __shared__ char smem_raw[];
+  Lds<H, I, W>& S = *(Lds<H, I, W>*)smem_raw;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  void* ws = d.workspace;
+  // ---- placement: XCD from hardware, dense rank from an arrival counter ------------------------------------
+  __shared__ int s_rank;
+  __shared__ uint32_t s_base;
+  const uint32_t x = xcc_id();
+  if (tid == 0) {
+    const uint32_t launch = ld_u32_dev(ws, Ws::kLaunch);
+    const uint32_t old = __hip_atomic_fetch_add((uint32_t*)((char*)ws + Ws::kCensus + 4 * (x & 7)), 1u,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int r = (int)(old - launch * kPerXcd);
+    if (x >= kXcd || r < 0 || r >= kPerXcd) {
+      st_u32_dev(ws, Ws::kErr, 2u);
+      r = -1;
+    }
+    // every position this launch writes must lie inside the cache, and the start token inside the vocabulary
+    const int64_t pos0 = d.pos[0], tok0 = d.id0[0];
+    if (pos0 < 0 || pos0 + n_frames > d.max_len || tok0 < 0 || tok0 >= d.vocab) {
+      st_u32_dev(ws, Ws::kErr, 5u);
+      r = -1;
+    }
+    s_rank = r;
+    s_base = ld_u32_dev(ws, Ws::kTick);
+    for (int i = 0; i < 8; i++) S.flags[i] = 0;
+  }
+  __syncthreads();
+  const int r = s_rank;
+  if (r < 0) return;
+  Ctx c;
+  c.d = d;
+  c.ws = ws;
+  c.cells = (char*)ws + Ws::kCells;
+  c.x = x;
+  c.r = r;
+  c.g = (int)x * kPerXcd + r;
+  c.base = s_base;
+  c.tpf = (uint32_t)d.n_layers * 8u + 8u;
+  c.pos0 = (int)d.pos[0];
+  c.n_frames = n_frames;
+  c.L = d.n_layers;
+  if (wave == W) run_control<H, I, W>(c, S, lane);
+  else run_compute<H, I, W>(c, S, wave, tid, lane);
+  // ---- end of launch: epoch base and launch count (workgroup 0; every workgroup finished its census) --------
+  if (c.g == 0 && tid == 0) {
+    st_u32_dev(ws, Ws::kTick, c.base + (uint32_t)n_frames * c.tpf);
+    st_u32_dev(ws, Ws::kLaunch, ld_u32_dev(ws, Ws::kLaunch) + 1u);
+  }
+}
+template <int H, int I, int W>
+int launch_frames(const sk_talker_desc* d, int n_frames, hipStream_t st) {
+  if (d->max_len > Cfg<H, I, W>::kMaxLen) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: max_len too long");
+  const size_t lds = sizeof(Lds<H, I, W>) < 96 * 1024 ? 96 * 1024 : sizeof(Lds<H, I, W>);  // one workgroup per CU
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipFuncSetAttribute((const void*)k_frames<H, I, W>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_frames<H, I, W>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, n_frames);
+  return sk_check_launch(hipGetLastError(), "sk_talker_frames");
+}
+
+}  // namespace
+
+extern "C" int64_t sk_talker_workspace_size(int hidden, int inter) {
+  if (hidden <= 0 || inter <= 0) return 0;
+  const Layout LY(hidden, inter);
+  return (int64_t)Ws::kCells + (int64_t)LY.total * 8;
+}
+
+extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* stream) {
+  if (!d || n_frames <= 0) return sk_set_error(SK_EINVAL, "sk_talker_frames: bad arguments");
+  if (d->nq != kNQ || d->nkv != kNKV || d->vocab != kV || d->wd != SK_WD_I8ROW || d->ct != SK_CT_BF16)
+    return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs 16 q / 8 kv heads, vocab 3072, i8row, bf16 cache");
+  if (!d->layers || !d->norm || !d->head_w || !d->head_s || !d->emb || !d->rope || !d->id0 || !d->pos || !d->workspace)
+    return sk_set_error(SK_EINVAL, "sk_talker_frames: null pointer");
+  if (d->workspace_bytes < sk_talker_workspace_size(d->hidden, d->inter))
+    return sk_set_error(SK_EWORKSPACE, "sk_talker_frames: workspace too small");
+  int dev = 0, cus = 0;
+  hipGetDevice(&dev);
+  hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (cus != kWG) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs a 256-CU device (8 XCDs x 32)");
+  hipStream_t st = (hipStream_t)stream;
+  if (d->hidden == 1024 && d->inter == 3072) return launch_frames<1024, 3072, 4>(d, n_frames, st);
+  if (d->hidden == 2048 && d->inter == 6144) return launch_frames<2048, 6144, 8>(d, n_frames, st);
+  return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: shapes other than the 0.6B / 1.7B talker");
+}

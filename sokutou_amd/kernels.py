@@ -16,6 +16,7 @@ the primary format), ``i8g32`` (the reference's int8 + fp16 per-32 scale), ``bf1
 
 from __future__ import annotations
 
+import ctypes
 import time
 
 import torch
@@ -131,7 +132,7 @@ class Qwen3Kernels(Qwen3Fast):
 
     def __init__(self, tts, sampling: Sampling | None = None, max_cache: int = 1024, wd: str = "bf16",
                  graphs: bool = True, sampler: str = "fused", l2_keep_mb: float | None = None,
-                 cp_pair: bool | None = None, suppress_tail: int = 1024):
+                 cp_pair: bool | None = None, suppress_tail: int = 1024, frame_kernel: bool | None = None):
         super().__init__(tts, sampling, max_cache=max_cache, compile=False, graphs=graphs, suppress_tail=suppress_tail)
         if sampler not in ("fused", "torch"):
             raise ValueError(sampler)
@@ -179,6 +180,65 @@ class Qwen3Kernels(Qwen3Fast):
         nbytes = int(L.sk_attn_workspace_size(P.nq, P.nkv, max_cache))
         self.attn_ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         self.trace: list[torch.Tensor] | None = None
+        # whole frames in one persistent launch (greedy decoding of the 0.6B / 1.7B talker shapes)
+        supported = (self.frame_kernel_supported() and sampler == "fused" and not self.s.do_sample)
+        if frame_kernel and not supported:
+            raise ValueError("frame_kernel=True needs greedy decoding, i8row weights, 16 q / 8 kv heads, vocab 3072, "
+                             "hidden 1024 or 2048 and a cache of at most 1024 (0.6B) / 2048 (1.7B) positions")
+        self.frame_kernel = supported if frame_kernel is None else bool(frame_kernel)
+        if self.frame_kernel:
+            self._setup_frame_kernel()
+
+    # --- the persistent frame kernel ------------------------------------------------------------------------
+    def frame_kernel_supported(self) -> bool:
+        P = self.T
+        shapes = {(1024, 3072): 1024, (2048, 6144): 2048}
+        return (self.wd == "i8row" and self.ct == "bf16" and P.nq == 16 and P.nkv == 8 and self.V == 3072
+                and (P.H, P.I) in shapes and self.max_cache <= shapes[(P.H, P.I)])
+
+    def _setup_frame_kernel(self) -> None:
+        P = self.T
+        L = _lib.load()
+        arr = (_lib.SkLayerDesc * len(P.layers))()
+        for i, Ly in enumerate(P.layers):
+            arr[i] = _lib.SkLayerDesc(Ly["qkv"].w.data_ptr(), Ly["qkv"].s.data_ptr(), Ly["o"].w.data_ptr(),
+                                      Ly["o"].s.data_ptr(), Ly["gu"].w.data_ptr(), Ly["gu"].s.data_ptr(),
+                                      Ly["down"].w.data_ptr(), Ly["down"].s.data_ptr(), Ly["in_norm"].data_ptr(),
+                                      Ly["post_norm"].data_ptr(), Ly["qn"].data_ptr(), Ly["kn"].data_ptr(),
+                                      self.tk[i].data_ptr(), self.tv[i].data_ptr())
+        self._layer_desc = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8).to(self.device)
+        self.frame_ws = torch.zeros(int(L.sk_talker_workspace_size(P.H, P.I)), dtype=torch.uint8, device=self.device)
+        self.frame_ids = torch.zeros(4096, dtype=torch.int64, device=self.device)
+        self.layer_out: torch.Tensor | None = None
+        s = self.s
+        proc = s.repetition_penalty != 1.0 or self.suppress_tail != 0 or s.min_new_tokens > 0
+        self._desc = _lib.SkTalkerDesc(
+            n_layers=len(P.layers), hidden=P.H, inter=P.I, nq=P.nq, nkv=P.nkv, vocab=self.V, max_len=P.max_len,
+            wd=_lib.WD[self.wd], ct=_lib.CT[self.ct], eps=P.eps, layers=self._layer_desc.data_ptr(),
+            norm=P.norm.data_ptr(), head_w=self.codec_head.w.data_ptr(), head_s=self.codec_head.s.data_ptr(),
+            emb=self.temb.data_ptr(), rope=P.rope.data_ptr(), id0=self.id0.data_ptr(), pos=self.pos.data_ptr(),
+            next_id0=self.next_id0.data_ptr(), out=self.frame_ids.data_ptr(), seen=self.seen.data_ptr(),
+            ngen=self.ngen.data_ptr(), suppress=self.suppress.data_ptr() if self.suppress_tail else None,
+            rep_pen=s.repetition_penalty, min_new=s.min_new_tokens, eos=self.eos, talker_processor=int(proc),
+            logits=self.logit_t.data_ptr(), layer_out=None, workspace=self.frame_ws.data_ptr(),
+            workspace_bytes=self.frame_ws.numel())
+
+    def run_frames(self, n: int) -> None:
+        """``n`` greedy frames in one launch of sk_talker_frames; the chosen ids land in ``frame_ids[:n]``."""
+        if n > self.frame_ids.numel():
+            raise ValueError("at most 4096 frames per launch")
+        self._desc.layer_out = None if self.layer_out is None else self.layer_out.data_ptr()
+        _lib.check(_lib.load().sk_talker_frames(ctypes.byref(self._desc), int(n), _lib.stream()), "sk_talker_frames")
+
+    def frame_error(self) -> int:
+        """Error word of the frame kernel's workspace (0 when healthy; reads device memory, so it synchronises).
+        Codes: 2 placement, 5 position/token out of range, 11..18 a poll of stage S1, S2, S3, S4, S5, S6, head,
+        pick timed out (``frame_diag`` tells the frame, layer and workgroup)."""
+        return int(self.frame_ws[:4].view(torch.int32).item())
+
+    def frame_diag(self) -> dict:
+        w = self.frame_ws[16:32].view(torch.int32).tolist()
+        return {"code": w[0], "frame": w[1], "layer": w[2], "workgroup": w[3]}
 
     # --- launches -----------------------------------------------------------------------------------------
     def _rms_gemv(self, h, nw, eps, lin: _Lin, out, swiglu: bool) -> None:
@@ -228,6 +288,9 @@ class Qwen3Kernels(Qwen3Fast):
     def _frame(self) -> None:
         s = self.s
         self.codes[:, :1].copy_(self.id0)
+        if self.frame_kernel:
+            self.run_frames(1)
+            return
         self._talker()
         if self.fs is not None:
             # processor and the state update (next_id0, id0, seen, ngen, pos) happen inside the kernel

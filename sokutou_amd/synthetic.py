@@ -182,6 +182,8 @@ WORKLOADS = {
     "talker17b": dict(shape="1.7b", n_layers=28, kv=1024, frames=64),
     # tiny two-layer model for quick checks
     "tiny": dict(shape="tiny", n_layers=2, kv=24, frames=8),
+    # two 0.6B-shaped layers (the persistent frame kernel needs the real head counts)
+    "small06b": dict(shape="0.6b", n_layers=2, kv=40, frames=8),
 }
 
 
@@ -191,7 +193,7 @@ def workload_shape(name: str) -> TalkerShape:
 
 
 def make_engine(name: str, seed: int = 0, wd: str = "i8row", device="cuda", graphs: bool = True,
-                max_cache: int | None = None, frames: int | None = None):
+                max_cache: int | None = None, frames: int | None = None, frame_kernel: bool | None = False):
     """Builds a Qwen3Kernels engine over the seeded synthetic talker of workload ``name`` with the prior KV
     cache loaded and the frame state set at position ``kv``. Greedy decoding without the processor (plain
     argmax over the whole codec vocabulary). Returns (engine, start token)."""
@@ -204,7 +206,7 @@ def make_engine(name: str, seed: int = 0, wd: str = "i8row", device="cuda", grap
     max_cache = max_cache or (w["kv"] + frames + 1)
     tts = make_tts(seed, s, device=device)
     eng = Qwen3Kernels(tts, Sampling.greedy(processor=False), max_cache=max_cache, wd=wd, graphs=graphs,
-                       sampler="fused", suppress_tail=0)
+                       sampler="fused", suppress_tail=0, frame_kernel=frame_kernel)
     tts.model.talker = None  # the fp32 source weights are no longer needed once packed
     eng.talker = None
     del tts
