@@ -1,15 +1,19 @@
 """Talker decode benchmark on one MI355X: frames/s of the 0.6B-shaped int8 talker at batch 1, KV 512.
 
-    python bench.py [--steps K] [--warmup W] [--workload talker06b|talker17b] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload talker06b|talker17b] [--engine frames|graph|multi] [--no-cpu]
 
 A step is one greedy decode run of 64 frames starting at KV length 512 (positions 512..575 are rewritten on
-every step, so every step does identical work): each frame is one replay of the captured HIP graph
-(embed -> 28 x [rms_gemv qkv, attention, gemv o, rms_gemv gate/up, gemv down] -> rmsnorm -> codec head ->
-argmax). Weights are seeded random-init of the real architecture, int8 per output channel with bf16 scales
-(``i8row``); the KV cache is bf16. Inputs are resident in HBM before timing starts.
+every step, so every step does identical work). Each frame is embed -> 28 decoder layers (RMSNorm + qkv, q/k norm
++ RoPE + KV append + attention, o + residual, RMSNorm + gate/up + SwiGLU, down + residual) -> final RMSNorm ->
+codec head -> argmax, feeding the next frame. Engines:
+  frames  the persistent kernel sk_talker_frames: all 64 frames of a step in one launch (default)
+  graph   one captured HIP graph replay per frame, each holding one sk_talker_frames launch
+  multi   one captured HIP graph per frame of the per-op kernels (5 launches per layer)
+Weights are seeded random-init of the real architecture, int8 per output channel with bf16 scales (``i8row``);
+the KV cache is bf16. Inputs are resident in HBM before timing starts.
 
-Prints one JSON line with the metric, the roofline of the dominant kernel (algorithmic bytes per launch over
-its average duration, timed with HIP events on the launch stream) and the CPU oracle timed on this host.
+Prints one JSON line with the metric, the roofline of the dominant kernel (algorithmic bytes per launch over its
+average duration, timed with HIP events on the launch stream) and the CPU oracle timed on this host.
 """
 
 from __future__ import annotations
@@ -48,7 +52,7 @@ def algorithmic_bytes(s, T: int, wd: str = "i8row") -> dict:
 
 
 def time_kernels(eng, reps: int = 200) -> dict:
-    """Average duration of each launch kind of one layer, timed with HIP events on the launch stream."""
+    """Average duration of each per-op launch kind of one layer, timed with HIP events on the launch stream."""
     import torch
 
     P = eng.T
@@ -111,6 +115,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="talker06b", choices=["talker06b", "talker17b"])
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--engine", default="frames", choices=["frames", "graph", "multi"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -127,48 +132,85 @@ def main() -> None:
     spec = syn.WORKLOADS[name]
     frames = spec["frames"]
     t0 = time.perf_counter()
-    eng, tok = syn.make_engine(name, seed=args.seed, wd="i8row", device=dev)
-    eng.capture()
+    eng, tok = syn.make_engine(name, seed=args.seed, wd="i8row", device=dev, frame_kernel=args.engine != "multi")
+    if args.engine != "frames":
+        eng.capture()
     setup_s = time.perf_counter() - t0
     s = syn.workload_shape(name)
     pos0 = spec["kv"]
+    ev = []  # (start, end) events around the dominant launch of each timed step
 
-    def step():
+    def step(record: bool = False):
         eng.reset(pos0, tok)
-        for _ in range(frames):
-            eng.graph.replay()
+        if args.engine == "frames":
+            if record:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                eng.run_frames(frames)
+                e1.record()
+                ev.append((e0, e1))
+            else:
+                eng.run_frames(frames)
+        else:
+            for _ in range(frames):
+                eng.graph.replay()
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        step(record=True)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms_per_step = dt * 1e3 / args.steps
     fps = frames * args.steps / dt
+    if args.engine != "multi" and eng.frame_error():
+        raise RuntimeError(f"frame kernel error {eng.frame_diag()}")
 
     # correctness of the measured path: one more step, codes against the oracle fixture when present
     eng.reset(pos0, tok)
-    codes = []
-    for _ in range(frames):
-        eng.graph.replay()
-        codes.append(int(eng.next_id0.item()))
+    if args.engine == "frames":
+        eng.run_frames(frames)
+        codes = eng.frame_ids[:frames].cpu().tolist()
+    else:
+        codes = []
+        for _ in range(frames):
+            eng.graph.replay()
+            codes.append(int(eng.next_id0.item()))
     gold = ROOT / "tests" / "golden" / f"{name}_seed{args.seed}.json"
     parity = None
     if gold.exists():
         parity = codes == json.loads(gold.read_text())["codes"]
 
-    # bytes per frame summed over the attended lengths of the 64 frames
+    # algorithmic bytes per frame, summed over the attended lengths of the 64 frames
     ab = [algorithmic_bytes(s, pos0 + 1 + f) for f in range(frames)]
-    frame_bytes = sum(a["frame"] for a in ab) / frames
+    step_bytes = sum(a["frame"] for a in ab)
+    frame_bytes = step_bytes / frames
     frame_gbs = frame_bytes * fps / 1e9
-    kt = time_kernels(eng)
-    per = ab[0]["per_layer"]
-    per_frame_us = {k: kt[k] * s.n_layers for k in kt}
-    dom = max(per_frame_us, key=per_frame_us.get)
-    achieved = per[dom] / (kt[dom] * 1e-6) / 1e9
+    if args.engine == "frames":
+        launch_us = sum(a.elapsed_time(b) for a, b in ev) * 1e3 / len(ev)
+        roof = {"bound": "hbm", "kernel": "k_frames (sk_talker_frames, 64 frames per launch)",
+                "achieved": round(step_bytes / (launch_us * 1e-6) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "traffic": None, "bytes_per_launch": int(step_bytes), "avg_launch_us": round(launch_us, 2)}
+        roof["frac"] = round(roof["achieved"] / PEAK_HBM_GBS, 4)
+        extra = {}
+    else:
+        kt = time_kernels(eng) if args.engine == "multi" else {}
+        per = ab[0]["per_layer"]
+        if kt:
+            per_frame_us = {k: kt[k] * s.n_layers for k in kt}
+            dom = max(per_frame_us, key=per_frame_us.get)
+            achieved = per[dom] / (kt[dom] * 1e-6) / 1e9
+            roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "bytes_per_launch": per[dom],
+                    "avg_launch_us": round(kt[dom], 3)}
+            extra = {"kernel_us_per_frame": {k: round(v, 1) for k, v in per_frame_us.items()}}
+        else:
+            roof = {"bound": "hbm", "kernel": "k_frames (one frame per launch)", "achieved": round(frame_gbs, 1),
+                    "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(frame_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                    "bytes_per_launch": int(frame_bytes), "avg_launch_us": round(1e6 / fps, 2)}
+            extra = {}
     res = {
         "metric": "talker decode frames/sec (0.6B int8, bs1, KV 512); achieved HBM GB/s vs peak" if name == "talker06b"
         else "talker decode frames/sec (1.7B int8, bs1, KV 1024)",
@@ -178,14 +220,11 @@ def main() -> None:
         "config": {"workload": f"{name}: {s.n_layers} layers, hidden {s.hidden}, {s.nq}q/{s.nkv}kv heads x 128, "
                                f"intermediate {s.inter}, codec vocab {s.vocab}, i8row weights, batch 1, KV {pos0}, "
                                f"{frames} greedy frames per step", "batch": 1, "kv_start": pos0, "frames_per_step": frames,
-                   "weights": "i8row", "engine": "Qwen3Kernels, one HIP graph per frame"},
-        "roofline": {"bound": "hbm", "kernel": f"{dom} (sk_{'rms_gemv' if dom in ('qkv', 'gu') else 'attn' if dom == 'attn' else 'gemv'})",
-                     "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "bytes_per_launch": per[dom], "avg_launch_us": round(kt[dom], 3)},
+                   "weights": "i8row", "engine": args.engine},
+        "roofline": roof,
         "frame": {"us_per_frame": round(1e6 / fps, 2), "us_per_layer": round(1e6 / fps / s.n_layers, 3),
                   "algorithmic_bytes_per_frame": int(frame_bytes), "effective_GBs": round(frame_gbs, 1),
-                  "frac_of_peak": round(frame_gbs / PEAK_HBM_GBS, 4), "kernel_us_per_frame": {k: round(v, 1) for k, v in per_frame_us.items()}},
+                  "frac_of_peak": round(frame_gbs / PEAK_HBM_GBS, 4), **extra},
         "parity_codes_match_oracle": parity, "setup_s": round(setup_s, 1),
     }
     if not args.no_cpu:

@@ -76,7 +76,8 @@ __device__ __forceinline__ void wg_sync() {
 // ---- layout of the workspace (bytes) -------------------------------------------------------------------------
 struct Ws {
   // control words
-  static constexpr uint32_t kErr = 0, kTick = 4, kLaunch = 8, kDiag = 16, kCensus = 64;  // census: 8 counters
+  static constexpr uint32_t kErr = 0, kTick = 4, kLaunch = 8, kDiag = 16, kTraceOn = 32, kCensus = 64;  // census: 8 counters
+  static constexpr int kTraceLayers = 32, kTraceEvents = 8;  // optional per-stage timestamps of frame 0
   static constexpr uint32_t kCells = 256;
 };
 
@@ -137,6 +138,7 @@ struct Lds {
   float opart[W][4][16][17];
   float mrg[kChunks][10];  // S3 inputs per chunk: m, l, o[8] of one q head
   float inv;
+  sk_layer_desc desc[Ws::kTraceLayers];  // the layer descriptors, copied once per launch
   uint64_t cand[W];
   int flags[8];
   int64_t tok;
@@ -185,14 +187,18 @@ __device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, 
 
 // ---- compute-wave GEMV pieces ------------------------------------------------------------------------------
 // A wave owns RW consecutive rows starting at row0 (wave-uniform); lane reads chunk lane + 64 c of each row.
+// The row scales come with the weights through vector loads: a scalar load would make every later LDS wait
+// (lgkmcnt) wait for it as well.
 template <int RW, int C>
-__device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], const int8_t* W, int row0, int nvalid, int K, int lane) {
+__device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], float (&s)[RW], const int8_t* W, const uint16_t* S,
+                                          int row0, int nvalid, int K, int lane) {
 #pragma unroll
   for (int r = 0; r < RW; r++) {
     const int row = r < nvalid ? row0 + r : row0;
     const uint4* p = (const uint4*)(W + (size_t)row * K);
 #pragma unroll
     for (int c = 0; c < C; c++) w[r][c] = ld_stream(p + lane + 64 * c);
+    s[r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(make_rsrc(S), (uint32_t)row * 2u, 0, 0));
   }
 }
 // y[r] = (row r) . xs, reduced over the wave (uniform result), without the row scale
@@ -209,9 +215,6 @@ __device__ __forceinline__ void dot_rows(const uint4 (&w)[RW][C], const float* x
   }
 #pragma unroll
   for (int r = 0; r < RW; r++) y[r] = wave_sum(acc[r]);
-}
-__device__ __forceinline__ float row_scale_u(const uint16_t* S, int row) {
-  return bf2f(S[__builtin_amdgcn_readfirstlane(row)]);
 }
 
 // Position bookkeeping of a frame for this workgroup's attention chunk.
@@ -259,6 +262,11 @@ struct Ctx {
   int r, g;       // rank in the XCD, global workgroup index
   uint32_t base, tpf;
   int pos0, n_frames, L;
+  uint64_t* trace;  // per-stage timestamps of frame 0 (null when tracing is off)
+  __device__ void tr(int role, int f, int l, int ev) const {
+    if (trace && f == 0 && l < Ws::kTraceLayers)
+      trace[(((size_t)g * 2 + role) * Ws::kTraceLayers + l) * Ws::kTraceEvents + ev] = (uint64_t)wall_clock64();
+  }
   __device__ uint32_t tick(int f, int l, int s) const {
     return base + 1u + (uint32_t)f * tpf + (uint32_t)l * 8u + (uint32_t)s;
   }
@@ -291,27 +299,38 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
     const int pos = c.pos0 + f;
     const Chunk ck(pos, c.r);
     for (int l = 0; l < c.L; l++) {
-      const sk_layer_desc& Ly = c.d.layers[l];
+      const sk_layer_desc& Ly = S.desc[l];
+      // this layer's norm weights, in registers before any poll (lane holds elements lane + 64 k)
+      float nin[H / 64], npost[H / 64];
+#pragma unroll
+      for (int k = 0; k < H / 64; k++) { nin[k] = Ly.in_norm[lane + 64 * k]; npost[k] = Ly.post_norm[lane + 64 * k]; }
       // S1 input: embedding row (layer 0) or the previous layer's residual, times the input norm
       bool ok = true;
+      if (lane == 0) c.tr(0, f, l, 0);
       if (l == 0) {
-        for (int i = lane; i < H; i += 64) S.hin[i] = bf2f(emb[(size_t)tok * H + i]);
+        float ev[H / 64];
+#pragma unroll
+        for (int k = 0; k < H / 64; k++) ev[k] = bf2f(emb[(size_t)tok * H + lane + 64 * k]);
+#pragma unroll
+        for (int k = 0; k < H / 64; k++) S.hin[lane + 64 * k] = ev[k];
       } else {
         ok = poll_cells<8>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
       }
       float ss = 0.f;
       for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
       ss = wave_sum(ss);
-      for (int i = lane; i < H; i += 64) S.xs[0][i] = S.hin[i] * Ly.in_norm[i];
-      if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[0] = !ok; }
+#pragma unroll
+      for (int k = 0; k < H / 64; k++) S.xs[0][lane + 64 * k] = S.hin[lane + 64 * k] * nin[k];
+      if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[0] = !ok; c.tr(0, f, l, 1); }
       wg_sync();
       if (!ok) return;
       // S2 input: this head's q/k/v
       ok = poll_cells<4>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
-      if (lane == 0) S.flags[1] = !ok;
+      if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
       if (!ok) return;
       for (int b = 0; b < attn_barriers(ck); b++) wg_sync();
+      if (lane == 0) c.tr(0, f, l, 3);
       // S3: merge of the 32 chunk partials for q head 2x + r/16, dims [8 (r % 16), 8 (r % 16) + 8)
       {
         const uint32_t e = c.tick(f, l, 1);
@@ -348,10 +367,11 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
           }
           put(c.cells, LY.e3 + (2 * c.x + mh) * SK_HD + md0 + lane, Lw > 0.f ? O / Lw : 0.f, c.tick(f, l, 2));
         }
+        if (lane == 0) c.tr(0, f, l, 4);
       }
       // S4 input: the whole attention output
       ok = ok && poll_cells<16>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
-      if (lane == 0) S.flags[2] = !ok;
+      if (lane == 0) { S.flags[2] = !ok; c.tr(0, f, l, 5); }
       wg_sync();
       if (!ok) return;
       // S5 input: residual after o, times the post-attention norm
@@ -359,22 +379,27 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
       ss = 0.f;
       for (int i = lane; i < H; i += 64) { const float v = S.hmid[i]; ss += v * v; }
       ss = wave_sum(ss);
-      for (int i = lane; i < H; i += 64) S.xs[0][i] = S.hmid[i] * Ly.post_norm[i];
-      if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[3] = !ok; }
+#pragma unroll
+      for (int k = 0; k < H / 64; k++) S.xs[0][lane + 64 * k] = S.hmid[lane + 64 * k] * npost[k];
+      if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[3] = !ok; c.tr(0, f, l, 6); }
       wg_sync();
       if (!ok) return;
       // S6 input: the whole SwiGLU activation
       ok = poll_cells<16>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
-      if (lane == 0) S.flags[4] = !ok;
+      if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
       wg_sync();
       if (!ok) return;
     }
     // head input: final residual times the final norm
+    float nfin[H / 64];
+#pragma unroll
+    for (int k = 0; k < H / 64; k++) nfin[k] = c.d.norm[lane + 64 * k];
     bool ok = poll_cells<8>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
     float ss = 0.f;
     for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
     ss = wave_sum(ss);
-    for (int i = lane; i < H; i += 64) S.xs[0][i] = S.hin[i] * c.d.norm[i];
+#pragma unroll
+    for (int k = 0; k < H / 64; k++) S.xs[0][lane + 64 * k] = S.hin[lane + 64 * k] * nfin[k];
     if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[5] = !ok; }
     wg_sync();
     if (!ok) return;
@@ -461,27 +486,40 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
   const bool att_thread = tid < 256;
 
   uint4 wq[C::RW_QKV][C::CH], wo[C::RW_O][C::CQ], wg[C::RW_GU][C::CH], wd[C::RW_D][C::CI];
+  float sq[C::RW_QKV], so[C::RW_O], sg[C::RW_GU], sd[C::RW_D];
   uint4 kr[C::KVL], vr[C::KVL];
+  float a_cs = 0.f, a_sn = 0.f, a_qn = 0.f, a_kn = 0.f;  // RoPE row and q/k norm weights of the next attention
+  auto load_attn_vec = [&](const sk_layer_desc& Lx, int posx) {
+    if (att_thread) {
+      a_cs = c.d.rope[(size_t)posx * SK_HD + (dd & 63)];
+      a_sn = c.d.rope[(size_t)posx * SK_HD + 64 + (dd & 63)];
+      a_qn = Lx.qn[dd];
+      a_kn = Lx.kn[dd];
+    }
+  };
   {
-    const sk_layer_desc& L0 = c.d.layers[0];
-    load_rows<C::RW_QKV, C::CH>(wq, (const int8_t*)L0.qkv_w, q_w0, C::RW_QKV, H, lane);
+    const sk_layer_desc& L0 = S.desc[0];
+    load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
     load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), Chunk(c.pos0, r), cw, ag, asl);
-    load_rows<C::RW_O, C::CQ>(wo, (const int8_t*)L0.o_w, o_w0, o_wn, kQ, lane);
-    load_rows<C::RW_GU, C::CH>(wg, (const int8_t*)L0.gu_w, gu_w0, C::RW_GU, H, lane);
-    load_rows<C::RW_D, C::CI>(wd, (const int8_t*)L0.down_w, d_w0, d_wn, I, lane);
+    load_attn_vec(L0, c.pos0);
+    load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
+    load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
+    load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
   }
   const bool block_eos0 = c.d.talker_processor && c.d.ngen;
+  const int64_t ngen0 = c.d.ngen ? c.d.ngen[0] : 0;
   for (int f = 0; f < c.n_frames; f++) {
     const int pos = c.pos0 + f;
     const Chunk ck(pos, r);
     for (int l = 0; l < c.L; l++) {
-      const sk_layer_desc& Ly = c.d.layers[l];
+      const sk_layer_desc& Ly = S.desc[l];
       const bool last_layer = l == c.L - 1;
-      const sk_layer_desc& Ln = c.d.layers[last_layer ? 0 : l + 1];
+      const sk_layer_desc& Ln = S.desc[last_layer ? 0 : l + 1];
       const bool more = !last_layer || f + 1 < c.n_frames;
       // ---- S1: qkv rows -----------------------------------------------------------------------------------
       wg_sync();
       if (S.flags[0]) return;
+      if (tid == 0) c.tr(1, f, l, 0);
       {
         float y[C::RW_QKV];
         dot_rows<C::RW_QKV, C::CH>(wq, S.xs[0], lane, y);
@@ -490,19 +528,21 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
 #pragma unroll
           for (int i = 0; i < C::RW_QKV; i++)
             put(c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r + C::RW_QKV * cw + i,
-                y[i] * row_scale_u(Ly.qkv_s, q_w0 + i) * inv, c.tick(f, l, 0));
+                y[i] * sq[i] * inv, c.tick(f, l, 0));
         }
-        if (more) load_rows<C::RW_QKV, C::CH>(wq, (const int8_t*)Ln.qkv_w, q_w0, C::RW_QKV, H, lane);
+        if (tid == 0) c.tr(1, f, l, 1);
+        if (more) load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
       }
       // ---- S2: attention over this workgroup's chunk ----------------------------------------------------
       wg_sync();
       if (S.flags[1]) return;
+      if (tid == 0) c.tr(1, f, l, 2);
       {
         const bool has_pos = ck.has_pos();
         float qv = 0.f, kv = 0.f, cs = 0.f, sn = 0.f;
         if (att_thread) {
-          cs = c.d.rope[(size_t)pos * SK_HD + (dd & 63)];
-          sn = c.d.rope[(size_t)pos * SK_HD + 64 + (dd & 63)];
+          cs = a_cs;
+          sn = a_sn;
           qv = S.qkv[p * SK_HD + dd];
           kv = S.qkv[256 + p * SK_HD + dd];  // p 0: k, p 1: v
         }
@@ -510,8 +550,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
         if (att_thread && lane == 0) { S.red[cw] = sqv; S.red[4 + cw] = skv; }
         wg_sync();  // attention barrier 1
         if (att_thread) {
-          S.qs[p][dd] = qv * rsqrtf((S.red[2 * p] + S.red[2 * p + 1]) / SK_HD + eps) * Ly.qn[dd];
-          if (p == 0) S.kn[dd] = kv * rsqrtf((S.red[4] + S.red[5]) / SK_HD + eps) * Ly.kn[dd];
+          S.qs[p][dd] = qv * rsqrtf((S.red[2 * p] + S.red[2 * p + 1]) / SK_HD + eps) * a_qn;
+          if (p == 0) S.kn[dd] = kv * rsqrtf((S.red[4] + S.red[5]) / SK_HD + eps) * a_kn;
           else S.vn[dd] = bf2f(f2bf(kv));
         }
         wg_sync();  // 2
@@ -606,11 +646,16 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
           if (dd == 0) { put(c.cells, pb + 2 * p, m, e); put(c.cells, pb + 2 * p + 1, lsum, e); }
           put(c.cells, pb + 4 + p * SK_HD + dd, o, e);
         }
-        if (more) load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), Chunk(last_layer ? pos + 1 : pos, r), cw, ag, asl);
+        if (tid == 0) c.tr(1, f, l, 3);
+        if (more) {
+          load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), Chunk(last_layer ? pos + 1 : pos, r), cw, ag, asl);
+          load_attn_vec(Ln, last_layer ? pos + 1 : pos);
+        }
       }
       // ---- S4: o projection rows, added to the layer's input residual ------------------------------------
       wg_sync();
       if (S.flags[2]) return;
+      if (tid == 0) c.tr(1, f, l, 4);
       {
         float y[C::RW_O];
         dot_rows<C::RW_O, C::CQ>(wo, S.xs[1], lane, y);
@@ -618,9 +663,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
 #pragma unroll
           for (int i = 0; i < C::RW_O; i++)
             if (i < o_wn)
-              put(c.cells, LY.e4 + o_w0 + i, S.hin[o_w0 + i] + y[i] * row_scale_u(Ly.o_s, o_w0 + i), c.tick(f, l, 3));
+              put(c.cells, LY.e4 + o_w0 + i, S.hin[o_w0 + i] + y[i] * so[i], c.tick(f, l, 3));
         }
-        if (more) load_rows<C::RW_O, C::CQ>(wo, (const int8_t*)Ln.o_w, o_w0, o_wn, kQ, lane);
+        if (tid == 0) c.tr(1, f, l, 5);
+        if (more) load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
       }
       // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
       wg_sync();
@@ -633,10 +679,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
 #pragma unroll
           for (int i = 0; i < C::RW_GU; i += 2)
             put(c.cells, LY.e5 + (gu_w0 + i) / 2,
-                silu_mul(y[i] * row_scale_u(Ly.gu_s, gu_w0 + i) * inv, y[i + 1] * row_scale_u(Ly.gu_s, gu_w0 + i + 1) * inv),
+                silu_mul(y[i] * sg[i] * inv, y[i + 1] * sg[i + 1] * inv),
                 c.tick(f, l, 4));
         }
-        if (more) load_rows<C::RW_GU, C::CH>(wg, (const int8_t*)Ln.gu_w, gu_w0, C::RW_GU, H, lane);
+        if (tid == 0) c.tr(1, f, l, 6);
+        if (more) load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
       }
       // ---- S6: down rows, added to the residual after o --------------------------------------------------
       wg_sync();
@@ -648,32 +695,34 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
 #pragma unroll
           for (int i = 0; i < C::RW_D; i++) {
             if (i < d_wn) {
-              const float hv = S.hmid[d_w0 + i] + y[i] * row_scale_u(Ly.down_s, d_w0 + i);
+              const float hv = S.hmid[d_w0 + i] + y[i] * sd[i];
               put(c.cells, LY.e6 + d_w0 + i, hv, c.tick(f, l, 5));
               if (c.d.layer_out && f == c.n_frames - 1) c.d.layer_out[(size_t)l * H + d_w0 + i] = hv;
             }
           }
         }
-        if (more) load_rows<C::RW_D, C::CI>(wd, (const int8_t*)Ln.down_w, d_w0, d_wn, I, lane);
+        if (tid == 0) c.tr(1, f, l, 7);
+        if (more) load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
       }
     }
     // ---- head rows (loaded now; the final residual is a full layer away), processor, local argmax ----------
     uint4 wh[C::RW_HEAD][C::CH];
-    load_rows<C::RW_HEAD, C::CH>(wh, (const int8_t*)c.d.head_w, h_w0, h_wn, H, lane);
+    float sh[C::RW_HEAD];
+    load_rows<C::RW_HEAD, C::CH>(wh, sh, (const int8_t*)c.d.head_w, c.d.head_s, h_w0, h_wn, H, lane);
     wg_sync();
     if (S.flags[5]) return;
     {
       float y[C::RW_HEAD];
       dot_rows<C::RW_HEAD, C::CH>(wh, S.xs[0], lane, y);
       const float inv = S.inv;
-      const bool block_eos = block_eos0 && (c.d.ngen[0] + f) < c.d.min_new;
+      const bool block_eos = block_eos0 && (ngen0 + f) < c.d.min_new;
       uint64_t best = 0;
       if (lane == 0) {
 #pragma unroll
         for (int i = 0; i < C::RW_HEAD; i++) {
           if (i >= h_wn) break;
           const int row = h_w0 + i;
-          float v = y[i] * row_scale_u(c.d.head_s, row) * inv;
+          float v = y[i] * sh[i] * inv;
           if (c.d.logits && f == c.n_frames - 1) c.d.logits[row] = v;
           if (c.d.talker_processor) {
             if (c.d.seen && ((ld_u32_dev(c.d.seen, (uint32_t)row & ~3u) >> (8 * (row & 3))) & 0xffu))
@@ -736,6 +785,10 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n
   c.pos0 = (int)d.pos[0];
   c.n_frames = n_frames;
   c.L = d.n_layers;
+  for (int i = tid; i < d.n_layers * (int)(sizeof(sk_layer_desc) / 8); i += blockDim.x)
+    ((uint64_t*)S.desc)[i] = ((const uint64_t*)d.layers)[i];
+  __syncthreads();
+  c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
   if (wave == W) run_control<H, I, W>(c, S, lane);
   else run_compute<H, I, W>(c, S, wave, tid, lane);
   // ---- end of launch: epoch base and launch count (workgroup 0; every workgroup finished its census) --------
@@ -762,7 +815,7 @@ int launch_frames(const sk_talker_desc* d, int n_frames, hipStream_t st) {
 extern "C" int64_t sk_talker_workspace_size(int hidden, int inter) {
   if (hidden <= 0 || inter <= 0) return 0;
   const Layout LY(hidden, inter);
-  return (int64_t)Ws::kCells + (int64_t)LY.total * 8;
+  return (int64_t)Ws::kCells + (int64_t)LY.total * 8 + (int64_t)kWG * 2 * Ws::kTraceLayers * Ws::kTraceEvents * 8;
 }
 
 extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* stream) {
@@ -771,6 +824,8 @@ extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* str
     return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs 16 q / 8 kv heads, vocab 3072, i8row, bf16 cache");
   if (!d->layers || !d->norm || !d->head_w || !d->head_s || !d->emb || !d->rope || !d->id0 || !d->pos || !d->workspace)
     return sk_set_error(SK_EINVAL, "sk_talker_frames: null pointer");
+  if (d->n_layers <= 0 || d->n_layers > Ws::kTraceLayers)
+    return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: 1..32 layers");
   if (d->workspace_bytes < sk_talker_workspace_size(d->hidden, d->inter))
     return sk_set_error(SK_EWORKSPACE, "sk_talker_frames: workspace too small");
   int dev = 0, cus = 0;
