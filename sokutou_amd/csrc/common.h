@@ -139,11 +139,29 @@ __device__ __forceinline__ float row_scale(const uint16_t* __restrict__ S, int r
   else return 1.f;
 }
 
+// ---- address space and uniformity ----------------------------------------------------------------------------
+// A pointer read from memory (a descriptor table) is generic to the compiler. Loads through it become FLAT
+// instructions, which count against the LDS wait counter as well, so every later LDS wait would also wait for
+// them; and a buffer resource built from it needs a waterfall loop. `gptr` views memory as global, `uniform`
+// moves a wave-uniform pointer into scalar registers.
+template <class T> using gptr = __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ T* uniform(T* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+template <class T>
+__device__ __forceinline__ T gload(const T* p) { return *(gptr<const T>)p; }
+template <class T>
+__device__ __forceinline__ void gstore(T* p, T v) { *(gptr<T>)p = v; }
+
 // ---- streaming loads -------------------------------------------------------------------------------------
 // Weights are read once per frame: nontemporal hint keeps them from displacing reused lines in L2/MALL.
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 r = __builtin_nontemporal_load((const u32x4*)p);
+  u32x4 r = __builtin_nontemporal_load((gptr<const u32x4>)p);
   return make_uint4(r.x, r.y, r.z, r.w);
 }
 

@@ -54,6 +54,10 @@ __device__ __forceinline__ void put(void* cells, uint32_t idx, float v, uint32_t
   u32x2 x = {__float_as_uint(v), e};
   __builtin_amdgcn_raw_buffer_store_b64(x, make_rsrc(cells), idx * 8u, 0, kPolDev);
 }
+__device__ __forceinline__ void put2(void* cells, uint32_t idx, float v0, float v1, uint32_t e) {  // idx even
+  u32x4 x = {__float_as_uint(v0), e, __float_as_uint(v1), e};
+  __builtin_amdgcn_raw_buffer_store_b128(x, make_rsrc(cells), idx * 8u, 0, kPolDev);
+}
 __device__ __forceinline__ u32x4 get2(const void* cells, uint32_t idx) {  // cells idx, idx+1
   return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(cells), idx * 8u, 0, kPolDev);
 }
@@ -137,6 +141,9 @@ struct Lds {
   float red[32];
   float opart[W][4][16][17];
   float mrg[kChunks][10];  // S3 inputs per chunk: m, l, o[8] of one q head
+  float pub[64];           // this workgroup's outputs of a stage, published by the last compute wave to finish
+  uint32_t pubcnt;         // compute-wave arrivals at publish (counts up; the wave that makes it a multiple of W
+                           // publishes)
   float inv;
   sk_layer_desc desc[Ws::kTraceLayers];  // the layer descriptors, copied once per launch
   uint64_t cand[W];
@@ -147,6 +154,9 @@ struct Lds {
 // Records a timeout: error code, then frame and layer of the stage that gave up (diagnostic words of the workspace).
 struct Ctx;
 __device__ void fail(const Ctx& c, uint32_t code, int f, int l);
+
+// Loads per lane in one polling round: the whole vector when it fits in 24 (96 registers of the control wave).
+constexpr int mb(int n) { return n / 128 < 24 ? n / 128 : 24; }
 
 // ---- control wave: poll cells into LDS ---------------------------------------------------------------------
 // Waits until cells [idx0, idx0 + n) (n even, idx0 even) all carry epoch e, copying the values to dst.
@@ -187,10 +197,11 @@ __device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, 
 
 // ---- compute-wave GEMV pieces ------------------------------------------------------------------------------
 // A wave owns RW consecutive rows starting at row0 (wave-uniform); lane reads chunk lane + 64 c of each row.
-// The row scales come with the weights through vector loads: a scalar load would make every later LDS wait
-// (lgkmcnt) wait for it as well.
+// The row scales come with the weights through vector loads (a scalar load would make every later LDS wait,
+// lgkmcnt, wait for it as well) and stay raw bf16 bits until the dot that uses them: converting on arrival would
+// make the wave wait for the load right after issuing it.
 template <int RW, int C>
-__device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], float (&s)[RW], const int8_t* W, const uint16_t* S,
+__device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], uint16_t (&s)[RW], const int8_t* W, const uint16_t* S,
                                           int row0, int nvalid, int K, int lane) {
 #pragma unroll
   for (int r = 0; r < RW; r++) {
@@ -198,7 +209,8 @@ __device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], float (&s)[RW], con
     const uint4* p = (const uint4*)(W + (size_t)row * K);
 #pragma unroll
     for (int c = 0; c < C; c++) w[r][c] = ld_stream(p + lane + 64 * c);
-    s[r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(make_rsrc(S), (uint32_t)row * 2u, 0, 0));
+    // one ushort load per row: merged wider loads would be split into halves right away, waiting for them
+    s[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), (uint32_t)row * 2u, 0, 0);
   }
 }
 // y[r] = (row r) . xs, reduced over the wave (uniform result), without the row scale
@@ -215,6 +227,20 @@ __device__ __forceinline__ void dot_rows(const uint4 (&w)[RW][C], const float* x
   }
 #pragma unroll
   for (int r = 0; r < RW; r++) y[r] = wave_sum(acc[r]);
+}
+
+// Publishes a stage's outputs. Every compute wave has left its values in S.pub (lane 0, before the call); the last
+// wave to arrive writes the workgroup's n cells [idx0, idx0 + n) (idx0 and n even) with 16-byte stores, so each
+// line of cells is written by one wave at one time (lines written piecewise by several waves reach the pollers
+// later). There is no barrier: the control wave may be polling the next stage's input meanwhile.
+template <int W, class L>
+__device__ __forceinline__ void publish(L& S, void* cells, uint32_t idx0, int n, uint32_t e, int lane) {
+  uint32_t old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(&S.pubcnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+  old = __builtin_amdgcn_readfirstlane(old);
+  if (old % W == W - 1) {
+    for (int i = 2 * lane; i < n; i += 128) put2(cells, idx0 + i, S.pub[i], S.pub[i + 1], e);
+  }
 }
 
 // Position bookkeeping of a frame for this workgroup's attention chunk.
@@ -234,17 +260,16 @@ struct Chunk {
 template <int W, int KVL>
 __device__ __forceinline__ void load_kv(uint4 (&kr)[KVL], uint4 (&vr)[KVL], const bf16_t* Kh, const bf16_t* Vh,
                                         const Chunk& ck, int w, int g, int sl) {
+// Loads are unconditional, from a position clamped to ck.pos (< max_len): a load under a condition would need a
+// select on its result, and a select makes the wave wait for the load at once. Slots beyond the chunk and the
+// slot of `pos` itself (not written yet) are never read back: the attention code skips or replaces them.
 #pragma unroll
   for (int i = 0; i < KVL; i++) {
     const int jj = 4 * W * i + 4 * w + g;
-    if (jj < ck.n && ck.t0 + jj != ck.pos) {
-      const uint32_t off = (uint32_t)((ck.t0 + jj) * SK_HD + 8 * sl) * 2u;
-      kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(Kh), off, 0, kPolDev));
-      vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(Vh), off, 0, kPolDev));
-    } else {
-      kr[i] = make_uint4(0, 0, 0, 0);
-      vr[i] = make_uint4(0, 0, 0, 0);
-    }
+    const int t = min(ck.t0 + jj, ck.pos);
+    const uint32_t off = (uint32_t)(t * SK_HD + 8 * sl) * 2u;
+    kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Kh)), off, 0, kPolDev));
+    vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Vh)), off, 0, kPolDev));
   }
 }
 
@@ -294,7 +319,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
   const Layout LY(H, I);
   const float eps = c.d.eps;
   const bf16_t* emb = (const bf16_t*)c.d.emb;
-  int64_t tok = c.d.id0[0];
+  int64_t tok = gload(c.d.id0);
   for (int f = 0; f < c.n_frames; f++) {
     const int pos = c.pos0 + f;
     const Chunk ck(pos, c.r);
@@ -303,18 +328,18 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
       // this layer's norm weights, in registers before any poll (lane holds elements lane + 64 k)
       float nin[H / 64], npost[H / 64];
 #pragma unroll
-      for (int k = 0; k < H / 64; k++) { nin[k] = Ly.in_norm[lane + 64 * k]; npost[k] = Ly.post_norm[lane + 64 * k]; }
+      for (int k = 0; k < H / 64; k++) { nin[k] = gload(Ly.in_norm + lane + 64 * k); npost[k] = gload(Ly.post_norm + lane + 64 * k); }
       // S1 input: embedding row (layer 0) or the previous layer's residual, times the input norm
       bool ok = true;
       if (lane == 0) c.tr(0, f, l, 0);
       if (l == 0) {
         float ev[H / 64];
 #pragma unroll
-        for (int k = 0; k < H / 64; k++) ev[k] = bf2f(emb[(size_t)tok * H + lane + 64 * k]);
+        for (int k = 0; k < H / 64; k++) ev[k] = bf2f(gload(emb + (size_t)tok * H + lane + 64 * k));
 #pragma unroll
         for (int k = 0; k < H / 64; k++) S.hin[lane + 64 * k] = ev[k];
       } else {
-        ok = poll_cells<8>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
+        ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
       }
       float ss = 0.f;
       for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
@@ -325,7 +350,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
       wg_sync();
       if (!ok) return;
       // S2 input: this head's q/k/v
-      ok = poll_cells<4>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
+      ok = poll_cells<mb(512)>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
       if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
       if (!ok) return;
@@ -337,15 +362,25 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
         const int mh = c.r >> 4, md0 = 8 * (c.r & 15);
         for (uint32_t spin = 0;; spin++) {
           bool good = true;
-          // per chunk 5 cell pairs: (m, l) of head mh, then 4 pairs of its o slice
-          for (int it = lane; it < kChunks * 5; it += 64) {
+          // per chunk 5 cell pairs: (m, l) of head mh, then 4 pairs of its o slice; all loads issued first
+          constexpr int kItems = kChunks * 5, kPer = (kItems + 63) / 64;
+          u32x4 q[kPer];
+#pragma unroll
+          for (int j = 0; j < kPer; j++) {
+            const int it = min(lane + 64 * j, kItems - 1);
             const int ch = it / 5, k = it % 5;
             const uint32_t pb = LY.e2 + (c.x * kChunks + ch) * kPartN;
-            const uint32_t idx = k == 0 ? pb + 2 * mh : pb + 4 + mh * SK_HD + md0 + 2 * (k - 1);
-            const u32x4 q = get2(c.cells, idx);
-            good &= q.y == e && q.w == e;
-            S.mrg[ch][2 * k] = __uint_as_float(q.x);
-            S.mrg[ch][2 * k + 1] = __uint_as_float(q.z);
+            q[j] = get2(c.cells, k == 0 ? pb + 2 * mh : pb + 4 + mh * SK_HD + md0 + 2 * (k - 1));
+          }
+#pragma unroll
+          for (int j = 0; j < kPer; j++) {
+            const int it = lane + 64 * j;
+            if (it < kItems) {
+              const int ch = it / 5, k = it % 5;
+              good &= q[j].y == e && q[j].w == e;
+              S.mrg[ch][2 * k] = __uint_as_float(q[j].x);
+              S.mrg[ch][2 * k + 1] = __uint_as_float(q[j].z);
+            }
           }
           if (__all(good)) break;
           if ((spin & 63) == 63) {
@@ -370,12 +405,12 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
         if (lane == 0) c.tr(0, f, l, 4);
       }
       // S4 input: the whole attention output
-      ok = ok && poll_cells<16>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
+      ok = ok && poll_cells<mb(kQ)>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
       if (lane == 0) { S.flags[2] = !ok; c.tr(0, f, l, 5); }
       wg_sync();
       if (!ok) return;
       // S5 input: residual after o, times the post-attention norm
-      ok = poll_cells<8>(c.cells, LY.e4, H, c.tick(f, l, 3), S.hmid, c.ws, lane, c, 15u, f, l);
+      ok = poll_cells<mb(H)>(c.cells, LY.e4, H, c.tick(f, l, 3), S.hmid, c.ws, lane, c, 15u, f, l);
       ss = 0.f;
       for (int i = lane; i < H; i += 64) { const float v = S.hmid[i]; ss += v * v; }
       ss = wave_sum(ss);
@@ -385,7 +420,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
       wg_sync();
       if (!ok) return;
       // S6 input: the whole SwiGLU activation
-      ok = poll_cells<16>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+      ok = poll_cells<mb(I)>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
       if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
       wg_sync();
       if (!ok) return;
@@ -393,8 +428,8 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
     // head input: final residual times the final norm
     float nfin[H / 64];
 #pragma unroll
-    for (int k = 0; k < H / 64; k++) nfin[k] = c.d.norm[lane + 64 * k];
-    bool ok = poll_cells<8>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
+    for (int k = 0; k < H / 64; k++) nfin[k] = gload(c.d.norm + lane + 64 * k);
+    bool ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
     float ss = 0.f;
     for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
     ss = wave_sum(ss);
@@ -408,8 +443,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
       uint64_t best = 0;
       for (int i = 0; i < W; i++) best = S.cand[i] > best ? S.cand[i] : best;
       const uint32_t e = c.tick(f, c.L, 0);
-      put(c.cells, LY.e7 + 2 * c.g, __uint_as_float((uint32_t)(best >> 32)), e);
-      put(c.cells, LY.e7 + 2 * c.g + 1, __uint_as_float((uint32_t)best), e);
+      put2(c.cells, LY.e7 + 2 * c.g, __uint_as_float((uint32_t)(best >> 32)), __uint_as_float((uint32_t)best), e);
     }
     // pick: reduce the 256 candidates
     {
@@ -418,10 +452,13 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
       for (uint32_t spin = 0;; spin++) {
         bool good = true;
         best = 0;
-        for (int it = lane; it < kWG; it += 64) {
-          const u32x4 q = get2(c.cells, LY.e7 + 2 * it);
-          good &= q.y == e && q.w == e;
-          const uint64_t k = ((uint64_t)q.x << 32) | q.z;
+        u32x4 q[kWG / 64];
+#pragma unroll
+        for (int j = 0; j < kWG / 64; j++) q[j] = get2(c.cells, LY.e7 + 2 * (lane + 64 * j));
+#pragma unroll
+        for (int j = 0; j < kWG / 64; j++) {
+          good &= q[j].y == e && q[j].w == e;
+          const uint64_t k = ((uint64_t)q[j].x << 32) | q[j].z;
           best = k > best ? k : best;
         }
         if (__all(good)) break;
@@ -443,20 +480,20 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
     if (!ok) return;
     if (c.g == 0 && lane == 0) {
       // device-side frame state, as the sampler leaves it (qwen3/sampler.py:147-156)
-      if (c.d.out) c.d.out[f] = tok;
+      if (c.d.out) gstore(c.d.out + f, tok);
       if (c.d.seen) {
         // read back by later frames of this launch through device-coherent loads
-        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)1, make_rsrc(c.d.seen), (uint32_t)tok, 0, kPolDev);
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)1, make_rsrc(uniform(c.d.seen)), (uint32_t)tok, 0, kPolDev);
         __builtin_amdgcn_s_waitcnt(0);
       }
     }
   }
   if (c.g == 0 && lane == 0) {
     if (ld_u32_dev(c.ws, Ws::kErr) == 0) {
-      c.d.id0[0] = tok;
-      if (c.d.next_id0) c.d.next_id0[0] = tok;
-      c.d.pos[0] = c.pos0 + c.n_frames;
-      if (c.d.ngen) c.d.ngen[0] += c.n_frames;
+      gstore(c.d.id0, tok);
+      if (c.d.next_id0) gstore(c.d.next_id0, tok);
+      gstore(c.d.pos, (int64_t)(c.pos0 + c.n_frames));
+      if (c.d.ngen) gstore(c.d.ngen, gload(c.d.ngen) + (int64_t)c.n_frames);
     }
   }
 }
@@ -486,16 +523,14 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
   const bool att_thread = tid < 256;
 
   uint4 wq[C::RW_QKV][C::CH], wo[C::RW_O][C::CQ], wg[C::RW_GU][C::CH], wd[C::RW_D][C::CI];
-  float sq[C::RW_QKV], so[C::RW_O], sg[C::RW_GU], sd[C::RW_D];
+  uint16_t sq[C::RW_QKV], so[C::RW_O], sg[C::RW_GU], sd[C::RW_D];  // raw bf16 row scales
   uint4 kr[C::KVL], vr[C::KVL];
   float a_cs = 0.f, a_sn = 0.f, a_qn = 0.f, a_kn = 0.f;  // RoPE row and q/k norm weights of the next attention
-  auto load_attn_vec = [&](const sk_layer_desc& Lx, int posx) {
-    if (att_thread) {
-      a_cs = c.d.rope[(size_t)posx * SK_HD + (dd & 63)];
-      a_sn = c.d.rope[(size_t)posx * SK_HD + 64 + (dd & 63)];
-      a_qn = Lx.qn[dd];
-      a_kn = Lx.kn[dd];
-    }
+  auto load_attn_vec = [&](const sk_layer_desc& Lx, int posx) {  // every compute thread: no select on the loads
+    a_cs = gload(c.d.rope + (size_t)posx * SK_HD + (dd & 63));
+    a_sn = gload(c.d.rope + (size_t)posx * SK_HD + 64 + (dd & 63));
+    a_qn = gload(Lx.qn + dd);
+    a_kn = gload(Lx.kn + dd);
   };
   {
     const sk_layer_desc& L0 = S.desc[0];
@@ -507,7 +542,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
     load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
   }
   const bool block_eos0 = c.d.talker_processor && c.d.ngen;
-  const int64_t ngen0 = c.d.ngen ? c.d.ngen[0] : 0;
+  const int64_t ngen0 = c.d.ngen ? gload(c.d.ngen) : 0;
+  // Wait once for the first layer's loads. The compiler places one static wait count per use; without this it
+  // would have to allow for the prologue's own load order on every layer, and waits would come out shallow.
+  __builtin_amdgcn_s_waitcnt(0);
   for (int f = 0; f < c.n_frames; f++) {
     const int pos = c.pos0 + f;
     const Chunk ck(pos, r);
@@ -515,7 +553,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
       const sk_layer_desc& Ly = S.desc[l];
       const bool last_layer = l == c.L - 1;
       const sk_layer_desc& Ln = S.desc[last_layer ? 0 : l + 1];
-      const bool more = !last_layer || f + 1 < c.n_frames;
+      // The next layer's weights and K/V are prefetched unconditionally (after the last layer of the last frame
+      // that reloads layer 0, unused): a prefetch under a condition makes the compiler assume it may not have
+      // been issued, and then every later wait for older loads also waits for the younger ones.
+      const int npos = (last_layer && f + 1 < c.n_frames) ? pos + 1 : pos;  // always < max_len
       // ---- S1: qkv rows -----------------------------------------------------------------------------------
       wg_sync();
       if (S.flags[0]) return;
@@ -526,12 +567,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
         const float inv = S.inv;
         if (lane == 0) {
 #pragma unroll
-          for (int i = 0; i < C::RW_QKV; i++)
-            put(c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r + C::RW_QKV * cw + i,
-                y[i] * sq[i] * inv, c.tick(f, l, 0));
+          for (int i = 0; i < C::RW_QKV; i++) S.pub[C::RW_QKV * cw + i] = y[i] * bf2f(sq[i]) * inv;
         }
+        publish<W>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, 16, c.tick(f, l, 0), lane);
         if (tid == 0) c.tr(1, f, l, 1);
-        if (more) load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+        load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
       }
       // ---- S2: attention over this workgroup's chunk ----------------------------------------------------
       wg_sync();
@@ -539,13 +579,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
       if (tid == 0) c.tr(1, f, l, 2);
       {
         const bool has_pos = ck.has_pos();
-        float qv = 0.f, kv = 0.f, cs = 0.f, sn = 0.f;
-        if (att_thread) {
-          cs = a_cs;
-          sn = a_sn;
-          qv = S.qkv[p * SK_HD + dd];
-          kv = S.qkv[256 + p * SK_HD + dd];  // p 0: k, p 1: v
-        }
+        // read by every compute thread (no select on the prefetched registers); threads past the attention
+        // mapping (p > 1) compute values that are never stored
+        const float cs = a_cs, sn = a_sn;
+        const float qv = S.qkv[(p & 1) * SK_HD + dd];
+        const float kv = S.qkv[256 + (p & 1) * SK_HD + dd];  // p 0: k, p 1: v
         const float sqv = wave_sum(qv * qv), skv = wave_sum(kv * kv);
         if (att_thread && lane == 0) { S.red[cw] = sqv; S.red[4 + cw] = skv; }
         wg_sync();  // attention barrier 1
@@ -567,8 +605,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
           if (has_pos) {
             // append the new K/V at pos (device-coherent: later frames read it from other workgroups)
             const uint32_t off = (uint32_t)(pos * SK_HD + dd) * 2u;
-            if (p == 0) __builtin_amdgcn_raw_buffer_store_b16(f2bf(krot), make_rsrc(c.kh(Ly)), off, 0, kPolDev);
-            else __builtin_amdgcn_raw_buffer_store_b16(f2bf(S.vn[dd]), make_rsrc(c.vh(Ly)), off, 0, kPolDev);
+            if (p == 0) __builtin_amdgcn_raw_buffer_store_b16(f2bf(krot), make_rsrc(uniform(c.kh(Ly))), off, 0, kPolDev);
+            else __builtin_amdgcn_raw_buffer_store_b16(f2bf(S.vn[dd]), make_rsrc(uniform(c.vh(Ly))), off, 0, kPolDev);
           }
         }
         wg_sync();  // 4
@@ -647,10 +685,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
           put(c.cells, pb + 4 + p * SK_HD + dd, o, e);
         }
         if (tid == 0) c.tr(1, f, l, 3);
-        if (more) {
-          load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), Chunk(last_layer ? pos + 1 : pos, r), cw, ag, asl);
-          load_attn_vec(Ln, last_layer ? pos + 1 : pos);
-        }
+        load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), Chunk(npos, r), cw, ag, asl);
+        load_attn_vec(Ln, npos);
       }
       // ---- S4: o projection rows, added to the layer's input residual ------------------------------------
       wg_sync();
@@ -662,11 +698,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
         if (lane == 0) {
 #pragma unroll
           for (int i = 0; i < C::RW_O; i++)
-            if (i < o_wn)
-              put(c.cells, LY.e4 + o_w0 + i, S.hin[o_w0 + i] + y[i] * so[i], c.tick(f, l, 3));
+            if (i < o_wn) S.pub[C::RW_O * cw + i] = S.hin[o_w0 + i] + y[i] * bf2f(so[i]);
         }
+        publish<W>(S, c.cells, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
         if (tid == 0) c.tr(1, f, l, 5);
-        if (more) load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
+        load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
       }
       // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
       wg_sync();
@@ -678,12 +714,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
         if (lane == 0) {
 #pragma unroll
           for (int i = 0; i < C::RW_GU; i += 2)
-            put(c.cells, LY.e5 + (gu_w0 + i) / 2,
-                silu_mul(y[i] * sg[i] * inv, y[i + 1] * sg[i + 1] * inv),
-                c.tick(f, l, 4));
+            S.pub[(C::RW_GU * cw + i) / 2] = silu_mul(y[i] * bf2f(sg[i]) * inv, y[i + 1] * bf2f(sg[i + 1]) * inv);
         }
+        publish<W>(S, c.cells, LY.e5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
         if (tid == 0) c.tr(1, f, l, 6);
-        if (more) load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
+        load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
       }
       // ---- S6: down rows, added to the residual after o --------------------------------------------------
       wg_sync();
@@ -695,19 +730,20 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
 #pragma unroll
           for (int i = 0; i < C::RW_D; i++) {
             if (i < d_wn) {
-              const float hv = S.hmid[d_w0 + i] + y[i] * sd[i];
-              put(c.cells, LY.e6 + d_w0 + i, hv, c.tick(f, l, 5));
-              if (c.d.layer_out && f == c.n_frames - 1) c.d.layer_out[(size_t)l * H + d_w0 + i] = hv;
+              const float hv = S.hmid[d_w0 + i] + y[i] * bf2f(sd[i]);
+              S.pub[C::RW_D * cw + i] = hv;
+              if (c.d.layer_out && f == c.n_frames - 1) gstore(c.d.layer_out + (size_t)l * H + d_w0 + i, hv);
             }
           }
         }
+        publish<W>(S, c.cells, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
         if (tid == 0) c.tr(1, f, l, 7);
-        if (more) load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
+        load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
       }
     }
     // ---- head rows (loaded now; the final residual is a full layer away), processor, local argmax ----------
     uint4 wh[C::RW_HEAD][C::CH];
-    float sh[C::RW_HEAD];
+    uint16_t sh[C::RW_HEAD];
     load_rows<C::RW_HEAD, C::CH>(wh, sh, (const int8_t*)c.d.head_w, c.d.head_s, h_w0, h_wn, H, lane);
     wg_sync();
     if (S.flags[5]) return;
@@ -722,12 +758,12 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
         for (int i = 0; i < C::RW_HEAD; i++) {
           if (i >= h_wn) break;
           const int row = h_w0 + i;
-          float v = y[i] * sh[i] * inv;
-          if (c.d.logits && f == c.n_frames - 1) c.d.logits[row] = v;
+          float v = y[i] * bf2f(sh[i]) * inv;
+          if (c.d.logits && f == c.n_frames - 1) gstore(c.d.logits + row, v);
           if (c.d.talker_processor) {
-            if (c.d.seen && ((ld_u32_dev(c.d.seen, (uint32_t)row & ~3u) >> (8 * (row & 3))) & 0xffu))
+            if (c.d.seen && ((ld_u32_dev(uniform(c.d.seen), (uint32_t)row & ~3u) >> (8 * (row & 3))) & 0xffu))
               v = v < 0.f ? v * c.d.rep_pen : v / c.d.rep_pen;
-            if (c.d.suppress && c.d.suppress[row]) v = -INFINITY;
+            if (c.d.suppress && gload(c.d.suppress + row)) v = -INFINITY;
             if (block_eos && row == c.d.eos) v = -INFINITY;
           }
           if (v == v) { const uint64_t k = pick_key(v, row); best = k > best ? k : best; }
@@ -738,6 +774,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
     wg_sync();  // candidates ready for the control wave
     wg_sync();  // pick done
     if (S.flags[6]) return;
+    // The head dot already waited for the youngest loads; draining here keeps the next frame's first layer from
+    // inheriting a shallow wait count from this path.
+    __builtin_amdgcn_s_waitcnt(0);
   }
 }
 
@@ -761,7 +800,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n
       r = -1;
     }
     // every position this launch writes must lie inside the cache, and the start token inside the vocabulary
-    const int64_t pos0 = d.pos[0], tok0 = d.id0[0];
+    const int64_t pos0 = gload(d.pos), tok0 = gload(d.id0);
     if (pos0 < 0 || pos0 + n_frames > d.max_len || tok0 < 0 || tok0 >= d.vocab) {
       st_u32_dev(ws, Ws::kErr, 5u);
       r = -1;
@@ -769,6 +808,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n
     s_rank = r;
     s_base = ld_u32_dev(ws, Ws::kTick);
     for (int i = 0; i < 8; i++) S.flags[i] = 0;
+    S.pubcnt = 0;
   }
   __syncthreads();
   const int r = s_rank;
@@ -782,11 +822,11 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n
   c.g = (int)x * kPerXcd + r;
   c.base = s_base;
   c.tpf = (uint32_t)d.n_layers * 8u + 8u;
-  c.pos0 = (int)d.pos[0];
+  c.pos0 = (int)gload(d.pos);
   c.n_frames = n_frames;
   c.L = d.n_layers;
   for (int i = tid; i < d.n_layers * (int)(sizeof(sk_layer_desc) / 8); i += blockDim.x)
-    ((uint64_t*)S.desc)[i] = ((const uint64_t*)d.layers)[i];
+    ((uint64_t*)S.desc)[i] = gload((const uint64_t*)d.layers + i);
   __syncthreads();
   c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
   if (wave == W) run_control<H, I, W>(c, S, lane);
