@@ -80,8 +80,15 @@ __device__ __forceinline__ void wg_sync() {
 // ---- layout of the workspace (bytes) -------------------------------------------------------------------------
 struct Ws {
   // control words
-  static constexpr uint32_t kErr = 0, kTick = 4, kLaunch = 8, kDiag = 16, kTraceOn = 32, kCensus = 64;  // census: 8 counters
-  static constexpr int kTraceLayers = 32, kTraceEvents = 8;  // optional per-stage timestamps of frame 0
+  static constexpr uint32_t kErr = 0, kTick = 4, kLaunch = 8, kDiag = 16, kTraceOn = 32, kPollDelay = 36,
+                            kCensus = 64;  // census: 8 counters
+  // Polling of a stage's input starts this many sleep units (s_sleep 1: 64 shader clocks, ~27 ns at 2.4 GHz)
+  // after the workgroup published its own part of it. Reads that reach the cells before the producers' stores
+  // are visible come back stale and make the whole exchange slower than one late, successful read. Shader-clock
+  // sleeps, not the real-time counter: reading that counter is a scalar-memory round trip of ~0.7 us.
+  // The kPollDelay word overrides the default (value - 1) when non-zero.
+  static constexpr uint32_t kPollDelayDefault = 26;
+  static constexpr int kTraceLayers = 32, kTraceEvents = 16;  // optional per-stage timestamps of frame 0
   static constexpr uint32_t kCells = 256;
 };
 
@@ -149,19 +156,27 @@ struct Lds {
   uint64_t cand[W];
   int flags[8];
   int64_t tok;
+  uint32_t pubseq;  // stage publications completed by the compute waves
 };
 
 // Records a timeout: error code, then frame and layer of the stage that gave up (diagnostic words of the workspace).
 struct Ctx;
 __device__ void fail(const Ctx& c, uint32_t code, int f, int l);
 
+// GEMV inputs are staged in LDS swizzled: element i = 16 (L + 64 c) + 4 j + t, which lane L multiplies with byte
+// 4 j + t of its weight chunk c, sits at float4 slot (4 c + j) * 64 + L. Each 16-byte LDS read of the dot then
+// covers 64 consecutive slots, free of bank conflicts (the natural order puts lanes 64 bytes apart: 4-way).
+__device__ __forceinline__ int xsw(int i) {
+  return ((((i >> 10) << 2) | ((i >> 2) & 3)) << 8) | (((i >> 4) & 63) << 2) | (i & 3);
+}
+
 // Loads per lane in one polling round: the whole vector when it fits in 24 (96 registers of the control wave).
-constexpr int mb(int n) { return n / 128 < 24 ? n / 128 : 24; }
+constexpr int mb(int n) { return n / 128 < 16 ? n / 128 : 16; }
 
 // ---- control wave: poll cells into LDS ---------------------------------------------------------------------
 // Waits until cells [idx0, idx0 + n) (n even, idx0 even) all carry epoch e, copying the values to dst.
 // Returns false on timeout or when the global error word is set.
-template <int MAXB>
+template <int MAXB, bool SW = false>
 __device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, float* dst, void* ws, int lane,
                            const Ctx& c, uint32_t code, int f, int l) {
   for (uint32_t spin = 0;; spin++) {
@@ -178,8 +193,9 @@ __device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, 
         const int i = base + 128 * b + 2 * lane;
         if (i < n) {
           ok &= q[b].y == e && q[b].w == e;
-          dst[i] = __uint_as_float(q[b].x);
-          dst[i + 1] = __uint_as_float(q[b].z);
+          const int o = SW ? xsw(i) : i;  // i even: i + 1 lands at o + 1
+          dst[o] = __uint_as_float(q[b].x);
+          dst[o + 1] = __uint_as_float(q[b].z);
         }
       }
     }
@@ -213,17 +229,28 @@ __device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], uint16_t (&s)[RW], 
     s[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), (uint32_t)row * 2u, 0, 0);
   }
 }
-// y[r] = (row r) . xs, reduced over the wave (uniform result), without the row scale
+// y[r] = (row r) . xs, reduced over the wave (uniform result), without the row scale; xs is swizzled (xsw)
 template <int RW, int C>
 __device__ __forceinline__ void dot_rows(const uint4 (&w)[RW][C], const float* xs, int lane, float (&y)[RW]) {
   float acc[RW];
 #pragma unroll
   for (int r = 0; r < RW; r++) acc[r] = 0.f;
+  const float4* xs4 = (const float4*)xs;
 #pragma unroll
   for (int c = 0; c < C; c++) {
-    const float* xp = xs + 16 * (lane + 64 * c);
 #pragma unroll
-    for (int r = 0; r < RW; r++) acc[r] += dot_i8x16(w[r][c], xp);
+    for (int j = 0; j < 4; j++) {  // one quarter of the chunk (4 bytes per row) at a time: 4 live x registers
+      const float4 v = xs4[(4 * c + j) * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < RW; r++) {
+        const uint32_t q = j == 0 ? w[r][c].x : j == 1 ? w[r][c].y : j == 2 ? w[r][c].z : w[r][c].w;
+        float t = (float)(int8_t)q * v.x;
+        t = __builtin_fmaf((float)(int8_t)(q >> 8), v.y, t);
+        t = __builtin_fmaf((float)(int8_t)(q >> 16), v.z, t);
+        t = __builtin_fmaf((float)(int8_t)(q >> 24), v.w, t);
+        acc[r] += t;
+      }
+    }
   }
 #pragma unroll
   for (int r = 0; r < RW; r++) y[r] = wave_sum(acc[r]);
@@ -240,7 +267,24 @@ __device__ __forceinline__ void publish(L& S, void* cells, uint32_t idx0, int n,
   old = __builtin_amdgcn_readfirstlane(old);
   if (old % W == W - 1) {
     for (int i = 2 * lane; i < n; i += 128) put2(cells, idx0 + i, S.pub[i], S.pub[i + 1], e);
+    if (lane == 0) __hip_atomic_store(&S.pubseq, (old + 1) / W, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
+}
+
+// Sleeps n units of 64 shader clocks.
+__device__ __forceinline__ void sleep_units(uint32_t n) {
+  for (uint32_t i = 0; i < n; i++) __builtin_amdgcn_s_sleep(1);
+}
+// Control wave: waits in LDS (no memory traffic) until this workgroup's compute waves have completed `seq` stage
+// publications, then `delay` sleep units more. Bounded: a wait that outlasts ~30 ms falls through and the poll
+// that follows reports the error.
+template <class L>
+__device__ __forceinline__ void after_publish(L& S, uint32_t seq, uint32_t delay) {
+  for (uint32_t i = 0; i < (1u << 20); i++) {
+    if (__hip_atomic_load(&S.pubseq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= seq) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  sleep_units(delay);
 }
 
 // Position bookkeeping of a frame for this workgroup's attention chunk.
@@ -288,9 +332,14 @@ struct Ctx {
   uint32_t base, tpf;
   int pos0, n_frames, L;
   uint64_t* trace;  // per-stage timestamps of frame 0 (null when tracing is off)
+  uint32_t delay;   // poll start delay, ticks
   __device__ void tr(int role, int f, int l, int ev) const {
     if (trace && f == 0 && l < Ws::kTraceLayers)
       trace[(((size_t)g * 2 + role) * Ws::kTraceLayers + l) * Ws::kTraceEvents + ev] = (uint64_t)wall_clock64();
+  }
+  __device__ void tr_clk(int role, int f, int l, int ev) const {  // shader clock counter instead of wall clock
+    if (trace && f == 0 && l < Ws::kTraceLayers)
+      trace[(((size_t)g * 2 + role) * Ws::kTraceLayers + l) * Ws::kTraceEvents + ev] = (uint64_t)clock64();
   }
   __device__ uint32_t tick(int f, int l, int s) const {
     return base + 1u + (uint32_t)f * tpf + (uint32_t)l * 8u + (uint32_t)s;
@@ -325,10 +374,10 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
     const Chunk ck(pos, c.r);
     for (int l = 0; l < c.L; l++) {
       const sk_layer_desc& Ly = S.desc[l];
-      // this layer's norm weights, in registers before any poll (lane holds elements lane + 64 k)
-      float nin[H / 64], npost[H / 64];
+      // the input norm weights, in registers before the poll (lane holds elements lane + 64 k)
+      float nin[H / 64];
 #pragma unroll
-      for (int k = 0; k < H / 64; k++) { nin[k] = gload(Ly.in_norm + lane + 64 * k); npost[k] = gload(Ly.post_norm + lane + 64 * k); }
+      for (int k = 0; k < H / 64; k++) nin[k] = gload(Ly.in_norm + lane + 64 * k);
       // S1 input: embedding row (layer 0) or the previous layer's residual, times the input norm
       bool ok = true;
       if (lane == 0) c.tr(0, f, l, 0);
@@ -339,17 +388,19 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
 #pragma unroll
         for (int k = 0; k < H / 64; k++) S.hin[lane + 64 * k] = ev[k];
       } else {
+        after_publish(S, (uint32_t)(f * c.L + l) * 4u, c.delay);  // own part of the previous layer's down output
         ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
       }
       float ss = 0.f;
       for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
       ss = wave_sum(ss);
 #pragma unroll
-      for (int k = 0; k < H / 64; k++) S.xs[0][lane + 64 * k] = S.hin[lane + 64 * k] * nin[k];
+      for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hin[lane + 64 * k] * nin[k];
       if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[0] = !ok; c.tr(0, f, l, 1); }
       wg_sync();
       if (!ok) return;
       // S2 input: this head's q/k/v
+      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 1u, c.delay);
       ok = poll_cells<mb(512)>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
       if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
@@ -360,6 +411,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
       {
         const uint32_t e = c.tick(f, l, 1);
         const int mh = c.r >> 4, md0 = 8 * (c.r & 15);
+        sleep_units(c.delay);  // the compute waves publish their partial right after the last attention barrier
         for (uint32_t spin = 0;; spin++) {
           bool good = true;
           // per chunk 5 cell pairs: (m, l) of head mh, then 4 pairs of its o slice; all loads issued first
@@ -389,38 +441,57 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
           }
           __builtin_amdgcn_s_sleep(1);
         }
-        if (ok && lane < 8) {
-          float M = -INFINITY;
-          for (int ch = 0; ch < kChunks; ch++) M = fmaxf(M, S.mrg[ch][0]);
-          float Lw = 0.f, O = 0.f;
-          for (int ch = 0; ch < kChunks; ch++) {
-            const float mc = S.mrg[ch][0];
-            if (mc == -INFINITY) continue;
-            const float fct = expf(mc - M);
-            Lw = __builtin_fmaf(fct, S.mrg[ch][1], Lw);
-            O = __builtin_fmaf(fct, S.mrg[ch][2 + lane], O);
+        if (lane == 0) c.tr(0, f, l, 8);
+        if (ok) {
+          // lane = chunk + 32 * half: one exp per chunk, then wave reductions; half hh produces dims
+          // md0 + 4 hh .. md0 + 4 hh + 3 (empty chunks carry m = -inf and weigh nothing)
+          static_assert(kChunks == 32, "merge lane mapping");
+          const int ch = lane & 31, hh = lane >> 5;
+          const float mc = S.mrg[ch][0];
+          const float M = wave_max(mc);
+          const float fct = mc == -INFINITY ? 0.f : expf(mc - M);
+          const float Lw = wave_sum(hh == 0 ? fct * S.mrg[ch][1] : 0.f);
+          float od[4];
+#pragma unroll
+          for (int d = 0; d < 4; d++) {
+            const float v = row16_sum(fct * S.mrg[ch][2 + 4 * hh + d]);
+            const float h0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+            const float h1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+            od[d] = Lw > 0.f ? (hh ? h1 : h0) / Lw : 0.f;
           }
-          put(c.cells, LY.e3 + (2 * c.x + mh) * SK_HD + md0 + lane, Lw > 0.f ? O / Lw : 0.f, c.tick(f, l, 2));
+          if (ch == 0) {
+            const uint32_t o0 = LY.e3 + (2 * c.x + mh) * SK_HD + md0 + 4 * hh, e3 = c.tick(f, l, 2);
+            put2(c.cells, o0, od[0], od[1], e3);
+            put2(c.cells, o0 + 2, od[2], od[3], e3);
+          }
         }
+        sleep_units(c.delay);  // S4 input: the merges of all workgroups, this one's included
         if (lane == 0) c.tr(0, f, l, 4);
       }
       // S4 input: the whole attention output
-      ok = ok && poll_cells<mb(kQ)>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
+      ok = ok && poll_cells<mb(kQ), true>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
       if (lane == 0) { S.flags[2] = !ok; c.tr(0, f, l, 5); }
       wg_sync();
       if (!ok) return;
-      // S5 input: residual after o, times the post-attention norm
+      // S5 input: residual after o, times the post-attention norm (loaded while the exchange is under way)
+      float npost[H / 64];
+#pragma unroll
+      for (int k = 0; k < H / 64; k++) npost[k] = gload(Ly.post_norm + lane + 64 * k);
+      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 2u, c.delay);
       ok = poll_cells<mb(H)>(c.cells, LY.e4, H, c.tick(f, l, 3), S.hmid, c.ws, lane, c, 15u, f, l);
       ss = 0.f;
       for (int i = lane; i < H; i += 64) { const float v = S.hmid[i]; ss += v * v; }
       ss = wave_sum(ss);
 #pragma unroll
-      for (int k = 0; k < H / 64; k++) S.xs[0][lane + 64 * k] = S.hmid[lane + 64 * k] * npost[k];
+      for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hmid[lane + 64 * k] * npost[k];
       if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[3] = !ok; c.tr(0, f, l, 6); }
       wg_sync();
       if (!ok) return;
       // S6 input: the whole SwiGLU activation
-      ok = poll_cells<mb(I)>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 3u, c.delay);
+      ok = poll_cells<mb(I), true>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
       if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
       wg_sync();
       if (!ok) return;
@@ -429,12 +500,13 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
     float nfin[H / 64];
 #pragma unroll
     for (int k = 0; k < H / 64; k++) nfin[k] = gload(c.d.norm + lane + 64 * k);
+    after_publish(S, (uint32_t)((f + 1) * c.L) * 4u, c.delay);
     bool ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
     float ss = 0.f;
     for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
     ss = wave_sum(ss);
 #pragma unroll
-    for (int k = 0; k < H / 64; k++) S.xs[0][lane + 64 * k] = S.hin[lane + 64 * k] * nfin[k];
+    for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hin[lane + 64 * k] * nfin[k];
     if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[5] = !ok; }
     wg_sync();
     if (!ok) return;
@@ -448,6 +520,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
     // pick: reduce the 256 candidates
     {
       const uint32_t e = c.tick(f, c.L, 0);
+      sleep_units(c.delay);
       uint64_t best = 0;
       for (uint32_t spin = 0;; spin++) {
         bool good = true;
@@ -564,6 +637,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
       {
         float y[C::RW_QKV];
         dot_rows<C::RW_QKV, C::CH>(wq, S.xs[0], lane, y);
+        if (tid == 0) c.tr(1, f, l, 8);
         const float inv = S.inv;
         if (lane == 0) {
 #pragma unroll
@@ -694,7 +768,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
       if (tid == 0) c.tr(1, f, l, 4);
       {
         float y[C::RW_O];
+        if (tid == 0) c.tr_clk(1, f, l, 14);
         dot_rows<C::RW_O, C::CQ>(wo, S.xs[1], lane, y);
+        if (tid == 0) c.tr(1, f, l, 9);
+        if (tid == 0) c.tr_clk(1, f, l, 15);
         if (lane == 0) {
 #pragma unroll
           for (int i = 0; i < C::RW_O; i++)
@@ -707,9 +784,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
       // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
       wg_sync();
       if (S.flags[3]) return;
+      if (tid == 0) c.tr(1, f, l, 12);
       {
         float y[C::RW_GU];
         dot_rows<C::RW_GU, C::CH>(wg, S.xs[0], lane, y);
+        if (tid == 0) c.tr(1, f, l, 10);
         const float inv = S.inv;
         if (lane == 0) {
 #pragma unroll
@@ -723,9 +802,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
       // ---- S6: down rows, added to the residual after o --------------------------------------------------
       wg_sync();
       if (S.flags[4]) return;
+      if (tid == 0) c.tr(1, f, l, 13);
       {
         float y[C::RW_D];
         dot_rows<C::RW_D, C::CI>(wd, S.xs[1], lane, y);
+        if (tid == 0) c.tr(1, f, l, 11);
         if (lane == 0) {
 #pragma unroll
           for (int i = 0; i < C::RW_D; i++) {
@@ -809,6 +890,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n
     s_base = ld_u32_dev(ws, Ws::kTick);
     for (int i = 0; i < 8; i++) S.flags[i] = 0;
     S.pubcnt = 0;
+    S.pubseq = 0;
   }
   __syncthreads();
   const int r = s_rank;
@@ -828,6 +910,10 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n
   for (int i = tid; i < d.n_layers * (int)(sizeof(sk_layer_desc) / 8); i += blockDim.x)
     ((uint64_t*)S.desc)[i] = gload((const uint64_t*)d.layers + i);
   __syncthreads();
+  {
+    const uint32_t pd = ld_u32_dev(ws, Ws::kPollDelay);
+    c.delay = pd ? pd - 1 : Ws::kPollDelayDefault;
+  }
   c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
   if (wave == W) run_control<H, I, W>(c, S, lane);
   else run_compute<H, I, W>(c, S, wave, tid, lane);
