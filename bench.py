@@ -29,6 +29,18 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
+TRAFFIC_PROFILE = ROOT / "profiles" / "k_frames_talker06b_traffic.md"
+
+
+def measured_traffic(name: str, engine: str):
+    """HBM bytes per launch of the frame kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (calibrated against a plain copy of known size), or None when no summary covers this workload."""
+    if name != "talker06b" or engine != "frames" or not TRAFFIC_PROFILE.exists():
+        return None
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
 
 
 def algorithmic_bytes(s, T: int, wd: str = "i8row") -> dict:
@@ -52,7 +64,8 @@ def algorithmic_bytes(s, T: int, wd: str = "i8row") -> dict:
 
 
 def time_kernels(eng, reps: int = 200) -> dict:
-    """Average duration of each per-op launch kind of one layer, timed with HIP events on the launch stream."""
+    """Average duration of each per-op launch kind of one layer: `reps` launches captured in one HIP graph and
+    replayed, timed with HIP events on the replay stream (so host launch overhead is not counted)."""
     import torch
 
     P = eng.T
@@ -65,13 +78,22 @@ def time_kernels(eng, reps: int = 200) -> dict:
         "down": lambda: eng._gemv(eng.act_t, L["down"], None, eng.ph32, False),
     }
     out = {}
+    side = torch.cuda.Stream()
     for name, fn in calls.items():
-        for _ in range(10):
-            fn()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(reps):
-            fn()
+        g.replay()
         e1.record()
         torch.cuda.synchronize()
         out[name] = e0.elapsed_time(e1) * 1e3 / reps  # us
@@ -117,6 +139,9 @@ def main() -> None:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--engine", default="frames", choices=["frames", "graph", "multi"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="after the run, copy this many MiB device-to-device twice (a plain copy of known size that "
+                         "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the talker decode step at batch 1 runs on a single MI355X "
@@ -192,7 +217,8 @@ def main() -> None:
         launch_us = sum(a.elapsed_time(b) for a, b in ev) * 1e3 / len(ev)
         roof = {"bound": "hbm", "kernel": "k_frames (sk_talker_frames, 64 frames per launch)",
                 "achieved": round(step_bytes / (launch_us * 1e-6) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "traffic": None, "bytes_per_launch": int(step_bytes), "avg_launch_us": round(launch_us, 2)}
+                "traffic": measured_traffic(name, args.engine), "bytes_per_launch": int(step_bytes),
+                "avg_launch_us": round(launch_us, 2)}
         roof["frac"] = round(roof["achieved"] / PEAK_HBM_GBS, 4)
         extra = {}
     else:
@@ -230,6 +256,12 @@ def main() -> None:
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(name, args.seed)
     print(json.dumps(res), flush=True)
+    if args.calibration_copy_mib > 0:
+        src = torch.randint(0, 255, (args.calibration_copy_mib << 20,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
 
 if __name__ == "__main__":
