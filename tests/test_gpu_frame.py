@@ -109,3 +109,30 @@ def test_bad_position_is_an_error_not_a_write(gpu):
     eng.run_frames(2)
     torch.cuda.synchronize()
     assert eng.frame_error() == 0, eng.frame_diag()
+
+
+@pytest.mark.timeout(900)
+def test_talker17b_64_frames_one_launch(gpu):
+    """The 1.7B shape (hidden 2048, intermediate 6144, KV 1024): per-layer residuals of frame 0, then the
+    remaining 63 frames in one launch, against the oracle fixture."""
+    print("talker17b: building the seeded 1.7B weights on the host (about a minute), then 64 frames", flush=True)
+    meta = json.loads((GOLD / "talker17b_seed0.json").read_text())
+    gold = np.load(GOLD / "talker17b_seed0.npz")
+    eng, tok = _engine("talker17b", 0, gpu)
+    assert tok == meta["start_token"]
+    eng.layer_out = torch.zeros((28, 2048), device=gpu)
+    eng.run_frames(1)
+    torch.cuda.synchronize()
+    assert eng.frame_error() == 0, eng.frame_diag()
+    errs = [rel_err(eng.layer_out[i], gold["layer_out0"][i]) for i in range(28)]
+    print(f"per-layer max rel err {max(errs):.3e}", flush=True)
+    assert max(errs) < TOL
+    assert rel_err(eng.logit_t.view(-1), gold["logits_first"]) < TOL
+    assert int(eng.frame_ids[0]) == meta["codes"][0]
+    eng.layer_out = None
+    eng.run_frames(63)
+    torch.cuda.synchronize()
+    assert eng.frame_error() == 0, eng.frame_diag()
+    codes = [meta["codes"][0]] + eng.frame_ids[:63].cpu().tolist()
+    assert codes == meta["codes"]
+    assert rel_err(eng.logit_t.view(-1), gold["logits_last"]) < TOL
