@@ -165,6 +165,39 @@ int64_t sk_talker_workspace_size(int hidden, int inter);
  * (codec_head) and sample (qwen3/sampler.py:37-159 with do_sample = 0). */
 int sk_talker_frames(const sk_talker_desc* desc, int n_frames, void* stream);
 
+/* The code predictor of one frame, all device pointers. `layers` holds its decoder stack (kc / vc are
+ * [nkv][n_positions][128] bf16). emb / head_w / head_s are device arrays of n_positions pointers: position 0 takes
+ * the vector x0 (the talker's last hidden state after its final norm) and has no head; position g >= 1 takes row
+ * codes[g - 1] of table emb[g] (bf16 [rows][hidden]; codes[0] = *id0 must be < emb0_rows) and ends in the final
+ * norm, head g (int8 [vocab][hidden] + bf16 row scales) and a greedy pick (lowest index wins ties) into codes[g]. */
+typedef struct sk_cp_desc {
+  int n_layers, hidden, inter, nq, nkv, vocab, n_positions, wd, ct;
+  float eps;
+  const sk_layer_desc* layers;
+  const float* norm;          /* final RMSNorm weight [hidden], applied before every head */
+  const float* rope;          /* [n_positions][cos 64 | sin 64] */
+  const float* x0;            /* position 0 input, fp32 [hidden] */
+  const int64_t* id0;         /* code 0 */
+  int emb0_rows;
+  const void* const* emb;
+  const void* const* head_w;
+  const void* const* head_s;
+  int64_t* codes;             /* [n_positions]: codes[0] = code 0, codes[g] = the pick at position g */
+  float* logits;              /* optional: head output of the last position (before the pick) */
+  float* layer_out;           /* optional: [n_layers][hidden] residual after every layer at the last position */
+  void* workspace;            /* sk_talker_workspace_size(hidden, inter) bytes, zeroed as for sk_talker_frames */
+  int64_t workspace_bytes;
+} sk_cp_desc;
+
+/* All positions of the code predictor of one frame in ONE launch (the persistent kernel of sk_talker_frames in
+ * its code-predictor mode): greedy sub-codes 1..n_positions-1. Supports the Qwen3-TTS code predictor shape:
+ * hidden 1024, intermediate 3072, 16 q / 8 kv heads, vocab 2048, i8row weights, bf16 cache, a 256-CU device.
+ * Replaces, for greedy sub-codes, the code-predictor loop of Qwen3Kernels._frame (qwen3/kernels.py:666-675) with
+ * _cp_first / _cp_input (qwen3/kernels.py:629-655), _layers (619-627), rms_gemv over cp_heads[g - 1] and sample
+ * (qwen3/sampler.py:37-159 with do_sample = 0, no processor). Positions 0 and 1 run one after the other (the
+ * reference can pair them, qwen3/kernels.py:600-617, with the same result). */
+int sk_cp_frame(const sk_cp_desc* desc, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

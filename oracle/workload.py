@@ -59,3 +59,21 @@ def talker_oracle(name: str, seed: int = 0, wd: str = "i8row", max_len: int | No
     weights = {"layers": layers, "norm": f["norm"], "head": O.quantize(f["head"], wd)[2], "emb": f["emb"],
                "rope": O.rope_table(syn.inv_freq(s), max_len), "eps": s.eps, "nq": s.nq, "nkv": s.nkv}
     return O.TalkerOracle(weights, K, V, cache_bf16), syn.start_token(seed, s), s
+
+
+def cp_oracle(name: str = "cp06b", seed: int = 0, wd: str = "i8row", cache_bf16: bool = True,
+              digests: dict | None = None):
+    """Returns (CodePredictorOracle, shape) for a code-predictor workload, weights quantised by the oracle."""
+    spec = syn.WORKLOADS[name]
+    s = syn.workload_shape(name)
+    n = spec["positions"]
+    w = syn.cp_weights(seed, s, n)
+    if digests is not None:
+        digests["layer0.q"] = syn.sha256(w["layers"][0]["q"])
+        digests["head1"] = syn.sha256(w["heads"][0])
+        digests["cemb2"] = syn.sha256(w["cemb"][0])
+        digests["temb"] = syn.sha256(w["temb"])
+    weights = {"layers": [pack_layer(L, wd) for L in w["layers"]], "norm": w["norm"],
+               "heads": [O.quantize(h, wd)[2] for h in w["heads"]], "cemb": w["cemb"], "temb": w["temb"],
+               "rope": O.rope_table(syn.inv_freq(s), n), "eps": s.eps, "nq": s.nq, "nkv": s.nkv}
+    return O.CodePredictorOracle(weights, n, cache_bf16), s

@@ -56,8 +56,19 @@ class SkTalkerDesc(ctypes.Structure):
                 ("layer_out", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_int64)]
 
 
+class SkCpDesc(ctypes.Structure):
+    """Mirror of ``sk_cp_desc`` (include/sokutou_amd.h)."""
+    _fields_ = [("n_layers", c_int), ("hidden", c_int), ("inter", c_int), ("nq", c_int), ("nkv", c_int),
+                ("vocab", c_int), ("n_positions", c_int), ("wd", c_int), ("ct", c_int), ("eps", c_float),
+                ("layers", c_void_p), ("norm", c_void_p), ("rope", c_void_p), ("x0", c_void_p), ("id0", c_void_p),
+                ("emb0_rows", c_int), ("emb", c_void_p), ("head_w", c_void_p), ("head_s", c_void_p),
+                ("codes", c_void_p), ("logits", c_void_p), ("layer_out", c_void_p), ("workspace", c_void_p),
+                ("workspace_bytes", c_int64)]
+
+
 _SIGS["sk_talker_workspace_size"] = (c_int64, [c_int, c_int])
 _SIGS["sk_talker_frames"] = (c_int, [ctypes.POINTER(SkTalkerDesc), c_int, _P])
+_SIGS["sk_cp_frame"] = (c_int, [ctypes.POINTER(SkCpDesc), _P])
 
 _lib = None
 

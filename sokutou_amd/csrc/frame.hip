@@ -39,8 +39,7 @@ constexpr int kXcd = 8, kPerXcd = 32, kWG = kXcd * kPerXcd;
 constexpr int kChunks = kPerXcd;           // attention split of the cache length per head
 constexpr int kPartN = 4 + 2 * SK_HD;      // m0 l0 m1 l1 o0[128] o1[128]
 constexpr int kNQ = 16, kNKV = 8, kQKV = (kNQ + 2 * kNKV) * SK_HD, kQ = kNQ * SK_HD;
-constexpr int kV = 3072;                   // codec vocabulary
-constexpr int kHeadRows = kV / kWG;        // 12
+constexpr int kTalkerV = 3072;             // talker codec vocabulary
 constexpr uint32_t kSpinLimit = 1u << 19;
 constexpr float kInvSqrtHd = 0.08838834764831845f;
 
@@ -120,11 +119,12 @@ __device__ __forceinline__ uint64_t pick_key(float v, int i) {
   return ((uint64_t)k << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
 }
 
-template <int H, int I, int W>
+template <int H, int I, int W, int V, bool CP>
 struct Cfg {
   static constexpr int R_O = H / kWG, R_GU = 2 * I / kWG, R_D = H / kWG;
   static constexpr int RW_QKV = 16 / W;                       // rows per compute wave
   static constexpr int RW_O = (R_O + W - 1) / W, RW_GU = R_GU / W, RW_D = (R_D + W - 1) / W;
+  static constexpr int kHeadRows = V / kWG;                   // head rows per workgroup: 12 (talker), 8 (code predictor)
   static constexpr int RW_HEAD = (kHeadRows + W - 1) / W;
   static constexpr int CH = H / 1024, CQ = kQ / 1024, CI = I / 1024;  // 16-byte chunks per lane per row
   static constexpr int KVL = 2;                                // K (and V) loads per lane
@@ -134,7 +134,7 @@ struct Cfg {
 };
 
 // LDS of the frame kernel
-template <int H, int I, int W>
+template <int H, int I, int W, int V, bool CP>
 struct Lds {
   static constexpr int XS = I > kQ ? I : kQ;
   float hin[H];        // residual entering the layer (S1; read back by S4), or the final residual (head)
@@ -144,7 +144,7 @@ struct Lds {
   float qkv[512];      // S2: q0 | q1 | k | v of this workgroup's head
   float qs[2][SK_HD];  // normalised, rotated, scaled q
   float kn[SK_HD], vn[SK_HD];
-  float sc[2][Cfg<H, I, W>::kMaxChunk];
+  float sc[2][Cfg<H, I, W, V, CP>::kMaxChunk];
   float red[32];
   float opart[W][4][16][17];
   float mrg[kChunks][10];  // S3 inputs per chunk: m, l, o[8] of one q head
@@ -322,9 +322,21 @@ __device__ __forceinline__ void unpack8(uint4 a, float* o) {
   o[4] = bf2f(a.z & 0xffffu); o[5] = bf2f(a.z >> 16); o[6] = bf2f(a.w & 0xffffu); o[7] = bf2f(a.w >> 16);
 }
 
+// Code-predictor launch (CP): per-position inputs and heads. Position 0 takes the vector x0, position g >= 1
+// the row of table emb[g] chosen by the previous code (code 0 for g = 1) and ends in head g; the codes go to
+// d.out. Unused (all null) for the talker.
+struct CpArgs {
+  const float* x0;
+  const void* const* emb;     // [n_positions] device array of bf16 tables; [0] unused
+  const void* const* head_w;  // [n_positions] int8 heads; [0] unused
+  const void* const* head_s;  // [n_positions] bf16 row scales
+  int emb0_rows;              // rows of emb[1] (the range code 0 must lie in)
+};
+
 // Everything a role function needs about this workgroup and launch.
 struct Ctx {
   sk_talker_desc d;
+  CpArgs cp;
   void* ws;
   char* cells;
   uint32_t x;     // XCD = kv head
@@ -363,12 +375,13 @@ __device__ __forceinline__ int attn_barriers(const Chunk& ck) { return 4 + (ck.n
 // ================================================================================================================
 // Control wave
 // ================================================================================================================
-template <int H, int I, int W>
-__device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
+template <int H, int I, int W, int V, bool CP>
+__device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
   const Layout LY(H, I);
   const float eps = c.d.eps;
   const bf16_t* emb = (const bf16_t*)c.d.emb;
   int64_t tok = gload(c.d.id0);
+  if (CP && c.g == 0 && lane == 0 && c.d.out) gstore(c.d.out, tok);  // code 0 passes through
   for (int f = 0; f < c.n_frames; f++) {
     const int pos = c.pos0 + f;
     const Chunk ck(pos, c.r);
@@ -383,8 +396,14 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
       if (lane == 0) c.tr(0, f, l, 0);
       if (l == 0) {
         float ev[H / 64];
+        if (CP && f == 0) {
 #pragma unroll
-        for (int k = 0; k < H / 64; k++) ev[k] = bf2f(gload(emb + (size_t)tok * H + lane + 64 * k));
+          for (int k = 0; k < H / 64; k++) ev[k] = gload(c.cp.x0 + lane + 64 * k);
+        } else {
+          const bf16_t* tab = CP ? (const bf16_t*)uniform(gload(c.cp.emb + f)) : emb;
+#pragma unroll
+          for (int k = 0; k < H / 64; k++) ev[k] = bf2f(gload(tab + (size_t)tok * H + lane + 64 * k));
+        }
 #pragma unroll
         for (int k = 0; k < H / 64; k++) S.hin[lane + 64 * k] = ev[k];
       } else {
@@ -496,6 +515,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
       wg_sync();
       if (!ok) return;
     }
+    if (CP && f == 0) continue;  // the code predictor's position 0 has no head
     // head input: final residual times the final norm
     float nfin[H / 64];
 #pragma unroll
@@ -561,7 +581,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
       }
     }
   }
-  if (c.g == 0 && lane == 0) {
+  if (!CP && c.g == 0 && lane == 0) {
     if (ld_u32_dev(c.ws, Ws::kErr) == 0) {
       gstore(c.d.id0, tok);
       if (c.d.next_id0) gstore(c.d.next_id0, tok);
@@ -574,9 +594,9 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W>& S, int lane) {
 // ================================================================================================================
 // Compute waves
 // ================================================================================================================
-template <int H, int I, int W>
-__device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int lane) {
-  using C = Cfg<H, I, W>;
+template <int H, int I, int W, int V, bool CP>
+__device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
+  using C = Cfg<H, I, W, V, CP>;
   const Layout LY(H, I);
   const float eps = c.d.eps;
   const int ag = lane >> 4, asl = lane & 15;
@@ -590,7 +610,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
   const int o_w0 = C::R_O * g + C::RW_O * cw, o_wn = max(0, min(C::RW_O, C::R_O - C::RW_O * cw));
   const int gu_w0 = C::R_GU * g + C::RW_GU * cw;
   const int d_w0 = C::R_D * g + C::RW_D * cw, d_wn = max(0, min(C::RW_D, C::R_D - C::RW_D * cw));
-  const int h_w0 = kHeadRows * g + C::RW_HEAD * cw, h_wn = max(0, min(C::RW_HEAD, kHeadRows - C::RW_HEAD * cw));
+  const int h_w0 = C::kHeadRows * g + C::RW_HEAD * cw, h_wn = max(0, min(C::RW_HEAD, C::kHeadRows - C::RW_HEAD * cw));
   // the attention thread mapping uses the first 256 compute threads: head p = t / 128, dim dd = t % 128
   const int p = tid >> 7, dd = tid & 127;
   const bool att_thread = tid < 256;
@@ -822,10 +842,16 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
         load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
       }
     }
+    if (CP && f == 0) {  // the code predictor's position 0 has no head
+      __builtin_amdgcn_s_waitcnt(0);  // same drain as after a head (see below)
+      continue;
+    }
     // ---- head rows (loaded now; the final residual is a full layer away), processor, local argmax ----------
     uint4 wh[C::RW_HEAD][C::CH];
     uint16_t sh[C::RW_HEAD];
-    load_rows<C::RW_HEAD, C::CH>(wh, sh, (const int8_t*)c.d.head_w, c.d.head_s, h_w0, h_wn, H, lane);
+    const int8_t* hw = CP ? (const int8_t*)uniform(gload(c.cp.head_w + f)) : (const int8_t*)c.d.head_w;
+    const uint16_t* hsc = CP ? (const uint16_t*)uniform(gload(c.cp.head_s + f)) : c.d.head_s;
+    load_rows<C::RW_HEAD, C::CH>(wh, sh, hw, hsc, h_w0, h_wn, H, lane);
     wg_sync();
     if (S.flags[5]) return;
     {
@@ -861,10 +887,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W>& S, int cw, int tid, int 
   }
 }
 
-template <int H, int I, int W>
-__global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n_frames) {
+template <int H, int I, int W, int V, bool CP>
+__global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArgs cp, int n_frames) {
   extern __shared__ char smem_raw[];
-  Lds<H, I, W>& S = *(Lds<H, I, W>*)smem_raw;
+  Lds<H, I, W, V, CP>& S = *(Lds<H, I, W, V, CP>*)smem_raw;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   void* ws = d.workspace;
   // ---- placement: XCD from hardware, dense rank from an arrival counter ------------------------------------
@@ -881,8 +907,8 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n
       r = -1;
     }
     // every position this launch writes must lie inside the cache, and the start token inside the vocabulary
-    const int64_t pos0 = gload(d.pos), tok0 = gload(d.id0);
-    if (pos0 < 0 || pos0 + n_frames > d.max_len || tok0 < 0 || tok0 >= d.vocab) {
+    const int64_t pos0 = d.pos ? gload(d.pos) : 0, tok0 = gload(d.id0);
+    if (pos0 < 0 || pos0 + n_frames > d.max_len || tok0 < 0 || tok0 >= (CP ? cp.emb0_rows : d.vocab)) {
       st_u32_dev(ws, Ws::kErr, 5u);
       r = -1;
     }
@@ -897,6 +923,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n
   if (r < 0) return;
   Ctx c;
   c.d = d;
+  c.cp = cp;
   c.ws = ws;
   c.cells = (char*)ws + Ws::kCells;
   c.x = x;
@@ -904,7 +931,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n
   c.g = (int)x * kPerXcd + r;
   c.base = s_base;
   c.tpf = (uint32_t)d.n_layers * 8u + 8u;
-  c.pos0 = (int)gload(d.pos);
+  c.pos0 = d.pos ? (int)gload(d.pos) : 0;
   c.n_frames = n_frames;
   c.L = d.n_layers;
   for (int i = tid; i < d.n_layers * (int)(sizeof(sk_layer_desc) / 8); i += blockDim.x)
@@ -915,24 +942,24 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, int n
     c.delay = pd ? pd - 1 : Ws::kPollDelayDefault;
   }
   c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
-  if (wave == W) run_control<H, I, W>(c, S, lane);
-  else run_compute<H, I, W>(c, S, wave, tid, lane);
+  if (wave == W) run_control<H, I, W, V, CP>(c, S, lane);
+  else run_compute<H, I, W, V, CP>(c, S, wave, tid, lane);
   // ---- end of launch: epoch base and launch count (workgroup 0; every workgroup finished its census) --------
   if (c.g == 0 && tid == 0) {
     st_u32_dev(ws, Ws::kTick, c.base + (uint32_t)n_frames * c.tpf);
     st_u32_dev(ws, Ws::kLaunch, ld_u32_dev(ws, Ws::kLaunch) + 1u);
   }
 }
-template <int H, int I, int W>
-int launch_frames(const sk_talker_desc* d, int n_frames, hipStream_t st) {
-  if (d->max_len > Cfg<H, I, W>::kMaxLen) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: max_len too long");
-  const size_t lds = sizeof(Lds<H, I, W>) < 96 * 1024 ? 96 * 1024 : sizeof(Lds<H, I, W>);  // one workgroup per CU
+template <int H, int I, int W, int V, bool CP>
+int launch_frames(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
+  if (d->max_len > Cfg<H, I, W, V, CP>::kMaxLen) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: max_len too long");
+  const size_t lds = sizeof(Lds<H, I, W, V, CP>) < 96 * 1024 ? 96 * 1024 : sizeof(Lds<H, I, W, V, CP>);  // one workgroup per CU
   static bool attr_set = false;
   if (!attr_set) {
-    hipFuncSetAttribute((const void*)k_frames<H, I, W>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)k_frames<H, I, W, V, CP>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_frames<H, I, W>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, n_frames);
+  hipLaunchKernelGGL((k_frames<H, I, W, V, CP>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp, n_frames);
   return sk_check_launch(hipGetLastError(), "sk_talker_frames");
 }
 
@@ -946,7 +973,7 @@ extern "C" int64_t sk_talker_workspace_size(int hidden, int inter) {
 
 extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* stream) {
   if (!d || n_frames <= 0) return sk_set_error(SK_EINVAL, "sk_talker_frames: bad arguments");
-  if (d->nq != kNQ || d->nkv != kNKV || d->vocab != kV || d->wd != SK_WD_I8ROW || d->ct != SK_CT_BF16)
+  if (d->nq != kNQ || d->nkv != kNKV || d->vocab != kTalkerV || d->wd != SK_WD_I8ROW || d->ct != SK_CT_BF16)
     return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs 16 q / 8 kv heads, vocab 3072, i8row, bf16 cache");
   if (!d->layers || !d->norm || !d->head_w || !d->head_s || !d->emb || !d->rope || !d->id0 || !d->pos || !d->workspace)
     return sk_set_error(SK_EINVAL, "sk_talker_frames: null pointer");
@@ -959,7 +986,35 @@ extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* str
   hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (cus != kWG) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs a 256-CU device (8 XCDs x 32)");
   hipStream_t st = (hipStream_t)stream;
-  if (d->hidden == 1024 && d->inter == 3072) return launch_frames<1024, 3072, 4>(d, n_frames, st);
-  if (d->hidden == 2048 && d->inter == 6144) return launch_frames<2048, 6144, 8>(d, n_frames, st);
+  const CpArgs none{};
+  if (d->hidden == 1024 && d->inter == 3072) return launch_frames<1024, 3072, 4, kTalkerV, false>(d, none, n_frames, st);
+  if (d->hidden == 2048 && d->inter == 6144) return launch_frames<2048, 6144, 8, kTalkerV, false>(d, none, n_frames, st);
   return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: shapes other than the 0.6B / 1.7B talker");
+}
+
+extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
+  if (!d) return sk_set_error(SK_EINVAL, "sk_cp_frame: bad arguments");
+  if (d->nq != kNQ || d->nkv != kNKV || d->vocab != 2048 || d->hidden != 1024 || d->inter != 3072 ||
+      d->wd != SK_WD_I8ROW || d->ct != SK_CT_BF16)
+    return sk_set_error(SK_EUNSUPPORTED,
+                        "sk_cp_frame: needs hidden 1024, intermediate 3072, 16 q / 8 kv heads, vocab 2048, i8row, bf16 cache");
+  if (d->n_positions < 2 || d->n_positions > 64 || d->n_layers <= 0 || d->n_layers > Ws::kTraceLayers)
+    return sk_set_error(SK_EUNSUPPORTED, "sk_cp_frame: 2..64 positions and 1..32 layers");
+  if (!d->layers || !d->norm || !d->rope || !d->x0 || !d->id0 || !d->emb || !d->head_w || !d->head_s || !d->codes ||
+      !d->workspace || d->emb0_rows <= 0)
+    return sk_set_error(SK_EINVAL, "sk_cp_frame: null pointer");
+  if (d->workspace_bytes < sk_talker_workspace_size(d->hidden, d->inter))
+    return sk_set_error(SK_EWORKSPACE, "sk_cp_frame: workspace too small");
+  int dev = 0, cus = 0;
+  hipGetDevice(&dev);
+  hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (cus != kWG) return sk_set_error(SK_EUNSUPPORTED, "sk_cp_frame: needs a 256-CU device (8 XCDs x 32)");
+  sk_talker_desc t{};
+  t.n_layers = d->n_layers; t.hidden = d->hidden; t.inter = d->inter; t.nq = d->nq; t.nkv = d->nkv;
+  t.vocab = d->vocab; t.max_len = d->n_positions; t.wd = d->wd; t.ct = d->ct; t.eps = d->eps;
+  t.layers = d->layers; t.norm = d->norm; t.rope = d->rope; t.id0 = const_cast<int64_t*>(d->id0);
+  t.out = d->codes; t.rep_pen = 1.f; t.eos = -1; t.talker_processor = 0;
+  t.logits = d->logits; t.layer_out = d->layer_out; t.workspace = d->workspace; t.workspace_bytes = d->workspace_bytes;
+  const CpArgs cp{d->x0, d->emb, d->head_w, d->head_s, d->emb0_rows};
+  return launch_frames<1024, 3072, 4, 2048, true>(&t, cp, d->n_positions, (hipStream_t)stream);
 }

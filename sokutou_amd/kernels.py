@@ -121,6 +121,103 @@ class _Stack:
         return sum(L[k].bytes() for L in self.layers for k in ("qkv", "o", "gu", "down"))
 
 
+def _layer_descs(P: _Stack, kc: list, vc: list, device) -> torch.Tensor:
+    """Device array of ``sk_layer_desc`` for the layers of ``P`` with caches ``kc[i]`` / ``vc[i]``."""
+    arr = (_lib.SkLayerDesc * len(P.layers))()
+    for i, Ly in enumerate(P.layers):
+        arr[i] = _lib.SkLayerDesc(Ly["qkv"].w.data_ptr(), Ly["qkv"].s.data_ptr(), Ly["o"].w.data_ptr(),
+                                  Ly["o"].s.data_ptr(), Ly["gu"].w.data_ptr(), Ly["gu"].s.data_ptr(),
+                                  Ly["down"].w.data_ptr(), Ly["down"].s.data_ptr(), Ly["in_norm"].data_ptr(),
+                                  Ly["post_norm"].data_ptr(), Ly["qn"].data_ptr(), Ly["kn"].data_ptr(),
+                                  kc[i].data_ptr(), vc[i].data_ptr())
+    return torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8).to(device)
+
+
+class CodePredictor:
+    """The code predictor of one frame on the persistent kernel in its code-predictor mode (``sk_cp_frame``).
+
+    Weights as the reference reads them (qwen3/kernels.py:516-523): ``cp.model`` (its decoder stack, packed by
+    ``_Stack`` with a cache of ``n_positions``), ``cp.lm_head`` (head g - 1 produces code g) and
+    ``cp.get_input_embeddings()`` (table g - 2 embeds code g - 1 at position g). The loop is the reference's
+    (qwen3/kernels.py:666-675 with ``_cp_first`` 641-655): position 0 takes the talker's last hidden state,
+    position 1 the talker embedding row of code 0, position g >= 2 the embedding of code g - 1; each position
+    g >= 1 ends in the final RMSNorm, head g - 1 and a greedy pick. Greedy sub-codes only."""
+
+    def __init__(self, cp, temb: torch.Tensor, n_positions: int = 16, wd: str = "i8row", device=None):
+        if wd != "i8row":
+            raise ValueError("the code-predictor kernel reads i8row weights")
+        proj = getattr(cp, "small_to_mtp_projection", None)
+        if proj is not None and not isinstance(proj, torch.nn.Identity):
+            raise NotImplementedError("a code predictor narrower than the talker (small_to_mtp_projection) is not "
+                                      "supported by sk_cp_frame")
+        L = _lib.load()
+        self.device = torch.device(device) if device is not None else temb.device
+        self.n = int(n_positions)
+        with torch.no_grad():
+            self.C = _Stack(cp.model, wd, self.n)
+            self.heads = [_Lin(h.weight, wd) for h in cp.lm_head][: self.n - 1]
+            self.cemb = [e.weight.to(torch.bfloat16).contiguous() for e in cp.get_input_embeddings()][: self.n - 2]
+            self.temb = temb.to(torch.bfloat16).contiguous()
+        if len(self.heads) != self.n - 1 or len(self.cemb) != self.n - 2:
+            raise ValueError(f"{self.n} positions need {self.n - 1} heads and {self.n - 2} code tables")
+        P = self.C
+        self.V = self.heads[0].N
+        dev = self.device
+        self.kc = torch.zeros((len(P.layers), P.nkv, self.n, HD), dtype=torch.bfloat16, device=dev)
+        self.vc = torch.zeros_like(self.kc)
+        self.x0 = torch.zeros(P.H, dtype=torch.float32, device=dev)
+        self.id0 = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.codes = torch.zeros(self.n, dtype=torch.int64, device=dev)
+        self.logits = torch.zeros(self.V, dtype=torch.float32, device=dev)
+        self.layer_out: torch.Tensor | None = None
+        tabs = [0, self.temb.data_ptr()] + [t.data_ptr() for t in self.cemb]
+        hw = [0] + [h.w.data_ptr() for h in self.heads]
+        hs = [0] + [h.s.data_ptr() for h in self.heads]
+        self._ptrs = torch.tensor([tabs, hw, hs], dtype=torch.int64, device=dev)
+        self._layer_desc = _layer_descs(P, list(self.kc.unbind(0)), list(self.vc.unbind(0)), dev)
+        self.ws = torch.zeros(int(L.sk_talker_workspace_size(P.H, P.I)), dtype=torch.uint8, device=dev)
+        self._desc = _lib.SkCpDesc(
+            n_layers=len(P.layers), hidden=P.H, inter=P.I, nq=P.nq, nkv=P.nkv, vocab=self.V, n_positions=self.n,
+            wd=_lib.WD[wd], ct=_lib.CT["bf16"], eps=P.eps, layers=self._layer_desc.data_ptr(), norm=P.norm.data_ptr(),
+            rope=P.rope.data_ptr(), x0=self.x0.data_ptr(), id0=self.id0.data_ptr(), emb0_rows=self.temb.shape[0],
+            emb=self._ptrs[0].data_ptr(), head_w=self._ptrs[1].data_ptr(), head_s=self._ptrs[2].data_ptr(),
+            codes=self.codes.data_ptr(), logits=self.logits.data_ptr(), layer_out=None,
+            workspace=self.ws.data_ptr(), workspace_bytes=self.ws.numel())
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    def run(self) -> None:
+        """One frame on the current stream: reads ``x0`` and ``id0``, writes ``codes`` (and ``logits`` of the
+        last position)."""
+        self._desc.layer_out = None if self.layer_out is None else self.layer_out.data_ptr()
+        _lib.check(_lib.load().sk_cp_frame(ctypes.byref(self._desc), _lib.stream()), "sk_cp_frame")
+
+    def __call__(self, x0: torch.Tensor, id0) -> torch.Tensor:
+        self.x0.copy_(x0.reshape(-1))
+        self.id0.fill_(int(id0)) if not isinstance(id0, torch.Tensor) else self.id0.copy_(id0.reshape(1))
+        self.run()
+        return self.codes
+
+    def capture(self) -> None:
+        """Records one frame (one launch) as a HIP graph; replays read ``x0`` / ``id0`` in place."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.run()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.run()
+        torch.cuda.synchronize()
+        self.graph = g
+
+    def error(self) -> int:
+        """Error word of the kernel's workspace (0 when healthy; codes as ``Qwen3Kernels.frame_error``)."""
+        return int(self.ws[:4].view(torch.int32).item())
+
+    def weight_bytes(self) -> int:
+        return self.C.bytes() + sum(h.bytes() for h in self.heads)
+
+
 class Qwen3Kernels(Qwen3Fast):
     """The talker frame on the sokutou_amd kernels (qwen3/kernels.py:483-754 surface).
 
@@ -144,7 +241,8 @@ class Qwen3Kernels(Qwen3Fast):
         with torch.cuda.device(self.device):
             _lib.check(L.sk_device_check(), "sk_device_check")
         if self.cp is not None:
-            raise NotImplementedError("the code predictor (15 sub-steps per frame) is not part of this engine yet")
+            raise NotImplementedError("a talker frame fed by the code predictor (talker_in over 16 codes) is not part "
+                                      "of this engine yet; the code predictor alone runs on CodePredictor")
         t0 = time.perf_counter()
         self.wd = wd
         self.ct = "f32" if wd == "f32" else "bf16"
@@ -199,14 +297,7 @@ class Qwen3Kernels(Qwen3Fast):
     def _setup_frame_kernel(self) -> None:
         P = self.T
         L = _lib.load()
-        arr = (_lib.SkLayerDesc * len(P.layers))()
-        for i, Ly in enumerate(P.layers):
-            arr[i] = _lib.SkLayerDesc(Ly["qkv"].w.data_ptr(), Ly["qkv"].s.data_ptr(), Ly["o"].w.data_ptr(),
-                                      Ly["o"].s.data_ptr(), Ly["gu"].w.data_ptr(), Ly["gu"].s.data_ptr(),
-                                      Ly["down"].w.data_ptr(), Ly["down"].s.data_ptr(), Ly["in_norm"].data_ptr(),
-                                      Ly["post_norm"].data_ptr(), Ly["qn"].data_ptr(), Ly["kn"].data_ptr(),
-                                      self.tk[i].data_ptr(), self.tv[i].data_ptr())
-        self._layer_desc = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8).to(self.device)
+        self._layer_desc = _layer_descs(P, self.tk, self.tv, self.device)
         self.frame_ws = torch.zeros(int(L.sk_talker_workspace_size(P.H, P.I)), dtype=torch.uint8, device=self.device)
         self.frame_ids = torch.zeros(4096, dtype=torch.int64, device=self.device)
         self.layer_out: torch.Tensor | None = None

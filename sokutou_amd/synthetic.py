@@ -171,6 +171,50 @@ def make_tts(seed: int, s: TalkerShape, device="cpu", eos: int | None = None, **
 
 
 # ---------------------------------------------------------------------------------------------------------
+# code predictor (qwen3/kernels.py:516-523: cp.model, cp.lm_head[g], cp.get_input_embeddings()[g],
+# cp.small_to_mtp_projection)
+# ---------------------------------------------------------------------------------------------------------
+CP_LAYER0, CP_FINAL, CP_HEAD0, CP_EMB0, CP_TALKER_EMB, CP_FRAME0 = 100, 150, 200, 300, 400, 500
+
+
+def cp_weights(seed: int, s: TalkerShape, n_positions: int = 16, talker_vocab: int = 3072) -> dict:
+    """fp32 weights of a code predictor with ``s.n_layers`` layers: its layers, final norm, heads 1..n-1
+    ([vocab, hidden] each, head g produces code g), code-embedding tables 2..n-1 ([vocab, hidden] bf16; table g
+    embeds code g - 1) and the talker's own embedding table (which embeds code 0 at position 1)."""
+    return {
+        "layers": [layer_weights(seed, CP_LAYER0 + i, s) for i in range(s.n_layers)],
+        "norm": normal(seed, CP_FINAL, "norm", (s.hidden,), 0.1, 1.0),
+        "heads": [normal(seed, CP_HEAD0 + g, "head", (s.vocab, s.hidden), 0.02) for g in range(1, n_positions)],
+        "cemb": [bf16_values(normal(seed, CP_EMB0 + g, "emb", (s.vocab, s.hidden), 0.02)) for g in range(2, n_positions)],
+        "temb": bf16_values(normal(seed, CP_TALKER_EMB, "emb", (talker_vocab, s.hidden), 0.02)),
+    }
+
+
+def cp_frame_inputs(seed: int, f: int, s: TalkerShape, talker_vocab: int = 3072) -> tuple[np.ndarray, int]:
+    """Inputs of code-predictor frame ``f``: the talker's last hidden state x0 ~ N(0, 1) (fp32) and code 0."""
+    x0 = normal(seed, CP_FRAME0 + f, "h", (s.hidden,))
+    return x0, int(_rng(seed, CP_FRAME0 + f, "token").integers(0, talker_vocab))
+
+
+def make_code_predictor(seed: int, s: TalkerShape, device="cpu", n_positions: int = 16, w: dict | None = None):
+    """(cp, talker embedding) with the attributes the engine reads: ``cp.model`` (layers, norm, rotary_emb,
+    config), ``cp.lm_head`` (n - 1 heads), ``cp.get_input_embeddings()`` (n - 1 tables: entry g - 1 embeds
+    code g; the last one is only used by the talker's input), ``cp.small_to_mtp_projection`` (identity: the
+    talker and the code predictor are both 1024 wide) and ``cp.config.vocab_size``."""
+    w = w if w is not None else cp_weights(seed, s, n_positions)
+    base = make_talker(seed, s, device, layers=w["layers"],
+                       final={"norm": w["norm"], "head": w["heads"][0], "emb": w["temb"]})
+    cemb = [SimpleNamespace(weight=torch.from_numpy(t).to(device=device, dtype=torch.bfloat16)) for t in w["cemb"]]
+    # the talker's input also embeds the last code: one more table, unused by the code predictor itself
+    cemb.append(SimpleNamespace(weight=torch.zeros((s.vocab, s.hidden), dtype=torch.bfloat16, device=device)))
+    cp = SimpleNamespace(model=base.model, lm_head=[_p(h, device) for h in w["heads"]],
+                         small_to_mtp_projection=torch.nn.Identity(), config=SimpleNamespace(vocab_size=s.vocab))
+    cp.get_input_embeddings = lambda: cemb
+    temb = torch.from_numpy(w["temb"]).to(device=device, dtype=torch.bfloat16)
+    return cp, temb
+
+
+# ---------------------------------------------------------------------------------------------------------
 # named workloads
 # ---------------------------------------------------------------------------------------------------------
 WORKLOADS = {
@@ -184,12 +228,15 @@ WORKLOADS = {
     "tiny": dict(shape="tiny", n_layers=2, kv=24, frames=8),
     # two 0.6B-shaped layers (the persistent frame kernel needs the real head counts)
     "small06b": dict(shape="0.6b", n_layers=2, kv=40, frames=8),
+    # code predictor: 5 layers of the 0.6B shape, 2048-way heads, 16 positions (KV 1 -> 16) per frame, greedy
+    # sub-codes; a step is `frames` code-predictor frames with different (x0, code 0)
+    "cp06b": dict(shape="0.6b", n_layers=5, vocab=2048, kv=0, positions=16, frames=8),
 }
 
 
 def workload_shape(name: str) -> TalkerShape:
     w = WORKLOADS[name]
-    return shape(w["shape"], n_layers=w["n_layers"])
+    return shape(w["shape"], n_layers=w["n_layers"], **({"vocab": w["vocab"]} if "vocab" in w else {}))
 
 
 def make_engine(name: str, seed: int = 0, wd: str = "i8row", device="cuda", graphs: bool = True,
@@ -218,3 +265,13 @@ def make_engine(name: str, seed: int = 0, wd: str = "i8row", device="cuda", grap
     tok = start_token(seed, s)
     eng.reset(w["kv"], tok)
     return eng, tok
+
+
+def make_cp_engine(name: str = "cp06b", seed: int = 0, device="cuda"):
+    """A CodePredictor over the seeded synthetic code predictor of workload ``name`` (one frame per run)."""
+    from .kernels import CodePredictor
+
+    spec = WORKLOADS[name]
+    s = workload_shape(name)
+    cp, temb = make_code_predictor(seed, s, device=device, n_positions=spec["positions"])
+    return CodePredictor(cp, temb, n_positions=spec["positions"], wd="i8row", device=device)

@@ -114,12 +114,42 @@ def talker(name: str, seed: int, wd: str = "i8row") -> None:
     print(name, "codes", codes[:12], "... min margin", min(margins), meta["oracle_seconds"])
 
 
+def code_predictor(name: str = "cp06b", seed: int = 0) -> None:
+    """Code-predictor frames: codes of every position, top-1/top-2 margins, per-layer residuals at the last
+    position and its logits, for frame 0 (inputs x0 and code 0 differ per frame)."""
+    from oracle.workload import cp_oracle
+
+    spec = syn.WORKLOADS[name]
+    t0 = time.time()
+    dig: dict = {}
+    orc, s = cp_oracle(name, seed, digests=dig)
+    t1 = time.time()
+    codes, margins, inputs = [], [], []
+    layer_out: list = []
+    last = None
+    for f in range(spec["frames"]):
+        x0, id0 = syn.cp_frame_inputs(seed, f, s)
+        inputs.append({"id0": id0, "x0_sha256": syn.sha256(x0)})
+        c, lg = orc.frame(x0, id0, layer_out if f == 0 else None)
+        codes.append(c)
+        margins.append([float(np.diff(np.sort(v)[-2:])[0]) for v in lg])
+        if f == 0:
+            last = lg[-1]
+    t2 = time.time()
+    np.savez_compressed(HERE / f"{name}_seed{seed}.npz", layer_out_last0=np.stack(layer_out), logits_last0=last)
+    meta = {"workload": name, "seed": seed, "wd": "i8row", "positions": spec["positions"], "inputs": inputs,
+            "codes": codes, "margins": margins, "min_margin": min(min(m) for m in margins), "digests": dig,
+            "oracle_seconds": {"build": round(t1 - t0, 1), "frames": round(t2 - t1, 1)}}
+    (HERE / f"{name}_seed{seed}.json").write_text(json.dumps(meta, indent=1))
+    print(name, "codes[0]", codes[0], "min margin", meta["min_margin"], meta["oracle_seconds"])
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--only", default=None)
     a = ap.parse_args()
     jobs = {"layer06b": lambda: layer06b(0), "tiny": lambda: talker("tiny", 1), "talker06b": lambda: talker("talker06b", 0),
-            "talker17b": lambda: talker("talker17b", 0)}
+            "talker17b": lambda: talker("talker17b", 0), "cp06b": lambda: code_predictor("cp06b", 0)}
     for n, fn in jobs.items():
         if a.only in (None, n):
             fn()

@@ -1,0 +1,78 @@
+"""The code predictor on the persistent kernel (sk_cp_frame): greedy sub-codes of every position, per-layer
+residuals and logits at the last position, against the oracle fixture; graph replay; the error word."""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from sokutou_amd import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+TOL = 1e-2
+
+
+def rel_err(a, b) -> float:
+    a = a.detach().cpu().numpy() if isinstance(a, torch.Tensor) else a
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+@pytest.fixture(scope="module")
+def cp_engine(gpu):
+    print("cp06b: building the seeded code predictor (5 layers, 15 heads)", flush=True)
+    return syn.make_cp_engine("cp06b", 0, gpu)
+
+
+def test_code_predictor_frames_against_oracle(cp_engine, gpu):
+    meta = json.loads((GOLD / "cp06b_seed0.json").read_text())
+    gold = np.load(GOLD / "cp06b_seed0.npz")
+    eng = cp_engine
+    s = syn.workload_shape("cp06b")
+    eng.layer_out = torch.zeros((s.n_layers, s.hidden), device=gpu)
+    for f, ref in enumerate(meta["codes"]):
+        x0, id0 = syn.cp_frame_inputs(0, f, s)
+        assert id0 == meta["inputs"][f]["id0"]
+        print(f"frame {f}: one launch of {meta['positions']} positions", flush=True)
+        codes = eng(torch.from_numpy(x0).to(gpu), id0).cpu().tolist()
+        assert eng.error() == 0
+        assert codes == ref, (f, codes, ref)
+        if f == 0:
+            errs = [rel_err(eng.layer_out[i], gold["layer_out_last0"][i]) for i in range(s.n_layers)]
+            print(f"per-layer max rel err {max(errs):.3e}", flush=True)
+            assert max(errs) < TOL
+            assert rel_err(eng.logits, gold["logits_last0"]) < TOL
+    eng.layer_out = None
+
+
+def test_code_predictor_graph_replay(cp_engine, gpu):
+    meta = json.loads((GOLD / "cp06b_seed0.json").read_text())
+    eng = cp_engine
+    s = syn.workload_shape("cp06b")
+    eng.capture()
+    for f in (3, 0, 7, 3):
+        x0, id0 = syn.cp_frame_inputs(0, f, s)
+        eng.x0.copy_(torch.from_numpy(x0))
+        eng.id0.fill_(id0)
+        print(f"replay of frame {f}", flush=True)
+        eng.graph.replay()
+        assert eng.codes.cpu().tolist() == meta["codes"][f]
+    assert eng.error() == 0
+
+
+def test_code_zero_out_of_range_is_refused(cp_engine, gpu):
+    eng = cp_engine
+    print("code 0 beyond the talker table is refused on the device", flush=True)
+    eng.codes.fill_(-7)
+    eng.id0.fill_(eng.temb.shape[0])
+    eng.run()
+    torch.cuda.synchronize()
+    assert eng.error() == 5
+    assert eng.codes.cpu().tolist() == [-7] * eng.n
+    eng.ws.zero_()
+    s = syn.workload_shape("cp06b")
+    x0, id0 = syn.cp_frame_inputs(0, 1, s)
+    eng(torch.from_numpy(x0).to(gpu), id0)
+    assert eng.error() == 0

@@ -61,3 +61,17 @@ def test_sample_rejects_large_vocab_and_sampling():
     assert rc == _lib.SK_EUNSUPPORTED
     with pytest.raises(NotImplementedError):
         _lib.check(rc, "sk_sample")
+
+
+def test_cp_frame_rejects_bad_shapes_without_launching():
+    import ctypes
+
+    from sokutou_amd import _lib
+
+    L = _lib.load()
+    d = _lib.SkCpDesc(n_layers=5, hidden=1024, inter=3072, nq=16, nkv=8, vocab=3000, n_positions=16)
+    assert L.sk_cp_frame(ctypes.byref(d), None) == _lib.SK_EUNSUPPORTED
+    d.vocab = 2048
+    assert L.sk_cp_frame(ctypes.byref(d), None) == _lib.SK_EINVAL  # null pointers
+    d.n_positions = 1
+    assert L.sk_cp_frame(ctypes.byref(d), None) == _lib.SK_EUNSUPPORTED

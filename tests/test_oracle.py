@@ -292,3 +292,54 @@ def test_process_logits_matches_torch_processor():
             ref[0, eos] = -np.inf
         np.testing.assert_array_equal(ours, ref[0].numpy())
         assert O.argmax_first(ours) == int(torch.argmax(ref))
+
+
+# ---- code predictor composition -----------------------------------------------------------------------------
+def test_code_predictor_frame_matches_transformers_stack():
+    """The code-predictor loop (inputs per position, growing cache, final norm + per-position head, greedy
+    pick) against a stack of transformers' Qwen3DecoderLayer run position by position over one DynamicCache,
+    Qwen3RMSNorm and a torch matmul head, f32 cache: the same codes at every position and logits to fp32
+    rounding. Tiny shape, 2 layers, 6 positions."""
+    from transformers import DynamicCache
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+
+    s = syn.shape("tiny", n_layers=2, vocab=64)
+    n = 6
+    rng = np.random.default_rng(21)
+    layers = [syn.layer_weights(31, i, s) for i in range(s.n_layers)]
+    norm = (1 + 0.1 * rng.standard_normal(s.hidden)).astype(F32)
+    # large head weights so every position has a clear winner (the check is about composition, not ties)
+    heads = [(0.5 * rng.standard_normal((s.vocab, s.hidden))).astype(F32) for _ in range(n - 1)]
+    cemb = [rng.standard_normal((s.vocab, s.hidden)).astype(F32) for _ in range(n - 2)]
+    temb = rng.standard_normal((96, s.hidden)).astype(F32)
+    x0 = rng.standard_normal(s.hidden).astype(F32)
+    id0 = 77
+    rope = O.rope_table(syn.inv_freq(s), n)
+    orc = O.CodePredictorOracle({"layers": [_oracle_layer_weights(w) for w in layers], "norm": norm, "heads": heads,
+                                 "cemb": cemb, "temb": temb, "rope": rope, "eps": s.eps, "nq": s.nq, "nkv": s.nkv},
+                                n, cache_bf16=False)
+    codes, logits = orc.frame(x0, id0)
+    hf = [_hf_layer(s, w) for w in layers]
+    for i, (layer, _) in enumerate(hf):
+        layer.self_attn.layer_idx = i
+    fnorm = Qwen3RMSNorm(s.hidden, eps=s.eps)
+    with torch.no_grad():
+        fnorm.weight.copy_(torch.from_numpy(norm))
+    cache = DynamicCache()
+    ref_codes = [id0]
+    for g in range(n):
+        x = x0 if g == 0 else temb[id0] if g == 1 else cemb[g - 2][ref_codes[g - 1]]
+        h = torch.from_numpy(np.asarray(x, F32))[None, None, :]
+        pid = torch.tensor([[g]])
+        with torch.no_grad():
+            for layer, rot in hf:
+                h = layer(h, attention_mask=None, position_ids=pid, past_key_values=cache, use_cache=True,
+                          position_embeddings=rot(h, pid))
+                h = h[0] if isinstance(h, tuple) else h
+            if g == 0:
+                continue
+            lg = (fnorm(h)[0, 0] @ torch.from_numpy(heads[g - 1]).T).numpy()
+        ref_codes.append(int(np.argmax(lg)))
+        err = np.max(np.abs(logits[g - 1] - lg)) / np.max(np.abs(lg))
+        assert err < 1e-5, (g, err)
+    assert codes == ref_codes
