@@ -1,6 +1,6 @@
 """Talker decode benchmark on one MI355X: frames/s of the 0.6B-shaped int8 talker at batch 1, KV 512.
 
-    python bench.py [--steps K] [--warmup W] [--workload talker06b|talker17b] [--engine frames|graph|multi] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload talker06b|talker17b|cp06b] [--engine frames|graph|multi] [--no-cpu]
 
 A step is one greedy decode run of 64 frames starting at KV length 512 (positions 512..575 are rewritten on
 every step, so every step does identical work). Each frame is embed -> 28 decoder layers (RMSNorm + qkv, q/k norm
@@ -11,6 +11,9 @@ codec head -> argmax, feeding the next frame. Engines:
   multi   one captured HIP graph per frame of the per-op kernels (5 launches per layer)
 Weights are seeded random-init of the real architecture, int8 per output channel with bf16 scales (``i8row``);
 the KV cache is bf16. Inputs are resident in HBM before timing starts.
+
+``--workload cp06b`` measures the code predictor instead: a step is 8 code-predictor frames, each one launch of
+sk_cp_frame over 16 positions (5 layers of the 0.6B shape, 15 greedy sub-codes from 2048-way heads).
 
 Prints one JSON line with the metric, the roofline of the dominant kernel (algorithmic bytes per launch over its
 average duration, timed with HIP events on the launch stream) and the CPU oracle timed on this host.
@@ -100,6 +103,112 @@ def time_kernels(eng, reps: int = 200) -> dict:
     return out
 
 
+def cp_algorithmic_bytes(s, positions: int = 16) -> dict:
+    """Bytes one code-predictor frame must move: the stack's weights and scales once per pass, positions 0 and 1
+    counted as one pass as the reference pairs them (positions - 1 passes), plus the 15 heads once each and the
+    K/V reads and appends of every position."""
+    H, I, nq, nkv, hd = s.hidden, s.inter, s.nq, s.nkv, s.head_dim
+
+    def mat(N, K):
+        return N * K + 2 * N
+
+    layer = mat((nq + 2 * nkv) * hd, H) + mat(H, nq * hd) + mat(2 * I, H) + mat(H, I)
+    kv = sum(2 * nkv * (p + 1) * hd * 2 + 2 * nkv * hd * 2 for p in range(positions)) * s.n_layers
+    heads = (positions - 1) * mat(s.vocab, H)
+    return {"per_pass": layer * s.n_layers, "frame": (positions - 1) * layer * s.n_layers + heads + kv,
+            "frame_16_passes": positions * layer * s.n_layers + heads + kv}
+
+
+def run_cp(args) -> None:
+    """Code-predictor frames: HIP events around every sk_cp_frame launch of the timed steps."""
+    import numpy as np
+    import torch
+
+    from sokutou_amd import synthetic as syn
+
+    dev = torch.device("cuda:0")
+    name = "cp06b"
+    spec = syn.WORKLOADS[name]
+    s = syn.workload_shape(name)
+    t0 = time.perf_counter()
+    eng = syn.make_cp_engine(name, args.seed, dev)
+    x0, id0 = syn.cp_frame_inputs(args.seed, 0, s)
+    eng.x0.copy_(torch.from_numpy(x0))
+    eng.id0.fill_(id0)
+    setup_s = time.perf_counter() - t0
+    frames = spec["frames"]
+    ev = []
+
+    def step(record: bool = False):
+        for _ in range(frames):
+            if record:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                eng.run()
+                e1.record()
+                ev.append((e0, e1))
+            else:
+                eng.run()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(record=True)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    if eng.error():
+        raise RuntimeError(f"code-predictor kernel error {eng.error()}")
+    gold = ROOT / "tests" / "golden" / f"{name}_seed{args.seed}.json"
+    parity = None
+    if gold.exists():
+        parity = eng.codes.cpu().tolist() == json.loads(gold.read_text())["codes"][0]
+    fps = frames * args.steps / dt
+    launch_us = sum(a.elapsed_time(b) for a, b in ev) * 1e3 / len(ev)
+    ab = cp_algorithmic_bytes(s, spec["positions"])
+    achieved = ab["frame"] / (launch_us * 1e-6) / 1e9
+    res = {
+        "metric": "code predictor frames/sec (5 layers of the 0.6B shape, 16 positions, 15 greedy sub-codes, int8)",
+        "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8 weights x fp32 accumulate (bf16 KV cache)", "data": "synthetic",
+        "config": {"workload": f"{name}: {s.n_layers} layers, hidden {s.hidden}, {s.nq}q/{s.nkv}kv heads x 128, "
+                               f"intermediate {s.inter}, 15 heads of {s.vocab}, i8row, {spec['positions']} positions "
+                               f"(KV 1..16) per frame, {frames} frames per step", "weights": "i8row",
+                   "engine": "sk_cp_frame (one launch per frame)"},
+        "roofline": {"bound": "hbm", "kernel": "k_frames code-predictor mode (sk_cp_frame)",
+                     "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "bytes_per_launch": ab["frame"],
+                     "avg_launch_us": round(launch_us, 2),
+                     "note": "the 79 MB stack + 31 MB of heads fit in the 256 MB Infinity Cache across passes; "
+                             "the kernel runs positions 0 and 1 as two passes (16 passes, "
+                             f"{ab['frame_16_passes']} bytes touched)"},
+        "frame": {"us_per_frame": round(launch_us, 2), "us_per_position": round(launch_us / spec["positions"], 2),
+                  "us_per_layer_pass": round(launch_us / spec["positions"] / s.n_layers, 3)},
+        "parity_codes_match_oracle": parity, "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu:
+        from oracle.workload import cp_oracle
+
+        orc, _ = cp_oracle(name, args.seed)
+        orc.frame(x0, id0)  # warm-up
+        times = []
+        t_start = time.perf_counter()
+        while time.perf_counter() - t_start < 15.0 and len(times) < 64:
+            xf, i0 = syn.cp_frame_inputs(args.seed, len(times) % frames, s)
+            t1 = time.perf_counter()
+            orc.frame(xf, i0)
+            times.append(time.perf_counter() - t1)
+        from threadpoolctl import threadpool_info
+        med = float(np.median(times))
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        res["cpu_baseline"] = {"value": round(1.0 / med, 3), "unit": "frames/s", "cores": int(threads), "kind": "port",
+                               "sample": f"{len(times)} code-predictor frames after one warm-up, median {med * 1e3:.1f} "
+                                         "ms; numpy fp32 over dequantised int8 weights", "host_cpus": os.cpu_count()}
+    print(json.dumps(res), flush=True)
+
+
 def cpu_baseline(name: str, seed: int, budget_s: float = 15.0) -> dict:
     """The numpy oracle on this host's cores: frames of the same workload until ~budget_s of frame time."""
     import numpy as np
@@ -135,7 +244,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="talker06b", choices=["talker06b", "talker17b"])
+    ap.add_argument("--workload", default="talker06b", choices=["talker06b", "talker17b", "cp06b"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--engine", default="frames", choices=["frames", "graph", "multi"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
@@ -147,6 +256,10 @@ def main() -> None:
         print("bench.py measures one GPU: the talker decode step at batch 1 runs on a single MI355X "
               "(how it would shard is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "cp06b":
+        run_cp(args)
+        return
 
     import torch
 
