@@ -79,14 +79,15 @@ __device__ __forceinline__ void wg_sync() {
 // ---- layout of the workspace (bytes) -------------------------------------------------------------------------
 struct Ws {
   // control words
-  static constexpr uint32_t kErr = 0, kTick = 4, kLaunch = 8, kDiag = 16, kTraceOn = 32, kPollDelay = 36,
+  static constexpr uint32_t kErr = 0, kTick = 4, kLaunch = 8, kDiag = 16, kTraceOn = 32, kPollDelay = 40,
                             kCensus = 64;  // census: 8 counters
   // Polling of a stage's input starts this many sleep units (s_sleep 1: 64 shader clocks, ~27 ns at 2.4 GHz)
   // after the workgroup published its own part of it. Reads that reach the cells before the producers' stores
-  // are visible come back stale and make the whole exchange slower than one late, successful read. Shader-clock
-  // sleeps, not the real-time counter: reading that counter is a scalar-memory round trip of ~0.7 us.
-  // The kPollDelay word overrides the default (value - 1) when non-zero.
-  static constexpr uint32_t kPollDelayDefault = 26;
+  // are visible come back stale and make the whole exchange slower than one late, successful read. One delay
+  // per exchange (kHop*), since producers and timing differ: bytes kPollDelay + h of the workspace override
+  // the defaults (value - 1) when non-zero.
+  static constexpr int kHopS1 = 0, kHopS2 = 1, kHopS3 = 2, kHopS4 = 3, kHopS5 = 4, kHopS6 = 5, kHopHead = 6,
+                       kHopPick = 7, kHops = 8;
   static constexpr int kTraceLayers = 32, kTraceEvents = 16;  // optional per-stage timestamps of frame 0
   static constexpr uint32_t kCells = 256;
 };
@@ -348,7 +349,7 @@ struct Ctx {
   uint32_t base, tpf;
   int pos0, n_frames, L;
   uint64_t* trace;  // per-stage timestamps of frame 0 (null when tracing is off)
-  uint32_t delay;   // poll start delay, ticks
+  uint8_t dl[Ws::kHops];  // poll start delay of each exchange, sleep units
   __device__ void tr(int role, int f, int l, int ev) const {
     if (trace && f == 0 && l < Ws::kTraceLayers)
       trace[(((size_t)g * 2 + role) * Ws::kTraceLayers + l) * Ws::kTraceEvents + ev] = (uint64_t)wall_clock64();
@@ -411,7 +412,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 #pragma unroll
         for (int k = 0; k < H / 64; k++) S.hin[lane + 64 * k] = ev[k];
       } else {
-        after_publish(S, (uint32_t)(f * c.L + l) * 4u, c.delay);  // own part of the previous layer's down output
+        after_publish(S, (uint32_t)(f * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
         ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
       }
       float ss = 0.f;
@@ -423,7 +424,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       wg_sync();
       if (!ok) return;
       // S2 input: this head's q/k/v
-      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 1u, c.delay);
+      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 1u, c.dl[Ws::kHopS2]);
       ok = poll_cells<mb(512)>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
       if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
@@ -434,7 +435,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       {
         const uint32_t e = c.tick(f, l, 1);
         const int mh = c.r >> 4, md0 = 8 * (c.r & 15);
-        sleep_units(c.delay);  // the compute waves publish their partial right after the last attention barrier
+        sleep_units(c.dl[Ws::kHopS3]);  // the compute waves publish their partial right after the last attention barrier
         for (uint32_t spin = 0;; spin++) {
           bool good = true;
           // per chunk 5 cell pairs: (m, l) of head mh, then 4 pairs of its o slice; all loads issued first
@@ -490,7 +491,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
             put2(c.cells, o0 + 2, od[2], od[3], e3);
           }
         }
-        sleep_units(c.delay);  // S4 input: the merges of all workgroups, this one's included
+        sleep_units(c.dl[Ws::kHopS4]);  // S4 input: the merges of all workgroups, this one's included
         if (lane == 0) c.tr(0, f, l, 4);
       }
       // S4 input: the whole attention output
@@ -502,7 +503,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       float npost[H / 64];
 #pragma unroll
       for (int k = 0; k < H / 64; k++) npost[k] = gload(Ly.post_norm + lane + 64 * k);
-      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 2u, c.delay);
+      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
       ok = poll_cells<mb(H)>(c.cells, LY.e4, H, c.tick(f, l, 3), S.hmid, c.ws, lane, c, 15u, f, l);
       ss = 0.f;
       for (int i = lane; i < H; i += 64) { const float v = S.hmid[i]; ss += v * v; }
@@ -513,7 +514,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       wg_sync();
       if (!ok) return;
       // S6 input: the whole SwiGLU activation
-      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 3u, c.delay);
+      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 3u, c.dl[Ws::kHopS6]);
       ok = poll_cells<mb(I), true>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
       if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
       wg_sync();
@@ -524,7 +525,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     float nfin[H / 64];
 #pragma unroll
     for (int k = 0; k < H / 64; k++) nfin[k] = gload(c.d.norm + lane + 64 * k);
-    after_publish(S, (uint32_t)((f + 1) * c.L) * 4u, c.delay);
+    after_publish(S, (uint32_t)((f + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
     bool ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
     float ss = 0.f;
     for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
@@ -544,7 +545,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     // pick: reduce the 256 candidates
     {
       const uint32_t e = c.tick(f, c.L, 0);
-      sleep_units(c.delay);
+      sleep_units(c.dl[Ws::kHopPick]);
       uint64_t best = 0;
       for (uint32_t spin = 0;; spin++) {
         bool good = true;
@@ -942,8 +943,14 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     ((uint64_t*)S.desc)[i] = gload((const uint64_t*)d.layers + i);
   __syncthreads();
   {
-    const uint32_t pd = ld_u32_dev(ws, Ws::kPollDelay);
-    c.delay = pd ? pd - 1 : Ws::kPollDelayDefault;
+    // default start delays per exchange (tuned on the 0.6B talker), overridable through the workspace
+    constexpr uint8_t kDefault[Ws::kHops] = {17, 23, 35, 17, 20, 29, 26, 23};
+    const uint32_t w0 = ld_u32_dev(ws, Ws::kPollDelay), w1 = ld_u32_dev(ws, Ws::kPollDelay + 4);
+#pragma unroll
+    for (int h = 0; h < Ws::kHops; h++) {
+      const uint32_t v = ((h < 4 ? w0 : w1) >> (8 * (h & 3))) & 0xffu;
+      c.dl[h] = v ? (uint8_t)(v - 1) : kDefault[h];
+    }
   }
   c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
   if (wave == W) run_control<H, I, W, V, CP>(c, S, lane);
