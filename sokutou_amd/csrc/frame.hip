@@ -146,7 +146,6 @@ struct Lds {
   float qs[2][SK_HD];  // normalised, rotated, scaled q
   float kn[SK_HD], vn[SK_HD];
   float sc[2][Cfg<H, I, W, V, CP>::kMaxChunk];
-  float red[32];
   float opart[W][4][16][17];
   float mrg[kChunks][10];  // S3 inputs per chunk: m, l, o[8] of one q head
   float pub[64];           // this workgroup's outputs of a stage, published by the last compute wave to finish
@@ -375,7 +374,7 @@ __device__ void fail(const Ctx& c, uint32_t code, int f, int l) {
 }
 
 // Barriers of the attention stage after its input has arrived (both roles execute the same count).
-__device__ __forceinline__ int attn_barriers(const Chunk& ck) { return 4 + (ck.n > 0 ? 4 : 0); }
+__device__ __forceinline__ int attn_barriers(const Chunk& ck) { return 1 + (ck.n > 0 ? 2 : 0); }
 
 // ================================================================================================================
 // Control wave
@@ -623,12 +622,16 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   uint4 wq[C::RW_QKV][C::CH], wo[C::RW_O][C::CQ], wg[C::RW_GU][C::CH], wd[C::RW_D][C::CI];
   uint16_t sq[C::RW_QKV], so[C::RW_O], sg[C::RW_GU], sd[C::RW_D];  // raw bf16 row scales
   uint4 kr[C::KVL], vr[C::KVL];
-  float a_cs = 0.f, a_sn = 0.f, a_qn = 0.f, a_kn = 0.f;  // RoPE row and q/k norm weights of the next attention
-  auto load_attn_vec = [&](const sk_layer_desc& Lx, int posx) {  // every compute thread: no select on the loads
-    a_cs = gload(c.d.rope + (size_t)posx * SK_HD + (dd & 63));
-    a_sn = gload(c.d.rope + (size_t)posx * SK_HD + 64 + (dd & 63));
-    a_qn = gload(Lx.qn + dd);
-    a_kn = gload(Lx.kn + dd);
+  // RoPE row (cos, sin of pair `lane`) and the norm weights of dims lane, lane + 64 for this wave's vector in
+  // the next attention (q norm for waves 0, 1, k norm for wave 2; loaded by every compute wave: no select on
+  // loaded values, only on the address)
+  float a_cs = 0.f, a_sn = 0.f, a_n0 = 0.f, a_n1 = 0.f;
+  auto load_attn_vec = [&](const sk_layer_desc& Lx, int posx) {
+    const float* nw = (cw & 3) == 2 ? Lx.kn : Lx.qn;
+    a_cs = gload(c.d.rope + (size_t)posx * SK_HD + lane);
+    a_sn = gload(c.d.rope + (size_t)posx * SK_HD + 64 + lane);
+    a_n0 = gload(nw + lane);
+    a_n1 = gload(nw + 64 + lane);
   };
   {
     const sk_layer_desc& L0 = S.desc[0];
@@ -678,39 +681,37 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
       if (tid == 0) c.tr(1, f, l, 2);
       {
         const bool has_pos = ck.has_pos();
-        // read by every compute thread (no select on the prefetched registers); threads past the attention
-        // mapping (p > 1) compute values that are never stored
-        const float cs = a_cs, sn = a_sn;
-        const float qv = S.qkv[(p & 1) * SK_HD + dd];
-        const float kv = S.qkv[256 + (p & 1) * SK_HD + dd];  // p 0: k, p 1: v
-        const float sqv = wave_sum(qv * qv), skv = wave_sum(kv * kv);
-        if (att_thread && lane == 0) { S.red[cw] = sqv; S.red[4 + cw] = skv; }
-        wg_sync();  // attention barrier 1
-        if (att_thread) {
-          S.qs[p][dd] = qv * rsqrtf((S.red[2 * p] + S.red[2 * p + 1]) / SK_HD + eps) * a_qn;
-          if (p == 0) S.kn[dd] = kv * rsqrtf((S.red[4] + S.red[5]) / SK_HD + eps) * a_kn;
-          else S.vn[dd] = bf2f(f2bf(kv));
-        }
-        wg_sync();  // 2
-        float qr = 0.f, krot = 0.f;
-        if (att_thread) {
-          qr = (S.qs[p][dd] * cs + (dd < 64 ? -S.qs[p][dd + 64] : S.qs[p][dd - 64]) * sn) * kInvSqrtHd;
-          if (p == 0) krot = bf2f(f2bf(S.kn[dd] * cs + (dd < 64 ? -S.kn[dd + 64] : S.kn[dd - 64]) * sn));
-        }
-        wg_sync();  // 3
-        if (att_thread) {
-          S.qs[p][dd] = qr;
-          if (p == 0) S.kn[dd] = krot;
-          if (has_pos) {
-            // append the new K/V at pos (device-coherent: later frames read it from other workgroups)
-            const uint32_t off = (uint32_t)(pos * SK_HD + dd) * 2u;
-            if (p == 0) __builtin_amdgcn_raw_buffer_store_b16(f2bf(krot), make_rsrc(uniform(c.kh(Ly))), off, 0, kPolDev);
-            else __builtin_amdgcn_raw_buffer_store_b16(f2bf(S.vn[dd]), make_rsrc(uniform(c.vh(Ly))), off, 0, kPolDev);
+        // (1) one wave per vector, two dims per lane (d and d + 64, the RoPE pair): wave 0 q of head 2x, wave 1 q
+        // of head 2x + 1, wave 2 k, wave 3 v. RMSNorm over the head is a wave reduction, RoPE stays in the lane.
+        // Waves beyond 3 (8 compute waves) compute values that are never stored.
+        {
+          const int vw = cw & 3;
+          const float x0 = S.qkv[vw * SK_HD + lane], x1 = S.qkv[vw * SK_HD + 64 + lane];
+          const float inv = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / SK_HD + eps);
+          const float n0 = x0 * inv * a_n0, n1 = x1 * inv * a_n1;
+          const float r0 = n0 * a_cs - n1 * a_sn, r1 = n1 * a_cs + n0 * a_sn;  // rotate-half RoPE
+          if (cw < 2) {
+            S.qs[cw][lane] = r0 * kInvSqrtHd;
+            S.qs[cw][lane + 64] = r1 * kInvSqrtHd;
+          } else if (cw < 4) {
+            // k (normalised, rotated) or v (as is), rounded to the cache's bf16; the owner of pos appends them
+            // (device-coherent: later frames read them from other workgroups)
+            const float y0 = bf2f(f2bf(cw == 2 ? r0 : x0)), y1 = bf2f(f2bf(cw == 2 ? r1 : x1));
+            float* dst = cw == 2 ? S.kn : S.vn;
+            dst[lane] = y0;
+            dst[lane + 64] = y1;
+            if (has_pos) {
+              const __amdgpu_buffer_rsrc_t rs = make_rsrc(uniform(cw == 2 ? c.kh(Ly) : c.vh(Ly)));
+              const uint32_t off = (uint32_t)(pos * SK_HD + lane) * 2u;
+              __builtin_amdgcn_raw_buffer_store_b16(f2bf(y0), rs, off, 0, kPolDev);
+              __builtin_amdgcn_raw_buffer_store_b16(f2bf(y1), rs, off + 128u, 0, kPolDev);
+            }
           }
         }
-        wg_sync();  // 4
+        wg_sync();  // attention barrier 1
         float m = -INFINITY, lsum = 0.f, o = 0.f;
         if (ck.n > 0) {
+          // (2) scores of this chunk's positions (kr from the prefetch; the new position from LDS)
           {
             float q0[8], q1[8];
 #pragma unroll
@@ -733,17 +734,14 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
               if (asl == 0 && jj < ck.n) { S.sc[0][jj] = s0; S.sc[1][jj] = s1; }
             }
           }
-          wg_sync();  // 5
-          const float sv = (att_thread && dd < ck.n) ? S.sc[p][dd] : -INFINITY;
-          const float mx = wave_max(sv);
-          if (att_thread && lane == 0) S.red[8 + cw] = mx;
-          wg_sync();  // 6
-          const float mp = att_thread ? fmaxf(S.red[8 + 2 * p], S.red[8 + 2 * p + 1]) : 0.f;
-          const float ev = (att_thread && dd < ck.n) ? expf(sv - mp) : 0.f;
-          const float se = wave_sum(ev);
-          if (att_thread && dd < ck.n) S.sc[p][dd] = ev;
-          if (att_thread && lane == 0) S.red[12 + cw] = se;
-          wg_sync();  // 7
+          wg_sync();  // 2
+          // (3) softmax statistics, computed by every wave from the chunk's scores (at most 64 per head)
+          static_assert(C::kMaxChunk <= 64, "one score per lane");
+          const int jl = min(lane, C::kMaxChunk - 1);
+          const float s0l = lane < ck.n ? S.sc[0][jl] : -INFINITY, s1l = lane < ck.n ? S.sc[1][jl] : -INFINITY;
+          const float m0 = wave_max(s0l), m1 = wave_max(s1l);
+          const float l0 = wave_sum(lane < ck.n ? expf(s0l - m0) : 0.f), l1 = wave_sum(lane < ck.n ? expf(s1l - m1) : 0.f);
+          // (4) P V over this thread's positions
           {
             float a0[8], a1[8];
 #pragma unroll
@@ -759,7 +757,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
                 } else {
                   unpack8(vr[i], v8);
                 }
-                const float e0 = S.sc[0][jj], e1 = S.sc[1][jj];
+                const float e0 = expf(S.sc[0][jj] - m0), e1 = expf(S.sc[1][jj] - m1);
 #pragma unroll
                 for (int e = 0; e < 8; e++) { a0[e] = __builtin_fmaf(e0, v8[e], a0[e]); a1[e] = __builtin_fmaf(e1, v8[e], a1[e]); }
               }
@@ -767,10 +765,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
 #pragma unroll
             for (int e = 0; e < 8; e++) { S.opart[cw][ag][asl][e] = a0[e]; S.opart[cw][ag][asl][8 + e] = a1[e]; }
           }
-          wg_sync();  // 8
+          wg_sync();  // 3
           if (att_thread) {
-            m = mp;
-            lsum = S.red[12 + 2 * p] + S.red[12 + 2 * p + 1];
+            m = p ? m1 : m0;
+            lsum = p ? l1 : l0;
             for (int ww = 0; ww < W; ww++)
 #pragma unroll
               for (int gg = 0; gg < 4; gg++) o += S.opart[ww][gg][dd >> 3][p * 8 + (dd & 7)];
