@@ -942,7 +942,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   __syncthreads();
   {
     // default start delays per exchange (tuned on the 0.6B talker), overridable through the workspace
-    constexpr uint8_t kDefault[Ws::kHops] = {17, 23, 35, 17, 20, 29, 26, 23};
+    constexpr uint8_t kDefault[Ws::kHops] = {17, 23, 35, 23, 17, 32, 26, 20};
     const uint32_t w0 = ld_u32_dev(ws, Ws::kPollDelay), w1 = ld_u32_dev(ws, Ws::kPollDelay + 4);
 #pragma unroll
     for (int h = 0; h < Ws::kHops; h++) {
