@@ -1,6 +1,6 @@
 """Talker decode benchmark on one MI355X: frames/s of the 0.6B-shaped int8 talker at batch 1, KV 512.
 
-    python bench.py [--steps K] [--warmup W] [--workload talker06b|talker17b|cp06b] [--engine frames|graph|multi] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload talker06b|talker17b|cp06b|batch17b] [--engine frames|graph|multi] [--no-cpu]
 
 A step is one greedy decode run of 64 frames starting at KV length 512 (positions 512..575 are rewritten on
 every step, so every step does identical work). Each frame is embed -> 28 decoder layers (RMSNorm + qkv, q/k norm
@@ -11,6 +11,9 @@ codec head -> argmax, feeding the next frame. Engines:
   multi   one captured HIP graph per frame of the per-op kernels (5 launches per layer)
 Weights are seeded random-init of the real architecture, int8 per output channel with bf16 scales (``i8row``);
 the KV cache is bf16. Inputs are resident in HBM before timing starts.
+
+``--workload batch17b`` measures the batched path: a step is one run of 32 greedy frames of 16 1.7B-shaped streams
+with ragged prior KV lengths (64..2048), each frame one HIP graph replay of sk_batch_frame (M=16 MFMA GEMMs).
 
 ``--workload cp06b`` measures the code predictor instead: a step is 8 code-predictor frames, each one launch of
 sk_cp_frame over 16 positions (5 layers of the 0.6B shape, 15 greedy sub-codes from 2048-way heads).
@@ -209,6 +212,175 @@ def run_cp(args) -> None:
     print(json.dumps(res), flush=True)
 
 
+def batch_algorithmic_bytes(s, lengths, frames: int) -> dict:
+    """Bytes one batched decode step (every stream advances one token) must move, summed over the ``frames`` steps
+    of a run: the weights and scales once per step, each stream's K/V read at its attended length and its K/V
+    append, the head, and one embedding row per stream."""
+    w = algorithmic_bytes(s, 0)
+    weights = s.n_layers * sum(v for k, v in w["per_layer"].items() if k != "attn") + w["head"]
+    kv_row = 2 * s.nkv * s.head_dim * 2  # K and V of one position, all kv heads, bf16
+    run = 0
+    attn_first = 0
+    for f in range(frames):
+        kv = sum(kv_row * (T + 1 + f) + kv_row for T in lengths) * s.n_layers
+        run += weights + kv + len(lengths) * 2 * s.hidden
+        if f == 0:
+            attn_first = kv // s.n_layers
+    return {"weights": weights, "run": run, "step_mean": run / frames, "attn_layer_first": attn_first,
+            "per_layer": w["per_layer"]}
+
+
+def run_batch(args) -> None:
+    """16 ragged streams: one captured graph per batched step, 32 steps per run; per-kind kernel times from graphs
+    of repeated launches with HIP events."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from sokutou_amd import _lib
+    from sokutou_amd import synthetic as syn
+
+    dev = torch.device("cuda:0")
+    name = args.workload
+    spec = syn.WORKLOADS[name]
+    s = syn.workload_shape(name)
+    F, B = spec["frames"], spec["batch"]
+    t0 = time.perf_counter()
+    def progress(msg):
+        print(f"batch bench: {msg} ({time.perf_counter() - t0:.0f} s)", file=sys.stderr, flush=True)
+
+    eng, T, tok = syn.make_batch_engine(name, args.seed, dev, progress=progress)
+    eng.step()  # warm-up launch before capture
+    torch.cuda.synchronize()
+    eng.capture()
+    setup_s = time.perf_counter() - t0
+    print(f"batch bench: engine ready in {setup_s:.0f} s", file=sys.stderr, flush=True)
+
+    def run():
+        eng.reset(T, tok)
+        for _ in range(F):
+            eng.graph.replay()
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    if eng.error():
+        raise RuntimeError(f"batched step error {eng.error()}")
+    codes = eng.picked().cpu().numpy()
+    gold = ROOT / "tests" / "golden" / f"{name}_seed{args.seed}.json"
+    parity = None
+    if gold.exists():
+        parity = bool(np.array_equal(codes, np.array(json.loads(gold.read_text())["codes"])))
+    ab = batch_algorithmic_bytes(s, T, F)
+    step_us = dt * 1e6 / (args.steps * F)
+    # per-kind kernel times: `reps` launches of one kind in a graph, replayed, HIP events on the replay stream
+    P, Ly = eng.P, eng.P.layers[0]
+    p, st = _lib.ptr, None
+    H, I, nq, nkv = P.H, P.I, P.nq, P.nkv
+    nt = int(_lib.load().sk_batch_terms())
+    f32 = dict(dtype=torch.float32, device=dev)
+    x_h = torch.randn((nt, 16, H), device=dev).to(torch.bfloat16) * 0.01
+    x_a = torch.randn((nt, 16, nq * 128), device=dev).to(torch.bfloat16) * 0.01
+    x_i = torch.randn((nt, 16, I), device=dev).to(torch.bfloat16) * 0.01
+    ssp = torch.ones((H // 16, 16), **f32)
+    qkv = torch.randn((16, (nq + 2 * nkv) * 128), **f32)
+    h = torch.zeros((16, H), **f32)
+    act = torch.zeros((nt, 16, I), dtype=torch.bfloat16, device=dev)
+    xn = torch.zeros((nt, 16, H), dtype=torch.bfloat16, device=dev)
+    att = torch.zeros((nt, 16, nq * 128), dtype=torch.bfloat16, device=dev)
+    sso = torch.zeros((H // 16, 16), **f32)
+    aws = torch.zeros(int(_lib.load().sk_batch_attn_workspace_size(nkv)), dtype=torch.uint8, device=dev)
+    eng.reset(T, tok)
+    torch.cuda.synchronize()
+
+    def gemm(x, ss, np_, lin_w, lin_s, N, K, mode, out, a, xn_, nw, so):
+        _lib.call("sk_bgemm", p(x), p(ss), np_, P.eps, p(lin_w), p(lin_s), N, K, mode, p(out), p(a), p(xn_), p(nw),
+                  p(so), _lib.stream())
+
+    calls = {
+        "qkv": lambda: gemm(x_h, ssp, H // 16, Ly["qkv"].w, Ly["qkv"].s, (nq + 2 * nkv) * 128, H, 0, qkv, None, None,
+                            None, None),
+        "attn": lambda: _lib.call("sk_batch_attn", p(qkv), p(Ly["qn"]), p(Ly["kn"]), P.eps, p(P.rope), p(eng.kc[0]),
+                                  p(eng.vc[0]), p(eng.pos), B, eng.max_len, nq, nkv, p(att), p(aws), aws.numel(),
+                                  _lib.stream()),
+        "o": lambda: gemm(x_a, None, 0, Ly["o"].w, Ly["o"].s, H, nq * 128, 2, h, None, xn, Ly["post_norm"], sso),
+        "gu": lambda: gemm(x_h, ssp, H // 16, Ly["gu"].w, Ly["gu"].s, 2 * I, H, 1, None, act, None, None, None),
+        "down": lambda: gemm(x_i, None, 0, Ly["down"].w, Ly["down"].s, H, I, 2, h, None, xn, Ly["post_norm"], sso),
+    }
+    kt = {}
+    reps = 50
+    for k, fn in calls.items():
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        kt[k] = e0.elapsed_time(e1) * 1e3 / reps
+    per = dict(ab["per_layer"])
+    per["attn"] = ab["attn_layer_first"]
+    per_step_us = {k: v * s.n_layers for k, v in kt.items()}
+    dom = max(per_step_us, key=per_step_us.get)
+    achieved = per[dom] / (kt[dom] * 1e-6) / 1e9
+    gbs = ab["step_mean"] / (step_us * 1e-6) / 1e9
+    res = {
+        "metric": "batched talker decode stream-frames/sec (1.7B int8, 16 streams, ragged KV 64-2048, 32 frames)",
+        "value": round(B * F * args.steps / dt, 1), "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3 / args.steps, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 weights x bf16 MFMA (3 bf16 terms per activation), fp32 accumulate, bf16 KV cache",
+        "data": "synthetic",
+        "config": {"workload": f"{name}: {B} streams x {F} greedy frames, {s.n_layers} layers, hidden {s.hidden}, "
+                               f"{s.nq}q/{s.nkv}kv heads x 128, intermediate {s.inter}, vocab {s.vocab}, i8row, prior "
+                               f"KV lengths {min(T)}..{max(T)} (mean {sum(T) / len(T):.0f})", "batch": B,
+                   "frames_per_step": F, "engine": "sk_batch_frame, one HIP graph per batched step"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "bytes_per_launch": int(per[dom]),
+                     "avg_launch_us": round(kt[dom], 2)},
+        "frame": {"us_per_batched_step": round(step_us, 1), "us_per_layer": round(step_us / s.n_layers, 2),
+                  "algorithmic_bytes_per_step": int(ab["step_mean"]), "effective_GBs": round(gbs, 1),
+                  "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+                  "kernel_us_per_step": {k: round(v, 1) for k, v in per_step_us.items()},
+                  "kernel_avg_us": {k: round(v, 2) for k, v in kt.items()}},
+        "parity_codes_match_oracle": parity, "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu:
+        from oracle.workload import batch_oracle
+
+        orc, oT, otok, _ = batch_oracle(name, args.seed, streams=list(range(4)))
+        pos, t = list(oT), list(otok)
+        t, _ = orc.step(t, pos)  # warm-up
+        pos = [x + 1 for x in pos]
+        times = []
+        t_start = time.perf_counter()
+        while time.perf_counter() - t_start < 15.0 and len(times) < 8:
+            t1 = time.perf_counter()
+            t, _ = orc.step(t, pos)
+            times.append(time.perf_counter() - t1)
+            pos = [x + 1 for x in pos]
+        from threadpoolctl import threadpool_info
+        med = float(np.median(times))
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        res["cpu_baseline"] = {"value": round(4 / med, 3), "unit": "frames/s", "cores": int(threads), "kind": "port",
+                               "sample": f"{len(times)} batched steps of streams 0-3 (4 streams) after one warm-up, "
+                                         f"median {med * 1e3:.0f} ms; numpy fp32 over dequantised int8 weights",
+                               "host_cpus": os.cpu_count()}
+    print(json.dumps(res), flush=True)
+
+
 def cpu_baseline(name: str, seed: int, budget_s: float = 15.0) -> dict:
     """The numpy oracle on this host's cores: frames of the same workload until ~budget_s of frame time."""
     import numpy as np
@@ -244,7 +416,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="talker06b", choices=["talker06b", "talker17b", "cp06b"])
+    ap.add_argument("--workload", default="talker06b", choices=["talker06b", "talker17b", "cp06b", "batch17b"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--engine", default="frames", choices=["frames", "graph", "multi"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
@@ -259,6 +431,9 @@ def main() -> None:
 
     if args.workload == "cp06b":
         run_cp(args)
+        return
+    if args.workload == "batch17b":
+        run_batch(args)
         return
 
     import torch

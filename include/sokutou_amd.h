@@ -198,6 +198,82 @@ typedef struct sk_cp_desc {
  * reference can pair them, qwen3/kernels.py:600-617, with the same result). */
 int sk_cp_frame(const sk_cp_desc* desc, void* stream);
 
+
+/* ---- batched decode: up to 16 streams per step on the matrix cores -------------------------------------------
+ * The reference decodes one stream (qwen3/fast.py:146); these entry points have no reference kernel to replace.
+ * They run the same layer math as sk_talker_frames over a batch, with every projection an M = 16 skinny GEMM on
+ * bf16 MFMA: int8 weights (exact in bf16) in the tile layout of sk_tile_weights, activations passed as
+ * sk_batch_terms() bf16 planes whose sum is the fp32 value. */
+
+/* Number of bf16 terms per activation value (planes of every batched GEMM input). */
+int sk_batch_terms(void);
+
+/* Rewrites int8 weights [N, K] (row-major) into the batched GEMM's tile layout (same size): tile (g, c) is
+ * 1 KiB at byte (g * K/64 + c) * 1024 and holds W[16 g + n][64 c + 16 j + e] at byte 16 (n + 16 j) + e.
+ * N % 16 == 0, K % 64 == 0. */
+int sk_tile_weights(const void* w, void* tiled, int N, int K, void* stream);
+
+/* One M = 16 projection. x: bf16 planes [terms][16][K]; w_tiled / s: tiled int8 weights [N, K] + bf16 row scales.
+ * ssp (optional, [np][16]): partial sums of squares of the residual whose normalised copy x is; when given, row m
+ * is multiplied by rsqrt(Σ_q ssp[q][m] / K + eps) after the dot product (the fused RMSNorm of rms_gemv,
+ * qwen3/kernels.py:180-186, 224). mode 0: out[16][N] = result (fp32). mode 1: rows interleaved gate/up,
+ * act = planes [terms][16][N/2] of silu(gate) * up. mode 2: out[16][N] += result (the residual), then xn = planes
+ * [terms][16][N] of out ⊙ nw and ssp_out[N/16][16] = per 16-column partial sums of squares of out.
+ * K in {512, 1024, 2048, 3072, 4096, 6144}; N % 16 == 0 (N % 32 == 0 for mode 1). */
+int sk_bgemm(const void* x, const float* ssp, int np, float eps, const void* w_tiled, const uint16_t* s, int N, int K,
+             int mode, float* out, void* act, void* xn, const float* nw, float* ssp_out, void* stream);
+
+/* Workspace bytes of sk_batch_attn (zeroed once; its first 4 bytes are the error word, 5 = a position out of
+ * range). */
+int64_t sk_batch_attn_workspace_size(int nkv);
+
+/* Decode attention of `batch` streams, each at its own position pos[b] (device int64) of its own caches
+ * Kc / Vc [batch][nkv][max_len][128] bf16, with the math of sk_attn (per-head q/k RMSNorm, rotate-half RoPE,
+ * bf16 K/V append at pos[b], softmax over positions 0..pos[b]). qkv: [16][(nq + 2 nkv) * 128] fp32; att: bf16
+ * planes [terms][16][nq * 128] (the input of the o projection). Split over (stream, kv head, 64 positions) with a
+ * log-sum-exp merge; max_len <= 4096.
+ * Replaces, per stream, attn (qwen3/kernels.py:338-414). */
+int sk_batch_attn(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc, void* Vc,
+                  const int64_t* pos, int batch, int max_len, int nq, int nkv, void* att, void* workspace,
+                  int64_t workspace_bytes, void* stream);
+
+/* A batch of talker streams. layers is a HOST array of n_layers descriptors whose weights are tiled
+ * (sk_tile_weights) and whose caches kc / vc are [batch][nkv][max_len][128] bf16; head_w is tiled too. ids / pos /
+ * nstep are device int64 [batch]: each stream's current token, the position it is written at, and how many picks
+ * it has made; codes is [max_frames][16] int64 (codes[f][b] = pick f of stream b). logits (optional) receives
+ * [16][vocab] of the last step, layer_out (optional) [n_layers][16][hidden] residuals of the last step. */
+typedef struct sk_batch_desc {
+  int n_layers, hidden, inter, nq, nkv, vocab, batch, max_len;
+  float eps;
+  const sk_layer_desc* layers;
+  const float* norm;
+  const void* head_w;
+  const uint16_t* head_s;
+  const void* emb;            /* input embedding table [vocab, hidden] bf16 */
+  const float* rope;          /* [max_len][cos 64 | sin 64] */
+  int64_t* ids;
+  int64_t* pos;
+  int64_t* codes;
+  int64_t* nstep;
+  int max_frames;
+  float* logits;
+  float* layer_out;
+  void* workspace;
+  int64_t workspace_bytes;
+} sk_batch_desc;
+
+/* Workspace bytes for the batched step; zero it once before the first call (its first 4 bytes are the error
+ * word: 0 healthy, 5 a position or token out of range, 6 more picks than max_frames). */
+int64_t sk_batch_workspace_size(int hidden, int inter, int nq, int nkv, int vocab);
+
+/* Loads each stream's input for the next step: h = emb[ids[b]] and its normalised planes. */
+int sk_batch_embed(const sk_batch_desc* desc, void* stream);
+
+/* One decode step for every stream: n_layers x (qkv GEMM, ragged split-K attention with KV append at pos[b],
+ * o GEMM, gate/up GEMM, down GEMM), final RMSNorm + head GEMM, greedy pick per stream (lowest index on ties), then
+ * codes / ids / nstep / pos advance and the picked rows are embedded for the next step. 5 n_layers + 2 launches. */
+int sk_batch_frame(const sk_batch_desc* desc, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -149,22 +149,54 @@ def rmsnorm(h: np.ndarray, nw: np.ndarray, eps: float) -> np.ndarray:
     return (h * inv) * nw.astype(F32)
 
 
-def rms_gemv(h: np.ndarray, nw: np.ndarray, eps: float, W: np.ndarray, swiglu: bool = False) -> np.ndarray:
+def bf16_terms(x: np.ndarray, n: int) -> np.ndarray:
+    """x as the sum of ``n`` bf16 values (``t_0 = bf16(x)``, ``t_i = bf16(x - t_0 - ... - t_{i-1})``, each
+    difference exact in fp32), summed back in fp32: the input the batched path's matrix cores see. n = 0 is x."""
+    x = np.asarray(x, dtype=F32)
+    if n <= 0:
+        return x
+    r, acc = x.copy(), np.zeros_like(x)
+    for _ in range(n):
+        t = bf16_round(r)
+        acc = acc + t
+        r = r - t
+    return acc
+
+
+def _act(x: np.ndarray, act_bf16) -> np.ndarray:
+    # act_bf16: False/0 exact fp32 inputs, True/1 one bf16 term, n: a sum of n bf16 terms
+    return bf16_terms(x, int(act_bf16))
+
+
+def rms_gemv(h: np.ndarray, nw: np.ndarray, eps: float, W: np.ndarray, swiglu: bool = False,
+             act_bf16: bool = False) -> np.ndarray:
     """``y = W (h*nw) * rsqrt(mean(h^2)+eps)``; with swiglu the rows are interleaved gate/up and
-    ``out[n] = g/(1+exp(-g)) * u`` from rows 2n, 2n+1 (qwen3/kernels.py:255-275, 267)."""
+    ``out[n] = g/(1+exp(-g)) * u`` from rows 2n, 2n+1 (qwen3/kernels.py:255-275, 267).
+    ``act_bf16`` rounds the staged vector ``h*nw`` to bf16 before the product (the batched path's rounding point).
+    ``h`` may also be a batch [B, K] (one row per stream)."""
     h = h.astype(F32)
+    if h.ndim == 2:
+        ss = np.einsum("bk,bk->b", h, h).astype(F32)
+        inv = F32(1.0) / np.sqrt(ss / F32(h.shape[1]) + F32(eps), dtype=F32)
+        y = (_act(h * nw.astype(F32)[None, :], act_bf16) @ W.T) * inv[:, None]
+        if swiglu:
+            g, u = y[:, 0::2], y[:, 1::2]
+            return (g / (F32(1.0) + np.exp(-g))) * u
+        return y
     inv = F32(1.0) / np.sqrt(np.dot(h, h) / F32(h.size) + F32(eps), dtype=F32)
-    y = (W @ (h * nw.astype(F32))) * inv
+    y = (W @ _act(h * nw.astype(F32), act_bf16)) * inv
     if swiglu:
         g, u = y[0::2], y[1::2]
         return (g / (F32(1.0) + np.exp(-g))) * u
     return y
 
 
-def gemv(x: np.ndarray, W: np.ndarray, bias: np.ndarray | None = None, out: np.ndarray | None = None) -> np.ndarray:
+def gemv(x: np.ndarray, W: np.ndarray, bias: np.ndarray | None = None, out: np.ndarray | None = None,
+         act_bf16: bool = False) -> np.ndarray:
     """``out (+)= W x (+ bias)`` (qwen3/kernels.py:283-305): bias then the accumulated value are added to the
-    dot product, in that order."""
-    v = W @ x.astype(F32)
+    dot product, in that order. ``act_bf16`` rounds x to bf16 first; ``x`` may be a batch [B, K]."""
+    x = _act(x.astype(F32), act_bf16)
+    v = x @ W.T if x.ndim == 2 else W @ x
     if bias is not None:
         v = v + bias.astype(F32)
     if out is not None:
@@ -218,16 +250,17 @@ def attention(qkv: np.ndarray, qn: np.ndarray, kn: np.ndarray, eps: float, rope:
 
 
 def decoder_layer(h: np.ndarray, L: dict, eps: float, rope: np.ndarray, Kc: np.ndarray, Vc: np.ndarray, pos: int,
-                  nq: int, nkv: int, cache_bf16: bool = True) -> np.ndarray:
+                  nq: int, nkv: int, cache_bf16: bool = True, act_bf16: bool = False) -> np.ndarray:
     """One decoder layer on the fp32 residual ``h`` (qwen3/kernels.py:619-627):
     rms_gemv(qkv) -> attn -> gemv(o, +=h) -> rms_gemv(gu, swiglu) -> gemv(down, +=h).
     ``L`` holds dequantised fp32 matrices ``qkv`` [(nq+2nkv)*128, H], ``o``, ``gu`` (gate/up rows interleaved),
-    ``down`` and the fp32 norm vectors ``in_norm``, ``post_norm``, ``qn``, ``kn``."""
-    qkv = rms_gemv(h, L["in_norm"], eps, L["qkv"])
+    ``down`` and the fp32 norm vectors ``in_norm``, ``post_norm``, ``qn``, ``kn``. ``act_bf16`` rounds every
+    projection input to bf16 (the batched path)."""
+    qkv = rms_gemv(h, L["in_norm"], eps, L["qkv"], act_bf16=act_bf16)
     att = attention(qkv, L["qn"], L["kn"], eps, rope, Kc, Vc, pos, nq, nkv, cache_bf16)
-    h = gemv(att, L["o"], out=h)
-    act = rms_gemv(h, L["post_norm"], eps, L["gu"], swiglu=True)
-    return gemv(act, L["down"], out=h)
+    h = gemv(att, L["o"], out=h, act_bf16=act_bf16)
+    act = rms_gemv(h, L["post_norm"], eps, L["gu"], swiglu=True, act_bf16=act_bf16)
+    return gemv(act, L["down"], out=h, act_bf16=act_bf16)
 
 
 # ---------------------------------------------------------------------------------------------------------
@@ -354,3 +387,33 @@ class CodePredictorOracle:
             codes.append(argmax_first(lg))
             logits.append(lg)
         return codes, logits
+
+
+class BatchTalkerOracle:
+    """Independent talker streams stepped together, as the batched path runs them: stream b has its own caches
+    ``Ks[b]`` / ``Vs[b]`` ([layers, nkv, len, 128] fp32) and position. Each step embeds every stream's token, runs
+    the decoder stack with the projections of all streams as one matrix product (row b is exactly the M=1
+    ``decoder_layer`` math, qwen3/kernels.py:619-627), applies the final RMSNorm inside the head projection
+    (``rms_gemv`` with the final norm weight: the head GEMM of the batched path, equal in value to ``rmsnorm``
+    followed by ``gemv``) and picks each stream's argmax. ``act_terms`` as ``bf16_terms`` (0: fp32 inputs)."""
+
+    def __init__(self, weights: dict, Ks: list, Vs: list, cache_bf16: bool = True, act_terms: int = 0):
+        self.w, self.Ks, self.Vs = weights, Ks, Vs
+        self.cache_bf16, self.act = cache_bf16, act_terms
+
+    def step(self, tokens, pos, layer_out: list | None = None):
+        """Returns (codes [B], logits [B, V]); ``layer_out`` receives [B, H] after every layer."""
+        w, B = self.w, len(tokens)
+        h = np.stack([w["emb"][t] for t in tokens]).astype(F32)
+        for i, L in enumerate(w["layers"]):
+            qkv = rms_gemv(h, L["in_norm"], w["eps"], L["qkv"], act_bf16=self.act)
+            att = np.stack([attention(qkv[b], L["qn"], L["kn"], w["eps"], w["rope"], self.Ks[b][i], self.Vs[b][i],
+                                      int(pos[b]), w["nq"], w["nkv"], self.cache_bf16) for b in range(B)])
+            h = gemv(att, L["o"], out=h, act_bf16=self.act)
+            act = rms_gemv(h, L["post_norm"], w["eps"], L["gu"], swiglu=True, act_bf16=self.act)
+            h = gemv(act, L["down"], out=h, act_bf16=self.act)
+            if layer_out is not None:
+                layer_out.append(h.copy())
+        lg = rms_gemv(h, w["norm"], w["eps"], w["head"], act_bf16=self.act)
+        return [argmax_first(lg[b]) for b in range(B)], lg
+

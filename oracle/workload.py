@@ -77,3 +77,34 @@ def cp_oracle(name: str = "cp06b", seed: int = 0, wd: str = "i8row", cache_bf16:
                "heads": [O.quantize(h, wd)[2] for h in w["heads"]], "cemb": w["cemb"], "temb": w["temb"],
                "rope": O.rope_table(syn.inv_freq(s), n), "eps": s.eps, "nq": s.nq, "nkv": s.nkv}
     return O.CodePredictorOracle(weights, n, cache_bf16), s
+
+
+def batch_oracle(name: str, seed: int = 0, frames: int | None = None, cache_bf16: bool = True, act_terms: int = 0,
+                 streams: list | None = None):
+    """Returns (BatchTalkerOracle, lengths, tokens, shape) for a batched workload: the talker's weights quantised
+    by the oracle, every stream's prior cache regenerated. ``streams`` selects a subset of the streams."""
+    spec = syn.WORKLOADS[name]
+    s = syn.workload_shape(name)
+    frames = spec["frames"] if frames is None else frames
+    T = syn.batch_lengths(seed, name)
+    tok = syn.batch_tokens(seed, name)
+    streams = list(range(spec["batch"])) if streams is None else list(streams)
+    layers = [pack_layer(syn.layer_weights(seed, i, s), "i8row") for i in range(s.n_layers)]
+    f = syn.final_weights(seed, s)
+    max_len = syn.batch_max_len(name, frames)
+    weights = {"layers": layers, "norm": f["norm"], "head": O.quantize(f["head"], "i8row")[2], "emb": f["emb"],
+               "rope": O.rope_table(syn.inv_freq(s), max_len), "eps": s.eps, "nq": s.nq, "nkv": s.nkv}
+    Ks, Vs = [], []
+    for b in streams:
+        n = T[b] + frames + 1
+        K = np.zeros((s.n_layers, s.nkv, n, 128), np.float32)
+        V = np.zeros_like(K)
+        for i in range(s.n_layers):
+            k, v = syn.batch_prefill(seed, i, b, s, T[b])
+            K[i, :, :T[b]] = k
+            V[i, :, :T[b]] = v
+        Ks.append(K)
+        Vs.append(V)
+    orc = O.BatchTalkerOracle(weights, Ks, Vs, cache_bf16, act_terms)
+    return orc, [T[b] for b in streams], [tok[b] for b in streams], s
+

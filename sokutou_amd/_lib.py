@@ -66,6 +66,24 @@ class SkCpDesc(ctypes.Structure):
                 ("workspace_bytes", c_int64)]
 
 
+class SkBatchDesc(ctypes.Structure):
+    """Mirror of ``sk_batch_desc`` (include/sokutou_amd.h)."""
+    _fields_ = [("n_layers", c_int), ("hidden", c_int), ("inter", c_int), ("nq", c_int), ("nkv", c_int),
+                ("vocab", c_int), ("batch", c_int), ("max_len", c_int), ("eps", c_float), ("layers", c_void_p),
+                ("norm", c_void_p), ("head_w", c_void_p), ("head_s", c_void_p), ("emb", c_void_p), ("rope", c_void_p),
+                ("ids", c_void_p), ("pos", c_void_p), ("codes", c_void_p), ("nstep", c_void_p),
+                ("max_frames", c_int), ("logits", c_void_p), ("layer_out", c_void_p), ("workspace", c_void_p),
+                ("workspace_bytes", c_int64)]
+
+
+_SIGS["sk_batch_terms"] = (c_int, [])
+_SIGS["sk_tile_weights"] = (c_int, [_P, _P, c_int, c_int, _P])
+_SIGS["sk_bgemm"] = (c_int, [_P, _P, c_int, c_float, _P, _P, c_int, c_int, c_int, _P, _P, _P, _P, _P, _P])
+_SIGS["sk_batch_workspace_size"] = (c_int64, [c_int, c_int, c_int, c_int, c_int])
+_SIGS["sk_batch_attn_workspace_size"] = (c_int64, [c_int])
+_SIGS["sk_batch_attn"] = (c_int, [_P, _P, _P, c_float, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, _P, c_int64, _P])
+_SIGS["sk_batch_embed"] = (c_int, [ctypes.POINTER(SkBatchDesc), _P])
+_SIGS["sk_batch_frame"] = (c_int, [ctypes.POINTER(SkBatchDesc), _P])
 _SIGS["sk_talker_workspace_size"] = (c_int64, [c_int, c_int])
 _SIGS["sk_talker_frames"] = (c_int, [ctypes.POINTER(SkTalkerDesc), c_int, _P])
 _SIGS["sk_cp_frame"] = (c_int, [ctypes.POINTER(SkCpDesc), _P])

@@ -1,0 +1,693 @@
+// Batched talker decode: up to 16 streams per step, the projections as M=16 skinny GEMMs on the matrix cores.
+//
+// The reference decodes one stream (qwen3/fast.py:146 asserts batch 1) with M=1 GEMVs (qwen3/kernels.py:143-310).
+// With 16 streams the projections are dense [16 x K] x [K x N] contractions, so they go to
+// v_mfma_f32_16x16x32_bf16: int8 weights are exact in bf16 (|q| <= 127 has 7 significant bits), and each
+// activation is split into kTerms bf16 terms (x = t0 + t1 + ..., t_i = bf16 of what the earlier terms left), so
+// the products are exact and the sum keeps fp32 input precision; one bf16 term alone loses ~1e-2 of relative
+// accuracy over 28 layers.
+//
+// Data layout (all activations have 16 rows; rows of inactive streams stay zero):
+//   * weights: int8 in 1 KiB tiles. Tile (g, c) holds rows 16g..16g+15, columns 64c..64c+63; lane L = n + 16 j of
+//     a wave reads bytes [16 L, 16 L + 16) = W[16 g + n][64 c + 16 j .. + 16] with one 16-byte load, so a wave's
+//     load is one contiguous KiB. Within a chunk the contraction index is permuted identically for both operands
+//     (MFMA h = 0, 1 of the chunk takes bytes 8h..8h+7 of every lane), which leaves the dot product unchanged.
+//   * GEMM inputs: bf16 planes [kTerms][16][K]; lane (m + 16 j) reads x[m][64 c + 16 j .. + 16] of every plane.
+//   * RMSNorm: the kernel that updates the residual h also writes the planes of bf16(h ⊙ w_next) and, per
+//     16-column tile, the partial sums of squares of h; the consuming GEMM adds the partials of its row in a fixed
+//     order and applies rsqrt(Σh²/K + eps) after the dot product (qwen3/kernels.py:180-186, 224).
+//
+// Per layer: qkv GEMM -> ragged split-K attention -> o GEMM (+= h, norm planes) -> gate/up GEMM (SwiGLU planes)
+// -> down GEMM (+= h, norm planes of the next layer). Then the head GEMM and a greedy pick that also embeds the
+// chosen token for the next step. Every kernel is deterministic: fixed reduction orders, no float atomics.
+#include "common.h"
+#include "internal.h"
+
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+
+constexpr int kM = 16;         // rows of every activation buffer (streams)
+#ifndef SK_BATCH_TERMS
+#define SK_BATCH_TERMS 3
+#endif
+constexpr int kTerms = SK_BATCH_TERMS;
+constexpr int kThreads = 256;
+constexpr int kOutF32 = 0, kOutSwiglu = 1, kOutAcc = 2;
+
+// ---- conversions ----------------------------------------------------------------------------------------------
+// two floats whose low 16 bits are zero (small integers) -> packed bf16 pair, lo in the low half
+__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+// 8 int8 (two dwords) -> 8 bf16, exactly
+__device__ __forceinline__ bf16x8 i8x8_bf16(uint32_t a, uint32_t b) {
+  u32x4 r;
+  r.x = pack_hi16((float)(int8_t)a, (float)(int8_t)(a >> 8));
+  r.y = pack_hi16((float)(int8_t)(a >> 16), (float)(int8_t)(a >> 24));
+  r.z = pack_hi16((float)(int8_t)b, (float)(int8_t)(b >> 8));
+  r.w = pack_hi16((float)(int8_t)(b >> 16), (float)(int8_t)(b >> 24));
+  return __builtin_bit_cast(bf16x8, r);
+}
+__device__ __forceinline__ uint4 gload4(const uint4* p) {
+  const u32x4 v = *(gptr<const u32x4>)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
+  u32x4 r = {v.x, v.y, v.z, v.w};
+  return __builtin_bit_cast(bf16x8, r);
+}
+// v as kTerms bf16 terms written to planes [kTerms][plane] at index i
+__device__ __forceinline__ void store_terms(bf16_t* __restrict__ planes, size_t plane, size_t i, float v) {
+#pragma unroll
+  for (int t = 0; t < kTerms; t++) {
+    const bf16_t b = f2bf(v);
+    planes[t * plane + i] = b;
+    v -= bf2f(b);
+  }
+}
+
+struct GemmArgs {
+  const bf16_t* x;      // input planes [kTerms][16][K]
+  const float* ssp;     // [np][16] partial sums of squares behind x (NULL: no RMSNorm scale)
+  int np;
+  float eps;
+  const uint8_t* w;     // tiled int8 weights
+  const uint16_t* s;    // [N] bf16 row scales
+  int N, K;
+  float* out;           // F32: [16][N]; ACC: residual [16][N], updated in place
+  bf16_t* act;          // SWIGLU: planes [kTerms][16][N/2]
+  bf16_t* xn;           // ACC: planes [kTerms][16][N] of bf16(h ⊙ nw)
+  const float* nw;      // ACC: next RMSNorm weight [N]
+  float* ssp_out;       // ACC: [N/16][16] partial sums of squares of the updated residual
+};
+
+// One workgroup computes R 16-row groups of the output for all 16 rows; its 4 waves split K in quarters
+// (CW chunks of 64 each) and meet in LDS for a fixed-order sum. Every weight load of a wave is issued at the top
+// (the weight stream is the kernel's HBM traffic), the activation planes (L2-resident) run DA chunks ahead.
+template <int OUT, int R, int CW>
+__global__ __launch_bounds__(kThreads) void k_bgemm(GemmArgs p) {
+  constexpr int DA = CW < 4 ? CW : 4;
+  __shared__ float red[4][R][4][64];
+  __shared__ float ssq[16][kM];
+  __shared__ float inv_s[kM];
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  const int C = 4 * CW;                  // 64-wide chunks per row
+  const int g0 = blockIdx.x * R;
+  const int c0 = wv * CW;
+  const size_t plane = (size_t)kM * p.K;
+  const uint4* xp = (const uint4*)(p.x + (size_t)(lane & 15) * p.K + (size_t)c0 * 64 + 16 * (lane >> 4));
+  uint4 wq[CW][R], xa[DA][kTerms][2];
+#pragma unroll
+  for (int c = 0; c < CW; c++)
+#pragma unroll
+    for (int r = 0; r < R; r++)
+      wq[c][r] = ld_stream((const uint4*)p.w + ((size_t)(g0 + r) * C + c0 + c) * 64 + lane);
+  auto load_a = [&](int slot, int c) {
+#pragma unroll
+    for (int t = 0; t < kTerms; t++) {
+      const uint4* q = xp + (t * plane) / 8 + c * 8;
+      xa[slot][t][0] = gload4(q);
+      xa[slot][t][1] = gload4(q + 1);
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < DA; c++) load_a(c, c);
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 acc[R], acc2[R];  // first term, later terms (kept apart: the small terms accumulate at their own scale)
+#pragma unroll
+  for (int r = 0; r < R; r++) { acc[r] = f32x4{0.f, 0.f, 0.f, 0.f}; acc2[r] = acc[r]; }
+#pragma unroll
+  for (int c = 0; c < CW; c++) {
+    const int slot = c % DA;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const uint4 q = wq[c][r];
+        const bf16x8 b = h ? i8x8_bf16(q.z, q.w) : i8x8_bf16(q.x, q.y);
+        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[slot][0][h]), b, acc[r], 0, 0, 0);
+#pragma unroll
+        for (int t = 1; t < kTerms; t++)
+          acc2[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[slot][t][h]), b, acc2[r], 0, 0, 0);
+      }
+    }
+    if (c + DA < CW) load_a(slot, c + DA);
+  }
+  // D[m][n] sits in lane n + 16 (m / 4), element m % 4
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[wv][r][i][lane] = acc[r][i] + acc2[r][i];
+  if (p.ssp) {
+    float v = 0.f;
+    for (int q = tid >> 4; q < p.np; q += 16) v += gload(p.ssp + q * kM + (tid & 15));
+    ssq[tid >> 4][tid & 15] = v;
+  }
+  __syncthreads();
+  if (p.ssp && tid < kM) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 16; q++) s += ssq[q][tid];
+    inv_s[tid] = rsqrtf(s / p.K + p.eps);
+  }
+  __syncthreads();
+  const int i = tid >> 6, L = tid & 63;
+  const int m = 4 * (L >> 4) + i, nl = L & 15;
+  const float iv = p.ssp ? inv_s[m] : 1.f;
+  float ss = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const float v = (red[0][r][i][L] + red[1][r][i][L]) + (red[2][r][i][L] + red[3][r][i][L]);
+    const int n = (g0 + r) * 16 + nl;
+    const float y = v * bf2f(p.s[n]) * iv;
+    if constexpr (OUT == kOutF32) {
+      p.out[(size_t)m * p.N + n] = y;
+    } else if constexpr (OUT == kOutSwiglu) {
+      const float u = dpp<0xB1>(y);  // lane L ^ 1: the up row next to this gate row
+      if (!(nl & 1)) store_terms(p.act, (size_t)kM * (p.N / 2), (size_t)m * (p.N / 2) + n / 2, silu_mul(y, u));
+    } else {
+      float* hp = p.out + (size_t)m * p.N + n;
+      const float hn = *hp + y;
+      *hp = hn;
+      store_terms(p.xn, (size_t)kM * p.N, (size_t)m * p.N + n, hn * p.nw[n]);
+      ss = __builtin_fmaf(hn, hn, ss);
+    }
+  }
+  if constexpr (OUT == kOutAcc) {
+    ss = row16_sum(ss);
+    if (nl == 0) p.ssp_out[blockIdx.x * kM + m] = ss;
+  }
+}
+
+// ---- weight tiling -----------------------------------------------------------------------------------------
+__global__ void k_tile(const int8_t* __restrict__ w, int8_t* __restrict__ tiled, int N, int K) {
+  // one thread per 16-byte lane slot: tile t = g * C + c, lane L = n + 16 j
+  const size_t slot = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int C = K / 64;
+  if (slot >= (size_t)N * K / 16) return;
+  const int L = (int)(slot & 63);
+  const size_t t = slot >> 6;
+  const int g = (int)(t / C), c = (int)(t % C);
+  const int n = L & 15, j = L >> 4;
+  const uint4 v = *(const uint4*)(w + (size_t)(16 * g + n) * K + 64 * c + 16 * j);
+  *(uint4*)(tiled + slot * 16) = v;
+}
+
+// ---- ragged split-K decode attention -----------------------------------------------------------------------
+// Block (stream b, kv head g, split s) covers positions [64 s, 64 s + 64) of stream b's cache up to its current
+// position; the split that holds the position also normalises, rotates and appends this step's K and V. Partials
+// (max, sum, Σ p v) go to the workspace; the last split of (b, g) to arrive merges them in split order and writes
+// the attention output as bf16 term planes. Numerics as sk_attn (qwen3/kernels.py:338-414).
+constexpr int kAttnChunk = 64;
+constexpr int kAttnSplitMax = 64;  // max_len <= 4096
+constexpr int kPart = SK_HD + 2;
+constexpr float kInvSqrtHd = 0.08838834764831845f;
+
+struct AttnArgs {
+  const float* qkv;     // [16][(nq + 2 nkv) * 128]
+  const float* qn;
+  const float* kn;
+  float eps;
+  const float* rope;    // [max_len][cos 64 | sin 64]
+  bf16_t* Kc;           // [batch][nkv][max_len][128]
+  bf16_t* Vc;
+  const int64_t* pos;   // [batch]
+  int max_len, nq, nkv;
+  bf16_t* att;          // planes [kTerms][16][nq * 128]
+  float* part;          // [batch * nkv][2][kAttnSplitMax][kPart]
+  unsigned* counters;   // [batch * nkv]
+  int* err;
+};
+
+__global__ __launch_bounds__(kThreads) void k_battn(AttnArgs a) {
+  __shared__ float qsh[2][SK_HD];
+  __shared__ float ksh[SK_HD];
+  __shared__ float vsh[SK_HD];
+  __shared__ float sc[2][kAttnChunk];
+  __shared__ float red[16];
+  __shared__ float opart[4][4][16][17];
+  __shared__ float mls[2][kAttnSplitMax][2];
+  __shared__ int is_last;
+  const int bg = blockIdx.x, b = bg / a.nkv, kvh = bg % a.nkv, split = blockIdx.y;
+  const int t = threadIdx.x, p = t >> 7, d = t & (SK_HD - 1), w = t >> 6, lane = t & 63, gq = lane >> 4, sl = lane & 15;
+  const int qs = (a.nq + 2 * a.nkv) * SK_HD;
+  const int64_t pos64 = a.pos[b];
+  const size_t ap = (size_t)kM * a.nq * SK_HD;
+  if (pos64 < 0 || pos64 >= a.max_len) {  // a stream past its cache: zero output, error word set
+    if (split == 0) {
+      store_terms(a.att, ap, (size_t)b * a.nq * SK_HD + (2 * kvh + p) * SK_HD + d, 0.f);
+      if (t == 0) atomicCAS(a.err, 0, 5);
+    }
+    return;
+  }
+  const int pos = (int)pos64, T = pos + 1, ns = (T + kAttnChunk - 1) / kAttnChunk;
+  if (split >= ns) return;
+  const int t0 = split * kAttnChunk, n = min(kAttnChunk, T - t0);
+  const bool has_pos = split == ns - 1;
+  bf16_t* Kh = a.Kc + ((size_t)b * a.nkv + kvh) * a.max_len * SK_HD;
+  bf16_t* Vh = a.Vc + ((size_t)b * a.nkv + kvh) * a.max_len * SK_HD;
+  const float* qrow = a.qkv + (size_t)b * qs;
+
+  uint4 kr[4], vr[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int jj = 16 * i + 4 * w + gq;
+    if (jj < n && t0 + jj != pos) {
+      kr[i] = *(const uint4*)(Kh + (size_t)(t0 + jj) * SK_HD + 8 * sl);
+      vr[i] = *(const uint4*)(Vh + (size_t)(t0 + jj) * SK_HD + 8 * sl);
+    } else {
+      kr[i] = vr[i] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  // q of both heads (and, in the split holding pos, this step's k / v): per-head RMSNorm, RoPE, bf16 append
+  {
+    const float c = a.rope[(size_t)pos * SK_HD + (d & 63)], s = a.rope[(size_t)pos * SK_HD + 64 + (d & 63)];
+    const float qv = qrow[(2 * kvh + p) * SK_HD + d];
+    const float kv = has_pos ? qrow[a.nq * SK_HD + p * a.nkv * SK_HD + kvh * SK_HD + d] : 0.f;
+    const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+    if (lane == 0) { red[w] = sq; red[4 + w] = sk; }
+    __syncthreads();
+    qsh[p][d] = qv * rsqrtf((red[2 * p] + red[2 * p + 1]) / SK_HD + a.eps) * a.qn[d];
+    if (has_pos) {
+      if (p == 0) ksh[d] = kv * rsqrtf((red[4] + red[5]) / SK_HD + a.eps) * a.kn[d];
+      else vsh[d] = bf2f(f2bf(kv));
+    }
+    __syncthreads();
+    const float qr = (qsh[p][d] * c + (d < 64 ? -qsh[p][d + 64] : qsh[p][d - 64]) * s) * kInvSqrtHd;
+    float krot = 0.f;
+    if (has_pos && p == 0) krot = bf2f(f2bf(ksh[d] * c + (d < 64 ? -ksh[d + 64] : ksh[d - 64]) * s));
+    __syncthreads();
+    qsh[p][d] = qr;
+    if (has_pos) {
+      if (p == 0) { ksh[d] = krot; Kh[(size_t)pos * SK_HD + d] = f2bf(krot); }
+      else Vh[(size_t)pos * SK_HD + d] = f2bf(vsh[d]);
+    }
+    __syncthreads();
+  }
+  // scores of both heads
+  float q0[8], q1[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) { q0[e] = qsh[0][8 * sl + e]; q1[e] = qsh[1][8 * sl + e]; }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int jj = 16 * i + 4 * w + gq;
+    float k8[8];
+    if (jj < n && t0 + jj == pos) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) k8[e] = ksh[8 * sl + e];
+    } else {
+      const uint4 v = kr[i];
+      k8[0] = bf2f(v.x & 0xffffu); k8[1] = bf2f(v.x >> 16); k8[2] = bf2f(v.y & 0xffffu); k8[3] = bf2f(v.y >> 16);
+      k8[4] = bf2f(v.z & 0xffffu); k8[5] = bf2f(v.z >> 16); k8[6] = bf2f(v.w & 0xffffu); k8[7] = bf2f(v.w >> 16);
+    }
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) { s0 = __builtin_fmaf(q0[e], k8[e], s0); s1 = __builtin_fmaf(q1[e], k8[e], s1); }
+    s0 = row16_sum(s0);
+    s1 = row16_sum(s1);
+    if (sl == 0 && jj < n) { sc[0][jj] = s0; sc[1][jj] = s1; }
+  }
+  __syncthreads();
+  // softmax statistics per head (threads 0-127: head 0, 128-255: head 1)
+  const float sv = d < n ? sc[p][d] : -INFINITY;
+  const float mx = wave_max(sv);
+  if (lane == 0) red[8 + w] = mx;
+  __syncthreads();
+  const float mp = fmaxf(red[8 + 2 * p], red[8 + 2 * p + 1]);
+  const float ev = d < n ? expf(sv - mp) : 0.f;
+  const float se = wave_sum(ev);
+  if (d < n) sc[p][d] = ev;
+  if (lane == 0) red[12 + w] = se;
+  __syncthreads();
+  const float lp = red[12 + 2 * p] + red[12 + 2 * p + 1];
+  // Σ p_j v_j for both heads
+  float a0[8], a1[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) { a0[e] = 0.f; a1[e] = 0.f; }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int jj = 16 * i + 4 * w + gq;
+    if (jj < n) {
+      float v8[8];
+      if (t0 + jj == pos) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) v8[e] = vsh[8 * sl + e];
+      } else {
+        const uint4 v = vr[i];
+        v8[0] = bf2f(v.x & 0xffffu); v8[1] = bf2f(v.x >> 16); v8[2] = bf2f(v.y & 0xffffu); v8[3] = bf2f(v.y >> 16);
+        v8[4] = bf2f(v.z & 0xffffu); v8[5] = bf2f(v.z >> 16); v8[6] = bf2f(v.w & 0xffffu); v8[7] = bf2f(v.w >> 16);
+      }
+      const float e0 = sc[0][jj], e1 = sc[1][jj];
+#pragma unroll
+      for (int e = 0; e < 8; e++) { a0[e] = __builtin_fmaf(e0, v8[e], a0[e]); a1[e] = __builtin_fmaf(e1, v8[e], a1[e]); }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) { opart[w][gq][sl][e] = a0[e]; opart[w][gq][sl][8 + e] = a1[e]; }
+  __syncthreads();
+  float op = 0.f;
+#pragma unroll
+  for (int ww = 0; ww < 4; ww++)
+#pragma unroll
+    for (int gg = 0; gg < 4; gg++) op += opart[ww][gg][d >> 3][p * 8 + (d & 7)];
+
+  // publish the partial (device-coherent stores) and count the arrival
+  const uint32_t pofs = (uint32_t)(((bg * 2 + p) * kAttnSplitMax + split) * kPart) * 4;
+  if (d == 0) { buf_stf(a.part, pofs, mp); buf_stf(a.part, pofs + 4, lp); }
+  buf_stf(a.part, pofs + 8 + 4 * d, op);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(&a.counters[bg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == (unsigned)(ns - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  // merge in split order
+  if (t < 2 * ns) {
+    const int pp = t / ns, cc = t % ns;
+    const uint32_t of = (uint32_t)(((bg * 2 + pp) * kAttnSplitMax + cc) * kPart) * 4;
+    mls[pp][cc][0] = buf_ldf(a.part, of);
+    mls[pp][cc][1] = buf_ldf(a.part, of + 4);
+  }
+  __syncthreads();
+  float M = -INFINITY;
+  for (int cc = 0; cc < ns; cc++) M = fmaxf(M, mls[p][cc][0]);
+  float L = 0.f, O = 0.f;
+  for (int c0 = 0; c0 < ns; c0 += 16) {
+    float oc[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+      oc[k] = c0 + k < ns ? buf_ldf(a.part, (uint32_t)(((bg * 2 + p) * kAttnSplitMax + c0 + k) * kPart) * 4 + 8 + 4 * d)
+                          : 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (c0 + k < ns && mls[p][c0 + k][0] != -INFINITY) {
+        const float f = expf(mls[p][c0 + k][0] - M);
+        L = __builtin_fmaf(f, mls[p][c0 + k][1], L);
+        O = __builtin_fmaf(f, oc[k], O);
+      }
+    }
+  }
+  store_terms(a.att, ap, (size_t)b * a.nq * SK_HD + (2 * kvh + p) * SK_HD + d, L > 0.f ? O / L : 0.f);
+  if (t == 0) __hip_atomic_store(&a.counters[bg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- greedy pick + embedding of the next input ---------------------------------------------------------------
+// Block b: argmax of logits row b (largest value, lowest index on ties, NaN never wins; qwen3/sampler.py:114-149)
+// when pick != 0, else the stored id; then h[b] = emb[id] (bf16 -> fp32), the input planes of bf16(h ⊙ nw0) and
+// the row's sum of squares (one partial) for the first layer's RMSNorm.
+struct PickArgs {
+  const float* logits;  // [16][V]
+  int V, H, pick, max_frames;
+  int64_t* ids;         // [batch]
+  int64_t* pos;         // [batch]
+  int64_t* codes;       // [max_frames][16]
+  int64_t* nstep;       // [batch]
+  const bf16_t* emb;    // [V][H]
+  const float* nw0;     // [H]
+  float* h;             // [16][H]
+  bf16_t* xa;           // planes [kTerms][16][H]
+  float* ssa;           // [1][16]
+  int* err;
+};
+
+__global__ __launch_bounds__(kThreads) void k_bpick(PickArgs a) {
+  __shared__ float bv[kThreads];
+  __shared__ int bi[kThreads];
+  __shared__ float red[kThreads / SK_WAVE];
+  __shared__ int id_s;
+  const int b = blockIdx.x, t = threadIdx.x;
+  if (a.pick) {
+    const float* lg = a.logits + (size_t)b * a.V;
+    float best = 0.f;
+    int bidx = -1;
+    for (int k = t; k < a.V; k += kThreads) {
+      const float v = lg[k];
+      if (v == v && (bidx < 0 || v > best)) { best = v; bidx = k; }
+    }
+    bv[t] = best;
+    bi[t] = bidx;
+    __syncthreads();
+    for (int s = kThreads / 2; s > 0; s >>= 1) {
+      if (t < s) {
+        const int j2 = bi[t + s];
+        if (j2 >= 0 && (bi[t] < 0 || bv[t + s] > bv[t] || (bv[t + s] == bv[t] && j2 < bi[t]))) {
+          bv[t] = bv[t + s];
+          bi[t] = j2;
+        }
+      }
+      __syncthreads();
+    }
+    if (t == 0) {
+      const int id = bi[0] < 0 ? 0 : bi[0];
+      id_s = id;
+      a.ids[b] = id;
+      const int64_t f = a.nstep[b];
+      if (f >= 0 && f < a.max_frames) a.codes[f * kM + b] = id;
+      else atomicCAS(a.err, 0, 6);
+      a.nstep[b] = f + 1;
+      a.pos[b] = a.pos[b] + 1;
+    }
+  } else if (t == 0) {
+    int64_t id = a.ids[b];
+    if (id < 0 || id >= a.V) { atomicCAS(a.err, 0, 5); id = 0; }
+    id_s = (int)id;
+  }
+  __syncthreads();
+  const int id = id_s;
+  const bf16_t* row = a.emb + (size_t)id * a.H;
+  float ss = 0.f;
+  for (int k = t; k < a.H; k += kThreads) {
+    const float v = bf2f(row[k]);
+    a.h[(size_t)b * a.H + k] = v;
+    store_terms(a.xa, (size_t)kM * a.H, (size_t)b * a.H + k, v * a.nw0[k]);
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if ((t & 63) == 0) red[t >> 6] = ss;
+  __syncthreads();
+  if (t == 0) a.ssa[b] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// ---- dispatch ------------------------------------------------------------------------------------------------
+template <int OUT, int R, int CW>
+hipError_t launch_one(const GemmArgs& p, hipStream_t st) {
+  if constexpr (R * CW > 32) {  // more weight registers than a wave holds: never chosen by rgroups
+    return hipErrorInvalidValue;
+  } else {
+    hipLaunchKernelGGL((k_bgemm<OUT, R, CW>), dim3(p.N / (16 * R)), dim3(kThreads), 0, st, p);
+    return hipGetLastError();
+  }
+}
+template <int OUT, int R>
+hipError_t launch_cw(const GemmArgs& p, hipStream_t st) {
+  switch (p.K / 256) {
+    case 2: return launch_one<OUT, R, 2>(p, st);
+    case 4: return launch_one<OUT, R, 4>(p, st);
+    case 8: return launch_one<OUT, R, 8>(p, st);
+    case 12: return launch_one<OUT, R, 12>(p, st);
+    case 16: return launch_one<OUT, R, 16>(p, st);
+    case 24: return launch_one<OUT, R, 24>(p, st);
+  }
+  return hipErrorInvalidValue;
+}
+bool k_supported(int K) { return K == 512 || K == 1024 || K == 2048 || K == 3072 || K == 4096 || K == 6144; }
+
+// rows per workgroup: enough workgroups to spread the weight stream (at least 128), as many rows as that allows
+int rgroups(int N, int K, int mode) {
+  if (mode == kOutAcc) return 1;
+  if (K <= 2048 && N % 64 == 0 && N / 64 >= 128) return 4;
+  if (K <= 4096 && N % 32 == 0 && N / 32 >= 128) return 2;
+  return 1;
+}
+
+hipError_t launch_gemm(const GemmArgs& p, int mode, hipStream_t st) {
+  const int R = rgroups(p.N, p.K, mode);
+  if (mode == kOutF32) return R == 4 ? launch_cw<kOutF32, 4>(p, st) : R == 2 ? launch_cw<kOutF32, 2>(p, st) : launch_cw<kOutF32, 1>(p, st);
+  if (mode == kOutSwiglu)
+    return R == 4 ? launch_cw<kOutSwiglu, 4>(p, st) : R == 2 ? launch_cw<kOutSwiglu, 2>(p, st) : launch_cw<kOutSwiglu, 1>(p, st);
+  return launch_cw<kOutAcc, 1>(p, st);
+}
+
+int check_gemm(const GemmArgs& p, int mode) {
+  if (!p.x || !p.w || !p.s || (!p.out && mode != kOutSwiglu)) return SK_EINVAL;
+  if (p.N <= 0 || p.N % 16 || !k_supported(p.K)) return SK_EINVAL;
+  if (p.ssp && p.np < 1) return SK_EINVAL;
+  if (mode == kOutSwiglu && (!p.act || p.N % 32)) return SK_EINVAL;
+  if (mode == kOutAcc && (!p.xn || !p.nw || !p.ssp_out)) return SK_EINVAL;
+  if (mode < 0 || mode > kOutAcc) return SK_EINVAL;
+  if (!SK_ALIGNED16(p.x) || !SK_ALIGNED16(p.w)) return SK_EINVAL;
+  return SK_OK;
+}
+
+// workspace layout
+struct Ws {
+  int64_t err, h, xa, xb, ssa, ssb, qkv, att, act, logits, part, counters, total;
+};
+int64_t up256(int64_t v) { return (v + 255) / 256 * 256; }
+Ws ws_layout(int H, int I, int nq, int nkv, int V) {
+  Ws w;
+  int64_t o = 0;
+  auto take = [&](int64_t bytes) { const int64_t at = o; o += up256(bytes); return at; };
+  w.err = take(256);
+  w.h = take((int64_t)kM * H * 4);
+  w.xa = take((int64_t)kTerms * kM * H * 2);
+  w.xb = take((int64_t)kTerms * kM * H * 2);
+  w.ssa = take((int64_t)(H / 16) * kM * 4);
+  w.ssb = take((int64_t)(H / 16) * kM * 4);
+  w.qkv = take((int64_t)kM * (nq + 2 * nkv) * SK_HD * 4);
+  w.att = take((int64_t)kTerms * kM * nq * SK_HD * 2);
+  w.act = take((int64_t)kTerms * kM * I * 2);
+  w.logits = take((int64_t)kM * V * 4);
+  w.part = take((int64_t)kM * nkv * 2 * kAttnSplitMax * kPart * 4);
+  w.counters = take((int64_t)kM * nkv * 4);
+  w.total = o;
+  return w;
+}
+
+}  // namespace
+
+extern "C" int sk_tile_weights(const void* w, void* tiled, int N, int K, void* stream) {
+  if (!w || !tiled || N <= 0 || K <= 0 || N % 16 || K % 64) return sk_set_error(SK_EINVAL, "sk_tile_weights: bad arguments");
+  if (!SK_ALIGNED16(w) || !SK_ALIGNED16(tiled)) return sk_set_error(SK_EINVAL, "sk_tile_weights: pointers must be 16-byte aligned");
+  const size_t slots = (size_t)N * K / 16;
+  hipLaunchKernelGGL(k_tile, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const int8_t*)w, (int8_t*)tiled, N, K);
+  return sk_check_launch(hipGetLastError(), "sk_tile_weights");
+}
+
+extern "C" int sk_bgemm(const void* x, const float* ssp, int np, float eps, const void* w_tiled, const uint16_t* s, int N,
+                        int K, int mode, float* out, void* act, void* xn, const float* nw, float* ssp_out, void* stream) {
+  GemmArgs p{(const bf16_t*)x, ssp, np, eps, (const uint8_t*)w_tiled, s, N, K, out, (bf16_t*)act, (bf16_t*)xn, nw, ssp_out};
+  if (check_gemm(p, mode)) return sk_set_error(SK_EINVAL, "sk_bgemm: bad shape, mode or pointer");
+  return sk_check_launch(launch_gemm(p, mode, (hipStream_t)stream), "sk_bgemm");
+}
+
+extern "C" int sk_batch_terms(void) { return kTerms; }
+
+extern "C" int64_t sk_batch_workspace_size(int hidden, int inter, int nq, int nkv, int vocab) {
+  if (hidden <= 0 || inter <= 0 || nq <= 0 || nkv <= 0 || vocab <= 0) return 0;
+  return ws_layout(hidden, inter, nq, nkv, vocab).total;
+}
+
+namespace {
+int check_batch(const sk_batch_desc* d) {
+  if (!d) return sk_set_error(SK_EINVAL, "sk_batch: null descriptor");
+  const int H = d->hidden, I = d->inter;
+  if (d->batch < 1 || d->batch > kM) return sk_set_error(SK_EINVAL, "sk_batch: batch must be 1..16");
+  if (d->nkv <= 0 || d->nq != 2 * d->nkv) return sk_set_error(SK_EINVAL, "sk_batch: needs nq == 2 nkv (head_dim 128)");
+  if (!k_supported(H) || !k_supported(I) || !k_supported(d->nq * SK_HD) || H % 16)
+    return sk_set_error(SK_EINVAL, "sk_batch: hidden / inter / nq*128 must be 512, 1024, 2048, 3072, 4096 or 6144");
+  if (d->vocab <= 0 || d->vocab % 16) return sk_set_error(SK_EINVAL, "sk_batch: vocab must be a positive multiple of 16");
+  if (d->max_len <= 0 || d->max_len > kAttnChunk * kAttnSplitMax) return sk_set_error(SK_EINVAL, "sk_batch: max_len must be 1..4096");
+  if (d->n_layers <= 0 || !d->layers || !d->norm || !d->head_w || !d->head_s || !d->emb || !d->rope || !d->ids || !d->pos ||
+      !d->codes || !d->nstep || d->max_frames <= 0 || !d->workspace)
+    return sk_set_error(SK_EINVAL, "sk_batch: null pointer or bad count");
+  if (!SK_ALIGNED16(d->workspace)) return sk_set_error(SK_EINVAL, "sk_batch: workspace must be 16-byte aligned");
+  if (d->workspace_bytes < sk_batch_workspace_size(H, I, d->nq, d->nkv, d->vocab))
+    return sk_set_error(SK_EWORKSPACE, "sk_batch: workspace too small");
+  for (int l = 0; l < d->n_layers; l++) {
+    const sk_layer_desc& L = d->layers[l];
+    if (!L.qkv_w || !L.qkv_s || !L.o_w || !L.o_s || !L.gu_w || !L.gu_s || !L.down_w || !L.down_s || !L.in_norm ||
+        !L.post_norm || !L.qn || !L.kn || !L.kc || !L.vc)
+      return sk_set_error(SK_EINVAL, "sk_batch: null pointer in a layer descriptor");
+    if (!SK_ALIGNED16(L.kc) || !SK_ALIGNED16(L.vc)) return sk_set_error(SK_EINVAL, "sk_batch: caches must be 16-byte aligned");
+  }
+  return SK_OK;
+}
+
+hipError_t embed_launch(const sk_batch_desc* d, int pick, hipStream_t st) {
+  char* ws = (char*)d->workspace;
+  const Ws w = ws_layout(d->hidden, d->inter, d->nq, d->nkv, d->vocab);
+  PickArgs a{(const float*)(ws + w.logits), d->vocab, d->hidden, pick, d->max_frames, d->ids, d->pos, d->codes, d->nstep,
+             (const bf16_t*)d->emb, d->layers[0].in_norm, (float*)(ws + w.h), (bf16_t*)(ws + w.xa), (float*)(ws + w.ssa),
+             (int*)(ws + w.err)};
+  hipLaunchKernelGGL(k_bpick, dim3(d->batch), dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+}  // namespace
+
+extern "C" int64_t sk_batch_attn_workspace_size(int nkv) {
+  if (nkv <= 0) return 0;
+  return up256(256) + up256((int64_t)kM * nkv * 2 * kAttnSplitMax * kPart * 4) + up256((int64_t)kM * nkv * 4);
+}
+
+extern "C" int sk_batch_attn(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc,
+                             void* Vc, const int64_t* pos, int batch, int max_len, int nq, int nkv, void* att,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!qkv || !qn || !kn || !rope || !Kc || !Vc || !pos || !att || !workspace)
+    return sk_set_error(SK_EINVAL, "sk_batch_attn: null pointer");
+  if (batch < 1 || batch > kM || nkv <= 0 || nq != 2 * nkv || max_len <= 0 || max_len > kAttnChunk * kAttnSplitMax)
+    return sk_set_error(SK_EINVAL, "sk_batch_attn: needs batch 1..16, nq == 2 nkv, max_len 1..4096");
+  if (!SK_ALIGNED16(Kc) || !SK_ALIGNED16(Vc) || !SK_ALIGNED16(workspace))
+    return sk_set_error(SK_EINVAL, "sk_batch_attn: caches and workspace must be 16-byte aligned");
+  if (workspace_bytes < sk_batch_attn_workspace_size(nkv)) return sk_set_error(SK_EWORKSPACE, "sk_batch_attn: workspace too small");
+  char* ws = (char*)workspace;
+  const int64_t part = up256(256), ctr = part + up256((int64_t)kM * nkv * 2 * kAttnSplitMax * kPart * 4);
+  AttnArgs at{qkv, qn, kn, eps, rope, (bf16_t*)Kc, (bf16_t*)Vc, pos, max_len, nq, nkv, (bf16_t*)att,
+              (float*)(ws + part), (unsigned*)(ws + ctr), (int*)ws};
+  hipLaunchKernelGGL(k_battn, dim3(batch * nkv, (max_len + kAttnChunk - 1) / kAttnChunk), dim3(kThreads), 0,
+                     (hipStream_t)stream, at);
+  return sk_check_launch(hipGetLastError(), "sk_batch_attn");
+}
+
+extern "C" int sk_batch_embed(const sk_batch_desc* d, void* stream) {
+  int rc = check_batch(d);
+  if (rc) return rc;
+  return sk_check_launch(embed_launch(d, 0, (hipStream_t)stream), "sk_batch_embed");
+}
+
+extern "C" int sk_batch_frame(const sk_batch_desc* d, void* stream) {
+  int rc = check_batch(d);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)d->workspace;
+  const int H = d->hidden, I = d->inter, nq = d->nq, nkv = d->nkv, V = d->vocab;
+  const Ws w = ws_layout(H, I, nq, nkv, V);
+  float* h = (float*)(ws + w.h);
+  bf16_t* xa = (bf16_t*)(ws + w.xa);
+  bf16_t* xb = (bf16_t*)(ws + w.xb);
+  float* ssa = (float*)(ws + w.ssa);
+  float* ssb = (float*)(ws + w.ssb);
+  float* qkv = (float*)(ws + w.qkv);
+  bf16_t* att = (bf16_t*)(ws + w.att);
+  bf16_t* act = (bf16_t*)(ws + w.act);
+  float* logits = (float*)(ws + w.logits);
+  const int nqkv = (nq + 2 * nkv) * SK_HD;
+  hipError_t e = hipSuccess;
+  for (int l = 0; l < d->n_layers && e == hipSuccess; l++) {
+    const sk_layer_desc& L = d->layers[l];
+    const int np_a = l == 0 ? 1 : H / 16;
+    GemmArgs g1{xa, ssa, np_a, d->eps, (const uint8_t*)L.qkv_w, L.qkv_s, nqkv, H, qkv, nullptr, nullptr, nullptr, nullptr};
+    e = launch_gemm(g1, kOutF32, st);
+    if (e != hipSuccess) break;
+    AttnArgs at{qkv, L.qn, L.kn, d->eps, d->rope, (bf16_t*)L.kc, (bf16_t*)L.vc, d->pos, d->max_len, nq, nkv, att,
+                (float*)(ws + w.part), (unsigned*)(ws + w.counters), (int*)(ws + w.err)};
+    hipLaunchKernelGGL(k_battn, dim3(d->batch * nkv, (d->max_len + kAttnChunk - 1) / kAttnChunk), dim3(kThreads), 0, st, at);
+    e = hipGetLastError();
+    if (e != hipSuccess) break;
+    GemmArgs g2{att, nullptr, 0, d->eps, (const uint8_t*)L.o_w, L.o_s, H, nq * SK_HD, h, nullptr, xb, L.post_norm, ssb};
+    e = launch_gemm(g2, kOutAcc, st);
+    if (e != hipSuccess) break;
+    GemmArgs g3{xb, ssb, H / 16, d->eps, (const uint8_t*)L.gu_w, L.gu_s, 2 * I, H, nullptr, act, nullptr, nullptr, nullptr};
+    e = launch_gemm(g3, kOutSwiglu, st);
+    if (e != hipSuccess) break;
+    const float* nw_next = l + 1 < d->n_layers ? d->layers[l + 1].in_norm : d->norm;
+    GemmArgs g4{act, nullptr, 0, d->eps, (const uint8_t*)L.down_w, L.down_s, H, I, h, nullptr, xa, nw_next, ssa};
+    e = launch_gemm(g4, kOutAcc, st);
+    if (e != hipSuccess) break;
+    if (d->layer_out)
+      e = hipMemcpyAsync(d->layer_out + (size_t)l * kM * H, h, (size_t)kM * H * 4, hipMemcpyDeviceToDevice, st);
+  }
+  if (e == hipSuccess) {
+    GemmArgs gh{xa, ssa, H / 16, d->eps, (const uint8_t*)d->head_w, d->head_s, V, H, logits, nullptr, nullptr, nullptr, nullptr};
+    e = launch_gemm(gh, kOutF32, st);
+  }
+  if (e == hipSuccess && d->logits) e = hipMemcpyAsync(d->logits, logits, (size_t)kM * V * 4, hipMemcpyDeviceToDevice, st);
+  if (e == hipSuccess) e = embed_launch(d, 1, st);
+  return sk_check_launch(e, "sk_batch_frame");
+}

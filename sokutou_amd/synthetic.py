@@ -23,7 +23,8 @@ import numpy as np
 import torch
 
 _TAGS = {"q": 1, "k": 2, "v": 3, "o": 4, "gate": 5, "up": 6, "down": 7, "in_norm": 8, "post_norm": 9, "q_norm": 10,
-         "k_norm": 11, "norm": 12, "head": 13, "emb": 14, "kcache": 15, "vcache": 16, "h": 17, "token": 18}
+         "k_norm": 11, "norm": 12, "head": 13, "emb": 14, "kcache": 15, "vcache": 16, "h": 17, "token": 18,
+         "kvlen": 19}
 
 
 @dataclass(frozen=True)
@@ -231,12 +232,75 @@ WORKLOADS = {
     # code predictor: 5 layers of the 0.6B shape, 2048-way heads, 16 positions (KV 1 -> 16) per frame, greedy
     # sub-codes; a step is `frames` code-predictor frames with different (x0, code 0)
     "cp06b": dict(shape="0.6b", n_layers=5, vocab=2048, kv=0, positions=16, frames=8),
+    # 16 concurrent 1.7B-shaped streams, prior KV lengths uniform in [64, 2048], 32 greedy frames
+    "batch17b": dict(shape="1.7b", n_layers=28, kv=0, batch=16, kv_lo=64, kv_hi=2048, frames=32),
+    # the same with two layers and five streams, for quick checks
+    "batchsmall": dict(shape="1.7b", n_layers=2, kv=0, batch=5, kv_lo=8, kv_hi=200, frames=6),
 }
 
 
 def workload_shape(name: str) -> TalkerShape:
     w = WORKLOADS[name]
     return shape(w["shape"], n_layers=w["n_layers"], **({"vocab": w["vocab"]} if "vocab" in w else {}))
+
+
+# ---------------------------------------------------------------------------------------------------------
+# batched streams
+# ---------------------------------------------------------------------------------------------------------
+def batch_lengths(seed: int, name: str) -> list[int]:
+    """Prior KV length of every stream of a batched workload, uniform in [kv_lo, kv_hi]."""
+    w = WORKLOADS[name]
+    return [int(t) for t in _rng(seed, 0, "kvlen").integers(w["kv_lo"], w["kv_hi"] + 1, w["batch"])]
+
+
+def batch_tokens(seed: int, name: str) -> list[int]:
+    """First input token of every stream of a batched workload."""
+    w = WORKLOADS[name]
+    return [int(t) for t in _rng(seed, 1, "token").integers(0, workload_shape(name).vocab, w["batch"])]
+
+
+def batch_prefill(seed: int, i: int, b: int, s: TalkerShape, T: int) -> tuple[np.ndarray, np.ndarray]:
+    """Prior K/V of layer ``i`` of stream ``b``: [nkv, T, 128] N(0, 1) drawn in float32 and rounded to bf16."""
+    out = []
+    for tag in ("kcache", "vcache"):
+        g = np.random.default_rng(np.random.SeedSequence([int(seed), int(i) + 1, _TAGS[tag], 1000 + int(b)]))
+        out.append(bf16_values(g.standard_normal((s.nkv, T, s.head_dim), dtype=np.float32)))
+    return out[0], out[1]
+
+
+def batch_max_len(name: str, frames: int | None = None) -> int:
+    w = WORKLOADS[name]
+    return w["kv_hi"] + (w["frames"] if frames is None else frames) + 1
+
+
+def make_batch_engine(name: str, seed: int = 0, device="cuda", frames: int | None = None, progress=None):
+    """A BatchedTalker over the seeded synthetic talker of a batched workload, every stream's prior cache loaded
+    and the first tokens embedded. ``frames``: how many steps the cache must leave room for (default the
+    workload's); ``progress(message)`` is called after each stage. Returns (engine, lengths, tokens)."""
+    from .batch import BatchedTalker
+
+    w = WORKLOADS[name]
+    s = workload_shape(name)
+    frames = w["frames"] if frames is None else frames
+    tts = make_tts(seed, s, device=device)
+    if progress:
+        progress("weights generated")
+    eng = BatchedTalker(tts.model.talker, w["batch"], batch_max_len(name, frames), max_frames=max(frames, 1),
+                        device=device)
+    del tts
+    if progress:
+        progress("weights packed")
+    T = batch_lengths(seed, name)
+    for b in range(w["batch"]):
+        for i in range(s.n_layers):
+            k, v = batch_prefill(seed, i, b, s, T[b])
+            eng.kc[i, b, :, :T[b]].copy_(torch.from_numpy(k).to(torch.bfloat16))
+            eng.vc[i, b, :, :T[b]].copy_(torch.from_numpy(v).to(torch.bfloat16))
+        if progress:
+            progress(f"stream {b} prefilled ({T[b]} positions)")
+    tok = batch_tokens(seed, name)
+    eng.reset(T, tok)
+    return eng, T, tok
 
 
 def make_engine(name: str, seed: int = 0, wd: str = "i8row", device="cuda", graphs: bool = True,

@@ -144,12 +144,48 @@ def code_predictor(name: str = "cp06b", seed: int = 0) -> None:
     print(name, "codes[0]", codes[0], "min margin", meta["min_margin"], meta["oracle_seconds"])
 
 
+def batch(name: str = "batch17b", seed: int = 0, rows=(0, 1)) -> None:
+    """Batched ragged streams: codes of every step and stream, top-1/top-2 margins, per-layer residuals of the
+    first step for streams ``rows``, logits of every stream at the first and the last step."""
+    from oracle.workload import batch_oracle
+
+    spec = syn.WORKLOADS[name]
+    F = spec["frames"]
+    t0 = time.time()
+    orc, T, tok, s = batch_oracle(name, seed)
+    t1 = time.time()
+    pos, t = list(T), list(tok)
+    codes, margins, layer_out, first, last = [], [], [], None, None
+    for f in range(F):
+        lo = [] if f == 0 else None
+        t, lg = orc.step(t, pos, lo)
+        if f == 0:
+            layer_out = [x[list(rows)] for x in lo]
+            first = lg
+        last = lg
+        top = np.sort(lg, axis=1)[:, -2:]
+        margins.append((top[:, 1] - top[:, 0]).tolist())
+        codes.append(t)
+        pos = [p + 1 for p in pos]
+        print(f"  step {f}: {time.time() - t1:.0f} s", flush=True)
+    t2 = time.time()
+    np.savez_compressed(HERE / f"{name}_seed{seed}.npz", layer_out0=np.stack(layer_out), logits_first=first,
+                        logits_last=last)
+    meta = {"workload": name, "seed": seed, "wd": "i8row", "lengths": T, "tokens": tok, "frames": F,
+            "layer_out_streams": list(rows), "codes": codes, "margins": margins,
+            "min_margin": min(min(m) for m in margins),
+            "oracle_seconds": {"build": round(t1 - t0, 1), "frames": round(t2 - t1, 1)}}
+    (HERE / f"{name}_seed{seed}.json").write_text(json.dumps(meta, indent=1))
+    print(name, "codes[0]", codes[0], "min margin", meta["min_margin"], meta["oracle_seconds"])
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--only", default=None)
     a = ap.parse_args()
     jobs = {"layer06b": lambda: layer06b(0), "tiny": lambda: talker("tiny", 1), "talker06b": lambda: talker("talker06b", 0),
-            "talker17b": lambda: talker("talker17b", 0), "cp06b": lambda: code_predictor("cp06b", 0)}
+            "talker17b": lambda: talker("talker17b", 0), "cp06b": lambda: code_predictor("cp06b", 0),
+            "batch17b": lambda: batch("batch17b", 0)}
     for n, fn in jobs.items():
         if a.only in (None, n):
             fn()

@@ -75,3 +75,26 @@ def test_cp_frame_rejects_bad_shapes_without_launching():
     assert L.sk_cp_frame(ctypes.byref(d), None) == _lib.SK_EINVAL  # null pointers
     d.n_positions = 1
     assert L.sk_cp_frame(ctypes.byref(d), None) == _lib.SK_EUNSUPPORTED
+
+
+def test_batched_entry_points_reject_bad_shapes_without_launching():
+    import ctypes
+
+    L = _lib.load()
+    d = ctypes.c_void_p(256)
+    assert L.sk_batch_terms() in (1, 2, 3)
+    # K not a supported length, N not a multiple of 16, SwiGLU with N % 32 != 0, accumulate without its outputs
+    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 64, 1000, 0, d, None, None, None, None, None) == _lib.SK_EINVAL
+    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 40, 1024, 0, d, None, None, None, None, None) == _lib.SK_EINVAL
+    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 48, 1024, 1, None, d, None, None, None, None) == _lib.SK_EINVAL
+    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 64, 1024, 2, d, None, None, None, None, None) == _lib.SK_EINVAL
+    assert L.sk_bgemm(d, d, 0, 1e-6, d, d, 64, 1024, 0, d, None, None, None, None, None) == _lib.SK_EINVAL
+    assert L.sk_tile_weights(d, d, 40, 128, None) == _lib.SK_EINVAL
+    ws = L.sk_batch_workspace_size(2048, 6144, 16, 8, 3072)
+    assert ws > 16 * 8 * 2 * 64 * 130 * 4
+    desc = _lib.SkBatchDesc(n_layers=28, hidden=2048, inter=6144, nq=16, nkv=8, vocab=3072, batch=17, max_len=2100)
+    assert L.sk_batch_frame(ctypes.byref(desc), None) == _lib.SK_EINVAL  # batch > 16
+    desc.batch = 16
+    assert L.sk_batch_frame(ctypes.byref(desc), None) == _lib.SK_EINVAL  # null pointers
+    desc.max_len = 5000
+    assert L.sk_batch_embed(ctypes.byref(desc), None) == _lib.SK_EINVAL  # cache longer than the attention supports

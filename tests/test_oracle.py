@@ -343,3 +343,69 @@ def test_code_predictor_frame_matches_transformers_stack():
         err = np.max(np.abs(logits[g - 1] - lg)) / np.max(np.abs(lg))
         assert err < 1e-5, (g, err)
     assert codes == ref_codes
+
+
+# ---- batched streams ---------------------------------------------------------------------------------------
+def test_bf16_terms_bounds_and_exactness():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(200000) * np.exp(rng.uniform(-20, 20, 200000))).astype(F32)
+    assert np.array_equal(O.bf16_terms(x, 0), x)
+    assert np.array_equal(O.bf16_terms(x, 1), O.bf16_round(x))
+    # two terms keep 16 significant bits: |x - t0 - t1| <= 2^-17 |x| (two round-to-nearest steps of 2^-9 each)
+    e2 = np.abs(O.bf16_terms(x, 2).astype(np.float64) - x) / np.abs(x)
+    assert e2.max() <= 2.0 ** -17
+    # three terms reproduce every float32 value whose exponent leaves the last term normal
+    assert np.array_equal(O.bf16_terms(x, 3), x)
+    # brute force on a few values: the terms are bf16 values and their fp32 sum is x
+    for v in x[:50]:
+        r, ts = np.float32(v), []
+        for _ in range(3):
+            t = np.float32(torch.tensor(float(r)).to(torch.bfloat16).float().item())
+            ts.append(t)
+            r = np.float32(r - t)
+        assert np.float32(np.float32(ts[0] + ts[1]) + ts[2]) == v
+
+
+def test_batch_oracle_rows_equal_single_stream_oracle():
+    """Row b of a batched step is the M=1 talker step of stream b (same caches, same position); the head differs
+    only in applying the final norm's inverse RMS after the product, so logits agree to float rounding."""
+    s = syn.shape("tiny")
+    rng = np.random.default_rng(2)
+    layers = [syn.layer_weights(3, i, s) for i in range(s.n_layers)]
+    from oracle.workload import pack_layer
+
+    f = syn.final_weights(3, s)
+    w = {"layers": [pack_layer(L, "i8row") for L in layers], "norm": f["norm"], "head": O.quantize(f["head"], "i8row")[2],
+         "emb": f["emb"], "rope": O.rope_table(syn.inv_freq(s), 64), "eps": s.eps, "nq": s.nq, "nkv": s.nkv}
+    B, T = 3, [5, 17, 40]
+    Ks = [rng.standard_normal((s.n_layers, s.nkv, 64, 128)).astype(F32) for _ in range(B)]
+    Vs = [rng.standard_normal((s.n_layers, s.nkv, 64, 128)).astype(F32) for _ in range(B)]
+    Ks = [O.bf16_round(k) for k in Ks]
+    Vs = [O.bf16_round(v) for v in Vs]
+    tok = [7, 300, 511]
+    bo = O.BatchTalkerOracle(w, [k.copy() for k in Ks], [v.copy() for v in Vs])
+    lo = []
+    codes, lg = bo.step(tok, T, lo)
+    for b in range(B):
+        so = O.TalkerOracle(w, Ks[b].copy(), Vs[b].copy())
+        slo = []
+        c1, lg1 = so.step(tok[b], T[b], slo)
+        for i in range(s.n_layers):
+            assert np.max(np.abs(lo[i][b] - slo[i])) <= 1e-5 * np.max(np.abs(slo[i]))
+        assert np.max(np.abs(lg[b] - lg1)) <= 1e-5 * np.max(np.abs(lg1))
+        assert codes[b] == c1
+        # the step appended this stream's K/V at its own position only
+        assert np.array_equal(bo.Ks[b][:, :, T[b]], so.K[:, :, T[b]])
+        assert np.array_equal(bo.Ks[b][:, :, : T[b]], Ks[b][:, :, : T[b]])
+
+
+def test_batch_workload_inputs_are_seeded():
+    T = syn.batch_lengths(0, "batch17b")
+    assert len(T) == 16 and min(T) >= 64 and max(T) <= 2048 and T == syn.batch_lengths(0, "batch17b")
+    tok = syn.batch_tokens(0, "batch17b")
+    assert len(tok) == 16 and max(tok) < 3072
+    s = syn.workload_shape("batchsmall")
+    k1, v1 = syn.batch_prefill(0, 1, 2, s, 9)
+    k2, _ = syn.batch_prefill(0, 1, 3, s, 9)
+    assert k1.shape == (s.nkv, 9, 128) and not np.array_equal(k1, k2)
+    assert np.array_equal(O.bf16_round(k1), k1) and abs(float(v1.std()) - 1.0) < 0.05
