@@ -296,12 +296,15 @@ def run_batch(args) -> None:
     att = torch.zeros((nt, 16, nq * 128), dtype=torch.bfloat16, device=dev)
     sso = torch.zeros((H // 16, 16), **f32)
     aws = torch.zeros(int(_lib.load().sk_batch_attn_workspace_size(nkv)), dtype=torch.uint8, device=dev)
+    gws = torch.zeros(max(int(_lib.load().sk_bgemm_workspace_size(n_, k_))
+                          for n_, k_ in (((nq + 2 * nkv) * 128, H), (H, nq * 128), (2 * I, H), (H, I))),
+                      dtype=torch.uint8, device=dev)
     eng.reset(T, tok)
     torch.cuda.synchronize()
 
     def gemm(x, ss, np_, lin_w, lin_s, N, K, mode, out, a, xn_, nw, so):
         _lib.call("sk_bgemm", p(x), p(ss), np_, P.eps, p(lin_w), p(lin_s), N, K, mode, p(out), p(a), p(xn_), p(nw),
-                  p(so), _lib.stream())
+                  p(so), p(gws), gws.numel(), _lib.stream())
 
     calls = {
         "qkv": lambda: gemm(x_h, ssp, H // 16, Ly["qkv"].w, Ly["qkv"].s, (nq + 2 * nkv) * 128, H, 0, qkv, None, None,

@@ -213,15 +213,22 @@ int sk_batch_terms(void);
  * N % 16 == 0, K % 64 == 0. */
 int sk_tile_weights(const void* w, void* tiled, int N, int K, void* stream);
 
+/* Workspace bytes of sk_bgemm for an [N, K] projection (split-K partial sums and per-tile arrival counters; zero
+ * it once, every call leaves the counters zero). */
+int64_t sk_bgemm_workspace_size(int N, int K);
+
 /* One M = 16 projection. x: bf16 planes [terms][16][K]; w_tiled / s: tiled int8 weights [N, K] + bf16 row scales.
  * ssp (optional, [np][16]): partial sums of squares of the residual whose normalised copy x is; when given, row m
  * is multiplied by rsqrt(Σ_q ssp[q][m] / K + eps) after the dot product (the fused RMSNorm of rms_gemv,
  * qwen3/kernels.py:180-186, 224). mode 0: out[16][N] = result (fp32). mode 1: rows interleaved gate/up,
  * act = planes [terms][16][N/2] of silu(gate) * up. mode 2: out[16][N] += result (the residual), then xn = planes
  * [terms][16][N] of out ⊙ nw and ssp_out[N/16][16] = per 16-column partial sums of squares of out.
- * K in {512, 1024, 2048, 3072, 4096, 6144}; N % 16 == 0 (N % 32 == 0 for mode 1). */
+ * K in {512, 1024, 2048, 3072, 4096, 6144}; N % 16 == 0 (N % 32 == 0 for mode 1). Row groups of 16 outputs go
+ * to workgroups in sets of up to 4, and K is split over as many workgroups as it takes to occupy the GPU; the
+ * split sums are added in a fixed order by the last workgroup of each set, so results are deterministic. */
 int sk_bgemm(const void* x, const float* ssp, int np, float eps, const void* w_tiled, const uint16_t* s, int N, int K,
-             int mode, float* out, void* act, void* xn, const float* nw, float* ssp_out, void* stream);
+             int mode, float* out, void* act, void* xn, const float* nw, float* ssp_out, void* workspace,
+             int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes of sk_batch_attn (zeroed once; its first 4 bytes are the error word, 5 = a position out of
  * range). */

@@ -78,7 +78,8 @@ class SkBatchDesc(ctypes.Structure):
 
 _SIGS["sk_batch_terms"] = (c_int, [])
 _SIGS["sk_tile_weights"] = (c_int, [_P, _P, c_int, c_int, _P])
-_SIGS["sk_bgemm"] = (c_int, [_P, _P, c_int, c_float, _P, _P, c_int, c_int, c_int, _P, _P, _P, _P, _P, _P])
+_SIGS["sk_bgemm"] = (c_int, [_P, _P, c_int, c_float, _P, _P, c_int, c_int, c_int, _P, _P, _P, _P, _P, _P, c_int64, _P])
+_SIGS["sk_bgemm_workspace_size"] = (c_int64, [c_int, c_int])
 _SIGS["sk_batch_workspace_size"] = (c_int64, [c_int, c_int, c_int, c_int, c_int])
 _SIGS["sk_batch_attn_workspace_size"] = (c_int64, [c_int])
 _SIGS["sk_batch_attn"] = (c_int, [_P, _P, _P, c_float, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, _P, c_int64, _P])

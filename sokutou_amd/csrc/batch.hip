@@ -82,21 +82,29 @@ struct GemmArgs {
   bf16_t* xn;           // ACC: planes [kTerms][16][N] of bf16(h ⊙ nw)
   const float* nw;      // ACC: next RMSNorm weight [N]
   float* ssp_out;       // ACC: [N/16][16] partial sums of squares of the updated residual
+  int S;                // K slices (workgroups per output tile)
+  float* part;          // S > 1: [S][tiles][R][256] partial sums
+  unsigned* counters;   // S > 1: [tiles] arrivals, zero between launches
 };
 
-// One workgroup computes R 16-row groups of the output for all 16 rows; its 4 waves split K in quarters
-// (CW chunks of 64 each) and meet in LDS for a fixed-order sum. Every weight load of a wave is issued at the top
-// (the weight stream is the kernel's HBM traffic), the activation planes (L2-resident) run DA chunks ahead.
+// Workgroup (tile, slice) computes R 16-row groups of the output for all 16 rows over K slice `slice` (4 CW
+// chunks of 64); its 4 waves take CW chunks each and meet in LDS for a fixed-order sum. With S > 1 slices the
+// workgroups of a tile publish their sums (device-coherent stores) and the last to arrive adds them in slice
+// order and runs the epilogue, so the result does not depend on arrival order. Every weight load of a wave is
+// issued at the top (the weight stream is the kernel's HBM traffic); the activation planes (L2-resident) run DA
+// chunks ahead.
 template <int OUT, int R, int CW>
 __global__ __launch_bounds__(kThreads) void k_bgemm(GemmArgs p) {
   constexpr int DA = CW < 4 ? CW : 4;
   __shared__ float red[4][R][4][64];
   __shared__ float ssq[16][kM];
   __shared__ float inv_s[kM];
+  __shared__ int last_s;
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
-  const int C = 4 * CW;                  // 64-wide chunks per row
-  const int g0 = blockIdx.x * R;
-  const int c0 = wv * CW;
+  const int C = p.K / 64;                 // 64-wide chunks per row
+  const int tile = blockIdx.x, slice = blockIdx.y;
+  const int g0 = tile * R;
+  const int c0 = (slice * 4 + wv) * CW;
   const size_t plane = (size_t)kM * p.K;
   const uint4* xp = (const uint4*)(p.x + (size_t)(lane & 15) * p.K + (size_t)c0 * 64 + 16 * (lane >> 4));
   uint4 wq[CW][R], xa[DA][kTerms][2];
@@ -115,6 +123,9 @@ __global__ __launch_bounds__(kThreads) void k_bgemm(GemmArgs p) {
   };
 #pragma unroll
   for (int c = 0; c < DA; c++) load_a(c, c);
+  float ssv = 0.f;  // this thread's share of the RMSNorm partial sums (used by the epilogue workgroup)
+  if (p.ssp)
+    for (int q = tid >> 4; q < p.np; q += 16) ssv += gload(p.ssp + q * kM + (tid & 15));
   __builtin_amdgcn_sched_barrier(0);
   f32x4 acc[R], acc2[R];  // first term, later terms (kept apart: the small terms accumulate at their own scale)
 #pragma unroll
@@ -141,12 +152,33 @@ __global__ __launch_bounds__(kThreads) void k_bgemm(GemmArgs p) {
   for (int r = 0; r < R; r++)
 #pragma unroll
     for (int i = 0; i < 4; i++) red[wv][r][i][lane] = acc[r][i] + acc2[r][i];
-  if (p.ssp) {
-    float v = 0.f;
-    for (int q = tid >> 4; q < p.np; q += 16) v += gload(p.ssp + q * kM + (tid & 15));
-    ssq[tid >> 4][tid & 15] = v;
-  }
+  if (p.ssp) ssq[tid >> 4][tid & 15] = ssv;
   __syncthreads();
+  const int i = tid >> 6, L = tid & 63;
+  float v[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) v[r] = (red[0][r][i][L] + red[1][r][i][L]) + (red[2][r][i][L] + red[3][r][i][L]);
+  if (p.S > 1) {
+    const uint32_t base = (uint32_t)(((size_t)slice * gridDim.x + tile) * R) * 256;
+#pragma unroll
+    for (int r = 0; r < R; r++) buf_stf(p.part, (base + r * 256 + tid) * 4, v[r]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_s = prev == (unsigned)(p.S - 1);
+    }
+    __syncthreads();
+    if (!last_s) return;
+#pragma unroll
+    for (int r = 0; r < R; r++) v[r] = 0.f;
+    for (int q = 0; q < p.S; q++) {
+      const uint32_t b2 = (uint32_t)(((size_t)q * gridDim.x + tile) * R) * 256;
+#pragma unroll
+      for (int r = 0; r < R; r++) v[r] += buf_ldf(p.part, (b2 + r * 256 + tid) * 4);
+    }
+    if (tid == 0) __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   if (p.ssp && tid < kM) {
     float s = 0.f;
 #pragma unroll
@@ -154,15 +186,12 @@ __global__ __launch_bounds__(kThreads) void k_bgemm(GemmArgs p) {
     inv_s[tid] = rsqrtf(s / p.K + p.eps);
   }
   __syncthreads();
-  const int i = tid >> 6, L = tid & 63;
   const int m = 4 * (L >> 4) + i, nl = L & 15;
   const float iv = p.ssp ? inv_s[m] : 1.f;
-  float ss = 0.f;
 #pragma unroll
   for (int r = 0; r < R; r++) {
-    const float v = (red[0][r][i][L] + red[1][r][i][L]) + (red[2][r][i][L] + red[3][r][i][L]);
     const int n = (g0 + r) * 16 + nl;
-    const float y = v * bf2f(p.s[n]) * iv;
+    const float y = v[r] * bf2f(p.s[n]) * iv;
     if constexpr (OUT == kOutF32) {
       p.out[(size_t)m * p.N + n] = y;
     } else if constexpr (OUT == kOutSwiglu) {
@@ -173,12 +202,9 @@ __global__ __launch_bounds__(kThreads) void k_bgemm(GemmArgs p) {
       const float hn = *hp + y;
       *hp = hn;
       store_terms(p.xn, (size_t)kM * p.N, (size_t)m * p.N + n, hn * p.nw[n]);
-      ss = __builtin_fmaf(hn, hn, ss);
+      const float ss = row16_sum(hn * hn);
+      if (nl == 0) p.ssp_out[(g0 + r) * kM + m] = ss;
     }
-  }
-  if constexpr (OUT == kOutAcc) {
-    ss = row16_sum(ss);
-    if (nl == 0) p.ssp_out[blockIdx.x * kM + m] = ss;
   }
 }
 
@@ -476,41 +502,57 @@ __global__ __launch_bounds__(kThreads) void k_bpick(PickArgs a) {
 // ---- dispatch ------------------------------------------------------------------------------------------------
 template <int OUT, int R, int CW>
 hipError_t launch_one(const GemmArgs& p, hipStream_t st) {
-  if constexpr (R * CW > 32) {  // more weight registers than a wave holds: never chosen by rgroups
+  if constexpr (R * CW > 32) {  // more weight registers than a wave holds: never planned
     return hipErrorInvalidValue;
   } else {
-    hipLaunchKernelGGL((k_bgemm<OUT, R, CW>), dim3(p.N / (16 * R)), dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((k_bgemm<OUT, R, CW>), dim3(p.N / (16 * R), p.S), dim3(kThreads), 0, st, p);
     return hipGetLastError();
   }
 }
 template <int OUT, int R>
 hipError_t launch_cw(const GemmArgs& p, hipStream_t st) {
-  switch (p.K / 256) {
+  switch (p.K / (256 * p.S)) {
+    case 1: return launch_one<OUT, R, 1>(p, st);
     case 2: return launch_one<OUT, R, 2>(p, st);
+    case 3: return launch_one<OUT, R, 3>(p, st);
     case 4: return launch_one<OUT, R, 4>(p, st);
+    case 6: return launch_one<OUT, R, 6>(p, st);
     case 8: return launch_one<OUT, R, 8>(p, st);
-    case 12: return launch_one<OUT, R, 12>(p, st);
-    case 16: return launch_one<OUT, R, 16>(p, st);
-    case 24: return launch_one<OUT, R, 24>(p, st);
   }
   return hipErrorInvalidValue;
 }
 bool k_supported(int K) { return K == 512 || K == 1024 || K == 2048 || K == 3072 || K == 4096 || K == 6144; }
 
-// rows per workgroup: enough workgroups to spread the weight stream (at least 128), as many rows as that allows
-int rgroups(int N, int K, int mode) {
-  if (mode == kOutAcc) return 1;
-  if (K <= 2048 && N % 64 == 0 && N / 64 >= 128) return 4;
-  if (K <= 4096 && N % 32 == 0 && N / 32 >= 128) return 2;
-  return 1;
+// Launch plan: R 16-row groups per workgroup (as many as the row count allows, for reuse of the activation
+// loads) and the fewest K slices S that give at least kMinWg workgroups, each wave keeping at most 8 chunks.
+constexpr int kMinWg = 192;
+struct Plan { int R, S; };
+Plan plan(int N, int K) {
+  Plan pl{N % 64 == 0 ? 4 : N % 32 == 0 ? 2 : 1, 1};
+  const int tiles = N / (16 * pl.R);
+  auto cw_ok = [&](int S) {
+    if (K % (256 * S)) return false;
+    const int cw = K / (256 * S);
+    return (cw == 1 || cw == 2 || cw == 3 || cw == 4 || cw == 6 || cw == 8) && pl.R * cw <= 32;
+  };
+  auto splittable = [&](int S) { return K % (256 * S) == 0; };
+  while (pl.S < 64 && (!cw_ok(pl.S) || (tiles * pl.S < kMinWg && splittable(pl.S * 2) && cw_ok(pl.S * 2)))) pl.S *= 2;
+  return pl;
+}
+int64_t part_floats(int N, int K) {
+  const Plan pl = plan(N, K);
+  return pl.S > 1 ? (int64_t)pl.S * (N / 16) * 256 : 0;
 }
 
-hipError_t launch_gemm(const GemmArgs& p, int mode, hipStream_t st) {
-  const int R = rgroups(p.N, p.K, mode);
-  if (mode == kOutF32) return R == 4 ? launch_cw<kOutF32, 4>(p, st) : R == 2 ? launch_cw<kOutF32, 2>(p, st) : launch_cw<kOutF32, 1>(p, st);
+hipError_t launch_gemm(GemmArgs p, int mode, hipStream_t st) {
+  const Plan pl = plan(p.N, p.K);
+  p.S = pl.S;
+  if (mode == kOutF32)
+    return pl.R == 4 ? launch_cw<kOutF32, 4>(p, st) : pl.R == 2 ? launch_cw<kOutF32, 2>(p, st) : launch_cw<kOutF32, 1>(p, st);
   if (mode == kOutSwiglu)
-    return R == 4 ? launch_cw<kOutSwiglu, 4>(p, st) : R == 2 ? launch_cw<kOutSwiglu, 2>(p, st) : launch_cw<kOutSwiglu, 1>(p, st);
-  return launch_cw<kOutAcc, 1>(p, st);
+    return pl.R == 4 ? launch_cw<kOutSwiglu, 4>(p, st) : pl.R == 2 ? launch_cw<kOutSwiglu, 2>(p, st)
+                                                               : launch_cw<kOutSwiglu, 1>(p, st);
+  return pl.R == 4 ? launch_cw<kOutAcc, 4>(p, st) : pl.R == 2 ? launch_cw<kOutAcc, 2>(p, st) : launch_cw<kOutAcc, 1>(p, st);
 }
 
 int check_gemm(const GemmArgs& p, int mode) {
@@ -526,7 +568,7 @@ int check_gemm(const GemmArgs& p, int mode) {
 
 // workspace layout
 struct Ws {
-  int64_t err, h, xa, xb, ssa, ssb, qkv, att, act, logits, part, counters, total;
+  int64_t err, h, xa, xb, ssa, ssb, qkv, att, act, logits, part, counters, gpart, gctr, total;
 };
 int64_t up256(int64_t v) { return (v + 255) / 256 * 256; }
 Ws ws_layout(int H, int I, int nq, int nkv, int V) {
@@ -545,6 +587,15 @@ Ws ws_layout(int H, int I, int nq, int nkv, int V) {
   w.logits = take((int64_t)kM * V * 4);
   w.part = take((int64_t)kM * nkv * 2 * kAttnSplitMax * kPart * 4);
   w.counters = take((int64_t)kM * nkv * 4);
+  const int nqkv = (nq + 2 * nkv) * SK_HD;
+  int64_t pf = 0, nmax = 0;
+  const int shapes[5][2] = {{nqkv, H}, {H, nq * SK_HD}, {2 * I, H}, {H, I}, {V, H}};
+  for (const auto& sh : shapes) {
+    pf = pf > part_floats(sh[0], sh[1]) ? pf : part_floats(sh[0], sh[1]);
+    nmax = nmax > sh[0] ? nmax : sh[0];
+  }
+  w.gpart = take(pf * 4);
+  w.gctr = take(nmax / 16 * 4);
   w.total = o;
   return w;
 }
@@ -560,10 +611,21 @@ extern "C" int sk_tile_weights(const void* w, void* tiled, int N, int K, void* s
   return sk_check_launch(hipGetLastError(), "sk_tile_weights");
 }
 
+extern "C" int64_t sk_bgemm_workspace_size(int N, int K) {
+  if (N <= 0 || N % 16 || !k_supported(K)) return 0;
+  return up256(part_floats(N, K) * 4) + up256((int64_t)N / 16 * 4);
+}
+
 extern "C" int sk_bgemm(const void* x, const float* ssp, int np, float eps, const void* w_tiled, const uint16_t* s, int N,
-                        int K, int mode, float* out, void* act, void* xn, const float* nw, float* ssp_out, void* stream) {
-  GemmArgs p{(const bf16_t*)x, ssp, np, eps, (const uint8_t*)w_tiled, s, N, K, out, (bf16_t*)act, (bf16_t*)xn, nw, ssp_out};
+                        int K, int mode, float* out, void* act, void* xn, const float* nw, float* ssp_out,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
+  GemmArgs p{(const bf16_t*)x, ssp, np, eps, (const uint8_t*)w_tiled, s, N, K, out, (bf16_t*)act, (bf16_t*)xn, nw, ssp_out,
+             1, nullptr, nullptr};
   if (check_gemm(p, mode)) return sk_set_error(SK_EINVAL, "sk_bgemm: bad shape, mode or pointer");
+  if (!workspace || !SK_ALIGNED16(workspace)) return sk_set_error(SK_EINVAL, "sk_bgemm: workspace must be 16-byte aligned");
+  if (workspace_bytes < sk_bgemm_workspace_size(N, K)) return sk_set_error(SK_EWORKSPACE, "sk_bgemm: workspace too small");
+  p.part = (float*)workspace;
+  p.counters = (unsigned*)((char*)workspace + up256(part_floats(N, K) * 4));
   return sk_check_launch(launch_gemm(p, mode, (hipStream_t)stream), "sk_bgemm");
 }
 
@@ -657,12 +719,15 @@ extern "C" int sk_batch_frame(const sk_batch_desc* d, void* stream) {
   bf16_t* att = (bf16_t*)(ws + w.att);
   bf16_t* act = (bf16_t*)(ws + w.act);
   float* logits = (float*)(ws + w.logits);
+  float* gpart = (float*)(ws + w.gpart);
+  unsigned* gctr = (unsigned*)(ws + w.gctr);
   const int nqkv = (nq + 2 * nkv) * SK_HD;
   hipError_t e = hipSuccess;
   for (int l = 0; l < d->n_layers && e == hipSuccess; l++) {
     const sk_layer_desc& L = d->layers[l];
     const int np_a = l == 0 ? 1 : H / 16;
-    GemmArgs g1{xa, ssa, np_a, d->eps, (const uint8_t*)L.qkv_w, L.qkv_s, nqkv, H, qkv, nullptr, nullptr, nullptr, nullptr};
+    GemmArgs g1{xa, ssa, np_a, d->eps, (const uint8_t*)L.qkv_w, L.qkv_s, nqkv, H, qkv, nullptr, nullptr, nullptr, nullptr,
+                1, gpart, gctr};
     e = launch_gemm(g1, kOutF32, st);
     if (e != hipSuccess) break;
     AttnArgs at{qkv, L.qn, L.kn, d->eps, d->rope, (bf16_t*)L.kc, (bf16_t*)L.vc, d->pos, d->max_len, nq, nkv, att,
@@ -670,21 +735,25 @@ extern "C" int sk_batch_frame(const sk_batch_desc* d, void* stream) {
     hipLaunchKernelGGL(k_battn, dim3(d->batch * nkv, (d->max_len + kAttnChunk - 1) / kAttnChunk), dim3(kThreads), 0, st, at);
     e = hipGetLastError();
     if (e != hipSuccess) break;
-    GemmArgs g2{att, nullptr, 0, d->eps, (const uint8_t*)L.o_w, L.o_s, H, nq * SK_HD, h, nullptr, xb, L.post_norm, ssb};
+    GemmArgs g2{att, nullptr, 0, d->eps, (const uint8_t*)L.o_w, L.o_s, H, nq * SK_HD, h, nullptr, xb, L.post_norm, ssb,
+                1, gpart, gctr};
     e = launch_gemm(g2, kOutAcc, st);
     if (e != hipSuccess) break;
-    GemmArgs g3{xb, ssb, H / 16, d->eps, (const uint8_t*)L.gu_w, L.gu_s, 2 * I, H, nullptr, act, nullptr, nullptr, nullptr};
+    GemmArgs g3{xb, ssb, H / 16, d->eps, (const uint8_t*)L.gu_w, L.gu_s, 2 * I, H, nullptr, act, nullptr, nullptr, nullptr,
+                1, gpart, gctr};
     e = launch_gemm(g3, kOutSwiglu, st);
     if (e != hipSuccess) break;
     const float* nw_next = l + 1 < d->n_layers ? d->layers[l + 1].in_norm : d->norm;
-    GemmArgs g4{act, nullptr, 0, d->eps, (const uint8_t*)L.down_w, L.down_s, H, I, h, nullptr, xa, nw_next, ssa};
+    GemmArgs g4{act, nullptr, 0, d->eps, (const uint8_t*)L.down_w, L.down_s, H, I, h, nullptr, xa, nw_next, ssa,
+                1, gpart, gctr};
     e = launch_gemm(g4, kOutAcc, st);
     if (e != hipSuccess) break;
     if (d->layer_out)
       e = hipMemcpyAsync(d->layer_out + (size_t)l * kM * H, h, (size_t)kM * H * 4, hipMemcpyDeviceToDevice, st);
   }
   if (e == hipSuccess) {
-    GemmArgs gh{xa, ssa, H / 16, d->eps, (const uint8_t*)d->head_w, d->head_s, V, H, logits, nullptr, nullptr, nullptr, nullptr};
+    GemmArgs gh{xa, ssa, H / 16, d->eps, (const uint8_t*)d->head_w, d->head_s, V, H, logits, nullptr, nullptr, nullptr,
+                nullptr, 1, gpart, gctr};
     e = launch_gemm(gh, kOutF32, st);
   }
   if (e == hipSuccess && d->logits) e = hipMemcpyAsync(d->logits, logits, (size_t)kM * V * 4, hipMemcpyDeviceToDevice, st);

@@ -64,14 +64,15 @@ def test_bgemm_modes_against_fp32(gpu, N, K):
     xv = x.numpy()
     p = _lib.ptr
     st = _lib.stream()
+    ws = torch.zeros(int(_lib.load().sk_bgemm_workspace_size(N, K)), dtype=torch.uint8, device=gpu)
     # mode 0: out = (x W^T) * inv
     out = torch.zeros(16, N, device=gpu)
-    _lib.call("sk_bgemm", p(xp), p(ssp), npart, 1e-6, p(wt), p(lin.s), N, K, 0, p(out), None, None, None, None, st)
+    _lib.call("sk_bgemm", p(xp), p(ssp), npart, 1e-6, p(wt), p(lin.s), N, K, 0, p(out), None, None, None, None, p(ws), ws.numel(), st)
     ref = (xv @ deq.T) * inv[:, None]
     e0 = rel_err(out, ref)
     # mode 1: silu(gate) * up over interleaved rows
     act = torch.zeros((xp.shape[0], 16, N // 2), dtype=torch.bfloat16, device=gpu)
-    _lib.call("sk_bgemm", p(xp), p(ssp), npart, 1e-6, p(wt), p(lin.s), N, K, 1, None, p(act), None, None, None, st)
+    _lib.call("sk_bgemm", p(xp), p(ssp), npart, 1e-6, p(wt), p(lin.s), N, K, 1, None, p(act), None, None, None, p(ws), ws.numel(), st)
     gt, up = ref[:, 0::2], ref[:, 1::2]
     e1 = rel_err(act.float().sum(0), gt / (1 + np.exp(-gt)) * up)
     # mode 2: residual += x W^T, normalised planes of the result, per-tile sums of squares
@@ -80,7 +81,7 @@ def test_bgemm_modes_against_fp32(gpu, N, K):
     nw = (1 + 0.1 * torch.randn(N, generator=g)).to(gpu)
     xn = torch.zeros((xp.shape[0], 16, N), dtype=torch.bfloat16, device=gpu)
     sso = torch.zeros(N // 16, 16, device=gpu)
-    _lib.call("sk_bgemm", p(xp), None, 0, 1e-6, p(wt), p(lin.s), N, K, 2, p(h), None, p(xn), p(nw), p(sso), st)
+    _lib.call("sk_bgemm", p(xp), None, 0, 1e-6, p(wt), p(lin.s), N, K, 2, p(h), None, p(xn), p(nw), p(sso), p(ws), ws.numel(), st)
     href = h0.numpy() + xv @ deq.T
     e2 = rel_err(h, href)
     e3 = rel_err(xn.float().sum(0), href * nw.cpu().numpy())

@@ -84,12 +84,18 @@ def test_batched_entry_points_reject_bad_shapes_without_launching():
     d = ctypes.c_void_p(256)
     assert L.sk_batch_terms() in (1, 2, 3)
     # K not a supported length, N not a multiple of 16, SwiGLU with N % 32 != 0, accumulate without its outputs
-    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 64, 1000, 0, d, None, None, None, None, None) == _lib.SK_EINVAL
-    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 40, 1024, 0, d, None, None, None, None, None) == _lib.SK_EINVAL
-    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 48, 1024, 1, None, d, None, None, None, None) == _lib.SK_EINVAL
-    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 64, 1024, 2, d, None, None, None, None, None) == _lib.SK_EINVAL
-    assert L.sk_bgemm(d, d, 0, 1e-6, d, d, 64, 1024, 0, d, None, None, None, None, None) == _lib.SK_EINVAL
+    W = (d, 1 << 20, None)  # workspace, its size, stream
+    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 64, 1000, 0, d, None, None, None, None, *W) == _lib.SK_EINVAL
+    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 40, 1024, 0, d, None, None, None, None, *W) == _lib.SK_EINVAL
+    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 48, 1024, 1, None, d, None, None, None, *W) == _lib.SK_EINVAL
+    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 64, 1024, 2, d, None, None, None, None, *W) == _lib.SK_EINVAL
+    assert L.sk_bgemm(d, d, 0, 1e-6, d, d, 64, 1024, 0, d, None, None, None, None, *W) == _lib.SK_EINVAL
     assert L.sk_tile_weights(d, d, 40, 128, None) == _lib.SK_EINVAL
+    # a workspace smaller than the split-K partials of the 1.7B down projection
+    need = L.sk_bgemm_workspace_size(2048, 6144)
+    assert need > 0 and L.sk_bgemm_workspace_size(40, 1024) == 0
+    assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 2048, 6144, 0, d, None, None, None, None, d, need - 256, None) == \
+        _lib.SK_EWORKSPACE
     ws = L.sk_batch_workspace_size(2048, 6144, 16, 8, 3072)
     assert ws > 16 * 8 * 2 * 64 * 130 * 4
     desc = _lib.SkBatchDesc(n_layers=28, hidden=2048, inter=6144, nq=16, nkv=8, vocab=3072, batch=17, max_len=2100)
