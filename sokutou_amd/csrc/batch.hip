@@ -223,12 +223,15 @@ __global__ void k_tile(const int8_t* __restrict__ w, int8_t* __restrict__ tiled,
 }
 
 // ---- ragged split-K decode attention -----------------------------------------------------------------------
-// Block (stream b, kv head g, split s) covers positions [64 s, 64 s + 64) of stream b's cache up to its current
-// position; the split that holds the position also normalises, rotates and appends this step's K and V. Partials
-// (max, sum, Σ p v) go to the workspace; the last split of (b, g) to arrive merges them in split order and writes
-// the attention output as bf16 term planes. Numerics as sk_attn (qwen3/kernels.py:338-414).
-constexpr int kAttnChunk = 64;
-constexpr int kAttnSplitMax = 64;  // max_len <= 4096
+// Block (stream b, kv head g, split s) covers positions [128 s, 128 s + 128) of stream b's cache up to its current
+// position, in two passes of 64 positions whose K/V rows are all loaded at the top; the split that holds the position
+// also normalises, rotates and appends this step's K and V. Partials (max, sum, Σ p v) go to the workspace; the
+// last split of (b, g) to arrive merges them in split order and writes the attention output as bf16 term planes.
+// Numerics as sk_attn (qwen3/kernels.py:338-414).
+constexpr int kPass = 64;
+constexpr int kAttnPasses = 2;
+constexpr int kAttnChunk = kPass * kAttnPasses;
+constexpr int kAttnSplitMax = 32;  // max_len <= 4096
 constexpr int kPart = SK_HD + 2;
 constexpr float kInvSqrtHd = 0.08838834764831845f;
 
@@ -248,11 +251,16 @@ struct AttnArgs {
   int* err;
 };
 
+__device__ __forceinline__ void unpack8(uint4 v, float* o) {
+  o[0] = bf2f(v.x & 0xffffu); o[1] = bf2f(v.x >> 16); o[2] = bf2f(v.y & 0xffffu); o[3] = bf2f(v.y >> 16);
+  o[4] = bf2f(v.z & 0xffffu); o[5] = bf2f(v.z >> 16); o[6] = bf2f(v.w & 0xffffu); o[7] = bf2f(v.w >> 16);
+}
+
 __global__ __launch_bounds__(kThreads) void k_battn(AttnArgs a) {
   __shared__ float qsh[2][SK_HD];
   __shared__ float ksh[SK_HD];
   __shared__ float vsh[SK_HD];
-  __shared__ float sc[2][kAttnChunk];
+  __shared__ float sc[2][kPass];
   __shared__ float red[16];
   __shared__ float opart[4][4][16][17];
   __shared__ float mls[2][kAttnSplitMax][2];
@@ -271,34 +279,39 @@ __global__ __launch_bounds__(kThreads) void k_battn(AttnArgs a) {
   }
   const int pos = (int)pos64, T = pos + 1, ns = (T + kAttnChunk - 1) / kAttnChunk;
   if (split >= ns) return;
-  const int t0 = split * kAttnChunk, n = min(kAttnChunk, T - t0);
+  const int t0 = split * kAttnChunk, n = min(kAttnChunk, T - t0), npass = (n + kPass - 1) / kPass;
   const bool has_pos = split == ns - 1;
   bf16_t* Kh = a.Kc + ((size_t)b * a.nkv + kvh) * a.max_len * SK_HD;
   bf16_t* Vh = a.Vc + ((size_t)b * a.nkv + kvh) * a.max_len * SK_HD;
   const float* qrow = a.qkv + (size_t)b * qs;
-
-  uint4 kr[4], vr[4];
+  // lane (w, gq, sl) holds dims [8 sl, 8 sl + 8) of positions 16 i + 4 w + gq of a pass. Every load is issued
+  // unconditionally (rows past the block's range read row t0 instead and are never used; the row at pos is taken
+  // from LDS), so all of them are in flight together.
+  auto load_pass = [&](int ps, uint4 (&kr)[4], uint4 (&vr)[4]) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int jj = 16 * i + 4 * w + gq;
-    if (jj < n && t0 + jj != pos) {
-      kr[i] = *(const uint4*)(Kh + (size_t)(t0 + jj) * SK_HD + 8 * sl);
-      vr[i] = *(const uint4*)(Vh + (size_t)(t0 + jj) * SK_HD + 8 * sl);
-    } else {
-      kr[i] = vr[i] = make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < 4; i++) {
+      const int jj = ps * kPass + 16 * i + 4 * w + gq;
+      const size_t row = (size_t)(jj < n ? t0 + jj : t0) * SK_HD + 8 * sl;
+      kr[i] = gload4((const uint4*)(Kh + row));
+      vr[i] = gload4((const uint4*)(Vh + row));
     }
-  }
+  };
+  // this step's inputs first (the wait for them must not also wait for the cache rows), then every cache row
+  const float c = a.rope[(size_t)pos * SK_HD + (d & 63)], s = a.rope[(size_t)pos * SK_HD + 64 + (d & 63)];
+  const float qv = qrow[(2 * kvh + p) * SK_HD + d];
+  const float kv = has_pos ? qrow[a.nq * SK_HD + p * a.nkv * SK_HD + kvh * SK_HD + d] : 0.f;
+  const float qw = a.qn[d], kw = a.kn[d];
+  uint4 kr[kAttnPasses][4], vr[kAttnPasses][4];
+#pragma unroll
+  for (int ps = 0; ps < kAttnPasses; ps++) load_pass(ps, kr[ps], vr[ps]);
   // q of both heads (and, in the split holding pos, this step's k / v): per-head RMSNorm, RoPE, bf16 append
   {
-    const float c = a.rope[(size_t)pos * SK_HD + (d & 63)], s = a.rope[(size_t)pos * SK_HD + 64 + (d & 63)];
-    const float qv = qrow[(2 * kvh + p) * SK_HD + d];
-    const float kv = has_pos ? qrow[a.nq * SK_HD + p * a.nkv * SK_HD + kvh * SK_HD + d] : 0.f;
     const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
     if (lane == 0) { red[w] = sq; red[4 + w] = sk; }
     __syncthreads();
-    qsh[p][d] = qv * rsqrtf((red[2 * p] + red[2 * p + 1]) / SK_HD + a.eps) * a.qn[d];
+    qsh[p][d] = qv * rsqrtf((red[2 * p] + red[2 * p + 1]) / SK_HD + a.eps) * qw;
     if (has_pos) {
-      if (p == 0) ksh[d] = kv * rsqrtf((red[4] + red[5]) / SK_HD + a.eps) * a.kn[d];
+      if (p == 0) ksh[d] = kv * rsqrtf((red[4] + red[5]) / SK_HD + a.eps) * kw;
       else vsh[d] = bf2f(f2bf(kv));
     }
     __syncthreads();
@@ -313,77 +326,86 @@ __global__ __launch_bounds__(kThreads) void k_battn(AttnArgs a) {
     }
     __syncthreads();
   }
-  // scores of both heads
   float q0[8], q1[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) { q0[e] = qsh[0][8 * sl + e]; q1[e] = qsh[1][8 * sl + e]; }
+  float m = -INFINITY, l = 0.f, o = 0.f;  // running partial of head p, dim d
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int jj = 16 * i + 4 * w + gq;
-    float k8[8];
-    if (jj < n && t0 + jj == pos) {
+  for (int ps = 0; ps < kAttnPasses; ps++) {
+    if (ps >= npass) break;  // uniform over the block
+    const int base = ps * kPass, np = min(kPass, n - base);
+    // scores of both heads
 #pragma unroll
-      for (int e = 0; e < 8; e++) k8[e] = ksh[8 * sl + e];
-    } else {
-      const uint4 v = kr[i];
-      k8[0] = bf2f(v.x & 0xffffu); k8[1] = bf2f(v.x >> 16); k8[2] = bf2f(v.y & 0xffffu); k8[3] = bf2f(v.y >> 16);
-      k8[4] = bf2f(v.z & 0xffffu); k8[5] = bf2f(v.z >> 16); k8[6] = bf2f(v.w & 0xffffu); k8[7] = bf2f(v.w >> 16);
-    }
-    float s0 = 0.f, s1 = 0.f;
+    for (int i = 0; i < 4; i++) {
+      const int jl = 16 * i + 4 * w + gq;
+      float k8[8];
+      if (base + jl < n && t0 + base + jl == pos) {
 #pragma unroll
-    for (int e = 0; e < 8; e++) { s0 = __builtin_fmaf(q0[e], k8[e], s0); s1 = __builtin_fmaf(q1[e], k8[e], s1); }
-    s0 = row16_sum(s0);
-    s1 = row16_sum(s1);
-    if (sl == 0 && jj < n) { sc[0][jj] = s0; sc[1][jj] = s1; }
-  }
-  __syncthreads();
-  // softmax statistics per head (threads 0-127: head 0, 128-255: head 1)
-  const float sv = d < n ? sc[p][d] : -INFINITY;
-  const float mx = wave_max(sv);
-  if (lane == 0) red[8 + w] = mx;
-  __syncthreads();
-  const float mp = fmaxf(red[8 + 2 * p], red[8 + 2 * p + 1]);
-  const float ev = d < n ? expf(sv - mp) : 0.f;
-  const float se = wave_sum(ev);
-  if (d < n) sc[p][d] = ev;
-  if (lane == 0) red[12 + w] = se;
-  __syncthreads();
-  const float lp = red[12 + 2 * p] + red[12 + 2 * p + 1];
-  // Σ p_j v_j for both heads
-  float a0[8], a1[8];
-#pragma unroll
-  for (int e = 0; e < 8; e++) { a0[e] = 0.f; a1[e] = 0.f; }
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int jj = 16 * i + 4 * w + gq;
-    if (jj < n) {
-      float v8[8];
-      if (t0 + jj == pos) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) v8[e] = vsh[8 * sl + e];
+        for (int e = 0; e < 8; e++) k8[e] = ksh[8 * sl + e];
       } else {
-        const uint4 v = vr[i];
-        v8[0] = bf2f(v.x & 0xffffu); v8[1] = bf2f(v.x >> 16); v8[2] = bf2f(v.y & 0xffffu); v8[3] = bf2f(v.y >> 16);
-        v8[4] = bf2f(v.z & 0xffffu); v8[5] = bf2f(v.z >> 16); v8[6] = bf2f(v.w & 0xffffu); v8[7] = bf2f(v.w >> 16);
+        unpack8(kr[ps][i], k8);
       }
-      const float e0 = sc[0][jj], e1 = sc[1][jj];
+      float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; e++) { a0[e] = __builtin_fmaf(e0, v8[e], a0[e]); a1[e] = __builtin_fmaf(e1, v8[e], a1[e]); }
+      for (int e = 0; e < 8; e++) { s0 = __builtin_fmaf(q0[e], k8[e], s0); s1 = __builtin_fmaf(q1[e], k8[e], s1); }
+      s0 = row16_sum(s0);
+      s1 = row16_sum(s1);
+      if (sl == 0 && jl < np) { sc[0][jl] = s0; sc[1][jl] = s1; }
     }
+    __syncthreads();
+    // pass softmax statistics per head (threads 0-127: head 0, 128-255: head 1)
+    const float sv = d < np ? sc[p][d] : -INFINITY;
+    const float mx = wave_max(sv);
+    if (lane == 0) red[8 + w] = mx;
+    __syncthreads();
+    const float mp = fmaxf(red[8 + 2 * p], red[8 + 2 * p + 1]);
+    const float ev = d < np ? expf(sv - mp) : 0.f;
+    const float se = wave_sum(ev);
+    if (d < np) sc[p][d] = ev;
+    if (lane == 0) red[12 + w] = se;
+    __syncthreads();
+    const float lp = red[12 + 2 * p] + red[12 + 2 * p + 1];
+    // Σ p_j v_j for both heads
+    float a0[8], a1[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) { a0[e] = 0.f; a1[e] = 0.f; }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int jl = 16 * i + 4 * w + gq;
+      if (jl < np) {
+        float v8[8];
+        if (t0 + base + jl == pos) {
+#pragma unroll
+          for (int e = 0; e < 8; e++) v8[e] = vsh[8 * sl + e];
+        } else {
+          unpack8(vr[ps][i], v8);
+        }
+        const float e0 = sc[0][jl], e1 = sc[1][jl];
+#pragma unroll
+        for (int e = 0; e < 8; e++) { a0[e] = __builtin_fmaf(e0, v8[e], a0[e]); a1[e] = __builtin_fmaf(e1, v8[e], a1[e]); }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) { opart[w][gq][sl][e] = a0[e]; opart[w][gq][sl][8 + e] = a1[e]; }
+    __syncthreads();
+    float op = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ww++)
+#pragma unroll
+      for (int gg = 0; gg < 4; gg++) op += opart[ww][gg][d >> 3][p * 8 + (d & 7)];
+    // fold the pass into the running partial
+    const float mn = fmaxf(m, mp);
+    const float fo = m == -INFINITY ? 0.f : expf(m - mn), fp = expf(mp - mn);
+    o = o * fo + op * fp;
+    l = l * fo + lp * fp;
+    m = mn;
+    __syncthreads();  // sc / opart are rewritten by the next pass
   }
-#pragma unroll
-  for (int e = 0; e < 8; e++) { opart[w][gq][sl][e] = a0[e]; opart[w][gq][sl][8 + e] = a1[e]; }
-  __syncthreads();
-  float op = 0.f;
-#pragma unroll
-  for (int ww = 0; ww < 4; ww++)
-#pragma unroll
-    for (int gg = 0; gg < 4; gg++) op += opart[ww][gg][d >> 3][p * 8 + (d & 7)];
 
   // publish the partial (device-coherent stores) and count the arrival
   const uint32_t pofs = (uint32_t)(((bg * 2 + p) * kAttnSplitMax + split) * kPart) * 4;
-  if (d == 0) { buf_stf(a.part, pofs, mp); buf_stf(a.part, pofs + 4, lp); }
-  buf_stf(a.part, pofs + 8 + 4 * d, op);
+  if (d == 0) { buf_stf(a.part, pofs, m); buf_stf(a.part, pofs + 4, l); }
+  buf_stf(a.part, pofs + 8 + 4 * d, o);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (t == 0) {
@@ -399,23 +421,20 @@ __global__ __launch_bounds__(kThreads) void k_battn(AttnArgs a) {
     mls[pp][cc][0] = buf_ldf(a.part, of);
     mls[pp][cc][1] = buf_ldf(a.part, of + 4);
   }
+  float oc[kAttnSplitMax];
+#pragma unroll
+  for (int k = 0; k < kAttnSplitMax; k++)
+    oc[k] = k < ns ? buf_ldf(a.part, (uint32_t)(((bg * 2 + p) * kAttnSplitMax + k) * kPart) * 4 + 8 + 4 * d) : 0.f;
   __syncthreads();
   float M = -INFINITY;
   for (int cc = 0; cc < ns; cc++) M = fmaxf(M, mls[p][cc][0]);
   float L = 0.f, O = 0.f;
-  for (int c0 = 0; c0 < ns; c0 += 16) {
-    float oc[16];
 #pragma unroll
-    for (int k = 0; k < 16; k++)
-      oc[k] = c0 + k < ns ? buf_ldf(a.part, (uint32_t)(((bg * 2 + p) * kAttnSplitMax + c0 + k) * kPart) * 4 + 8 + 4 * d)
-                          : 0.f;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      if (c0 + k < ns && mls[p][c0 + k][0] != -INFINITY) {
-        const float f = expf(mls[p][c0 + k][0] - M);
-        L = __builtin_fmaf(f, mls[p][c0 + k][1], L);
-        O = __builtin_fmaf(f, oc[k], O);
-      }
+  for (int k = 0; k < kAttnSplitMax; k++) {
+    if (k < ns && mls[p][k][0] != -INFINITY) {
+      const float f = expf(mls[p][k][0] - M);
+      L = __builtin_fmaf(f, mls[p][k][1], L);
+      O = __builtin_fmaf(f, oc[k], O);
     }
   }
   store_terms(a.att, ap, (size_t)b * a.nq * SK_HD + (2 * kvh + p) * SK_HD + d, L > 0.f ? O / L : 0.f);
@@ -523,12 +542,14 @@ hipError_t launch_cw(const GemmArgs& p, hipStream_t st) {
 }
 bool k_supported(int K) { return K == 512 || K == 1024 || K == 2048 || K == 3072 || K == 4096 || K == 6144; }
 
-// Launch plan: R 16-row groups per workgroup (as many as the row count allows, for reuse of the activation
-// loads) and the fewest K slices S that give at least kMinWg workgroups, each wave keeping at most 8 chunks.
+// Launch plan: R 16-row groups per workgroup (4 for the wide gate/up projection, else 2: reuse of the activation
+// loads against enough workgroups) and the fewest K slices S that give at least kMinWg workgroups, each wave
+// keeping at most 8 chunks. Measured on MI355X for the 1.7B shapes: qkv R2 S2, o R2 S4, gate/up R4 S1, down R2 S4,
+// head R2 S2 were within 1% of the best of all (R, S).
 constexpr int kMinWg = 192;
 struct Plan { int R, S; };
 Plan plan(int N, int K) {
-  Plan pl{N % 64 == 0 ? 4 : N % 32 == 0 ? 2 : 1, 1};
+  Plan pl{N % 64 == 0 && N >= 8192 ? 4 : N % 32 == 0 ? 2 : 1, 1};
   const int tiles = N / (16 * pl.R);
   auto cw_ok = [&](int S) {
     if (K % (256 * S)) return false;
