@@ -93,8 +93,10 @@ int sk_attn(const float* qkv, const float* qn, const float* kn, float eps, const
  * do_sample == 0 is greedy argmax with the lowest index winning ties. seen / suppress are bool (1 byte) arrays,
  * NULL when unused; seed / counter are device uint64 (used only when sampling).
  * Replaces sample(logits, V, inv_temp, top_k, do_sample, seen, rep_pen, suppress, ngen, min_new, eos, seed,
- * counter, out, talker, id0, pos) (qwen3/sampler.py:37-159). This build implements the greedy path
- * (do_sample == 0); do_sample != 0 returns SK_EUNSUPPORTED. */
+ * counter, out, talker, id0, pos) (qwen3/sampler.py:37-159). do_sample != 0 scales by inv_temp (> 0), keeps the
+ * entries at or above the top_k-th largest (top_k <= 0 or >= V keeps all) that are not -inf and picks the largest
+ * v - log(-log(u)), u from Philox4x32-10 with counter (index, *counter) and key *seed; *counter += 1 after the draw
+ * (seed / counter are device uint64). The same seed and counter give the reference kernel's pick. */
 int sk_sample(const float* logits, int V, float inv_temp, int top_k, int do_sample, uint8_t* seen, float rep_pen,
               const uint8_t* suppress, int64_t* ngen, int min_new, int eos, const uint64_t* seed, uint64_t* counter,
               int64_t* out, int talker, int64_t* id0, int64_t* pos, void* stream);

@@ -26,6 +26,10 @@ How each function is pinned (independent checks, in ``tests/test_oracle.py``):
                                T=1 gives out = V; uniform K gives mean(V).
   * ``decoder_layer``        - transformers' Qwen3DecoderLayer (f32 cache) within 1e-5.
   * ``process_logits``/``argmax_first`` - crafted ties, NaN, all -inf; restated from qwen3/sampler.py:50-65, 129-149.
+  * ``philox4x32_10``        - the Random123 known-answer vectors of philox4x32_10.
+  * ``topk_threshold``       - brute force (count of strictly larger keys < k <= count of keys >= it).
+  * ``sample_draw``          - the empirical law of many draws against softmax over the top-k (chi-square), and
+                               the keep rule by hand on crafted ties / -inf / NaN.
 """
 
 from __future__ import annotations
@@ -280,6 +284,78 @@ def process_logits(logits: np.ndarray, seen: np.ndarray | None, rep_pen: float, 
     if ngen < min_new and 0 <= eos < v.size:
         v[eos] = -np.inf
     return v
+
+
+def order_key(v: np.ndarray) -> np.ndarray:
+    """fp32 -> uint32 key with the same order as the values (sign bit set for positives, all bits flipped for
+    negatives) (``fkey``, qwen3/sampler.py:21-24)."""
+    u = np.ascontiguousarray(v, dtype=F32).view(np.uint32)
+    return np.where(u & np.uint32(0x80000000), ~u, u | np.uint32(0x80000000)).astype(np.uint32)
+
+
+PHILOX_M = (0xD2511F53, 0xCD9E8D57)
+PHILOX_W = (0x9E3779B9, 0xBB67AE85)
+
+
+def philox4x32_10(ctr: np.ndarray, key: np.ndarray) -> np.ndarray:
+    """Philox4x32 with 10 rounds (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3",
+    SC'11): per round two 32x32->64-bit products of the counter words 0 and 2 with the published multipliers, the
+    high halves xored with the other words and the key, then the key bumped by the Weyl constants.
+    ``ctr`` [..., 4] and ``key`` [..., 2] uint32 (broadcast); returns [..., 4] uint32. The reference's sampler
+    uses this generator (qwen3/sampler.py:25-34)."""
+    c = [np.asarray(ctr[..., i], dtype=np.uint64) for i in range(4)]
+    k0 = np.asarray(key[..., 0], dtype=np.uint64)
+    k1 = np.asarray(key[..., 1], dtype=np.uint64)
+    m32 = np.uint64(0xFFFFFFFF)
+    for _ in range(10):
+        p0 = np.uint64(PHILOX_M[0]) * c[0]
+        p1 = np.uint64(PHILOX_M[1]) * c[2]
+        c = [((p1 >> np.uint64(32)) ^ c[1] ^ k0) & m32, p1 & m32, ((p0 >> np.uint64(32)) ^ c[3] ^ k1) & m32, p0 & m32]
+        k0 = (k0 + np.uint64(PHILOX_W[0])) & m32
+        k1 = (k1 + np.uint64(PHILOX_W[1])) & m32
+    return np.stack(np.broadcast_arrays(*c), axis=-1).astype(np.uint32)
+
+
+def topk_threshold(v: np.ndarray, top_k: int) -> int:
+    """Order key of the top_k-th largest value (0 keeps everything when top_k <= 0 or top_k >= V). The reference
+    finds it by a 4-pass 8-bit radix select over the keys (qwen3/sampler.py:67-112); the result is the key of
+    the k-th largest entry, ties included, which this computes by sorting."""
+    if top_k <= 0 or top_k >= v.size:
+        return 0
+    return int(np.sort(order_key(v))[::-1][top_k - 1])
+
+
+def gumbel_uniform(V: int, seed: int, counter: int) -> np.ndarray:
+    """The uniform in (0, 1) of every index for one draw: ``(r0 >> 8) + 0.5`` scaled by 2^-24 (exact in fp32), with
+    r = Philox4x32-10(counter = (i, draw lo, draw hi, 0x51), key = (seed lo, seed hi)) (qwen3/sampler.py:118-123)."""
+    i = np.arange(V, dtype=np.uint32)
+    ctr = np.stack([i, np.full(V, counter & 0xFFFFFFFF, np.uint32), np.full(V, (counter >> 32) & 0xFFFFFFFF, np.uint32),
+                    np.full(V, 0x51, np.uint32)], axis=1)
+    key = np.array([seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF], dtype=np.uint32)
+    r = philox4x32_10(ctr, key)
+    return ((r[:, 0] >> np.uint32(8)).astype(F32) + F32(0.5)) * F32(1.0 / 16777216.0)
+
+
+def sample_draw(v: np.ndarray, inv_temp: float, top_k: int, seed: int, counter: int, exact: bool = False):
+    """One sampled pick from processed logits ``v`` (qwen3/sampler.py:47-154 with do_sample = 1): v * inv_temp,
+    keep the entries whose key is at least the top_k threshold and that are not -inf, then the argmax of
+    v - log(-log(u)) (Gumbel-max: the same law as softmax sampling over the kept entries), lowest index on ties,
+    index 0 if nothing is kept. Returns (index, perturbed values) with the perturbation in fp32, or in float64
+    when ``exact`` (to measure how close the top two are)."""
+    x = np.asarray(v, dtype=F32) * F32(inv_temp)
+    thr = topk_threshold(x, top_k)
+    keep = (order_key(x) >= np.uint32(thr)) & (x != -np.inf)
+    u = gumbel_uniform(x.size, seed, counter)
+    if exact:
+        g = x.astype(np.float64) - np.log(-np.log(u.astype(np.float64)))
+    else:
+        g = x - np.log(-np.log(u)).astype(F32)
+    g = np.where(keep, g, -np.inf)
+    ok = ~np.isnan(g) & keep
+    if not ok.any():
+        return 0, g
+    m = g[ok].max()
+    return int(np.flatnonzero(ok & (g == m))[0]), g
 
 
 def argmax_first(v: np.ndarray) -> int:

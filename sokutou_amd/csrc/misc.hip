@@ -103,6 +103,143 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_greedy(const float* _
   }
 }
 
+// ---- sampled pick: processor, temperature, top-k threshold, Gumbel-max (qwen3/sampler.py:37-159) -----------------
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): ten rounds of two 32x32->64-bit products with the published
+// multipliers, the high halves xored with the other counter words and the key, the key bumped by Weyl constants.
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; r++) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c.x, p1 = (uint64_t)0xCD9E8D57u * c.z;
+    c = make_uint4((uint32_t)(p1 >> 32) ^ c.y ^ k0, (uint32_t)p1, (uint32_t)(p0 >> 32) ^ c.w ^ k1, (uint32_t)p0);
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c;
+}
+
+// One block of 1024 threads, 4 entries per thread. The top_k-th largest key is found by a radix select over the
+// four bytes of the order key, most significant first: a 256-bin LDS histogram of the entries that match the
+// digits chosen so far, then one wave scans the bins from the top to find the digit where the count reaches the
+// rank still needed. Every entry whose key is at least that threshold (ties included) and that is not -inf competes
+// with v - log(-log(u)), u from Philox4x32-10 with counter (index, draw lo, draw hi, 0x51) and key (seed lo, seed
+// hi); the largest wins, the lowest index on ties. Afterwards the draw counter advances by one.
+__global__ __launch_bounds__(kSampleThreads) void k_sample_draw(const float* __restrict__ logits, int V, float inv_temp,
+                                                                int top_k, uint8_t* __restrict__ seen, float rep_pen,
+                                                                const uint8_t* __restrict__ suppress,
+                                                                int64_t* __restrict__ ngen, int min_new, int eos,
+                                                                const uint64_t* __restrict__ seed,
+                                                                uint64_t* __restrict__ counter, int64_t* __restrict__ out,
+                                                                int talker, int64_t* __restrict__ id0,
+                                                                int64_t* __restrict__ pos) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t s_prefix, s_need;
+  __shared__ float best_v[kSampleThreads / SK_WAVE];
+  __shared__ int best_i[kSampleThreads / SK_WAVE];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const bool block_eos = talker && ngen && ngen[0] < min_new;
+  float l[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {
+    const int i = t + j * kSampleThreads;
+    float v = -INFINITY;
+    if (i < V) {
+      v = logits[i];
+      if (talker) {
+        if (seen && seen[i]) v = v < 0.f ? v * rep_pen : v / rep_pen;
+        if (suppress && suppress[i]) v = -INFINITY;
+        if (block_eos && i == eos) v = -INFINITY;
+      }
+      v *= inv_temp;
+    }
+    l[j] = v;
+  }
+  uint32_t thr = 0;
+  if (top_k > 0 && top_k < V) {
+    if (t == 0) { s_prefix = 0; s_need = (uint32_t)top_k; }
+    for (int pass = 0; pass < 4; pass++) {
+      const int shift = 24 - 8 * pass;
+      if (t < 256) hist[t] = 0;
+      __syncthreads();
+      const uint32_t prefix = s_prefix, need = s_need;
+#pragma unroll
+      for (int j = 0; j < kPer; j++) {
+        const int i = t + j * kSampleThreads;
+        if (i >= V) continue;
+        const uint32_t k = order_key(l[j]);
+        if (pass == 0 || ((k ^ prefix) >> (shift + 8)) == 0) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (w == 0) {
+        // lane L holds bins 255 - 4L .. 252 - 4L (descending); inclusive scan of the counts over the lanes
+        uint32_t c[4], sum = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) { c[q] = hist[255 - (4 * lane + q)]; sum += c[q]; }
+        uint32_t inc = sum;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t y = __shfl_up(inc, o);
+          if (lane >= o) inc += y;
+        }
+        const uint32_t before = inc - sum;
+        if (before < need && inc >= need) {
+          uint32_t acc = before;
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            if (acc + c[q] >= need) {
+              const uint32_t digit = 255u - (uint32_t)(4 * lane + q);
+              s_prefix = prefix | (digit << shift);
+              s_need = need - acc;
+              break;
+            }
+            acc += c[q];
+          }
+        }
+      }
+      __syncthreads();
+    }
+    thr = s_prefix;
+  }
+  const uint64_t sd = seed[0], cnt = counter[0];
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {
+    const int i = t + j * kSampleThreads;
+    if (i >= V) continue;
+    const float v = l[j];
+    if (order_key(v) < thr || v == -INFINITY) continue;
+    const uint4 r = philox4x32_10(make_uint4((uint32_t)i, (uint32_t)cnt, (uint32_t)(cnt >> 32), 0x51u), (uint32_t)sd,
+                                  (uint32_t)(sd >> 32));
+    const float u = ((float)(r.x >> 8) + 0.5f) * (1.0f / 16777216.0f);
+    const float g = v - logf(-logf(u));
+    if (g > best || (g == best && i < bi)) { best = g; bi = i; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ob = __shfl_xor(best, o);
+    const int oi = __shfl_xor(bi, o);
+    if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+  }
+  if (lane == 0) { best_v[w] = best; best_i[w] = bi; }
+  __syncthreads();
+  if (t != 0) return;
+  for (int q = 0; q < kSampleThreads / SK_WAVE; q++)
+    if (best_v[q] > best || (best_v[q] == best && best_i[q] < bi)) { best = best_v[q]; bi = best_i[q]; }
+  const int64_t id = bi == 0x7fffffff ? 0 : bi;
+  out[0] = id;
+  counter[0] = cnt + 1;
+  if (talker) {
+    if (id0) id0[0] = id;
+    if (seen) seen[id] = 1;
+    if (ngen) ngen[0] += 1;
+    if (pos) pos[0] += 1;
+  }
+}
+
 }  // namespace
 
 int sk_set_error(int rc, const char* msg) {
@@ -170,10 +307,15 @@ extern "C" int sk_sample(const float* logits, int V, float inv_temp, int top_k, 
                          float rep_pen, const uint8_t* suppress, int64_t* ngen, int min_new, int eos,
                          const uint64_t* seed, uint64_t* counter, int64_t* out, int talker, int64_t* id0, int64_t* pos,
                          void* stream) {
-  (void)inv_temp; (void)top_k; (void)seed; (void)counter;
   if (!logits || !out || V <= 0 || V > SK_MAX_V) return sk_set_error(SK_EINVAL, "sk_sample: bad arguments (V <= 4096)");
   if (talker && !ngen) return sk_set_error(SK_EINVAL, "sk_sample: talker mode needs ngen");
-  if (do_sample) return sk_set_error(SK_EUNSUPPORTED, "sk_sample: only greedy (do_sample=0) is built");
+  if (do_sample) {
+    if (!seed || !counter) return sk_set_error(SK_EINVAL, "sk_sample: sampling needs the device seed and counter");
+    if (!(inv_temp > 0.f) || inv_temp == INFINITY) return sk_set_error(SK_EINVAL, "sk_sample: temperature must be > 0");
+    hipLaunchKernelGGL(k_sample_draw, dim3(1), dim3(kSampleThreads), 0, (hipStream_t)stream, logits, V, inv_temp, top_k,
+                       seen, rep_pen, suppress, ngen, min_new, eos, seed, counter, out, talker, id0, pos);
+    return sk_check_launch(hipGetLastError(), "sk_sample");
+  }
   hipLaunchKernelGGL(k_sample_greedy, dim3(1), dim3(kSampleThreads), 0, (hipStream_t)stream, logits, V, seen, rep_pen,
                      suppress, ngen, min_new, eos, out, talker, id0, pos);
   return sk_check_launch(hipGetLastError(), "sk_sample");

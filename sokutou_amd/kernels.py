@@ -436,5 +436,12 @@ class Qwen3Kernels(Qwen3Fast):
             self.trace = None
         return out
 
+    def generate_codes(self, kw: dict, max_frames: int | None = None) -> torch.Tensor:
+        if self.fs is not None:
+            # the fused sampler's key is drawn from torch's CPU generator, so torch.manual_seed reproduces a run and
+            # successive calls differ (qwen3/kernels.py:709-713); the draw counter restarts at 0
+            self.fs.set_seed(int(torch.randint(0, 2**62, (1,)).item()))
+        return super().generate_codes(kw, max_frames=max_frames)
+
     def weight_bytes(self) -> dict:
         return {"talker": self.T.bytes() + self.codec_head.bytes(), "code_predictor": 0, "cp_heads": 0}

@@ -1,8 +1,10 @@
 """One-launch sampling step on the device (``sk_sample``), with the talker processor and the device-side state
 update, so a whole frame can be replayed from a graph without a host round trip.
 
-Mirrors ``FusedSampler`` of the reference (qwen3/sampler.py:165-191). This build provides the greedy path
-(``do_sample=False``); asking for sampling raises NotImplementedError from the library.
+Mirrors ``FusedSampler`` of the reference (qwen3/sampler.py:165-191): greedy (``do_sample=False``, lowest index
+on ties) or sampled (temperature, top-k threshold by radix select, Gumbel-max with Philox4x32-10 keyed by ``seed``
+and counted by ``counter``). The same seed and counter give the reference kernel's pick; the counter advances on
+the device, so each replay of a captured graph draws a new number.
 """
 
 from __future__ import annotations

@@ -304,10 +304,12 @@ def make_batch_engine(name: str, seed: int = 0, device="cuda", frames: int | Non
 
 
 def make_engine(name: str, seed: int = 0, wd: str = "i8row", device="cuda", graphs: bool = True,
-                max_cache: int | None = None, frames: int | None = None, frame_kernel: bool | None = False):
+                max_cache: int | None = None, frames: int | None = None, frame_kernel: bool | None = False,
+                sampling=None, suppress_tail: int = 0):
     """Builds a Qwen3Kernels engine over the seeded synthetic talker of workload ``name`` with the prior KV
-    cache loaded and the frame state set at position ``kv``. Greedy decoding without the processor (plain
-    argmax over the whole codec vocabulary). Returns (engine, start token)."""
+    cache loaded and the frame state set at position ``kv``. By default greedy decoding without the processor
+    (plain argmax over the whole codec vocabulary); ``sampling`` (a ``Sampling``) overrides. Returns
+    (engine, start token)."""
     from .fast import Sampling
     from .kernels import Qwen3Kernels
 
@@ -316,8 +318,8 @@ def make_engine(name: str, seed: int = 0, wd: str = "i8row", device="cuda", grap
     frames = w.get("frames", 1) if frames is None else frames
     max_cache = max_cache or (w["kv"] + frames + 1)
     tts = make_tts(seed, s, device=device)
-    eng = Qwen3Kernels(tts, Sampling.greedy(processor=False), max_cache=max_cache, wd=wd, graphs=graphs,
-                       sampler="fused", suppress_tail=0, frame_kernel=frame_kernel)
+    eng = Qwen3Kernels(tts, sampling or Sampling.greedy(processor=False), max_cache=max_cache, wd=wd, graphs=graphs,
+                       sampler="fused", suppress_tail=suppress_tail, frame_kernel=frame_kernel)
     tts.model.talker = None  # the fp32 source weights are no longer needed once packed
     eng.talker = None
     del tts

@@ -229,3 +229,88 @@ def test_plain_argmax_without_processor(gpu):
     fs(lgg, out, False, 1.0, 0)
     torch.cuda.synchronize()
     assert int(out) == 0
+
+
+def _near_tie(g, pick, ref, rel=1e-5) -> bool:
+    """True when the GPU's pick and the oracle's are within float rounding of each other (fp32 log on two devices)."""
+    a, b = float(g[pick]), float(g[ref])
+    return np.isfinite(a) and np.isfinite(b) and abs(a - b) <= rel * max(1.0, abs(b))
+
+
+def test_sampled_picks_match_oracle(gpu):
+    """do_sample = 1: processor, temperature, top-k threshold and the Gumbel-max draw from Philox4x32-10 give the
+    oracle's pick for the same seed and counter (qwen3/sampler.py:37-159); the counter advances once per draw."""
+    from sokutou_amd.sampler import FusedSampler
+
+    fs = FusedSampler(gpu)
+    seed = 0x1234_5678_9ABC
+    fs.set_seed(seed)
+    rng = np.random.default_rng(7)
+    out = torch.zeros(1, dtype=torch.int64, device=gpu)
+    bad, ties, n = [], 0, 1200
+    eos = 2150
+    for trial in range(n):
+        V = (3072, 2048, 4096, 97, 1, 3072)[trial % 6]
+        top_k = (0, 1, 50, V - 1, V, 2 * V, 17)[trial % 7]
+        T = (0.7, 1.0, 1.3, 0.05)[trial % 4]
+        lg = (rng.standard_normal(V) * 2).astype(F32)
+        if trial % 5 == 0 and V > 10:  # ties around the threshold, -inf entries
+            lg[rng.integers(0, V, 30)] = lg.max()
+            lg[rng.integers(0, V, 5)] = -np.inf
+        if trial % 13 == 0 and V > 10:
+            lg[rng.integers(0, V, 3)] = np.nan
+        talker = trial % 3 == 0 and V == 3072
+        lgg = _t(lg, gpu)
+        if talker:
+            seen = rng.random(V) < 0.05
+            sup = np.zeros(V, bool)
+            sup[V - 1024:] = True
+            ngen_v = trial % 4
+            proc = O.process_logits(lg, seen, 1.05, sup, ngen_v, 2, eos)
+            ngen = torch.tensor([ngen_v], dtype=torch.int64, device=gpu)
+            fs(lgg, out, True, T, top_k, talker=dict(seen=_t(seen, gpu), rep_pen=1.05, suppress=_t(sup, gpu), ngen=ngen,
+                                                     min_new=2, eos=eos, id0=None, pos=None))
+        else:
+            proc = lg
+            fs(lgg, out, True, T, top_k)
+        torch.cuda.synchronize()
+        ref, g = O.sample_draw(proc, float(np.float32(1.0 / T)), top_k, seed, trial, exact=True)
+        pick = int(out)
+        if pick != ref:
+            if _near_tie(g, pick, ref):
+                ties += 1
+            else:
+                bad.append((trial, V, top_k, T, pick, ref))
+    assert int(fs.counter) == n
+    print(f"  {n} draws: {n - len(bad) - ties} identical, {ties} within rounding of a tie", flush=True)
+    assert not bad, bad[:5]
+    assert ties <= 2
+
+
+def test_sampled_pick_replays_from_a_graph(gpu):
+    """The draw counter lives in device memory: every replay of a captured pick draws the next number."""
+    from sokutou_amd.sampler import FusedSampler
+
+    fs = FusedSampler(gpu)
+    fs.set_seed(99)
+    V, top_k, T = 3072, 50, 0.9
+    lg = (np.random.default_rng(3).standard_normal(V) * 2).astype(F32)
+    lgg = _t(lg, gpu)
+    out = torch.zeros(1, dtype=torch.int64, device=gpu)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fs(lgg, out, True, T, top_k)  # counter 0
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fs(lgg, out, True, T, top_k)
+    torch.cuda.synchronize()
+    picks = []
+    for _ in range(40):
+        g.replay()
+        torch.cuda.synchronize()
+        picks.append(int(out))
+    ref = [O.sample_draw(lg, float(np.float32(1.0 / T)), top_k, 99, c)[0] for c in range(1, 41)]
+    assert picks == ref
+    assert int(fs.counter) == 41 and len(set(picks)) > 5

@@ -119,3 +119,45 @@ def test_generate_codes_loop(gpu):
     assert eng.stats["frame_limited"] and not eng.stats["stopped"]
     with pytest.raises(ValueError):
         eng.generate_codes(dict(kw, top_p=0.5))
+
+
+def test_sampled_generation_matches_oracle(gpu):
+    """do_sample with the talker processor through the fused sampler (qwen3/kernels.py:676-693, 709-713): the key
+    comes from torch's CPU generator, the counter is the frame index; every code equals the oracle's draw."""
+    from oracle import talker as O
+    from oracle.workload import talker_oracle
+    from sokutou_amd.fast import Sampling
+
+    smp = Sampling(do_sample=True, temperature=0.9, top_k=50, repetition_penalty=1.05, min_new_tokens=2,
+                   max_new_tokens=64)
+    name, seed = "tiny", 2
+    eng, tok = syn.make_engine(name, seed=seed, device=gpu, sampling=smp, suppress_tail=64, max_cache=60)
+    pos0 = syn.WORKLOADS[name]["kv"]
+    eng.capture()
+    kw = {"prefill_len": pos0, "first_token": tok, "do_sample": True, "temperature": 0.9, "top_k": 50,
+          "repetition_penalty": 1.05, "min_new_tokens": 2, "max_new_tokens": 64, "subtalker_dosample": True}
+    torch.manual_seed(1234)
+    codes = eng.generate_codes(kw, max_frames=20)[:, 0].tolist()
+    torch.manual_seed(1234)
+    key = int(torch.randint(0, 2**62, (1,)).item())
+    orc, otok, s = talker_oracle(name, seed, "i8row", max_len=60)
+    assert otok == tok
+    V, eos = s.vocab, eng.eos
+    sup = np.zeros(V, bool)
+    sup[V - 64:] = True
+    sup[eos] = False
+    seen = np.zeros(V, bool)
+    seen[tok] = True
+    ngen, t, ref = 1, tok, []
+    for f in range(20):
+        if t == eos:
+            break
+        ref.append(t)
+        lg = orc.logits(orc.forward(orc.w["emb"][t], pos0 + f))
+        v = O.process_logits(lg, seen, 1.05, sup, ngen, 2, eos)
+        t, _ = O.sample_draw(v, float(np.float32(1.0 / 0.9)), 50, key, f)
+        seen[t] = True
+        ngen += 1
+    print(f"sampled tiny: {len(codes)} frames, {len(set(codes))} distinct codes", flush=True)
+    assert codes == ref
+    assert len(set(codes)) > 3

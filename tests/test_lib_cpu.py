@@ -53,13 +53,16 @@ def test_attn_rejects_bad_head_ratio():
     assert rc == _lib.SK_EINVAL
 
 
-def test_sample_rejects_large_vocab_and_sampling():
+def test_sample_rejects_bad_arguments_without_launching():
     L = _lib.load()
     d = ctypes.c_void_p(256)
     assert L.sk_sample(d, 5000, 1.0, 0, 0, None, 1.0, None, None, 0, -1, None, None, d, 0, None, None, None) == _lib.SK_EINVAL
-    rc = L.sk_sample(d, 100, 1.0, 50, 1, None, 1.0, None, None, 0, -1, d, d, d, 0, None, None, None)
-    assert rc == _lib.SK_EUNSUPPORTED
-    with pytest.raises(NotImplementedError):
+    # sampling needs the device seed and counter, and a positive temperature
+    assert L.sk_sample(d, 100, 1.0, 50, 1, None, 1.0, None, None, 0, -1, None, d, d, 0, None, None, None) == _lib.SK_EINVAL
+    assert L.sk_sample(d, 100, 0.0, 50, 1, None, 1.0, None, None, 0, -1, d, d, d, 0, None, None, None) == _lib.SK_EINVAL
+    rc = L.sk_sample(d, 100, -2.0, 50, 1, None, 1.0, None, None, 0, -1, d, d, d, 0, None, None, None)
+    assert rc == _lib.SK_EINVAL
+    with pytest.raises(ValueError):
         _lib.check(rc, "sk_sample")
 
 
@@ -97,7 +100,7 @@ def test_batched_entry_points_reject_bad_shapes_without_launching():
     assert L.sk_bgemm(d, None, 0, 1e-6, d, d, 2048, 6144, 0, d, None, None, None, None, d, need - 256, None) == \
         _lib.SK_EWORKSPACE
     ws = L.sk_batch_workspace_size(2048, 6144, 16, 8, 3072)
-    assert ws > 16 * 8 * 2 * 64 * 130 * 4
+    assert ws > 16 * 8 * 2 * 32 * 130 * 4  # attention partials of 16 streams x 8 kv heads x 32 splits
     desc = _lib.SkBatchDesc(n_layers=28, hidden=2048, inter=6144, nq=16, nkv=8, vocab=3072, batch=17, max_len=2100)
     assert L.sk_batch_frame(ctypes.byref(desc), None) == _lib.SK_EINVAL  # batch > 16
     desc.batch = 16

@@ -409,3 +409,74 @@ def test_batch_workload_inputs_are_seeded():
     k2, _ = syn.batch_prefill(0, 1, 3, s, 9)
     assert k1.shape == (s.nkv, 9, 128) and not np.array_equal(k1, k2)
     assert np.array_equal(O.bf16_round(k1), k1) and abs(float(v1.std()) - 1.0) < 0.05
+
+
+# ---- sampled picks ------------------------------------------------------------------------------------------
+PHILOX_KAT = [  # Random123 kat_vectors, philox4x32_10: counter, key, output
+    ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF,) * 4, (0xFFFFFFFF, 0xFFFFFFFF), (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+def test_philox_known_answers():
+    for c, k, e in PHILOX_KAT:
+        r = O.philox4x32_10(np.array(c, dtype=np.uint32), np.array(k, dtype=np.uint32))
+        assert [int(x) for x in r] == list(e)
+    # broadcasting over many counters gives the same words as one at a time
+    ctr = np.array([[i, 7, 0, 0x51] for i in range(5)], dtype=np.uint32)
+    key = np.array([3, 4], dtype=np.uint32)
+    many = O.philox4x32_10(ctr, key)
+    for i in range(5):
+        assert np.array_equal(many[i], O.philox4x32_10(ctr[i], key))
+
+
+def test_order_key_and_topk_threshold_brute_force():
+    rng = np.random.default_rng(11)
+    v = np.concatenate([rng.standard_normal(300).astype(F32), np.array([0.0, -0.0, 1.5, 1.5, 1.5, -np.inf], F32)])
+    k = O.order_key(v)
+    by_key = v[np.argsort(k, kind="stable")].astype(np.float64)
+    assert np.all(np.diff(by_key) >= 0)  # keys follow the values (-0.0 sorts just below +0.0)
+    assert O.order_key(np.array([-0.0], F32))[0] + 1 == O.order_key(np.array([0.0], F32))[0]
+    for top_k in (1, 2, 5, 17, 100, 305, 306, 0, 400):
+        thr = O.topk_threshold(v, top_k)
+        if top_k <= 0 or top_k >= v.size:
+            assert thr == 0
+            continue
+        above = int((k > thr).sum())
+        at_least = int((k >= thr).sum())
+        assert above < top_k <= at_least  # thr is the key of the k-th largest entry, ties included
+
+
+def test_sample_draw_keep_rule():
+    v = np.array([1.0, 3.0, 3.0, -np.inf, 2.0, np.nan, 0.5], F32)
+    kept = set()
+    for c in range(300):
+        i, g = O.sample_draw(v, 1.0, 2, seed=5, counter=c)
+        kept.add(i)
+    # top_k = 2: the threshold is the key of 3.0, both 3.0 entries are kept; the NaN entry is never picked
+    assert kept == {1, 2}
+    kept = {O.sample_draw(v, 1.0, 0, 9, c)[0] for c in range(2000)}
+    assert 3 not in kept and 5 not in kept and kept <= {0, 1, 2, 4, 6}
+    assert O.sample_draw(np.full(4, -np.inf, F32), 1.0, 0, 1, 0)[0] == 0
+
+
+def test_sample_draw_law_matches_softmax_over_top_k():
+    """Gumbel-max over the kept entries is softmax sampling: the empirical frequencies of many draws (successive
+    counters) match softmax(v / T) restricted to the top k within a chi-square bound."""
+    from scipy.stats import chisquare
+
+    rng = np.random.default_rng(4)
+    v = (rng.standard_normal(40) * 1.5).astype(F32)
+    T, top_k, n = 0.8, 12, 6000
+    x = v * F32(1.0 / T)
+    keep = np.argsort(-x.astype(np.float64))[:top_k]
+    p = np.exp(x[keep].astype(np.float64) - float(x[keep].max()))
+    p = p / p.sum()
+    counts = np.zeros(v.size)
+    for c in range(n):
+        counts[O.sample_draw(v, 1.0 / T, top_k, seed=123, counter=c)[0]] += 1
+    assert counts.sum() == counts[keep].sum()
+    stat, pval = chisquare(counts[keep], p * n)
+    assert pval > 1e-3, (stat, pval)
