@@ -72,8 +72,9 @@ int sk_embed(const void* table, const int64_t* idx, float* out, int dim, int ct,
 int sk_talker_in(const uint64_t* tabs, const int64_t* codes, const void* pad, float* out, int dim, int G, int ct,
                  void* stream);
 
-/* Bytes of scratch that sk_attn needs for nkv kv heads and caches of max_len positions (split-K partials and
- * per-head arrival counters). The counters must be zero before the first call; sk_attn leaves them zero. */
+/* Bytes of scratch that sk_attn needs for nkv kv heads and caches of max_len positions (per-head arrival counters,
+ * then split-K partials). The counters must be zero before the first call; sk_attn leaves them zero. One workspace
+ * sized for the longest cache serves calls with any shorter max_len. */
 int64_t sk_attn_workspace_size(int nq, int nkv, int max_len);
 
 /* One-token GQA decode attention. qkv is [nq·128 | nkv·128 | nkv·128] fp32; for each kv head: per-head RMSNorm

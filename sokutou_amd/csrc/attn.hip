@@ -35,6 +35,10 @@ int nsplit_for(int max_len) {
   return n < 1 ? 1 : (n > kSplitMax ? kSplitMax : n);
 }
 int64_t part_bytes(int nkv, int nsplit) { return ((int64_t)nkv * 2 * nsplit * kPart * 4 + 255) / 256 * 256; }
+// Workspace: the per-head arrival counters first, at a fixed place for any cache length, then the partials, so
+// one workspace serves calls with different max_len (talker and code predictor) without a partial landing on a
+// counter.
+int64_t counter_bytes(int nkv) { return ((int64_t)nkv * 4 + 255) / 256 * 256; }
 
 // 8 consecutive cache elements as raw bits: one uint4 for bf16, two for f32
 template <int CT> struct Row8;
@@ -242,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ qkv
 extern "C" int64_t sk_attn_workspace_size(int nq, int nkv, int max_len) {
   if (nkv <= 0 || max_len <= 0) return 0;
   (void)nq;
-  return part_bytes(nkv, nsplit_for(max_len)) + (int64_t)nkv * 4;
+  return counter_bytes(nkv) + part_bytes(nkv, nsplit_for(max_len));
 }
 
 extern "C" int sk_attn(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc,
@@ -260,8 +264,8 @@ extern "C" int sk_attn(const float* qkv, const float* qn, const float* kn, float
   if (workspace_bytes < sk_attn_workspace_size(nq, nkv, max_len))
     return sk_set_error(SK_EWORKSPACE, "sk_attn: workspace too small");
   const int nsplit = nsplit_for(max_len);
-  float* part = (float*)workspace;
-  unsigned* counters = (unsigned*)((char*)workspace + part_bytes(nkv, nsplit));
+  unsigned* counters = (unsigned*)workspace;
+  float* part = (float*)((char*)workspace + counter_bytes(nkv));
   hipStream_t st = (hipStream_t)stream;
   dim3 grid(nkv, nsplit);
   if (ct == SK_CT_BF16)

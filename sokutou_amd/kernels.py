@@ -240,9 +240,6 @@ class Qwen3Kernels(Qwen3Fast):
             raise RuntimeError("Qwen3Kernels runs on a HIP device")
         with torch.cuda.device(self.device):
             _lib.check(L.sk_device_check(), "sk_device_check")
-        if self.cp is not None:
-            raise NotImplementedError("a talker frame fed by the code predictor (talker_in over 16 codes) is not part "
-                                      "of this engine yet; the code predictor alone runs on CodePredictor")
         t0 = time.perf_counter()
         self.wd = wd
         self.ct = "f32" if wd == "f32" else "bf16"
@@ -278,14 +275,101 @@ class Qwen3Kernels(Qwen3Fast):
         nbytes = int(L.sk_attn_workspace_size(P.nq, P.nkv, max_cache))
         self.attn_ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         self.trace: list[torch.Tensor] | None = None
+        if self.cp is not None:
+            self._setup_code_predictor(wd, cdt)
         # whole frames in one persistent launch (greedy decoding of the 0.6B / 1.7B talker shapes)
-        supported = (self.frame_kernel_supported() and sampler == "fused" and not self.s.do_sample)
+        supported = (self.frame_kernel_supported() and sampler == "fused" and not self.s.do_sample and self.cp is None)
         if frame_kernel and not supported:
             raise ValueError("frame_kernel=True needs greedy decoding, i8row weights, 16 q / 8 kv heads, vocab 3072, "
-                             "hidden 1024 or 2048 and a cache of at most 1024 (0.6B) / 2048 (1.7B) positions")
+                             "hidden 1024 or 2048, a cache of at most 1024 (0.6B) / 2048 (1.7B) positions and a talker "
+                             "without a code predictor")
         self.frame_kernel = supported if frame_kernel is None else bool(frame_kernel)
         if self.frame_kernel:
             self._setup_frame_kernel()
+
+    # --- the code predictor -----------------------------------------------------------------------------------
+    def _setup_code_predictor(self, wd: str, cdt) -> None:
+        """The code predictor's stack, heads, code tables and optional projection (qwen3/kernels.py:514-523), its
+        cache [layers, nkv, G, 128] and buffers. Greedy sub-codes on the 0.6B-shaped code predictor with no
+        projection run on the one-launch kernel (CodePredictor); anything else runs position by position on the
+        per-op kernels, as the reference does (qwen3/kernels.py:629-675)."""
+        cp, dev = self.cp, self.device
+        with torch.no_grad():
+            self.C = _Stack(cp.model, wd, self.G)
+            self.cp_heads = [_Lin(h.weight, wd) for h in cp.lm_head][: self.G - 1]
+            self.cemb = [e.weight.to(cdt).contiguous() for e in cp.get_input_embeddings()]
+            proj = getattr(cp, "small_to_mtp_projection", None)
+            self.proj = None
+            if proj is not None and not isinstance(proj, torch.nn.Identity):
+                bias = getattr(proj, "bias", None)
+                self.proj = (_Lin(proj.weight, wd), None if bias is None else bias.float().contiguous())
+        if len(self.cp_heads) != self.G - 1 or len(self.cemb) < self.G - 1:
+            raise ValueError(f"{self.G} code groups need {self.G - 1} heads and {self.G - 1} code tables")
+        for h in self.cp_heads:
+            h.pol = 1
+        # talker input tables: code 0 from the talker's table, code g >= 1 from code table g - 1
+        self.tabs = torch.tensor([self.temb.data_ptr()] + [e.data_ptr() for e in self.cemb[: self.G - 1]],
+                                 dtype=torch.int64, device=dev)
+        P = self.C
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.pad16 = torch.zeros(self.T.H, dtype=cdt, device=dev)  # tts_pad_embed, added to every talker input
+        self.hc = torch.zeros(P.H, **f32)
+        self.e = torch.zeros(self.T.H, **f32)
+        self.qkv_c = torch.zeros((P.nq + 2 * P.nkv) * HD, **f32)
+        self.att_c = torch.zeros(P.nq * HD, **f32)
+        self.act_c = torch.zeros(P.I, **f32)
+        self.logit_c = torch.zeros((1, self.cp_heads[0].N), **f32)
+        self.ck = torch.zeros((len(P.layers), P.nkv, self.G, HD), dtype=cdt, device=dev)
+        self.cv = torch.zeros_like(self.ck)
+        self.cpk: CodePredictor | None = None
+        fast = (not self.s.sub_do_sample and self.proj is None and wd == "i8row" and self.ct == "bf16"
+                and (P.H, P.I, P.nq, P.nkv, self.cp_heads[0].N) == (1024, 3072, 16, 8, 2048) and 2 <= self.G <= 64)
+        if fast:
+            self.cpk = CodePredictor(cp, self.temb, n_positions=self.G, wd=wd, device=dev)
+
+    def _cp_input(self, x) -> None:
+        """Code-predictor input from a talker-width fp32 vector: the projection (with its bias) or a copy
+        (qwen3/kernels.py:629-637)."""
+        if self.proj is None:
+            self.hc.copy_(x)
+        else:
+            self._gemv(x, self.proj[0], self.proj[1], self.hc, False)
+
+    def _cp_frame(self) -> None:
+        """Sub-codes 1..G-1 of the frame into ``codes`` from ph32 (the talker's last hidden state after its final
+        norm) and code 0 (qwen3/kernels.py:666-675 with _cp_first 641-655): position 0 takes ph32, position 1 the
+        talker embedding of code 0, position g >= 2 code table g - 2 at code g - 1; position g >= 1 ends in the final
+        norm, head g - 1 and a pick with the sub-code settings (no processor)."""
+        s, codes = self.s, self.codes
+        codes[:, :1].copy_(self.id0)
+        if self.cpk is not None:
+            self.cpk.x0.copy_(self.ph32)
+            self.cpk.id0.copy_(self.id0.view(1))
+            self.cpk.run()
+            codes[0, 1:].copy_(self.cpk.codes[1:])
+            return
+        P = self.C
+        cptr = codes.data_ptr()
+        for g in range(self.G):
+            if g == 0:
+                self._cp_input(self.ph32)
+            else:
+                self._embed(self.temb if g == 1 else self.cemb[g - 2], self.id0 if g == 1 else cptr + 8 * (g - 1),
+                            self.e)
+                self._cp_input(self.e)
+            self._layers(P, self.hc, self.qkv_c, self.att_c, self.act_c, list(self.ck.unbind(0)),
+                         list(self.cv.unbind(0)), None, g)
+            if g == 0:
+                continue
+            self._rms_gemv(self.hc, P.norm, P.eps, self.cp_heads[g - 1], self.logit_c, False)
+            if self.fs is not None:
+                self.fs(self.logit_c.view(-1), cptr + 8 * g, s.sub_do_sample, s.sub_temperature, s.sub_top_k)
+            else:
+                codes[:, g:g + 1].copy_(_sample(self.logit_c, s.sub_do_sample, s.sub_temperature, s.sub_top_k))
+
+    def _state(self):
+        base = super()._state()
+        return base + (self.ph32,) if self.cp is not None else base
 
     # --- the persistent frame kernel ------------------------------------------------------------------------
     def frame_kernel_supported(self) -> bool:
@@ -369,16 +453,26 @@ class Qwen3Kernels(Qwen3Fast):
 
     # --- one frame ----------------------------------------------------------------------------------------
     def _talker(self) -> None:
-        """embed(id0) -> layers -> final RMSNorm -> codec head (logits in ``logit_t``)."""
+        """Input -> layers -> final RMSNorm -> codec head (logits in ``logit_t``). The input is the embedding of
+        code 0, or, with a code predictor, the sum of the embeddings of the frame's G codes plus the pad embedding
+        (talker_in, qwen3/kernels.py:686-687)."""
         P = self.T
-        self._embed(self.temb, self.id0, self.ht)
+        if self.cp is not None:
+            p = _lib.ptr
+            _lib.call("sk_talker_in", p(self.tabs), p(self.codes), p(self.pad16), p(self.ht), P.H, self.G,
+                      _lib.CT[self.ct], _lib.stream())
+        else:
+            self._embed(self.temb, self.id0, self.ht)
         self._layers(P, self.ht, self.qkv_t, self.att_t, self.act_t, self.tk, self.tv, self.pos, 0)
         self._rmsnorm(self.ht, P.norm, P.eps, self.ph32)
         self._gemv(self.ph32, self.codec_head, None, self.logit_t, False)
 
     def _frame(self) -> None:
         s = self.s
-        self.codes[:, :1].copy_(self.id0)
+        if self.cp is not None:
+            self._cp_frame()
+        else:
+            self.codes[:, :1].copy_(self.id0)
         if self.frame_kernel:
             self.run_frames(1)
             return
@@ -417,8 +511,16 @@ class Qwen3Kernels(Qwen3Fast):
         self.pos.fill_(int(pos))
 
     def _start(self, kw: dict) -> int:
+        """Frame state after a prompt whose prefill ran elsewhere: ``prefill_len``, ``first_token`` and, with a code
+        predictor, ``last_hidden`` (the talker's last hidden state after its final norm, which the reference takes
+        from the prefill, qwen3/kernels.py:678-679) and ``tts_pad_embed`` (qwen3/kernels.py:709)."""
         if "inputs_embeds" in kw:
             raise NotImplementedError("prompt prefill through Hugging Face modules is not part of this engine")
+        if self.cp is not None:
+            if "last_hidden" in kw:
+                self.ph32.copy_(torch.as_tensor(kw["last_hidden"]).reshape(-1).to(self.ph32))
+            if "tts_pad_embed" in kw:
+                self.pad16.copy_(torch.as_tensor(kw["tts_pad_embed"]).reshape(-1).to(self.pad16))
         L = int(kw["prefill_len"])
         self.reset(L, int(kw["first_token"]))
         return L
@@ -444,4 +546,6 @@ class Qwen3Kernels(Qwen3Fast):
         return super().generate_codes(kw, max_frames=max_frames)
 
     def weight_bytes(self) -> dict:
-        return {"talker": self.T.bytes() + self.codec_head.bytes(), "code_predictor": 0, "cp_heads": 0}
+        cp = self.C.bytes() if self.cp is not None else 0
+        heads = sum(h.bytes() for h in self.cp_heads) if self.cp is not None else 0
+        return {"talker": self.T.bytes() + self.codec_head.bytes(), "code_predictor": cp, "cp_heads": heads}

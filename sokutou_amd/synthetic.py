@@ -215,6 +215,21 @@ def make_code_predictor(seed: int, s: TalkerShape, device="cpu", n_positions: in
     return cp, temb
 
 
+def make_tts_with_cp(seed: int, s: TalkerShape, cp_shape: TalkerShape, device="cpu", n_groups: int = 16):
+    """A ``tts`` whose talker carries a code predictor of ``cp_shape`` (n_groups - 1 heads and code tables; its
+    position 1 embeds code 0 with the talker's own table), as the reference reads a real Qwen3-TTS model
+    (qwen3/kernels.py:514-523). Returns (tts, pad row): the pad row is the bf16 ``tts_pad_embed`` added to every
+    talker input, N(0, 0.02)."""
+    tts = make_tts(seed, s, device=device)
+    w = cp_weights(seed, cp_shape, n_groups, talker_vocab=s.vocab)
+    w["temb"] = final_weights(seed, s)["emb"]
+    cp, _ = make_code_predictor(seed, cp_shape, device=device, n_positions=n_groups, w=w)
+    tts.model.talker.code_predictor = cp
+    tts.model.config.talker_config.num_code_groups = n_groups
+    pad = bf16_values(normal(seed, CP_FRAME0 - 1, "emb", (s.hidden,), 0.02))
+    return tts, pad
+
+
 # ---------------------------------------------------------------------------------------------------------
 # named workloads
 # ---------------------------------------------------------------------------------------------------------

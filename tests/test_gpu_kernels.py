@@ -113,8 +113,8 @@ def test_attention(gpu, ct, nkv, max_len, pos):
     mask[pos] = False
     np.testing.assert_array_equal(Kg[:, mask], Ko[:, mask])
     np.testing.assert_array_equal(Vg[:, mask], Vo[:, mask])
-    # arrival counters are back at zero (the tail of the workspace)
-    assert int(ws[-nkv * 4:].sum()) == 0
+    # arrival counters are back at zero (the head of the workspace)
+    assert int(ws[: nkv * 4].sum()) == 0
 
 
 def test_attention_invalid_position_writes_nothing(gpu):
@@ -314,3 +314,28 @@ def test_sampled_pick_replays_from_a_graph(gpu):
     ref = [O.sample_draw(lg, float(np.float32(1.0 / T)), top_k, 99, c)[0] for c in range(1, 41)]
     assert picks == ref
     assert int(fs.counter) == 41 and len(set(picks)) > 5
+
+
+def test_attention_workspace_shared_across_cache_lengths(gpu):
+    """One workspace for attention over caches of different lengths (a talker and its code predictor): the
+    counters sit at a fixed place, so a long call's partials never corrupt a short call's counters."""
+    nkv, nq = 8, 16
+    L = _lib.load()
+    ws = torch.zeros(int(L.sk_attn_workspace_size(nq, nkv, 1024)), dtype=torch.uint8, device=gpu)
+    rng = np.random.default_rng(12)
+    rope_np = O.rope_table(np.float32(1.0) / (1e6 ** (np.arange(0, 128, 2) / 128)).astype(np.float32), 1024)
+    rope = torch.from_numpy(rope_np).to(gpu)
+    qn = torch.from_numpy((1 + 0.1 * rng.standard_normal(128)).astype(F32)).to(gpu)
+    kn = torch.from_numpy((1 + 0.1 * rng.standard_normal(128)).astype(F32)).to(gpu)
+    for max_len, pos in ((1024, 700), (16, 9), (1024, 300), (16, 15), (80, 50), (16, 3)):
+        Kc = torch.from_numpy(O.bf16_round(rng.standard_normal((nkv, max_len, 128)).astype(F32))).to(gpu).to(torch.bfloat16)
+        Vc = torch.from_numpy(O.bf16_round(rng.standard_normal((nkv, max_len, 128)).astype(F32))).to(gpu).to(torch.bfloat16)
+        qkv = rng.standard_normal((nq + 2 * nkv) * 128).astype(F32)
+        Kr, Vr = Kc.float().cpu().numpy().copy(), Vc.float().cpu().numpy().copy()
+        ref = O.attention(qkv, qn.cpu().numpy(), kn.cpu().numpy(), 1e-6, rope_np, Kr, Vr, pos, nq, nkv)
+        out = torch.zeros(nq * 128, device=gpu)
+        p = _lib.ptr
+        _lib.call("sk_attn", p(torch.from_numpy(qkv).to(gpu)), p(qn), p(kn), 1e-6, p(rope), p(Kc), p(Vc), None, pos,
+                  max_len, nq, nkv, p(out), p(ws), ws.numel(), 0, _lib.stream())
+        torch.cuda.synchronize()
+        assert rel_err(out, ref) < 1e-5, (max_len, pos)

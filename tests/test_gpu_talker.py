@@ -161,3 +161,103 @@ def test_sampled_generation_matches_oracle(gpu):
     print(f"sampled tiny: {len(codes)} frames, {len(set(codes))} distinct codes", flush=True)
     assert codes == ref
     assert len(set(codes)) > 3
+
+
+def _full_frame_oracle(seed, frames, sub_sample=None, sample=None, key=0):
+    """Talker (2 layers of the 0.6B shape) + code predictor (5 layers, 2048-way heads) + talker_in, composed as the
+    reference's frame (qwen3/kernels.py:666-693): code predictor from (ph32, code 0), then the talker on the sum of
+    the 16 code embeddings plus the pad row. Picks greedy unless (temperature, top_k) are given for the sub-codes
+    / code 0; sampled picks share one draw counter in frame order, as the one fused sampler does."""
+    from oracle import talker as O
+    from oracle.workload import cp_oracle, talker_oracle
+
+    torc, tok, s = talker_oracle("small06b", seed, "i8row", max_len=80)
+    corc, cs = cp_oracle("cp06b", seed)
+    temb = torc.w["emb"]
+    corc.w["temb"] = temb
+    w = syn.cp_weights(seed, cs, 16, talker_vocab=s.vocab)
+    tabs = [temb] + [O.bf16_round(t) for t in w["cemb"]] + [np.zeros_like(temb[:2048])]
+    pad = syn.bf16_values(syn.normal(seed, syn.CP_FRAME0 - 1, "emb", (s.hidden,), 0.02))
+    ph32, _ = syn.cp_frame_inputs(seed, 0, s)
+    pos, t, cnt, out = syn.WORKLOADS["small06b"]["kv"], tok, 0, []
+    for f in range(frames):
+        if sub_sample is None:
+            codes = corc.frame(ph32, t)[0]
+        else:
+            codes = [t]
+            K = np.zeros((5, 8, 16, 128), np.float32)
+            V = np.zeros_like(K)
+            for g in range(16):
+                x = ph32 if g == 0 else (temb[codes[0]] if g == 1 else corc.w["cemb"][g - 2][codes[g - 1]])
+                h = np.asarray(x, np.float32)
+                for i, L in enumerate(corc.w["layers"]):
+                    h = O.decoder_layer(h, L, cs.eps, corc.w["rope"], K[i], V[i], g, cs.nq, cs.nkv)
+                if g == 0:
+                    continue
+                lg = O.rms_gemv(h, corc.w["norm"], cs.eps, corc.w["heads"][g - 1])
+                codes.append(O.sample_draw(lg, float(np.float32(1.0 / sub_sample[0])), sub_sample[1], key, cnt)[0])
+                cnt += 1
+        out.append(list(codes))
+        x = np.zeros(s.hidden, np.float32)
+        for g in range(16):
+            x = x + tabs[g][codes[g]]
+        x = x + pad
+        h = torc.forward(x, pos + f)
+        ph32 = O.rmsnorm(h, torc.w["norm"], s.eps)
+        lg = O.gemv(ph32, torc.w["head"])
+        if sample is None:
+            t = O.argmax_first(lg)
+        else:
+            t = O.sample_draw(lg, float(np.float32(1.0 / sample[0])), sample[1], key, cnt)[0]
+            cnt += 1
+    return out, tok, pad
+
+
+@pytest.mark.parametrize("mode", ["greedy", "sampled"])
+def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
+    """The reference's whole frame: 15 sub-codes from the code predictor (one launch for greedy sub-codes,
+    per-op positions with the fused sampler for sampled ones), then the talker on talker_in of all 16 codes."""
+    from sokutou_amd.fast import Sampling
+    from sokutou_amd.kernels import Qwen3Kernels
+
+    seed, F = 4, 6
+    s = syn.workload_shape("small06b")
+    cs = syn.workload_shape("cp06b")
+    tts, pad = syn.make_tts_with_cp(seed, s, cs, device=gpu)
+    if mode == "greedy":
+        smp = Sampling.greedy(processor=False, max_new_tokens=64)
+    else:
+        smp = Sampling(do_sample=True, temperature=0.9, top_k=50, repetition_penalty=1.0, min_new_tokens=0,
+                       max_new_tokens=64, sub_do_sample=True, sub_temperature=0.8, sub_top_k=40)
+    eng = Qwen3Kernels(tts, smp, max_cache=80, wd="i8row", sampler="fused", suppress_tail=0)
+    assert (eng.cpk is not None) == (mode == "greedy")
+    kv = syn.WORKLOADS["small06b"]["kv"]
+    for i in range(s.n_layers):
+        k, v = syn.kv_prefill(seed, i, s, kv)
+        eng.kc[i, :, :kv].copy_(torch.from_numpy(k).to(eng.kc.dtype))
+        eng.vc[i, :, :kv].copy_(torch.from_numpy(v).to(eng.vc.dtype))
+    tok = syn.start_token(seed, s)
+    ph32, _ = syn.cp_frame_inputs(seed, 0, s)
+    eng.reset(kv, tok)  # capture's warm-up frames write the cache at the current position: keep them past the prefill
+    eng.capture()
+    kw = {"prefill_len": kv, "first_token": tok, "last_hidden": torch.from_numpy(ph32), "tts_pad_embed": torch.from_numpy(pad),
+          "do_sample": smp.do_sample, "temperature": smp.temperature, "top_k": smp.top_k,
+          "repetition_penalty": smp.repetition_penalty, "min_new_tokens": smp.min_new_tokens, "max_new_tokens": 64,
+          "subtalker_dosample": smp.sub_do_sample, "subtalker_temperature": smp.sub_temperature,
+          "subtalker_top_k": smp.sub_top_k}
+    torch.manual_seed(77)
+    got = eng.generate_codes(kw, max_frames=F).cpu().tolist()
+    torch.manual_seed(77)
+    key = int(torch.randint(0, 2**62, (1,)).item())
+    print(f"full frame ({mode}): building the oracle", flush=True)
+    if mode == "greedy":
+        ref, otok, _ = _full_frame_oracle(seed, F)
+    else:
+        ref, otok, _ = _full_frame_oracle(seed, F, sub_sample=(0.8, 40), sample=(0.9, 50), key=key)
+    assert otok == tok
+    print(f"full frame ({mode}): {len(got)} frames x 16 codes; first {got[0][:6]}", flush=True)
+    bad = [(f, g, got[f][g], ref[f][g]) for f in range(len(got)) for g in range(16) if got[f][g] != ref[f][g]]
+    if bad:
+        print(f"  first mismatches (frame, group, gpu, oracle): {bad[:6]}", flush=True)
+    # the loop stops early only if code 0 is EOS (possible when sampling)
+    assert got == ref[: len(got)] and (len(got) == F or ref[len(got)][0] == eng.eos)
