@@ -151,6 +151,18 @@ typedef struct sk_talker_desc {
   float* layer_out;
   void* workspace;
   int64_t workspace_bytes;
+  /* Optional talker_in input (qwen3/kernels.py:328-336, 686-687), for a talker fed by a code predictor: when
+   * in_groups > 0 the frame's input is Σ_g in_tabs[g][in_codes[g]] + in_pad instead of the embedding row of id0
+   * (in_tabs: device array of in_groups bf16 tables [rows, hidden]; in_codes: device int64 [in_groups], code 0
+   * < vocab and the others < in_rows; in_pad: bf16 [hidden]). Needs n_frames == 1 (the next frame's codes come
+   * from the code predictor). final_out (optional, fp32 [hidden]) receives the frame's final residual after
+   * the final norm (the rmsnorm output the code predictor's position 0 takes). Zero / NULL when unused. */
+  const uint64_t* in_tabs;
+  const int64_t* in_codes;
+  const void* in_pad;
+  int in_groups;
+  int in_rows;
+  float* final_out;
 } sk_talker_desc;
 
 /* Bytes of workspace sk_talker_frames needs. It must be zero before the first call and must be zeroed again

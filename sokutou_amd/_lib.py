@@ -53,7 +53,9 @@ class SkTalkerDesc(ctypes.Structure):
                 ("rope", c_void_p), ("id0", c_void_p), ("pos", c_void_p), ("next_id0", c_void_p), ("out", c_void_p),
                 ("seen", c_void_p), ("ngen", c_void_p), ("suppress", c_void_p), ("rep_pen", c_float),
                 ("min_new", c_int), ("eos", c_int), ("talker_processor", c_int), ("logits", c_void_p),
-                ("layer_out", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_int64)]
+                ("layer_out", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_int64),
+                ("in_tabs", c_void_p), ("in_codes", c_void_p), ("in_pad", c_void_p), ("in_groups", c_int),
+                ("in_rows", c_int), ("final_out", c_void_p)]
 
 
 class SkCpDesc(ctypes.Structure):

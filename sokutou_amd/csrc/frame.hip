@@ -403,6 +403,19 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         if (CP && f == 0) {
 #pragma unroll
           for (int k = 0; k < H / 64; k++) ev[k] = gload(c.cp.x0 + lane + 64 * k);
+        } else if (!CP && c.d.in_groups > 0) {
+          // talker_in: the embedding rows of the frame's codes summed in group order, then the pad row
+#pragma unroll
+          for (int k = 0; k < H / 64; k++) ev[k] = 0.f;
+          for (int gi = 0; gi < c.d.in_groups; gi++) {
+            const bf16_t* tab = (const bf16_t*)uniform((const void*)gload(c.d.in_tabs + gi));
+            const int64_t code = gload(c.d.in_codes + gi);
+#pragma unroll
+            for (int k = 0; k < H / 64; k++) ev[k] += bf2f(gload(tab + (size_t)code * H + lane + 64 * k));
+          }
+          const bf16_t* pad = (const bf16_t*)c.d.in_pad;
+#pragma unroll
+          for (int k = 0; k < H / 64; k++) ev[k] += bf2f(gload(pad + lane + 64 * k));
         } else {
           const bf16_t* tab = CP ? (const bf16_t*)uniform(gload(c.cp.emb + f)) : emb;
 #pragma unroll
@@ -532,6 +545,11 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 #pragma unroll
     for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hin[lane + 64 * k] * nfin[k];
     if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[5] = !ok; }
+    if (!CP && c.d.final_out && c.g == 0 && ok) {  // the final norm's output, h * inv * w (rmsnorm)
+      const float inv = rsqrtf(ss / H + eps);
+#pragma unroll
+      for (int k = 0; k < H / 64; k++) gstore(c.d.final_out + lane + 64 * k, (S.hin[lane + 64 * k] * inv) * nfin[k]);
+    }
     wg_sync();
     if (!ok) return;
     wg_sync();  // candidates of the compute waves are in S.cand
@@ -911,7 +929,13 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     }
     // every position this launch writes must lie inside the cache, and the start token inside the vocabulary
     const int64_t pos0 = d.pos ? gload(d.pos) : 0, tok0 = gload(d.id0);
-    if (pos0 < 0 || pos0 + n_frames > d.max_len || tok0 < 0 || tok0 >= (CP ? cp.emb0_rows : d.vocab)) {
+    bool bad = pos0 < 0 || pos0 + n_frames > d.max_len || tok0 < 0 || tok0 >= (CP ? cp.emb0_rows : d.vocab);
+    if (!CP)
+      for (int gi = 0; gi < d.in_groups; gi++) {  // talker_in codes: code 0 in the talker vocabulary, the rest in in_rows
+        const int64_t cg = gload(d.in_codes + gi);
+        bad |= cg < 0 || cg >= (gi == 0 ? d.vocab : d.in_rows);
+      }
+    if (bad) {
       st_u32_dev(ws, Ws::kErr, 5u);
       r = -1;
     }
@@ -990,6 +1014,9 @@ extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* str
     return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: 1..32 layers");
   if (d->workspace_bytes < sk_talker_workspace_size(d->hidden, d->inter))
     return sk_set_error(SK_EWORKSPACE, "sk_talker_frames: workspace too small");
+  if (d->in_groups < 0 || d->in_groups > 64 ||
+      (d->in_groups > 0 && (!d->in_tabs || !d->in_codes || !d->in_pad || d->in_rows <= 0 || n_frames != 1)))
+    return sk_set_error(SK_EINVAL, "sk_talker_frames: talker_in input needs its tables, codes, pad, rows and one frame");
   int dev = 0, cus = 0;
   hipGetDevice(&dev);
   hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);

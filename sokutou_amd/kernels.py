@@ -278,11 +278,12 @@ class Qwen3Kernels(Qwen3Fast):
         if self.cp is not None:
             self._setup_code_predictor(wd, cdt)
         # whole frames in one persistent launch (greedy decoding of the 0.6B / 1.7B talker shapes)
-        supported = (self.frame_kernel_supported() and sampler == "fused" and not self.s.do_sample and self.cp is None)
+        supported = (self.frame_kernel_supported() and sampler == "fused" and not self.s.do_sample
+                     and (self.cp is None or self.cpk is not None))
         if frame_kernel and not supported:
             raise ValueError("frame_kernel=True needs greedy decoding, i8row weights, 16 q / 8 kv heads, vocab 3072, "
-                             "hidden 1024 or 2048, a cache of at most 1024 (0.6B) / 2048 (1.7B) positions and a talker "
-                             "without a code predictor")
+                             "hidden 1024 or 2048, a cache of at most 1024 (0.6B) / 2048 (1.7B) positions and, with a "
+                             "code predictor, greedy sub-codes on its one-launch kernel")
         self.frame_kernel = supported if frame_kernel is None else bool(frame_kernel)
         if self.frame_kernel:
             self._setup_frame_kernel()
@@ -397,11 +398,22 @@ class Qwen3Kernels(Qwen3Fast):
             rep_pen=s.repetition_penalty, min_new=s.min_new_tokens, eos=self.eos, talker_processor=int(proc),
             logits=self.logit_t.data_ptr(), layer_out=None, workspace=self.frame_ws.data_ptr(),
             workspace_bytes=self.frame_ws.numel())
+        if self.cp is not None:
+            # one frame per launch, fed by talker_in of the frame's codes; the final norm's output feeds the next
+            # frame's code predictor
+            self._desc.in_tabs = self.tabs.data_ptr()
+            self._desc.in_codes = self.codes.data_ptr()
+            self._desc.in_pad = self.pad16.data_ptr()
+            self._desc.in_groups = self.G
+            self._desc.in_rows = min(int(e.shape[0]) for e in self.cemb[: self.G - 1])
+            self._desc.final_out = self.ph32.data_ptr()
 
     def run_frames(self, n: int) -> None:
         """``n`` greedy frames in one launch of sk_talker_frames; the chosen ids land in ``frame_ids[:n]``."""
         if n > self.frame_ids.numel():
             raise ValueError("at most 4096 frames per launch")
+        if self.cp is not None and n != 1:
+            raise ValueError("with a code predictor each launch runs one talker frame")
         self._desc.layer_out = None if self.layer_out is None else self.layer_out.data_ptr()
         _lib.check(_lib.load().sk_talker_frames(ctypes.byref(self._desc), int(n), _lib.stream()), "sk_talker_frames")
 

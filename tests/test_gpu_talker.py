@@ -213,10 +213,11 @@ def _full_frame_oracle(seed, frames, sub_sample=None, sample=None, key=0):
     return out, tok, pad
 
 
-@pytest.mark.parametrize("mode", ["greedy", "sampled"])
+@pytest.mark.parametrize("mode", ["greedy", "greedy_frame_kernel", "sampled"])
 def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
     """The reference's whole frame: 15 sub-codes from the code predictor (one launch for greedy sub-codes,
-    per-op positions with the fused sampler for sampled ones), then the talker on talker_in of all 16 codes."""
+    per-op positions with the fused sampler for sampled ones), then the talker on talker_in of all 16 codes (per-op
+    kernels, or one launch of the persistent talker kernel fed by talker_in)."""
     from sokutou_amd.fast import Sampling
     from sokutou_amd.kernels import Qwen3Kernels
 
@@ -224,13 +225,14 @@ def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
     s = syn.workload_shape("small06b")
     cs = syn.workload_shape("cp06b")
     tts, pad = syn.make_tts_with_cp(seed, s, cs, device=gpu)
-    if mode == "greedy":
+    if mode.startswith("greedy"):
         smp = Sampling.greedy(processor=False, max_new_tokens=64)
     else:
         smp = Sampling(do_sample=True, temperature=0.9, top_k=50, repetition_penalty=1.0, min_new_tokens=0,
                        max_new_tokens=64, sub_do_sample=True, sub_temperature=0.8, sub_top_k=40)
-    eng = Qwen3Kernels(tts, smp, max_cache=80, wd="i8row", sampler="fused", suppress_tail=0)
-    assert (eng.cpk is not None) == (mode == "greedy")
+    eng = Qwen3Kernels(tts, smp, max_cache=80, wd="i8row", sampler="fused", suppress_tail=0,
+                       frame_kernel=mode == "greedy_frame_kernel")
+    assert (eng.cpk is not None) == mode.startswith("greedy")
     kv = syn.WORKLOADS["small06b"]["kv"]
     for i in range(s.n_layers):
         k, v = syn.kv_prefill(seed, i, s, kv)
@@ -250,7 +252,7 @@ def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
     torch.manual_seed(77)
     key = int(torch.randint(0, 2**62, (1,)).item())
     print(f"full frame ({mode}): building the oracle", flush=True)
-    if mode == "greedy":
+    if mode.startswith("greedy"):
         ref, otok, _ = _full_frame_oracle(seed, F)
     else:
         ref, otok, _ = _full_frame_oracle(seed, F, sub_sample=(0.8, 40), sample=(0.9, 50), key=key)
