@@ -1,6 +1,6 @@
 """Talker decode benchmark on one MI355X: frames/s of the 0.6B-shaped int8 talker at batch 1, KV 512.
 
-    python bench.py [--steps K] [--warmup W] [--workload talker06b|talker17b|cp06b|batch17b] [--engine frames|graph|multi] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload talker06b|talker17b|cp06b|batch17b|frame06b] [--engine frames|graph|multi] [--no-cpu]
 
 A step is one greedy decode run of 64 frames starting at KV length 512 (positions 512..575 are rewritten on
 every step, so every step does identical work). Each frame is embed -> 28 decoder layers (RMSNorm + qkv, q/k norm
@@ -14,6 +14,9 @@ the KV cache is bf16. Inputs are resident in HBM before timing starts.
 
 ``--workload batch17b`` measures the batched path: a step is one run of 32 greedy frames of 16 1.7B-shaped streams
 with ragged prior KV lengths (64..2048), each frame one HIP graph replay of sk_batch_frame (M=16 MFMA GEMMs).
+
+``--workload frame06b`` measures the whole Qwen3-TTS frame: the code predictor (15 greedy sub-codes, one launch)
+then the talker fed by talker_in of the 16 codes (one launch of the persistent kernel), 64 frames per step.
 
 ``--workload cp06b`` measures the code predictor instead: a step is 8 code-predictor frames, each one launch of
 sk_cp_frame over 16 positions (5 layers of the 0.6B shape, 15 greedy sub-codes from 2048-way heads).
@@ -384,6 +387,112 @@ def run_batch(args) -> None:
     print(json.dumps(res), flush=True)
 
 
+def run_frame(args) -> None:
+    """The whole frame (code predictor, then the talker on talker_in): one graph replay per frame, 64 frames per
+    step from KV 512; HIP events around both launches of every frame."""
+    import numpy as np
+    import torch
+
+    from sokutou_amd import synthetic as syn
+
+    dev = torch.device("cuda:0")
+    name = args.workload
+    spec = syn.WORKLOADS[name]
+    s, cs = syn.workload_shape(name), syn.workload_shape(spec["cp"])
+    F, kv = spec["frames"], spec["kv"]
+    t0 = time.perf_counter()
+    eng, tok, kw = syn.make_frame_engine(name, args.seed, dev)
+    if not eng.frame_kernel:
+        raise RuntimeError("the whole-frame bench expects the persistent talker kernel")
+    eng.capture()
+    setup_s = time.perf_counter() - t0
+
+    def run():
+        eng._start(kw)
+        for _ in range(F):
+            eng.graph.replay()
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    if eng.frame_error() or eng.cpk.error():
+        raise RuntimeError(f"frame kernel error {eng.frame_diag()} / code predictor {eng.cpk.error()}")
+    # per-launch durations: events around the code-predictor and the talker launch of every frame of one step
+    eng._start(kw)
+    ev_cp, ev_t = [], []
+    for _ in range(F):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        eng._cp_frame()
+        e[1].record()
+        eng.run_frames(1)
+        e[2].record()
+        ev_cp.append((e[0], e[1]))
+        ev_t.append((e[1], e[2]))
+    torch.cuda.synchronize()
+    cp_us = sum(a.elapsed_time(b) for a, b in ev_cp) * 1e3 / F
+    t_us = sum(a.elapsed_time(b) for a, b in ev_t) * 1e3 / F
+    fps = F * args.steps / dt
+    talker_b = sum(algorithmic_bytes(s, kv + 1 + f)["frame"] for f in range(F)) / F
+    cp_b = cp_algorithmic_bytes(cs, 16)["frame"]
+    frame_b = talker_b + cp_b
+    res = {
+        "metric": "whole Qwen3-TTS frame frames/sec (0.6B talker int8 KV 512 + 5-layer code predictor, 16 code groups)",
+        "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 weights x fp32 accumulate (bf16 KV cache)", "data": "synthetic",
+        "config": {"workload": f"{name}: talker {s.n_layers} layers hidden {s.hidden} KV {kv}, code predictor "
+                               f"{cs.n_layers} layers, 15 heads of {cs.vocab}, 16 code groups, {F} greedy frames per step, "
+                               "talker_in of 16 codes + pad", "engine": "Qwen3Kernels graph: sk_cp_frame + sk_talker_frames"},
+        "roofline": {"bound": "hbm", "kernel": "k_frames code-predictor mode (sk_cp_frame)",
+                     "achieved": round(cp_b / (cp_us * 1e-6) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(cp_b / (cp_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_launch": int(cp_b), "avg_launch_us": round(cp_us, 2)},
+        "frame": {"us_per_frame": round(1e6 / fps, 2), "code_predictor_us": round(cp_us, 2), "talker_us": round(t_us, 2),
+                  "algorithmic_bytes_per_frame": int(frame_b),
+                  "effective_GBs": round(frame_b * fps / 1e9, 1)},
+        "reference_published": {"ms_per_frame": 2.84, "setup": "RTX 6000 Ada, real Qwen3-TTS 0.6B weights (i8g32), "
+                                "sampled decoding (docs/results.md:212, 226); a different workload, so vs_baseline is null"},
+        "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu:
+        from oracle import talker as O
+        from oracle.workload import cp_oracle, talker_oracle
+
+        torc, otok, _ = talker_oracle(name, args.seed, "i8row", max_len=kv + F + 1)
+        corc, _ = cp_oracle(spec["cp"], args.seed)
+        corc.w["temb"] = torc.w["emb"]
+        w = syn.cp_weights(args.seed, cs, 16, talker_vocab=s.vocab)
+        tabs = [torc.w["emb"]] + list(w["cemb"]) + [np.zeros((cs.vocab, s.hidden), np.float32)]
+        pad = kw["tts_pad_embed"].numpy()
+        ph, t, times = kw["last_hidden"].numpy(), otok, []
+        t_start = time.perf_counter()
+        for f in range(F):
+            t1 = time.perf_counter()
+            codes = corc.frame(ph, t)[0]
+            x = np.zeros(s.hidden, np.float32)
+            for g in range(16):
+                x = x + tabs[g][codes[g]]
+            h = torc.forward(x + pad, kv + f)
+            ph = O.rmsnorm(h, torc.w["norm"], s.eps)
+            t = O.argmax_first(O.gemv(ph, torc.w["head"]))
+            times.append(time.perf_counter() - t1)
+            if time.perf_counter() - t_start > 20.0 and len(times) >= 3:
+                break
+        from threadpoolctl import threadpool_info
+        med = float(np.median(times[1:] if len(times) > 1 else times))
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        res["cpu_baseline"] = {"value": round(1.0 / med, 3), "unit": "frames/s", "cores": int(threads), "kind": "port",
+                               "sample": f"{len(times)} whole frames (median of all but the first, {med * 1e3:.0f} ms); numpy "
+                                         "fp32 over dequantised int8 weights", "host_cpus": os.cpu_count()}
+    print(json.dumps(res), flush=True)
+
+
 def cpu_baseline(name: str, seed: int, budget_s: float = 15.0) -> dict:
     """The numpy oracle on this host's cores: frames of the same workload until ~budget_s of frame time."""
     import numpy as np
@@ -419,7 +528,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="talker06b", choices=["talker06b", "talker17b", "cp06b", "batch17b"])
+    ap.add_argument("--workload", default="talker06b", choices=["talker06b", "talker17b", "cp06b", "batch17b", "frame06b"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--engine", default="frames", choices=["frames", "graph", "multi"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
@@ -437,6 +546,9 @@ def main() -> None:
         return
     if args.workload == "batch17b":
         run_batch(args)
+        return
+    if args.workload == "frame06b":
+        run_frame(args)
         return
 
     import torch

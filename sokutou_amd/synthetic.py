@@ -247,6 +247,9 @@ WORKLOADS = {
     # code predictor: 5 layers of the 0.6B shape, 2048-way heads, 16 positions (KV 1 -> 16) per frame, greedy
     # sub-codes; a step is `frames` code-predictor frames with different (x0, code 0)
     "cp06b": dict(shape="0.6b", n_layers=5, vocab=2048, kv=0, positions=16, frames=8),
+    # the whole Qwen3-TTS frame: the 0.6B talker (KV 512) fed by a 5-layer code predictor (16 code groups),
+    # 64 greedy frames
+    "frame06b": dict(shape="0.6b", n_layers=28, kv=512, frames=64, cp="cp06b"),
     # 16 concurrent 1.7B-shaped streams, prior KV lengths uniform in [64, 2048], 32 greedy frames
     "batch17b": dict(shape="1.7b", n_layers=28, kv=0, batch=16, kv_lo=64, kv_hi=2048, frames=32),
     # the same with two layers and five streams, for quick checks
@@ -286,6 +289,34 @@ def batch_prefill(seed: int, i: int, b: int, s: TalkerShape, T: int) -> tuple[np
 def batch_max_len(name: str, frames: int | None = None) -> int:
     w = WORKLOADS[name]
     return w["kv_hi"] + (w["frames"] if frames is None else frames) + 1
+
+
+def make_frame_engine(name: str = "frame06b", seed: int = 0, device="cuda", frame_kernel: bool | None = None):
+    """A Qwen3Kernels engine over the seeded synthetic talker with a code predictor (workload ``name``), greedy,
+    prior cache loaded, state at position ``kv``. Returns (engine, start token, kw) where kw holds the prefill
+    results ``generate_codes`` takes (``prefill_len``, ``first_token``, ``last_hidden``, ``tts_pad_embed``)."""
+    from .fast import Sampling
+    from .kernels import Qwen3Kernels
+
+    w = WORKLOADS[name]
+    s = workload_shape(name)
+    cs = workload_shape(w["cp"])
+    tts, pad = make_tts_with_cp(seed, s, cs, device=device)
+    eng = Qwen3Kernels(tts, Sampling.greedy(processor=False, max_new_tokens=4096), max_cache=w["kv"] + w["frames"] + 1,
+                       wd="i8row", sampler="fused", suppress_tail=0, frame_kernel=frame_kernel)
+    eng.talker = None
+    del tts
+    for i in range(s.n_layers):
+        k, v = kv_prefill(seed, i, s, w["kv"])
+        eng.kc[i, :, :w["kv"]].copy_(torch.from_numpy(k).to(eng.kc.dtype))
+        eng.vc[i, :, :w["kv"]].copy_(torch.from_numpy(v).to(eng.vc.dtype))
+    tok = start_token(seed, s)
+    x0, _ = cp_frame_inputs(seed, 0, s)
+    kw = {"prefill_len": w["kv"], "first_token": tok, "last_hidden": torch.from_numpy(x0), "tts_pad_embed": torch.from_numpy(pad),
+          "do_sample": False, "repetition_penalty": 1.0, "min_new_tokens": 0, "max_new_tokens": 4096,
+          "subtalker_dosample": False}
+    eng._start(kw)
+    return eng, tok, kw
 
 
 def make_batch_engine(name: str, seed: int = 0, device="cuda", frames: int | None = None, progress=None):
