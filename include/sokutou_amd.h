@@ -163,6 +163,15 @@ typedef struct sk_talker_desc {
   int in_groups;
   int in_rows;
   float* final_out;
+  /* Sampled picks (the draw of sk_sample with do_sample != 0): when do_sample != 0 each frame's pick is the
+   * Gumbel-max over the processed logits times inv_temp (> 0) that are at or above the top_k-th largest
+   * (top_k <= 0 keeps all), with Philox4x32-10 keyed by *seed and draw *counter + frame; *counter advances by
+   * the number of draws (device uint64). */
+  int do_sample;
+  float inv_temp;
+  int top_k;
+  const uint64_t* seed;
+  uint64_t* counter;
 } sk_talker_desc;
 
 /* Bytes of workspace sk_talker_frames needs. It must be zero before the first call and must be zeroed again
@@ -202,6 +211,13 @@ typedef struct sk_cp_desc {
   float* layer_out;           /* optional: [n_layers][hidden] residual after every layer at the last position */
   void* workspace;            /* sk_talker_workspace_size(hidden, inter) bytes, zeroed as for sk_talker_frames */
   int64_t workspace_bytes;
+  /* Sampled sub-codes (no processor): as sk_talker_desc; position g >= 1 draws with counter *counter + g - 1,
+   * and *counter advances by n_positions - 1. */
+  int do_sample;
+  float inv_temp;
+  int top_k;
+  const uint64_t* seed;
+  uint64_t* counter;
 } sk_cp_desc;
 
 /* All positions of the code predictor of one frame in ONE launch (the persistent kernel of sk_talker_frames in

@@ -55,7 +55,8 @@ class SkTalkerDesc(ctypes.Structure):
                 ("min_new", c_int), ("eos", c_int), ("talker_processor", c_int), ("logits", c_void_p),
                 ("layer_out", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_int64),
                 ("in_tabs", c_void_p), ("in_codes", c_void_p), ("in_pad", c_void_p), ("in_groups", c_int),
-                ("in_rows", c_int), ("final_out", c_void_p)]
+                ("in_rows", c_int), ("final_out", c_void_p), ("do_sample", c_int), ("inv_temp", c_float),
+                ("top_k", c_int), ("seed", c_void_p), ("counter", c_void_p)]
 
 
 class SkCpDesc(ctypes.Structure):
@@ -65,7 +66,8 @@ class SkCpDesc(ctypes.Structure):
                 ("layers", c_void_p), ("norm", c_void_p), ("rope", c_void_p), ("x0", c_void_p), ("id0", c_void_p),
                 ("emb0_rows", c_int), ("emb", c_void_p), ("head_w", c_void_p), ("head_s", c_void_p),
                 ("codes", c_void_p), ("logits", c_void_p), ("layer_out", c_void_p), ("workspace", c_void_p),
-                ("workspace_bytes", c_int64)]
+                ("workspace_bytes", c_int64), ("do_sample", c_int), ("inv_temp", c_float), ("top_k", c_int),
+                ("seed", c_void_p), ("counter", c_void_p)]
 
 
 class SkBatchDesc(ctypes.Structure):

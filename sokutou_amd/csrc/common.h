@@ -190,3 +190,30 @@ template <int POL = kPolDev>
 __device__ __forceinline__ void buf_stf(void* base, uint32_t off, float v) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), make_rsrc(base), off, 0, POL);
 }
+
+// ---- sampled picks ---------------------------------------------------------------------------------------------
+// Order-preserving key of an fp32 value (the sign bit set for positives, all bits flipped for negatives).
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): ten rounds of two 32x32->64-bit products with the published
+// multipliers, the high halves xored with the other counter words and the key, the key bumped by Weyl constants.
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; r++) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c.x, p1 = (uint64_t)0xCD9E8D57u * c.z;
+    c = make_uint4((uint32_t)(p1 >> 32) ^ c.y ^ k0, (uint32_t)p1, (uint32_t)(p0 >> 32) ^ c.w ^ k1, (uint32_t)p0);
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c;
+}
+// The Gumbel-perturbed value of entry i for draw `cnt` under key (k0, k1): v - log(-log(u)), u in (0, 1) from the
+// top 24 bits of the first Philox word of counter (i, draw lo, draw hi, 0x51).
+__device__ __forceinline__ float gumbel(float v, uint32_t i, uint64_t cnt, uint32_t k0, uint32_t k1) {
+  const uint4 r = philox4x32_10(make_uint4(i, (uint32_t)cnt, (uint32_t)(cnt >> 32), 0x51u), k0, k1);
+  const float u = ((float)(r.x >> 8) + 0.5f) * (1.0f / 16777216.0f);
+  return v - logf(-logf(u));
+}
+

@@ -93,7 +93,7 @@ struct Ws {
 };
 
 struct Layout {
-  uint32_t e1, e2, e3, e4, e5, e6, e7, total;  // cell offsets (in cells) from the cell base
+  uint32_t e1, e2, e3, e4, e5, e6, e7, e8, total;  // cell offsets (in cells) from the cell base
   __host__ __device__ Layout(int H, int I) {
     e1 = 0;                                    // qkv        [8][512]
     e2 = e1 + kNKV * 512;                      // partials   [8][32][260]
@@ -102,7 +102,8 @@ struct Layout {
     e5 = e4 + H;                               // act        [I]
     e6 = e5 + I;                               // h after down [H]
     e7 = e6 + H;                               // candidates [256][2]
-    total = e7 + kWG * 2;
+    e8 = e7 + kWG * 2;                         // processed logits of a sampled pick [vocab <= 3072]
+    total = e8 + kTalkerV;
   }
 };
 
@@ -112,6 +113,66 @@ struct Layout {
 static_assert(sizeof(sk_layer_desc) == 14 * sizeof(void*), "sk_layer_desc layout");
 
 namespace {
+
+// ---- sampled pick by one wave (the control wave), over V values staged in LDS --------------------------------
+// The key of the top_k-th largest value: a radix select over the four bytes of the order key, most significant
+// first (LDS histogram of the values matching the digits so far, then a wave scan of the bins from the top).
+// top_k <= 0 or >= V keeps everything (key 0). Same rule as the fused sampler's block-wide select.
+__device__ uint32_t topk_key_wave(const float* v, int V, int top_k, uint32_t* hist, int lane) {
+  if (top_k <= 0 || top_k >= V) return 0;
+  uint32_t prefix = 0, need = (uint32_t)top_k;
+  for (int pass = 0; pass < 4; pass++) {
+    const int shift = 24 - 8 * pass;
+    for (int b = lane; b < 256; b += 64) hist[b] = 0;
+    for (int i = lane; i < V; i += 64) {
+      const uint32_t k = order_key(v[i]);
+      if (pass == 0 || ((k ^ prefix) >> (shift + 8)) == 0) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+    }
+    uint32_t cnt[4], sum = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) { cnt[q] = hist[255 - (4 * lane + q)]; sum += cnt[q]; }
+    uint32_t inc = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(inc, o);
+      if (lane >= o) inc += y;
+    }
+    const uint32_t before = inc - sum;
+    const bool mine = before < need && inc >= need;  // exactly one lane: the counts from the top reach `need` there
+    uint32_t digit = 0, rest = 0;
+    if (mine) {
+      uint32_t acc = before;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        if (acc + cnt[q] >= need) { digit = 255u - (uint32_t)(4 * lane + q); rest = need - acc; break; }
+        acc += cnt[q];
+      }
+    }
+    const int src = __builtin_ctzll(__ballot(mine));
+    prefix |= (uint32_t)__shfl((int)digit, src) << shift;
+    need = (uint32_t)__shfl((int)rest, src);
+  }
+  return prefix;
+}
+// Gumbel-max over the values at or above `thr` that are not -inf (largest v - log(-log u), lowest index on ties);
+// every lane returns the pick, 0 if nothing is kept.
+__device__ int gumbel_pick_wave(const float* v, int V, uint32_t thr, uint64_t cnt, uint32_t k0, uint32_t k1, int lane) {
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = lane; i < V; i += 64) {
+    const float x = v[i];
+    if (order_key(x) < thr || x == -INFINITY) continue;
+    const float g = gumbel(x, (uint32_t)i, cnt, k0, k1);
+    if (g > best || (g == best && i < bi)) { best = g; bi = i; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ob = __shfl_xor(best, o);
+    const int oi = __shfl_xor(bi, o);
+    if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+  }
+  return bi == 0x7fffffff ? 0 : bi;
+}
 
 // Order-preserving key of (value, index): larger value wins, then the lower index.
 __device__ __forceinline__ uint64_t pick_key(float v, int i) {
@@ -154,6 +215,8 @@ struct Lds {
   float inv;
   sk_layer_desc desc[Ws::kTraceLayers];  // the layer descriptors, copied once per launch
   uint64_t cand[W];
+  float hv[16];        // this workgroup's processed logits (sampled picks)
+  uint32_t hist[256];  // radix-select histogram (sampled picks)
   int flags[8];
   int64_t tok;
   uint32_t pubseq;  // stage publications completed by the compute waves
@@ -291,6 +354,36 @@ __device__ __forceinline__ void after_publish(L& S, uint32_t seq, uint32_t delay
   sleep_units(delay);
 }
 
+// ---- control wave: sampled pick ---------------------------------------------------------------------------
+// Publishes this workgroup's `rows` processed logits (cells idx0 + rows g ..), waits until all V carry epoch e,
+// then draws: top_k threshold by radix select and Gumbel-max with Philox draw `draw` under key `seed`. Every
+// workgroup computes the same pick from the same V values. Returns the pick, -1 when the error word is set, -2 on
+// timeout. Kept out of line: inlined, its registers raise the pressure of the whole control loop.
+__device__ __attribute__((noinline)) int64_t sampled_pick(char* cells, uint32_t idx0, int V, int rows, int g,
+                                                          uint32_t e, const float* hv, float* xs, uint32_t* hist,
+                                                          int top_k, uint64_t draw, uint64_t seed, void* ws,
+                                                          uint32_t delay, int lane) {
+  if (lane < rows / 2) put2(cells, idx0 + (uint32_t)(rows * g + 2 * lane), hv[2 * lane], hv[2 * lane + 1], e);
+  sleep_units(delay);
+  for (uint32_t spin = 0;; spin++) {
+    bool ok = true;
+    for (int i = 2 * lane; i < V; i += 128) {
+      const u32x4 q = get2(cells, idx0 + (uint32_t)i);
+      ok &= q.y == e && q.w == e;
+      xs[i] = __uint_as_float(q.x);
+      xs[i + 1] = __uint_as_float(q.z);
+    }
+    if (__all(ok)) break;
+    if ((spin & 63) == 63) {
+      if (ld_u32_dev(ws, Ws::kErr) != 0) return -1;
+      if (spin > kSpinLimit) return -2;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  const uint32_t thr = topk_key_wave(xs, V, top_k, hist, lane);
+  return gumbel_pick_wave(xs, V, thr, draw, (uint32_t)seed, (uint32_t)(seed >> 32), lane);
+}
+
 // Position bookkeeping of a frame for this workgroup's attention chunk.
 struct Chunk {
   int T, pos, t0, n;
@@ -347,6 +440,7 @@ struct Ctx {
   int r, g;       // rank in the XCD, global workgroup index
   uint32_t base, tpf;
   int pos0, n_frames, L;
+  uint64_t seed, cnt0;  // sampled picks: Philox key and the draw counter at launch
   uint64_t* trace;  // per-stage timestamps of frame 0 (null when tracing is off)
   uint8_t dl[Ws::kHops];  // poll start delay of each exchange, sleep units
   __device__ void tr(int role, int f, int l, int ev) const {
@@ -552,7 +646,17 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     }
     wg_sync();
     if (!ok) return;
-    wg_sync();  // candidates of the compute waves are in S.cand
+    wg_sync();  // candidates (greedy) or processed logits (sampled) of the compute waves are in S.cand / S.hv
+    if (c.d.do_sample) {
+      // every workgroup publishes its processed logits and every control wave draws the same pick from all of them
+      const int64_t t = sampled_pick(c.cells, LY.e8, V, V / kWG, c.g, c.tick(f, c.L, 1), S.hv, S.xs[1], S.hist,
+                                     c.d.top_k, c.cnt0 + (uint64_t)(CP ? f - 1 : f), c.seed, c.ws,
+                                     c.dl[Ws::kHopPick], lane);
+      ok = t >= 0;
+      if (ok) tok = t;
+      else if (t == -2 && lane == 0) fail(c, 19u, f, c.L);
+      if (lane == 0) { S.tok = tok; S.flags[6] = !ok; }
+    } else {
     if (lane == 0) {
       uint64_t best = 0;
       for (int i = 0; i < W; i++) best = S.cand[i] > best ? S.cand[i] : best;
@@ -591,6 +695,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       tok = best ? (int64_t)(0xffffffffu - (uint32_t)best) : 0;
       if (lane == 0) { S.tok = tok; S.flags[6] = !ok; }
     }
+    }
     wg_sync();
     if (!ok) return;
     if (c.g == 0 && lane == 0) {
@@ -611,6 +716,8 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if (c.d.ngen) gstore(c.d.ngen, gload(c.d.ngen) + (int64_t)c.n_frames);
     }
   }
+  if (c.d.do_sample && c.g == 0 && lane == 0 && ld_u32_dev(c.ws, Ws::kErr) == 0)
+    gstore(c.d.counter, c.cnt0 + (uint64_t)(CP ? c.n_frames - 1 : c.n_frames));
 }
 
 // ================================================================================================================
@@ -894,7 +1001,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
             if (c.d.suppress && gload(c.d.suppress + row)) v = -INFINITY;
             if (block_eos && row == c.d.eos) v = -INFINITY;
           }
-          if (v == v) { const uint64_t k = pick_key(v, row); best = k > best ? k : best; }
+          if (c.d.do_sample) S.hv[row - C::kHeadRows * g] = v * c.d.inv_temp;
+          else if (v == v) { const uint64_t k = pick_key(v, row); best = k > best ? k : best; }
         }
         S.cand[cw] = best;
       }
@@ -959,6 +1067,9 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   c.base = s_base;
   c.tpf = (uint32_t)d.n_layers * 8u + 8u;
   c.pos0 = d.pos ? (int)gload(d.pos) : 0;
+  // read before this workgroup publishes anything: workgroup 0 advances the counter once every pick is done
+  c.seed = d.do_sample ? gload(d.seed) : 0;
+  c.cnt0 = d.do_sample ? gload(d.counter) : 0;
   c.n_frames = n_frames;
   c.L = d.n_layers;
   for (int i = tid; i < d.n_layers * (int)(sizeof(sk_layer_desc) / 8); i += blockDim.x)
@@ -1017,6 +1128,8 @@ extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* str
   if (d->in_groups < 0 || d->in_groups > 64 ||
       (d->in_groups > 0 && (!d->in_tabs || !d->in_codes || !d->in_pad || d->in_rows <= 0 || n_frames != 1)))
     return sk_set_error(SK_EINVAL, "sk_talker_frames: talker_in input needs its tables, codes, pad, rows and one frame");
+  if (d->do_sample && (!d->seed || !d->counter || !(d->inv_temp > 0.f)))
+    return sk_set_error(SK_EINVAL, "sk_talker_frames: sampling needs seed, counter and inv_temp > 0");
   int dev = 0, cus = 0;
   hipGetDevice(&dev);
   hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -1041,6 +1154,8 @@ extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
     return sk_set_error(SK_EINVAL, "sk_cp_frame: null pointer");
   if (d->workspace_bytes < sk_talker_workspace_size(d->hidden, d->inter))
     return sk_set_error(SK_EWORKSPACE, "sk_cp_frame: workspace too small");
+  if (d->do_sample && (!d->seed || !d->counter || !(d->inv_temp > 0.f)))
+    return sk_set_error(SK_EINVAL, "sk_cp_frame: sampling needs seed, counter and inv_temp > 0");
   int dev = 0, cus = 0;
   hipGetDevice(&dev);
   hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -1051,6 +1166,7 @@ extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
   t.layers = d->layers; t.norm = d->norm; t.rope = d->rope; t.id0 = const_cast<int64_t*>(d->id0);
   t.out = d->codes; t.rep_pen = 1.f; t.eos = -1; t.talker_processor = 0;
   t.logits = d->logits; t.layer_out = d->layer_out; t.workspace = d->workspace; t.workspace_bytes = d->workspace_bytes;
+  t.do_sample = d->do_sample; t.inv_temp = d->inv_temp; t.top_k = d->top_k; t.seed = d->seed; t.counter = d->counter;
   const CpArgs cp{d->x0, d->emb, d->head_w, d->head_s, d->emb0_rows};
   return launch_frames<1024, 3072, 4, 2048, true>(&t, cp, d->n_positions, (hipStream_t)stream);
 }

@@ -104,23 +104,6 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_greedy(const float* _
 }
 
 // ---- sampled pick: processor, temperature, top-k threshold, Gumbel-max (qwen3/sampler.py:37-159) -----------------
-__device__ __forceinline__ uint32_t order_key(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): ten rounds of two 32x32->64-bit products with the published
-// multipliers, the high halves xored with the other counter words and the key, the key bumped by Weyl constants.
-__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint32_t k0, uint32_t k1) {
-#pragma unroll
-  for (int r = 0; r < 10; r++) {
-    const uint64_t p0 = (uint64_t)0xD2511F53u * c.x, p1 = (uint64_t)0xCD9E8D57u * c.z;
-    c = make_uint4((uint32_t)(p1 >> 32) ^ c.y ^ k0, (uint32_t)p1, (uint32_t)(p0 >> 32) ^ c.w ^ k1, (uint32_t)p0);
-    k0 += 0x9E3779B9u;
-    k1 += 0xBB67AE85u;
-  }
-  return c;
-}
-
 // One block of 1024 threads, 4 entries per thread. The top_k-th largest key is found by a radix select over the
 // four bytes of the order key, most significant first: a 256-bin LDS histogram of the entries that match the
 // digits chosen so far, then one wave scans the bins from the top to find the digit where the count reaches the
@@ -212,10 +195,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_draw(const float* __r
     if (i >= V) continue;
     const float v = l[j];
     if (order_key(v) < thr || v == -INFINITY) continue;
-    const uint4 r = philox4x32_10(make_uint4((uint32_t)i, (uint32_t)cnt, (uint32_t)(cnt >> 32), 0x51u), (uint32_t)sd,
-                                  (uint32_t)(sd >> 32));
-    const float u = ((float)(r.x >> 8) + 0.5f) * (1.0f / 16777216.0f);
-    const float g = v - logf(-logf(u));
+    const float g = gumbel(v, (uint32_t)i, cnt, (uint32_t)sd, (uint32_t)(sd >> 32));
     if (g > best || (g == best && i < bi)) { best = g; bi = i; }
   }
 #pragma unroll

@@ -141,7 +141,8 @@ class CodePredictor:
     ``cp.get_input_embeddings()`` (table g - 2 embeds code g - 1 at position g). The loop is the reference's
     (qwen3/kernels.py:666-675 with ``_cp_first`` 641-655): position 0 takes the talker's last hidden state,
     position 1 the talker embedding row of code 0, position g >= 2 the embedding of code g - 1; each position
-    g >= 1 ends in the final RMSNorm, head g - 1 and a greedy pick. Greedy sub-codes only."""
+    g >= 1 ends in the final RMSNorm, head g - 1 and a pick: greedy, or after ``set_sampling`` the fused
+    sampler's draw (temperature, top_k, Philox seed and counter in device memory; one draw per position g >= 1)."""
 
     def __init__(self, cp, temb: torch.Tensor, n_positions: int = 16, wd: str = "i8row", device=None):
         if wd != "i8row":
@@ -184,6 +185,19 @@ class CodePredictor:
             codes=self.codes.data_ptr(), logits=self.logits.data_ptr(), layer_out=None,
             workspace=self.ws.data_ptr(), workspace_bytes=self.ws.numel())
         self.graph: torch.cuda.CUDAGraph | None = None
+
+    def set_sampling(self, temperature: float, top_k: int, seed: torch.Tensor, counter: torch.Tensor) -> None:
+        """Sampled sub-codes from here on: position g >= 1 draws with counter ``counter + g - 1`` under key
+        ``seed`` (device int64 tensors, as the fused sampler keeps them), and ``counter`` advances by
+        ``n_positions - 1`` per frame. Call before ``capture``: a graph keeps the settings it was recorded with."""
+        if not temperature > 0:
+            raise ValueError("temperature must be positive")
+        self._desc.do_sample = 1
+        self._desc.inv_temp = 1.0 / float(temperature)
+        self._desc.top_k = int(top_k or 0)
+        self._seed, self._counter = seed, counter  # keep the tensors alive
+        self._desc.seed = seed.data_ptr()
+        self._desc.counter = counter.data_ptr()
 
     def run(self) -> None:
         """One frame on the current stream: reads ``x0`` and ``id0``, writes ``codes`` (and ``logits`` of the
@@ -277,13 +291,13 @@ class Qwen3Kernels(Qwen3Fast):
         self.trace: list[torch.Tensor] | None = None
         if self.cp is not None:
             self._setup_code_predictor(wd, cdt)
-        # whole frames in one persistent launch (greedy decoding of the 0.6B / 1.7B talker shapes)
-        supported = (self.frame_kernel_supported() and sampler == "fused" and not self.s.do_sample
+        # whole frames in one persistent launch (0.6B / 1.7B talker shapes; greedy or the fused sampler's draw)
+        supported = (self.frame_kernel_supported() and sampler == "fused"
                      and (self.cp is None or self.cpk is not None))
         if frame_kernel and not supported:
-            raise ValueError("frame_kernel=True needs greedy decoding, i8row weights, 16 q / 8 kv heads, vocab 3072, "
+            raise ValueError("frame_kernel=True needs the fused sampler, i8row weights, 16 q / 8 kv heads, vocab 3072, "
                              "hidden 1024 or 2048, a cache of at most 1024 (0.6B) / 2048 (1.7B) positions and, with a "
-                             "code predictor, greedy sub-codes on its one-launch kernel")
+                             "code predictor, its one-launch kernel (no projection)")
         self.frame_kernel = supported if frame_kernel is None else bool(frame_kernel)
         if self.frame_kernel:
             self._setup_frame_kernel()
@@ -323,10 +337,13 @@ class Qwen3Kernels(Qwen3Fast):
         self.ck = torch.zeros((len(P.layers), P.nkv, self.G, HD), dtype=cdt, device=dev)
         self.cv = torch.zeros_like(self.ck)
         self.cpk: CodePredictor | None = None
-        fast = (not self.s.sub_do_sample and self.proj is None and wd == "i8row" and self.ct == "bf16"
-                and (P.H, P.I, P.nq, P.nkv, self.cp_heads[0].N) == (1024, 3072, 16, 8, 2048) and 2 <= self.G <= 64)
+        fast = ((not self.s.sub_do_sample or self.fs is not None) and self.proj is None and wd == "i8row"
+                and self.ct == "bf16" and (P.H, P.I, P.nq, P.nkv, self.cp_heads[0].N) == (1024, 3072, 16, 8, 2048)
+                and 2 <= self.G <= 64)
         if fast:
             self.cpk = CodePredictor(cp, self.temb, n_positions=self.G, wd=wd, device=dev)
+            if self.s.sub_do_sample:  # the fused sampler's draws, in the same order as position by position
+                self.cpk.set_sampling(self.s.sub_temperature, self.s.sub_top_k, self.fs.seed, self.fs.counter)
 
     def _cp_input(self, x) -> None:
         """Code-predictor input from a talker-width fp32 vector: the projection (with its bias) or a copy
@@ -398,6 +415,12 @@ class Qwen3Kernels(Qwen3Fast):
             rep_pen=s.repetition_penalty, min_new=s.min_new_tokens, eos=self.eos, talker_processor=int(proc),
             logits=self.logit_t.data_ptr(), layer_out=None, workspace=self.frame_ws.data_ptr(),
             workspace_bytes=self.frame_ws.numel())
+        if s.do_sample:  # the fused sampler's draw: one counter step per frame, seed and counter shared with it
+            self._desc.do_sample = 1
+            self._desc.inv_temp = 1.0 / s.temperature
+            self._desc.top_k = int(s.top_k or 0)
+            self._desc.seed = self.fs.seed.data_ptr()
+            self._desc.counter = self.fs.counter.data_ptr()
         if self.cp is not None:
             # one frame per launch, fed by talker_in of the frame's codes; the final norm's output feeds the next
             # frame's code predictor
@@ -409,7 +432,7 @@ class Qwen3Kernels(Qwen3Fast):
             self._desc.final_out = self.ph32.data_ptr()
 
     def run_frames(self, n: int) -> None:
-        """``n`` greedy frames in one launch of sk_talker_frames; the chosen ids land in ``frame_ids[:n]``."""
+        """``n`` frames in one launch of sk_talker_frames; the chosen ids land in ``frame_ids[:n]``."""
         if n > self.frame_ids.numel():
             raise ValueError("at most 4096 frames per launch")
         if self.cp is not None and n != 1:
@@ -420,7 +443,8 @@ class Qwen3Kernels(Qwen3Fast):
     def frame_error(self) -> int:
         """Error word of the frame kernel's workspace (0 when healthy; reads device memory, so it synchronises).
         Codes: 2 placement, 5 position/token out of range, 11..18 a poll of stage S1, S2, S3, S4, S5, S6, head,
-        pick timed out (``frame_diag`` tells the frame, layer and workgroup)."""
+        pick timed out, 19 the exchange of a sampled pick timed out (``frame_diag`` tells the frame, layer and
+        workgroup)."""
         return int(self.frame_ws[:4].view(torch.int32).item())
 
     def frame_diag(self) -> dict:

@@ -136,3 +136,92 @@ def test_talker17b_64_frames_one_launch(gpu):
     codes = [meta["codes"][0]] + eng.frame_ids[:63].cpu().tolist()
     assert codes == meta["codes"]
     assert rel_err(eng.logit_t.view(-1), gold["logits_last"]) < TOL
+
+
+def _sampled_engine(gpu, top_k, seed=2, name="small06b", frames=24):
+    from sokutou_amd.fast import Sampling
+
+    smp = Sampling(do_sample=True, temperature=0.9, top_k=top_k, repetition_penalty=1.05, min_new_tokens=2,
+                   max_new_tokens=64)
+    eng, tok = syn.make_engine(name, seed=seed, wd="i8row", device=gpu, frame_kernel=True, sampling=smp,
+                               suppress_tail=64, frames=frames)
+    assert eng.frame_kernel
+    return eng, tok
+
+
+def _sampled_oracle(name, seed, tok, key, frames, top_k, eos, cnt0=0):
+    """Codes of ``frames`` sampled frames: processor (repetition penalty 1.05 on the seen ids, the last 64 ids but
+    EOS suppressed, EOS blocked while fewer than 2 codes exist), temperature 0.9, top_k, draw cnt0 + f."""
+    from oracle import talker as O
+    from oracle.workload import talker_oracle
+
+    orc, otok, s = talker_oracle(name, seed, "i8row", max_len=syn.WORKLOADS[name]["kv"] + frames + 1)
+    assert otok == tok
+    V = s.vocab
+    sup = np.zeros(V, bool)
+    sup[V - 64:] = True
+    sup[eos] = False
+    seen = np.zeros(V, bool)
+    seen[tok] = True
+    pos, t, out = syn.WORKLOADS[name]["kv"], tok, []
+    for f in range(frames):
+        lg = orc.logits(orc.forward(orc.w["emb"][t], pos + f))
+        v = O.process_logits(lg, seen, 1.05, sup, 1 + f, 2, eos)
+        t, _ = O.sample_draw(v, float(np.float32(1.0 / 0.9)), top_k, key, cnt0 + f)
+        seen[t] = True
+        out.append(t)
+    return out
+
+
+@pytest.mark.parametrize("top_k", [50, 0, 1])
+def test_sampled_frames_one_launch_against_oracle(gpu, top_k):
+    """Sampled picks inside the persistent kernel: 24 frames in one launch with the talker processor, every code
+    equal to the oracle's draw (Philox key from torch's generator, draw counter = frame index); top_k 0 keeps the
+    whole vocabulary, top_k 1 reduces to the argmax of the processed logits. The counter advances by the frames."""
+    F = 24
+    print(f"small06b: {F} sampled frames (top_k {top_k}) in one launch against the oracle", flush=True)
+    eng, tok = _sampled_engine(gpu, top_k, frames=F)
+    torch.manual_seed(5 + top_k)
+    key = int(torch.randint(0, 2**62, (1,)).item())
+    eng.fs.set_seed(key)
+    eng.run_frames(F)
+    torch.cuda.synchronize()
+    assert eng.frame_error() == 0, eng.frame_diag()
+    codes = eng.frame_ids[:F].cpu().tolist()
+    ref = _sampled_oracle("small06b", 2, tok, key, F, top_k, eng.eos)
+    print(f"  codes {codes[:8]}..., {len(set(codes))} distinct", flush=True)
+    assert codes == ref
+    assert int(eng.fs.counter.item()) == F
+    assert int(eng.ngen.item()) == 1 + F and int(eng.pos.item()) == syn.WORKLOADS["small06b"]["kv"] + F
+    assert int(eng.next_id0.item()) == ref[-1]
+    if top_k != 1:
+        assert len(set(codes)) > 3
+
+
+def test_sampled_frames_split_launches_and_graph_replay(gpu):
+    """The same sampled run as 1 + 7 + 16 frames over three launches, and as 24 replays of a captured one-frame
+    launch: the counter carries the draws across launches, so the codes equal one launch of 24."""
+    F, key = 24, 0x1234_5678_9ABC_DEF
+    eng, tok = _sampled_engine(gpu, 50, frames=F)
+    ref = _sampled_oracle("small06b", 2, tok, key, F, 50, eng.eos)
+    print("small06b: sampled frames over launches of 1, 7 and 16", flush=True)
+    eng.fs.set_seed(key)
+    got = []
+    for n in (1, 7, 16):
+        eng.run_frames(n)
+        got += eng.frame_ids[:n].cpu().tolist()
+    assert eng.frame_error() == 0, eng.frame_diag()
+    assert got == ref and int(eng.fs.counter.item()) == F
+    print("small06b: captured sampled frame replayed 24 times", flush=True)
+    e2, tok2 = _sampled_engine(gpu, 50, frames=F)
+    e2.capture()
+    e2.kc.copy_(eng.kc)  # positions >= kv are rewritten by the replays
+    e2.vc.copy_(eng.vc)
+    e2.reset(syn.WORKLOADS["small06b"]["kv"], tok2)
+    e2.fs.set_seed(key)
+    codes = []
+    for _ in range(F):
+        e2.graph.replay()
+        codes.append(int(e2.next_id0.item()))
+    assert e2.frame_error() == 0, e2.frame_diag()
+    assert codes == ref

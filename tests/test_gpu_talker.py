@@ -213,11 +213,13 @@ def _full_frame_oracle(seed, frames, sub_sample=None, sample=None, key=0):
     return out, tok, pad
 
 
-@pytest.mark.parametrize("mode", ["greedy", "greedy_frame_kernel", "sampled"])
+@pytest.mark.parametrize("mode", ["greedy", "greedy_frame_kernel", "sampled_per_op", "sampled",
+                                  "sampled_frame_kernel"])
 def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
-    """The reference's whole frame: 15 sub-codes from the code predictor (one launch for greedy sub-codes,
-    per-op positions with the fused sampler for sampled ones), then the talker on talker_in of all 16 codes (per-op
-    kernels, or one launch of the persistent talker kernel fed by talker_in)."""
+    """The reference's whole frame: 15 sub-codes from the code predictor (one launch, greedy or with the fused
+    sampler's draws inside it; ``sampled_per_op`` runs its positions on the per-op kernels and the fused sampler),
+    then the talker on talker_in of all 16 codes (per-op kernels, or one launch of the persistent talker kernel fed
+    by talker_in, greedy or sampled). The one draw counter runs through sub-codes and code 0 in frame order."""
     from sokutou_amd.fast import Sampling
     from sokutou_amd.kernels import Qwen3Kernels
 
@@ -231,8 +233,10 @@ def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
         smp = Sampling(do_sample=True, temperature=0.9, top_k=50, repetition_penalty=1.0, min_new_tokens=0,
                        max_new_tokens=64, sub_do_sample=True, sub_temperature=0.8, sub_top_k=40)
     eng = Qwen3Kernels(tts, smp, max_cache=80, wd="i8row", sampler="fused", suppress_tail=0,
-                       frame_kernel=mode == "greedy_frame_kernel")
-    assert (eng.cpk is not None) == mode.startswith("greedy")
+                       frame_kernel=mode.endswith("frame_kernel"))
+    assert eng.cpk is not None
+    if mode == "sampled_per_op":
+        eng.cpk = None  # the code predictor's positions on the per-op kernels
     kv = syn.WORKLOADS["small06b"]["kv"]
     for i in range(s.n_layers):
         k, v = syn.kv_prefill(seed, i, s, kv)

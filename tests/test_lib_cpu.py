@@ -107,3 +107,25 @@ def test_batched_entry_points_reject_bad_shapes_without_launching():
     assert L.sk_batch_frame(ctypes.byref(desc), None) == _lib.SK_EINVAL  # null pointers
     desc.max_len = 5000
     assert L.sk_batch_embed(ctypes.byref(desc), None) == _lib.SK_EINVAL  # cache longer than the attention supports
+
+
+def test_frame_kernels_reject_sampling_without_seed_or_temperature():
+    """Sampled picks inside the persistent kernels need the device seed and counter and inv_temp > 0; the
+    checks run before the kernel is launched (and before the device is queried)."""
+    L = _lib.load()
+    d = ctypes.c_void_p(256)
+    ws = int(L.sk_talker_workspace_size(1024, 3072))
+    t = _lib.SkTalkerDesc(n_layers=2, hidden=1024, inter=3072, nq=16, nkv=8, vocab=3072, max_len=64,
+                          wd=_lib.WD["i8row"], ct=_lib.CT["bf16"], eps=1e-6, layers=d, norm=d, head_w=d, head_s=d,
+                          emb=d, rope=d, id0=d, pos=d, workspace=d, workspace_bytes=ws, do_sample=1, inv_temp=1.0,
+                          top_k=50, seed=None, counter=d)
+    assert L.sk_talker_frames(ctypes.byref(t), 1, None) == _lib.SK_EINVAL
+    assert b"sampling" in L.sk_last_error()
+    t.seed, t.inv_temp = d, 0.0
+    assert L.sk_talker_frames(ctypes.byref(t), 1, None) == _lib.SK_EINVAL
+    c = _lib.SkCpDesc(n_layers=5, hidden=1024, inter=3072, nq=16, nkv=8, vocab=2048, n_positions=16,
+                      wd=_lib.WD["i8row"], ct=_lib.CT["bf16"], eps=1e-6, layers=d, norm=d, rope=d, x0=d, id0=d,
+                      emb0_rows=3072, emb=d, head_w=d, head_s=d, codes=d, workspace=d, workspace_bytes=ws,
+                      do_sample=1, inv_temp=1.25, top_k=40, seed=d, counter=None)
+    assert L.sk_cp_frame(ctypes.byref(c), None) == _lib.SK_EINVAL
+    assert b"sampling" in L.sk_last_error()
