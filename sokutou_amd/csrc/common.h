@@ -195,7 +195,7 @@ __device__ __forceinline__ void buf_stf(void* base, uint32_t off, float v) {
 // Order-preserving key of an fp32 value (the sign bit set for positives, all bits flipped for negatives).
 __device__ __forceinline__ uint32_t order_key(float f) {
   const uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);  // all bits flipped for negatives, the sign for the rest
 }
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): ten rounds of two 32x32->64-bit products with the published
 // multipliers, the high halves xored with the other counter words and the key, the key bumped by Weyl constants.

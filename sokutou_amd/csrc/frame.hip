@@ -101,7 +101,7 @@ struct Layout {
     e4 = e3 + kQ;                              // h after o  [H]
     e5 = e4 + H;                               // act        [I]
     e6 = e5 + I;                               // h after down [H]
-    e7 = e6 + H;                               // candidates [256][2]
+    e7 = e6 + H;                               // candidates [256][2] (greedy), maxima [256] (sampled)
     e8 = e7 + kWG * 2;                         // processed logits of a sampled pick [vocab <= 3072]
     total = e8 + kTalkerV;
   }
@@ -113,66 +113,6 @@ struct Layout {
 static_assert(sizeof(sk_layer_desc) == 14 * sizeof(void*), "sk_layer_desc layout");
 
 namespace {
-
-// ---- sampled pick by one wave (the control wave), over V values staged in LDS --------------------------------
-// The key of the top_k-th largest value: a radix select over the four bytes of the order key, most significant
-// first (LDS histogram of the values matching the digits so far, then a wave scan of the bins from the top).
-// top_k <= 0 or >= V keeps everything (key 0). Same rule as the fused sampler's block-wide select.
-__device__ uint32_t topk_key_wave(const float* v, int V, int top_k, uint32_t* hist, int lane) {
-  if (top_k <= 0 || top_k >= V) return 0;
-  uint32_t prefix = 0, need = (uint32_t)top_k;
-  for (int pass = 0; pass < 4; pass++) {
-    const int shift = 24 - 8 * pass;
-    for (int b = lane; b < 256; b += 64) hist[b] = 0;
-    for (int i = lane; i < V; i += 64) {
-      const uint32_t k = order_key(v[i]);
-      if (pass == 0 || ((k ^ prefix) >> (shift + 8)) == 0) atomicAdd(&hist[(k >> shift) & 255u], 1u);
-    }
-    uint32_t cnt[4], sum = 0;
-#pragma unroll
-    for (int q = 0; q < 4; q++) { cnt[q] = hist[255 - (4 * lane + q)]; sum += cnt[q]; }
-    uint32_t inc = sum;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = __shfl_up(inc, o);
-      if (lane >= o) inc += y;
-    }
-    const uint32_t before = inc - sum;
-    const bool mine = before < need && inc >= need;  // exactly one lane: the counts from the top reach `need` there
-    uint32_t digit = 0, rest = 0;
-    if (mine) {
-      uint32_t acc = before;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        if (acc + cnt[q] >= need) { digit = 255u - (uint32_t)(4 * lane + q); rest = need - acc; break; }
-        acc += cnt[q];
-      }
-    }
-    const int src = __builtin_ctzll(__ballot(mine));
-    prefix |= (uint32_t)__shfl((int)digit, src) << shift;
-    need = (uint32_t)__shfl((int)rest, src);
-  }
-  return prefix;
-}
-// Gumbel-max over the values at or above `thr` that are not -inf (largest v - log(-log u), lowest index on ties);
-// every lane returns the pick, 0 if nothing is kept.
-__device__ int gumbel_pick_wave(const float* v, int V, uint32_t thr, uint64_t cnt, uint32_t k0, uint32_t k1, int lane) {
-  float best = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int i = lane; i < V; i += 64) {
-    const float x = v[i];
-    if (order_key(x) < thr || x == -INFINITY) continue;
-    const float g = gumbel(x, (uint32_t)i, cnt, k0, k1);
-    if (g > best || (g == best && i < bi)) { best = g; bi = i; }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ob = __shfl_xor(best, o);
-    const int oi = __shfl_xor(bi, o);
-    if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
-  }
-  return bi == 0x7fffffff ? 0 : bi;
-}
 
 // Order-preserving key of (value, index): larger value wins, then the lower index.
 __device__ __forceinline__ uint64_t pick_key(float v, int i) {
@@ -216,7 +156,6 @@ struct Lds {
   sk_layer_desc desc[Ws::kTraceLayers];  // the layer descriptors, copied once per launch
   uint64_t cand[W];
   float hv[16];        // this workgroup's processed logits (sampled picks)
-  uint32_t hist[256];  // radix-select histogram (sampled picks)
   int flags[8];
   int64_t tok;
   uint32_t pubseq;  // stage publications completed by the compute waves
@@ -355,33 +294,246 @@ __device__ __forceinline__ void after_publish(L& S, uint32_t seq, uint32_t delay
 }
 
 // ---- control wave: sampled pick ---------------------------------------------------------------------------
-// Publishes this workgroup's `rows` processed logits (cells idx0 + rows g ..), waits until all V carry epoch e,
-// then draws: top_k threshold by radix select and Gumbel-max with Philox draw `draw` under key `seed`. Every
-// workgroup computes the same pick from the same V values. Returns the pick, -1 when the error word is set, -2 on
-// timeout. Kept out of line: inlined, its registers raise the pressure of the whole control loop.
-__device__ __attribute__((noinline)) int64_t sampled_pick(char* cells, uint32_t idx0, int V, int rows, int g,
-                                                          uint32_t e, const float* hv, float* xs, uint32_t* hist,
-                                                          int top_k, uint64_t draw, uint64_t seed, void* ws,
-                                                          uint32_t delay, int lane) {
-  if (lane < rows / 2) put2(cells, idx0 + (uint32_t)(rows * g + 2 * lane), hv[2 * lane], hv[2 * lane + 1], e);
+// Integer wave64 reductions over DPP (every lane's value; the results are wave-uniform).
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ uint32_t dppu(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  v += dppu<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dppu<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dppu<0x124>(v);  // row_ror:4
+  v += dppu<0x128>(v);  // row_ror:8
+  v += dppu<0x142, 0xA>(v);  // row_bcast:15
+  v += dppu<0x143, 0xC>(v);  // row_bcast:31
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dppu<0xB1>(v));
+  v = max(v, dppu<0x4E>(v));
+  v = max(v, dppu<0x124>(v));
+  v = max(v, dppu<0x128>(v));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+// Inclusive prefix sum over the 64 lanes (row_shr within rows of 16, then row_bcast across rows).
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  // Hillis-Steele within each row of 16 (a source lane outside the row reads as 0), then the row totals carried
+  // across rows: lane 15 of rows 0 / 2 into rows 1 / 3, then lane 31 (rows 0-1) into rows 2 and 3
+  v += dppu<0x111>(v);        // row_shr:1
+  v += dppu<0x112>(v);        // row_shr:2
+  v += dppu<0x114>(v);        // row_shr:4
+  v += dppu<0x118>(v);        // row_shr:8
+  v += dppu<0x142, 0xA>(v);  // row_bcast:15
+  v += dppu<0x143, 0xC>(v);  // row_bcast:31
+  return v;
+}
+
+// The largest key t in [lo, hi] whose count c(t) (keys >= t) reaches K, given c(lo) >= K and c(hi + 1) < K. Bits
+// above the highest bit where lo and hi differ are common to every such t; below it the prefix grows one bit at a
+// time, the bit kept when the count at the prefix with the bit set reaches K.
+template <class F>
+__device__ __forceinline__ uint32_t bisect_keys(uint32_t lo, uint32_t hi, uint32_t K, F count) {
+  if (lo >= hi) return lo;
+  const int top = 31 - __builtin_clz(lo ^ hi);
+  uint32_t p = top == 31 ? 0u : lo & ~((2u << top) - 1u);
+  for (int b = top; b >= 0; b--) {
+    const uint32_t t = p | (1u << b);
+    if (count(t) >= K) p = t;
+  }
+  return p;
+}
+
+// Publishes this workgroup's ROWS processed logits (cells vals + ROWS g ..) and their largest order key (cell
+// maxs + g), waits until all V values and the 256 maxima carry epoch e, then draws as the fused sampler does: the
+// key of the top_k-th largest value (ties kept; top_k <= 0 or >= V keeps everything), then the largest
+// v - log(-log u) over the kept values that are not -inf, u from Philox draw `draw` under key `seed`, lowest index
+// on ties, 0 if nothing is kept. Every workgroup computes the same pick from the same V values. Returns the pick,
+// -1 when the error word is set, -2 on timeout.
+//
+// The threshold without a histogram. Lane l holds the maxima of workgroups 2l, 2l+1, 128+2l, 129+2l; for
+// top_k <= 64 the top_k-th largest of the 64 lane maxima is a lower bound lb of the top_k-th largest value (they
+// are 64 of the values). lb is found while the first values are still in flight; as each batch of values arrives
+// the indices of those >= lb are compacted into LDS (ci; the values go to cv by index): a per-lane count, a scan
+// over the lanes, then every lane writes its own run (non-candidates to a trash slot, so no branch). A bisection
+// of the keys then counts, per key t, the candidates >= t; below lb every count is at least top_k, as it is over
+// all values, so it ends on the same key. The kept candidates are compacted once more so each lane draws the
+// Philox noise of at most one of them when at most 64 are kept. Counts are ballots of one comparison each, with
+// the number of comparisons per step fixed outside the bisection (a branch per step costs more than the ballot).
+// Kept out of line (one call per frame) and only in the sampling instantiation of the kernel. The arguments
+// arrive in vector registers under the call convention; they are made wave-uniform first so the control flow stays
+// scalar. `tp` (null unless tracing) receives wall-clock stamps (tp[10..14]) and shader-clock stamps (tp[0..4])
+// after the bound, the gather with the compaction, the bisection, the kept compaction and the draw, and lb and
+// the counts of candidates and kept values (tp[5..7]).
+template <int V, int ROWS>
+__device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t vals_, uint32_t maxs_, int g_,
+                                                          uint32_t e_, const float* hv_, float* cv_, uint32_t* ci_,
+                                                          int top_k_, uint64_t draw_, uint64_t seed_, void* ws_,
+                                                          uint32_t delay_, int lane, uint64_t* tp_) {
+  constexpr int NB = V / 128;  // value cell pairs per lane: lane holds indices 2 lane + 128 b and 2 lane + 128 b + 1
+  constexpr int kBatch = 8;    // cell pairs per lane and batch (a small register footprint)
+  static_assert(V % 128 == 0 && V == ROWS * kWG && ROWS % 2 == 0 && ROWS <= 16, "vocabulary of 256 x ROWS");
+  static_assert(NB % kBatch == 0, "batches");
+  typedef __attribute__((address_space(3))) float lds_f32;
+  typedef __attribute__((address_space(3))) uint16_t lds_u16;
+  char* cells = uniform(cells_);
+  void* ws = uniform(ws_);
+  uint64_t* tp = uniform(tp_);
+  const float* hv = uniform(hv_);
+  lds_f32* cv = (lds_f32*)uniform(cv_);  // LDS arrays: ds_* accesses rather than flat
+  lds_u16* ci = (lds_u16*)uniform(ci_);  // candidate indices [V], then one trash slot per lane
+  const uint32_t vals = __builtin_amdgcn_readfirstlane(vals_), maxs = __builtin_amdgcn_readfirstlane(maxs_);
+  const uint32_t e = __builtin_amdgcn_readfirstlane(e_);
+  const int g = __builtin_amdgcn_readfirstlane(g_);
+  const int top_k = __builtin_amdgcn_readfirstlane(top_k_);
+  const uint32_t delay = __builtin_amdgcn_readfirstlane(delay_);
+  const uint32_t d0 = __builtin_amdgcn_readfirstlane((uint32_t)draw_), d1 = __builtin_amdgcn_readfirstlane((uint32_t)(draw_ >> 32));
+  const uint32_t k0 = __builtin_amdgcn_readfirstlane((uint32_t)seed_), k1 = __builtin_amdgcn_readfirstlane((uint32_t)(seed_ >> 32));
+  const uint64_t draw = ((uint64_t)d1 << 32) | d0;
+
+  // publish: the values, then this workgroup's largest key
+  const float own = lane < ROWS ? hv[lane] : -INFINITY;
+  const uint32_t own_max = wave_max_u32(lane < ROWS ? order_key(own) : 0u);
+  if (lane < ROWS / 2) put2(cells, vals + (uint32_t)(ROWS * g + 2 * lane), hv[2 * lane], hv[2 * lane + 1], e);
+  if (lane == 0) put(cells, maxs + (uint32_t)g, __uint_as_float(own_max), e);
   sleep_units(delay);
+  u32x4 qa[kBatch], qb[kBatch];  // double buffer: the next batch is in flight while one is waited for and processed
+  auto load_batch = [&](u32x4 (&q)[kBatch], int b0) {
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) q[b] = get2(cells, vals + (uint32_t)(2 * lane + 128 * (b0 + b)));
+  };
+  load_batch(qa, 0);  // in flight while the maxima are polled and the bound is found
+  // the 256 maxima: lane l holds workgroups 2l, 2l+1, 128+2l, 129+2l
+  u32x4 mq[2];
   for (uint32_t spin = 0;; spin++) {
-    bool ok = true;
-    for (int i = 2 * lane; i < V; i += 128) {
-      const u32x4 q = get2(cells, idx0 + (uint32_t)i);
-      ok &= q.y == e && q.w == e;
-      xs[i] = __uint_as_float(q.x);
-      xs[i + 1] = __uint_as_float(q.z);
-    }
-    if (__all(ok)) break;
+    mq[0] = get2(cells, maxs + (uint32_t)(2 * lane));
+    mq[1] = get2(cells, maxs + (uint32_t)(128 + 2 * lane));
+    if (__all(mq[0].y == e && mq[0].w == e && mq[1].y == e && mq[1].w == e)) break;
     if ((spin & 63) == 63) {
       if (ld_u32_dev(ws, Ws::kErr) != 0) return -1;
       if (spin > kSpinLimit) return -2;
     }
     __builtin_amdgcn_s_sleep(1);
   }
-  const uint32_t thr = topk_key_wave(xs, V, top_k, hist, lane);
-  return gumbel_pick_wave(xs, V, thr, draw, (uint32_t)seed, (uint32_t)(seed >> 32), lane);
+  const uint32_t lm = max(max(mq[0].x, mq[0].z), max(mq[1].x, mq[1].z));  // the maxima are order keys already
+  const uint32_t top_key = wave_max_u32(lm);                               // the largest key of all
+  const bool keep_all = top_k <= 0 || top_k >= V;
+  const uint32_t K = (uint32_t)top_k;
+  uint32_t lb = 0;
+  if (!keep_all && top_k <= 64) {
+    const uint32_t lmin = ~wave_max_u32(~lm);  // 64 lane maxima reach the smallest of them, and 64 >= K
+    lb = bisect_keys(lmin, top_key, K, [&](uint32_t t) { return (uint32_t)__popcll(__ballot(lm >= t)); });
+  }
+  if (tp && lane == 0) { tp[10] = (uint64_t)wall_clock64(); tp[0] = (uint64_t)clock64(); }
+  // the values, batch by batch: staged into cv by index, the indices of those >= lb appended to ci
+  uint32_t n = 0;
+  const uint32_t trash = (uint32_t)(V + lane);
+#pragma unroll
+  for (int b0 = 0; b0 < NB; b0 += kBatch) {
+    u32x4 (&q)[kBatch] = (b0 / kBatch) % 2 ? qb : qa;
+    // the next batch goes out before this one is waited for: two batches in flight
+    if (b0 + kBatch < NB) load_batch((b0 / kBatch) % 2 ? qa : qb, b0 + kBatch);
+    for (uint32_t spin = 0;; spin++) {
+      bool ok = true;
+#pragma unroll
+      for (int b = 0; b < kBatch; b++) ok &= q[b].y == e && q[b].w == e;
+      if (__all(ok)) break;
+      if ((spin & 63) == 63) {
+        if (ld_u32_dev(ws, Ws::kErr) != 0) return -1;
+        if (spin > kSpinLimit) return -2;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      load_batch(q, b0);
+    }
+    bool tk[2 * kBatch];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const int i = 2 * lane + 128 * (b0 + b);
+      cv[i] = __uint_as_float(q[b].x);
+      cv[i + 1] = __uint_as_float(q[b].z);
+      tk[2 * b] = order_key(__uint_as_float(q[b].x)) >= lb;
+      tk[2 * b + 1] = order_key(__uint_as_float(q[b].z)) >= lb;
+      cnt += (uint32_t)tk[2 * b] + (uint32_t)tk[2 * b + 1];
+    }
+    const uint32_t incl = wave_incl_scan_u32(cnt);
+    uint32_t at = n + incl - cnt;
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        ci[tk[2 * b + h] ? at : trash] = (uint16_t)(2 * lane + 128 * (b0 + b) + h);
+        at += (uint32_t)tk[2 * b + h];
+      }
+    }
+    n += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  }
+  const int nm = (int)((n + 63) / 64);
+  if (tp && lane == 0) { tp[11] = (uint64_t)wall_clock64(); tp[1] = (uint64_t)clock64(); }
+  uint32_t thr = 0;
+  if (!keep_all) {
+    constexpr int kReg = 4;  // candidate keys held in registers (n <= 256); the rest are read from LDS
+    uint32_t kk[kReg];
+#pragma unroll
+    for (int m = 0; m < kReg; m++) {
+      const uint32_t j = (uint32_t)(lane + 64 * m);
+      kk[m] = j < n ? order_key(cv[ci[j]]) : 0u;  // 0 never counts: every probed key t is at least 1
+    }
+    if (nm <= 1) {
+      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) { return (uint32_t)__popcll(__ballot(kk[0] >= t)); });
+    } else if (nm <= 2) {
+      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
+        return (uint32_t)__popcll(__ballot(kk[0] >= t)) + (uint32_t)__popcll(__ballot(kk[1] >= t));
+      });
+    } else if (nm <= 4) {
+      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
+        return (uint32_t)__popcll(__ballot(kk[0] >= t)) + (uint32_t)__popcll(__ballot(kk[1] >= t)) +
+               (uint32_t)__popcll(__ballot(kk[2] >= t)) + (uint32_t)__popcll(__ballot(kk[3] >= t));
+      });
+    } else {
+      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int m = 0; m < kReg; m++) c += (uint32_t)__popcll(__ballot(kk[m] >= t));
+        for (int m = kReg; m < nm; m++) {
+          const uint32_t j = (uint32_t)(lane + 64 * m);
+          c += (uint32_t)__popcll(__ballot(j < n && order_key(cv[ci[j]]) >= t));
+        }
+        return c;
+      });
+    }
+  }
+  if (tp && lane == 0) { tp[12] = (uint64_t)wall_clock64(); tp[2] = (uint64_t)clock64(); }
+  // the kept candidates (key >= thr, not -inf), compacted in place: a batch writes below its own start or over
+  // itself, after all its lanes have read their entries
+  uint32_t nk = 0;
+  for (int m = 0; m < nm; m++) {
+    const uint32_t j = (uint32_t)(lane + 64 * m);
+    uint32_t i = 0;
+    bool take = false;
+    if (j < n) {
+      i = ci[j];
+      const float x = cv[i];
+      take = order_key(x) >= thr && x != -INFINITY;
+    }
+    const uint64_t msk = __ballot(take);
+    if (take) ci[nk + __builtin_amdgcn_mbcnt_hi((uint32_t)(msk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)msk, 0u))] = (uint16_t)i;
+    nk += (uint32_t)__popcll(msk);
+  }
+  if (tp && lane == 0) { tp[13] = (uint64_t)wall_clock64(); tp[3] = (uint64_t)clock64(); tp[5] = lb; tp[6] = n; tp[7] = nk; }
+  // Gumbel-max: the largest perturbed value, then the lowest index among the lanes that hold it
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (uint32_t j = (uint32_t)lane; j < nk; j += 64) {
+    const int i = (int)ci[j];
+    const float gv = gumbel(cv[i], (uint32_t)i, draw, k0, k1);
+    if (gv > best || (gv == best && i < bi)) { best = gv; bi = i; }
+  }
+  const float gmax = wave_max(best);
+  const uint32_t pick = ~wave_max_u32(best == gmax ? ~(uint32_t)bi : 0u);
+  if (tp && lane == 0) { tp[14] = (uint64_t)wall_clock64(); tp[4] = (uint64_t)clock64(); }
+  return pick == 0x7fffffffu || nk == 0 ? 0 : (int64_t)pick;
 }
 
 // Position bookkeeping of a frame for this workgroup's attention chunk.
@@ -447,6 +599,11 @@ struct Ctx {
     if (trace && f == 0 && l < Ws::kTraceLayers)
       trace[(((size_t)g * 2 + role) * Ws::kTraceLayers + l) * Ws::kTraceEvents + ev] = (uint64_t)wall_clock64();
   }
+  __device__ uint64_t* tslot(int role, int f, int l, int ev) const {  // trace slot address, null when not traced
+    return (trace && f == 0 && l < Ws::kTraceLayers)
+               ? trace + (((size_t)g * 2 + role) * Ws::kTraceLayers + l) * Ws::kTraceEvents + ev
+               : nullptr;
+  }
   __device__ void tr_clk(int role, int f, int l, int ev) const {  // shader clock counter instead of wall clock
     if (trace && f == 0 && l < Ws::kTraceLayers)
       trace[(((size_t)g * 2 + role) * Ws::kTraceLayers + l) * Ws::kTraceEvents + ev] = (uint64_t)clock64();
@@ -473,7 +630,7 @@ __device__ __forceinline__ int attn_barriers(const Chunk& ck) { return 1 + (ck.n
 // ================================================================================================================
 // Control wave
 // ================================================================================================================
-template <int H, int I, int W, int V, bool CP>
+template <int H, int I, int W, int V, bool CP, bool SMP>
 __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
   const Layout LY(H, I);
   const float eps = c.d.eps;
@@ -647,11 +804,13 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     wg_sync();
     if (!ok) return;
     wg_sync();  // candidates (greedy) or processed logits (sampled) of the compute waves are in S.cand / S.hv
-    if (c.d.do_sample) {
+    if (SMP && lane == 0) c.tr(0, f, c.L, 9);
+    if constexpr (SMP) {
       // every workgroup publishes its processed logits and every control wave draws the same pick from all of them
-      const int64_t t = sampled_pick(c.cells, LY.e8, V, V / kWG, c.g, c.tick(f, c.L, 1), S.hv, S.xs[1], S.hist,
-                                     c.d.top_k, c.cnt0 + (uint64_t)(CP ? f - 1 : f), c.seed, c.ws,
-                                     c.dl[Ws::kHopPick], lane);
+      // S.xs[0] and S.xs[1] are free here: the head dot has consumed its input and the compute waves wait
+      const int64_t t = sampled_pick<V, V / kWG>(c.cells, LY.e8, LY.e7, c.g, c.tick(f, c.L, 1), S.hv, S.xs[1],
+                                                 (uint32_t*)S.xs[0], c.d.top_k, c.cnt0 + (uint64_t)(CP ? f - 1 : f),
+                                                 c.seed, c.ws, c.dl[Ws::kHopPick], lane, c.tslot(0, f, c.L, 0));
       ok = t >= 0;
       if (ok) tok = t;
       else if (t == -2 && lane == 0) fail(c, 19u, f, c.L);
@@ -696,6 +855,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if (lane == 0) { S.tok = tok; S.flags[6] = !ok; }
     }
     }
+    if (SMP && lane == 0) c.tr(0, f, c.L, 15);
     wg_sync();
     if (!ok) return;
     if (c.g == 0 && lane == 0) {
@@ -716,14 +876,14 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if (c.d.ngen) gstore(c.d.ngen, gload(c.d.ngen) + (int64_t)c.n_frames);
     }
   }
-  if (c.d.do_sample && c.g == 0 && lane == 0 && ld_u32_dev(c.ws, Ws::kErr) == 0)
+  if (SMP && c.g == 0 && lane == 0 && ld_u32_dev(c.ws, Ws::kErr) == 0)
     gstore(c.d.counter, c.cnt0 + (uint64_t)(CP ? c.n_frames - 1 : c.n_frames));
 }
 
 // ================================================================================================================
 // Compute waves
 // ================================================================================================================
-template <int H, int I, int W, int V, bool CP>
+template <int H, int I, int W, int V, bool CP, bool SMP>
 __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
   using C = Cfg<H, I, W, V, CP>;
   const Layout LY(H, I);
@@ -1001,7 +1161,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
             if (c.d.suppress && gload(c.d.suppress + row)) v = -INFINITY;
             if (block_eos && row == c.d.eos) v = -INFINITY;
           }
-          if (c.d.do_sample) S.hv[row - C::kHeadRows * g] = v * c.d.inv_temp;
+          if constexpr (SMP) S.hv[row - C::kHeadRows * g] = v * c.d.inv_temp;
           else if (v == v) { const uint64_t k = pick_key(v, row); best = k > best ? k : best; }
         }
         S.cand[cw] = best;
@@ -1016,7 +1176,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   }
 }
 
-template <int H, int I, int W, int V, bool CP>
+// SMP: sampled picks (do_sample != 0). The greedy instantiation carries none of the sampling code, whose call and
+// registers would otherwise weigh on the control loop of every greedy frame.
+template <int H, int I, int W, int V, bool CP, bool SMP>
 __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArgs cp, int n_frames) {
   extern __shared__ char smem_raw[];
   Lds<H, I, W, V, CP>& S = *(Lds<H, I, W, V, CP>*)smem_raw;
@@ -1068,8 +1230,8 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   c.tpf = (uint32_t)d.n_layers * 8u + 8u;
   c.pos0 = d.pos ? (int)gload(d.pos) : 0;
   // read before this workgroup publishes anything: workgroup 0 advances the counter once every pick is done
-  c.seed = d.do_sample ? gload(d.seed) : 0;
-  c.cnt0 = d.do_sample ? gload(d.counter) : 0;
+  c.seed = SMP ? gload(d.seed) : 0;
+  c.cnt0 = SMP ? gload(d.counter) : 0;
   c.n_frames = n_frames;
   c.L = d.n_layers;
   for (int i = tid; i < d.n_layers * (int)(sizeof(sk_layer_desc) / 8); i += blockDim.x)
@@ -1086,25 +1248,30 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     }
   }
   c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
-  if (wave == W) run_control<H, I, W, V, CP>(c, S, lane);
-  else run_compute<H, I, W, V, CP>(c, S, wave, tid, lane);
+  if (wave == W) run_control<H, I, W, V, CP, SMP>(c, S, lane);
+  else run_compute<H, I, W, V, CP, SMP>(c, S, wave, tid, lane);
   // ---- end of launch: epoch base and launch count (workgroup 0; every workgroup finished its census) --------
   if (c.g == 0 && tid == 0) {
     st_u32_dev(ws, Ws::kTick, c.base + (uint32_t)n_frames * c.tpf);
     st_u32_dev(ws, Ws::kLaunch, ld_u32_dev(ws, Ws::kLaunch) + 1u);
   }
 }
-template <int H, int I, int W, int V, bool CP>
-int launch_frames(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
-  if (d->max_len > Cfg<H, I, W, V, CP>::kMaxLen) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: max_len too long");
+template <int H, int I, int W, int V, bool CP, bool SMP>
+int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
   const size_t lds = sizeof(Lds<H, I, W, V, CP>) < 96 * 1024 ? 96 * 1024 : sizeof(Lds<H, I, W, V, CP>);  // one workgroup per CU
   static bool attr_set = false;
   if (!attr_set) {
-    hipFuncSetAttribute((const void*)k_frames<H, I, W, V, CP>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)k_frames<H, I, W, V, CP, SMP>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_frames<H, I, W, V, CP>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp, n_frames);
+  hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp, n_frames);
   return sk_check_launch(hipGetLastError(), "sk_talker_frames");
+}
+template <int H, int I, int W, int V, bool CP>
+int launch_frames(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
+  if (d->max_len > Cfg<H, I, W, V, CP>::kMaxLen) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: max_len too long");
+  return d->do_sample ? launch_kernel<H, I, W, V, CP, true>(d, cp, n_frames, st)
+                      : launch_kernel<H, I, W, V, CP, false>(d, cp, n_frames, st);
 }
 
 }  // namespace

@@ -291,10 +291,14 @@ def batch_max_len(name: str, frames: int | None = None) -> int:
     return w["kv_hi"] + (w["frames"] if frames is None else frames) + 1
 
 
-def make_frame_engine(name: str = "frame06b", seed: int = 0, device="cuda", frame_kernel: bool | None = None):
-    """A Qwen3Kernels engine over the seeded synthetic talker with a code predictor (workload ``name``), greedy,
-    prior cache loaded, state at position ``kv``. Returns (engine, start token, kw) where kw holds the prefill
-    results ``generate_codes`` takes (``prefill_len``, ``first_token``, ``last_hidden``, ``tts_pad_embed``)."""
+def make_frame_engine(name: str = "frame06b", seed: int = 0, device="cuda", frame_kernel: bool | None = None,
+                      sampled: bool = False):
+    """A Qwen3Kernels engine over the seeded synthetic talker with a code predictor (workload ``name``), prior cache
+    loaded, state at position ``kv``. Greedy without the processor, or with ``sampled`` the reference's default
+    settings (``Sampling()``: temperature 0.9, top_k 50, repetition penalty 1.05, 2 codes before EOS, sub-codes at
+    0.9 / 50, the last 1024 ids suppressed). Returns (engine, start token, kw) where kw holds the prefill results
+    ``generate_codes`` takes (``prefill_len``, ``first_token``, ``last_hidden``, ``tts_pad_embed``) and the
+    sampling settings."""
     from .fast import Sampling
     from .kernels import Qwen3Kernels
 
@@ -302,8 +306,9 @@ def make_frame_engine(name: str = "frame06b", seed: int = 0, device="cuda", fram
     s = workload_shape(name)
     cs = workload_shape(w["cp"])
     tts, pad = make_tts_with_cp(seed, s, cs, device=device)
-    eng = Qwen3Kernels(tts, Sampling.greedy(processor=False, max_new_tokens=4096), max_cache=w["kv"] + w["frames"] + 1,
-                       wd="i8row", sampler="fused", suppress_tail=0, frame_kernel=frame_kernel)
+    smp = Sampling(max_new_tokens=4096) if sampled else Sampling.greedy(processor=False, max_new_tokens=4096)
+    eng = Qwen3Kernels(tts, smp, max_cache=w["kv"] + w["frames"] + 1, wd="i8row", sampler="fused",
+                       suppress_tail=1024 if sampled else 0, frame_kernel=frame_kernel)
     eng.talker = None
     del tts
     for i in range(s.n_layers):
@@ -313,8 +318,10 @@ def make_frame_engine(name: str = "frame06b", seed: int = 0, device="cuda", fram
     tok = start_token(seed, s)
     x0, _ = cp_frame_inputs(seed, 0, s)
     kw = {"prefill_len": w["kv"], "first_token": tok, "last_hidden": torch.from_numpy(x0), "tts_pad_embed": torch.from_numpy(pad),
-          "do_sample": False, "repetition_penalty": 1.0, "min_new_tokens": 0, "max_new_tokens": 4096,
-          "subtalker_dosample": False}
+          "do_sample": smp.do_sample, "temperature": smp.temperature, "top_k": smp.top_k,
+          "repetition_penalty": smp.repetition_penalty, "min_new_tokens": smp.min_new_tokens, "max_new_tokens": 4096,
+          "subtalker_dosample": smp.sub_do_sample, "subtalker_temperature": smp.sub_temperature,
+          "subtalker_top_k": smp.sub_top_k}
     eng._start(kw)
     return eng, tok, kw
 
