@@ -132,6 +132,12 @@ struct Cfg {
   static constexpr int KVL = 2;                                // K (and V) loads per lane
   static constexpr int kMaxChunk = 4 * W * KVL;                // positions per attention workgroup: 32 / 64
   static constexpr int kMaxLen = kMaxChunk * kChunks;          // 1024 / 2048
+  // Prefetch distances. With 4 compute waves every stage's weights for the next layer are held in registers (a
+  // full layer ahead). With 8 compute waves the register budget is 168 per lane and a full layer of 1.7B weights
+  // (96 registers) does not fit beside the rest; each stage's weights are then loaded two or three exchanges
+  // before their use, so no more than o + gate/up + the next K/V are in flight at once: o and gate/up after the
+  // attention of their layer, down and the next layer's qkv after gate/up.
+  static constexpr bool kLate = W == 8;
   static_assert(16 % W == 0 && R_GU % W == 0 && R_GU % 2 == 0, "row split");
 };
 
@@ -923,9 +929,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
     load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
     load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), Chunk(c.pos0, r), cw, ag, asl);
     load_attn_vec(L0, c.pos0);
-    load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
-    load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
-    load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
+    if constexpr (!C::kLate) {
+      load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
+      load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
+      load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
+    }
   }
   const bool block_eos0 = c.d.talker_processor && c.d.ngen;
   const int64_t ngen0 = c.d.ngen ? gload(c.d.ngen) : 0;
@@ -958,7 +966,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         }
         publish<W>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, 16, c.tick(f, l, 0), lane);
         if (tid == 0) c.tr(1, f, l, 1);
-        load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+        if constexpr (!C::kLate) load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
       }
       // ---- S2: attention over this workgroup's chunk ----------------------------------------------------
       wg_sync();
@@ -1069,6 +1077,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         if (tid == 0) c.tr(1, f, l, 3);
         load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), Chunk(npos, r), cw, ag, asl);
         load_attn_vec(Ln, npos);
+        if constexpr (C::kLate) {
+          load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
+          load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+        }
       }
       // ---- S4: o projection rows, added to the layer's input residual ------------------------------------
       wg_sync();
@@ -1087,7 +1099,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         }
         publish<W>(S, c.cells, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
         if (tid == 0) c.tr(1, f, l, 5);
-        load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
+        if constexpr (!C::kLate) load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
       }
       // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
       wg_sync();
@@ -1105,7 +1117,12 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         }
         publish<W>(S, c.cells, LY.e5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
         if (tid == 0) c.tr(1, f, l, 6);
-        load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
+        if constexpr (C::kLate) {
+          load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
+          load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+        } else {
+          load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
+        }
       }
       // ---- S6: down rows, added to the residual after o --------------------------------------------------
       wg_sync();
@@ -1127,7 +1144,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         }
         publish<W>(S, c.cells, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
         if (tid == 0) c.tr(1, f, l, 7);
-        load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
+        if constexpr (!C::kLate) load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
       }
     }
     if (CP && f == 0) {  // the code predictor's position 0 has no head
