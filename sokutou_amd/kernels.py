@@ -144,7 +144,10 @@ class CodePredictor:
     g >= 1 ends in the final RMSNorm, head g - 1 and a pick: greedy, or after ``set_sampling`` the fused
     sampler's draw (temperature, top_k, Philox seed and counter in device memory; one draw per position g >= 1)."""
 
-    def __init__(self, cp, temb: torch.Tensor, n_positions: int = 16, wd: str = "i8row", device=None):
+    def __init__(self, cp, temb: torch.Tensor, n_positions: int = 16, wd: str = "i8row", device=None,
+                 x0: torch.Tensor | None = None, id0: torch.Tensor | None = None, codes: torch.Tensor | None = None):
+        """``x0`` (fp32 [hidden]), ``id0`` (int64, one element) and ``codes`` (int64 [n_positions]) may be a caller's
+        own contiguous device buffers: the kernel then reads and writes them in place (no copies per frame)."""
         if wd != "i8row":
             raise ValueError("the code-predictor kernel reads i8row weights")
         proj = getattr(cp, "small_to_mtp_projection", None)
@@ -166,9 +169,16 @@ class CodePredictor:
         dev = self.device
         self.kc = torch.zeros((len(P.layers), P.nkv, self.n, HD), dtype=torch.bfloat16, device=dev)
         self.vc = torch.zeros_like(self.kc)
-        self.x0 = torch.zeros(P.H, dtype=torch.float32, device=dev)
-        self.id0 = torch.zeros(1, dtype=torch.int64, device=dev)
-        self.codes = torch.zeros(self.n, dtype=torch.int64, device=dev)
+        def bind(t, n, dtype):
+            if t is None:
+                return torch.zeros(n, dtype=dtype, device=dev)
+            if t.numel() != n or t.dtype != dtype or not t.is_contiguous() or t.device != dev:
+                raise ValueError(f"a bound buffer must be a contiguous {dtype} tensor of {n} elements on {dev}")
+            return t.view(n)
+
+        self.x0 = bind(x0, P.H, torch.float32)
+        self.id0 = bind(id0, 1, torch.int64)
+        self.codes = bind(codes, self.n, torch.int64)
         self.logits = torch.zeros(self.V, dtype=torch.float32, device=dev)
         self.layer_out: torch.Tensor | None = None
         tabs = [0, self.temb.data_ptr()] + [t.data_ptr() for t in self.cemb]
@@ -341,7 +351,9 @@ class Qwen3Kernels(Qwen3Fast):
                 and self.ct == "bf16" and (P.H, P.I, P.nq, P.nkv, self.cp_heads[0].N) == (1024, 3072, 16, 8, 2048)
                 and 2 <= self.G <= 64)
         if fast:
-            self.cpk = CodePredictor(cp, self.temb, n_positions=self.G, wd=wd, device=dev)
+            # bound to the frame state: reads ph32 and code 0, writes all G codes, with no copy per frame
+            self.cpk = CodePredictor(cp, self.temb, n_positions=self.G, wd=wd, device=dev, x0=self.ph32, id0=self.id0,
+                                     codes=self.codes)
             if self.s.sub_do_sample:  # the fused sampler's draws, in the same order as position by position
                 self.cpk.set_sampling(self.s.sub_temperature, self.s.sub_top_k, self.fs.seed, self.fs.counter)
 
@@ -359,13 +371,10 @@ class Qwen3Kernels(Qwen3Fast):
         talker embedding of code 0, position g >= 2 code table g - 2 at code g - 1; position g >= 1 ends in the final
         norm, head g - 1 and a pick with the sub-code settings (no processor)."""
         s, codes = self.s, self.codes
-        codes[:, :1].copy_(self.id0)
-        if self.cpk is not None:
-            self.cpk.x0.copy_(self.ph32)
-            self.cpk.id0.copy_(self.id0.view(1))
+        if self.cpk is not None:  # reads ph32 and id0, writes codes[0, :G] (code 0 passes through)
             self.cpk.run()
-            codes[0, 1:].copy_(self.cpk.codes[1:])
             return
+        codes[:, :1].copy_(self.id0)
         P = self.C
         cptr = codes.data_ptr()
         for g in range(self.G):
