@@ -173,11 +173,13 @@ def _sampled_oracle(name, seed, tok, key, frames, top_k, eos, cnt0=0):
     return out
 
 
-@pytest.mark.parametrize("top_k", [50, 0, 1])
+@pytest.mark.parametrize("top_k", [50, 0, 1, 64, 100])
 def test_sampled_frames_one_launch_against_oracle(gpu, top_k):
     """Sampled picks inside the persistent kernel: 24 frames in one launch with the talker processor, every code
     equal to the oracle's draw (Philox key from torch's generator, draw counter = frame index); top_k 0 keeps the
-    whole vocabulary, top_k 1 reduces to the argmax of the processed logits. The counter advances by the frames."""
+    whole vocabulary, top_k 1 reduces to the argmax of the processed logits, 64 is the largest top_k with the
+    lane-maxima bound and 100 takes the unbounded path (every value a candidate). The counter advances by the
+    frames."""
     F = 24
     print(f"small06b: {F} sampled frames (top_k {top_k}) in one launch against the oracle", flush=True)
     eng, tok = _sampled_engine(gpu, top_k, frames=F)
