@@ -542,7 +542,7 @@ def main() -> None:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the talker decode step at batch 1 runs on a single MI355X "
-              "(how it would shard is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "(this build has no multi-GPU path); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     if args.workload == "cp06b":

@@ -4,7 +4,7 @@ transformers' Qwen3DecoderLayer (an independent implementation of the same layer
     python tests/golden/make_golden.py [--only NAME]
 
 Fixtures are data: inputs (by seed and SHA-256 digest of every generated tensor), expected outputs and the
-numbers needed to judge argmax robustness (top-1/top-2 logit margins).
+numbers needed to assess argmax robustness (top-1/top-2 logit margins).
 """
 
 from __future__ import annotations
