@@ -1,0 +1,1336 @@
+#pragma once
+// Persistent talker decode kernel (device code and launch templates; the entry points are in frame.hip for the
+// talker and frame_cp.hip for the code predictor, separate translation units so that the code generated for one
+// mode does not depend on the other's): whole frames (28 layers + final norm + codec head + greedy pick + next
+// embedding) in one launch of 256 workgroups, one per CU.
+//
+// It computes what the five per-layer launches of the reference compute (qwen3/kernels.py:619-627, frame order
+// 676-685, with `embed` feeding the next token as in qwen3/kernels.py:642), but as a dataflow over the whole chip:
+//
+//  * XCD-aware placement. The talker has 8 kv heads and MI355X has 8 XCDs: kv head x is owned by the 32 workgroups
+//    of XCD x. Each workgroup learns its XCD from the hardware XCC_ID register and a dense rank 0..31 from an
+//    arrival counter (the block -> XCD assignment is round-robin with a start that moves between dispatches).
+//  * Stages of a layer, each a set of rows of one projection per workgroup:
+//      S1 qkv     rows of head x (q of heads 2x, 2x+1, k and v of head x), 16 per workgroup
+//      S2 attn    positions [t0, t1) of head x (the cache length split 32 ways), both q heads; unnormalised
+//                 partial (m, l, o) per workgroup; the owner of `pos` appends K/V to the cache
+//      S3 merge   dims [8r, 8r+8) of heads 2x, 2x+1: log-sum-exp merge of the 32 partials
+//      S4 o       H/256 rows of the output projection, added to the residual
+//      S5 gu      2I/256 interleaved gate/up rows with RMSNorm, silu(g)*u
+//      S6 down    H/256 rows of the down projection, added to the residual
+//    then per frame: head rows (with the talker processor) and a local argmax, and every workgroup reduces the
+//    256 candidates itself and loads the next embedding row.
+//  * Exchanges use 8-byte cells {value, epoch} written and read with device-coherent (sc1) accesses: a consumer
+//    polls the cells it needs until all carry the producer's epoch. A 64-bit aligned store is single-copy atomic,
+//    so data and readiness arrive together and no fence, flag or L2 writeback is needed.
+//  * Wave roles. Waves 0..W-1 compute; wave W (the control wave) does all polling and copies inputs into LDS.
+//    The compute waves issue only weight and K/V loads: as soon as a stage's registers are consumed, the same
+//    registers are reloaded with that stage's weights of the next layer, so the HBM stream runs a full layer
+//    ahead of the dependency chain. The hardware waits for loads in issue order per wave, which is why polling
+//    (whose completion time is unknown) lives in a wave that has no prefetches queued.
+//  * Every wait is bounded. A timeout or an inconsistent placement sets an error word in the workspace; every
+//    poll also watches that word, so all workgroups leave promptly and the host reports the error.
+//
+// Numerics are those of the per-op kernels: fp32 residual and accumulation, bf16 K/V cache written round to
+// nearest even, per-row bf16 weight scales applied after the dot, RMSNorm scale applied after the dot.
+#include <type_traits>
+
+#include "common.h"
+#include "internal.h"
+
+namespace {
+
+constexpr int kXcd = 8, kPerXcd = 32, kWG = kXcd * kPerXcd;
+constexpr int kChunks = kPerXcd;           // attention split of the cache length per head
+constexpr int kPartN = 4 + 2 * SK_HD;      // m0 l0 m1 l1 o0[128] o1[128]
+constexpr int kNQ = 16, kNKV = 8, kQKV = (kNQ + 2 * kNKV) * SK_HD, kQ = kNQ * SK_HD;
+constexpr int kTalkerV = 3072;             // talker codec vocabulary
+constexpr uint32_t kSpinLimit = 1u << 19;
+constexpr float kInvSqrtHd = 0.08838834764831845f;
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11)) & 0xfu; }
+
+// ---- exchange cells ------------------------------------------------------------------------------------------
+__device__ __forceinline__ void put(void* cells, uint32_t idx, float v, uint32_t e) {
+  u32x2 x = {__float_as_uint(v), e};
+  __builtin_amdgcn_raw_buffer_store_b64(x, make_rsrc(cells), idx * 8u, 0, kPolDev);
+}
+__device__ __forceinline__ void put2(void* cells, uint32_t idx, float v0, float v1, uint32_t e) {  // idx even
+  u32x4 x = {__float_as_uint(v0), e, __float_as_uint(v1), e};
+  __builtin_amdgcn_raw_buffer_store_b128(x, make_rsrc(cells), idx * 8u, 0, kPolDev);
+}
+__device__ __forceinline__ u32x4 get2(const void* cells, uint32_t idx) {  // cells idx, idx+1
+  return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(cells), idx * 8u, 0, kPolDev);
+}
+__device__ __forceinline__ uint32_t ld_u32_dev(const void* base, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(base), off, 0, kPolDev);
+}
+__device__ __forceinline__ void st_u32_dev(void* base, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, make_rsrc(base), off, 0, kPolDev);
+}
+
+// Workgroup barrier that does not wait for outstanding global loads (the compute waves keep their weight
+// prefetches in flight across it); it only makes this wave's LDS writes visible first.
+__device__ __forceinline__ void wg_sync() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt untouched
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// ---- layout of the workspace (bytes) -------------------------------------------------------------------------
+struct Ws {
+  // control words
+  static constexpr uint32_t kErr = 0, kTick = 4, kLaunch = 8, kDiag = 16, kTraceOn = 32, kPollDelay = 40,
+                            kCensus = 64;  // census: 8 counters
+  // Polling of a stage's input starts this many sleep units (s_sleep 1: 64 shader clocks, ~27 ns at 2.4 GHz)
+  // after the workgroup published its own part of it. Reads that reach the cells before the producers' stores
+  // are visible come back stale and make the whole exchange slower than one late, successful read. One delay
+  // per exchange (kHop*), since producers and timing differ: bytes kPollDelay + h of the workspace override
+  // the defaults (value - 1) when non-zero.
+  static constexpr int kHopS1 = 0, kHopS2 = 1, kHopS3 = 2, kHopS4 = 3, kHopS5 = 4, kHopS6 = 5, kHopHead = 6,
+                       kHopPick = 7, kHops = 8;
+  static constexpr int kTraceLayers = 32, kTraceEvents = 16;  // optional per-stage timestamps of frame 0
+  static constexpr uint32_t kCells = 256;
+};
+
+struct Layout {
+  uint32_t e1, e2, e3, e4, e5, e6, e7, e8, total;  // cell offsets (in cells) from the cell base
+  __host__ __device__ Layout(int H, int I) {
+    e1 = 0;                                    // qkv        [8][512]
+    e2 = e1 + kNKV * 512;                      // partials   [8][32][260]
+    e3 = e2 + kNKV * kChunks * kPartN;         // att        [2048]
+    e4 = e3 + kQ;                              // h after o  [H]
+    e5 = e4 + H;                               // act        [I]
+    e6 = e5 + I;                               // h after down [H]
+    e7 = e6 + H;                               // candidates [256][2] (greedy), maxima [256] (sampled)
+    e8 = e7 + kWG * 2;                         // processed logits of a sampled pick [vocab <= 3072]
+    total = e8 + kTalkerV;
+  }
+};
+
+}  // namespace
+
+// Descriptor layouts shared with the host (declared in sokutou_amd.h).
+static_assert(sizeof(sk_layer_desc) == 14 * sizeof(void*), "sk_layer_desc layout");
+
+namespace {
+
+// Order-preserving key of (value, index): larger value wins, then the lower index.
+__device__ __forceinline__ uint64_t pick_key(float v, int i) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)k << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+}
+
+template <int H, int I, int W, int V, bool CP>
+struct Cfg {
+  static constexpr int R_O = H / kWG, R_GU = 2 * I / kWG, R_D = H / kWG;
+  static constexpr int RW_QKV = 16 / W;                       // rows per compute wave
+  static constexpr int RW_O = (R_O + W - 1) / W, RW_GU = R_GU / W, RW_D = (R_D + W - 1) / W;
+  static constexpr int kHeadRows = V / kWG;                   // head rows per workgroup: 12 (talker), 8 (code predictor)
+  static constexpr int RW_HEAD = (kHeadRows + W - 1) / W;
+  static constexpr int CH = H / 1024, CQ = kQ / 1024, CI = I / 1024;  // 16-byte chunks per lane per row
+  static constexpr int KVL = 2;                                // K (and V) loads per lane
+  static constexpr int kMaxChunk = 4 * W * KVL;                // positions per attention workgroup: 32 / 64
+  static constexpr int kMaxLen = kMaxChunk * kChunks;          // 1024 / 2048
+  // Prefetch distances. With 4 compute waves every stage's weights for the next layer are held in registers (a
+  // full layer ahead). With 8 compute waves the register budget is 168 per lane and a full layer of 1.7B weights
+  // (96 registers) does not fit beside the rest; each stage's weights are then loaded two or three exchanges
+  // before their use, so no more than o + gate/up + the next K/V are in flight at once: o and gate/up after the
+  // attention of their layer, down and the next layer's qkv after gate/up.
+  static constexpr bool kLate = W == 8;
+  // code-predictor caches short enough for one workgroup to attend over all of them (see Chunk::whole)
+  static __device__ bool whole(int pos) { return CP && pos + 1 <= kMaxChunk; }
+  static_assert(16 % W == 0 && R_GU % W == 0 && R_GU % 2 == 0, "row split");
+};
+
+// LDS of the frame kernel
+template <int H, int I, int W, int V, bool CP>
+struct Lds {
+  static constexpr int XS = I > kQ ? I : kQ;
+  float hin[H];        // residual entering the layer (S1; read back by S4), or the final residual (head)
+  float hmid[H];       // residual after the o projection (S5; read back by S6)
+  float xs[2][XS];     // staged GEMV inputs, alternating so the control wave can fill the next stage's input
+                       // while the compute waves still read the current one: [0] S1/S5/head, [1] S4/S6
+  float qkv[512];      // S2: q0 | q1 | k | v of this workgroup's head
+  float qs[2][SK_HD];  // normalised, rotated, scaled q
+  float kn[SK_HD], vn[SK_HD];
+  float sc[2][Cfg<H, I, W, V, CP>::kMaxChunk];
+  float opart[W][4][16][17];
+  float mrg[kChunks][10];  // S3 inputs per chunk: m, l, o[8] of one q head
+  float pub[64];           // this workgroup's outputs of a stage, published by the last compute wave to finish
+  uint32_t pubcnt;         // compute-wave arrivals at publish (counts up; the wave that makes it a multiple of W
+                           // publishes)
+  float inv;
+  sk_layer_desc desc[Ws::kTraceLayers];  // the layer descriptors, copied once per launch
+  uint64_t cand[W];
+  float hv[16];        // this workgroup's processed logits (sampled picks)
+  int flags[8];
+  int64_t tok;
+  uint32_t pubseq;  // stage publications completed by the compute waves
+};
+
+// Records a timeout: error code, then frame and layer of the stage that gave up (diagnostic words of the workspace).
+struct Ctx;
+__device__ void fail(const Ctx& c, uint32_t code, int f, int l);
+
+// GEMV inputs are staged in LDS swizzled: element i = 16 (L + 64 c) + 4 j + t, which lane L multiplies with byte
+// 4 j + t of its weight chunk c, sits at 16-byte slot (4 c + j) * 64 + L, word t (the natural order puts the lanes
+// of a read 64 bytes apart). The dot reads each slot as two 8-byte halves; measured on the frame kernel this is
+// faster than both 16-byte reads of the same slots and a layout of separate 8-byte slots.
+__device__ __forceinline__ int xsw(int i) {
+  return ((((i >> 10) << 2) | ((i >> 2) & 3)) << 8) | (((i >> 4) & 63) << 2) | (i & 3);
+}
+
+// Loads per lane in one polling round: the whole vector when it fits in 24 (96 registers of the control wave).
+constexpr int mb(int n) { return n / 128 < 16 ? n / 128 : 16; }
+
+// ---- control wave: poll cells into LDS ---------------------------------------------------------------------
+// Waits until cells [idx0, idx0 + n) (n even, idx0 even) all carry epoch e, copying the values to dst.
+// Returns false on timeout or when the global error word is set.
+template <int MAXB, bool SW = false>
+__device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, float* dst, void* ws, int lane,
+                           const Ctx& c, uint32_t code, int f, int l) {
+  for (uint32_t spin = 0;; spin++) {
+    bool ok = true;
+    for (int base = 0; base < n; base += 128 * MAXB) {
+      u32x4 q[MAXB];
+#pragma unroll
+      for (int b = 0; b < MAXB; b++) {
+        const int i = base + 128 * b + 2 * lane;
+        if (i < n) q[b] = get2(cells, idx0 + i);
+      }
+#pragma unroll
+      for (int b = 0; b < MAXB; b++) {
+        const int i = base + 128 * b + 2 * lane;
+        if (i < n) {
+          ok &= q[b].y == e && q[b].w == e;
+          const int o = SW ? xsw(i) : i;  // i even: i + 1 lands at o + 1
+          dst[o] = __uint_as_float(q[b].x);
+          dst[o + 1] = __uint_as_float(q[b].z);
+        }
+      }
+    }
+    if (__all(ok)) return true;
+    if ((spin & 63) == 63) {
+      if (ld_u32_dev(ws, Ws::kErr) != 0) return false;
+      if (spin > kSpinLimit) {
+        if (lane == 0) fail(c, code, f, l);
+        return false;
+      }
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// ---- compute-wave GEMV pieces ------------------------------------------------------------------------------
+// A wave owns RW consecutive rows starting at row0 (wave-uniform); lane reads chunk lane + 64 c of each row.
+// The row scales come with the weights through vector loads (a scalar load would make every later LDS wait,
+// lgkmcnt, wait for it as well) and stay raw bf16 bits until the dot that uses them: converting on arrival would
+// make the wave wait for the load right after issuing it.
+template <int RW, int C>
+__device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], uint16_t (&s)[RW], const int8_t* W, const uint16_t* S,
+                                          int row0, int nvalid, int K, int lane) {
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const int row = r < nvalid ? row0 + r : row0;
+    const uint4* p = (const uint4*)(W + (size_t)row * K);
+#pragma unroll
+    for (int c = 0; c < C; c++) w[r][c] = ld_stream(p + lane + 64 * c);
+    // one ushort load per row: merged wider loads would be split into halves right away, waiting for them
+    s[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), (uint32_t)row * 2u, 0, 0);
+  }
+}
+// y[r] = (row r) . xs, reduced over the wave (uniform result), without the row scale; xs is swizzled (xsw)
+template <int RW, int C>
+__device__ __forceinline__ void dot_rows(const uint4 (&w)[RW][C], const float* xs, int lane, float (&y)[RW]) {
+  float acc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; r++) acc[r] = 0.f;
+  const float2* xs2 = (const float2*)xs;
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {  // one quarter of the chunk (4 bytes per row) at a time: 4 live x registers
+      // two 8-byte LDS reads: 16-byte LDS reads stall the LDS on gfx950 (SQ_LDS_UNALIGNED_STALL; measured
+      // 2250 against 820 cycles for the same 8 KB)
+      const float2 u0 = xs2[2 * ((4 * c + j) * 64 + lane)], u1 = xs2[2 * ((4 * c + j) * 64 + lane) + 1];
+      const float4 v = make_float4(u0.x, u0.y, u1.x, u1.y);
+#pragma unroll
+      for (int r = 0; r < RW; r++) {
+        const uint32_t q = j == 0 ? w[r][c].x : j == 1 ? w[r][c].y : j == 2 ? w[r][c].z : w[r][c].w;
+        float t = (float)(int8_t)q * v.x;
+        t = __builtin_fmaf((float)(int8_t)(q >> 8), v.y, t);
+        t = __builtin_fmaf((float)(int8_t)(q >> 16), v.z, t);
+        t = __builtin_fmaf((float)(int8_t)(q >> 24), v.w, t);
+        acc[r] += t;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; r++) y[r] = wave_sum(acc[r]);
+}
+
+// Publishes a stage's outputs. Every compute wave has left its values in S.pub (lane 0, before the call); the last
+// wave to arrive writes the workgroup's n cells [idx0, idx0 + n) (idx0 and n even) with 16-byte stores, so each
+// line of cells is written by one wave at one time (lines written piecewise by several waves reach the pollers
+// later). There is no barrier: the control wave may be polling the next stage's input meanwhile.
+template <int W, class L>
+__device__ __forceinline__ void publish(L& S, void* cells, uint32_t idx0, int n, uint32_t e, int lane) {
+  uint32_t old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(&S.pubcnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+  old = __builtin_amdgcn_readfirstlane(old);
+  if (old % W == W - 1) {
+    for (int i = 2 * lane; i < n; i += 128) put2(cells, idx0 + i, S.pub[i], S.pub[i + 1], e);
+    if (lane == 0) __hip_atomic_store(&S.pubseq, (old + 1) / W, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+}
+
+// Sleeps n units of 64 shader clocks.
+__device__ __forceinline__ void sleep_units(uint32_t n) {
+  for (uint32_t i = 0; i < n; i++) __builtin_amdgcn_s_sleep(1);
+}
+// Control wave: waits in LDS (no memory traffic) until this workgroup's compute waves have completed `seq` stage
+// publications, then `delay` sleep units more. Bounded: a wait that outlasts ~30 ms falls through and the poll
+// that follows reports the error.
+template <class L>
+__device__ __forceinline__ void after_publish(L& S, uint32_t seq, uint32_t delay) {
+  for (uint32_t i = 0; i < (1u << 20); i++) {
+    if (__hip_atomic_load(&S.pubseq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= seq) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  sleep_units(delay);
+}
+
+// ---- control wave: sampled pick ---------------------------------------------------------------------------
+// Integer wave64 reductions over DPP (every lane's value; the results are wave-uniform).
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ uint32_t dppu(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  v += dppu<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dppu<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dppu<0x124>(v);  // row_ror:4
+  v += dppu<0x128>(v);  // row_ror:8
+  v += dppu<0x142, 0xA>(v);  // row_bcast:15
+  v += dppu<0x143, 0xC>(v);  // row_bcast:31
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dppu<0xB1>(v));
+  v = max(v, dppu<0x4E>(v));
+  v = max(v, dppu<0x124>(v));
+  v = max(v, dppu<0x128>(v));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+// Inclusive prefix sum over the 64 lanes (row_shr within rows of 16, then row_bcast across rows).
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  // Hillis-Steele within each row of 16 (a source lane outside the row reads as 0), then the row totals carried
+  // across rows: lane 15 of rows 0 / 2 into rows 1 / 3, then lane 31 (rows 0-1) into rows 2 and 3
+  v += dppu<0x111>(v);        // row_shr:1
+  v += dppu<0x112>(v);        // row_shr:2
+  v += dppu<0x114>(v);        // row_shr:4
+  v += dppu<0x118>(v);        // row_shr:8
+  v += dppu<0x142, 0xA>(v);  // row_bcast:15
+  v += dppu<0x143, 0xC>(v);  // row_bcast:31
+  return v;
+}
+
+// The largest key t in [lo, hi] whose count c(t) (keys >= t) reaches K, given c(lo) >= K and c(hi + 1) < K. Bits
+// above the highest bit where lo and hi differ are common to every such t; below it the prefix grows one bit at a
+// time, the bit kept when the count at the prefix with the bit set reaches K.
+template <class F>
+__device__ __forceinline__ uint32_t bisect_keys(uint32_t lo, uint32_t hi, uint32_t K, F count) {
+  if (lo >= hi) return lo;
+  const int top = 31 - __builtin_clz(lo ^ hi);
+  uint32_t p = top == 31 ? 0u : lo & ~((2u << top) - 1u);
+  for (int b = top; b >= 0; b--) {
+    const uint32_t t = p | (1u << b);
+    if (count(t) >= K) p = t;
+  }
+  return p;
+}
+
+// Publishes this workgroup's ROWS processed logits (cells vals + ROWS g ..) and their largest order key (cell
+// maxs + g), waits until all V values and the 256 maxima carry epoch e, then draws as the fused sampler does: the
+// key of the top_k-th largest value (ties kept; top_k <= 0 or >= V keeps everything), then the largest
+// v - log(-log u) over the kept values that are not -inf, u from Philox draw `draw` under key `seed`, lowest index
+// on ties, 0 if nothing is kept. Every workgroup computes the same pick from the same V values. Returns the pick,
+// -1 when the error word is set, -2 on timeout.
+//
+// The threshold without a histogram. Lane l holds the maxima of workgroups 2l, 2l+1, 128+2l, 129+2l; for
+// top_k <= 64 the top_k-th largest of the 64 lane maxima is a lower bound lb of the top_k-th largest value (they
+// are 64 of the values). lb is found while the first values are still in flight; as each batch of values arrives
+// the indices of those >= lb are compacted into LDS (ci; the values go to cv by index): a per-lane count, a scan
+// over the lanes, then every lane writes its own run (non-candidates to a trash slot, so no branch). A bisection
+// of the keys then counts, per key t, the candidates >= t; below lb every count is at least top_k, as it is over
+// all values, so it ends on the same key. The kept candidates are compacted once more so each lane draws the
+// Philox noise of at most one of them when at most 64 are kept. Counts are ballots of one comparison each, with
+// the number of comparisons per step fixed outside the bisection (a branch per step costs more than the ballot).
+// Kept out of line (one call per frame) and only in the sampling instantiation of the kernel. The arguments
+// arrive in vector registers under the call convention; they are made wave-uniform first so the control flow stays
+// scalar. `tp` (null unless tracing) receives wall-clock stamps (tp[10..14]) and shader-clock stamps (tp[0..4])
+// after the bound, the gather with the compaction, the bisection, the kept compaction and the draw, and lb and
+// the counts of candidates and kept values (tp[5..7]).
+template <int V, int ROWS>
+__device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t vals_, uint32_t maxs_, int g_,
+                                                          uint32_t e_, const float* hv_, float* cv_, uint32_t* ci_,
+                                                          int top_k_, uint64_t draw_, uint64_t seed_, void* ws_,
+                                                          uint32_t delay_, int lane, uint64_t* tp_) {
+  constexpr int NB = V / 128;  // value cell pairs per lane: lane holds indices 2 lane + 128 b and 2 lane + 128 b + 1
+  constexpr int kBatch = 8;    // cell pairs per lane and batch (a small register footprint)
+  static_assert(V % 128 == 0 && V == ROWS * kWG && ROWS % 2 == 0 && ROWS <= 16, "vocabulary of 256 x ROWS");
+  static_assert(NB % kBatch == 0, "batches");
+  typedef __attribute__((address_space(3))) float lds_f32;
+  typedef __attribute__((address_space(3))) uint16_t lds_u16;
+  char* cells = uniform(cells_);
+  void* ws = uniform(ws_);
+  uint64_t* tp = uniform(tp_);
+  const float* hv = uniform(hv_);
+  lds_f32* cv = (lds_f32*)uniform(cv_);  // LDS arrays: ds_* accesses rather than flat
+  lds_u16* ci = (lds_u16*)uniform(ci_);  // candidate indices [V], then one trash slot per lane
+  const uint32_t vals = __builtin_amdgcn_readfirstlane(vals_), maxs = __builtin_amdgcn_readfirstlane(maxs_);
+  const uint32_t e = __builtin_amdgcn_readfirstlane(e_);
+  const int g = __builtin_amdgcn_readfirstlane(g_);
+  const int top_k = __builtin_amdgcn_readfirstlane(top_k_);
+  const uint32_t delay = __builtin_amdgcn_readfirstlane(delay_);
+  const uint32_t d0 = __builtin_amdgcn_readfirstlane((uint32_t)draw_), d1 = __builtin_amdgcn_readfirstlane((uint32_t)(draw_ >> 32));
+  const uint32_t k0 = __builtin_amdgcn_readfirstlane((uint32_t)seed_), k1 = __builtin_amdgcn_readfirstlane((uint32_t)(seed_ >> 32));
+  const uint64_t draw = ((uint64_t)d1 << 32) | d0;
+
+  // publish: the values, then this workgroup's largest key
+  const float own = lane < ROWS ? hv[lane] : -INFINITY;
+  const uint32_t own_max = wave_max_u32(lane < ROWS ? order_key(own) : 0u);
+  if (lane < ROWS / 2) put2(cells, vals + (uint32_t)(ROWS * g + 2 * lane), hv[2 * lane], hv[2 * lane + 1], e);
+  if (lane == 0) put(cells, maxs + (uint32_t)g, __uint_as_float(own_max), e);
+  sleep_units(delay);
+  u32x4 qa[kBatch], qb[kBatch];  // double buffer: the next batch is in flight while one is waited for and processed
+  auto load_batch = [&](u32x4 (&q)[kBatch], int b0) {
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) q[b] = get2(cells, vals + (uint32_t)(2 * lane + 128 * (b0 + b)));
+  };
+  load_batch(qa, 0);  // in flight while the maxima are polled and the bound is found
+  // the 256 maxima: lane l holds workgroups 2l, 2l+1, 128+2l, 129+2l
+  u32x4 mq[2];
+  for (uint32_t spin = 0;; spin++) {
+    mq[0] = get2(cells, maxs + (uint32_t)(2 * lane));
+    mq[1] = get2(cells, maxs + (uint32_t)(128 + 2 * lane));
+    if (__all(mq[0].y == e && mq[0].w == e && mq[1].y == e && mq[1].w == e)) break;
+    if ((spin & 63) == 63) {
+      if (ld_u32_dev(ws, Ws::kErr) != 0) return -1;
+      if (spin > kSpinLimit) return -2;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  const uint32_t lm = max(max(mq[0].x, mq[0].z), max(mq[1].x, mq[1].z));  // the maxima are order keys already
+  const uint32_t top_key = wave_max_u32(lm);                               // the largest key of all
+  const bool keep_all = top_k <= 0 || top_k >= V;
+  const uint32_t K = (uint32_t)top_k;
+  uint32_t lb = 0;
+  if (!keep_all && top_k <= 64) {
+    const uint32_t lmin = ~wave_max_u32(~lm);  // 64 lane maxima reach the smallest of them, and 64 >= K
+    lb = bisect_keys(lmin, top_key, K, [&](uint32_t t) { return (uint32_t)__popcll(__ballot(lm >= t)); });
+  }
+  if (tp && lane == 0) { tp[10] = (uint64_t)wall_clock64(); tp[0] = (uint64_t)clock64(); }
+  // the values, batch by batch: staged into cv by index, the indices of those >= lb appended to ci
+  uint32_t n = 0;
+  const uint32_t trash = (uint32_t)(V + lane);
+#pragma unroll
+  for (int b0 = 0; b0 < NB; b0 += kBatch) {
+    u32x4 (&q)[kBatch] = (b0 / kBatch) % 2 ? qb : qa;
+    // the next batch goes out before this one is waited for: two batches in flight
+    if (b0 + kBatch < NB) load_batch((b0 / kBatch) % 2 ? qa : qb, b0 + kBatch);
+    for (uint32_t spin = 0;; spin++) {
+      bool ok = true;
+#pragma unroll
+      for (int b = 0; b < kBatch; b++) ok &= q[b].y == e && q[b].w == e;
+      if (__all(ok)) break;
+      if ((spin & 63) == 63) {
+        if (ld_u32_dev(ws, Ws::kErr) != 0) return -1;
+        if (spin > kSpinLimit) return -2;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      load_batch(q, b0);
+    }
+    bool tk[2 * kBatch];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const int i = 2 * lane + 128 * (b0 + b);
+      cv[i] = __uint_as_float(q[b].x);
+      cv[i + 1] = __uint_as_float(q[b].z);
+      tk[2 * b] = order_key(__uint_as_float(q[b].x)) >= lb;
+      tk[2 * b + 1] = order_key(__uint_as_float(q[b].z)) >= lb;
+      cnt += (uint32_t)tk[2 * b] + (uint32_t)tk[2 * b + 1];
+    }
+    const uint32_t incl = wave_incl_scan_u32(cnt);
+    uint32_t at = n + incl - cnt;
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        ci[tk[2 * b + h] ? at : trash] = (uint16_t)(2 * lane + 128 * (b0 + b) + h);
+        at += (uint32_t)tk[2 * b + h];
+      }
+    }
+    n += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  }
+  const int nm = (int)((n + 63) / 64);
+  if (tp && lane == 0) { tp[11] = (uint64_t)wall_clock64(); tp[1] = (uint64_t)clock64(); }
+  uint32_t thr = 0;
+  if (!keep_all) {
+    constexpr int kReg = 4;  // candidate keys held in registers (n <= 256); the rest are read from LDS
+    uint32_t kk[kReg];
+#pragma unroll
+    for (int m = 0; m < kReg; m++) {
+      const uint32_t j = (uint32_t)(lane + 64 * m);
+      kk[m] = j < n ? order_key(cv[ci[j]]) : 0u;  // 0 never counts: every probed key t is at least 1
+    }
+    if (nm <= 1) {
+      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) { return (uint32_t)__popcll(__ballot(kk[0] >= t)); });
+    } else if (nm <= 2) {
+      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
+        return (uint32_t)__popcll(__ballot(kk[0] >= t)) + (uint32_t)__popcll(__ballot(kk[1] >= t));
+      });
+    } else if (nm <= 4) {
+      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
+        return (uint32_t)__popcll(__ballot(kk[0] >= t)) + (uint32_t)__popcll(__ballot(kk[1] >= t)) +
+               (uint32_t)__popcll(__ballot(kk[2] >= t)) + (uint32_t)__popcll(__ballot(kk[3] >= t));
+      });
+    } else {
+      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int m = 0; m < kReg; m++) c += (uint32_t)__popcll(__ballot(kk[m] >= t));
+        for (int m = kReg; m < nm; m++) {
+          const uint32_t j = (uint32_t)(lane + 64 * m);
+          c += (uint32_t)__popcll(__ballot(j < n && order_key(cv[ci[j]]) >= t));
+        }
+        return c;
+      });
+    }
+  }
+  if (tp && lane == 0) { tp[12] = (uint64_t)wall_clock64(); tp[2] = (uint64_t)clock64(); }
+  // the kept candidates (key >= thr, not -inf), compacted in place: a batch writes below its own start or over
+  // itself, after all its lanes have read their entries
+  uint32_t nk = 0;
+  for (int m = 0; m < nm; m++) {
+    const uint32_t j = (uint32_t)(lane + 64 * m);
+    uint32_t i = 0;
+    bool take = false;
+    if (j < n) {
+      i = ci[j];
+      const float x = cv[i];
+      take = order_key(x) >= thr && x != -INFINITY;
+    }
+    const uint64_t msk = __ballot(take);
+    if (take) ci[nk + __builtin_amdgcn_mbcnt_hi((uint32_t)(msk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)msk, 0u))] = (uint16_t)i;
+    nk += (uint32_t)__popcll(msk);
+  }
+  if (tp && lane == 0) { tp[13] = (uint64_t)wall_clock64(); tp[3] = (uint64_t)clock64(); tp[5] = lb; tp[6] = n; tp[7] = nk; }
+  // Gumbel-max: the largest perturbed value, then the lowest index among the lanes that hold it
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (uint32_t j = (uint32_t)lane; j < nk; j += 64) {
+    const int i = (int)ci[j];
+    const float gv = gumbel(cv[i], (uint32_t)i, draw, k0, k1);
+    if (gv > best || (gv == best && i < bi)) { best = gv; bi = i; }
+  }
+  const float gmax = wave_max(best);
+  const uint32_t pick = ~wave_max_u32(best == gmax ? ~(uint32_t)bi : 0u);
+  if (tp && lane == 0) { tp[14] = (uint64_t)wall_clock64(); tp[4] = (uint64_t)clock64(); }
+  return pick == 0x7fffffffu || nk == 0 ? 0 : (int64_t)pick;
+}
+
+// Position bookkeeping of a frame for this workgroup's attention chunk.
+// Positions [t0, t0 + n) of the cache (T = pos + 1 positions) that workgroup r of a head attends over: the cache
+// split 32 ways; the owner of `pos` appends its K/V row.
+struct Chunk {
+  static constexpr bool whole = false;
+  int T, pos, t0, n;
+  __device__ Chunk(int pos_, int r) {
+    pos = pos_;
+    T = pos + 1;
+    const int ch = (T + kChunks - 1) / kChunks;
+    t0 = r * ch;
+    const int t1 = min(T, t0 + ch);
+    n = t1 > t0 ? t1 - t0 : 0;
+  }
+  __device__ bool has_pos() const { return n > 0 && t0 <= pos && pos < t0 + n; }
+};
+// The code predictor's chunk: when `whole` (a cache no longer than one workgroup's capacity) every workgroup of
+// the head attends over the whole cache, so no partials are merged, and workgroup 0 of the head appends the row.
+struct CpChunk {
+  int T, pos, t0, n;
+  bool whole, r0;
+  __device__ CpChunk(int pos_, int r, bool whole_) {
+    pos = pos_;
+    T = pos + 1;
+    const int ch = whole_ ? T : (T + kChunks - 1) / kChunks;
+    t0 = whole_ ? 0 : r * ch;
+    const int t1 = min(T, t0 + ch);
+    n = t1 > t0 ? t1 - t0 : 0;
+    whole = whole_;
+    r0 = r == 0;
+  }
+  __device__ bool has_pos() const { return whole ? r0 : n > 0 && t0 <= pos && pos < t0 + n; }
+};
+template <bool CP>
+using ChunkOf = typename std::conditional<CP, CpChunk, Chunk>::type;
+template <bool CP>
+__device__ __forceinline__ ChunkOf<CP> make_chunk(int pos, int r, bool whole) {
+  if constexpr (CP) return CpChunk(pos, r, whole);
+  else return Chunk(pos, r);
+}
+
+template <int W, int KVL, class Ck>
+__device__ __forceinline__ void load_kv(uint4 (&kr)[KVL], uint4 (&vr)[KVL], const bf16_t* Kh, const bf16_t* Vh,
+                                        const Ck& ck, int w, int g, int sl) {
+// Loads are unconditional, from a position clamped to ck.pos (< max_len): a load under a condition would need a
+// select on its result, and a select makes the wave wait for the load at once. Slots beyond the chunk and the
+// slot of `pos` itself (not written yet) are never read back: the attention code skips or replaces them.
+#pragma unroll
+  for (int i = 0; i < KVL; i++) {
+    const int jj = 4 * W * i + 4 * w + g;
+    const int t = min(ck.t0 + jj, ck.pos);
+    const uint32_t off = (uint32_t)(t * SK_HD + 8 * sl) * 2u;
+    kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Kh)), off, 0, kPolDev));
+    vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Vh)), off, 0, kPolDev));
+  }
+}
+
+__device__ __forceinline__ void unpack8(uint4 a, float* o) {
+  o[0] = bf2f(a.x & 0xffffu); o[1] = bf2f(a.x >> 16); o[2] = bf2f(a.y & 0xffffu); o[3] = bf2f(a.y >> 16);
+  o[4] = bf2f(a.z & 0xffffu); o[5] = bf2f(a.z >> 16); o[6] = bf2f(a.w & 0xffffu); o[7] = bf2f(a.w >> 16);
+}
+
+// Code-predictor launch (CP): per-position inputs and heads. Position 0 takes the vector x0, position g >= 1
+// the row of table emb[g] chosen by the previous code (code 0 for g = 1) and ends in head g; the codes go to
+// d.out. Unused (all null) for the talker.
+struct CpArgs {
+  const float* x0;
+  const void* const* emb;     // [n_positions] device array of bf16 tables; [0] unused
+  const void* const* head_w;  // [n_positions] int8 heads; [0] unused
+  const void* const* head_s;  // [n_positions] bf16 row scales
+  int emb0_rows;              // rows of emb[1] (the range code 0 must lie in)
+};
+
+// Everything a role function needs about this workgroup and launch.
+struct Ctx {
+  sk_talker_desc d;
+  CpArgs cp;
+  void* ws;
+  char* cells;
+  uint32_t x;     // XCD = kv head
+  int r, g;       // rank in the XCD, global workgroup index
+  uint32_t base, tpf;
+  int pos0, n_frames, L;
+  uint64_t seed, cnt0;  // sampled picks: Philox key and the draw counter at launch
+  uint64_t* trace;  // per-stage timestamps of frame 0 (null when tracing is off)
+  uint8_t dl[Ws::kHops];  // poll start delay of each exchange, sleep units
+  __device__ void tr(int role, int f, int l, int ev) const {
+    if (trace && f == 0 && l < Ws::kTraceLayers)
+      trace[(((size_t)g * 2 + role) * Ws::kTraceLayers + l) * Ws::kTraceEvents + ev] = (uint64_t)wall_clock64();
+  }
+  __device__ uint64_t* tslot(int role, int f, int l, int ev) const {  // trace slot address, null when not traced
+    return (trace && f == 0 && l < Ws::kTraceLayers)
+               ? trace + (((size_t)g * 2 + role) * Ws::kTraceLayers + l) * Ws::kTraceEvents + ev
+               : nullptr;
+  }
+  __device__ void tr_clk(int role, int f, int l, int ev) const {  // shader clock counter instead of wall clock
+    if (trace && f == 0 && l < Ws::kTraceLayers)
+      trace[(((size_t)g * 2 + role) * Ws::kTraceLayers + l) * Ws::kTraceEvents + ev] = (uint64_t)clock64();
+  }
+  __device__ uint32_t tick(int f, int l, int s) const {
+    return base + 1u + (uint32_t)f * tpf + (uint32_t)l * 8u + (uint32_t)s;
+  }
+  __device__ const bf16_t* kh(const sk_layer_desc& Ly) const { return (const bf16_t*)Ly.kc + (size_t)x * d.max_len * SK_HD; }
+  __device__ const bf16_t* vh(const sk_layer_desc& Ly) const { return (const bf16_t*)Ly.vc + (size_t)x * d.max_len * SK_HD; }
+};
+
+__device__ void fail(const Ctx& c, uint32_t code, int f, int l) {
+  st_u32_dev(c.ws, Ws::kDiag, code);
+  st_u32_dev(c.ws, Ws::kDiag + 4, (uint32_t)f);
+  st_u32_dev(c.ws, Ws::kDiag + 8, (uint32_t)l);
+  st_u32_dev(c.ws, Ws::kDiag + 12, (uint32_t)c.g);
+  __builtin_amdgcn_s_waitcnt(0);
+  st_u32_dev(c.ws, Ws::kErr, code);
+}
+
+// Barriers of the attention stage after its input has arrived (both roles execute the same count).
+template <class Ck>
+__device__ __forceinline__ int attn_barriers(const Ck& ck) { return 1 + (ck.n > 0 ? 2 : 0); }
+
+// ================================================================================================================
+// Control wave
+// ================================================================================================================
+template <int H, int I, int W, int V, bool CP, bool SMP>
+__device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
+  const Layout LY(H, I);
+  const float eps = c.d.eps;
+  const bf16_t* emb = (const bf16_t*)c.d.emb;
+  int64_t tok = gload(c.d.id0);
+  if (CP && c.g == 0 && lane == 0 && c.d.out) gstore(c.d.out, tok);  // code 0 passes through
+  for (int f = 0; f < c.n_frames; f++) {
+    const int pos = c.pos0 + f;
+    const auto ck = make_chunk<CP>(pos, c.r, Cfg<H, I, W, V, CP>::whole(pos));
+    for (int l = 0; l < c.L; l++) {
+      const sk_layer_desc& Ly = S.desc[l];
+      // the input norm weights, in registers before the poll (lane holds elements lane + 64 k)
+      float nin[H / 64];
+#pragma unroll
+      for (int k = 0; k < H / 64; k++) nin[k] = gload(Ly.in_norm + lane + 64 * k);
+      // S1 input: embedding row (layer 0) or the previous layer's residual, times the input norm
+      bool ok = true;
+      if (lane == 0) c.tr(0, f, l, 0);
+      if (l == 0) {
+        float ev[H / 64];
+        if (CP && f == 0) {
+#pragma unroll
+          for (int k = 0; k < H / 64; k++) ev[k] = gload(c.cp.x0 + lane + 64 * k);
+        } else if (!CP && c.d.in_groups > 0) {
+          // talker_in: the embedding rows of the frame's codes summed in group order, then the pad row
+#pragma unroll
+          for (int k = 0; k < H / 64; k++) ev[k] = 0.f;
+          for (int gi = 0; gi < c.d.in_groups; gi++) {
+            const bf16_t* tab = (const bf16_t*)uniform((const void*)gload(c.d.in_tabs + gi));
+            const int64_t code = gload(c.d.in_codes + gi);
+#pragma unroll
+            for (int k = 0; k < H / 64; k++) ev[k] += bf2f(gload(tab + (size_t)code * H + lane + 64 * k));
+          }
+          const bf16_t* pad = (const bf16_t*)c.d.in_pad;
+#pragma unroll
+          for (int k = 0; k < H / 64; k++) ev[k] += bf2f(gload(pad + lane + 64 * k));
+        } else {
+          const bf16_t* tab = CP ? (const bf16_t*)uniform(gload(c.cp.emb + f)) : emb;
+#pragma unroll
+          for (int k = 0; k < H / 64; k++) ev[k] = bf2f(gload(tab + (size_t)tok * H + lane + 64 * k));
+        }
+#pragma unroll
+        for (int k = 0; k < H / 64; k++) S.hin[lane + 64 * k] = ev[k];
+      } else {
+        after_publish(S, (uint32_t)(f * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
+        ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
+      }
+      float ss = 0.f;
+      for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
+      ss = wave_sum(ss);
+#pragma unroll
+      for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hin[lane + 64 * k] * nin[k];
+      if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[0] = !ok; c.tr(0, f, l, 1); }
+      wg_sync();
+      if (!ok) return;
+      // S2 input: this head's q/k/v
+      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 1u, c.dl[Ws::kHopS2]);
+      ok = poll_cells<mb(512)>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
+      if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
+      wg_sync();
+      if (!ok) return;
+      for (int b = 0; b < attn_barriers(ck); b++) wg_sync();
+      if (lane == 0) c.tr(0, f, l, 3);
+      // S3: merge of the 32 chunk partials for q head 2x + r/16, dims [8 (r % 16), 8 (r % 16) + 8)
+      {
+        const uint32_t e = c.tick(f, l, 1);
+        const int mh = c.r >> 4, md0 = 8 * (c.r & 15);
+        if (!ck.whole) {  // whole-cache attention publishes the S4 input itself
+          sleep_units(c.dl[Ws::kHopS3]);  // the compute waves publish their partial right after the last attention barrier
+          for (uint32_t spin = 0;; spin++) {
+            bool good = true;
+            // per chunk 5 cell pairs: (m, l) of head mh, then 4 pairs of its o slice; all loads issued first
+            constexpr int kItems = kChunks * 5, kPer = (kItems + 63) / 64;
+            u32x4 q[kPer];
+#pragma unroll
+            for (int j = 0; j < kPer; j++) {
+              const int it = min(lane + 64 * j, kItems - 1);
+              const int ch = it / 5, k = it % 5;
+              const uint32_t pb = LY.e2 + (c.x * kChunks + ch) * kPartN;
+              q[j] = get2(c.cells, k == 0 ? pb + 2 * mh : pb + 4 + mh * SK_HD + md0 + 2 * (k - 1));
+            }
+#pragma unroll
+            for (int j = 0; j < kPer; j++) {
+              const int it = lane + 64 * j;
+              if (it < kItems) {
+                const int ch = it / 5, k = it % 5;
+                good &= q[j].y == e && q[j].w == e;
+                S.mrg[ch][2 * k] = __uint_as_float(q[j].x);
+                S.mrg[ch][2 * k + 1] = __uint_as_float(q[j].z);
+              }
+            }
+            if (__all(good)) break;
+            if ((spin & 63) == 63) {
+              if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
+              if (spin > kSpinLimit) { if (lane == 0) fail(c, 13u, f, l); ok = false; break; }
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+          if (lane == 0) c.tr(0, f, l, 8);
+          if (ok) {
+            // lane = chunk + 32 * half: one exp per chunk, then wave reductions; half hh produces dims
+            // md0 + 4 hh .. md0 + 4 hh + 3 (empty chunks carry m = -inf and weigh nothing)
+            static_assert(kChunks == 32, "merge lane mapping");
+            const int ch = lane & 31, hh = lane >> 5;
+            const float mc = S.mrg[ch][0];
+            const float M = wave_max(mc);
+            const float fct = mc == -INFINITY ? 0.f : expf(mc - M);
+            const float Lw = wave_sum(hh == 0 ? fct * S.mrg[ch][1] : 0.f);
+            float od[4];
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+              const float v = row16_sum(fct * S.mrg[ch][2 + 4 * hh + d]);
+              const float h0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+                               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+              const float h1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
+                               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+              od[d] = Lw > 0.f ? (hh ? h1 : h0) / Lw : 0.f;
+            }
+            if (ch == 0) {
+              const uint32_t o0 = LY.e3 + (2 * c.x + mh) * SK_HD + md0 + 4 * hh, e3 = c.tick(f, l, 2);
+              put2(c.cells, o0, od[0], od[1], e3);
+              put2(c.cells, o0 + 2, od[2], od[3], e3);
+            }
+          }
+        }
+        sleep_units(c.dl[Ws::kHopS4]);  // S4 input: the merges of all workgroups, this one's included
+        if (lane == 0) c.tr(0, f, l, 4);
+      }
+      // S4 input: the whole attention output
+      ok = ok && poll_cells<mb(kQ), true>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
+      if (lane == 0) { S.flags[2] = !ok; c.tr(0, f, l, 5); }
+      wg_sync();
+      if (!ok) return;
+      // S5 input: residual after o, times the post-attention norm (loaded while the exchange is under way)
+      float npost[H / 64];
+#pragma unroll
+      for (int k = 0; k < H / 64; k++) npost[k] = gload(Ly.post_norm + lane + 64 * k);
+      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
+      ok = poll_cells<mb(H)>(c.cells, LY.e4, H, c.tick(f, l, 3), S.hmid, c.ws, lane, c, 15u, f, l);
+      ss = 0.f;
+      for (int i = lane; i < H; i += 64) { const float v = S.hmid[i]; ss += v * v; }
+      ss = wave_sum(ss);
+#pragma unroll
+      for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hmid[lane + 64 * k] * npost[k];
+      if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[3] = !ok; c.tr(0, f, l, 6); }
+      wg_sync();
+      if (!ok) return;
+      // S6 input: the whole SwiGLU activation
+      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 3u, c.dl[Ws::kHopS6]);
+      ok = poll_cells<mb(I), true>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+      if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
+      wg_sync();
+      if (!ok) return;
+    }
+    if (CP && f == 0) continue;  // the code predictor's position 0 has no head
+    // head input: final residual times the final norm
+    float nfin[H / 64];
+#pragma unroll
+    for (int k = 0; k < H / 64; k++) nfin[k] = gload(c.d.norm + lane + 64 * k);
+    after_publish(S, (uint32_t)((f + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
+    bool ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
+    float ss = 0.f;
+    for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
+    ss = wave_sum(ss);
+#pragma unroll
+    for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hin[lane + 64 * k] * nfin[k];
+    if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[5] = !ok; }
+    if (!CP && c.d.final_out && c.g == 0 && ok) {  // the final norm's output, h * inv * w (rmsnorm)
+      const float inv = rsqrtf(ss / H + eps);
+#pragma unroll
+      for (int k = 0; k < H / 64; k++) gstore(c.d.final_out + lane + 64 * k, (S.hin[lane + 64 * k] * inv) * nfin[k]);
+    }
+    wg_sync();
+    if (!ok) return;
+    wg_sync();  // candidates (greedy) or processed logits (sampled) of the compute waves are in S.cand / S.hv
+    if (SMP && lane == 0) c.tr(0, f, c.L, 9);
+    if constexpr (SMP) {
+      // every workgroup publishes its processed logits and every control wave draws the same pick from all of them
+      // S.xs[0] and S.xs[1] are free here: the head dot has consumed its input and the compute waves wait
+      const int64_t t = sampled_pick<V, V / kWG>(c.cells, LY.e8, LY.e7, c.g, c.tick(f, c.L, 1), S.hv, S.xs[1],
+                                                 (uint32_t*)S.xs[0], c.d.top_k, c.cnt0 + (uint64_t)(CP ? f - 1 : f),
+                                                 c.seed, c.ws, c.dl[Ws::kHopPick], lane, c.tslot(0, f, c.L, 0));
+      ok = t >= 0;
+      if (ok) tok = t;
+      else if (t == -2 && lane == 0) fail(c, 19u, f, c.L);
+      if (lane == 0) { S.tok = tok; S.flags[6] = !ok; }
+    } else {
+    if (lane == 0) {
+      uint64_t best = 0;
+      for (int i = 0; i < W; i++) best = S.cand[i] > best ? S.cand[i] : best;
+      const uint32_t e = c.tick(f, c.L, 0);
+      put2(c.cells, LY.e7 + 2 * c.g, __uint_as_float((uint32_t)(best >> 32)), __uint_as_float((uint32_t)best), e);
+    }
+    // pick: reduce the 256 candidates
+    {
+      const uint32_t e = c.tick(f, c.L, 0);
+      sleep_units(c.dl[Ws::kHopPick]);
+      uint64_t best = 0;
+      for (uint32_t spin = 0;; spin++) {
+        bool good = true;
+        best = 0;
+        u32x4 q[kWG / 64];
+#pragma unroll
+        for (int j = 0; j < kWG / 64; j++) q[j] = get2(c.cells, LY.e7 + 2 * (lane + 64 * j));
+#pragma unroll
+        for (int j = 0; j < kWG / 64; j++) {
+          good &= q[j].y == e && q[j].w == e;
+          const uint64_t k = ((uint64_t)q[j].x << 32) | q[j].z;
+          best = k > best ? k : best;
+        }
+        if (__all(good)) break;
+        if ((spin & 63) == 63) {
+          if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
+          if (spin > kSpinLimit) { if (lane == 0) fail(c, 18u, f, c.L); ok = false; break; }
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t b = __shfl_xor(best, o);
+        best = b > best ? b : best;
+      }
+      tok = best ? (int64_t)(0xffffffffu - (uint32_t)best) : 0;
+      if (lane == 0) { S.tok = tok; S.flags[6] = !ok; }
+    }
+    }
+    if (SMP && lane == 0) c.tr(0, f, c.L, 15);
+    wg_sync();
+    if (!ok) return;
+    if (c.g == 0 && lane == 0) {
+      // device-side frame state, as the sampler leaves it (qwen3/sampler.py:147-156)
+      if (c.d.out) gstore(c.d.out + f, tok);
+      if (c.d.seen) {
+        // read back by later frames of this launch through device-coherent loads
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)1, make_rsrc(uniform(c.d.seen)), (uint32_t)tok, 0, kPolDev);
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+    }
+  }
+  if (!CP && c.g == 0 && lane == 0) {
+    if (ld_u32_dev(c.ws, Ws::kErr) == 0) {
+      gstore(c.d.id0, tok);
+      if (c.d.next_id0) gstore(c.d.next_id0, tok);
+      gstore(c.d.pos, (int64_t)(c.pos0 + c.n_frames));
+      if (c.d.ngen) gstore(c.d.ngen, gload(c.d.ngen) + (int64_t)c.n_frames);
+    }
+  }
+  if (SMP && c.g == 0 && lane == 0 && ld_u32_dev(c.ws, Ws::kErr) == 0)
+    gstore(c.d.counter, c.cnt0 + (uint64_t)(CP ? c.n_frames - 1 : c.n_frames));
+}
+
+// ================================================================================================================
+// Compute waves
+// ================================================================================================================
+template <int H, int I, int W, int V, bool CP, bool SMP>
+__device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
+  using C = Cfg<H, I, W, V, CP>;
+  const Layout LY(H, I);
+  const float eps = c.d.eps;
+  const int ag = lane >> 4, asl = lane & 15;
+  const int x = (int)c.x, r = c.r, g = c.g;
+  // S1 rows: 512 rows of head x (q of heads 2x, 2x+1, then k and v of head x), 16 per workgroup
+  int qkv_row0;
+  if (r < 16) qkv_row0 = 256 * x + 16 * r;
+  else if (r < 24) qkv_row0 = kQ + 128 * x + 16 * (r - 16);
+  else qkv_row0 = kQ + kNKV * 128 + 128 * x + 16 * (r - 24);
+  const int q_w0 = qkv_row0 + C::RW_QKV * cw;
+  const int o_w0 = C::R_O * g + C::RW_O * cw, o_wn = max(0, min(C::RW_O, C::R_O - C::RW_O * cw));
+  const int gu_w0 = C::R_GU * g + C::RW_GU * cw;
+  const int d_w0 = C::R_D * g + C::RW_D * cw, d_wn = max(0, min(C::RW_D, C::R_D - C::RW_D * cw));
+  const int h_w0 = C::kHeadRows * g + C::RW_HEAD * cw, h_wn = max(0, min(C::RW_HEAD, C::kHeadRows - C::RW_HEAD * cw));
+  // the attention thread mapping uses the first 256 compute threads: head p = t / 128, dim dd = t % 128
+  const int p = tid >> 7, dd = tid & 127;
+  const bool att_thread = tid < 256;
+
+  uint4 wq[C::RW_QKV][C::CH], wo[C::RW_O][C::CQ], wg[C::RW_GU][C::CH], wd[C::RW_D][C::CI];
+  uint16_t sq[C::RW_QKV], so[C::RW_O], sg[C::RW_GU], sd[C::RW_D];  // raw bf16 row scales
+  uint4 kr[C::KVL], vr[C::KVL];
+  // RoPE row (cos, sin of pair `lane`) and the norm weights of dims lane, lane + 64 for this wave's vector in
+  // the next attention (q norm for waves 0, 1, k norm for wave 2; loaded by every compute wave: no select on
+  // loaded values, only on the address)
+  float a_cs = 0.f, a_sn = 0.f, a_n0 = 0.f, a_n1 = 0.f;
+  auto load_attn_vec = [&](const sk_layer_desc& Lx, int posx) {
+    const float* nw = (cw & 3) == 2 ? Lx.kn : Lx.qn;
+    a_cs = gload(c.d.rope + (size_t)posx * SK_HD + lane);
+    a_sn = gload(c.d.rope + (size_t)posx * SK_HD + 64 + lane);
+    a_n0 = gload(nw + lane);
+    a_n1 = gload(nw + 64 + lane);
+  };
+  {
+    const sk_layer_desc& L0 = S.desc[0];
+    load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
+    load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), make_chunk<CP>(c.pos0, r, C::whole(c.pos0)), cw, ag, asl);
+    load_attn_vec(L0, c.pos0);
+    if constexpr (!C::kLate) {
+      load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
+      load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
+      load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
+    }
+  }
+  const bool block_eos0 = c.d.talker_processor && c.d.ngen;
+  const int64_t ngen0 = c.d.ngen ? gload(c.d.ngen) : 0;
+  // Wait once for the first layer's loads. The compiler places one static wait count per use; without this it
+  // would have to allow for the prologue's own load order on every layer, and waits would come out shallow.
+  __builtin_amdgcn_s_waitcnt(0);
+  for (int f = 0; f < c.n_frames; f++) {
+    const int pos = c.pos0 + f;
+    const auto ck = make_chunk<CP>(pos, r, C::whole(pos));
+    for (int l = 0; l < c.L; l++) {
+      const sk_layer_desc& Ly = S.desc[l];
+      const bool last_layer = l == c.L - 1;
+      const sk_layer_desc& Ln = S.desc[last_layer ? 0 : l + 1];
+      // The next layer's weights and K/V are prefetched unconditionally (after the last layer of the last frame
+      // that reloads layer 0, unused): a prefetch under a condition makes the compiler assume it may not have
+      // been issued, and then every later wait for older loads also waits for the younger ones.
+      const int npos = (last_layer && f + 1 < c.n_frames) ? pos + 1 : pos;  // always < max_len
+      // ---- S1: qkv rows -----------------------------------------------------------------------------------
+      wg_sync();
+      if (S.flags[0]) return;
+      if (tid == 0) c.tr(1, f, l, 0);
+      {
+        float y[C::RW_QKV];
+        dot_rows<C::RW_QKV, C::CH>(wq, S.xs[0], lane, y);
+        if (tid == 0) c.tr(1, f, l, 8);
+        const float inv = S.inv;
+        if (lane == 0) {
+#pragma unroll
+          for (int i = 0; i < C::RW_QKV; i++) S.pub[C::RW_QKV * cw + i] = y[i] * bf2f(sq[i]) * inv;
+        }
+        publish<W>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, 16, c.tick(f, l, 0), lane);
+        if (tid == 0) c.tr(1, f, l, 1);
+        if constexpr (!C::kLate) load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+      }
+      // ---- S2: attention over this workgroup's chunk ----------------------------------------------------
+      wg_sync();
+      if (S.flags[1]) return;
+      if (tid == 0) c.tr(1, f, l, 2);
+      {
+        const bool has_pos = ck.has_pos();
+        // (1) one wave per vector, two dims per lane (d and d + 64, the RoPE pair): wave 0 q of head 2x, wave 1 q
+        // of head 2x + 1, wave 2 k, wave 3 v. RMSNorm over the head is a wave reduction, RoPE stays in the lane.
+        // Waves beyond 3 (8 compute waves) compute values that are never stored.
+        {
+          const int vw = cw & 3;
+          const float x0 = S.qkv[vw * SK_HD + lane], x1 = S.qkv[vw * SK_HD + 64 + lane];
+          const float inv = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / SK_HD + eps);
+          const float n0 = x0 * inv * a_n0, n1 = x1 * inv * a_n1;
+          const float r0 = n0 * a_cs - n1 * a_sn, r1 = n1 * a_cs + n0 * a_sn;  // rotate-half RoPE
+          if (cw < 2) {
+            S.qs[cw][lane] = r0 * kInvSqrtHd;
+            S.qs[cw][lane + 64] = r1 * kInvSqrtHd;
+          } else if (cw < 4) {
+            // k (normalised, rotated) or v (as is), rounded to the cache's bf16; the owner of pos appends them
+            // (device-coherent: later frames read them from other workgroups)
+            const float y0 = bf2f(f2bf(cw == 2 ? r0 : x0)), y1 = bf2f(f2bf(cw == 2 ? r1 : x1));
+            float* dst = cw == 2 ? S.kn : S.vn;
+            dst[lane] = y0;
+            dst[lane + 64] = y1;
+            if (has_pos) {
+              const __amdgpu_buffer_rsrc_t rs = make_rsrc(uniform(cw == 2 ? c.kh(Ly) : c.vh(Ly)));
+              const uint32_t off = (uint32_t)(pos * SK_HD + lane) * 2u;
+              __builtin_amdgcn_raw_buffer_store_b16(f2bf(y0), rs, off, 0, kPolDev);
+              __builtin_amdgcn_raw_buffer_store_b16(f2bf(y1), rs, off + 128u, 0, kPolDev);
+            }
+          }
+        }
+        wg_sync();  // attention barrier 1
+        float m = -INFINITY, lsum = 0.f, o = 0.f;
+        if (ck.n > 0) {
+          // (2) scores of this chunk's positions (kr from the prefetch; the new position from LDS)
+          {
+            float q0[8], q1[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) { q0[e] = S.qs[0][8 * asl + e]; q1[e] = S.qs[1][8 * asl + e]; }
+#pragma unroll
+            for (int i = 0; i < C::KVL; i++) {
+              const int jj = 4 * W * i + 4 * cw + ag;
+              float k8[8];
+              if (jj < ck.n && ck.t0 + jj == pos) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) k8[e] = S.kn[8 * asl + e];
+              } else {
+                unpack8(kr[i], k8);
+              }
+              float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+              for (int e = 0; e < 8; e++) { s0 = __builtin_fmaf(q0[e], k8[e], s0); s1 = __builtin_fmaf(q1[e], k8[e], s1); }
+              s0 = row16_sum(s0);
+              s1 = row16_sum(s1);
+              if (asl == 0 && jj < ck.n) { S.sc[0][jj] = s0; S.sc[1][jj] = s1; }
+            }
+          }
+          wg_sync();  // 2
+          // (3) softmax statistics, computed by every wave from the chunk's scores (at most 64 per head)
+          static_assert(C::kMaxChunk <= 64, "one score per lane");
+          const int jl = min(lane, C::kMaxChunk - 1);
+          const float s0l = lane < ck.n ? S.sc[0][jl] : -INFINITY, s1l = lane < ck.n ? S.sc[1][jl] : -INFINITY;
+          const float m0 = wave_max(s0l), m1 = wave_max(s1l);
+          const float l0 = wave_sum(lane < ck.n ? expf(s0l - m0) : 0.f), l1 = wave_sum(lane < ck.n ? expf(s1l - m1) : 0.f);
+          // (4) P V over this thread's positions
+          {
+            float a0[8], a1[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) { a0[e] = 0.f; a1[e] = 0.f; }
+#pragma unroll
+            for (int i = 0; i < C::KVL; i++) {
+              const int jj = 4 * W * i + 4 * cw + ag;
+              if (jj < ck.n) {
+                float v8[8];
+                if (ck.t0 + jj == pos) {
+#pragma unroll
+                  for (int e = 0; e < 8; e++) v8[e] = S.vn[8 * asl + e];
+                } else {
+                  unpack8(vr[i], v8);
+                }
+                const float e0 = expf(S.sc[0][jj] - m0), e1 = expf(S.sc[1][jj] - m1);
+#pragma unroll
+                for (int e = 0; e < 8; e++) { a0[e] = __builtin_fmaf(e0, v8[e], a0[e]); a1[e] = __builtin_fmaf(e1, v8[e], a1[e]); }
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) { S.opart[cw][ag][asl][e] = a0[e]; S.opart[cw][ag][asl][8 + e] = a1[e]; }
+          }
+          wg_sync();  // 3
+          if (att_thread) {
+            m = p ? m1 : m0;
+            lsum = p ? l1 : l0;
+            for (int ww = 0; ww < W; ww++)
+#pragma unroll
+              for (int gg = 0; gg < 4; gg++) o += S.opart[ww][gg][dd >> 3][p * 8 + (dd & 7)];
+          }
+        }
+        if (ck.whole) {
+          // the whole cache in this workgroup: its slice of the S4 input (q head 2x + r/16, dims 8 (r % 16) ..
+          // + 8), normalised, as the merge would write it
+          if (att_thread && p == (r >> 4) && (dd >> 3) == (r & 15))
+            put(c.cells, LY.e3 + (2 * x + p) * SK_HD + dd, lsum > 0.f ? o / lsum : 0.f, c.tick(f, l, 2));
+        } else if (att_thread) {
+          // publish the partial: [m0 l0 m1 l1 | o0[128] | o1[128]]
+          const uint32_t pb = LY.e2 + ((uint32_t)x * kChunks + r) * kPartN;
+          const uint32_t e = c.tick(f, l, 1);
+          if (dd == 0) { put(c.cells, pb + 2 * p, m, e); put(c.cells, pb + 2 * p + 1, lsum, e); }
+          put(c.cells, pb + 4 + p * SK_HD + dd, o, e);
+        }
+        if (tid == 0) c.tr(1, f, l, 3);
+        load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
+        load_attn_vec(Ln, npos);
+        if constexpr (C::kLate) {
+          load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
+          load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+        }
+      }
+      // ---- S4: o projection rows, added to the layer's input residual ------------------------------------
+      wg_sync();
+      if (S.flags[2]) return;
+      if (tid == 0) c.tr(1, f, l, 4);
+      {
+        float y[C::RW_O];
+        if (tid == 0) c.tr_clk(1, f, l, 14);
+        dot_rows<C::RW_O, C::CQ>(wo, S.xs[1], lane, y);
+        if (tid == 0) c.tr(1, f, l, 9);
+        if (tid == 0) c.tr_clk(1, f, l, 15);
+        if (lane == 0) {
+#pragma unroll
+          for (int i = 0; i < C::RW_O; i++)
+            if (i < o_wn) S.pub[C::RW_O * cw + i] = S.hin[o_w0 + i] + y[i] * bf2f(so[i]);
+        }
+        publish<W>(S, c.cells, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
+        if (tid == 0) c.tr(1, f, l, 5);
+        if constexpr (!C::kLate) load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
+      }
+      // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
+      wg_sync();
+      if (S.flags[3]) return;
+      if (tid == 0) c.tr(1, f, l, 12);
+      {
+        float y[C::RW_GU];
+        dot_rows<C::RW_GU, C::CH>(wg, S.xs[0], lane, y);
+        if (tid == 0) c.tr(1, f, l, 10);
+        const float inv = S.inv;
+        if (lane == 0) {
+#pragma unroll
+          for (int i = 0; i < C::RW_GU; i += 2)
+            S.pub[(C::RW_GU * cw + i) / 2] = silu_mul(y[i] * bf2f(sg[i]) * inv, y[i + 1] * bf2f(sg[i + 1]) * inv);
+        }
+        publish<W>(S, c.cells, LY.e5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
+        if (tid == 0) c.tr(1, f, l, 6);
+        if constexpr (C::kLate) {
+          load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
+          load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+        } else {
+          load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
+        }
+      }
+      // ---- S6: down rows, added to the residual after o --------------------------------------------------
+      wg_sync();
+      if (S.flags[4]) return;
+      if (tid == 0) c.tr(1, f, l, 13);
+      {
+        float y[C::RW_D];
+        dot_rows<C::RW_D, C::CI>(wd, S.xs[1], lane, y);
+        if (tid == 0) c.tr(1, f, l, 11);
+        if (lane == 0) {
+#pragma unroll
+          for (int i = 0; i < C::RW_D; i++) {
+            if (i < d_wn) {
+              const float hv = S.hmid[d_w0 + i] + y[i] * bf2f(sd[i]);
+              S.pub[C::RW_D * cw + i] = hv;
+              if (c.d.layer_out && f == c.n_frames - 1) gstore(c.d.layer_out + (size_t)l * H + d_w0 + i, hv);
+            }
+          }
+        }
+        publish<W>(S, c.cells, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
+        if (tid == 0) c.tr(1, f, l, 7);
+        if constexpr (!C::kLate) load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
+      }
+    }
+    if (CP && f == 0) {  // the code predictor's position 0 has no head
+      __builtin_amdgcn_s_waitcnt(0);  // same drain as after a head (see below)
+      continue;
+    }
+    // ---- head rows (loaded now; the final residual is a full layer away), processor, local argmax ----------
+    uint4 wh[C::RW_HEAD][C::CH];
+    uint16_t sh[C::RW_HEAD];
+    const int8_t* hw = CP ? (const int8_t*)uniform(gload(c.cp.head_w + f)) : (const int8_t*)c.d.head_w;
+    const uint16_t* hsc = CP ? (const uint16_t*)uniform(gload(c.cp.head_s + f)) : c.d.head_s;
+    load_rows<C::RW_HEAD, C::CH>(wh, sh, hw, hsc, h_w0, h_wn, H, lane);
+    wg_sync();
+    if (S.flags[5]) return;
+    {
+      float y[C::RW_HEAD];
+      dot_rows<C::RW_HEAD, C::CH>(wh, S.xs[0], lane, y);
+      const float inv = S.inv;
+      const bool block_eos = block_eos0 && (ngen0 + f) < c.d.min_new;
+      uint64_t best = 0;
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < C::RW_HEAD; i++) {
+          if (i >= h_wn) break;
+          const int row = h_w0 + i;
+          float v = y[i] * bf2f(sh[i]) * inv;
+          if (c.d.logits && f == c.n_frames - 1) gstore(c.d.logits + row, v);
+          if (c.d.talker_processor) {
+            if (c.d.seen && ((ld_u32_dev(uniform(c.d.seen), (uint32_t)row & ~3u) >> (8 * (row & 3))) & 0xffu))
+              v = v < 0.f ? v * c.d.rep_pen : v / c.d.rep_pen;
+            if (c.d.suppress && gload(c.d.suppress + row)) v = -INFINITY;
+            if (block_eos && row == c.d.eos) v = -INFINITY;
+          }
+          if constexpr (SMP) S.hv[row - C::kHeadRows * g] = v * c.d.inv_temp;
+          else if (v == v) { const uint64_t k = pick_key(v, row); best = k > best ? k : best; }
+        }
+        S.cand[cw] = best;
+      }
+    }
+    wg_sync();  // candidates ready for the control wave
+    wg_sync();  // pick done
+    if (S.flags[6]) return;
+    // The head dot already waited for the youngest loads; draining here keeps the next frame's first layer from
+    // inheriting a shallow wait count from this path.
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+}
+
+// SMP: sampled picks (do_sample != 0). The greedy instantiation carries none of the sampling code, whose call and
+// registers would otherwise weigh on the control loop of every greedy frame.
+template <int H, int I, int W, int V, bool CP, bool SMP>
+__global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArgs cp, int n_frames) {
+  extern __shared__ char smem_raw[];
+  Lds<H, I, W, V, CP>& S = *(Lds<H, I, W, V, CP>*)smem_raw;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  void* ws = d.workspace;
+  // ---- placement: XCD from hardware, dense rank from an arrival counter ------------------------------------
+  __shared__ int s_rank;
+  __shared__ uint32_t s_base;
+  const uint32_t x = xcc_id();
+  if (tid == 0) {
+    const uint32_t launch = ld_u32_dev(ws, Ws::kLaunch);
+    const uint32_t old = __hip_atomic_fetch_add((uint32_t*)((char*)ws + Ws::kCensus + 4 * (x & 7)), 1u,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int r = (int)(old - launch * kPerXcd);
+    if (x >= kXcd || r < 0 || r >= kPerXcd) {
+      st_u32_dev(ws, Ws::kErr, 2u);
+      r = -1;
+    }
+    // every position this launch writes must lie inside the cache, and the start token inside the vocabulary
+    const int64_t pos0 = d.pos ? gload(d.pos) : 0, tok0 = gload(d.id0);
+    bool bad = pos0 < 0 || pos0 + n_frames > d.max_len || tok0 < 0 || tok0 >= (CP ? cp.emb0_rows : d.vocab);
+    if (!CP)
+      for (int gi = 0; gi < d.in_groups; gi++) {  // talker_in codes: code 0 in the talker vocabulary, the rest in in_rows
+        const int64_t cg = gload(d.in_codes + gi);
+        bad |= cg < 0 || cg >= (gi == 0 ? d.vocab : d.in_rows);
+      }
+    if (bad) {
+      st_u32_dev(ws, Ws::kErr, 5u);
+      r = -1;
+    }
+    s_rank = r;
+    s_base = ld_u32_dev(ws, Ws::kTick);
+    for (int i = 0; i < 8; i++) S.flags[i] = 0;
+    S.pubcnt = 0;
+    S.pubseq = 0;
+  }
+  __syncthreads();
+  const int r = s_rank;
+  if (r < 0) return;
+  Ctx c;
+  c.d = d;
+  c.cp = cp;
+  c.ws = ws;
+  c.cells = (char*)ws + Ws::kCells;
+  c.x = x;
+  c.r = r;
+  c.g = (int)x * kPerXcd + r;
+  c.base = s_base;
+  c.tpf = (uint32_t)d.n_layers * 8u + 8u;
+  c.pos0 = d.pos ? (int)gload(d.pos) : 0;
+  // read before this workgroup publishes anything: workgroup 0 advances the counter once every pick is done
+  c.seed = SMP ? gload(d.seed) : 0;
+  c.cnt0 = SMP ? gload(d.counter) : 0;
+  c.n_frames = n_frames;
+  c.L = d.n_layers;
+  for (int i = tid; i < d.n_layers * (int)(sizeof(sk_layer_desc) / 8); i += blockDim.x)
+    ((uint64_t*)S.desc)[i] = gload((const uint64_t*)d.layers + i);
+  __syncthreads();
+  {
+    // default start delays per exchange (tuned on the 0.6B talker), overridable through the workspace
+    constexpr uint8_t kDefault[Ws::kHops] = {17, 23, 35, 23, 17, 32, 26, 20};
+    const uint32_t w0 = ld_u32_dev(ws, Ws::kPollDelay), w1 = ld_u32_dev(ws, Ws::kPollDelay + 4);
+#pragma unroll
+    for (int h = 0; h < Ws::kHops; h++) {
+      const uint32_t v = ((h < 4 ? w0 : w1) >> (8 * (h & 3))) & 0xffu;
+      c.dl[h] = v ? (uint8_t)(v - 1) : kDefault[h];
+    }
+  }
+  c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
+  if (wave == W) run_control<H, I, W, V, CP, SMP>(c, S, lane);
+  else run_compute<H, I, W, V, CP, SMP>(c, S, wave, tid, lane);
+  // ---- end of launch: epoch base and launch count (workgroup 0; every workgroup finished its census) --------
+  if (c.g == 0 && tid == 0) {
+    st_u32_dev(ws, Ws::kTick, c.base + (uint32_t)n_frames * c.tpf);
+    st_u32_dev(ws, Ws::kLaunch, ld_u32_dev(ws, Ws::kLaunch) + 1u);
+  }
+}
+template <int H, int I, int W, int V, bool CP, bool SMP>
+int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
+  const size_t lds = sizeof(Lds<H, I, W, V, CP>) < 96 * 1024 ? 96 * 1024 : sizeof(Lds<H, I, W, V, CP>);  // one workgroup per CU
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipFuncSetAttribute((const void*)k_frames<H, I, W, V, CP, SMP>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp, n_frames);
+  return sk_check_launch(hipGetLastError(), "sk_talker_frames");
+}
+template <int H, int I, int W, int V, bool CP>
+int launch_frames(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
+  if (d->max_len > Cfg<H, I, W, V, CP>::kMaxLen) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: max_len too long");
+  return d->do_sample ? launch_kernel<H, I, W, V, CP, true>(d, cp, n_frames, st)
+                      : launch_kernel<H, I, W, V, CP, false>(d, cp, n_frames, st);
+}
+
+}  // namespace
