@@ -244,6 +244,8 @@ WORKLOADS = {
     "tiny": dict(shape="tiny", n_layers=2, kv=24, frames=8),
     # two 0.6B-shaped layers (the persistent frame kernel needs the real head counts)
     "small06b": dict(shape="0.6b", n_layers=2, kv=40, frames=8),
+    # two 1.7B-shaped layers (the frame kernel's 8-compute-wave variant)
+    "small17b": dict(shape="1.7b", n_layers=2, kv=40, frames=8),
     # code predictor: 5 layers of the 0.6B shape, 2048-way heads, 16 positions (KV 1 -> 16) per frame, greedy
     # sub-codes; a step is `frames` code-predictor frames with different (x0, code 0)
     "cp06b": dict(shape="0.6b", n_layers=5, vocab=2048, kv=0, positions=16, frames=8),

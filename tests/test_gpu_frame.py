@@ -26,14 +26,15 @@ def _engine(name, seed, gpu):
     return eng, tok
 
 
-def test_small_model_against_oracle(gpu):
-    """Two 0.6B-shaped layers: 8 frames in one launch against the oracle, then per-layer residuals."""
+@pytest.mark.parametrize("name", ["small06b", "small17b"])
+def test_small_model_against_oracle(gpu, name):
+    """Two 0.6B- or 1.7B-shaped layers: 8 frames in one launch against the oracle, then per-layer residuals."""
     from oracle.workload import talker_oracle
 
-    print("small06b: persistent kernel, 8 frames in one launch", flush=True)
-    spec = syn.WORKLOADS["small06b"]
-    eng, tok = _engine("small06b", 2, gpu)
-    orc, otok, s = talker_oracle("small06b", 2, "i8row")
+    print(f"{name}: persistent kernel, 8 frames in one launch", flush=True)
+    spec = syn.WORKLOADS[name]
+    eng, tok = _engine(name, 2, gpu)
+    orc, otok, s = talker_oracle(name, 2, "i8row")
     assert otok == tok
     layer_out = []
     ref_codes, ref_logits = [], None
@@ -173,16 +174,17 @@ def _sampled_oracle(name, seed, tok, key, frames, top_k, eos, cnt0=0):
     return out
 
 
-@pytest.mark.parametrize("top_k", [50, 0, 1, 64, 100])
-def test_sampled_frames_one_launch_against_oracle(gpu, top_k):
+@pytest.mark.parametrize("top_k,name", [(50, "small06b"), (0, "small06b"), (1, "small06b"), (64, "small06b"),
+                                         (100, "small06b"), (50, "small17b")])
+def test_sampled_frames_one_launch_against_oracle(gpu, top_k, name):
     """Sampled picks inside the persistent kernel: 24 frames in one launch with the talker processor, every code
     equal to the oracle's draw (Philox key from torch's generator, draw counter = frame index); top_k 0 keeps the
     whole vocabulary, top_k 1 reduces to the argmax of the processed logits, 64 is the largest top_k with the
     lane-maxima bound and 100 takes the unbounded path (every value a candidate). The counter advances by the
     frames."""
     F = 24
-    print(f"small06b: {F} sampled frames (top_k {top_k}) in one launch against the oracle", flush=True)
-    eng, tok = _sampled_engine(gpu, top_k, frames=F)
+    print(f"{name}: {F} sampled frames (top_k {top_k}) in one launch against the oracle", flush=True)
+    eng, tok = _sampled_engine(gpu, top_k, name=name, frames=F)
     torch.manual_seed(5 + top_k)
     key = int(torch.randint(0, 2**62, (1,)).item())
     eng.fs.set_seed(key)
@@ -190,11 +192,11 @@ def test_sampled_frames_one_launch_against_oracle(gpu, top_k):
     torch.cuda.synchronize()
     assert eng.frame_error() == 0, eng.frame_diag()
     codes = eng.frame_ids[:F].cpu().tolist()
-    ref = _sampled_oracle("small06b", 2, tok, key, F, top_k, eng.eos)
+    ref = _sampled_oracle(name, 2, tok, key, F, top_k, eng.eos)
     print(f"  codes {codes[:8]}..., {len(set(codes))} distinct", flush=True)
     assert codes == ref
     assert int(eng.fs.counter.item()) == F
-    assert int(eng.ngen.item()) == 1 + F and int(eng.pos.item()) == syn.WORKLOADS["small06b"]["kv"] + F
+    assert int(eng.ngen.item()) == 1 + F and int(eng.pos.item()) == syn.WORKLOADS[name]["kv"] + F
     assert int(eng.next_id0.item()) == ref[-1]
     if top_k != 1:
         assert len(set(codes)) > 3
