@@ -1,5 +1,10 @@
-// Entry points of the persistent kernel in talker mode (sk_talker_workspace_size, sk_talker_frames); the kernel
-// itself is in frame_impl.h.
+// Entry points of the persistent kernel in talker mode (sk_talker_workspace_size, sk_talker_frames) and the 0.6B
+// talker's instantiations; the kernel itself is in frame_impl.h. The 1.7B talker runs the instantiations of
+// frame17.hip (polls staged through LDS); its instantiations here, with the register polls, are the comparison
+// point (SOKUTOU_TALKER_POLL=regs). They also keep this module as the 0.6B kernels were tuned in: their register
+// allocation changes with what else the module holds, and measured 2.5% slower without them.
+#include <cstdlib>
+#include <cstring>
 #include "frame_impl.h"
 
 extern "C" int64_t sk_talker_workspace_size(int hidden, int inter) {
@@ -30,6 +35,10 @@ extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* str
   hipStream_t st = (hipStream_t)stream;
   const CpArgs none{};
   if (d->hidden == 1024 && d->inter == 3072) return launch_frames<1024, 3072, 4, kTalkerV, false>(d, none, n_frames, st);
-  if (d->hidden == 2048 && d->inter == 6144) return launch_frames<2048, 6144, 8, kTalkerV, false>(d, none, n_frames, st);
+  if (d->hidden == 2048 && d->inter == 6144) {
+    const char* poll = std::getenv("SOKUTOU_TALKER_POLL");
+    if (poll && !std::strcmp(poll, "regs")) return launch_frames<2048, 6144, 8, kTalkerV, false>(d, none, n_frames, st);
+    return sk_talker_frames_2048(d, n_frames, st);
+  }
   return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: shapes other than the 0.6B / 1.7B talker");
 }

@@ -26,12 +26,15 @@ def _engine(name, seed, gpu):
     return eng, tok
 
 
-@pytest.mark.parametrize("name", ["small06b", "small17b"])
-def test_small_model_against_oracle(gpu, name):
-    """Two 0.6B- or 1.7B-shaped layers: 8 frames in one launch against the oracle, then per-layer residuals."""
+@pytest.mark.parametrize("name,poll", [("small06b", None), ("small17b", None), ("small17b", "regs")])
+def test_small_model_against_oracle(gpu, name, poll, monkeypatch):
+    """Two 0.6B- or 1.7B-shaped layers: 8 frames in one launch against the oracle, then per-layer residuals. The
+    1.7B shape runs the LDS-staged polls, and with SOKUTOU_TALKER_POLL=regs the register polls."""
     from oracle.workload import talker_oracle
 
-    print(f"{name}: persistent kernel, 8 frames in one launch", flush=True)
+    if poll:
+        monkeypatch.setenv("SOKUTOU_TALKER_POLL", poll)
+    print(f"{name}: persistent kernel ({poll or 'default'} polls), 8 frames in one launch", flush=True)
     spec = syn.WORKLOADS[name]
     eng, tok = _engine(name, 2, gpu)
     orc, otok, s = talker_oracle(name, 2, "i8row")
