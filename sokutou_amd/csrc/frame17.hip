@@ -65,6 +65,10 @@ __device__ __forceinline__ bool poll_cells_lds(const void* cells, uint32_t idx0,
 }
 
 constexpr int kH = 2048, kI = 6144;
+template <>
+struct SpreadLate<kH, kI> {
+  static constexpr bool value = true;
+};
 static_assert(sizeof(Lds<kH, kI, 8, kTalkerV, false>) + sizeof(g_poll_raw) + 64 <= 160 * 1024, "LDS over 160 KB");
 static_assert(kI <= kRawCells && kH <= kRawCells && kQ <= kRawCells, "poll staging too small");
 

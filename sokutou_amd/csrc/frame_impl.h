@@ -126,6 +126,14 @@ __device__ __forceinline__ uint64_t pick_key(float v, int i) {
   return ((uint64_t)k << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
 }
 
+// Spread late prefetch (8 compute waves only): gate/up in two halves (after the attention and after the o
+// projection), down after gate/up, the next qkv after down, so no exchange waits behind more than 64 KB of weight
+// loads per CU. Off unless a translation unit specialises it for its shape before instantiating the kernel.
+template <int H, int I>
+struct SpreadLate {
+  static constexpr bool value = false;
+};
+
 template <int H, int I, int W, int V, bool CP>
 struct Cfg {
   static constexpr int R_O = H / kWG, R_GU = 2 * I / kWG, R_D = H / kWG;
@@ -143,6 +151,7 @@ struct Cfg {
   // before their use, so no more than o + gate/up + the next K/V are in flight at once: o and gate/up after the
   // attention of their layer, down and the next layer's qkv after gate/up.
   static constexpr bool kLate = W == 8;
+  static constexpr bool kSpread = kLate && SpreadLate<H, I>::value;
   // code-predictor caches short enough for one workgroup to attend over all of them (see Chunk::whole)
   static __device__ bool whole(int pos) { return CP && pos + 1 <= kMaxChunk; }
   static_assert(16 % W == 0 && R_GU % W == 0 && R_GU % 2 == 0, "row split");
@@ -242,6 +251,20 @@ __device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], uint16_t (&s)[RW], 
 #pragma unroll
     for (int c = 0; c < C; c++) w[r][c] = ld_stream(p + lane + 64 * c);
     // one ushort load per row: merged wider loads would be split into halves right away, waiting for them
+    s[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), (uint32_t)row * 2u, 0, 0);
+  }
+}
+// load_rows for rows [R0, R1) of the wave's RW only
+template <int RW, int C, int R0, int R1>
+__device__ __forceinline__ void load_rows_part(uint4 (&w)[RW][C], uint16_t (&s)[RW], const int8_t* W, const uint16_t* S,
+                                               int row0, int nvalid, int K, int lane) {
+  static_assert(0 <= R0 && R0 < R1 && R1 <= RW, "row range");
+#pragma unroll
+  for (int r = R0; r < R1; r++) {
+    const int row = r < nvalid ? row0 + r : row0;
+    const uint4* p = (const uint4*)(W + (size_t)row * K);
+#pragma unroll
+    for (int c = 0; c < C; c++) w[r][c] = ld_stream(p + lane + 64 * c);
     s[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), (uint32_t)row * 2u, 0, 0);
   }
 }
@@ -1121,7 +1144,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         load_attn_vec(Ln, npos);
         if constexpr (C::kLate) {
           load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
-          load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+          if constexpr (C::kSpread)
+            load_rows_part<C::RW_GU, C::CH, 0, C::RW_GU / 2>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+          else
+            load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
         }
       }
       // ---- S4: o projection rows, added to the layer's input residual ------------------------------------
@@ -1142,6 +1168,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         publish<W>(S, c.cells, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
         if (tid == 0) c.tr(1, f, l, 5);
         if constexpr (!C::kLate) load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
+        if constexpr (C::kSpread)
+          load_rows_part<C::RW_GU, C::CH, C::RW_GU / 2, C::RW_GU>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
       }
       // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
       wg_sync();
@@ -1161,7 +1189,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         if (tid == 0) c.tr(1, f, l, 6);
         if constexpr (C::kLate) {
           load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
-          load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+          if constexpr (!C::kSpread)
+            load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
         } else {
           load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
         }
@@ -1187,6 +1216,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         publish<W>(S, c.cells, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
         if (tid == 0) c.tr(1, f, l, 7);
         if constexpr (!C::kLate) load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
+        if constexpr (C::kSpread)
+          load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
       }
     }
     if (CP && f == 0) {  // the code predictor's position 0 has no head
