@@ -1140,8 +1140,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           put(c.cells, pb + 4 + p * SK_HD + dd, o, e);
         }
         if (tid == 0) c.tr(1, f, l, 3);
-        load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
-        load_attn_vec(Ln, npos);
+        if constexpr (!C::kSpread) {
+          load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
+          load_attn_vec(Ln, npos);
+        }
         if constexpr (C::kLate) {
           load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
           if constexpr (C::kSpread)
@@ -1216,8 +1218,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         publish<W>(S, c.cells, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
         if (tid == 0) c.tr(1, f, l, 7);
         if constexpr (!C::kLate) load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
-        if constexpr (C::kSpread)
+        if constexpr (C::kSpread) {
           load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+          load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
+          load_attn_vec(Ln, npos);
+        }
       }
     }
     if (CP && f == 0) {  // the code predictor's position 0 has no head
