@@ -126,9 +126,10 @@ __device__ __forceinline__ uint64_t pick_key(float v, int i) {
   return ((uint64_t)k << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
 }
 
-// Spread late prefetch (8 compute waves only): gate/up in two halves (after the attention and after the o
-// projection), down after gate/up, the next qkv after down, so no exchange waits behind more than 64 KB of weight
-// loads per CU. Off unless a translation unit specialises it for its shape before instantiating the kernel.
+// Spread late prefetch (8 compute waves only): o after the attention, gate/up after o, down after gate/up, the
+// next layer's qkv and K/V after down. Each stage's weights are then in flight across exactly one exchange, and
+// the registers they occupy are live from one stage to the next only. Off unless a translation unit specialises
+// it for its shape before instantiating the kernel.
 template <int H, int I>
 struct SpreadLate {
   static constexpr bool value = false;
@@ -147,9 +148,9 @@ struct Cfg {
   static constexpr int kMaxLen = kMaxChunk * kChunks;          // 1024 / 2048
   // Prefetch distances. With 4 compute waves every stage's weights for the next layer are held in registers (a
   // full layer ahead). With 8 compute waves the register budget is 168 per lane and a full layer of 1.7B weights
-  // (96 registers) does not fit beside the rest; each stage's weights are then loaded two or three exchanges
-  // before their use, so no more than o + gate/up + the next K/V are in flight at once: o and gate/up after the
-  // attention of their layer, down and the next layer's qkv after gate/up.
+  // (96 registers) does not fit beside the rest; each stage's weights are then loaded one to three exchanges
+  // before their use (kLate): o and gate/up after the attention of their layer, down and the next layer's qkv
+  // after gate/up. kSpread (SpreadLate) moves them later still, one exchange before their use.
   static constexpr bool kLate = W == 8;
   static constexpr bool kSpread = kLate && SpreadLate<H, I>::value;
   // code-predictor caches short enough for one workgroup to attend over all of them (see Chunk::whole)
@@ -251,20 +252,6 @@ __device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], uint16_t (&s)[RW], 
 #pragma unroll
     for (int c = 0; c < C; c++) w[r][c] = ld_stream(p + lane + 64 * c);
     // one ushort load per row: merged wider loads would be split into halves right away, waiting for them
-    s[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), (uint32_t)row * 2u, 0, 0);
-  }
-}
-// load_rows for rows [R0, R1) of the wave's RW only
-template <int RW, int C, int R0, int R1>
-__device__ __forceinline__ void load_rows_part(uint4 (&w)[RW][C], uint16_t (&s)[RW], const int8_t* W, const uint16_t* S,
-                                               int row0, int nvalid, int K, int lane) {
-  static_assert(0 <= R0 && R0 < R1 && R1 <= RW, "row range");
-#pragma unroll
-  for (int r = R0; r < R1; r++) {
-    const int row = r < nvalid ? row0 + r : row0;
-    const uint4* p = (const uint4*)(W + (size_t)row * K);
-#pragma unroll
-    for (int c = 0; c < C; c++) w[r][c] = ld_stream(p + lane + 64 * c);
     s[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), (uint32_t)row * 2u, 0, 0);
   }
 }
@@ -1146,9 +1133,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         }
         if constexpr (C::kLate) {
           load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
-          if constexpr (C::kSpread)
-            load_rows_part<C::RW_GU, C::CH, 0, C::RW_GU / 2>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
-          else
+          if constexpr (!C::kSpread)
             load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
         }
       }
@@ -1171,7 +1156,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         if (tid == 0) c.tr(1, f, l, 5);
         if constexpr (!C::kLate) load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
         if constexpr (C::kSpread)
-          load_rows_part<C::RW_GU, C::CH, C::RW_GU / 2, C::RW_GU>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+          load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
       }
       // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
       wg_sync();
