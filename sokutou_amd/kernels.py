@@ -556,18 +556,59 @@ class Qwen3Kernels(Qwen3Fast):
         self.pos.fill_(int(pos))
 
     def _start(self, kw: dict) -> int:
-        """Frame state after a prompt whose prefill ran elsewhere: ``prefill_len``, ``first_token`` and, with a code
-        predictor, ``last_hidden`` (the talker's last hidden state after its final norm, which the reference takes
-        from the prefill, qwen3/kernels.py:678-679) and ``tts_pad_embed`` (qwen3/kernels.py:709)."""
+        """Frame state after the prompt. With ``inputs_embeds`` (the reference's generate kwargs) the prompt runs
+        through the talker's Hugging Face modules here (``_prefill_hf``); otherwise the prefill ran elsewhere and
+        ``prefill_len``, ``first_token`` and, with a code predictor, ``last_hidden`` (the talker's last hidden state
+        after its final norm, which the reference takes from the prefill, qwen3/kernels.py:678-679) give its
+        results. ``tts_pad_embed`` as in qwen3/kernels.py:709."""
+        if self.cp is not None and "tts_pad_embed" in kw:
+            self.pad16.copy_(torch.as_tensor(kw["tts_pad_embed"]).reshape(-1).to(self.pad16))
         if "inputs_embeds" in kw:
-            raise NotImplementedError("prompt prefill through Hugging Face modules is not part of this engine")
-        if self.cp is not None:
-            if "last_hidden" in kw:
-                self.ph32.copy_(torch.as_tensor(kw["last_hidden"]).reshape(-1).to(self.ph32))
-            if "tts_pad_embed" in kw:
-                self.pad16.copy_(torch.as_tensor(kw["tts_pad_embed"]).reshape(-1).to(self.pad16))
+            return self._prefill_hf(torch.as_tensor(kw["inputs_embeds"]))
+        if self.cp is not None and "last_hidden" in kw:
+            self.ph32.copy_(torch.as_tensor(kw["last_hidden"]).reshape(-1).to(self.ph32))
         L = int(kw["prefill_len"])
         self.reset(L, int(kw["first_token"]))
+        return L
+
+    def warm_prefill(self, lengths) -> float:
+        """The reference records one prefill graph per prompt length (qwen3/fast.py:287-293); this engine's
+        prefill runs eagerly, so there is nothing to record. Returns the seconds spent: 0.0."""
+        return 0.0
+
+    @torch.no_grad()
+    def _prefill_hf(self, embeds: torch.Tensor) -> int:
+        """The prompt (1, L, H) through the talker's Hugging Face modules, as the reference's _prefill_body
+        (qwen3/fast.py:251-263): one forward pass over positions 0..L-1 with a fresh cache, whose keys and values
+        are then written into this engine's cache (positions [0, L), in the cache's dtype; the reference shares
+        the StaticCache tensors instead, qwen3/kernels.py:695-703); the first code from the last hidden state through
+        the codec head, the processor and the torch-path sampler, as the reference draws it; and the last hidden
+        state (after the final norm) kept for the code predictor (qwen3/kernels.py:653-654). Runs eagerly (the
+        reference replays one captured graph per prompt length)."""
+        from transformers import DynamicCache
+
+        if embeds.dim() != 3 or embeds.shape[0] != 1:
+            raise ValueError(f"inputs_embeds must be (1, L, H), got {tuple(embeds.shape)}")
+        L = int(embeds.shape[1])
+        if L < 1 or L >= self.max_cache:
+            raise ValueError(f"prompt too long ({L} tokens, cache {self.max_cache})")
+        self.seen.zero_()
+        self.ngen.zero_()
+        cache = DynamicCache()
+        out = self.talker.model(inputs_embeds=embeds.to(self.device), past_key_values=cache,
+                                cache_position=torch.arange(L, device=self.device), use_cache=True)
+        hidden = out.last_hidden_state
+        if len(cache.layers) != self.kc.shape[0]:
+            raise RuntimeError("the prefill cache has a different layer count than the talker stack")
+        for i, layer in enumerate(cache.layers):
+            self.kc[i, :, :L].copy_(layer.keys[0])
+            self.vc[i, :, :L].copy_(layer.values[0])
+        head = self.talker.codec_head
+        logits = head(hidden) if callable(head) else torch.nn.functional.linear(hidden, head.weight.to(hidden.dtype))
+        first = _sample(self._process(logits[:, -1, :].to(torch.float32)), self.s.do_sample, self.s.temperature,
+                        self.s.top_k)
+        self.ph32.copy_(hidden[0, -1].float())
+        self.reset(L, int(first.item()))
         return L
 
     @torch.no_grad()

@@ -24,7 +24,7 @@ import torch
 
 _TAGS = {"q": 1, "k": 2, "v": 3, "o": 4, "gate": 5, "up": 6, "down": 7, "in_norm": 8, "post_norm": 9, "q_norm": 10,
          "k_norm": 11, "norm": 12, "head": 13, "emb": 14, "kcache": 15, "vcache": 16, "h": 17, "token": 18,
-         "kvlen": 19}
+         "kvlen": 19, "prompt": 20}
 
 
 @dataclass(frozen=True)
@@ -386,6 +386,56 @@ def make_engine(name: str, seed: int = 0, wd: str = "i8row", device="cuda", grap
     tok = start_token(seed, s)
     eng.reset(w["kv"], tok)
     return eng, tok
+
+
+def hf_talker_model(seed: int, s: TalkerShape, device="cpu"):
+    """transformers' Qwen3Model (fp32, eager attention) holding the seeded synthetic weights of shape ``s``: a
+    runnable stand-in for ``tts.model.talker.model``, for prompts given as ``inputs_embeds``."""
+    from transformers import Qwen3Config, Qwen3Model
+
+    cfg = Qwen3Config(hidden_size=s.hidden, intermediate_size=s.inter, num_attention_heads=s.nq,
+                      num_key_value_heads=s.nkv, head_dim=s.head_dim, rms_norm_eps=s.eps, num_hidden_layers=s.n_layers,
+                      vocab_size=s.vocab, rope_parameters={"rope_type": "default", "rope_theta": s.theta},
+                      attention_bias=False)
+    cfg._attn_implementation = "eager"
+    model = Qwen3Model(cfg).float().eval()
+    final = final_weights(seed, s)
+    with torch.no_grad():
+        for i, layer in enumerate(model.layers):
+            w = layer_weights(seed, i, s)
+            a, m = layer.self_attn, layer.mlp
+            for mod, key in ((a.q_proj, "q"), (a.k_proj, "k"), (a.v_proj, "v"), (a.o_proj, "o"), (m.gate_proj, "gate"),
+                             (m.up_proj, "up"), (m.down_proj, "down"), (a.q_norm, "q_norm"), (a.k_norm, "k_norm"),
+                             (layer.input_layernorm, "in_norm"), (layer.post_attention_layernorm, "post_norm")):
+                mod.weight.copy_(torch.from_numpy(w[key]))
+        model.norm.weight.copy_(torch.from_numpy(final["norm"]))
+        model.embed_tokens.weight.copy_(torch.from_numpy(final["emb"]))
+    return model.to(device)
+
+
+def prompt_embeds(seed: int, s: TalkerShape, L: int) -> np.ndarray:
+    """A prompt of L input rows (1, L, H): N(0, 0.02) rounded to bf16 (as float32), like embedding rows."""
+    return bf16_values(normal(seed, 0, "prompt", (1, L, s.hidden), 0.02))
+
+
+def make_prefill_engine(name: str, seed: int = 0, L: int = 24, frames: int = 8, device="cuda",
+                        frame_kernel: bool | None = False):
+    """A Qwen3Kernels engine whose talker modules are runnable (``hf_talker_model``), an empty cache of
+    L + frames + 1 positions and greedy settings without the processor; the prompt goes in through
+    ``generate_codes({"inputs_embeds": ...})``. Returns (engine, generate kwargs)."""
+    from .fast import Sampling
+    from .kernels import Qwen3Kernels
+
+    s = workload_shape(name)
+    tts = make_tts(seed, s, device=device)
+    tts.model.talker.model = hf_talker_model(seed, s, device)
+    smp = Sampling.greedy(processor=False)
+    eng = Qwen3Kernels(tts, smp, max_cache=L + frames + 1, wd="i8row", graphs=True, sampler="fused",
+                       suppress_tail=0, frame_kernel=frame_kernel)
+    kw = {"inputs_embeds": torch.from_numpy(prompt_embeds(seed, s, L)).to(device), "do_sample": False,
+          "subtalker_dosample": False, "max_new_tokens": smp.max_new_tokens, "repetition_penalty": 1.0,
+          "min_new_tokens": 0}
+    return eng, kw
 
 
 def make_cp_engine(name: str = "cp06b", seed: int = 0, device="cuda"):
