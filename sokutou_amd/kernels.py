@@ -585,6 +585,23 @@ class Qwen3Kernels(Qwen3Fast):
         the codec head, the processor and the torch-path sampler, as the reference draws it; and the last hidden
         state (after the final norm) kept for the code predictor (qwen3/kernels.py:653-654). Runs eagerly (the
         reference replays one captured graph per prompt length)."""
+        L, hidden = self._prefill_run(embeds)
+        self.seen.zero_()
+        self.ngen.zero_()
+        first = _sample(self._process(self._head_logits(hidden)), self.s.do_sample, self.s.temperature, self.s.top_k)
+        self.ph32.copy_(hidden[0, -1].float())
+        self.reset(L, int(first.item()))
+        return L
+
+    def _head_logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        """fp32 (1, V) codec-head logits of the last position of ``hidden`` through the talker's own module."""
+        head = self.talker.codec_head
+        logits = head(hidden) if callable(head) else torch.nn.functional.linear(hidden, head.weight.to(hidden.dtype))
+        return logits[:, -1, :].to(torch.float32)
+
+    def _prefill_run(self, embeds: torch.Tensor) -> tuple[int, torch.Tensor]:
+        """The talker's Hugging Face modules over the prompt (1, L, H) with a fresh cache; its keys and values are
+        written into positions [0, L) of this engine's cache. Returns (L, last_hidden_state)."""
         from transformers import DynamicCache
 
         if embeds.dim() != 3 or embeds.shape[0] != 1:
@@ -592,8 +609,6 @@ class Qwen3Kernels(Qwen3Fast):
         L = int(embeds.shape[1])
         if L < 1 or L >= self.max_cache:
             raise ValueError(f"prompt too long ({L} tokens, cache {self.max_cache})")
-        self.seen.zero_()
-        self.ngen.zero_()
         cache = DynamicCache()
         out = self.talker.model(inputs_embeds=embeds.to(self.device), past_key_values=cache,
                                 cache_position=torch.arange(L, device=self.device), use_cache=True)
@@ -603,13 +618,53 @@ class Qwen3Kernels(Qwen3Fast):
         for i, layer in enumerate(cache.layers):
             self.kc[i, :, :L].copy_(layer.keys[0])
             self.vc[i, :, :L].copy_(layer.values[0])
-        head = self.talker.codec_head
-        logits = head(hidden) if callable(head) else torch.nn.functional.linear(hidden, head.weight.to(hidden.dtype))
-        first = _sample(self._process(logits[:, -1, :].to(torch.float32)), self.s.do_sample, self.s.temperature,
-                        self.s.top_k)
+        return L, hidden
+
+    @torch.no_grad()
+    def teacher_logits(self, kw: dict, codes: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Teacher forcing (qwen3/kernels.py:714-753): the prompt ``kw["inputs_embeds"]`` through the talker's
+        Hugging Face modules, then for each frame f of ``codes`` (frames, G) the code predictor's positions fed the
+        given codes (position 0 the talker's last hidden state, position 1 code 0 in the talker's table, position
+        g >= 2 code g - 1 in table g - 2), the logits of heads 1..G-1, then the talker step on talker_in of the
+        frame's codes at position L + f and its logits. Returns (talker logits (1 + frames, V), code-predictor
+        logits (frames, G - 1, V_cp)), float32 on the CPU. Runs on the per-op kernels: the one-launch kernels pick
+        their own codes. Draws no random numbers and leaves the frame state (``id0``, ``pos``, ``seen``) as the
+        last frame put it, as the reference does."""
+        if self.cp is None:
+            raise ValueError("teacher_logits needs a code predictor")
+        codes = torch.as_tensor(codes)
+        if codes.dim() != 2 or codes.shape[1] != self.G:
+            raise ValueError(f"codes must be (frames, {self.G}), got {tuple(codes.shape)}")
+        if "tts_pad_embed" in kw:
+            self.pad16.copy_(torch.as_tensor(kw["tts_pad_embed"]).reshape(-1).to(self.pad16))
+        L, hidden = self._prefill_run(torch.as_tensor(kw["inputs_embeds"]))
+        if L + codes.shape[0] > self.max_cache:
+            raise ValueError(f"prompt of {L} and {codes.shape[0]} frames exceed the cache ({self.max_cache})")
+        l0 = [self._head_logits(hidden).cpu()]
         self.ph32.copy_(hidden[0, -1].float())
-        self.reset(L, int(first.item()))
-        return L
+        P, lcp = self.C, []
+        ck, cv = list(self.ck.unbind(0)), list(self.cv.unbind(0))
+        cptr = self.codes.data_ptr()
+        for f in range(codes.shape[0]):
+            self.codes.copy_(codes[f].view(1, -1).to(self.codes))
+            self.id0.copy_(self.codes[:, :1])
+            frame = []
+            for g in range(self.G):
+                if g == 0:
+                    self._cp_input(self.ph32)
+                else:
+                    self._embed(self.temb if g == 1 else self.cemb[g - 2], self.id0 if g == 1 else cptr + 8 * (g - 1),
+                                self.e)
+                    self._cp_input(self.e)
+                self._layers(P, self.hc, self.qkv_c, self.att_c, self.act_c, ck, cv, None, g)
+                if g > 0:
+                    self._rms_gemv(self.hc, P.norm, P.eps, self.cp_heads[g - 1], self.logit_c, False)
+                    frame.append(self.logit_c.clone().view(1, -1))
+            self.pos.fill_(L + f)
+            self._talker()  # talker_in of the frame's codes; the final norm's output lands in ph32
+            lcp.append(torch.cat(frame, dim=0).cpu())
+            l0.append(self.logit_t.clone().view(1, -1).cpu())
+        return torch.cat(l0, dim=0), torch.stack(lcp, dim=0)
 
     @torch.no_grad()
     def layer_trace(self, token: int, pos: int) -> list[torch.Tensor]:

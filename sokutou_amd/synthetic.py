@@ -419,15 +419,20 @@ def prompt_embeds(seed: int, s: TalkerShape, L: int) -> np.ndarray:
 
 
 def make_prefill_engine(name: str, seed: int = 0, L: int = 24, frames: int = 8, device="cuda",
-                        frame_kernel: bool | None = False):
+                        frame_kernel: bool | None = False, cp: str | None = None):
     """A Qwen3Kernels engine whose talker modules are runnable (``hf_talker_model``), an empty cache of
-    L + frames + 1 positions and greedy settings without the processor; the prompt goes in through
+    L + frames + 1 positions and greedy settings without the processor; with ``cp`` (a code-predictor workload
+    name) the talker carries that code predictor and the pad row. The prompt goes in through
     ``generate_codes({"inputs_embeds": ...})``. Returns (engine, generate kwargs)."""
     from .fast import Sampling
     from .kernels import Qwen3Kernels
 
     s = workload_shape(name)
-    tts = make_tts(seed, s, device=device)
+    pad = None
+    if cp is None:
+        tts = make_tts(seed, s, device=device)
+    else:
+        tts, pad = make_tts_with_cp(seed, s, workload_shape(cp), device=device)
     tts.model.talker.model = hf_talker_model(seed, s, device)
     smp = Sampling.greedy(processor=False)
     eng = Qwen3Kernels(tts, smp, max_cache=L + frames + 1, wd="i8row", graphs=True, sampler="fused",
@@ -435,6 +440,8 @@ def make_prefill_engine(name: str, seed: int = 0, L: int = 24, frames: int = 8, 
     kw = {"inputs_embeds": torch.from_numpy(prompt_embeds(seed, s, L)).to(device), "do_sample": False,
           "subtalker_dosample": False, "max_new_tokens": smp.max_new_tokens, "repetition_penalty": 1.0,
           "min_new_tokens": 0}
+    if pad is not None:
+        kw["tts_pad_embed"] = torch.from_numpy(pad).to(device)
     return eng, kw
 
 

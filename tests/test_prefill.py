@@ -1,7 +1,8 @@
 """Prompt prefill through the talker's Hugging Face modules (Qwen3Kernels._start with ``inputs_embeds``,
 qwen3/fast.py:251-263): the keys, values and last hidden state that transformers' Qwen3Model leaves for a prompt
 against the oracle run position by position (CPU), then the engine's greedy frames after such a prefill against
-the oracle (GPU, per-op kernels and the persistent frame kernel)."""
+the oracle (GPU, per-op kernels and the persistent frame kernel), and teacher forcing (teacher_logits) against
+greedy generation from the same prompt."""
 
 import numpy as np
 import pytest
@@ -87,3 +88,21 @@ def test_engine_frames_after_hf_prefill(gpu, frame_kernel):
     assert got == ref[: len(got)], (got, ref)
     assert len(got) == frames and int(eng.next_id0.item()) == ref[frames]
     assert int(eng.pos.item()) == L + frames
+
+
+@pytest.mark.gpu
+def test_teacher_logits_reproduce_greedy_frames(gpu):
+    """teacher_logits (qwen3/kernels.py:714-753) fed the codes that greedy generation produced from the same
+    prompt (talker with a 5-layer code predictor, 16 code groups): every talker and code-predictor logits row
+    picks the code that generation chose next, on the per-op kernels against the one-launch kernels."""
+    L, frames = 20, 6
+    print(f"small06b + cp06b: prompt of {L} rows, {frames} greedy frames, then teacher forcing", flush=True)
+    eng, kw = syn.make_prefill_engine("small06b", 4, L, frames, device=gpu, frame_kernel=True, cp="cp06b")
+    assert eng.frame_kernel and eng.cpk is not None
+    codes = eng.generate_codes(kw, max_frames=frames)
+    nxt = int(eng.next_id0.item())
+    assert codes.shape == (frames, 16)
+    l0, lcp = eng.teacher_logits(kw, codes)
+    assert l0.shape == (frames + 1, 3072) and lcp.shape == (frames, 15, 2048)
+    assert l0.argmax(dim=1).tolist() == codes[:, 0].cpu().tolist() + [nxt]
+    assert lcp.argmax(dim=2).tolist() == codes[:, 1:].cpu().tolist()
