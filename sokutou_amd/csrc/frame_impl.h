@@ -1319,15 +1319,17 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   __syncthreads();
   {
     // default start delays per exchange, overridable through the workspace: tuned by coordinate descent on the
-    // 0.6B talker, and on the 1.7B talker for the spread prefetch (longer exchanges; the merge poll starts ~3 us
-    // after the attention)
+    // 0.6B talker, on the 1.7B talker for the spread prefetch (longer exchanges; the merge poll starts ~3 us
+    // after the attention) and on the code predictor (no merge; whole-cache attention)
     constexpr uint8_t kDefault[Ws::kHops] = {17, 23, 35, 23, 17, 32, 26, 20};
     constexpr uint8_t kDefaultSpread[Ws::kHops] = {17, 15, 91, 31, 57, 48, 18, 52};
+    constexpr uint8_t kDefaultCp[Ws::kHops] = {20, 14, 35, 35, 29, 32, 17, 23};
     const uint32_t w0 = ld_u32_dev(ws, Ws::kPollDelay), w1 = ld_u32_dev(ws, Ws::kPollDelay + 4);
 #pragma unroll
     for (int h = 0; h < Ws::kHops; h++) {
       const uint32_t v = ((h < 4 ? w0 : w1) >> (8 * (h & 3))) & 0xffu;
-      c.dl[h] = v ? (uint8_t)(v - 1) : (Cfg<H, I, W, V, CP>::kSpread ? kDefaultSpread[h] : kDefault[h]);
+      c.dl[h] = v ? (uint8_t)(v - 1)
+                  : CP ? kDefaultCp[h] : (Cfg<H, I, W, V, CP>::kSpread ? kDefaultSpread[h] : kDefault[h]);
     }
   }
   c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
