@@ -604,6 +604,8 @@ class Qwen3Kernels(Qwen3Fast):
         written into positions [0, L) of this engine's cache. Returns (L, last_hidden_state)."""
         from transformers import DynamicCache
 
+        if self.talker is None or not callable(getattr(self.talker, "model", None)):
+            raise RuntimeError("prompt prefill needs the talker's runnable Hugging Face modules (tts.model.talker)")
         if embeds.dim() != 3 or embeds.shape[0] != 1:
             raise ValueError(f"inputs_embeds must be (1, L, H), got {tuple(embeds.shape)}")
         L = int(embeds.shape[1])
