@@ -22,8 +22,11 @@ typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 // poll_cells does. Each producer writes its `stride` consecutive cells with one store instruction, so a round
 // first probes the last cell of every producer and reads the whole vector only once all of them carry epoch e (a
 // failed read of the whole vector costs a round trip and the LDS pass). The read itself checks every cell's epoch:
-// the probe only chooses when to read. n is a multiple of 128 and of stride, at most kRawCells; idx0 is even.
-template <bool SW>
+// the probe only chooses when to read. Without PROBE every round reads the whole vector. Measured on the 1.7B
+// talker: the probe pays for the gate/up activation (48 KB per read) and the local q | k | v exchange, and costs
+// 6-9% on the attention output and the o / down outputs (16 KB), which are read whole. n is a multiple of 128 and
+// of stride, at most kRawCells; idx0 is even.
+template <bool SW, bool PROBE = true>
 __device__ __forceinline__ bool poll_cells_lds(const void* cells, uint32_t idx0, int n, int stride, uint32_t e,
                                                float* dst, void* ws, int lane, const Ctx& c, uint32_t code, int f,
                                                int l) {
@@ -31,10 +34,12 @@ __device__ __forceinline__ bool poll_cells_lds(const void* cells, uint32_t idx0,
   const int nprod = n / stride;
   for (uint32_t spin = 0;; spin++) {
     bool ready = true;
-    for (int pr = lane; pr < nprod; pr += 64) {
-      const uint32_t cell = idx0 + (uint32_t)((pr + 1) * stride - 1);
-      const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(cells), cell * 8u, 0, kPolDev);
-      ready &= q.y == e;
+    if constexpr (PROBE) {
+      for (int pr = lane; pr < nprod; pr += 64) {
+        const uint32_t cell = idx0 + (uint32_t)((pr + 1) * stride - 1);
+        const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(cells), cell * 8u, 0, kPolDev);
+        ready &= q.y == e;
+      }
     }
     if (__all(ready)) {
 #pragma unroll 1
@@ -73,10 +78,10 @@ static_assert(sizeof(Lds<kH, kI, 8, kTalkerV, false>) + sizeof(g_poll_raw) + 64 
 static_assert(kI <= kRawCells && kH <= kRawCells && kQ <= kRawCells, "poll staging too small");
 
 // The polls of the 1.7B control wave, by the (MAXB, SW) pair poll_cells is instantiated with:
-//   <mb(512), false>: q | k | v of one kv head, 32 rows of 16 cells, each row published by one workgroup;
-//   <mb(H), false>: o projection or down projection output, H / 256 cells per workgroup;
-//   <mb(I), true> with n = I: gate/up activation, I / 256 cells per workgroup;
-//   <mb(kQ), true> with n = kQ: attention output, 4 cells per merging lane group.
+//   <mb(512), false>: q | k | v of one kv head, 32 rows of 16 cells, each row published by one workgroup (probed);
+//   <mb(H), false>: o projection or down projection output, H / 256 cells per workgroup (read whole);
+//   <mb(I), true> with n = I: gate/up activation, I / 256 cells per workgroup (probed);
+//   <mb(kQ), true> with n = kQ: attention output, 4 cells per merging lane group (read whole).
 static_assert(mb(512) == 4 && mb(kH) == 16 && mb(kI) == 16 && mb(kQ) == 16, "poll instantiations moved");
 template <>
 __device__ bool poll_cells<4, false>(const void* cells, uint32_t idx0, int n, uint32_t e, float* dst, void* ws,
@@ -86,12 +91,13 @@ __device__ bool poll_cells<4, false>(const void* cells, uint32_t idx0, int n, ui
 template <>
 __device__ bool poll_cells<16, false>(const void* cells, uint32_t idx0, int n, uint32_t e, float* dst, void* ws,
                                       int lane, const Ctx& c, uint32_t code, int f, int l) {
-  return poll_cells_lds<false>(cells, idx0, n, n / kWG, e, dst, ws, lane, c, code, f, l);
+  return poll_cells_lds<false, false>(cells, idx0, n, n / kWG, e, dst, ws, lane, c, code, f, l);
 }
 template <>
 __device__ bool poll_cells<16, true>(const void* cells, uint32_t idx0, int n, uint32_t e, float* dst, void* ws,
                                      int lane, const Ctx& c, uint32_t code, int f, int l) {
-  return poll_cells_lds<true>(cells, idx0, n, n == kQ ? 4 : n / kWG, e, dst, ws, lane, c, code, f, l);
+  if (n == kQ) return poll_cells_lds<true, false>(cells, idx0, n, 4, e, dst, ws, lane, c, code, f, l);
+  return poll_cells_lds<true>(cells, idx0, n, n / kWG, e, dst, ws, lane, c, code, f, l);
 }
 
 }  // namespace

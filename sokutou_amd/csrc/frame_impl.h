@@ -1322,7 +1322,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     // 0.6B talker, on the 1.7B talker for the spread prefetch (longer exchanges; the merge poll starts ~3 us
     // after the attention) and on the code predictor (no merge; whole-cache attention)
     constexpr uint8_t kDefault[Ws::kHops] = {17, 23, 35, 23, 17, 32, 26, 20};
-    constexpr uint8_t kDefaultSpread[Ws::kHops] = {17, 15, 91, 31, 57, 48, 18, 52};
+    constexpr uint8_t kDefaultSpread[Ws::kHops] = {53, 3, 91, 55, 51, 36, 0, 46};
     constexpr uint8_t kDefaultCp[Ws::kHops] = {20, 14, 35, 35, 29, 32, 17, 23};
     const uint32_t w0 = ld_u32_dev(ws, Ws::kPollDelay), w1 = ld_u32_dev(ws, Ws::kPollDelay + 4);
 #pragma unroll
