@@ -75,6 +75,11 @@ template <>
 struct SpreadLate<kH, kI> {
   static constexpr bool value = true;
 };
+// the sampled pick with half the value registers in flight: the 168-register budget of 9 waves
+template <>
+struct PickBatch<kTalkerV, kTalkerV / kWG> {
+  static constexpr int value = 4;
+};
 static_assert(sizeof(Lds<kH, kI, 8, kTalkerV, false>) + sizeof(g_poll_raw) + 64 <= 160 * 1024, "LDS over 160 KB");
 static_assert(kI <= kRawCells && kH <= kRawCells && kQ <= kRawCells, "poll staging too small");
 

@@ -389,13 +389,20 @@ __device__ __forceinline__ uint32_t bisect_keys(uint32_t lo, uint32_t hi, uint32
 // scalar. `tp` (null unless tracing) receives wall-clock stamps (tp[10..14]) and shader-clock stamps (tp[0..4])
 // after the bound, the gather with the compaction, the bisection, the kept compaction and the draw, and lb and
 // the counts of candidates and kept values (tp[5..7]).
+// Cell pairs per lane and batch of sampled_pick's value gather (two batches in flight). A translation unit may
+// specialise it before instantiating the kernel, for a smaller register footprint.
+template <int V, int ROWS>
+struct PickBatch {
+  static constexpr int value = 8;
+};
+
 template <int V, int ROWS>
 __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t vals_, uint32_t maxs_, int g_,
                                                           uint32_t e_, const float* hv_, float* cv_, uint32_t* ci_,
                                                           int top_k_, uint64_t draw_, uint64_t seed_, void* ws_,
                                                           uint32_t delay_, int lane, uint64_t* tp_) {
   constexpr int NB = V / 128;  // value cell pairs per lane: lane holds indices 2 lane + 128 b and 2 lane + 128 b + 1
-  constexpr int kBatch = 8;    // cell pairs per lane and batch (a small register footprint)
+  constexpr int kBatch = PickBatch<V, ROWS>::value;  // cell pairs per lane and batch (a small register footprint)
   static_assert(V % 128 == 0 && V == ROWS * kWG && ROWS % 2 == 0 && ROWS <= 16, "vocabulary of 256 x ROWS");
   static_assert(NB % kBatch == 0, "batches");
   typedef __attribute__((address_space(3))) float lds_f32;
