@@ -72,16 +72,19 @@ int sk_embed(const void* table, const int64_t* idx, float* out, int dim, int ct,
 int sk_talker_in(const uint64_t* tabs, const int64_t* codes, const void* pad, float* out, int dim, int G, int ct,
                  void* stream);
 
-/* Bytes of scratch that sk_attn needs for nkv kv heads and caches of max_len positions (per-head arrival counters,
- * then split-K partials). The counters must be zero before the first call; sk_attn leaves them zero. One workspace
- * sized for the longest cache serves calls with any shorter max_len. */
+/* Bytes of scratch that sk_attn needs for nkv kv heads and caches of max_len positions: the error word (bytes 0..3),
+ * per-head arrival counters, then split-K partials. The error word and the counters must be zero before the first
+ * call; sk_attn leaves the counters zero. One workspace sized for the longest cache serves calls with any shorter
+ * max_len. */
 int64_t sk_attn_workspace_size(int nq, int nkv, int max_len);
 
 /* One-token GQA decode attention. qkv is [nq·128 | nkv·128 | nkv·128] fp32; for each kv head: per-head RMSNorm
  * of k (weight kn) and q (weight qn), rotate-half RoPE from rope[pos] = [cos 64 | sin 64], K and V stored at
  * position pos of Kc/Vc ([nkv][max_len][128], element type ct), q scaled by 1/sqrt(128), softmax over positions
  * 0..pos, out = [nq·128] fp32. pos = (pos_ptr ? *pos_ptr : 0) + pos_add, read on the device. nq == 2·nkv.
- * The cache length is split across blocks and merged with a log-sum-exp (online softmax) combine.
+ * The cache length is split across blocks and merged with a log-sum-exp (online softmax) combine. A position
+ * outside [0, max_len) sets the workspace's error word to 5 (it stays set until the caller clears it) and the call
+ * reads and writes nothing else.
  * Replaces attn(qkv, qn, kn, eps, rope, Kc, Vc, pos_ptr, pos_add, max_len, nq, nkv, out)
  * (qwen3/kernels.py:341-414). */
 int sk_attn(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc, void* Vc,

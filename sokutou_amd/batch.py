@@ -123,8 +123,22 @@ class BatchedTalker:
         _lib.check(_lib.load().sk_batch_frame(ctypes.byref(self._desc), _lib.stream()), "sk_batch_frame")
 
     def capture(self) -> None:
-        """Records one step as a HIP graph (after one eager warm-up step whose effects are undone by the caller's
-        next ``reset``)."""
+        """Records one step as a HIP graph. One eager warm-up step runs first on a side stream (first-use set-up
+        stays out of the graph); then positions, tokens, pick counts and the error word are restored and the inputs
+        re-embedded from the restored tokens, so capturing leaves the streams where they were (the warm-up's cache
+        row at each stream's position is rewritten by the next step)."""
+        saved = [t.clone() for t in (self.pos, self.ids, self.nstep)]
+        err = self.ws[:4].clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.step()
+        torch.cuda.current_stream().wait_stream(side)
+        for t, v in zip((self.pos, self.ids, self.nstep), saved):
+            t.copy_(v)
+        self.ws[:4].copy_(err)
+        _lib.check(_lib.load().sk_batch_embed(ctypes.byref(self._desc), _lib.stream()), "sk_batch_embed")
+        torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             self.step()

@@ -34,11 +34,12 @@ int nsplit_for(int max_len) {
   int n = (max_len + 15) / 16;
   return n < 1 ? 1 : (n > kSplitMax ? kSplitMax : n);
 }
-int64_t part_bytes(int nkv, int nsplit) { return ((int64_t)nkv * 2 * nsplit * kPart * 4 + 255) / 256 * 256; }
-// Workspace: the per-head arrival counters first, at a fixed place for any cache length, then the partials, so
-// one workspace serves calls with different max_len (talker and code predictor) without a partial landing on a
-// counter.
-int64_t counter_bytes(int nkv) { return ((int64_t)nkv * 4 + 255) / 256 * 256; }
+constexpr int64_t part_bytes(int nkv, int nsplit) { return ((int64_t)nkv * 2 * nsplit * kPart * 4 + 255) / 256 * 256; }
+// Workspace: the error word (byte 0) and the per-head arrival counters (from byte 4) first, at a fixed place for
+// any cache length, then the partials, so one workspace serves calls with different max_len (talker and code
+// predictor) without a partial landing on a counter.
+constexpr uint32_t kErrBadPos = 5;  // the position lies outside [0, max_len): nothing is read or written
+constexpr int64_t counter_bytes(int nkv) { return ((int64_t)nkv * 4 + 4 + 255) / 256 * 256; }
 
 // 8 consecutive cache elements as raw bits: one uint4 for bf16, two for f32
 template <int CT> struct Row8;
@@ -67,7 +68,8 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ qkv
                                                    typename Cache<CT>::T* __restrict__ Vc,
                                                    const int64_t* __restrict__ pos_ptr, int pos_add, int max_len, int nq,
                                                    int nkv, float* __restrict__ out, float* __restrict__ part,
-                                                   unsigned* __restrict__ counters, int nsplit) {
+                                                   unsigned* __restrict__ err, unsigned* __restrict__ counters,
+                                                   int nsplit) {
   using C = Cache<CT>;
   __shared__ float qsh[2][SK_HD];
   __shared__ float ksh[SK_HD];
@@ -79,14 +81,18 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ qkv
   __shared__ int is_last;
   const int kvh = blockIdx.x, split = blockIdx.y;
   const int t = threadIdx.x, p = t >> 7, d = t & (SK_HD - 1), w = t >> 6, lane = t & 63, g = lane >> 4, sl = lane & 15;
-  int pos = (pos_ptr ? (int)pos_ptr[0] : 0) + pos_add;
-  const bool pos_ok = pos >= 0 && pos < max_len;
-  if (!pos_ok) pos = 0;
-  const int T = pos_ok ? pos + 1 : 0;
+  const int64_t pos64 = (pos_ptr ? pos_ptr[0] : 0) + (int64_t)pos_add;
+  if (pos64 < 0 || pos64 >= max_len) {
+    // every block takes this exit (the position is uniform), so no counter moves and nothing is written
+    if (kvh == 0 && split == 0 && t == 0) __hip_atomic_store(err, kErrBadPos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  const int pos = (int)pos64;
+  const int T = pos + 1;
   const int chunk = (T + nsplit - 1) / nsplit;
   const int t0 = split * chunk, t1 = min(T, t0 + chunk);
   const int n = t1 > t0 ? t1 - t0 : 0;
-  const bool has_pos = pos_ok && t0 <= pos && pos < t1;
+  const bool has_pos = t0 <= pos && pos < t1;
   typename C::T* Kh = Kc + (size_t)kvh * max_len * SK_HD;
   typename C::T* Vh = Vc + (size_t)kvh * max_len * SK_HD;
 
@@ -249,30 +255,48 @@ extern "C" int64_t sk_attn_workspace_size(int nq, int nkv, int max_len) {
   return counter_bytes(nkv) + part_bytes(nkv, nsplit_for(max_len));
 }
 
-extern "C" int sk_attn(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc,
-                       void* Vc, const int64_t* pos_ptr, int pos_add, int max_len, int nq, int nkv, float* out,
-                       void* workspace, int64_t workspace_bytes, int ct, void* stream) {
-  if (!qkv || !qn || !kn || !rope || !Kc || !Vc || !out || !workspace)
-    return sk_set_error(SK_EINVAL, "sk_attn: null pointer");
+namespace {
+
+// Checks shared by both entry points; SK_OK or the status already recorded.
+int check_attn(const float* qkv, const float* qn, const float* kn, const float* rope, const void* Kc, const void* Vc,
+               int max_len, int nq, int nkv, const float* out, int ct) {
+  if (!qkv || !qn || !kn || !rope || !Kc || !Vc || !out) return sk_set_error(SK_EINVAL, "sk_attn: null pointer");
   if (nkv <= 0 || nq != 2 * nkv || max_len <= 0)
     return sk_set_error(SK_EINVAL, "sk_attn: needs nq == 2*nkv and max_len > 0 (head_dim 128)");
   if ((int64_t)nkv * 2 * kSplitMax * kPart * 4 >= (int64_t)1 << 31 || (int64_t)max_len * nkv * SK_HD * 4 >= (int64_t)1 << 40)
     return sk_set_error(SK_EINVAL, "sk_attn: sizes out of range");
   if (ct != SK_CT_BF16 && ct != SK_CT_F32) return sk_set_error(SK_EINVAL, "sk_attn: bad cache type");
   if (!SK_ALIGNED16(Kc) || !SK_ALIGNED16(Vc)) return sk_set_error(SK_EINVAL, "sk_attn: caches must be 16-byte aligned");
-  if (!SK_ALIGNED16(workspace)) return sk_set_error(SK_EINVAL, "sk_attn: workspace must be 16-byte aligned");
-  if (workspace_bytes < sk_attn_workspace_size(nq, nkv, max_len))
-    return sk_set_error(SK_EWORKSPACE, "sk_attn: workspace too small");
+  return SK_OK;
+}
+
+int launch_attn(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc, void* Vc,
+                const int64_t* pos_ptr, int pos_add, int max_len, int nq, int nkv, float* out, float* part,
+                unsigned* err, unsigned* counters, int ct, hipStream_t st, const char* name) {
   const int nsplit = nsplit_for(max_len);
-  unsigned* counters = (unsigned*)workspace;
-  float* part = (float*)((char*)workspace + counter_bytes(nkv));
-  hipStream_t st = (hipStream_t)stream;
   dim3 grid(nkv, nsplit);
   if (ct == SK_CT_BF16)
     hipLaunchKernelGGL((k_attn<SK_CT_BF16>), grid, dim3(kThreads), 0, st, qkv, qn, kn, eps, rope, (bf16_t*)Kc,
-                       (bf16_t*)Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, counters, nsplit);
+                       (bf16_t*)Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, err, counters, nsplit);
   else
     hipLaunchKernelGGL((k_attn<SK_CT_F32>), grid, dim3(kThreads), 0, st, qkv, qn, kn, eps, rope, (float*)Kc,
-                       (float*)Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, counters, nsplit);
-  return sk_check_launch(hipGetLastError(), "sk_attn");
+                       (float*)Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, err, counters, nsplit);
+  return sk_check_launch(hipGetLastError(), name);
+}
+
+}  // namespace
+
+extern "C" int sk_attn(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc,
+                       void* Vc, const int64_t* pos_ptr, int pos_add, int max_len, int nq, int nkv, float* out,
+                       void* workspace, int64_t workspace_bytes, int ct, void* stream) {
+  const int rc = check_attn(qkv, qn, kn, rope, Kc, Vc, max_len, nq, nkv, out, ct);
+  if (rc != SK_OK) return rc;
+  if (!workspace) return sk_set_error(SK_EINVAL, "sk_attn: null pointer");
+  if (!SK_ALIGNED16(workspace)) return sk_set_error(SK_EINVAL, "sk_attn: workspace must be 16-byte aligned");
+  if (workspace_bytes < sk_attn_workspace_size(nq, nkv, max_len))
+    return sk_set_error(SK_EWORKSPACE, "sk_attn: workspace too small");
+  unsigned* err = (unsigned*)workspace;
+  float* part = (float*)((char*)workspace + counter_bytes(nkv));
+  return launch_attn(qkv, qn, kn, eps, rope, Kc, Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, err, err + 1, ct,
+                     (hipStream_t)stream, "sk_attn");
 }

@@ -37,16 +37,15 @@ extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* str
     return sk_set_error(SK_EINVAL, "sk_talker_frames: talker_in input needs its tables, codes, pad, rows and one frame");
   if (d->do_sample && (!d->seed || !d->counter || !(d->inv_temp > 0.f)))
     return sk_set_error(SK_EINVAL, "sk_talker_frames: sampling needs seed, counter and inv_temp > 0");
-  int dev = 0, cus = 0;
-  hipGetDevice(&dev);
-  hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (cus != kWG) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs a 256-CU device (8 XCDs x 32)");
   hipStream_t st = (hipStream_t)stream;
   const CpArgs none{};
   if (d->hidden == 1024 && d->inter == 3072) return launch_frames<1024, 3072, 4, kTalkerV, false>(d, none, n_frames, st);
   if (d->hidden == 2048 && d->inter == 6144) {
-    const char* poll = std::getenv("SOKUTOU_TALKER_POLL");
-    if (poll && !std::strcmp(poll, "regs")) return launch_frames<2048, 6144, 8, kTalkerV, false>(d, none, n_frames, st);
+    static const bool regs = [] {  // read once per process
+      const char* poll = std::getenv("SOKUTOU_TALKER_POLL");
+      return poll && !std::strcmp(poll, "regs");
+    }();
+    if (regs) return launch_frames<2048, 6144, 8, kTalkerV, false>(d, none, n_frames, st);
     return sk_talker_frames_2048(d, n_frames, st);
   }
   return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: shapes other than the 0.6B / 1.7B talker");

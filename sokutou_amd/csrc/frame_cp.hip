@@ -18,10 +18,6 @@ extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
     return sk_set_error(SK_EWORKSPACE, "sk_cp_frame: workspace too small");
   if (d->do_sample && (!d->seed || !d->counter || !(d->inv_temp > 0.f)))
     return sk_set_error(SK_EINVAL, "sk_cp_frame: sampling needs seed, counter and inv_temp > 0");
-  int dev = 0, cus = 0;
-  hipGetDevice(&dev);
-  hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (cus != kWG) return sk_set_error(SK_EUNSUPPORTED, "sk_cp_frame: needs a 256-CU device (8 XCDs x 32)");
   sk_talker_desc t{};
   t.n_layers = d->n_layers; t.hidden = d->hidden; t.inter = d->inter; t.nq = d->nq; t.nkv = d->nkv;
   t.vocab = d->vocab; t.max_len = d->n_positions; t.wd = d->wd; t.ct = d->ct; t.eps = d->eps;

@@ -1272,7 +1272,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   void* ws = d.workspace;
   // ---- placement: XCD from hardware, dense rank from an arrival counter ------------------------------------
-  __shared__ int s_rank;
+  __shared__ int s_rank, s_bad;
   __shared__ uint32_t s_base;
   const uint32_t x = xcc_id();
   if (tid == 0) {
@@ -1292,9 +1292,11 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
         const int64_t cg = gload(d.in_codes + gi);
         bad |= cg < 0 || cg >= (gi == 0 ? d.vocab : d.in_rows);
       }
-    if (bad) {
+    if (bad) {  // refused, but the placement stands: the launch count still advances below (no stale census)
       st_u32_dev(ws, Ws::kErr, 5u);
-      r = -1;
+      s_bad = 1;
+    } else {
+      s_bad = 0;
     }
     s_rank = r;
     s_base = ld_u32_dev(ws, Ws::kTick);
@@ -1305,6 +1307,13 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   __syncthreads();
   const int r = s_rank;
   if (r < 0) return;
+  if (s_bad) {  // every workgroup sees the same inputs, so all of them leave here; workgroup 0 closes the launch
+    if (x == 0 && r == 0 && tid == 0) {
+      st_u32_dev(ws, Ws::kTick, s_base);
+      st_u32_dev(ws, Ws::kLaunch, ld_u32_dev(ws, Ws::kLaunch) + 1u);
+    }
+    return;
+  }
   Ctx c;
   c.d = d;
   c.cp = cp;
@@ -1348,14 +1357,38 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     st_u32_dev(ws, Ws::kLaunch, ld_u32_dev(ws, Ws::kLaunch) + 1u);
   }
 }
+// First launch of an instantiation on a device: raise its LDS limit and check that the 256 workgroups can all be
+// resident at once, one per CU (every exchange waits for all of them; a device with fewer CUs, or one whose CUs
+// cannot hold a workgroup, would only surface as poll timeouts). Done once per device and instantiation; a failure
+// is reported every time and retried on the next call.
+constexpr int kMaxDevices = 64;
+template <int H, int I, int W, int V, bool CP, bool SMP>
+int prepare_kernel(size_t lds) {
+  static bool ready[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return sk_set_error(SK_EDEVICE, "sk_talker_frames: no current HIP device");
+  if (ready[dev]) return SK_OK;
+  const void* fn = (const void*)k_frames<H, I, W, V, CP, SMP>;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return sk_check_launch(e, "sk_talker_frames: raising the LDS limit");
+  int cus = 0, per_cu = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return sk_check_launch(e, "sk_talker_frames: reading the CU count");
+  if (cus != kWG) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs a 256-CU device (8 XCDs x 32)");
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, (W + 1) * 64, lds);
+  if (e != hipSuccess) return sk_check_launch(e, "sk_talker_frames: occupancy query");
+  if (per_cu < 1)
+    return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: a CU cannot hold one workgroup of the frame kernel, so the "
+                                         "256 workgroups cannot be co-resident");
+  ready[dev] = true;
+  return SK_OK;
+}
 template <int H, int I, int W, int V, bool CP, bool SMP>
 int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
   const size_t lds = sizeof(Lds<H, I, W, V, CP>) < 96 * 1024 ? 96 * 1024 : sizeof(Lds<H, I, W, V, CP>);  // one workgroup per CU
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipFuncSetAttribute((const void*)k_frames<H, I, W, V, CP, SMP>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    attr_set = true;
-  }
+  const int rc = prepare_kernel<H, I, W, V, CP, SMP>(lds);
+  if (rc != SK_OK) return rc;
   hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp, n_frames);
   return sk_check_launch(hipGetLastError(), "sk_talker_frames");
 }

@@ -126,6 +126,14 @@ class Qwen3Fast:
     def _frame(self) -> None:
         raise NotImplementedError
 
+    # Frames between reads of the kernels' device error words in generate_codes (and once after the loop). A kernel
+    # that fails leaves the frame state alone, so the loop would replay the same frame; the check bounds that to
+    # this many frames, and the codes are never returned.
+    ERROR_CHECK_EVERY = 16
+
+    def _check_errors(self) -> None:
+        """Raises RuntimeError if a kernel of the frame reported an error on the device; subclasses override."""
+
     # --- capture ------------------------------------------------------------------------------------------
     def _state(self):
         return (self.id0, self.pos, self.seen, self.ngen)
@@ -173,6 +181,9 @@ class Qwen3Fast:
             step()
             frames.append(self.codes.clone())
             nid = int(self.next_id0.item())
+            if len(frames) % self.ERROR_CHECK_EVERY == 0:
+                self._check_errors()
+        self._check_errors()
         self.stats["prompt_tokens"] = L
         self.stats["stopped"] = nid == self.eos
         self.stats["cache_limited"] = nid != self.eos and len(frames) == limit and limit < self.s.max_new_tokens - 1

@@ -238,6 +238,16 @@ class CodePredictor:
         """Error word of the kernel's workspace (0 when healthy; codes as ``Qwen3Kernels.frame_error``)."""
         return int(self.ws[:4].view(torch.int32).item())
 
+    def diag(self) -> dict:
+        w = self.ws[16:32].view(torch.int32).tolist()
+        return {"code": w[0], "frame": w[1], "layer": w[2], "workgroup": w[3]}
+
+    def clear_error(self) -> None:
+        """Zeroes the kernel's whole workspace (error word, launch census, epoch base and exchange cells), so the
+        next launch starts clean after a failed one. Stream-ordered on the current stream; not to be called while a
+        launch of this code predictor may be in flight on another stream."""
+        self.ws.zero_()
+
     def weight_bytes(self) -> int:
         return self.C.bytes() + sum(h.bytes() for h in self.heads)
 
@@ -459,6 +469,33 @@ class Qwen3Kernels(Qwen3Fast):
     def frame_diag(self) -> dict:
         w = self.frame_ws[16:32].view(torch.int32).tolist()
         return {"code": w[0], "frame": w[1], "layer": w[2], "workgroup": w[3]}
+
+    def clear_frame_error(self) -> None:
+        """Clears every device error word of the engine so frames can run again after a failure: the frame kernel's
+        and the one-launch code predictor's whole workspaces (error word, launch census, epoch base and exchange cells
+        all restart from zero, so no stale cell can match a new epoch) and the attention workspace's error word.
+        Stream-ordered on the current stream."""
+        if self.frame_kernel:
+            self.frame_ws.zero_()
+        if self.cp is not None and self.cpk is not None:
+            self.cpk.clear_error()
+        self.attn_ws[:4].zero_()
+
+    def _check_errors(self) -> None:
+        """Reads the device error words of the kernels this engine runs (frame kernel, one-launch code predictor,
+        per-op attention) and raises RuntimeError naming the first one set; clear_frame_error() resets them."""
+        words = []
+        if self.frame_kernel:
+            words.append(("sk_talker_frames", self.frame_ws, self.frame_diag))
+        if self.cp is not None and self.cpk is not None:
+            words.append(("sk_cp_frame", self.cpk.ws, self.cpk.diag))
+        words.append(("sk_attn", self.attn_ws, None))
+        for name, ws, diag in words:
+            code = int(ws[:4].view(torch.int32).item())
+            if code:
+                extra = f" {diag()}" if diag is not None else ""
+                raise RuntimeError(f"{name} reported device error {code}{extra}; the frame state was not advanced "
+                                   f"(clear_frame_error() resets the error words)")
 
     # --- launches -----------------------------------------------------------------------------------------
     def _rms_gemv(self, h, nw, eps, lin: _Lin, out, swiglu: bool) -> None:

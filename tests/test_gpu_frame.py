@@ -115,6 +115,48 @@ def test_bad_position_is_an_error_not_a_write(gpu):
     assert eng.frame_error() == 0, eng.frame_diag()
 
 
+def test_refused_launch_then_public_reset_runs_cleanly(gpu):
+    """A launch refused on the device (position past the cache) leaves the error word set but the launch census
+    consistent; clear_frame_error() then lets the same engine run frames that match an untouched engine's."""
+    print("small06b: refused launch, clear_frame_error(), then 4 frames", flush=True)
+    kv = syn.WORKLOADS["small06b"]["kv"]
+    ref, tok = _engine("small06b", 2, gpu)
+    ref.run_frames(4)
+    torch.cuda.synchronize()
+    assert ref.frame_error() == 0
+    want = ref.frame_ids[:4].cpu().tolist()
+    eng, _ = _engine("small06b", 2, gpu)
+    for _ in range(2):  # twice: the refused launches must not leave the census ahead of the launch count
+        eng.pos.fill_(eng.max_cache)
+        eng.run_frames(1)
+        torch.cuda.synchronize()
+        assert eng.frame_error() == 5
+    eng.clear_frame_error()
+    eng.reset(kv, tok)
+    eng.run_frames(4)
+    torch.cuda.synchronize()
+    assert eng.frame_error() == 0, eng.frame_diag()
+    assert eng.frame_ids[:4].cpu().tolist() == want
+
+
+def test_generate_codes_raises_on_device_error(gpu):
+    """A start token outside the vocabulary is refused by the kernel (error 5) and the frame state is not advanced;
+    generate_codes reads the error word and raises instead of returning repeated stale codes."""
+    print("small06b: generate_codes with a token the kernel refuses", flush=True)
+    from sokutou_amd.fast import Sampling
+
+    eng, tok = syn.make_engine("small06b", seed=2, wd="i8row", device=gpu, frame_kernel=True,
+                               sampling=Sampling.greedy(processor=False), suppress_tail=0)
+    kw = dict(prefill_len=syn.WORKLOADS["small06b"]["kv"], first_token=eng.V + 7, do_sample=False,
+              subtalker_dosample=False, repetition_penalty=1.0, min_new_tokens=0, max_new_tokens=2048)
+    with pytest.raises(RuntimeError, match="device error 5"):
+        eng.generate_codes(kw, max_frames=40)
+    eng.clear_frame_error()
+    kw["first_token"] = tok
+    codes = eng.generate_codes(kw, max_frames=4)
+    assert codes.shape[0] == 4 and eng.frame_error() == 0
+
+
 @pytest.mark.timeout(900)
 def test_talker17b_64_frames_one_launch(gpu):
     """The 1.7B shape (hidden 2048, intermediate 6144, KV 1024): per-layer residuals of frame 0, then the

@@ -117,7 +117,7 @@ def test_attention(gpu, ct, nkv, max_len, pos):
     assert int(ws[: nkv * 4].sum()) == 0
 
 
-def test_attention_invalid_position_writes_nothing(gpu):
+def test_attention_invalid_position_sets_error_word(gpu):
     nkv, max_len = 8, 64
     rng = np.random.default_rng(5)
     Kg = torch.zeros((nkv, max_len, 128), dtype=torch.bfloat16, device=gpu)
@@ -133,8 +133,19 @@ def test_attention_invalid_position_writes_nothing(gpu):
     _lib.call("sk_attn", p(qkv), p(ones), p(ones), 1e-6, p(rope), p(Kg), p(Vg), p(posg), 0, max_len, 16, nkv, p(out),
               p(ws), ws.numel(), 0, _lib.stream())
     torch.cuda.synchronize()
+    # refused on the device: error word 5, caches and output untouched
+    assert int(ws[:4].view(torch.int32).item()) == 5
     assert float(Kg.abs().sum()) == 0 and float(Vg.abs().sum()) == 0
-    assert float(out.abs().sum()) == 0
+    assert bool((out == 7.0).all())
+    # the arrival counters are still zero: a later valid call on the same workspace (error word cleared) merges
+    ws[:4].zero_()
+    posg.fill_(3)
+    _lib.call("sk_attn", p(qkv), p(ones), p(ones), 1e-6, p(rope), p(Kg), p(Vg), p(posg), 0, max_len, 16, nkv, p(out),
+              p(ws), ws.numel(), 0, _lib.stream())
+    torch.cuda.synchronize()
+    assert int(ws[:4].view(torch.int32).item()) == 0
+    assert int(ws[4:4 + 4 * nkv].view(torch.int32).abs().sum().item()) == 0
+    assert bool(torch.isfinite(out).all()) and not bool((out == 7.0).any())
 
 
 def test_rmsnorm_embed(gpu):
