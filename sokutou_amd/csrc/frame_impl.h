@@ -1272,7 +1272,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   void* ws = d.workspace;
   // ---- placement: XCD from hardware, dense rank from an arrival counter ------------------------------------
-  __shared__ int s_rank, s_bad;
+  __shared__ int s_rank;
   __shared__ uint32_t s_base;
   const uint32_t x = xcc_id();
   if (tid == 0) {
@@ -1284,7 +1284,9 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
       st_u32_dev(ws, Ws::kErr, 2u);
       r = -1;
     }
-    // every position this launch writes must lie inside the cache, and the start token inside the vocabulary
+    // every position this launch writes must lie inside the cache, and the start token inside the vocabulary.
+    // A refused launch leaves the launch count behind the census; the host's reset (the whole workspace zeroed)
+    // brings them back together.
     const int64_t pos0 = d.pos ? gload(d.pos) : 0, tok0 = gload(d.id0);
     bool bad = pos0 < 0 || pos0 + n_frames > d.max_len || tok0 < 0 || tok0 >= (CP ? cp.emb0_rows : d.vocab);
     if (!CP)
@@ -1292,11 +1294,9 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
         const int64_t cg = gload(d.in_codes + gi);
         bad |= cg < 0 || cg >= (gi == 0 ? d.vocab : d.in_rows);
       }
-    if (bad) {  // refused, but the placement stands: the launch count still advances below (no stale census)
+    if (bad) {
       st_u32_dev(ws, Ws::kErr, 5u);
-      s_bad = 1;
-    } else {
-      s_bad = 0;
+      r = -1;
     }
     s_rank = r;
     s_base = ld_u32_dev(ws, Ws::kTick);
@@ -1307,13 +1307,6 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   __syncthreads();
   const int r = s_rank;
   if (r < 0) return;
-  if (s_bad) {  // every workgroup sees the same inputs, so all of them leave here; workgroup 0 closes the launch
-    if (x == 0 && r == 0 && tid == 0) {
-      st_u32_dev(ws, Ws::kTick, s_base);
-      st_u32_dev(ws, Ws::kLaunch, ld_u32_dev(ws, Ws::kLaunch) + 1u);
-    }
-    return;
-  }
   Ctx c;
   c.d = d;
   c.cp = cp;

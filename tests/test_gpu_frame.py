@@ -140,19 +140,28 @@ def test_refused_launch_then_public_reset_runs_cleanly(gpu):
 
 
 def test_generate_codes_raises_on_device_error(gpu):
-    """A start token outside the vocabulary is refused by the kernel (error 5) and the frame state is not advanced;
-    generate_codes reads the error word and raises instead of returning repeated stale codes."""
-    print("small06b: generate_codes with a token the kernel refuses", flush=True)
+    """A device position past the cache (forced from the host after the prompt state is set) is refused by the
+    kernel (error 5) and the frame state is not advanced; generate_codes reads the error word and raises instead of
+    returning repeated stale codes."""
+    print("small06b: generate_codes with a position the kernel refuses", flush=True)
     from sokutou_amd.fast import Sampling
 
     eng, tok = syn.make_engine("small06b", seed=2, wd="i8row", device=gpu, frame_kernel=True,
                                sampling=Sampling.greedy(processor=False), suppress_tail=0)
-    kw = dict(prefill_len=syn.WORKLOADS["small06b"]["kv"], first_token=eng.V + 7, do_sample=False,
+    kw = dict(prefill_len=syn.WORKLOADS["small06b"]["kv"], first_token=tok, do_sample=False,
               subtalker_dosample=False, repetition_penalty=1.0, min_new_tokens=0, max_new_tokens=2048)
+    start = eng._start
+
+    def start_past_the_cache(k):
+        n = start(k)
+        eng.pos.fill_(eng.max_cache)
+        return n
+
+    eng._start = start_past_the_cache
     with pytest.raises(RuntimeError, match="device error 5"):
         eng.generate_codes(kw, max_frames=40)
+    del eng._start
     eng.clear_frame_error()
-    kw["first_token"] = tok
     codes = eng.generate_codes(kw, max_frames=4)
     assert codes.shape[0] == 4 and eng.frame_error() == 0
 
