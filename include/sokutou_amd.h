@@ -91,6 +91,18 @@ int sk_attn(const float* qkv, const float* qn, const float* kn, float eps, const
             const int64_t* pos_ptr, int pos_add, int max_len, int nq, int nkv, float* out, void* workspace,
             int64_t workspace_bytes, int ct, void* stream);
 
+/* sk_attn without a workspace, for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. Same arguments and results as
+ * sk_attn, except that the split-K scratch (arrival counters and partials) lives in a static device array of the
+ * library, 520 KiB per device, held until the process ends: at most 16 kv heads (more is SK_EINVAL). err (nullable,
+ * device int32) receives 5 when the position lies outside [0, max_len) (the call then writes nothing else) and is
+ * left alone otherwise. The call allocates nothing; its first call on a device looks up the array and launches a
+ * small kernel that clears the counters. Every call on one device shares the array: calls that overlap on one
+ * device (concurrent streams or threads) race and must be serialised by the caller. */
+int sk_attn_noalloc(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc, void* Vc,
+                    const int64_t* pos_ptr, int pos_add, int max_len, int nq, int nkv, float* out, int* err, int ct,
+                    void* stream);
+
 /* One sampling step over V <= SK_MAX_V fp32 logits, writing the chosen id to out[0] (int64).
  * talker != 0 applies the talker processor first (repetition penalty on seen, suppressed ids, EOS blocked while
  * ngen < min_new) and then updates the device state: id0 = id, seen[id] = 1, ngen += 1, pos += 1.

@@ -33,6 +33,7 @@ _SIGS = {
     "sk_talker_in": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P]),
     "sk_attn_workspace_size": (c_int64, [c_int, c_int, c_int]),
     "sk_attn": (c_int, [_P, _P, _P, c_float, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, _P, c_int64, c_int, _P]),
+    "sk_attn_noalloc": (c_int, [_P, _P, _P, c_float, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, _P, c_int, _P]),
     "sk_sample": (c_int, [_P, c_int, c_float, c_int, c_int, _P, c_float, _P, _P, c_int, c_int, _P, _P, _P, c_int, _P,
                           _P, _P]),
 }

@@ -300,3 +300,58 @@ extern "C" int sk_attn(const float* qkv, const float* qn, const float* kn, float
   return launch_attn(qkv, qn, kn, eps, rope, Kc, Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, err, err + 1, ct,
                      (hipStream_t)stream, "sk_attn");
 }
+
+// ---- allocation-free variant -------------------------------------------------------------------------------------
+// sk_attn_noalloc keeps its split-K scratch (error word, arrival counters, partials) in this file-scope device array
+// instead of a caller workspace: at most kNoAllocMaxKv kv heads. Each device holds its own copy until the process
+// ends. The host never passes the array's name to a kernel: the first call on a device looks up the device address
+// with hipGetSymbolAddress and keeps it per device.
+namespace {
+constexpr int kNoAllocMaxKv = 16;
+constexpr int64_t kNoAllocBytes = counter_bytes(kNoAllocMaxKv) + part_bytes(kNoAllocMaxKv, kSplitMax);
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+namespace {
+
+void* g_scratch[kMaxDevices];  // device address of `scratch` per device (null until the first call there)
+
+// Clears the error word and the arrival counters (the first counter_bytes of the scratch): a fill kernel, not a
+// memset node, so the clear is also safe inside a captured graph.
+__global__ void k_clear_words(unsigned* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+}  // namespace
+
+extern "C" int sk_attn_noalloc(const float* qkv, const float* qn, const float* kn, float eps, const float* rope,
+                               void* Kc, void* Vc, const int64_t* pos_ptr, int pos_add, int max_len, int nq, int nkv,
+                               float* out, int* err, int ct, void* stream) {
+  const int rc = check_attn(qkv, qn, kn, rope, Kc, Vc, max_len, nq, nkv, out, ct);
+  if (rc != SK_OK) return rc;
+  if (nkv > kNoAllocMaxKv)
+    return sk_set_error(SK_EINVAL, "sk_attn_noalloc: at most 16 kv heads (the static scratch holds 520 KiB)");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return sk_set_error(SK_EDEVICE, "sk_attn_noalloc: no current HIP device");
+  hipStream_t st = (hipStream_t)stream;
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return sk_check_launch(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                                      "sk_attn_noalloc: hipGetSymbolAddress(scratch)");
+    const int words = (int)(counter_bytes(kNoAllocMaxKv) / 4);
+    hipLaunchKernelGGL(k_clear_words, dim3(1), dim3(words), 0, st, (unsigned*)p, words);
+    const int lrc = sk_check_launch(hipGetLastError(), "sk_attn_noalloc: clearing the scratch counters");
+    if (lrc != SK_OK) return lrc;
+    g_scratch[dev] = p;
+  }
+  unsigned* base = (unsigned*)g_scratch[dev];
+  float* part = (float*)((char*)base + counter_bytes(kNoAllocMaxKv));
+  unsigned* errw = err ? (unsigned*)err : base;  // word 0 of the scratch when the caller takes no error word
+  return launch_attn(qkv, qn, kn, eps, rope, Kc, Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, errw, base + 1, ct,
+                     st, "sk_attn_noalloc");
+}
