@@ -1,0 +1,129 @@
+"""Per-stage timing of the persistent frame kernel from its own trace stamps.
+
+    python -m sokutou_amd.stage_trace [talker06b|talker17b] [--frames N]
+
+The kernel keeps optional wall-clock stamps (100 MHz) of frame 0 of a launch for every workgroup and layer when
+the workspace's trace word is set: the compute waves stamp the start of each stage (after its barrier), the end of
+each dot and their publication; the control wave stamps when each stage's input has arrived and been staged. This
+tool runs one traced launch of the synthetic workload, then prints, as markdown:
+
+* the median time of each step of a layer (median over the 256 workgroups and the middle layers);
+* each exchange: from the last producer's publication to the median consumer's input being ready;
+* the median layer time.
+
+This is the reference's per-frame profiling role (qwen3/prof_frame.py:41-87, which times the frame's kernels with
+CUDA events) for a kernel that runs a whole frame in one launch.
+"""
+
+from __future__ import annotations
+
+import argparse
+import sys
+
+import numpy as np
+import torch
+
+from . import _lib
+from . import synthetic as syn
+
+# trace layout: [workgroup 256][role 2: control, compute][layer 32][event 16] of int64 stamps
+_TRACE_LAYERS, _TRACE_EVENTS, _WG = 32, 16, 256
+# compute-wave events
+C_S1, C_S1DOT, C_S1PUB, C_S2, C_S2END, C_S4, C_S4DOT, C_S4PUB = 0, 8, 1, 2, 3, 4, 9, 5
+C_S5, C_S5DOT, C_S5PUB, C_S6, C_S6DOT, C_S6PUB = 12, 10, 6, 13, 11, 7
+# control-wave events
+K_START, K_S1IN, K_QKV, K_ATTB, K_MRGPOLL, K_MRGDONE, K_ATT, K_HMID, K_ACT = 0, 1, 2, 3, 8, 4, 5, 6, 7
+
+
+def traced_launch(name: str, frames: int = 2):
+    """Builds the workload's engine, warms it up, then runs one launch of ``frames`` frames with tracing on.
+    Returns (stamps in us as float64 [256, 2, 32, 16], shape, us of the launch)."""
+    dev = torch.device("cuda:0")
+    eng, tok = syn.make_engine(name, seed=0, wd="i8row", device=dev, frame_kernel=True)
+    s = syn.workload_shape(name)
+    kv = syn.WORKLOADS[name]["kv"]
+    L = _lib.load()
+    total = int(L.sk_talker_workspace_size(s.hidden, s.inter))
+    nbytes = _WG * 2 * _TRACE_LAYERS * _TRACE_EVENTS * 8
+    for _ in range(3):
+        eng.reset(kv, tok)
+        eng.run_frames(frames)
+    eng.frame_ws[32:36].view(torch.int32).fill_(1)
+    eng.reset(kv, tok)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    eng.run_frames(frames)
+    e1.record()
+    torch.cuda.synchronize()
+    if eng.frame_error():
+        raise RuntimeError(f"frame kernel error {eng.frame_diag()}")
+    raw = eng.frame_ws[total - nbytes:total].view(torch.int64).view(_WG, 2, _TRACE_LAYERS, _TRACE_EVENTS)
+    eng.frame_ws[32:36].zero_()
+    return raw.cpu().numpy().astype(np.float64) * 0.01, s, e0.elapsed_time(e1) * 1e3
+
+
+def summarise(t: np.ndarray, n_layers: int) -> dict:
+    """Medians of the layer steps and exchanges over workgroups and the middle layers (1 .. n_layers - 2)."""
+    ctl, cmp_ = t[:, 0], t[:, 1]
+    layers = range(1, min(n_layers, _TRACE_LAYERS) - 1)
+    xcd = np.arange(_WG) // 32  # the kernel's dense rank: workgroup g = 32 * XCD + rank
+
+    def med(f):
+        return float(np.median([f(l) for l in layers]))
+
+    steps = [
+        ("S1 qkv dot", lambda l: np.median(cmp_[:, l, C_S1DOT] - cmp_[:, l, C_S1])),
+        ("S1 publish", lambda l: np.median(cmp_[:, l, C_S1PUB] - cmp_[:, l, C_S1DOT])),
+        ("S1 publish -> S2 start (qkv exchange, XCD-local)", lambda l: np.median(cmp_[:, l, C_S2] - cmp_[:, l, C_S1PUB])),
+        ("S2 attention (norm, RoPE, scores, softmax, PV, partial published)", lambda l: np.median(cmp_[:, l, C_S2END] - cmp_[:, l, C_S2])),
+        ("S2 end -> S4 start (partials exchange, merge, attention-output exchange)", lambda l: np.median(cmp_[:, l, C_S4] - cmp_[:, l, C_S2END])),
+        ("S4 o dot", lambda l: np.median(cmp_[:, l, C_S4DOT] - cmp_[:, l, C_S4])),
+        ("S4 publish", lambda l: np.median(cmp_[:, l, C_S4PUB] - cmp_[:, l, C_S4DOT])),
+        ("S4 publish -> S5 start (h after o exchange, RMSNorm staging)", lambda l: np.median(cmp_[:, l, C_S5] - cmp_[:, l, C_S4PUB])),
+        ("S5 gate/up dot", lambda l: np.median(cmp_[:, l, C_S5DOT] - cmp_[:, l, C_S5])),
+        ("S5 SwiGLU + publish", lambda l: np.median(cmp_[:, l, C_S5PUB] - cmp_[:, l, C_S5DOT])),
+        ("S5 publish -> S6 start (activation exchange)", lambda l: np.median(cmp_[:, l, C_S6] - cmp_[:, l, C_S5PUB])),
+        ("S6 down dot", lambda l: np.median(cmp_[:, l, C_S6DOT] - cmp_[:, l, C_S6])),
+        ("S6 publish", lambda l: np.median(cmp_[:, l, C_S6PUB] - cmp_[:, l, C_S6DOT])),
+        ("S6 publish -> next S1 start (residual exchange, RMSNorm staging)", lambda l: np.median(cmp_[:, l + 1, C_S1] - cmp_[:, l, C_S6PUB])),
+    ]
+
+    def local_last(l, ev):  # per consumer: the last publication among the 32 workgroups of its XCD
+        last = np.array([cmp_[xcd == x, l, ev].max() for x in range(8)])
+        return last[xcd]
+
+    exchanges = [
+        ("residual h (global, 256 producers)", lambda l: np.median(ctl[:, l + 1, K_S1IN]) - cmp_[:, l, C_S6PUB].max()),
+        ("q|k|v of the head (XCD-local, 32 producers)", lambda l: np.median(ctl[:, l, K_QKV] - local_last(l, C_S1PUB))),
+        ("attention partials (XCD-local, 32 producers)", lambda l: np.median(ctl[:, l, K_MRGPOLL] - local_last(l, C_S2END))),
+        ("attention output (global, 256 producers; from the partials' arrival)", lambda l: np.median(ctl[:, l, K_ATT] - ctl[:, l, K_MRGPOLL])),
+        ("h after o (global, 256 producers)", lambda l: np.median(ctl[:, l, K_HMID]) - cmp_[:, l, C_S4PUB].max()),
+        ("SwiGLU activation (global, 256 producers)", lambda l: np.median(ctl[:, l, K_ACT]) - cmp_[:, l, C_S5PUB].max()),
+    ]
+    layer = med(lambda l: np.median(cmp_[:, l + 1, C_S1] - cmp_[:, l, C_S1]))
+    return {"steps": [(n, med(f)) for n, f in steps], "exchanges": [(n, med(f)) for n, f in exchanges],
+            "layer_us": layer, "layers": f"{layers.start}..{layers.stop - 1}"}
+
+
+def to_markdown(name: str, s, summ: dict, launch_us: float, frames: int) -> str:
+    out = [f"Workload {name}: {s.n_layers} layers, hidden {s.hidden}, intermediate {s.inter}; one traced launch of "
+           f"{frames} frames ({launch_us:.1f} us, stamps of frame 0). Medians over the 256 workgroups and layers "
+           f"{summ['layers']}.", "", "| step of a layer | us |", "|---|---|"]
+    out += [f"| {n} | {v:.2f} |" for n, v in summ["steps"]]
+    out += [f"| **layer (S1 start to next S1 start)** | **{summ['layer_us']:.2f}** |", "",
+            "| exchange: last producer's publication -> median consumer's input ready | us |", "|---|---|"]
+    out += [f"| {n} | {v:.2f} |" for n, v in summ["exchanges"]]
+    return "\n".join(out)
+
+
+def main(argv=None) -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("workload", nargs="?", default="talker06b", choices=["talker06b", "talker17b"])
+    ap.add_argument("--frames", type=int, default=2)
+    a = ap.parse_args(argv)
+    t, s, us = traced_launch(a.workload, a.frames)
+    print(to_markdown(a.workload, s, summarise(t, s.n_layers), us, a.frames), flush=True)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])
