@@ -196,8 +196,11 @@ __device__ __forceinline__ int xsw(int i) {
   return ((((i >> 10) << 2) | ((i >> 2) & 3)) << 8) | (((i >> 4) & 63) << 2) | (i & 3);
 }
 
-// Loads per lane in one polling round: the whole vector when it fits in 24 (96 registers of the control wave).
+// Loads per lane in one polling round: at most 16 (64 registers of the control wave).
 constexpr int mb(int n) { return n / 128 < 16 ? n / 128 : 16; }
+// The hidden-1024 shapes poll a vector of up to 3072 cells in one round (24 loads, 96 registers): a second round
+// trip costs about 0.5 us per exchange.
+constexpr int mbh(int n, int H) { return H <= 1024 ? (n / 128 < 24 ? n / 128 : 24) : mb(n); }
 
 // ---- control wave: poll cells into LDS ---------------------------------------------------------------------
 // Waits until cells [idx0, idx0 + n) (n even, idx0 even) all carry epoch e, copying the values to dst.
@@ -234,6 +237,62 @@ __device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, 
       }
     }
     __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// ---- control wave: a whole vector into registers -----------------------------------------------------------
+// Waits until cells [idx0, idx0 + 128 NB) all carry epoch e. Lane holds cells 2 lane + 128 b and 2 lane + 128 b + 1
+// in q[b].x and q[b].z; nothing goes through LDS here, the caller uses the values from registers (reading them
+// back from LDS would cost one LDS round trip per dependent read). Returns false on timeout or when the global
+// error word is set.
+template <int NB>
+__device__ bool poll_regs(const void* cells, uint32_t idx0, uint32_t e, u32x4 (&q)[NB], void* ws, int lane,
+                          const Ctx& c, uint32_t code, int f, int l) {
+  for (uint32_t spin = 0;; spin++) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) q[b] = get2(cells, idx0 + (uint32_t)(2 * lane + 128 * b));
+    bool ok = true;
+#pragma unroll
+    for (int b = 0; b < NB; b++) ok &= q[b].y == e && q[b].w == e;
+    if (__all(ok)) return true;
+    if ((spin & 63) == 63) {
+      if (ld_u32_dev(ws, Ws::kErr) != 0) return false;
+      if (spin > kSpinLimit) {
+        if (lane == 0) fail(c, code, f, l);
+        return false;
+      }
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+template <int NB>
+__device__ __forceinline__ void cells_to_pairs(const u32x4 (&q)[NB], float2 (&v)[NB]) {
+#pragma unroll
+  for (int b = 0; b < NB; b++) v[b] = make_float2(__uint_as_float(q[b].x), __uint_as_float(q[b].z));
+}
+// RMSNorm input staging from registers (lane holds elements 2 lane + 128 b and 2 lane + 128 b + 1 of the residual
+// in v[b], and the norm weights of the same elements in w[b]): the residual to res (natural order, read back by the
+// residual adds), the residual times the weights to xs (swizzled GEMV input), and the sum of squares of the whole
+// vector as the result (wave-uniform). Every LDS write is issued without waiting for another.
+template <int NB>
+__device__ __forceinline__ float stage_rms(const float2 (&v)[NB], const float2 (&w)[NB], float* res, float* xs, int lane) {
+  float ss = 0.f;
+#pragma unroll
+  for (int b = 0; b < NB; b++) {
+    const int i = 2 * lane + 128 * b;  // even: its pair stays adjacent under the swizzle (xsw(i + 1) == xsw(i) + 1)
+    *(float2*)(res + i) = v[b];
+    *(float2*)(xs + xsw(i)) = make_float2(v[b].x * w[b].x, v[b].y * w[b].y);
+    ss += v[b].x * v[b].x;
+    ss += v[b].y * v[b].y;
+  }
+  return wave_sum(ss);
+}
+template <int NB>
+__device__ __forceinline__ void load_pairs(const float* p, float2 (&w)[NB], int lane) {
+#pragma unroll
+  for (int b = 0; b < NB; b++) {
+    const uint64_t u = gload((const uint64_t*)p + lane + 64 * b);  // elements 2 lane + 128 b, + 1
+    w[b] = make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
   }
 }
 
@@ -690,6 +749,10 @@ __device__ __forceinline__ int attn_barriers(const Ck& ck) { return 1 + (ck.n > 
 // ================================================================================================================
 template <int H, int I, int W, int V, bool CP, bool SMP>
 __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
+  // hidden 1024: the RMSNorm inputs are polled into registers and staged from there (kNP element pairs per lane);
+  // the hidden-2048 kernels keep their LDS-staged polls
+  constexpr bool kRegRms = H <= 1024;
+  constexpr int kNP = H / 128;
   const Layout LY(H, I);
   const float eps = c.d.eps;
   const bf16_t* emb = (const bf16_t*)c.d.emb;
@@ -700,12 +763,58 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     const auto ck = make_chunk<CP>(pos, c.r, Cfg<H, I, W, V, CP>::whole(pos));
     for (int l = 0; l < c.L; l++) {
       const sk_layer_desc& Ly = S.desc[l];
+      bool ok = true;
+      float ss = 0.f;
+      if constexpr (kRegRms) {
+        // S1 input from registers: embedding row (layer 0) or the previous layer's residual (polled), times the
+        // input norm; lane holds elements 2 lane + 128 b, + 1
+        float2 w[kNP], v[kNP];
+        load_pairs<kNP>(Ly.in_norm, w, lane);
+        if (lane == 0) c.tr(0, f, l, 0);
+        if (l == 0) {
+          if (CP && f == 0) {
+            load_pairs<kNP>(c.cp.x0, v, lane);
+          } else if (!CP && c.d.in_groups > 0) {
+            // talker_in: the embedding rows of the frame's codes summed in group order, then the pad row
+#pragma unroll
+            for (int b = 0; b < kNP; b++) v[b] = make_float2(0.f, 0.f);
+            for (int gi = 0; gi < c.d.in_groups; gi++) {
+              const bf16_t* tab = (const bf16_t*)uniform((const void*)gload(c.d.in_tabs + gi));
+              const int64_t code = gload(c.d.in_codes + gi);
+#pragma unroll
+              for (int b = 0; b < kNP; b++) {
+                const uint32_t u = gload((const uint32_t*)(tab + (size_t)code * H) + lane + 64 * b);
+                v[b].x += bf2f(u & 0xffffu);
+                v[b].y += bf2f(u >> 16);
+              }
+            }
+#pragma unroll
+            for (int b = 0; b < kNP; b++) {
+              const uint32_t u = gload((const uint32_t*)c.d.in_pad + lane + 64 * b);
+              v[b].x += bf2f(u & 0xffffu);
+              v[b].y += bf2f(u >> 16);
+            }
+          } else {
+            const bf16_t* tab = CP ? (const bf16_t*)uniform(gload(c.cp.emb + f)) : emb;
+#pragma unroll
+            for (int b = 0; b < kNP; b++) {
+              const uint32_t u = gload((const uint32_t*)(tab + (size_t)tok * H) + lane + 64 * b);
+              v[b] = make_float2(bf2f(u & 0xffffu), bf2f(u >> 16));
+            }
+          }
+        } else {
+          after_publish(S, (uint32_t)(f * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
+          u32x4 q[kNP];
+          ok = poll_regs<kNP>(c.cells, LY.e6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
+          cells_to_pairs<kNP>(q, v);
+        }
+        ss = stage_rms<kNP>(v, w, S.hin, S.xs[0], lane);
+      } else {
       // the input norm weights, in registers before the poll (lane holds elements lane + 64 k)
       float nin[H / 64];
 #pragma unroll
       for (int k = 0; k < H / 64; k++) nin[k] = gload(Ly.in_norm + lane + 64 * k);
       // S1 input: embedding row (layer 0) or the previous layer's residual, times the input norm
-      bool ok = true;
       if (lane == 0) c.tr(0, f, l, 0);
       if (l == 0) {
         float ev[H / 64];
@@ -736,11 +845,11 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         after_publish(S, (uint32_t)(f * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
         ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
       }
-      float ss = 0.f;
       for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
       ss = wave_sum(ss);
 #pragma unroll
       for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hin[lane + 64 * k] * nin[k];
+      }
       if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[0] = !ok; c.tr(0, f, l, 1); }
       wg_sync();
       if (!ok) return;
@@ -823,6 +932,15 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       wg_sync();
       if (!ok) return;
       // S5 input: residual after o, times the post-attention norm (loaded while the exchange is under way)
+      if constexpr (kRegRms) {
+        float2 w[kNP], v[kNP];
+        load_pairs<kNP>(Ly.post_norm, w, lane);
+        after_publish(S, (uint32_t)(f * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
+        u32x4 q[kNP];
+        ok = poll_regs<kNP>(c.cells, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
+        cells_to_pairs<kNP>(q, v);
+        ss = stage_rms<kNP>(v, w, S.hmid, S.xs[0], lane);
+      } else {
       float npost[H / 64];
 #pragma unroll
       for (int k = 0; k < H / 64; k++) npost[k] = gload(Ly.post_norm + lane + 64 * k);
@@ -833,24 +951,45 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       ss = wave_sum(ss);
 #pragma unroll
       for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hmid[lane + 64 * k] * npost[k];
+      }
       if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[3] = !ok; c.tr(0, f, l, 6); }
       wg_sync();
       if (!ok) return;
       // S6 input: the whole SwiGLU activation
       after_publish(S, (uint32_t)(f * c.L + l) * 4u + 3u, c.dl[Ws::kHopS6]);
-      ok = poll_cells<mb(I), true>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+      ok = poll_cells<mbh(I, H), true>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
       if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
       wg_sync();
       if (!ok) return;
     }
     if (CP && f == 0) continue;  // the code predictor's position 0 has no head
     // head input: final residual times the final norm
+    bool ok;
+    float ss = 0.f;
+    if constexpr (kRegRms) {
+      float2 w[kNP], v[kNP];
+      load_pairs<kNP>(c.d.norm, w, lane);
+      after_publish(S, (uint32_t)((f + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
+      u32x4 q[kNP];
+      ok = poll_regs<kNP>(c.cells, LY.e6, c.tick(f, c.L - 1, 5), q, c.ws, lane, c, 17u, f, c.L);
+      cells_to_pairs<kNP>(q, v);
+      ss = stage_rms<kNP>(v, w, S.hin, S.xs[0], lane);
+      if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[5] = !ok; }
+      if (!CP && c.d.final_out && c.g == 0 && ok) {  // the final norm's output, h * inv * w (rmsnorm)
+        const float inv = rsqrtf(ss / H + eps);
+#pragma unroll
+        for (int b = 0; b < kNP; b++)
+        {
+          gstore(c.d.final_out + 2 * lane + 128 * b, (v[b].x * inv) * w[b].x);
+          gstore(c.d.final_out + 2 * lane + 128 * b + 1, (v[b].y * inv) * w[b].y);
+        }
+      }
+    } else {
     float nfin[H / 64];
 #pragma unroll
     for (int k = 0; k < H / 64; k++) nfin[k] = gload(c.d.norm + lane + 64 * k);
     after_publish(S, (uint32_t)((f + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
-    bool ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
-    float ss = 0.f;
+    ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
     for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
     ss = wave_sum(ss);
 #pragma unroll
@@ -860,6 +999,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       const float inv = rsqrtf(ss / H + eps);
 #pragma unroll
       for (int k = 0; k < H / 64; k++) gstore(c.d.final_out + lane + 64 * k, (S.hin[lane + 64 * k] * inv) * nfin[k]);
+    }
     }
     wg_sync();
     if (!ok) return;
