@@ -867,59 +867,103 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         const int mh = c.r >> 4, md0 = 8 * (c.r & 15);
         if (!ck.whole) {  // whole-cache attention publishes the S4 input itself
           sleep_units(c.dl[Ws::kHopS3]);  // the compute waves publish their partial right after the last attention barrier
-          for (uint32_t spin = 0;; spin++) {
-            bool good = true;
-            // per chunk 5 cell pairs: (m, l) of head mh, then 4 pairs of its o slice; all loads issued first
-            constexpr int kItems = kChunks * 5, kPer = (kItems + 63) / 64;
-            u32x4 q[kPer];
-#pragma unroll
-            for (int j = 0; j < kPer; j++) {
-              const int it = min(lane + 64 * j, kItems - 1);
-              const int ch = it / 5, k = it % 5;
-              const uint32_t pb = LY.e2 + (c.x * kChunks + ch) * kPartN;
-              q[j] = get2(c.cells, k == 0 ? pb + 2 * mh : pb + 4 + mh * SK_HD + md0 + 2 * (k - 1));
-            }
-#pragma unroll
-            for (int j = 0; j < kPer; j++) {
-              const int it = lane + 64 * j;
-              if (it < kItems) {
-                const int ch = it / 5, k = it % 5;
-                good &= q[j].y == e && q[j].w == e;
-                S.mrg[ch][2 * k] = __uint_as_float(q[j].x);
-                S.mrg[ch][2 * k + 1] = __uint_as_float(q[j].z);
-              }
-            }
-            if (__all(good)) break;
-            if ((spin & 63) == 63) {
-              if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
-              if (spin > kSpinLimit) { if (lane == 0) fail(c, 13u, f, l); ok = false; break; }
-            }
-            __builtin_amdgcn_s_sleep(1);
-          }
-          if (lane == 0) c.tr(0, f, l, 8);
-          if (ok) {
-            // lane = chunk + 32 * half: one exp per chunk, then wave reductions; half hh produces dims
-            // md0 + 4 hh .. md0 + 4 hh + 3 (empty chunks carry m = -inf and weigh nothing)
+          if constexpr (kRegRms) {
+            // lane = chunk + 32 * half: lane polls its chunk's (m, l) of head mh and the 4 dims md0 + 4 half .. + 3 of
+            // its o slice straight into registers (both halves read the same (m, l)), so the merge needs no LDS
             static_assert(kChunks == 32, "merge lane mapping");
             const int ch = lane & 31, hh = lane >> 5;
-            const float mc = S.mrg[ch][0];
-            const float M = wave_max(mc);
-            const float fct = mc == -INFINITY ? 0.f : expf(mc - M);
-            const float Lw = wave_sum(hh == 0 ? fct * S.mrg[ch][1] : 0.f);
-            float od[4];
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-              const float v = row16_sum(fct * S.mrg[ch][2 + 4 * hh + d]);
-              const float h0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
-                               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-              const float h1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
-                               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-              od[d] = Lw > 0.f ? (hh ? h1 : h0) / Lw : 0.f;
+            const uint32_t pb = LY.e2 + (c.x * kChunks + ch) * kPartN;
+            const uint32_t po = pb + 4 + mh * SK_HD + md0 + 4 * hh;
+            u32x4 ml, oa, ob;
+            for (uint32_t spin = 0;; spin++) {
+              ml = get2(c.cells, pb + 2 * mh);
+              oa = get2(c.cells, po);
+              ob = get2(c.cells, po + 2);
+              if (__all(ml.y == e && ml.w == e && oa.y == e && oa.w == e && ob.y == e && ob.w == e)) break;
+              if ((spin & 63) == 63) {
+                if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
+                if (spin > kSpinLimit) { if (lane == 0) fail(c, 13u, f, l); ok = false; break; }
+              }
+              __builtin_amdgcn_s_sleep(1);
             }
-            if (ch == 0) {
-              const uint32_t o0 = LY.e3 + (2 * c.x + mh) * SK_HD + md0 + 4 * hh, e3 = c.tick(f, l, 2);
-              put2(c.cells, o0, od[0], od[1], e3);
-              put2(c.cells, o0 + 2, od[2], od[3], e3);
+            if (lane == 0) c.tr(0, f, l, 8);
+            if (ok) {
+              // one exp per chunk; each half sums its 32 lanes (rows 0 + 1, rows 2 + 3), so lanes 16 and 48 end with
+              // the weight sum and the 4 merged dims of their half (empty chunks carry m = -inf and weigh nothing)
+              const float mc = __uint_as_float(ml.x);
+              const float rm = row16_max(mc);
+              const float M = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 0)),
+                                    __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 16)));
+              const float fct = mc == -INFINITY ? 0.f : expf(mc - M);
+              float v[5] = {fct * __uint_as_float(ml.z), fct * __uint_as_float(oa.x), fct * __uint_as_float(oa.z),
+                            fct * __uint_as_float(ob.x), fct * __uint_as_float(ob.z)};
+#pragma unroll
+              for (int d = 0; d < 5; d++) {
+                v[d] = row16_sum(v[d]);
+                v[d] += dpp<0x142, 0xA>(v[d]);  // row_bcast:15 into rows 1 and 3
+              }
+              if (ch == 16) {
+                const float Lw = v[0];
+                const uint32_t o0 = LY.e3 + (2 * c.x + mh) * SK_HD + md0 + 4 * hh, e3 = c.tick(f, l, 2);
+                put2(c.cells, o0, Lw > 0.f ? v[1] / Lw : 0.f, Lw > 0.f ? v[2] / Lw : 0.f, e3);
+                put2(c.cells, o0 + 2, Lw > 0.f ? v[3] / Lw : 0.f, Lw > 0.f ? v[4] / Lw : 0.f, e3);
+              }
+            }
+          } else {
+            for (uint32_t spin = 0;; spin++) {
+              bool good = true;
+              // per chunk 5 cell pairs: (m, l) of head mh, then 4 pairs of its o slice; all loads issued first
+              constexpr int kItems = kChunks * 5, kPer = (kItems + 63) / 64;
+              u32x4 q[kPer];
+#pragma unroll
+              for (int j = 0; j < kPer; j++) {
+                const int it = min(lane + 64 * j, kItems - 1);
+                const int ch = it / 5, k = it % 5;
+                const uint32_t pb = LY.e2 + (c.x * kChunks + ch) * kPartN;
+                q[j] = get2(c.cells, k == 0 ? pb + 2 * mh : pb + 4 + mh * SK_HD + md0 + 2 * (k - 1));
+              }
+#pragma unroll
+              for (int j = 0; j < kPer; j++) {
+                const int it = lane + 64 * j;
+                if (it < kItems) {
+                  const int ch = it / 5, k = it % 5;
+                  good &= q[j].y == e && q[j].w == e;
+                  S.mrg[ch][2 * k] = __uint_as_float(q[j].x);
+                  S.mrg[ch][2 * k + 1] = __uint_as_float(q[j].z);
+                }
+              }
+              if (__all(good)) break;
+              if ((spin & 63) == 63) {
+                if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
+                if (spin > kSpinLimit) { if (lane == 0) fail(c, 13u, f, l); ok = false; break; }
+              }
+              __builtin_amdgcn_s_sleep(1);
+            }
+            if (lane == 0) c.tr(0, f, l, 8);
+            if (ok) {
+              // lane = chunk + 32 * half: one exp per chunk, then wave reductions; half hh produces dims
+              // md0 + 4 hh .. md0 + 4 hh + 3 (empty chunks carry m = -inf and weigh nothing)
+              static_assert(kChunks == 32, "merge lane mapping");
+              const int ch = lane & 31, hh = lane >> 5;
+              const float mc = S.mrg[ch][0];
+              const float M = wave_max(mc);
+              const float fct = mc == -INFINITY ? 0.f : expf(mc - M);
+              const float Lw = wave_sum(hh == 0 ? fct * S.mrg[ch][1] : 0.f);
+              float od[4];
+#pragma unroll
+              for (int d = 0; d < 4; d++) {
+                const float v = row16_sum(fct * S.mrg[ch][2 + 4 * hh + d]);
+                const float h0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+                                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+                const float h1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
+                                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+                od[d] = Lw > 0.f ? (hh ? h1 : h0) / Lw : 0.f;
+              }
+              if (ch == 0) {
+                const uint32_t o0 = LY.e3 + (2 * c.x + mh) * SK_HD + md0 + 4 * hh, e3 = c.tick(f, l, 2);
+                put2(c.cells, o0, od[0], od[1], e3);
+                put2(c.cells, o0 + 2, od[2], od[3], e3);
+              }
             }
           }
         }
@@ -1470,7 +1514,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     // default start delays per exchange, overridable through the workspace: tuned by coordinate descent on the
     // 0.6B talker, on the 1.7B talker for the spread prefetch (longer exchanges; the merge poll starts ~3 us
     // after the attention) and on the code predictor (no merge; whole-cache attention)
-    constexpr uint8_t kDefault[Ws::kHops] = {17, 23, 35, 23, 17, 32, 26, 20};
+    constexpr uint8_t kDefault[Ws::kHops] = {17, 23, 31, 21, 17, 34, 34, 24};
     constexpr uint8_t kDefaultSpread[Ws::kHops] = {53, 3, 91, 55, 51, 36, 0, 46};
     constexpr uint8_t kDefaultCp[Ws::kHops] = {20, 14, 35, 35, 29, 32, 17, 23};
     const uint32_t w0 = ld_u32_dev(ws, Ws::kPollDelay), w1 = ld_u32_dev(ws, Ws::kPollDelay + 4);
