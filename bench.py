@@ -536,6 +536,8 @@ def main() -> None:
     ap.add_argument("--workload", default="talker06b", choices=["talker06b", "talker17b", "cp06b", "batch17b", "frame06b"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--engine", default="frames", choices=["frames", "graph", "multi"])
+    ap.add_argument("--wd", default="i8row", choices=["i8row", "i8g32", "bf16"],
+                    help="weight format of the talker (the reference's i8g32 and bf16 formats as well as i8row)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--sampling", action="store_true",
                     help="talker06b / talker17b / frame06b with the reference's default sampled decoding (temperature "
@@ -573,7 +575,7 @@ def main() -> None:
         from sokutou_amd.fast import Sampling
 
         smp = Sampling(max_new_tokens=4096)
-    eng, tok = syn.make_engine(name, seed=args.seed, wd="i8row", device=dev, frame_kernel=args.engine != "multi",
+    eng, tok = syn.make_engine(name, seed=args.seed, wd=args.wd, device=dev, frame_kernel=args.engine != "multi",
                                sampling=smp, suppress_tail=1024 if args.sampling else 0)
     if args.engine != "frames":
         eng.capture()
@@ -620,13 +622,14 @@ def main() -> None:
         for _ in range(frames):
             eng.graph.replay()
             codes.append(int(eng.next_id0.item()))
-    gold = ROOT / "tests" / "golden" / f"{name}_seed{args.seed}.json"
+    gold = ROOT / "tests" / "golden" / (f"{name}_seed{args.seed}.json" if args.wd == "i8row" else
+                                        f"{name}_{args.wd}_seed{args.seed}.json")
     parity = None  # sampled runs are checked against the oracle's draws by the tests, not here
     if gold.exists() and not args.sampling:
         parity = codes == json.loads(gold.read_text())["codes"]
 
     # algorithmic bytes per frame, summed over the attended lengths of the 64 frames
-    ab = [algorithmic_bytes(s, pos0 + 1 + f) for f in range(frames)]
+    ab = [algorithmic_bytes(s, pos0 + 1 + f, args.wd) for f in range(frames)]
     step_bytes = sum(a["frame"] for a in ab)
     frame_bytes = step_bytes / frames
     frame_gbs = frame_bytes * fps / 1e9
@@ -659,11 +662,12 @@ def main() -> None:
         else "talker decode frames/sec (1.7B int8, bs1, KV 1024)",
         "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 weights x fp32 accumulate (bf16 KV cache)", "data": "synthetic",
+        "dtype": ("int8" if args.wd.startswith("i8") else args.wd) + " weights x fp32 accumulate (bf16 KV cache)",
+        "data": "synthetic",
         "config": {"workload": f"{name}: {s.n_layers} layers, hidden {s.hidden}, {s.nq}q/{s.nkv}kv heads x 128, "
-                               f"intermediate {s.inter}, codec vocab {s.vocab}, i8row weights, batch 1, KV {pos0}, "
+                               f"intermediate {s.inter}, codec vocab {s.vocab}, {args.wd} weights, batch 1, KV {pos0}, "
                                f"{frames} {'sampled' if args.sampling else 'greedy'} frames per step", "batch": 1, "kv_start": pos0, "frames_per_step": frames,
-                   "weights": "i8row", "engine": args.engine},
+                   "weights": args.wd, "engine": args.engine},
         "roofline": roof,
         "frame": {"us_per_frame": round(1e6 / fps, 2), "us_per_layer": round(1e6 / fps / s.n_layers, 3),
                   "algorithmic_bytes_per_frame": int(frame_bytes), "effective_GBs": round(frame_gbs, 1),

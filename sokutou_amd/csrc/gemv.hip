@@ -1,20 +1,29 @@
-// M=1 weight-only GEMV for the talker projections (qkv, o, gate/up, down, codec head).
+// M=1 weight-only GEMV for the talker projections (qkv, o, gate/up, down, codec head): sk_rms_gemv and sk_gemv,
+// replacing the reference's `rms_gemv` / `gemv` (qwen3/kernels.py:255-310; math of gemv_core 143-253).
 //
-// Replaces the reference's `rms_gemv` / `gemv` kernels (qwen3/kernels.py:143-310). One 256-thread block is four
-// wave64s; each wave owns RPW consecutive rows. Lane l reads 16-byte chunks l, l+64, ... of every row it owns, so
-// a wave's loads of one row are one contiguous 1 KiB stretch of HBM (global_load_dwordx4, nontemporal for
-// weights that are read once per frame). The first chunks are requested before the input vector is staged in
-// LDS, so the weight stream starts at the top of the kernel. Dequantisation happens in registers
-// (v_cvt_f32_i32 with a sign-extended byte select per weight, then v_fmac), and each row's partial sums are
-// reduced across the wave with DPP row operations.
+// Design for CDNA4 (wave64, 256 CUs):
+//  * One workgroup is ONE wave and owns 4 * RG consecutive rows. The wave is four 16-lane groups; group g takes rows
+//    r0 + g + 4 k (k < RG) and its 16 lanes split K: lane q reads 16-byte chunks q, q + 16, q + 32, ... of each of its
+//    rows. A row's result is a 16-lane DPP row sum (four DPP steps; no cross-row or cross-wave reduction). Small
+//    projections (1024 rows) still launch 256 workgroups and fill the chip.
+//  * Each wave stages the input itself in LDS, chunk-major: quarter j (4 floats) of chunk c sits at 16-byte slot
+//    j * nc + c. In one read instruction the 16 lanes of a group read 16 consecutive slots and the four groups read
+//    the same slots (broadcast), and the staging writes are consecutive slots too: no bank conflicts either way, and
+//    no workgroup barrier (one wave). The fused RMSNorm's sum of squares comes from the same staging reads.
+//  * Weights are loaded P chunks per lane and row at a time, double-buffered across passes (two register sets used
+//    alternately, never copied, so no pass waits for younger loads). The first pass is requested before the input is
+//    staged. Loads past the end of a row are clamped to its first chunk and their products dropped, so every load
+//    is unconditional.
+//  * Dequantisation in registers: int8 -> fp32 per byte, fp32 FMA; i8row applies the bf16 row scale after the row
+//    sum, i8g32 the fp16 scale of each 32-element group per 16-element chunk; the RMSNorm factor multiplies the
+//    result (the reference's order, qwen3/kernels.py:180-186, 224).
 #include "common.h"
 #include "internal.h"
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * SK_WAVE;
-constexpr int kU = 4;  // chunks per lane kept in flight per row
+constexpr int kGroups = 4;  // 16-lane row groups per wave
+constexpr int kP = 4;       // chunks per lane and row in one pass
 
 template <int POL>
 __device__ __forceinline__ uint4 ldw(const uint4* p) {
@@ -22,99 +31,155 @@ __device__ __forceinline__ uint4 ldw(const uint4* p) {
   else return *p;
 }
 
-// mode: 0 write, 1 accumulate into out, 2 SwiGLU over interleaved gate/up rows (out[row/2]).
-template <int WD, int RPW, int POL>
-__global__ __launch_bounds__(kThreads) void k_gemv(const float* __restrict__ x, const float* __restrict__ nw, float eps,
-                                                   const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
-                                                   const float* __restrict__ bias, float* __restrict__ out, int N, int K,
-                                                   int mode) {
-  extern __shared__ float xs[];
-  constexpr int E = WdInfo<WD>::E;
-  const int w = threadIdx.x / SK_WAVE, lane = threadIdx.x % SK_WAVE;
-  const int row0 = (blockIdx.x * kWaves + w) * RPW;
-  const int nc = K / E;  // 16-byte chunks per row
-  const size_t row_bytes = (size_t)K * WdInfo<WD>::BYTES;
-  const uint4* wr[RPW];
+// Dot of one 16-byte weight chunk with its E inputs, held as E / 4 float4 quarters.
+template <int WD>
+__device__ __forceinline__ float chunk_dot4(uint4 v, const float4* xv) {
+  if constexpr (WD == SK_WD_I8ROW || WD == SK_WD_I8G32) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float a = 0.f;
 #pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    const int row = row0 + r < N ? row0 + r : 0;
-    wr[r] = (const uint4*)(W + (size_t)row * row_bytes);
-  }
-  uint4 v[kU][RPW];
-#pragma unroll
-  for (int u = 0; u < kU; u++) {
-    const int c = lane + u * SK_WAVE;
-#pragma unroll
-    for (int r = 0; r < RPW; r++)
-      if (c < nc) v[u][r] = ldw<POL>(wr[r] + c);
-  }
-  // stage the input (times the norm weight) and, for the fused RMSNorm, the per-wave sum of squares of x
-  float inv = 1.f;
-  if (nw) {
-    float ss = 0.f;
-    for (int i = lane * 4; i < K; i += SK_WAVE * 4) {
-      float4 a = *(const float4*)(x + i);
-      ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    for (int j = 0; j < 4; j++) {
+      a = __builtin_fmaf((float)(int8_t)(w[j]), xv[j].x, a);
+      a = __builtin_fmaf((float)(int8_t)(w[j] >> 8), xv[j].y, a);
+      a = __builtin_fmaf((float)(int8_t)(w[j] >> 16), xv[j].z, a);
+      a = __builtin_fmaf((float)(int8_t)(w[j] >> 24), xv[j].w, a);
     }
-    inv = rsqrtf(wave_sum(ss) / K + eps);
-    for (int i = threadIdx.x * 4; i < K; i += kThreads * 4) {
-      float4 a = *(const float4*)(x + i), b = *(const float4*)(nw + i);
-      *(float4*)(xs + i) = make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
-    }
+    return a;
+  } else if constexpr (WD == SK_WD_BF16) {
+    float a = bf2f(v.x & 0xffffu) * xv[0].x;
+    a = __builtin_fmaf(bf2f(v.x >> 16), xv[0].y, a);
+    a = __builtin_fmaf(bf2f(v.y & 0xffffu), xv[0].z, a);
+    a = __builtin_fmaf(bf2f(v.y >> 16), xv[0].w, a);
+    a = __builtin_fmaf(bf2f(v.z & 0xffffu), xv[1].x, a);
+    a = __builtin_fmaf(bf2f(v.z >> 16), xv[1].y, a);
+    a = __builtin_fmaf(bf2f(v.w & 0xffffu), xv[1].z, a);
+    a = __builtin_fmaf(bf2f(v.w >> 16), xv[1].w, a);
+    return a;
   } else {
-    for (int i = threadIdx.x * 4; i < K; i += kThreads * 4) *(float4*)(xs + i) = *(const float4*)(x + i);
+    float a = __uint_as_float(v.x) * xv[0].x;
+    a = __builtin_fmaf(__uint_as_float(v.y), xv[0].y, a);
+    a = __builtin_fmaf(__uint_as_float(v.z), xv[0].z, a);
+    a = __builtin_fmaf(__uint_as_float(v.w), xv[0].w, a);
+    return a;
   }
-  __syncthreads();
-  int rs[RPW];  // row index for scale reads, clamped like the weight pointers
+}
+
+// mode: 0 write, 1 accumulate into out, 2 SwiGLU over interleaved gate/up rows (out[row / 2]).
+template <int WD, int RG, int POL>
+__global__ __launch_bounds__(SK_WAVE) void k_gemv(const float* __restrict__ x, const float* __restrict__ nw, float eps,
+                                                  const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
+                                                  const float* __restrict__ bias, float* __restrict__ out, int N, int K,
+                                                  int mode) {
+  constexpr int E = WdInfo<WD>::E, Q = E / 4;  // elements per 16-byte chunk, float4 quarters per chunk
+  extern __shared__ float4 xq[];               // staged input: quarter j of chunk c at slot j * nc + c
+  const int lane = threadIdx.x, grp = lane >> 4, q = lane & 15;
+  const int nc = K / E;  // chunks per row (a multiple of 32: K % 512 == 0)
+  const size_t row_bytes = (size_t)K * WdInfo<WD>::BYTES;
+  const int r0 = blockIdx.x * kGroups * RG;
+  int rows[RG];
+  const uint4* wp[RG];
 #pragma unroll
-  for (int r = 0; r < RPW; r++) rs[r] = row0 + r < N ? row0 + r : 0;
-  float acc[RPW];
+  for (int k = 0; k < RG; k++) {
+    const int row = r0 + grp + kGroups * k;
+    rows[k] = row < N ? row : N - 1;
+    wp[k] = (const uint4*)(W + (size_t)rows[k] * row_bytes);
+  }
+  // pass p covers chunks c = 16 (kP p + i) + q, i < kP; a chunk past the row end is loaded from chunk 0 and dropped
+  // (i8g32: the fp16 scale of each chunk's 32-element group comes with it)
+  auto load_pass = [&](uint4 (&wv)[RG][kP], uint16_t (&sv)[RG][kP], int p) {
 #pragma unroll
-  for (int r = 0; r < RPW; r++) acc[r] = 0.f;
-  for (int base = 0; base < nc; base += kU * SK_WAVE) {
+    for (int i = 0; i < kP; i++) {
+      const int c = 16 * (kP * p + i) + q;
+      const int cc = c < nc ? c : 0;
 #pragma unroll
-    for (int u = 0; u < kU; u++) {
-      const int c = base + lane + u * SK_WAVE;
-      if (c < nc) {
-#pragma unroll
-        for (int r = 0; r < RPW; r++) acc[r] += chunk_dot<WD>(v[u][r], xs + c * E, S, rs[r], K, c);
+      for (int k = 0; k < RG; k++) {
+        wv[k][i] = ldw<POL>(wp[k] + cc);
+        if constexpr (WD == SK_WD_I8G32) sv[k][i] = S[(size_t)rows[k] * (K >> 5) + (cc >> 1)];
       }
     }
-#pragma unroll
-    for (int u = 0; u < kU; u++) {
-      const int c = base + (kU + u) * SK_WAVE + lane;
-#pragma unroll
-      for (int r = 0; r < RPW; r++)
-        if (c < nc) v[u][r] = ldw<POL>(wr[r] + c);
+  };
+  uint4 wa[RG][kP], wb[RG][kP];
+  uint16_t sa[RG][kP], sb[RG][kP];
+  load_pass(wa, sa, 0);
+  // stage the input (times the norm weight), consecutive slots per instruction; sum of squares for the RMSNorm
+  float ss = 0.f;
+  const int nslots = nc * Q;
+  for (int s = lane; s < nslots; s += SK_WAVE) {
+    const int j = s / nc, c = s - j * nc;
+    const int e = c * E + 4 * j;  // first element of the quarter
+    float4 a = *(const float4*)(x + e);
+    if (nw) {
+      ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+      const float4 b = *(const float4*)(nw + e);
+      a = make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
     }
+    xq[s] = a;
   }
-  float y[RPW];
+  const float inv = nw ? rsqrtf(wave_sum(ss) / K + eps) : 1.f;
+  __syncthreads();  // one wave: orders the LDS writes before the reads
+  float acc[RG];
 #pragma unroll
-  for (int r = 0; r < RPW; r++) y[r] = wave_sum(acc[r]) * row_scale<WD>(S, rs[r]) * inv;
-  if (lane != 0) return;
+  for (int k = 0; k < RG; k++) acc[k] = 0.f;
+  auto consume = [&](const uint4 (&wv)[RG][kP], const uint16_t (&sv)[RG][kP], int p) {
+#pragma unroll
+    for (int i = 0; i < kP; i++) {
+      const int c = 16 * (kP * p + i) + q;
+      if (c < nc) {
+        float4 xv[Q];
+#pragma unroll
+        for (int j = 0; j < Q; j++) xv[j] = xq[j * nc + c];
+#pragma unroll
+        for (int k = 0; k < RG; k++) {
+          const float d = chunk_dot4<WD>(wv[k][i], xv);
+          if constexpr (WD == SK_WD_I8G32) acc[k] = __builtin_fmaf(h2f(sv[k][i]), d, acc[k]);
+          else acc[k] += d;
+        }
+      }
+    }
+  };
+  const int npass = (nc + 16 * kP - 1) / (16 * kP);
+  for (int p = 0; p < npass; p += 2) {
+    if (p + 1 < npass) load_pass(wb, sb, p + 1);
+    consume(wa, sa, p);
+    if (p + 1 >= npass) break;
+    if (p + 2 < npass) load_pass(wa, sa, p + 2);
+    consume(wb, sb, p + 1);
+  }
+  float y[RG];
+#pragma unroll
+  for (int k = 0; k < RG; k++) {
+    y[k] = row16_sum(acc[k]);
+    if constexpr (WD == SK_WD_I8ROW) y[k] *= bf2f(S[rows[k]]);
+    y[k] *= inv;
+  }
   if (mode == 2) {
+    // rows 2n (group 0 / 2) and 2n + 1 (group 1 / 3) meet through a lane permute
 #pragma unroll
-    for (int r = 0; r + 1 < RPW; r += 2)
-      if (row0 + r + 1 < N) out[(row0 + r) >> 1] = silu_mul(y[r], y[r + 1]);
+    for (int k = 0; k < RG; k++) {
+      const float up = __shfl_down(y[k], 16);
+      const int row = r0 + grp + kGroups * k;
+      if (q == 0 && (grp & 1) == 0 && row + 1 < N) out[row >> 1] = silu_mul(y[k], up);
+    }
     return;
   }
+  if (q != 0) return;
 #pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    const int row = row0 + r;
+  for (int k = 0; k < RG; k++) {
+    const int row = r0 + grp + kGroups * k;
     if (row >= N) break;
-    float o = y[r];
+    float o = y[k];
     if (bias) o += bias[row];
     if (mode == 1) o += out[row];
     out[row] = o;
   }
 }
 
-template <int WD, int RPW, int POL>
-hipError_t launch_rpw(const float* x, const float* nw, float eps, const void* W, const uint16_t* S, const float* bias,
-                      float* out, int N, int K, int mode, hipStream_t st) {
-  const int rows_per_block = kWaves * RPW;
+template <int WD, int RG, int POL>
+hipError_t launch_rg(const float* x, const float* nw, float eps, const void* W, const uint16_t* S, const float* bias,
+                     float* out, int N, int K, int mode, hipStream_t st) {
+  const int rows_per_block = kGroups * RG;
   dim3 grid((N + rows_per_block - 1) / rows_per_block);
-  hipLaunchKernelGGL((k_gemv<WD, RPW, POL>), grid, dim3(kThreads), K * sizeof(float), st, x, nw, eps,
+  hipLaunchKernelGGL((k_gemv<WD, RG, POL>), grid, dim3(SK_WAVE), K * sizeof(float), st, x, nw, eps,
                      (const uint8_t*)W, S, bias, out, N, K, mode);
   return hipGetLastError();
 }
@@ -122,11 +187,9 @@ hipError_t launch_rpw(const float* x, const float* nw, float eps, const void* W,
 template <int WD, int POL>
 hipError_t launch_wd(const float* x, const float* nw, float eps, const void* W, const uint16_t* S, const float* bias,
                      float* out, int N, int K, int mode, hipStream_t st) {
-  // Pick the rows per wave so that the grid has at least 256 blocks (one per CU) when N allows; SwiGLU needs an
-  // even count so gate and up rows meet in one wave.
-  if (N >= 256 * kWaves * 4) return launch_rpw<WD, 4, POL>(x, nw, eps, W, S, bias, out, N, K, mode, st);
-  if (N >= 256 * kWaves * 2 || mode == 2) return launch_rpw<WD, 2, POL>(x, nw, eps, W, S, bias, out, N, K, mode, st);
-  return launch_rpw<WD, 1, POL>(x, nw, eps, W, S, bias, out, N, K, mode, st);
+  // two rows per group once that still leaves at least 512 workgroups (two waves per CU)
+  if (N >= 512 * kGroups * 2) return launch_rg<WD, 2, POL>(x, nw, eps, W, S, bias, out, N, K, mode, st);
+  return launch_rg<WD, 1, POL>(x, nw, eps, W, S, bias, out, N, K, mode, st);
 }
 
 template <int POL>

@@ -104,31 +104,77 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_greedy(const float* _
 }
 
 // ---- sampled pick: processor, temperature, top-k threshold, Gumbel-max (qwen3/sampler.py:37-159) -----------------
-// One block of 1024 threads, 4 entries per thread. The top_k-th largest key is found by a radix select over the
-// four bytes of the order key, most significant first: a 256-bin LDS histogram of the entries that match the
-// digits chosen so far, then one wave scans the bins from the top to find the digit where the count reaches the
-// rank still needed. Every entry whose key is at least that threshold (ties included) and that is not -inf competes
-// with v - log(-log(u)), u from Philox4x32-10 with counter (index, draw lo, draw hi, 0x51) and key (seed lo, seed
-// hi); the largest wins, the lowest index on ties. Afterwards the draw counter advances by one.
-__global__ __launch_bounds__(kSampleThreads) void k_sample_draw(const float* __restrict__ logits, int V, float inv_temp,
-                                                                int top_k, uint8_t* __restrict__ seen, float rep_pen,
-                                                                const uint8_t* __restrict__ suppress,
-                                                                int64_t* __restrict__ ngen, int min_new, int eos,
-                                                                const uint64_t* __restrict__ seed,
-                                                                uint64_t* __restrict__ counter, int64_t* __restrict__ out,
-                                                                int talker, int64_t* __restrict__ id0,
-                                                                int64_t* __restrict__ pos) {
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t s_prefix, s_need;
-  __shared__ float best_v[kSampleThreads / SK_WAVE];
-  __shared__ int best_i[kSampleThreads / SK_WAVE];
+// One block of 1024 threads; thread t holds entries t + 1024 j (j < 4) in registers as processed values and their
+// order keys. The threshold (the key of the top_k-th largest value, ties kept) is found without a histogram:
+//  * bound: the top_k-th largest of 256 group maxima (16 consecutive entries per group, a DPP row max) is a lower
+//    bound of the threshold, since the maxima are themselves entries (top_k <= 256);
+//  * candidates: the keys at or above the bound are compacted into LDS (one ballot per register and one LDS atomic
+//    per wave for the wave's offset); typically a few times top_k of them;
+//  * wave 0 bisects the key space, bit by bit from the highest bit where the bound and the largest key differ,
+//    counting the candidates at or above each probe with ballots. Below the bound every count reaches top_k, as it
+//    does over all entries, so the result is the full-vocabulary threshold.
+// Larger top_k (256 < top_k < V) bisects over all entries, every wave counting its own with ballots per step.
+// Entries past V carry key 0, which no probe counts (every probe is at least 1). Then every entry at or above the
+// threshold that is not -inf draws its Gumbel value v - log(-log(u)), u from Philox4x32-10 with counter (index,
+// draw lo, draw hi, 0x51) and key (seed lo, seed hi); the largest wins, the lowest index on ties (a wave max of the
+// value, then a wave max of the complemented index among the lanes holding it). Afterwards the draw counter advances.
+constexpr int kDrawThreads = 1024, kDrawWaves = kDrawThreads / SK_WAVE, kDrawPer = SK_MAX_V / kDrawThreads;
+constexpr int kBoundGroups = 256;  // groups of 16 entries: SK_MAX_V / 16
+
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = max(v, dpp_u32<0x124>(v));  // row_ror:4
+  v = max(v, dpp_u32<0x128>(v));  // row_ror:8
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {  // uniform result
+  v = row16_max_u32(v);
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+// The largest key t in [lo, hi] whose count (keys >= t) reaches K, given count(lo) >= K: the bits above the highest
+// bit where lo and hi differ are common to every such key; below it the key grows one bit at a time, each bit kept
+// when the count at the key with that bit set still reaches K.
+template <class F>
+__device__ __forceinline__ uint32_t kth_key(uint32_t lo, uint32_t hi, uint32_t K, F count) {
+  if (lo >= hi) return lo;
+  const int top = 31 - __builtin_clz(lo ^ hi);
+  uint32_t p = top == 31 ? 0u : lo & ~((2u << top) - 1u);
+  for (int b = top; b >= 0; b--) {
+    const uint32_t t = p | (1u << b);
+    if (count(t) >= K) p = t;
+  }
+  return p;
+}
+
+__global__ __launch_bounds__(kDrawThreads) void k_sample_draw(const float* __restrict__ logits, int V, float inv_temp,
+                                                               int top_k, uint8_t* __restrict__ seen, float rep_pen,
+                                                               const uint8_t* __restrict__ suppress,
+                                                               int64_t* __restrict__ ngen, int min_new, int eos,
+                                                               const uint64_t* __restrict__ seed,
+                                                               uint64_t* __restrict__ counter, int64_t* __restrict__ out,
+                                                               int talker, int64_t* __restrict__ id0,
+                                                               int64_t* __restrict__ pos) {
+  __shared__ uint32_t gmax[kBoundGroups];
+  __shared__ uint32_t cand[SK_MAX_V];
+  __shared__ uint32_t wsum[kDrawWaves];
+  __shared__ uint32_t wpick[kDrawWaves];
+  __shared__ uint32_t s_n, s_lb, s_thr;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const bool block_eos = talker && ngen && ngen[0] < min_new;
-  float l[kPer];
+  float xv[kDrawPer];
+  uint32_t key[kDrawPer];
 #pragma unroll
-  for (int j = 0; j < kPer; j++) {
-    const int i = t + j * kSampleThreads;
+  for (int j = 0; j < kDrawPer; j++) {
+    const int i = t + j * kDrawThreads;
     float v = -INFINITY;
+    key[j] = 0u;
     if (i < V) {
       v = logits[i];
       if (talker) {
@@ -137,79 +183,127 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_draw(const float* __r
         if (block_eos && i == eos) v = -INFINITY;
       }
       v *= inv_temp;
+      key[j] = order_key(v);
     }
-    l[j] = v;
+    xv[j] = v;
   }
-  uint32_t thr = 0;
+  uint32_t thr = 0;  // 0 keeps every entry (top_k <= 0 or >= V)
   if (top_k > 0 && top_k < V) {
-    if (t == 0) { s_prefix = 0; s_need = (uint32_t)top_k; }
-    for (int pass = 0; pass < 4; pass++) {
-      const int shift = 24 - 8 * pass;
-      if (t < 256) hist[t] = 0;
-      __syncthreads();
-      const uint32_t prefix = s_prefix, need = s_need;
+    const uint32_t K = (uint32_t)top_k;
+    if (top_k <= kBoundGroups) {
+      // bound: group maxima (lanes 16 r .. 16 r + 15 hold 16 consecutive entries of each j)
 #pragma unroll
-      for (int j = 0; j < kPer; j++) {
-        const int i = t + j * kSampleThreads;
-        if (i >= V) continue;
-        const uint32_t k = order_key(l[j]);
-        if (pass == 0 || ((k ^ prefix) >> (shift + 8)) == 0) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+      for (int j = 0; j < kDrawPer; j++) {
+        const uint32_t m = row16_max_u32(key[j]);
+        if ((lane & 15) == 0) gmax[(j * kDrawWaves + w) * 4 + (lane >> 4)] = m;
+      }
+      if (t == 0) s_n = 0;
+      __syncthreads();
+      if (w == 0) {
+        uint32_t g4[4], lo = 0xffffffffu, hi = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          g4[q] = gmax[lane + 64 * q];
+          lo = min(lo, g4[q]);
+          hi = max(hi, g4[q]);
+        }
+        lo = ~wave_max_u32(~lo);
+        hi = wave_max_u32(hi);
+        const uint32_t lb = kth_key(lo, hi, K, [&](uint32_t x) {
+          uint32_t c = 0;
+#pragma unroll
+          for (int q = 0; q < 4; q++) c += (uint32_t)__popcll(__ballot(g4[q] >= x));
+          return c;
+        });
+        if (lane == 0) s_lb = lb;
+      }
+      __syncthreads();
+      const uint32_t lb = s_lb;
+      // candidates: keys >= lb (key 0 is never a candidate: no probe counts it)
+#pragma unroll
+      for (int j = 0; j < kDrawPer; j++) {
+        const bool take = key[j] >= lb && key[j] != 0u;
+        const uint64_t msk = __ballot(take);
+        uint32_t base = 0;
+        if (lane == 0 && msk) base = atomicAdd(&s_n, (uint32_t)__popcll(msk));
+        base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+        if (take) cand[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(msk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)msk, 0u))] = key[j];
       }
       __syncthreads();
       if (w == 0) {
-        // lane L holds bins 255 - 4L .. 252 - 4L (descending); inclusive scan of the counts over the lanes
-        uint32_t c[4], sum = 0;
+        const uint32_t n = s_n;
+        uint32_t hi = 0;
+        for (uint32_t c = (uint32_t)lane; c < n; c += 64) hi = max(hi, cand[c]);
+        hi = wave_max_u32(hi);
+        uint32_t r;
+        if (n <= 256) {  // the candidate keys stay in registers for the whole bisection
+          uint32_t c4[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) { c[q] = hist[255 - (4 * lane + q)]; sum += c[q]; }
-        uint32_t inc = sum;
+          for (int q = 0; q < 4; q++) c4[q] = (uint32_t)(lane + 64 * q) < n ? cand[lane + 64 * q] : 0u;
+          r = kth_key(lb, hi, K, [&](uint32_t x) {
+            uint32_t c = 0;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const uint32_t y = __shfl_up(inc, o);
-          if (lane >= o) inc += y;
-        }
-        const uint32_t before = inc - sum;
-        if (before < need && inc >= need) {
-          uint32_t acc = before;
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            if (acc + c[q] >= need) {
-              const uint32_t digit = 255u - (uint32_t)(4 * lane + q);
-              s_prefix = prefix | (digit << shift);
-              s_need = need - acc;
-              break;
+            for (int q = 0; q < 4; q++) c += (uint32_t)__popcll(__ballot(c4[q] >= x));
+            return c;
+          });
+        } else {
+          r = kth_key(lb, hi, K, [&](uint32_t x) {
+            uint32_t c = 0;
+            for (uint32_t b = 0; b < n; b += 64) {
+              const uint32_t i = b + (uint32_t)lane;
+              c += (uint32_t)__popcll(__ballot(i < n && cand[i] >= x));
             }
-            acc += c[q];
-          }
+            return c;
+          });
         }
+        if (lane == 0) s_thr = r;
       }
       __syncthreads();
+      thr = s_thr;
+    } else {
+      // every wave counts its own keys per probe; the counts meet in LDS (two barriers per bit)
+      uint32_t p = 0;
+      for (int b = 31; b >= 0; b--) {
+        const uint32_t x = p | (1u << b);
+        uint32_t c = 0;
+#pragma unroll
+        for (int j = 0; j < kDrawPer; j++) c += (uint32_t)__popcll(__ballot(key[j] >= x));
+        if (lane == 0) wsum[w] = c;
+        __syncthreads();
+        uint32_t tot = 0;
+#pragma unroll
+        for (int q = 0; q < kDrawWaves; q++) tot += wsum[q];
+        __syncthreads();
+        if (tot >= K) p = x;
+      }
+      thr = p;
     }
-    thr = s_prefix;
   }
+  // Gumbel-max over the kept entries
   const uint64_t sd = seed[0], cnt = counter[0];
   float best = -INFINITY;
-  int bi = 0x7fffffff;
+  uint32_t bi = 0xffffffffu;
 #pragma unroll
-  for (int j = 0; j < kPer; j++) {
-    const int i = t + j * kSampleThreads;
-    if (i >= V) continue;
-    const float v = l[j];
-    if (order_key(v) < thr || v == -INFINITY) continue;
-    const float g = gumbel(v, (uint32_t)i, cnt, (uint32_t)sd, (uint32_t)(sd >> 32));
-    if (g > best || (g == best && i < bi)) { best = g; bi = i; }
+  for (int j = 0; j < kDrawPer; j++) {
+    const int i = t + j * kDrawThreads;
+    if (i >= V || key[j] < thr || xv[j] == -INFINITY) continue;
+    const float g = gumbel(xv[j], (uint32_t)i, cnt, (uint32_t)sd, (uint32_t)(sd >> 32));
+    if (g > best || (g == best && (uint32_t)i < bi)) { best = g; bi = (uint32_t)i; }  // NaN never wins
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ob = __shfl_xor(best, o);
-    const int oi = __shfl_xor(bi, o);
-    if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
-  }
-  if (lane == 0) { best_v[w] = best; best_i[w] = bi; }
+  // wave: the largest value (as an order key; -0 made +0 so equal values have equal keys), then the lowest index
+  // among the lanes holding it
+  const uint32_t mk = order_key(best == 0.f ? 0.f : best);
+  const uint32_t bk = wave_max_u32(mk);
+  const uint32_t bidx = ~wave_max_u32(mk == bk ? ~bi : 0u);
+  if (lane == 0) { wsum[w] = bk; wpick[w] = bidx; }
   __syncthreads();
-  if (t != 0) return;
-  for (int q = 0; q < kSampleThreads / SK_WAVE; q++)
-    if (best_v[q] > best || (best_v[q] == best && best_i[q] < bi)) { best = best_v[q]; bi = best_i[q]; }
-  const int64_t id = bi == 0x7fffffff ? 0 : bi;
+  if (w != 0) return;
+  const uint32_t k2 = lane < kDrawWaves ? wsum[lane] : 0u;
+  const uint32_t i2 = lane < kDrawWaves ? wpick[lane] : 0xffffffffu;
+  const uint32_t tk = wave_max_u32(k2);
+  const uint32_t pick = ~wave_max_u32(k2 == tk ? ~i2 : 0u);
+  if (lane != 0) return;
+  const int64_t id = pick >= (uint32_t)V ? 0 : (int64_t)pick;  // nothing kept: index 0
   out[0] = id;
   counter[0] = cnt + 1;
   if (talker) {
@@ -292,7 +386,7 @@ extern "C" int sk_sample(const float* logits, int V, float inv_temp, int top_k, 
   if (do_sample) {
     if (!seed || !counter) return sk_set_error(SK_EINVAL, "sk_sample: sampling needs the device seed and counter");
     if (!(inv_temp > 0.f) || inv_temp == INFINITY) return sk_set_error(SK_EINVAL, "sk_sample: temperature must be > 0");
-    hipLaunchKernelGGL(k_sample_draw, dim3(1), dim3(kSampleThreads), 0, (hipStream_t)stream, logits, V, inv_temp, top_k,
+    hipLaunchKernelGGL(k_sample_draw, dim3(1), dim3(kDrawThreads), 0, (hipStream_t)stream, logits, V, inv_temp, top_k,
                        seen, rep_pen, suppress, ngen, min_new, eos, seed, counter, out, talker, id0, pos);
     return sk_check_launch(hipGetLastError(), "sk_sample");
   }
