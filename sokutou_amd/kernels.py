@@ -28,6 +28,54 @@ from .sampler import FusedSampler
 HD = 128
 
 
+def _engine_kv_cache(config, max_len: int, kc: torch.Tensor, vc: torch.Tensor):
+    """The engine's talker cache as a transformers ``StaticCache`` whose layers' key and value tensors are views of
+    ``kc[i]`` / ``vc[i]`` ([nkv, max_len, 128] -> [1, nkv, max_len, 128], the same memory layout), so the talker's
+    Hugging Face modules write a prompt's keys and values straight into the cache the kernels read (the reference
+    shares the StaticCache tensors the same way, qwen3/kernels.py:695-703). transformers 5 static layers keep their own
+    write position instead of reading ``cache_position``; ``seek(pos)`` sets it (every layer, on the device, so it
+    can be recorded in a graph). A model computing in another precision than the cache attends over this call's rows
+    in its own precision and over earlier rows as stored."""
+    from transformers import StaticCache
+    from transformers.cache_utils import StaticLayer
+
+    class _ViewLayer(StaticLayer):
+        def __init__(self, keys: torch.Tensor, values: torch.Tensor):
+            super().__init__(max_cache_len=int(keys.shape[1]))
+            self.keys, self.values = keys.unsqueeze(0), values.unsqueeze(0)
+            self.dtype, self.device = keys.dtype, keys.device
+            self.batch_size, self.num_heads = 1, int(keys.shape[0])
+            self.k_head_dim = self.v_head_dim = int(keys.shape[-1])
+            self.cumulative_length = torch.zeros((), dtype=torch.long, device=keys.device)
+            self.is_initialized = True
+
+        def update(self, key_states, value_states, *args, **kwargs):
+            idx = torch.arange(int(key_states.shape[-2]), device=self.device) + self.cumulative_length
+            self.cumulative_length.add_(int(key_states.shape[-2]))
+            self.keys.index_copy_(2, idx, key_states.to(self.dtype))
+            self.values.index_copy_(2, idx, value_states.to(self.dtype))
+            if key_states.dtype == self.dtype:
+                return self.keys, self.values
+            k, v = self.keys.to(key_states.dtype), self.values.to(value_states.dtype)
+            k.index_copy_(2, idx, key_states)
+            v.index_copy_(2, idx, value_states)
+            return k, v
+
+        def reset(self) -> None:
+            self.cumulative_length.zero_()
+
+    class _EngineCache(StaticCache):
+        def seek(self, pos: int = 0) -> None:
+            for layer in self.layers:
+                layer.cumulative_length.fill_(int(pos))
+
+    cache = _EngineCache(config=config, max_cache_len=max_len)
+    if len(cache.layers) != kc.shape[0]:
+        raise ValueError(f"the talker config has {len(cache.layers)} layers, the engine's cache {kc.shape[0]}")
+    cache.layers = [_ViewLayer(kc[i], vc[i]) for i in range(kc.shape[0])]
+    return cache
+
+
 class _Lin:
     """One matrix [N, K] in the kernels' format. ``wd``: ``i8row`` int8 + bf16 scale per row
     (s = bf16(max(max|w|/127, 1e-12)), q = clamp(round_half_even(w/s), +-127)); ``i8g32`` int8 + fp16 scale per
@@ -306,6 +354,10 @@ class Qwen3Kernels(Qwen3Fast):
         self.vc = torch.zeros_like(self.kc)
         self.tk = list(self.kc.unbind(0))
         self.tv = list(self.vc.unbind(0))
+        # the same cache for the talker's Hugging Face modules (the prompt prefill), when they are runnable
+        hf_cfg = getattr(getattr(self.talker, "model", None), "config", None)
+        self.tcache = (_engine_kv_cache(hf_cfg, max_cache, self.kc, self.vc)
+                       if hasattr(hf_cfg, "get_text_config") and callable(self.talker.model) else None)
         nbytes = int(L.sk_attn_workspace_size(P.nq, P.nkv, max_cache))
         self.attn_ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         self.trace: list[torch.Tensor] | None = None
@@ -594,41 +646,55 @@ class Qwen3Kernels(Qwen3Fast):
 
     def _start(self, kw: dict) -> int:
         """Frame state after the prompt. With ``inputs_embeds`` (the reference's generate kwargs) the prompt runs
-        through the talker's Hugging Face modules here (``_prefill_hf``); otherwise the prefill ran elsewhere and
+        through the talker's Hugging Face modules into the shared cache (``_prefill``: one recorded graph per prompt
+        length, or eagerly without graphs); otherwise the prefill ran elsewhere and
         ``prefill_len``, ``first_token`` and, with a code predictor, ``last_hidden`` (the talker's last hidden state
         after its final norm, which the reference takes from the prefill, qwen3/kernels.py:678-679) give its
         results. ``tts_pad_embed`` as in qwen3/kernels.py:709."""
         if self.cp is not None and "tts_pad_embed" in kw:
             self.pad16.copy_(torch.as_tensor(kw["tts_pad_embed"]).reshape(-1).to(self.pad16))
         if "inputs_embeds" in kw:
-            return self._prefill_hf(torch.as_tensor(kw["inputs_embeds"]))
+            embeds = torch.as_tensor(kw["inputs_embeds"])
+            self._check_prompt(embeds)
+            self._prefill(embeds.to(device=self.device, dtype=self._prompt_dtype()))
+            return int(embeds.shape[1])
         if self.cp is not None and "last_hidden" in kw:
             self.ph32.copy_(torch.as_tensor(kw["last_hidden"]).reshape(-1).to(self.ph32))
         L = int(kw["prefill_len"])
         self.reset(L, int(kw["first_token"]))
         return L
 
-    def warm_prefill(self, lengths) -> float:
-        """The reference records one prefill graph per prompt length (qwen3/fast.py:287-293); this engine's
-        prefill runs eagerly, so there is nothing to record. Returns the seconds spent: 0.0."""
-        return 0.0
+    def _prompt_dtype(self) -> torch.dtype:
+        model = getattr(self.talker, "model", None)
+        params = getattr(model, "parameters", None)
+        p = next(params(), None) if callable(params) else None
+        return p.dtype if p is not None else self.dtype
 
-    @torch.no_grad()
-    def _prefill_hf(self, embeds: torch.Tensor) -> int:
-        """The prompt (1, L, H) through the talker's Hugging Face modules, as the reference's _prefill_body
-        (qwen3/fast.py:251-263): one forward pass over positions 0..L-1 with a fresh cache, whose keys and values
-        are then written into this engine's cache (positions [0, L), in the cache's dtype; the reference shares
-        the StaticCache tensors instead, qwen3/kernels.py:695-703); the first code from the last hidden state through
-        the codec head, the processor and the torch-path sampler, as the reference draws it; and the last hidden
-        state (after the final norm) kept for the code predictor (qwen3/kernels.py:653-654). Runs eagerly (the
-        reference replays one captured graph per prompt length)."""
-        L, hidden = self._prefill_run(embeds)
+    def _check_prompt(self, embeds: torch.Tensor) -> None:
+        if self.tcache is None:
+            raise RuntimeError("prompt prefill needs the talker's runnable Hugging Face modules (tts.model.talker.model)")
+        if embeds.dim() != 3 or embeds.shape[0] != 1:
+            raise ValueError(f"inputs_embeds must be (1, L, H), got {tuple(embeds.shape)}")
+        L = int(embeds.shape[1])
+        if L < 1 or L >= self.max_cache:
+            raise ValueError(f"prompt too long ({L} tokens, cache {self.max_cache})")
+
+    def _prefill_body(self, embeds: torch.Tensor, cpos: torch.Tensor) -> None:
+        """The prompt through the talker's Hugging Face modules into the shared cache (positions [0, L)), then what
+        the reference's _prefill_body leaves (qwen3/fast.py:251-263 with _after_prefill, qwen3/kernels.py:695-703):
+        the first code drawn from the codec head through the processor and the torch-path sampler, ``seen`` holding
+        it, ``ngen`` 1, ``pos`` L, and the last hidden state (after the final norm) for the code predictor. Device
+        work only, so it can be recorded in a graph."""
         self.seen.zero_()
         self.ngen.zero_()
+        hidden = self._prefill_run(embeds, cpos)
         first = _sample(self._process(self._head_logits(hidden)), self.s.do_sample, self.s.temperature, self.s.top_k)
+        self.id0.copy_(first)
+        self.next_id0.copy_(first)
         self.ph32.copy_(hidden[0, -1].float())
-        self.reset(L, int(first.item()))
-        return L
+        self.seen.scatter_(1, first, True)
+        self.ngen.fill_(1)
+        self.pos.fill_(int(embeds.shape[1]))
 
     def _head_logits(self, hidden: torch.Tensor) -> torch.Tensor:
         """fp32 (1, V) codec-head logits of the last position of ``hidden`` through the talker's own module."""
@@ -636,28 +702,14 @@ class Qwen3Kernels(Qwen3Fast):
         logits = head(hidden) if callable(head) else torch.nn.functional.linear(hidden, head.weight.to(hidden.dtype))
         return logits[:, -1, :].to(torch.float32)
 
-    def _prefill_run(self, embeds: torch.Tensor) -> tuple[int, torch.Tensor]:
-        """The talker's Hugging Face modules over the prompt (1, L, H) with a fresh cache; its keys and values are
-        written into positions [0, L) of this engine's cache. Returns (L, last_hidden_state)."""
-        from transformers import DynamicCache
-
-        if self.talker is None or not callable(getattr(self.talker, "model", None)):
-            raise RuntimeError("prompt prefill needs the talker's runnable Hugging Face modules (tts.model.talker)")
-        if embeds.dim() != 3 or embeds.shape[0] != 1:
-            raise ValueError(f"inputs_embeds must be (1, L, H), got {tuple(embeds.shape)}")
+    def _prefill_run(self, embeds: torch.Tensor, cpos: torch.Tensor | None = None) -> torch.Tensor:
+        """The talker's Hugging Face modules over the prompt (1, L, H), writing its keys and values into positions
+        [0, L) of the engine's cache through ``tcache``. Returns the last hidden state (after the final norm)."""
         L = int(embeds.shape[1])
-        if L < 1 or L >= self.max_cache:
-            raise ValueError(f"prompt too long ({L} tokens, cache {self.max_cache})")
-        cache = DynamicCache()
-        out = self.talker.model(inputs_embeds=embeds.to(self.device), past_key_values=cache,
-                                cache_position=torch.arange(L, device=self.device), use_cache=True)
-        hidden = out.last_hidden_state
-        if len(cache.layers) != self.kc.shape[0]:
-            raise RuntimeError("the prefill cache has a different layer count than the talker stack")
-        for i, layer in enumerate(cache.layers):
-            self.kc[i, :, :L].copy_(layer.keys[0])
-            self.vc[i, :, :L].copy_(layer.values[0])
-        return L, hidden
+        cpos = torch.arange(L, device=self.device) if cpos is None else cpos
+        self.tcache.seek(0)
+        out = self.talker.model(inputs_embeds=embeds, past_key_values=self.tcache, cache_position=cpos, use_cache=True)
+        return out.last_hidden_state
 
     @torch.no_grad()
     def teacher_logits(self, kw: dict, codes: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -676,7 +728,10 @@ class Qwen3Kernels(Qwen3Fast):
             raise ValueError(f"codes must be (frames, {self.G}), got {tuple(codes.shape)}")
         if "tts_pad_embed" in kw:
             self.pad16.copy_(torch.as_tensor(kw["tts_pad_embed"]).reshape(-1).to(self.pad16))
-        L, hidden = self._prefill_run(torch.as_tensor(kw["inputs_embeds"]))
+        embeds = torch.as_tensor(kw["inputs_embeds"])
+        self._check_prompt(embeds)
+        L = int(embeds.shape[1])
+        hidden = self._prefill_run(embeds.to(device=self.device, dtype=self._prompt_dtype()))
         if L + codes.shape[0] > self.max_cache:
             raise ValueError(f"prompt of {L} and {codes.shape[0]} frames exceed the cache ({self.max_cache})")
         l0 = [self._head_logits(hidden).cpu()]

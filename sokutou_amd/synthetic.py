@@ -388,16 +388,17 @@ def make_engine(name: str, seed: int = 0, wd: str = "i8row", device="cuda", grap
     return eng, tok
 
 
-def hf_talker_model(seed: int, s: TalkerShape, device="cpu"):
-    """transformers' Qwen3Model (fp32, eager attention) holding the seeded synthetic weights of shape ``s``: a
-    runnable stand-in for ``tts.model.talker.model``, for prompts given as ``inputs_embeds``."""
+def hf_talker_model(seed: int, s: TalkerShape, device="cpu", attn: str = "sdpa"):
+    """transformers' Qwen3Model (fp32; SDPA attention as the reference loads the talker, qwen3/serve.py:89, or
+    ``attn``) holding the seeded synthetic weights of shape ``s``: a runnable stand-in for
+    ``tts.model.talker.model``, for prompts given as ``inputs_embeds``."""
     from transformers import Qwen3Config, Qwen3Model
 
     cfg = Qwen3Config(hidden_size=s.hidden, intermediate_size=s.inter, num_attention_heads=s.nq,
                       num_key_value_heads=s.nkv, head_dim=s.head_dim, rms_norm_eps=s.eps, num_hidden_layers=s.n_layers,
                       vocab_size=s.vocab, rope_parameters={"rope_type": "default", "rope_theta": s.theta},
                       attention_bias=False)
-    cfg._attn_implementation = "eager"
+    cfg._attn_implementation = attn
     model = Qwen3Model(cfg).float().eval()
     final = final_weights(seed, s)
     with torch.no_grad():
@@ -453,3 +454,78 @@ def make_cp_engine(name: str = "cp06b", seed: int = 0, device="cuda"):
     s = workload_shape(name)
     cp, temb = make_code_predictor(seed, s, device=device, n_positions=spec["positions"])
     return CodePredictor(cp, temb, n_positions=spec["positions"], wd="i8row", device=device)
+
+
+# ---------------------------------------------------------------------------------------------------------
+# an HF-shaped stand-in for the qwen-tts object (prompt interception, prefill, speech-tokenizer decode)
+# ---------------------------------------------------------------------------------------------------------
+class _ToyCodecDecoder(torch.nn.Module):
+    """A causal stand-in for the speech tokenizer's decoder: codes (1, G, F) int64 -> waveform (1, 1, F * up). Each
+    frame's samples come from the sum of its G code embeddings plus half the previous frame's (one frame of left
+    context), so a prefix of frames decodes the same whatever follows, as the real causal decoder does."""
+
+    def __init__(self, seed: int, groups: int, vocab: int, up: int):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        self.tables = torch.nn.Parameter(torch.randn(groups, vocab, up, generator=g) * 0.1, requires_grad=False)
+        self.total_upsample = up
+
+    def forward(self, codes: torch.Tensor) -> torch.Tensor:
+        G = self.tables.shape[0]
+        x = sum(self.tables[g][codes[0, g]] for g in range(G))  # (F, up)
+        prev = torch.cat([torch.zeros_like(x[:1]), x[:-1]], dim=0)
+        return torch.tanh(x + 0.5 * prev).reshape(1, 1, -1)
+
+
+def make_hf_tts(name: str = "small06b", seed: int = 0, device="cpu", up: int = 40):
+    """A ``tts`` object with what the prompt, prefill and decode paths of the engine read from qwen-tts
+    (qwen3/fast.py:127-147, 251-368): ``generate_custom_voice`` builds a prompt from the text (rows N(0, 0.02) from
+    a seed of the text, length 6 + len(text)) and hands it to ``model.talker.generate`` with the official keyword
+    arguments; ``model.talker.model`` is a runnable transformers Qwen3Model (fp32) holding the synthetic weights;
+    ``model.speech_tokenizer`` decodes codes with a small causal decoder (``decode`` and ``model.decoder``,
+    ``total_upsample``, ``decode_upsample_rate``, ``get_output_sample_rate``). Greedy settings by default."""
+    s = workload_shape(name)
+    tts = make_tts(seed, s, device=device)
+    talker = tts.model.talker
+    talker.model = hf_talker_model(seed, s, device)
+    talker.dtype = torch.float32
+
+    def talker_generate(**kw):  # the official generation; the engine intercepts this call and never runs it
+        raise RuntimeError("the stand-in talker cannot generate")
+
+    talker.generate = talker_generate
+    pad = torch.from_numpy(bf16_values(normal(seed, 0, "prompt", (1, 1, s.hidden), 0.02))).to(device)
+
+    def generate_custom_voice(text: str, speaker: str, language: str, do_sample: bool = False, top_k: int = 50,
+                              top_p: float = 1.0, temperature: float = 0.9, repetition_penalty: float = 1.0,
+                              min_new_tokens: int = 0, max_new_tokens: int = 2048, subtalker_dosample: bool = False,
+                              subtalker_top_k: int = 50, subtalker_top_p: float = 1.0,
+                              subtalker_temperature: float = 0.9):
+        L = 6 + len(text)
+        h = int.from_bytes(hashlib.sha256(f"{speaker}|{language}|{text}".encode()).digest()[:4], "little")
+        rows = bf16_values(np.random.default_rng(h).standard_normal((1, L, s.hidden)) * 0.02)
+        emb = torch.from_numpy(rows.astype(np.float32)).to(device)
+        return talker.generate(inputs_embeds=emb, attention_mask=torch.ones((1, L), dtype=torch.long, device=device),
+                               trailing_text_hidden=pad.clone(), tts_pad_embed=pad.clone(), do_sample=do_sample,
+                               top_k=top_k, top_p=top_p, temperature=temperature,
+                               repetition_penalty=repetition_penalty, min_new_tokens=min_new_tokens,
+                               max_new_tokens=max_new_tokens, subtalker_dosample=subtalker_dosample,
+                               subtalker_top_k=subtalker_top_k, subtalker_top_p=subtalker_top_p,
+                               subtalker_temperature=subtalker_temperature)
+
+    groups = int(tts.model.config.talker_config.num_code_groups)
+    decoder = _ToyCodecDecoder(seed, groups, s.vocab, up).to(device)
+
+    def tok_decode(items):
+        wavs = []
+        with torch.inference_mode():
+            for it in items:
+                c = torch.clamp(torch.as_tensor(it["audio_codes"]), min=0).t().unsqueeze(0).to(device)
+                wavs.append(decoder(c).reshape(-1).float().cpu().numpy())
+        return wavs, 24000
+
+    tok_model = SimpleNamespace(decoder=decoder, decode_upsample_rate=up, get_output_sample_rate=lambda: 24000)
+    tts.model.speech_tokenizer = SimpleNamespace(model=tok_model, decode=tok_decode)
+    tts.generate_custom_voice = generate_custom_voice
+    tts.get_supported_speakers = lambda: ["vivian"]
+    return tts
