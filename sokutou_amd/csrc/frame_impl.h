@@ -344,6 +344,79 @@ __device__ __forceinline__ void dot_rows(const uint4 (&w)[RW][C], const float* x
   for (int r = 0; r < RW; r++) y[r] = wave_sum(acc[r]);
 }
 
+// i8g32 weights (the reference's format: one fp16 scale per 32 weights of a row, applied per 16-weight chunk,
+// qwen3/kernels.py:104-110): a lane's chunk c of a row covers weights 16 (lane + 64 c) .. + 15, inside group
+// (lane + 64 c) / 2, whose scale comes with the chunk (raw fp16 bits until the dot).
+template <int RW, int C>
+__device__ __forceinline__ void load_rows_g32(uint4 (&w)[RW][C], uint16_t (&g)[RW][C], const int8_t* W, const uint16_t* S,
+                                              int row0, int nvalid, int K, int lane) {
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const int row = r < nvalid ? row0 + r : row0;
+    const uint4* p = (const uint4*)(W + (size_t)row * K);
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      w[r][c] = ld_stream(p + lane + 64 * c);
+      g[r][c] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)),
+                                                     ((uint32_t)row * (uint32_t)(K >> 5) + (uint32_t)((lane + 64 * c) >> 1)) * 2u,
+                                                     0, 0);
+    }
+  }
+}
+// y[r] = sum over the lane's chunks of (group scale) * (chunk . xs), reduced over the wave; xs swizzled (xsw)
+template <int RW, int C>
+__device__ __forceinline__ void dot_rows_g32(const uint4 (&w)[RW][C], const uint16_t (&g)[RW][C], const float* xs,
+                                             int lane, float (&y)[RW]) {
+  float acc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; r++) acc[r] = 0.f;
+  const float2* xs2 = (const float2*)xs;
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+    float part[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) part[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float2 u0 = xs2[2 * ((4 * c + j) * 64 + lane)], u1 = xs2[2 * ((4 * c + j) * 64 + lane) + 1];
+      const float4 v = make_float4(u0.x, u0.y, u1.x, u1.y);
+#pragma unroll
+      for (int r = 0; r < RW; r++) {
+        const uint32_t q = j == 0 ? w[r][c].x : j == 1 ? w[r][c].y : j == 2 ? w[r][c].z : w[r][c].w;
+        float t = (float)(int8_t)q * v.x;
+        t = __builtin_fmaf((float)(int8_t)(q >> 8), v.y, t);
+        t = __builtin_fmaf((float)(int8_t)(q >> 16), v.z, t);
+        t = __builtin_fmaf((float)(int8_t)(q >> 24), v.w, t);
+        part[r] += t;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RW; r++) acc[r] = __builtin_fmaf(h2f(g[r][c]), part[r], acc[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; r++) y[r] = wave_sum(acc[r]);
+}
+// Weight-format dispatch of the compute waves: i8row keeps one bf16 scale per row (applied by the caller through
+// row_scale), i8g32 one fp16 scale per chunk (applied inside the dot; row_scale is then 1). The group-scale arrays
+// of the i8row kernels are [1][1] and unused.
+template <int WD, int RW, int C, int GR, int GC>
+__device__ __forceinline__ void load_w(uint4 (&w)[RW][C], uint16_t (&s)[RW], uint16_t (&g)[GR][GC], const int8_t* W,
+                                       const uint16_t* S, int row0, int nvalid, int K, int lane) {
+  if constexpr (WD == SK_WD_I8G32) load_rows_g32<RW, C>(w, g, W, S, row0, nvalid, K, lane);
+  else load_rows<RW, C>(w, s, W, S, row0, nvalid, K, lane);
+}
+template <int WD, int RW, int C, int GR, int GC>
+__device__ __forceinline__ void dot_w(const uint4 (&w)[RW][C], const uint16_t (&g)[GR][GC], const float* xs, int lane,
+                                      float (&y)[RW]) {
+  if constexpr (WD == SK_WD_I8G32) dot_rows_g32<RW, C>(w, g, xs, lane, y);
+  else dot_rows<RW, C>(w, xs, lane, y);
+}
+template <int WD>
+__device__ __forceinline__ float row_scale_of(uint16_t s) {
+  if constexpr (WD == SK_WD_I8G32) return 1.f;
+  else return bf2f(s);
+}
+
 // Publishes a stage's outputs. Every compute wave has left its values in S.pub (lane 0, before the call); the last
 // wave to arrive writes the workgroup's n cells [idx0, idx0 + n) (idx0 and n even) with 16-byte stores, so each
 // line of cells is written by one wave at one time (lines written piecewise by several waves reach the pollers
@@ -1127,7 +1200,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 // ================================================================================================================
 // Compute waves
 // ================================================================================================================
-template <int H, int I, int W, int V, bool CP, bool SMP>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD>
 __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
   using C = Cfg<H, I, W, V, CP>;
   const Layout LY(H, I);
@@ -1150,6 +1223,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
 
   uint4 wq[C::RW_QKV][C::CH], wo[C::RW_O][C::CQ], wg[C::RW_GU][C::CH], wd[C::RW_D][C::CI];
   uint16_t sq[C::RW_QKV], so[C::RW_O], sg[C::RW_GU], sd[C::RW_D];  // raw bf16 row scales
+  constexpr bool G32 = WD == SK_WD_I8G32;  // i8g32: raw fp16 group scales, one per row and chunk
+  uint16_t gq[G32 ? C::RW_QKV : 1][G32 ? C::CH : 1], go[G32 ? C::RW_O : 1][G32 ? C::CQ : 1];
+  uint16_t gg[G32 ? C::RW_GU : 1][G32 ? C::CH : 1], gd[G32 ? C::RW_D : 1][G32 ? C::CI : 1];
   uint4 kr[C::KVL], vr[C::KVL];
   // RoPE row (cos, sin of pair `lane`) and the norm weights of dims lane, lane + 64 for this wave's vector in
   // the next attention (q norm for waves 0, 1, k norm for wave 2; loaded by every compute wave: no select on
@@ -1164,13 +1240,13 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   };
   {
     const sk_layer_desc& L0 = S.desc[0];
-    load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
+    load_w<WD, C::RW_QKV, C::CH>(wq, sq, gq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
     load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), make_chunk<CP>(c.pos0, r, C::whole(c.pos0)), cw, ag, asl);
     load_attn_vec(L0, c.pos0);
     if constexpr (!C::kLate) {
-      load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
-      load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
-      load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
+      load_w<WD, C::RW_O, C::CQ>(wo, so, go, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
+      load_w<WD, C::RW_GU, C::CH>(wg, sg, gg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
+      load_w<WD, C::RW_D, C::CI>(wd, sd, gd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
     }
   }
   const bool block_eos0 = c.d.talker_processor && c.d.ngen;
@@ -1195,16 +1271,16 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
       if (tid == 0) c.tr(1, f, l, 0);
       {
         float y[C::RW_QKV];
-        dot_rows<C::RW_QKV, C::CH>(wq, S.xs[0], lane, y);
+        dot_w<WD, C::RW_QKV, C::CH>(wq, gq, S.xs[0], lane, y);
         if (tid == 0) c.tr(1, f, l, 8);
         const float inv = S.inv;
         if (lane == 0) {
 #pragma unroll
-          for (int i = 0; i < C::RW_QKV; i++) S.pub[C::RW_QKV * cw + i] = y[i] * bf2f(sq[i]) * inv;
+          for (int i = 0; i < C::RW_QKV; i++) S.pub[C::RW_QKV * cw + i] = y[i] * row_scale_of<WD>(sq[i]) * inv;
         }
         publish<W>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, 16, c.tick(f, l, 0), lane);
         if (tid == 0) c.tr(1, f, l, 1);
-        if constexpr (!C::kLate) load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+        if constexpr (!C::kLate) load_w<WD, C::RW_QKV, C::CH>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
       }
       // ---- S2: attention over this workgroup's chunk ----------------------------------------------------
       wg_sync();
@@ -1323,9 +1399,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           load_attn_vec(Ln, npos);
         }
         if constexpr (C::kLate) {
-          load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
+          load_w<WD, C::RW_O, C::CQ>(wo, so, go, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
           if constexpr (!C::kSpread)
-            load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+            load_w<WD, C::RW_GU, C::CH>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
         }
       }
       // ---- S4: o projection rows, added to the layer's input residual ------------------------------------
@@ -1335,19 +1411,19 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
       {
         float y[C::RW_O];
         if (tid == 0) c.tr_clk(1, f, l, 14);
-        dot_rows<C::RW_O, C::CQ>(wo, S.xs[1], lane, y);
+        dot_w<WD, C::RW_O, C::CQ>(wo, go, S.xs[1], lane, y);
         if (tid == 0) c.tr(1, f, l, 9);
         if (tid == 0) c.tr_clk(1, f, l, 15);
         if (lane == 0) {
 #pragma unroll
           for (int i = 0; i < C::RW_O; i++)
-            if (i < o_wn) S.pub[C::RW_O * cw + i] = S.hin[o_w0 + i] + y[i] * bf2f(so[i]);
+            if (i < o_wn) S.pub[C::RW_O * cw + i] = S.hin[o_w0 + i] + y[i] * row_scale_of<WD>(so[i]);
         }
         publish<W>(S, c.cells, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
         if (tid == 0) c.tr(1, f, l, 5);
-        if constexpr (!C::kLate) load_rows<C::RW_O, C::CQ>(wo, so, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
+        if constexpr (!C::kLate) load_w<WD, C::RW_O, C::CQ>(wo, so, go, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
         if constexpr (C::kSpread)
-          load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+          load_w<WD, C::RW_GU, C::CH>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
       }
       // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
       wg_sync();
@@ -1355,22 +1431,22 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
       if (tid == 0) c.tr(1, f, l, 12);
       {
         float y[C::RW_GU];
-        dot_rows<C::RW_GU, C::CH>(wg, S.xs[0], lane, y);
+        dot_w<WD, C::RW_GU, C::CH>(wg, gg, S.xs[0], lane, y);
         if (tid == 0) c.tr(1, f, l, 10);
         const float inv = S.inv;
         if (lane == 0) {
 #pragma unroll
           for (int i = 0; i < C::RW_GU; i += 2)
-            S.pub[(C::RW_GU * cw + i) / 2] = silu_mul(y[i] * bf2f(sg[i]) * inv, y[i + 1] * bf2f(sg[i + 1]) * inv);
+            S.pub[(C::RW_GU * cw + i) / 2] = silu_mul(y[i] * row_scale_of<WD>(sg[i]) * inv, y[i + 1] * row_scale_of<WD>(sg[i + 1]) * inv);
         }
         publish<W>(S, c.cells, LY.e5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
         if (tid == 0) c.tr(1, f, l, 6);
         if constexpr (C::kLate) {
-          load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
+          load_w<WD, C::RW_D, C::CI>(wd, sd, gd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
           if constexpr (!C::kSpread)
-            load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+            load_w<WD, C::RW_QKV, C::CH>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
         } else {
-          load_rows<C::RW_GU, C::CH>(wg, sg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
+          load_w<WD, C::RW_GU, C::CH>(wg, sg, gg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
         }
       }
       // ---- S6: down rows, added to the residual after o --------------------------------------------------
@@ -1379,13 +1455,13 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
       if (tid == 0) c.tr(1, f, l, 13);
       {
         float y[C::RW_D];
-        dot_rows<C::RW_D, C::CI>(wd, S.xs[1], lane, y);
+        dot_w<WD, C::RW_D, C::CI>(wd, gd, S.xs[1], lane, y);
         if (tid == 0) c.tr(1, f, l, 11);
         if (lane == 0) {
 #pragma unroll
           for (int i = 0; i < C::RW_D; i++) {
             if (i < d_wn) {
-              const float hv = S.hmid[d_w0 + i] + y[i] * bf2f(sd[i]);
+              const float hv = S.hmid[d_w0 + i] + y[i] * row_scale_of<WD>(sd[i]);
               S.pub[C::RW_D * cw + i] = hv;
               if (c.d.layer_out && f == c.n_frames - 1) gstore(c.d.layer_out + (size_t)l * H + d_w0 + i, hv);
             }
@@ -1393,9 +1469,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         }
         publish<W>(S, c.cells, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
         if (tid == 0) c.tr(1, f, l, 7);
-        if constexpr (!C::kLate) load_rows<C::RW_D, C::CI>(wd, sd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
+        if constexpr (!C::kLate) load_w<WD, C::RW_D, C::CI>(wd, sd, gd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
         if constexpr (C::kSpread) {
-          load_rows<C::RW_QKV, C::CH>(wq, sq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+          load_w<WD, C::RW_QKV, C::CH>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
           load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
           load_attn_vec(Ln, npos);
         }
@@ -1408,14 +1484,15 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
     // ---- head rows (loaded now; the final residual is a full layer away), processor, local argmax ----------
     uint4 wh[C::RW_HEAD][C::CH];
     uint16_t sh[C::RW_HEAD];
+    uint16_t gh[G32 ? C::RW_HEAD : 1][G32 ? C::CH : 1];
     const int8_t* hw = CP ? (const int8_t*)uniform(gload(c.cp.head_w + f)) : (const int8_t*)c.d.head_w;
     const uint16_t* hsc = CP ? (const uint16_t*)uniform(gload(c.cp.head_s + f)) : c.d.head_s;
-    load_rows<C::RW_HEAD, C::CH>(wh, sh, hw, hsc, h_w0, h_wn, H, lane);
+    load_w<WD, C::RW_HEAD, C::CH>(wh, sh, gh, hw, hsc, h_w0, h_wn, H, lane);
     wg_sync();
     if (S.flags[5]) return;
     {
       float y[C::RW_HEAD];
-      dot_rows<C::RW_HEAD, C::CH>(wh, S.xs[0], lane, y);
+      dot_w<WD, C::RW_HEAD, C::CH>(wh, gh, S.xs[0], lane, y);
       const float inv = S.inv;
       const bool block_eos = block_eos0 && (ngen0 + f) < c.d.min_new;
       uint64_t best = 0;
@@ -1424,7 +1501,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         for (int i = 0; i < C::RW_HEAD; i++) {
           if (i >= h_wn) break;
           const int row = h_w0 + i;
-          float v = y[i] * bf2f(sh[i]) * inv;
+          float v = y[i] * row_scale_of<WD>(sh[i]) * inv;
           if (c.d.logits && f == c.n_frames - 1) gstore(c.d.logits + row, v);
           if (c.d.talker_processor) {
             if (c.d.seen && ((ld_u32_dev(uniform(c.d.seen), (uint32_t)row & ~3u) >> (8 * (row & 3))) & 0xffu))
@@ -1449,7 +1526,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
 
 // SMP: sampled picks (do_sample != 0). The greedy instantiation carries none of the sampling code, whose call and
 // registers would otherwise weigh on the control loop of every greedy frame.
-template <int H, int I, int W, int V, bool CP, bool SMP>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD>
 __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArgs cp, int n_frames) {
   extern __shared__ char smem_raw[];
   Lds<H, I, W, V, CP>& S = *(Lds<H, I, W, V, CP>*)smem_raw;
@@ -1527,7 +1604,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   }
   c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
   if (wave == W) run_control<H, I, W, V, CP, SMP>(c, S, lane);
-  else run_compute<H, I, W, V, CP, SMP>(c, S, wave, tid, lane);
+  else run_compute<H, I, W, V, CP, SMP, WD>(c, S, wave, tid, lane);
   // ---- end of launch: epoch base and launch count (workgroup 0; every workgroup finished its census) --------
   if (c.g == 0 && tid == 0) {
     st_u32_dev(ws, Ws::kTick, c.base + (uint32_t)n_frames * c.tpf);
@@ -1539,14 +1616,14 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
 // cannot hold a workgroup, would only surface as poll timeouts). Done once per device and instantiation; a failure
 // is reported every time and retried on the next call.
 constexpr int kMaxDevices = 64;
-template <int H, int I, int W, int V, bool CP, bool SMP>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD>
 int prepare_kernel(size_t lds) {
   static bool ready[kMaxDevices] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return sk_set_error(SK_EDEVICE, "sk_talker_frames: no current HIP device");
   if (ready[dev]) return SK_OK;
-  const void* fn = (const void*)k_frames<H, I, W, V, CP, SMP>;
+  const void* fn = (const void*)k_frames<H, I, W, V, CP, SMP, WD>;
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return sk_check_launch(e, "sk_talker_frames: raising the LDS limit");
   int cus = 0, per_cu = 0;
@@ -1561,19 +1638,19 @@ int prepare_kernel(size_t lds) {
   ready[dev] = true;
   return SK_OK;
 }
-template <int H, int I, int W, int V, bool CP, bool SMP>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD>
 int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
   const size_t lds = sizeof(Lds<H, I, W, V, CP>) < 96 * 1024 ? 96 * 1024 : sizeof(Lds<H, I, W, V, CP>);  // one workgroup per CU
-  const int rc = prepare_kernel<H, I, W, V, CP, SMP>(lds);
+  const int rc = prepare_kernel<H, I, W, V, CP, SMP, WD>(lds);
   if (rc != SK_OK) return rc;
-  hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp, n_frames);
+  hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP, WD>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp, n_frames);
   return sk_check_launch(hipGetLastError(), "sk_talker_frames");
 }
-template <int H, int I, int W, int V, bool CP>
+template <int H, int I, int W, int V, bool CP, int WD = SK_WD_I8ROW>
 int launch_frames(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
   if (d->max_len > Cfg<H, I, W, V, CP>::kMaxLen) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: max_len too long");
-  return d->do_sample ? launch_kernel<H, I, W, V, CP, true>(d, cp, n_frames, st)
-                      : launch_kernel<H, I, W, V, CP, false>(d, cp, n_frames, st);
+  return d->do_sample ? launch_kernel<H, I, W, V, CP, true, WD>(d, cp, n_frames, st)
+                      : launch_kernel<H, I, W, V, CP, false, WD>(d, cp, n_frames, st);
 }
 
 }  // namespace

@@ -367,7 +367,8 @@ class Qwen3Kernels(Qwen3Fast):
         supported = (self.frame_kernel_supported() and sampler == "fused"
                      and (self.cp is None or self.cpk is not None))
         if frame_kernel and not supported:
-            raise ValueError("frame_kernel=True needs the fused sampler, i8row weights, 16 q / 8 kv heads, vocab 3072, "
+            raise ValueError("frame_kernel=True needs the fused sampler, i8row weights (or i8g32 at hidden 1024), "
+                             "16 q / 8 kv heads, vocab 3072, "
                              "hidden 1024 or 2048, a cache of at most 1024 (0.6B) / 2048 (1.7B) positions and, with a "
                              "code predictor, its one-launch kernel (no projection)")
         self.frame_kernel = supported if frame_kernel is None else bool(frame_kernel)
@@ -462,9 +463,12 @@ class Qwen3Kernels(Qwen3Fast):
 
     # --- the persistent frame kernel ------------------------------------------------------------------------
     def frame_kernel_supported(self) -> bool:
+        """The persistent kernel covers the 0.6B and 1.7B talker shapes with i8row weights, and the 0.6B shape with
+        the reference's i8g32 weights too."""
         P = self.T
         shapes = {(1024, 3072): 1024, (2048, 6144): 2048}
-        return (self.wd == "i8row" and self.ct == "bf16" and P.nq == 16 and P.nkv == 8 and self.V == 3072
+        wd_ok = self.wd == "i8row" or (self.wd == "i8g32" and (P.H, P.I) == (1024, 3072))
+        return (wd_ok and self.ct == "bf16" and P.nq == 16 and P.nkv == 8 and self.V == 3072
                 and (P.H, P.I) in shapes and self.max_cache <= shapes[(P.H, P.I)])
 
     def _setup_frame_kernel(self) -> None:

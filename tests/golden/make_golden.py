@@ -105,13 +105,14 @@ def talker(name: str, seed: int, wd: str = "i8row") -> None:
         codes.append(token_next)
         token = token_next
     t2 = time.time()
-    np.savez_compressed(HERE / f"{name}_seed{seed}.npz", layer_out0=np.stack(layer_out), logits_first=logits[0],
+    stem = f"{name}_seed{seed}" if wd == "i8row" else f"{name}_{wd}_seed{seed}"
+    np.savez_compressed(HERE / f"{stem}.npz", layer_out0=np.stack(layer_out), logits_first=logits[0],
                         logits_last=logits[-1])
     meta = {"workload": name, "seed": seed, "wd": wd, "start_token": tok, "start_pos": pos0, "frames": frames,
             "codes": codes, "margins": margins, "digests": dig,
             "oracle_seconds": {"build": round(t1 - t0, 1), "frames": round(t2 - t1, 1)}}
-    (HERE / f"{name}_seed{seed}.json").write_text(json.dumps(meta, indent=1))
-    print(name, "codes", codes[:12], "... min margin", min(margins), meta["oracle_seconds"])
+    (HERE / f"{stem}.json").write_text(json.dumps(meta, indent=1))
+    print(stem, "codes", codes[:12], "... min margin", min(margins), meta["oracle_seconds"])
 
 
 def code_predictor(name: str = "cp06b", seed: int = 0) -> None:
@@ -184,6 +185,7 @@ if __name__ == "__main__":
     ap.add_argument("--only", default=None)
     a = ap.parse_args()
     jobs = {"layer06b": lambda: layer06b(0), "tiny": lambda: talker("tiny", 1), "talker06b": lambda: talker("talker06b", 0),
+            "talker06b_i8g32": lambda: talker("talker06b", 0, "i8g32"),
             "talker17b": lambda: talker("talker17b", 0), "cp06b": lambda: code_predictor("cp06b", 0),
             "batch17b": lambda: batch("batch17b", 0)}
     for n, fn in jobs.items():

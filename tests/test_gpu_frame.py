@@ -86,6 +86,32 @@ def test_talker06b_64_frames_one_launch(gpu):
     assert int(eng.pos.item()) == meta["start_pos"] + 64
 
 
+def test_talker06b_i8g32_64_frames_one_launch(gpu):
+    """The reference's i8g32 weights (fp16 scale per 32 weights, applied per 16-weight chunk) on the persistent
+    kernel: per-layer residuals and logits of frame 0, then 63 frames in one launch, against the i8g32 oracle."""
+    print("talker06b i8g32: frame 0 with residuals, then 63 frames in one launch", flush=True)
+    meta = json.loads((GOLD / "talker06b_i8g32_seed0.json").read_text())
+    gold = np.load(GOLD / "talker06b_i8g32_seed0.npz")
+    eng, tok = syn.make_engine("talker06b", seed=0, wd="i8g32", device=gpu, frame_kernel=True)
+    assert eng.frame_kernel and tok == meta["start_token"]
+    eng.layer_out = torch.zeros((28, 1024), device=gpu)
+    eng.run_frames(1)
+    torch.cuda.synchronize()
+    assert eng.frame_error() == 0, eng.frame_diag()
+    errs = [rel_err(eng.layer_out[i], gold["layer_out0"][i]) for i in range(28)]
+    print(f"per-layer max rel err {max(errs):.3e}", flush=True)
+    assert max(errs) < TOL
+    assert rel_err(eng.logit_t.view(-1), gold["logits_first"]) < TOL
+    assert int(eng.frame_ids[0]) == meta["codes"][0]
+    eng.layer_out = None
+    eng.run_frames(63)
+    torch.cuda.synchronize()
+    assert eng.frame_error() == 0, eng.frame_diag()
+    codes = [meta["codes"][0]] + eng.frame_ids[:63].cpu().tolist()
+    assert codes == meta["codes"]
+    assert rel_err(eng.logit_t.view(-1), gold["logits_last"]) < TOL
+
+
 def test_talker06b_graph_replay_one_frame_per_launch(gpu):
     print("talker06b: captured single-frame launch replayed 64 times", flush=True)
     meta = json.loads((GOLD / "talker06b_seed0.json").read_text())
