@@ -1,8 +1,8 @@
 // Entry points of the persistent kernel in talker mode (sk_talker_workspace_size, sk_talker_frames) and the 0.6B
 // talker's instantiations; the kernel itself is in frame_impl.h. The 1.7B talker runs the instantiations of
-// frame17.hip (polls staged through LDS); its instantiations here, with the register polls, are the comparison
-// point (SOKUTOU_TALKER_POLL=regs). They also keep this module as the 0.6B kernels were tuned in: their register
-// allocation changes with what else the module holds, and measured 2.5% slower without them.
+// frame17.hip (4 compute waves, register polls); its instantiations here, with 8 compute waves and register polls,
+// are a comparison point (SOKUTOU_TALKER_POLL=regs). They also keep this module as the 0.6B kernels were tuned in:
+// their register allocation changes with what else the module holds, and measured 2.5% slower without them.
 #include <cstdlib>
 #include <cstring>
 #include "frame_impl.h"

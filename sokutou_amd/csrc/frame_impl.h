@@ -65,6 +65,12 @@ __device__ __forceinline__ void put2(void* cells, uint32_t idx, float v0, float 
 __device__ __forceinline__ u32x4 get2(const void* cells, uint32_t idx) {  // cells idx, idx+1
   return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(cells), idx * 8u, 0, kPolDev);
 }
+// cells idx + 2 lane, + 1 with idx wave-uniform: the lane part goes in the one vector offset every such load shares
+// (16 lane bytes), the uniform part in the scalar offset, so a poll of many loads holds one address register.
+__device__ __forceinline__ u32x4 get2l(const void* cells, uint32_t idx, int lane) {
+  return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(cells), (uint32_t)lane * 16u,
+                                               __builtin_amdgcn_readfirstlane(idx * 8u), kPolDev);
+}
 __device__ __forceinline__ uint32_t ld_u32_dev(const void* base, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(base), off, 0, kPolDev);
 }
@@ -134,6 +140,14 @@ template <int H, int I>
 struct SpreadLate {
   static constexpr bool value = false;
 };
+// Poll addressing of a shape's control wave: true = get2l (one shared lane-offset register per poll), false = a
+// vector offset per load. The hidden-2048 kernel (frame17.hip) takes get2l: with 4 compute waves its control wave
+// otherwise spills the offsets of its 16-load polls. The hidden-1024 kernels keep per-load offsets, the code they
+// were tuned with (measured 4% slower with get2l).
+template <int H>
+struct LaneOffsetPolls {
+  static constexpr bool value = false;
+};
 
 template <int H, int I, int W, int V, bool CP>
 struct Cfg {
@@ -143,15 +157,15 @@ struct Cfg {
   static constexpr int kHeadRows = V / kWG;                   // head rows per workgroup: 12 (talker), 8 (code predictor)
   static constexpr int RW_HEAD = (kHeadRows + W - 1) / W;
   static constexpr int CH = H / 1024, CQ = kQ / 1024, CI = I / 1024;  // 16-byte chunks per lane per row
-  static constexpr int KVL = 2;                                // K (and V) loads per lane
+  static constexpr int KVL = (W == 4 && H > 1024) ? 4 : 2;     // K (and V) loads per lane
   static constexpr int kMaxChunk = 4 * W * KVL;                // positions per attention workgroup: 32 / 64
   static constexpr int kMaxLen = kMaxChunk * kChunks;          // 1024 / 2048
-  // Prefetch distances. With 4 compute waves every stage's weights for the next layer are held in registers (a
-  // full layer ahead). With 8 compute waves the register budget is 168 per lane and a full layer of 1.7B weights
-  // (96 registers) does not fit beside the rest; each stage's weights are then loaded one to three exchanges
-  // before their use (kLate): o and gate/up after the attention of their layer, down and the next layer's qkv
-  // after gate/up. kSpread (SpreadLate) moves them later still, one exchange before their use.
-  static constexpr bool kLate = W == 8;
+  // Prefetch distances. At hidden 1024 with 4 compute waves every stage's weights for the next layer are held in
+  // registers (a full layer ahead). A full layer of 1.7B weights does not fit beside the rest (192 registers per
+  // wave with 4 compute waves; 96 of a 168-register budget with 8); each stage's weights are then loaded one to
+  // three exchanges before their use (kLate): o and gate/up after the attention of their layer, down and the next
+  // layer's qkv after gate/up. kSpread (SpreadLate) moves them later still, one exchange before their use.
+  static constexpr bool kLate = W == 8 || H > 1024;
   static constexpr bool kSpread = kLate && SpreadLate<H, I>::value;
   // code-predictor caches short enough for one workgroup to attend over all of them (see Chunk::whole)
   static __device__ bool whole(int pos) { return CP && pos + 1 <= kMaxChunk; }
@@ -198,14 +212,14 @@ __device__ __forceinline__ int xsw(int i) {
 
 // Loads per lane in one polling round: at most 16 (64 registers of the control wave).
 constexpr int mb(int n) { return n / 128 < 16 ? n / 128 : 16; }
-// The hidden-1024 shapes poll a vector of up to 3072 cells in one round (24 loads, 96 registers): a second round
-// trip costs about 0.5 us per exchange.
-constexpr int mbh(int n, int H) { return H <= 1024 ? (n / 128 < 24 ? n / 128 : 24) : mb(n); }
+// With 4 compute waves (256 registers for the control wave) a round holds up to 24 loads (96 registers): the 3072-cell
+// activation of the hidden-1024 shape in one round (a second round trip costs about 0.5 us per exchange).
+constexpr int mbh(int n, int W) { return W == 4 ? (n / 128 < 24 ? n / 128 : 24) : mb(n); }
 
 // ---- control wave: poll cells into LDS ---------------------------------------------------------------------
 // Waits until cells [idx0, idx0 + n) (n even, idx0 even) all carry epoch e, copying the values to dst.
 // Returns false on timeout or when the global error word is set.
-template <int MAXB, bool SW = false>
+template <int MAXB, bool SW = false, bool LO = false>
 __device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, float* dst, void* ws, int lane,
                            const Ctx& c, uint32_t code, int f, int l) {
   for (uint32_t spin = 0;; spin++) {
@@ -214,8 +228,12 @@ __device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, 
       u32x4 q[MAXB];
 #pragma unroll
       for (int b = 0; b < MAXB; b++) {
-        const int i = base + 128 * b + 2 * lane;
-        if (i < n) q[b] = get2(cells, idx0 + i);
+        if constexpr (LO) {  // n is a multiple of 128: the condition is wave-uniform
+          if (base + 128 * b < n) q[b] = get2l(cells, idx0 + (uint32_t)(base + 128 * b), lane);
+        } else {
+          const int i = base + 128 * b + 2 * lane;
+          if (i < n) q[b] = get2(cells, idx0 + i);
+        }
       }
 #pragma unroll
       for (int b = 0; b < MAXB; b++) {
@@ -245,12 +263,13 @@ __device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, 
 // in q[b].x and q[b].z; nothing goes through LDS here, the caller uses the values from registers (reading them
 // back from LDS would cost one LDS round trip per dependent read). Returns false on timeout or when the global
 // error word is set.
-template <int NB>
+template <int NB, bool LO = false>
 __device__ bool poll_regs(const void* cells, uint32_t idx0, uint32_t e, u32x4 (&q)[NB], void* ws, int lane,
                           const Ctx& c, uint32_t code, int f, int l) {
   for (uint32_t spin = 0;; spin++) {
 #pragma unroll
-    for (int b = 0; b < NB; b++) q[b] = get2(cells, idx0 + (uint32_t)(2 * lane + 128 * b));
+    for (int b = 0; b < NB; b++)
+      q[b] = LO ? get2l(cells, idx0 + (uint32_t)(128 * b), lane) : get2(cells, idx0 + (uint32_t)(2 * lane + 128 * b));
     bool ok = true;
 #pragma unroll
     for (int b = 0; b < NB; b++) ok &= q[b].y == e && q[b].w == e;
@@ -822,10 +841,11 @@ __device__ __forceinline__ int attn_barriers(const Ck& ck) { return 1 + (ck.n > 
 // ================================================================================================================
 template <int H, int I, int W, int V, bool CP, bool SMP>
 __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
-  // hidden 1024: the RMSNorm inputs are polled into registers and staged from there (kNP element pairs per lane);
-  // the hidden-2048 kernels keep their LDS-staged polls
-  constexpr bool kRegRms = H <= 1024;
+  // 4 compute waves (256 registers for the control wave): the RMSNorm inputs are polled into registers and staged
+  // from there (kNP element pairs per lane); with 8 compute waves (168 registers) they are staged through LDS
+  constexpr bool kRegRms = W == 4;
   constexpr int kNP = H / 128;
+  constexpr bool kLO = LaneOffsetPolls<H>::value;
   const Layout LY(H, I);
   const float eps = c.d.eps;
   const bf16_t* emb = (const bf16_t*)c.d.emb;
@@ -878,7 +898,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         } else {
           after_publish(S, (uint32_t)(f * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
           u32x4 q[kNP];
-          ok = poll_regs<kNP>(c.cells, LY.e6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
+          ok = poll_regs<kNP, kLO>(c.cells, LY.e6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
           cells_to_pairs<kNP>(q, v);
         }
         ss = stage_rms<kNP>(v, w, S.hin, S.xs[0], lane);
@@ -916,7 +936,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         for (int k = 0; k < H / 64; k++) S.hin[lane + 64 * k] = ev[k];
       } else {
         after_publish(S, (uint32_t)(f * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
-        ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
+        ok = poll_cells<mb(H), false, kLO>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
       }
       for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
       ss = wave_sum(ss);
@@ -928,7 +948,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if (!ok) return;
       // S2 input: this head's q/k/v
       after_publish(S, (uint32_t)(f * c.L + l) * 4u + 1u, c.dl[Ws::kHopS2]);
-      ok = poll_cells<mb(512)>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
+      ok = poll_cells<mb(512), false, kLO>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
       if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
       if (!ok) return;
@@ -1044,7 +1064,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         if (lane == 0) c.tr(0, f, l, 4);
       }
       // S4 input: the whole attention output
-      ok = ok && poll_cells<mb(kQ), true>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
+      ok = ok && poll_cells<mb(kQ), true, kLO>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
       if (lane == 0) { S.flags[2] = !ok; c.tr(0, f, l, 5); }
       wg_sync();
       if (!ok) return;
@@ -1054,7 +1074,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         load_pairs<kNP>(Ly.post_norm, w, lane);
         after_publish(S, (uint32_t)(f * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
         u32x4 q[kNP];
-        ok = poll_regs<kNP>(c.cells, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
+        ok = poll_regs<kNP, kLO>(c.cells, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
         cells_to_pairs<kNP>(q, v);
         ss = stage_rms<kNP>(v, w, S.hmid, S.xs[0], lane);
       } else {
@@ -1062,7 +1082,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 #pragma unroll
       for (int k = 0; k < H / 64; k++) npost[k] = gload(Ly.post_norm + lane + 64 * k);
       after_publish(S, (uint32_t)(f * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
-      ok = poll_cells<mb(H)>(c.cells, LY.e4, H, c.tick(f, l, 3), S.hmid, c.ws, lane, c, 15u, f, l);
+      ok = poll_cells<mb(H), false, kLO>(c.cells, LY.e4, H, c.tick(f, l, 3), S.hmid, c.ws, lane, c, 15u, f, l);
       ss = 0.f;
       for (int i = lane; i < H; i += 64) { const float v = S.hmid[i]; ss += v * v; }
       ss = wave_sum(ss);
@@ -1074,7 +1094,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if (!ok) return;
       // S6 input: the whole SwiGLU activation
       after_publish(S, (uint32_t)(f * c.L + l) * 4u + 3u, c.dl[Ws::kHopS6]);
-      ok = poll_cells<mbh(I, H), true>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+      ok = poll_cells<mbh(I, W), true, kLO>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
       if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
       wg_sync();
       if (!ok) return;
@@ -1088,7 +1108,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       load_pairs<kNP>(c.d.norm, w, lane);
       after_publish(S, (uint32_t)((f + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
       u32x4 q[kNP];
-      ok = poll_regs<kNP>(c.cells, LY.e6, c.tick(f, c.L - 1, 5), q, c.ws, lane, c, 17u, f, c.L);
+      ok = poll_regs<kNP, kLO>(c.cells, LY.e6, c.tick(f, c.L - 1, 5), q, c.ws, lane, c, 17u, f, c.L);
       cells_to_pairs<kNP>(q, v);
       ss = stage_rms<kNP>(v, w, S.hin, S.xs[0], lane);
       if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[5] = !ok; }
@@ -1106,7 +1126,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 #pragma unroll
     for (int k = 0; k < H / 64; k++) nfin[k] = gload(c.d.norm + lane + 64 * k);
     after_publish(S, (uint32_t)((f + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
-    ok = poll_cells<mb(H)>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
+    ok = poll_cells<mb(H), false, kLO>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
     for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
     ss = wave_sum(ss);
 #pragma unroll

@@ -29,12 +29,12 @@ def _engine(name, seed, gpu):
 @pytest.mark.parametrize("name,poll", [("small06b", None), ("small17b", None), ("small17b", "regs")])
 def test_small_model_against_oracle(gpu, name, poll, monkeypatch):
     """Two 0.6B- or 1.7B-shaped layers: 8 frames in one launch against the oracle, then per-layer residuals. The
-    1.7B shape runs the LDS-staged polls, and with SOKUTOU_TALKER_POLL=regs the register polls."""
+    1.7B shape runs its default kernel (4 compute waves), and with SOKUTOU_TALKER_POLL=regs the 8-wave kernel."""
     from oracle.workload import talker_oracle
 
     if poll:
         monkeypatch.setenv("SOKUTOU_TALKER_POLL", poll)
-    print(f"{name}: persistent kernel ({poll or 'default'} polls), 8 frames in one launch", flush=True)
+    print(f"{name}: persistent kernel ({poll or 'default'} kernel), 8 frames in one launch", flush=True)
     spec = syn.WORKLOADS[name]
     eng, tok = _engine(name, 2, gpu)
     orc, otok, s = talker_oracle(name, 2, "i8row")
