@@ -2,11 +2,13 @@
 //
 // Four compute waves leave the control wave 256 registers, enough to poll every exchange straight into registers
 // (the 0.6B kernels' polls); a full layer of 1.7B weights does not fit in the compute waves' registers beside the
-// rest, so each stage's weights are loaded one exchange before their use (SpreadLate). The polls address their
-// cells through one shared lane-offset register (LaneOffsetPolls): with a vector offset per load the control wave
-// spilled them. Measured on the 64-frame 1.7B workload: 27.0 us per layer, against 38.8 us for 8 compute waves
-// with polls staged through LDS (the 168-register budget of 9 waves) and 69 us for 8 compute waves with register
-// polls (SOKUTOU_TALKER_POLL=regs, frame.hip).
+// rest, so each stage's weights are loaded one exchange before their use (SpreadLate; issuing o and gate/up
+// together after the attention measured 28.4 us per layer). Every cell, weight-row and cache access of this shape
+// keeps its lane part in one shared vector offset and its uniform part in the scalar offset (LaneOffsetPolls):
+// with a vector address per access the waves spilled ~140 addresses and reloaded them from scratch on every
+// exchange; with the shared offsets nothing spills. Measured on the 64-frame 1.7B workload: 25.3 us per layer,
+// against 38.8 us for 8 compute waves with polls staged through LDS (the 168-register budget of 9 waves) and 69 us
+// for 8 compute waves with register polls (SOKUTOU_TALKER_POLL=regs, frame.hip).
 #include "frame_impl.h"
 
 namespace {

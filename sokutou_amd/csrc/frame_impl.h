@@ -47,6 +47,7 @@ constexpr int kNQ = 16, kNKV = 8, kQKV = (kNQ + 2 * kNKV) * SK_HD, kQ = kNQ * SK
 constexpr int kTalkerV = 3072;             // talker codec vocabulary
 constexpr uint32_t kSpinLimit = 1u << 19;
 constexpr float kInvSqrtHd = 0.08838834764831845f;
+constexpr int kNT = 2;  // buffer cache policy bit nt (non-temporal): the streamed weights
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -70,6 +71,16 @@ __device__ __forceinline__ u32x4 get2(const void* cells, uint32_t idx) {  // cel
 __device__ __forceinline__ u32x4 get2l(const void* cells, uint32_t idx, int lane) {
   return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(cells), (uint32_t)lane * 16u,
                                                __builtin_amdgcn_readfirstlane(idx * 8u), kPolDev);
+}
+// The stores of the same addressing: cells idx + 2 lane, + 1 (put2l); cell idx + vbytes / 8 (putl, vbytes per lane)
+__device__ __forceinline__ void put2l(void* cells, uint32_t idx, int lane, float v0, float v1, uint32_t e) {
+  u32x4 x = {__float_as_uint(v0), e, __float_as_uint(v1), e};
+  __builtin_amdgcn_raw_buffer_store_b128(x, make_rsrc(cells), (uint32_t)lane * 16u,
+                                         __builtin_amdgcn_readfirstlane(idx * 8u), kPolDev);
+}
+__device__ __forceinline__ void putl(void* cells, uint32_t idx, uint32_t vbytes, float v, uint32_t e) {
+  u32x2 x = {__float_as_uint(v), e};
+  __builtin_amdgcn_raw_buffer_store_b64(x, make_rsrc(cells), vbytes, __builtin_amdgcn_readfirstlane(idx * 8u), kPolDev);
 }
 __device__ __forceinline__ uint32_t ld_u32_dev(const void* base, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(base), off, 0, kPolDev);
@@ -140,10 +151,12 @@ template <int H, int I>
 struct SpreadLate {
   static constexpr bool value = false;
 };
-// Poll addressing of a shape's control wave: true = get2l (one shared lane-offset register per poll), false = a
-// vector offset per load. The hidden-2048 kernel (frame17.hip) takes get2l: with 4 compute waves its control wave
-// otherwise spills the offsets of its 16-load polls. The hidden-1024 kernels keep per-load offsets, the code they
-// were tuned with (measured 4% slower with get2l).
+// Global addressing of a shape's kernel: true = the lane part of every cell, weight-row and cache address in one
+// shared vector offset (lane bytes) and the wave-uniform part in the scalar offset of buffer instructions
+// (get2l, put2l, putl, weight rows by row start); false = a vector address per load or store. The hidden-2048
+// kernel (frame17.hip) takes the shared offsets: with a vector address per load its waves spilled the addresses
+// (per-row weight pointers, poll and publish offsets) and reloaded them from scratch on every exchange. The
+// hidden-1024 kernels keep per-load addresses, the code they were tuned with (measured 4% slower with get2l polls).
 template <int H>
 struct LaneOffsetPolls {
   static constexpr bool value = false;
@@ -320,12 +333,21 @@ __device__ __forceinline__ void load_pairs(const float* p, float2 (&w)[NB], int 
 // The row scales come with the weights through vector loads (a scalar load would make every later LDS wait,
 // lgkmcnt, wait for it as well) and stay raw bf16 bits until the dot that uses them: converting on arrival would
 // make the wave wait for the load right after issuing it.
-template <int RW, int C>
+template <int RW, int C, bool LO = false>
 __device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], uint16_t (&s)[RW], const int8_t* W, const uint16_t* S,
                                           int row0, int nvalid, int K, int lane) {
 #pragma unroll
   for (int r = 0; r < RW; r++) {
     const int row = r < nvalid ? row0 + r : row0;
+    if constexpr (LO) {  // row start in the scalar offset, lane bytes (+ chunk) in the shared vector offset
+      const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)row * (uint32_t)K);
+#pragma unroll
+      for (int c = 0; c < C; c++)
+        w[r][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(W)),
+                                                                                  (uint32_t)lane * 16u + 1024u * c, so, kNT));
+      s[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), 0, __builtin_amdgcn_readfirstlane((uint32_t)row * 2u), 0);
+      continue;
+    }
     const uint4* p = (const uint4*)(W + (size_t)row * K);
 #pragma unroll
     for (int c = 0; c < C; c++) w[r][c] = ld_stream(p + lane + 64 * c);
@@ -418,11 +440,11 @@ __device__ __forceinline__ void dot_rows_g32(const uint4 (&w)[RW][C], const uint
 // Weight-format dispatch of the compute waves: i8row keeps one bf16 scale per row (applied by the caller through
 // row_scale), i8g32 one fp16 scale per chunk (applied inside the dot; row_scale is then 1). The group-scale arrays
 // of the i8row kernels are [1][1] and unused.
-template <int WD, int RW, int C, int GR, int GC>
+template <int WD, int RW, int C, bool LO = false, int GR, int GC>
 __device__ __forceinline__ void load_w(uint4 (&w)[RW][C], uint16_t (&s)[RW], uint16_t (&g)[GR][GC], const int8_t* W,
                                        const uint16_t* S, int row0, int nvalid, int K, int lane) {
   if constexpr (WD == SK_WD_I8G32) load_rows_g32<RW, C>(w, g, W, S, row0, nvalid, K, lane);
-  else load_rows<RW, C>(w, s, W, S, row0, nvalid, K, lane);
+  else load_rows<RW, C, LO>(w, s, W, S, row0, nvalid, K, lane);
 }
 template <int WD, int RW, int C, int GR, int GC>
 __device__ __forceinline__ void dot_w(const uint4 (&w)[RW][C], const uint16_t (&g)[GR][GC], const float* xs, int lane,
@@ -440,13 +462,18 @@ __device__ __forceinline__ float row_scale_of(uint16_t s) {
 // wave to arrive writes the workgroup's n cells [idx0, idx0 + n) (idx0 and n even) with 16-byte stores, so each
 // line of cells is written by one wave at one time (lines written piecewise by several waves reach the pollers
 // later). There is no barrier: the control wave may be polling the next stage's input meanwhile.
-template <int W, class L>
+template <int W, bool LO = false, class L>
 __device__ __forceinline__ void publish(L& S, void* cells, uint32_t idx0, int n, uint32_t e, int lane) {
   uint32_t old = 0;
   if (lane == 0) old = __hip_atomic_fetch_add(&S.pubcnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
   old = __builtin_amdgcn_readfirstlane(old);
   if (old % W == W - 1) {
-    for (int i = 2 * lane; i < n; i += 128) put2(cells, idx0 + i, S.pub[i], S.pub[i + 1], e);
+    if constexpr (LO) {
+      for (int k = 0; 128 * k < n; k++)
+        if (2 * lane + 128 * k < n) put2l(cells, idx0 + 128u * k, lane, S.pub[2 * lane + 128 * k], S.pub[2 * lane + 128 * k + 1], e);
+    } else {
+      for (int i = 2 * lane; i < n; i += 128) put2(cells, idx0 + i, S.pub[i], S.pub[i + 1], e);
+    }
     if (lane == 0) __hip_atomic_store(&S.pubseq, (old + 1) / W, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
@@ -1223,6 +1250,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 template <int H, int I, int W, int V, bool CP, bool SMP, int WD>
 __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
   using C = Cfg<H, I, W, V, CP>;
+  constexpr bool kLO = LaneOffsetPolls<H>::value;
   const Layout LY(H, I);
   const float eps = c.d.eps;
   const int ag = lane >> 4, asl = lane & 15;
@@ -1260,13 +1288,13 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   };
   {
     const sk_layer_desc& L0 = S.desc[0];
-    load_w<WD, C::RW_QKV, C::CH>(wq, sq, gq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
+    load_w<WD, C::RW_QKV, C::CH, kLO>(wq, sq, gq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
     load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), make_chunk<CP>(c.pos0, r, C::whole(c.pos0)), cw, ag, asl);
     load_attn_vec(L0, c.pos0);
     if constexpr (!C::kLate) {
-      load_w<WD, C::RW_O, C::CQ>(wo, so, go, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
-      load_w<WD, C::RW_GU, C::CH>(wg, sg, gg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
-      load_w<WD, C::RW_D, C::CI>(wd, sd, gd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
+      load_w<WD, C::RW_O, C::CQ, kLO>(wo, so, go, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
+      load_w<WD, C::RW_GU, C::CH, kLO>(wg, sg, gg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
+      load_w<WD, C::RW_D, C::CI, kLO>(wd, sd, gd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
     }
   }
   const bool block_eos0 = c.d.talker_processor && c.d.ngen;
@@ -1298,9 +1326,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
 #pragma unroll
           for (int i = 0; i < C::RW_QKV; i++) S.pub[C::RW_QKV * cw + i] = y[i] * row_scale_of<WD>(sq[i]) * inv;
         }
-        publish<W>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, 16, c.tick(f, l, 0), lane);
+        publish<W, kLO>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, 16, c.tick(f, l, 0), lane);
         if (tid == 0) c.tr(1, f, l, 1);
-        if constexpr (!C::kLate) load_w<WD, C::RW_QKV, C::CH>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+        if constexpr (!C::kLate) load_w<WD, C::RW_QKV, C::CH, kLO>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
       }
       // ---- S2: attention over this workgroup's chunk ----------------------------------------------------
       wg_sync();
@@ -1329,9 +1357,15 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
             dst[lane + 64] = y1;
             if (has_pos) {
               const __amdgpu_buffer_rsrc_t rs = make_rsrc(uniform(cw == 2 ? c.kh(Ly) : c.vh(Ly)));
-              const uint32_t off = (uint32_t)(pos * SK_HD + lane) * 2u;
-              __builtin_amdgcn_raw_buffer_store_b16(f2bf(y0), rs, off, 0, kPolDev);
-              __builtin_amdgcn_raw_buffer_store_b16(f2bf(y1), rs, off + 128u, 0, kPolDev);
+              if constexpr (kLO) {
+                const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)pos * SK_HD * 2u);
+                __builtin_amdgcn_raw_buffer_store_b16(f2bf(y0), rs, (uint32_t)lane * 2u, so, kPolDev);
+                __builtin_amdgcn_raw_buffer_store_b16(f2bf(y1), rs, (uint32_t)lane * 2u + 128u, so, kPolDev);
+              } else {
+                const uint32_t off = (uint32_t)(pos * SK_HD + lane) * 2u;
+                __builtin_amdgcn_raw_buffer_store_b16(f2bf(y0), rs, off, 0, kPolDev);
+                __builtin_amdgcn_raw_buffer_store_b16(f2bf(y1), rs, off + 128u, 0, kPolDev);
+              }
             }
           }
         }
@@ -1410,8 +1444,13 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           // publish the partial: [m0 l0 m1 l1 | o0[128] | o1[128]]
           const uint32_t pb = LY.e2 + ((uint32_t)x * kChunks + r) * kPartN;
           const uint32_t e = c.tick(f, l, 1);
-          if (dd == 0) { put(c.cells, pb + 2 * p, m, e); put(c.cells, pb + 2 * p + 1, lsum, e); }
-          put(c.cells, pb + 4 + p * SK_HD + dd, o, e);
+          if constexpr (kLO) {  // tid = p * 128 + dd
+            if (dd == 0) { putl(c.cells, pb, (uint32_t)p * 16u, m, e); putl(c.cells, pb, (uint32_t)p * 16u + 8u, lsum, e); }
+            putl(c.cells, pb + 4, (uint32_t)tid * 8u, o, e);
+          } else {
+            if (dd == 0) { put(c.cells, pb + 2 * p, m, e); put(c.cells, pb + 2 * p + 1, lsum, e); }
+            put(c.cells, pb + 4 + p * SK_HD + dd, o, e);
+          }
         }
         if (tid == 0) c.tr(1, f, l, 3);
         if constexpr (!C::kSpread) {
@@ -1419,9 +1458,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           load_attn_vec(Ln, npos);
         }
         if constexpr (C::kLate) {
-          load_w<WD, C::RW_O, C::CQ>(wo, so, go, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
+          load_w<WD, C::RW_O, C::CQ, kLO>(wo, so, go, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
           if constexpr (!C::kSpread)
-            load_w<WD, C::RW_GU, C::CH>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+            load_w<WD, C::RW_GU, C::CH, kLO>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
         }
       }
       // ---- S4: o projection rows, added to the layer's input residual ------------------------------------
@@ -1439,11 +1478,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           for (int i = 0; i < C::RW_O; i++)
             if (i < o_wn) S.pub[C::RW_O * cw + i] = S.hin[o_w0 + i] + y[i] * row_scale_of<WD>(so[i]);
         }
-        publish<W>(S, c.cells, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
+        publish<W, kLO>(S, c.cells, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
         if (tid == 0) c.tr(1, f, l, 5);
-        if constexpr (!C::kLate) load_w<WD, C::RW_O, C::CQ>(wo, so, go, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
+        if constexpr (!C::kLate) load_w<WD, C::RW_O, C::CQ, kLO>(wo, so, go, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
         if constexpr (C::kSpread)
-          load_w<WD, C::RW_GU, C::CH>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+          load_w<WD, C::RW_GU, C::CH, kLO>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
       }
       // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
       wg_sync();
@@ -1459,14 +1498,14 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           for (int i = 0; i < C::RW_GU; i += 2)
             S.pub[(C::RW_GU * cw + i) / 2] = silu_mul(y[i] * row_scale_of<WD>(sg[i]) * inv, y[i + 1] * row_scale_of<WD>(sg[i + 1]) * inv);
         }
-        publish<W>(S, c.cells, LY.e5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
+        publish<W, kLO>(S, c.cells, LY.e5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
         if (tid == 0) c.tr(1, f, l, 6);
         if constexpr (C::kLate) {
-          load_w<WD, C::RW_D, C::CI>(wd, sd, gd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
+          load_w<WD, C::RW_D, C::CI, kLO>(wd, sd, gd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
           if constexpr (!C::kSpread)
-            load_w<WD, C::RW_QKV, C::CH>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+            load_w<WD, C::RW_QKV, C::CH, kLO>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
         } else {
-          load_w<WD, C::RW_GU, C::CH>(wg, sg, gg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
+          load_w<WD, C::RW_GU, C::CH, kLO>(wg, sg, gg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
         }
       }
       // ---- S6: down rows, added to the residual after o --------------------------------------------------
@@ -1487,11 +1526,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
             }
           }
         }
-        publish<W>(S, c.cells, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
+        publish<W, kLO>(S, c.cells, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
         if (tid == 0) c.tr(1, f, l, 7);
-        if constexpr (!C::kLate) load_w<WD, C::RW_D, C::CI>(wd, sd, gd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
+        if constexpr (!C::kLate) load_w<WD, C::RW_D, C::CI, kLO>(wd, sd, gd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
         if constexpr (C::kSpread) {
-          load_w<WD, C::RW_QKV, C::CH>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+          load_w<WD, C::RW_QKV, C::CH, kLO>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
           load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
           load_attn_vec(Ln, npos);
         }
@@ -1507,7 +1546,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
     uint16_t gh[G32 ? C::RW_HEAD : 1][G32 ? C::CH : 1];
     const int8_t* hw = CP ? (const int8_t*)uniform(gload(c.cp.head_w + f)) : (const int8_t*)c.d.head_w;
     const uint16_t* hsc = CP ? (const uint16_t*)uniform(gload(c.cp.head_s + f)) : c.d.head_s;
-    load_w<WD, C::RW_HEAD, C::CH>(wh, sh, gh, hw, hsc, h_w0, h_wn, H, lane);
+    load_w<WD, C::RW_HEAD, C::CH, kLO>(wh, sh, gh, hw, hsc, h_w0, h_wn, H, lane);
     wg_sync();
     if (S.flags[5]) return;
     {
