@@ -38,15 +38,17 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
-TRAFFIC_PROFILE = ROOT / "profiles" / "k_frames_talker06b_traffic.md"
+TRAFFIC_PROFILES = {"talker06b": ROOT / "profiles" / "k_frames_talker06b_traffic.md",
+                    "talker17b": ROOT / "profiles" / "k_frames_talker17b_traffic.md"}
 
 
-def measured_traffic(name: str, engine: str):
-    """HBM bytes per launch of the frame kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-    (calibrated against a plain copy of known size), or None when no summary covers this workload."""
-    if name != "talker06b" or engine != "frames" or not TRAFFIC_PROFILE.exists():
+def measured_traffic(name: str, engine: str, wd: str = "i8row"):
+    """HBM bytes per launch of the frame kernel (i8row weights, 64 frames) from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a plain copy of known size), or None when no summary covers this run."""
+    prof = TRAFFIC_PROFILES.get(name)
+    if engine != "frames" or wd != "i8row" or prof is None or not prof.exists():
         return None
-    for line in TRAFFIC_PROFILE.read_text().splitlines():
+    for line in prof.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
             return int(line.split(":", 1)[1].strip())
     return None
@@ -551,14 +553,10 @@ def main() -> None:
               "(this build has no multi-GPU path); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
-    if args.workload == "cp06b":
-        run_cp(args)
-        return
-    if args.workload == "batch17b":
-        run_batch(args)
-        return
-    if args.workload == "frame06b":
-        run_frame(args)
+    other = {"cp06b": run_cp, "batch17b": run_batch, "frame06b": run_frame}.get(args.workload)
+    if other is not None:
+        other(args)
+        calibration_copy(args.calibration_copy_mib)
         return
 
     import torch
@@ -637,7 +635,7 @@ def main() -> None:
         launch_us = sum(a.elapsed_time(b) for a, b in ev) * 1e3 / len(ev)
         roof = {"bound": "hbm", "kernel": "k_frames (sk_talker_frames, 64 frames per launch)",
                 "achieved": round(step_bytes / (launch_us * 1e-6) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "traffic": measured_traffic(name, args.engine), "bytes_per_launch": int(step_bytes),
+                "traffic": measured_traffic(name, args.engine, args.wd), "bytes_per_launch": int(step_bytes),
                 "avg_launch_us": round(launch_us, 2)}
         roof["frac"] = round(roof["achieved"] / PEAK_HBM_GBS, 4)
         extra = {}
@@ -677,12 +675,21 @@ def main() -> None:
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(name, args.seed)
     print(json.dumps(res), flush=True)
-    if args.calibration_copy_mib > 0:
-        src = torch.randint(0, 255, (args.calibration_copy_mib << 20,), dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(2):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+    calibration_copy(args.calibration_copy_mib)
+
+
+def calibration_copy(mib: int) -> None:
+    """Two plain device copies of ``mib`` MiB after the timed run: a dispatch of known traffic (reads and writes
+    exactly mib MiB) that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counts of the same run."""
+    if mib <= 0:
+        return
+    import torch
+
+    src = torch.randint(0, 255, (mib << 20,), dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 if __name__ == "__main__":

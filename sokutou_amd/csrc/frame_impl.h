@@ -1261,10 +1261,15 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   else if (r < 24) qkv_row0 = kQ + 128 * x + 16 * (r - 16);
   else qkv_row0 = kQ + kNKV * 128 + 128 * x + 16 * (r - 24);
   const int q_w0 = qkv_row0 + C::RW_QKV * cw;
-  const int o_w0 = C::R_O * g + C::RW_O * cw, o_wn = max(0, min(C::RW_O, C::R_O - C::RW_O * cw));
+  // With more waves than rows (RW * W > R) a wave with no rows of its own loads the workgroup's last row (in range,
+  // values unused; load_rows repeats row0 for rows past nvalid) instead of one past the workgroup's rows, which is
+  // past the matrix for the last workgroup.
+  constexpr bool kClO = C::RW_O * W > C::R_O, kClD = C::RW_D * W > C::R_D, kClH = C::RW_HEAD * W > C::kHeadRows;
+  const int o_w0 = C::R_O * g + (kClO ? min(C::RW_O * cw, C::R_O - 1) : C::RW_O * cw), o_wn = max(0, min(C::RW_O, C::R_O - C::RW_O * cw));
   const int gu_w0 = C::R_GU * g + C::RW_GU * cw;
-  const int d_w0 = C::R_D * g + C::RW_D * cw, d_wn = max(0, min(C::RW_D, C::R_D - C::RW_D * cw));
-  const int h_w0 = C::kHeadRows * g + C::RW_HEAD * cw, h_wn = max(0, min(C::RW_HEAD, C::kHeadRows - C::RW_HEAD * cw));
+  const int d_w0 = C::R_D * g + (kClD ? min(C::RW_D * cw, C::R_D - 1) : C::RW_D * cw), d_wn = max(0, min(C::RW_D, C::R_D - C::RW_D * cw));
+  const int h_w0 = C::kHeadRows * g + (kClH ? min(C::RW_HEAD * cw, C::kHeadRows - 1) : C::RW_HEAD * cw),
+            h_wn = max(0, min(C::RW_HEAD, C::kHeadRows - C::RW_HEAD * cw));
   // the attention thread mapping uses the first 256 compute threads: head p = t / 128, dim dd = t % 128
   const int p = tid >> 7, dd = tid & 127;
   const bool att_thread = tid < 256;
