@@ -233,6 +233,10 @@ typedef struct sk_cp_desc {
   int top_k;
   const uint64_t* seed;
   uint64_t* counter;
+  /* Nonzero: the layer weights are loaded through the caches (they are read once per position, 16 times per frame,
+   * and stay in L2 / the Infinity Cache); 0: streamed with non-temporal loads, as the heads always are. The
+   * reference's l2_keep_mb policy (qwen3/kernels.py:525-542), for the code predictor's layers as a whole. */
+  int keep_layers;
 } sk_cp_desc;
 
 /* All positions of the code predictor of one frame in ONE launch (the persistent kernel of sk_talker_frames in

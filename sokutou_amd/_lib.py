@@ -68,7 +68,7 @@ class SkCpDesc(ctypes.Structure):
                 ("emb0_rows", c_int), ("emb", c_void_p), ("head_w", c_void_p), ("head_s", c_void_p),
                 ("codes", c_void_p), ("logits", c_void_p), ("layer_out", c_void_p), ("workspace", c_void_p),
                 ("workspace_bytes", c_int64), ("do_sample", c_int), ("inv_temp", c_float), ("top_k", c_int),
-                ("seed", c_void_p), ("counter", c_void_p)]
+                ("seed", c_void_p), ("counter", c_void_p), ("keep_layers", c_int)]
 
 
 class SkBatchDesc(ctypes.Structure):

@@ -26,5 +26,6 @@ extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
   t.logits = d->logits; t.layer_out = d->layer_out; t.workspace = d->workspace; t.workspace_bytes = d->workspace_bytes;
   t.do_sample = d->do_sample; t.inv_temp = d->inv_temp; t.top_k = d->top_k; t.seed = d->seed; t.counter = d->counter;
   const CpArgs cp{d->x0, d->emb, d->head_w, d->head_s, d->emb0_rows};
+  if (d->keep_layers) return launch_frames<1024, 3072, 4, 2048, true, SK_WD_I8ROW, true>(&t, cp, d->n_positions, (hipStream_t)stream);
   return launch_frames<1024, 3072, 4, 2048, true>(&t, cp, d->n_positions, (hipStream_t)stream);
 }

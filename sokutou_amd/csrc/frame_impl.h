@@ -333,7 +333,12 @@ __device__ __forceinline__ void load_pairs(const float* p, float2 (&w)[NB], int 
 // The row scales come with the weights through vector loads (a scalar load would make every later LDS wait,
 // lgkmcnt, wait for it as well) and stay raw bf16 bits until the dot that uses them: converting on arrival would
 // make the wave wait for the load right after issuing it.
-template <int RW, int C, bool LO = false>
+// A weight chunk through the caches (the code predictor's layers with keep_layers: read 16 times per frame).
+__device__ __forceinline__ uint4 ld_keep(const uint4* p) {
+  const u32x4 r = *(gptr<const u32x4>)p;
+  return make_uint4(r.x, r.y, r.z, r.w);
+}
+template <int RW, int C, bool LO = false, bool KEEP = false>
 __device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], uint16_t (&s)[RW], const int8_t* W, const uint16_t* S,
                                           int row0, int nvalid, int K, int lane) {
 #pragma unroll
@@ -350,7 +355,7 @@ __device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], uint16_t (&s)[RW], 
     }
     const uint4* p = (const uint4*)(W + (size_t)row * K);
 #pragma unroll
-    for (int c = 0; c < C; c++) w[r][c] = ld_stream(p + lane + 64 * c);
+    for (int c = 0; c < C; c++) w[r][c] = KEEP ? ld_keep(p + lane + 64 * c) : ld_stream(p + lane + 64 * c);
     // one ushort load per row: merged wider loads would be split into halves right away, waiting for them
     s[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), (uint32_t)row * 2u, 0, 0);
   }
@@ -440,11 +445,11 @@ __device__ __forceinline__ void dot_rows_g32(const uint4 (&w)[RW][C], const uint
 // Weight-format dispatch of the compute waves: i8row keeps one bf16 scale per row (applied by the caller through
 // row_scale), i8g32 one fp16 scale per chunk (applied inside the dot; row_scale is then 1). The group-scale arrays
 // of the i8row kernels are [1][1] and unused.
-template <int WD, int RW, int C, bool LO = false, int GR, int GC>
+template <int WD, int RW, int C, bool LO = false, bool KEEP = false, int GR, int GC>
 __device__ __forceinline__ void load_w(uint4 (&w)[RW][C], uint16_t (&s)[RW], uint16_t (&g)[GR][GC], const int8_t* W,
                                        const uint16_t* S, int row0, int nvalid, int K, int lane) {
   if constexpr (WD == SK_WD_I8G32) load_rows_g32<RW, C>(w, g, W, S, row0, nvalid, K, lane);
-  else load_rows<RW, C, LO>(w, s, W, S, row0, nvalid, K, lane);
+  else load_rows<RW, C, LO, KEEP>(w, s, W, S, row0, nvalid, K, lane);
 }
 template <int WD, int RW, int C, int GR, int GC>
 __device__ __forceinline__ void dot_w(const uint4 (&w)[RW][C], const uint16_t (&g)[GR][GC], const float* xs, int lane,
@@ -1247,7 +1252,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 // ================================================================================================================
 // Compute waves
 // ================================================================================================================
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP>
 __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
   using C = Cfg<H, I, W, V, CP>;
   constexpr bool kLO = LaneOffsetPolls<H>::value;
@@ -1293,13 +1298,13 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   };
   {
     const sk_layer_desc& L0 = S.desc[0];
-    load_w<WD, C::RW_QKV, C::CH, kLO>(wq, sq, gq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
+    load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
     load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), make_chunk<CP>(c.pos0, r, C::whole(c.pos0)), cw, ag, asl);
     load_attn_vec(L0, c.pos0);
     if constexpr (!C::kLate) {
-      load_w<WD, C::RW_O, C::CQ, kLO>(wo, so, go, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
-      load_w<WD, C::RW_GU, C::CH, kLO>(wg, sg, gg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
-      load_w<WD, C::RW_D, C::CI, kLO>(wd, sd, gd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
+      load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
+      load_w<WD, C::RW_GU, C::CH, kLO, KEEP>(wg, sg, gg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
+      load_w<WD, C::RW_D, C::CI, kLO, KEEP>(wd, sd, gd, (const int8_t*)L0.down_w, L0.down_s, d_w0, d_wn, I, lane);
     }
   }
   const bool block_eos0 = c.d.talker_processor && c.d.ngen;
@@ -1333,7 +1338,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         }
         publish<W, kLO>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, 16, c.tick(f, l, 0), lane);
         if (tid == 0) c.tr(1, f, l, 1);
-        if constexpr (!C::kLate) load_w<WD, C::RW_QKV, C::CH, kLO>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+        if constexpr (!C::kLate) load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
       }
       // ---- S2: attention over this workgroup's chunk ----------------------------------------------------
       wg_sync();
@@ -1463,9 +1468,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           load_attn_vec(Ln, npos);
         }
         if constexpr (C::kLate) {
-          load_w<WD, C::RW_O, C::CQ, kLO>(wo, so, go, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
+          load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
           if constexpr (!C::kSpread)
-            load_w<WD, C::RW_GU, C::CH, kLO>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+            load_w<WD, C::RW_GU, C::CH, kLO, KEEP>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
         }
       }
       // ---- S4: o projection rows, added to the layer's input residual ------------------------------------
@@ -1485,9 +1490,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         }
         publish<W, kLO>(S, c.cells, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
         if (tid == 0) c.tr(1, f, l, 5);
-        if constexpr (!C::kLate) load_w<WD, C::RW_O, C::CQ, kLO>(wo, so, go, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
+        if constexpr (!C::kLate) load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
         if constexpr (C::kSpread)
-          load_w<WD, C::RW_GU, C::CH, kLO>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+          load_w<WD, C::RW_GU, C::CH, kLO, KEEP>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
       }
       // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
       wg_sync();
@@ -1506,11 +1511,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         publish<W, kLO>(S, c.cells, LY.e5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
         if (tid == 0) c.tr(1, f, l, 6);
         if constexpr (C::kLate) {
-          load_w<WD, C::RW_D, C::CI, kLO>(wd, sd, gd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
+          load_w<WD, C::RW_D, C::CI, kLO, KEEP>(wd, sd, gd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
           if constexpr (!C::kSpread)
-            load_w<WD, C::RW_QKV, C::CH, kLO>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+            load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
         } else {
-          load_w<WD, C::RW_GU, C::CH, kLO>(wg, sg, gg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
+          load_w<WD, C::RW_GU, C::CH, kLO, KEEP>(wg, sg, gg, (const int8_t*)Ln.gu_w, Ln.gu_s, gu_w0, C::RW_GU, H, lane);
         }
       }
       // ---- S6: down rows, added to the residual after o --------------------------------------------------
@@ -1533,9 +1538,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         }
         publish<W, kLO>(S, c.cells, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
         if (tid == 0) c.tr(1, f, l, 7);
-        if constexpr (!C::kLate) load_w<WD, C::RW_D, C::CI, kLO>(wd, sd, gd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
+        if constexpr (!C::kLate) load_w<WD, C::RW_D, C::CI, kLO, KEEP>(wd, sd, gd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
         if constexpr (C::kSpread) {
-          load_w<WD, C::RW_QKV, C::CH, kLO>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+          load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
           load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
           load_attn_vec(Ln, npos);
         }
@@ -1590,7 +1595,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
 
 // SMP: sampled picks (do_sample != 0). The greedy instantiation carries none of the sampling code, whose call and
 // registers would otherwise weigh on the control loop of every greedy frame.
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP>
 __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArgs cp, int n_frames) {
   extern __shared__ char smem_raw[];
   Lds<H, I, W, V, CP>& S = *(Lds<H, I, W, V, CP>*)smem_raw;
@@ -1668,7 +1673,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   }
   c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
   if (wave == W) run_control<H, I, W, V, CP, SMP>(c, S, lane);
-  else run_compute<H, I, W, V, CP, SMP, WD>(c, S, wave, tid, lane);
+  else run_compute<H, I, W, V, CP, SMP, WD, KEEP>(c, S, wave, tid, lane);
   // ---- end of launch: epoch base and launch count (workgroup 0; every workgroup finished its census) --------
   if (c.g == 0 && tid == 0) {
     st_u32_dev(ws, Ws::kTick, c.base + (uint32_t)n_frames * c.tpf);
@@ -1680,14 +1685,14 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
 // cannot hold a workgroup, would only surface as poll timeouts). Done once per device and instantiation; a failure
 // is reported every time and retried on the next call.
 constexpr int kMaxDevices = 64;
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP>
 int prepare_kernel(size_t lds) {
   static bool ready[kMaxDevices] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return sk_set_error(SK_EDEVICE, "sk_talker_frames: no current HIP device");
   if (ready[dev]) return SK_OK;
-  const void* fn = (const void*)k_frames<H, I, W, V, CP, SMP, WD>;
+  const void* fn = (const void*)k_frames<H, I, W, V, CP, SMP, WD, KEEP>;
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return sk_check_launch(e, "sk_talker_frames: raising the LDS limit");
   int cus = 0, per_cu = 0;
@@ -1702,19 +1707,21 @@ int prepare_kernel(size_t lds) {
   ready[dev] = true;
   return SK_OK;
 }
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP>
 int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
   const size_t lds = sizeof(Lds<H, I, W, V, CP>) < 96 * 1024 ? 96 * 1024 : sizeof(Lds<H, I, W, V, CP>);  // one workgroup per CU
-  const int rc = prepare_kernel<H, I, W, V, CP, SMP, WD>(lds);
+  const int rc = prepare_kernel<H, I, W, V, CP, SMP, WD, KEEP>(lds);
   if (rc != SK_OK) return rc;
-  hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP, WD>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp, n_frames);
+  hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP, WD, KEEP>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp, n_frames);
   return sk_check_launch(hipGetLastError(), "sk_talker_frames");
 }
-template <int H, int I, int W, int V, bool CP, int WD = SK_WD_I8ROW>
+// KEEP: the layer weights are loaded through the caches instead of as non-temporal streams (the code predictor
+// with keep_layers; the heads and every talker weight stream).
+template <int H, int I, int W, int V, bool CP, int WD = SK_WD_I8ROW, bool KEEP = false>
 int launch_frames(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
   if (d->max_len > Cfg<H, I, W, V, CP>::kMaxLen) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: max_len too long");
-  return d->do_sample ? launch_kernel<H, I, W, V, CP, true, WD>(d, cp, n_frames, st)
-                      : launch_kernel<H, I, W, V, CP, false, WD>(d, cp, n_frames, st);
+  return d->do_sample ? launch_kernel<H, I, W, V, CP, true, WD, KEEP>(d, cp, n_frames, st)
+                      : launch_kernel<H, I, W, V, CP, false, WD, KEEP>(d, cp, n_frames, st);
 }
 
 }  // namespace

@@ -169,6 +169,22 @@ class _Stack:
         return sum(L[k].bytes() for L in self.layers for k in ("qkv", "o", "gu", "down"))
 
 
+def _keep_policies(layers: list, l2_keep_mb: float | None) -> int:
+    """Cache policy of the code predictor's matrices (qwen3/kernels.py:525-542): walking the layers in order, a
+    matrix that fits the remaining budget of ``l2_keep_mb`` MiB stays cacheable (``pol`` 0) and uses up its
+    bytes, one that does not is streamed (``pol`` 1). ``None`` is an unbounded budget. Returns the kept bytes."""
+    budget = float("inf") if l2_keep_mb is None else float(l2_keep_mb) * 2**20
+    kept = 0
+    for Ly in layers:
+        for m in ("qkv", "o", "gu", "down"):
+            b = Ly[m].bytes()
+            Ly[m].pol = 0 if b <= budget else 1
+            if b <= budget:
+                budget -= b
+                kept += b
+    return kept
+
+
 def _layer_descs(P: _Stack, kc: list, vc: list, device) -> torch.Tensor:
     """Device array of ``sk_layer_desc`` for the layers of ``P`` with caches ``kc[i]`` / ``vc[i]``."""
     arr = (_lib.SkLayerDesc * len(P.layers))()
@@ -193,9 +209,12 @@ class CodePredictor:
     sampler's draw (temperature, top_k, Philox seed and counter in device memory; one draw per position g >= 1)."""
 
     def __init__(self, cp, temb: torch.Tensor, n_positions: int = 16, wd: str = "i8row", device=None,
-                 x0: torch.Tensor | None = None, id0: torch.Tensor | None = None, codes: torch.Tensor | None = None):
+                 x0: torch.Tensor | None = None, id0: torch.Tensor | None = None, codes: torch.Tensor | None = None,
+                 keep_layers: bool = True):
         """``x0`` (fp32 [hidden]), ``id0`` (int64, one element) and ``codes`` (int64 [n_positions]) may be a caller's
-        own contiguous device buffers: the kernel then reads and writes them in place (no copies per frame)."""
+        own contiguous device buffers: the kernel then reads and writes them in place (no copies per frame).
+        ``keep_layers`` loads the layer weights through the caches (read once per position, they stay in L2 and
+        the Infinity Cache across the frame) instead of streaming them like the heads (``sk_cp_desc.keep_layers``)."""
         if wd != "i8row":
             raise ValueError("the code-predictor kernel reads i8row weights")
         proj = getattr(cp, "small_to_mtp_projection", None)
@@ -241,7 +260,8 @@ class CodePredictor:
             rope=P.rope.data_ptr(), x0=self.x0.data_ptr(), id0=self.id0.data_ptr(), emb0_rows=self.temb.shape[0],
             emb=self._ptrs[0].data_ptr(), head_w=self._ptrs[1].data_ptr(), head_s=self._ptrs[2].data_ptr(),
             codes=self.codes.data_ptr(), logits=self.logits.data_ptr(), layer_out=None,
-            workspace=self.ws.data_ptr(), workspace_bytes=self.ws.numel())
+            workspace=self.ws.data_ptr(), workspace_bytes=self.ws.numel(), keep_layers=int(bool(keep_layers)))
+        self.keep_layers = bool(keep_layers)
         self.graph: torch.cuda.CUDAGraph | None = None
 
     def set_sampling(self, temperature: float, top_k: int, seed: torch.Tensor, counter: torch.Tensor) -> None:
@@ -303,9 +323,12 @@ class CodePredictor:
 class Qwen3Kernels(Qwen3Fast):
     """The talker frame on the sokutou_amd kernels (qwen3/kernels.py:483-754 surface).
 
-    Constructor arguments as the reference; ``wd`` adds ``i8row``. ``l2_keep_mb`` and ``cp_pair`` are accepted
-    for interface parity: the talker's weights are always streamed (policy 1), and the code predictor is not
-    part of this engine yet. ``suppress_tail`` (default 1024, as the reference) sets how many trailing ids the
+    Constructor arguments as the reference; ``wd`` adds ``i8row``. ``l2_keep_mb`` is the reference's cache budget
+    for the code predictor's layers (qwen3/kernels.py:525-542): matrices within it, in layer order, are loaded
+    cacheable (policy 0), the rest and every talker and head weight are streamed (policy 1); unset, it covers all
+    of them (their 79 MB fit MI355X's 256 MB Infinity Cache). The one-launch code-predictor kernel applies one
+    policy to all its layers: cacheable only when the budget covers every layer. ``cp_pair`` is accepted for
+    interface parity (positions 0 and 1 run as two passes). ``suppress_tail`` (default 1024, as the reference) sets how many trailing ids the
     processor suppresses; 0 disables suppression.
     """
 
@@ -327,6 +350,7 @@ class Qwen3Kernels(Qwen3Fast):
         self.ct = "f32" if wd == "f32" else "bf16"
         cdt = torch.float32 if self.ct == "f32" else torch.bfloat16
         self.cp_pair = bool(cp_pair) if cp_pair is not None else True
+        self._l2_keep_arg = l2_keep_mb
         self.l2_keep_mb = l2_keep_mb if l2_keep_mb is not None else 0.0
         dev = self.device
         with torch.no_grad():
@@ -395,6 +419,9 @@ class Qwen3Kernels(Qwen3Fast):
             raise ValueError(f"{self.G} code groups need {self.G - 1} heads and {self.G - 1} code tables")
         for h in self.cp_heads:
             h.pol = 1
+        self.l2_kept_bytes = _keep_policies(self.C.layers, self._l2_keep_arg)
+        if self._l2_keep_arg is None:
+            self.l2_keep_mb = self.l2_kept_bytes / 2**20
         # talker input tables: code 0 from the talker's table, code g >= 1 from code table g - 1
         self.tabs = torch.tensor([self.temb.data_ptr()] + [e.data_ptr() for e in self.cemb[: self.G - 1]],
                                  dtype=torch.int64, device=dev)
@@ -415,8 +442,9 @@ class Qwen3Kernels(Qwen3Fast):
                 and 2 <= self.G <= 64)
         if fast:
             # bound to the frame state: reads ph32 and code 0, writes all G codes, with no copy per frame
+            keep = all(Ly[m].pol == 0 for Ly in P.layers for m in ("qkv", "o", "gu", "down"))
             self.cpk = CodePredictor(cp, self.temb, n_positions=self.G, wd=wd, device=dev, x0=self.ph32, id0=self.id0,
-                                     codes=self.codes)
+                                     codes=self.codes, keep_layers=keep)
             if self.s.sub_do_sample:  # the fused sampler's draws, in the same order as position by position
                 self.cpk.set_sampling(self.s.sub_temperature, self.s.sub_top_k, self.fs.seed, self.fs.counter)
 

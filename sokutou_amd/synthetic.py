@@ -446,14 +446,15 @@ def make_prefill_engine(name: str, seed: int = 0, L: int = 24, frames: int = 8, 
     return eng, kw
 
 
-def make_cp_engine(name: str = "cp06b", seed: int = 0, device="cuda"):
-    """A CodePredictor over the seeded synthetic code predictor of workload ``name`` (one frame per run)."""
+def make_cp_engine(name: str = "cp06b", seed: int = 0, device="cuda", keep_layers: bool = True):
+    """A CodePredictor over the seeded synthetic code predictor of workload ``name`` (one frame per run);
+    ``keep_layers`` as CodePredictor's (layer weights loaded cacheable, the default, or streamed)."""
     from .kernels import CodePredictor
 
     spec = WORKLOADS[name]
     s = workload_shape(name)
     cp, temb = make_code_predictor(seed, s, device=device, n_positions=spec["positions"])
-    return CodePredictor(cp, temb, n_positions=spec["positions"], wd="i8row", device=device)
+    return CodePredictor(cp, temb, n_positions=spec["positions"], wd="i8row", device=device, keep_layers=keep_layers)
 
 
 # ---------------------------------------------------------------------------------------------------------

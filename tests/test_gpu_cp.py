@@ -1,5 +1,6 @@
-"""The code predictor on the persistent kernel (sk_cp_frame): greedy sub-codes of every position, per-layer
-residuals and logits at the last position, against the oracle fixture; graph replay; the error word."""
+"""The code predictor on the persistent kernel (sk_cp_frame), with its layer weights kept or streamed: greedy
+sub-codes of every position, per-layer residuals and logits at the last position, against the oracle fixture;
+graph replay; the error word."""
 
 import json
 from pathlib import Path
@@ -20,10 +21,11 @@ def rel_err(a, b) -> float:
     return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
 
 
-@pytest.fixture(scope="module")
-def cp_engine(gpu):
-    print("cp06b: building the seeded code predictor (5 layers, 15 heads)", flush=True)
-    return syn.make_cp_engine("cp06b", 0, gpu)
+@pytest.fixture(scope="module", params=[True, False], ids=["keep", "stream"])
+def cp_engine(gpu, request):
+    """Both instantiations of the kernel: layer weights loaded cacheable (the default) or streamed."""
+    print(f"cp06b: building the seeded code predictor (5 layers, 15 heads), keep_layers={request.param}", flush=True)
+    return syn.make_cp_engine("cp06b", 0, gpu, keep_layers=request.param)
 
 
 def test_code_predictor_frames_against_oracle(cp_engine, gpu):

@@ -129,3 +129,26 @@ def test_frame_kernels_reject_sampling_without_seed_or_temperature():
                       do_sample=1, inv_temp=1.25, top_k=40, seed=d, counter=None)
     assert L.sk_cp_frame(ctypes.byref(c), None) == _lib.SK_EINVAL
     assert b"sampling" in L.sk_last_error()
+
+
+def test_code_predictor_keep_policies_follow_the_reference_budget():
+    """l2_keep_mb walks the code predictor's matrices in layer order (qwen3/kernels.py:525-542): a matrix that fits
+    what is left of the budget stays cacheable and uses it up, one that does not is streamed (a later, smaller one
+    may still fit); no budget keeps everything."""
+    from sokutou_amd.kernels import _keep_policies
+
+    class M:
+        def __init__(self, n):
+            self.n, self.pol = n, None
+
+        def bytes(self):
+            return self.n
+
+    MiB = 2**20
+    layers = [{"qkv": M(4 * MiB), "o": M(2 * MiB), "gu": M(6 * MiB), "down": M(3 * MiB)} for _ in range(2)]
+    assert _keep_policies(layers, None) == 30 * MiB
+    assert all(Ly[m].pol == 0 for Ly in layers for m in Ly)
+    assert _keep_policies(layers, 10) == 9 * MiB  # qkv 4 + o 2 kept, gu 6 > 4 left streamed, down 3 kept
+    assert [layers[0][m].pol for m in ("qkv", "o", "gu", "down")] == [0, 0, 1, 0]
+    assert [layers[1][m].pol for m in ("qkv", "o", "gu", "down")] == [1, 1, 1, 1]
+    assert _keep_policies(layers, 0) == 0 and all(Ly[m].pol == 1 for Ly in layers for m in Ly)
