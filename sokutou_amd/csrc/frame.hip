@@ -25,9 +25,9 @@ extern "C" int64_t sk_talker_workspace_size(int hidden, int inter) {
 extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* stream) {
   if (!d || n_frames <= 0) return sk_set_error(SK_EINVAL, "sk_talker_frames: bad arguments");
   if (d->nq != kNQ || d->nkv != kNKV || d->vocab != kTalkerV || d->ct != SK_CT_BF16 ||
-      !(d->wd == SK_WD_I8ROW || (d->wd == SK_WD_I8G32 && d->hidden == 1024 && d->inter == 3072)))
+      !(d->wd == SK_WD_I8ROW || d->wd == SK_WD_I8G32))
     return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs 16 q / 8 kv heads, vocab 3072, bf16 cache and i8row "
-                                         "weights (or i8g32 at hidden 1024)");
+                                         "or i8g32 weights");
   if (!d->layers || !d->norm || !d->head_w || !d->head_s || !d->emb || !d->rope || !d->id0 || !d->pos || !d->workspace)
     return sk_set_error(SK_EINVAL, "sk_talker_frames: null pointer");
   if (d->n_layers <= 0 || d->n_layers > Ws::kTraceLayers)
@@ -49,7 +49,7 @@ extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* str
       const char* poll = std::getenv("SOKUTOU_TALKER_POLL");
       return poll && !std::strcmp(poll, "regs");
     }();
-    if (regs) return launch_frames<2048, 6144, 8, kTalkerV, false>(d, none, n_frames, st);
+    if (regs && d->wd == SK_WD_I8ROW) return launch_frames<2048, 6144, 8, kTalkerV, false>(d, none, n_frames, st);
     return sk_talker_frames_2048(d, n_frames, st);
   }
   return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: shapes other than the 0.6B / 1.7B talker");

@@ -28,5 +28,6 @@ static_assert(Cfg<kH, kI, 4, kTalkerV, false>::kMaxLen >= 2048, "1.7B caches up 
 
 int sk_talker_frames_2048(const sk_talker_desc* d, int n_frames, hipStream_t st) {
   const CpArgs none{};
+  if (d->wd == SK_WD_I8G32) return sk_talker_frames_2048_g32(d, n_frames, st);
   return launch_frames<kH, kI, 4, kTalkerV, false>(d, none, n_frames, st);
 }

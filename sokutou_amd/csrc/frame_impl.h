@@ -393,12 +393,23 @@ __device__ __forceinline__ void dot_rows(const uint4 (&w)[RW][C], const float* x
 // i8g32 weights (the reference's format: one fp16 scale per 32 weights of a row, applied per 16-weight chunk,
 // qwen3/kernels.py:104-110): a lane's chunk c of a row covers weights 16 (lane + 64 c) .. + 15, inside group
 // (lane + 64 c) / 2, whose scale comes with the chunk (raw fp16 bits until the dot).
-template <int RW, int C>
+template <int RW, int C, bool LO = false>
 __device__ __forceinline__ void load_rows_g32(uint4 (&w)[RW][C], uint16_t (&g)[RW][C], const int8_t* W, const uint16_t* S,
                                               int row0, int nvalid, int K, int lane) {
 #pragma unroll
   for (int r = 0; r < RW; r++) {
     const int row = r < nvalid ? row0 + r : row0;
+    if constexpr (LO) {  // row starts in the scalar offsets; the scale of chunk c is at byte (lane & ~1) + 64 c
+      const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)row * (uint32_t)K);
+      const uint32_t sg = __builtin_amdgcn_readfirstlane((uint32_t)row * (uint32_t)(K >> 4));
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        w[r][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(W)),
+                                                                                  (uint32_t)lane * 16u + 1024u * c, so, kNT));
+        g[r][c] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), ((uint32_t)lane & ~1u) + 64u * c, sg, 0);
+      }
+      continue;
+    }
     const uint4* p = (const uint4*)(W + (size_t)row * K);
 #pragma unroll
     for (int c = 0; c < C; c++) {
@@ -448,7 +459,7 @@ __device__ __forceinline__ void dot_rows_g32(const uint4 (&w)[RW][C], const uint
 template <int WD, int RW, int C, bool LO = false, bool KEEP = false, int GR, int GC>
 __device__ __forceinline__ void load_w(uint4 (&w)[RW][C], uint16_t (&s)[RW], uint16_t (&g)[GR][GC], const int8_t* W,
                                        const uint16_t* S, int row0, int nvalid, int K, int lane) {
-  if constexpr (WD == SK_WD_I8G32) load_rows_g32<RW, C>(w, g, W, S, row0, nvalid, K, lane);
+  if constexpr (WD == SK_WD_I8G32) load_rows_g32<RW, C, LO>(w, g, W, S, row0, nvalid, K, lane);
   else load_rows<RW, C, LO, KEEP>(w, s, W, S, row0, nvalid, K, lane);
 }
 template <int WD, int RW, int C, int GR, int GC>

@@ -7,10 +7,12 @@
 int sk_set_error(int rc, const char* msg);
 // Maps a launch status to SK_OK / SK_ELAUNCH, recording the HIP error string.
 int sk_check_launch(hipError_t e, const char* where);
-// Launches the frame kernel of the 1.7B talker shape (hidden 2048, intermediate 6144, 4 compute waves) on a
-// validated descriptor; a translation unit of its own (frame17.hip), called by sk_talker_frames.
+// Launches the frame kernel of the 1.7B talker shape (hidden 2048, intermediate 6144, 4 compute waves; i8row or
+// i8g32 weights) on a validated descriptor; a translation unit of its own (frame17.hip), called by sk_talker_frames.
 int sk_talker_frames_2048(const sk_talker_desc* d, int n_frames, hipStream_t st);
 // Launches the frame kernel of the 0.6B talker shape with i8g32 weights (frame_g32.hip) on a validated descriptor.
+// The 1.7B shape's i8g32 kernel (frame17_g32.hip), called by sk_talker_frames_2048.
+int sk_talker_frames_2048_g32(const sk_talker_desc* d, int n_frames, hipStream_t st);
 int sk_talker_frames_g32(const sk_talker_desc* d, int n_frames, hipStream_t st);
 
 #define SK_ALIGNED16(p) ((((uintptr_t)(p)) & 15u) == 0)

@@ -491,11 +491,10 @@ class Qwen3Kernels(Qwen3Fast):
 
     # --- the persistent frame kernel ------------------------------------------------------------------------
     def frame_kernel_supported(self) -> bool:
-        """The persistent kernel covers the 0.6B and 1.7B talker shapes with i8row weights, and the 0.6B shape with
-        the reference's i8g32 weights too."""
+        """The persistent kernel covers the 0.6B and 1.7B talker shapes with i8row weights or the reference's i8g32."""
         P = self.T
         shapes = {(1024, 3072): 1024, (2048, 6144): 2048}
-        wd_ok = self.wd == "i8row" or (self.wd == "i8g32" and (P.H, P.I) == (1024, 3072))
+        wd_ok = self.wd in ("i8row", "i8g32")
         return (wd_ok and self.ct == "bf16" and P.nq == 16 and P.nkv == 8 and self.V == 3072
                 and (P.H, P.I) in shapes and self.max_cache <= shapes[(P.H, P.I)])
 
