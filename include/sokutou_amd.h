@@ -237,15 +237,25 @@ typedef struct sk_cp_desc {
    * and stay in L2 / the Infinity Cache); 0: streamed with non-temporal loads, as the heads always are. The
    * reference's l2_keep_mb policy (qwen3/kernels.py:525-542), for the code predictor's layers as a whole. */
   int keep_layers;
+  /* Nonzero: positions 0 and 1 run as one pass with two rows per stage, in a launch of their own before the
+   * other positions' (each layer's weights read once for both; the reference's cp_pair, qwen3/kernels.py:600-617);
+   * the workspace is then sk_cp_workspace_size(hidden, inter, 1) bytes. 0: one position after the other, one
+   * launch. Either gives the same codes up to fp32 summation order. */
+  int pair;
 } sk_cp_desc;
 
-/* All positions of the code predictor of one frame in ONE launch (the persistent kernel of sk_talker_frames in
- * its code-predictor mode): greedy sub-codes 1..n_positions-1. Supports the Qwen3-TTS code predictor shape:
+/* Bytes of workspace sk_cp_frame needs: sk_talker_workspace_size plus, for pair = 1, the second row's cells. */
+int64_t sk_cp_workspace_size(int hidden, int inter, int pair);
+
+/* All positions of the code predictor of one frame in ONE launch, or two with desc->pair (the paired pass of
+ * positions 0 and 1, then the rest), of the persistent kernel of sk_talker_frames in its code-predictor mode:
+ * greedy sub-codes 1..n_positions-1. Supports the Qwen3-TTS code predictor shape:
  * hidden 1024, intermediate 3072, 16 q / 8 kv heads, vocab 2048, i8row weights, bf16 cache, a 256-CU device.
  * Replaces, for greedy sub-codes, the code-predictor loop of Qwen3Kernels._frame (qwen3/kernels.py:666-675) with
  * _cp_first / _cp_input (qwen3/kernels.py:629-655), _layers (619-627), rms_gemv over cp_heads[g - 1] and sample
- * (qwen3/sampler.py:37-159 with do_sample = 0, no processor). Positions 0 and 1 run one after the other (the
- * reference can pair them, qwen3/kernels.py:600-617, with the same result). */
+ * (qwen3/sampler.py:37-159 with do_sample = 0, no processor). Positions 0 and 1 run one after the other, or as one
+ * paired pass (desc->pair: _cp_first with cp_pair, qwen3/kernels.py:641-646, and _cp_layers_pair, 600-617, whose
+ * rms_gemv2 / gemv2 read each weight once for both rows, qwen3/kernels.py:276-310). */
 int sk_cp_frame(const sk_cp_desc* desc, void* stream);
 
 

@@ -68,7 +68,7 @@ class SkCpDesc(ctypes.Structure):
                 ("emb0_rows", c_int), ("emb", c_void_p), ("head_w", c_void_p), ("head_s", c_void_p),
                 ("codes", c_void_p), ("logits", c_void_p), ("layer_out", c_void_p), ("workspace", c_void_p),
                 ("workspace_bytes", c_int64), ("do_sample", c_int), ("inv_temp", c_float), ("top_k", c_int),
-                ("seed", c_void_p), ("counter", c_void_p), ("keep_layers", c_int)]
+                ("seed", c_void_p), ("counter", c_void_p), ("keep_layers", c_int), ("pair", c_int)]
 
 
 class SkBatchDesc(ctypes.Structure):
@@ -93,6 +93,7 @@ _SIGS["sk_batch_frame"] = (c_int, [ctypes.POINTER(SkBatchDesc), _P])
 _SIGS["sk_talker_workspace_size"] = (c_int64, [c_int, c_int])
 _SIGS["sk_talker_frames"] = (c_int, [ctypes.POINTER(SkTalkerDesc), c_int, _P])
 _SIGS["sk_cp_frame"] = (c_int, [ctypes.POINTER(SkCpDesc), _P])
+_SIGS["sk_cp_workspace_size"] = (c_int64, [c_int, c_int, c_int])
 
 _lib = None
 

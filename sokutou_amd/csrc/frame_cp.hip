@@ -1,7 +1,16 @@
-// Entry point of the persistent kernel in code-predictor mode (sk_cp_frame); the kernel itself is in
-// frame_impl.h. A translation unit of its own: the code predictor's instantiations do not share one with the
-// talker's, so changes to either mode leave the other's generated code alone.
+// Entry point of the persistent kernel in code-predictor mode (sk_cp_frame, sk_cp_workspace_size); the kernel
+// itself is in frame_impl.h. With desc->pair, launch_frames runs the paired pass of positions 0 and 1 as a launch
+// of its own (k_frames with PAIRK) before the launch of the other positions. A translation unit of its own: the
+// code predictor's instantiations do not share one with the talker's, so changes to either mode leave the other's
+// generated code alone.
 #include "frame_impl.h"
+
+extern "C" int64_t sk_cp_workspace_size(int hidden, int inter, int pair) {
+  if (hidden <= 0 || inter <= 0) return 0;
+  const int64_t base = sk_talker_workspace_size(hidden, inter);
+  const int64_t paired = (int64_t)Ws::kCells + (int64_t)PairLayout(hidden, inter).total * 8;
+  return pair && paired > base ? paired : base;
+}
 
 extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
   if (!d) return sk_set_error(SK_EINVAL, "sk_cp_frame: bad arguments");
@@ -14,7 +23,7 @@ extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
   if (!d->layers || !d->norm || !d->rope || !d->x0 || !d->id0 || !d->emb || !d->head_w || !d->head_s || !d->codes ||
       !d->workspace || d->emb0_rows <= 0)
     return sk_set_error(SK_EINVAL, "sk_cp_frame: null pointer");
-  if (d->workspace_bytes < sk_talker_workspace_size(d->hidden, d->inter))
+  if (d->workspace_bytes < sk_cp_workspace_size(d->hidden, d->inter, d->pair))
     return sk_set_error(SK_EWORKSPACE, "sk_cp_frame: workspace too small");
   if (d->do_sample && (!d->seed || !d->counter || !(d->inv_temp > 0.f)))
     return sk_set_error(SK_EINVAL, "sk_cp_frame: sampling needs seed, counter and inv_temp > 0");
@@ -25,7 +34,8 @@ extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
   t.out = d->codes; t.rep_pen = 1.f; t.eos = -1; t.talker_processor = 0;
   t.logits = d->logits; t.layer_out = d->layer_out; t.workspace = d->workspace; t.workspace_bytes = d->workspace_bytes;
   t.do_sample = d->do_sample; t.inv_temp = d->inv_temp; t.top_k = d->top_k; t.seed = d->seed; t.counter = d->counter;
-  const CpArgs cp{d->x0, d->emb, d->head_w, d->head_s, d->emb0_rows};
+  // pairing needs a position 1 to pair with (n_positions >= 2, checked above)
+  const CpArgs cp{d->x0, d->emb, d->head_w, d->head_s, d->emb0_rows, d->pair ? 1 : 0};
   if (d->keep_layers) return launch_frames<1024, 3072, 4, 2048, true, SK_WD_I8ROW, true>(&t, cp, d->n_positions, (hipStream_t)stream);
   return launch_frames<1024, 3072, 4, 2048, true>(&t, cp, d->n_positions, (hipStream_t)stream);
 }

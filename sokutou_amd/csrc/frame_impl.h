@@ -211,6 +211,34 @@ struct Lds {
   uint32_t pubseq;  // stage publications completed by the compute waves
 };
 
+// The second row of the code predictor's paired first pass (positions 0 and 1 together): its residuals, staged
+// GEMV inputs, q|k|v and attention vectors. Placed after Lds in the code-predictor kernels' LDS only.
+template <int H, int I>
+struct LdsPair {
+  static constexpr int XS = I > kQ ? I : kQ;
+  float hin[H], hmid[H];
+  float xs[2][XS];
+  float qkv[512];
+  float qs[2][SK_HD];
+  float kn[SK_HD], vn[SK_HD];
+  float red[8];
+  float inv;
+  int bad;  // a compute wave's poll of the second row failed (cleared at the start of the pass)
+};
+// Cells of the paired pass's second row, after the trace stamps of the workspace: q|k|v [8][512], attention output
+// [2048], h after o [H], activation [I], h after down [H] (the first row uses the regular regions).
+struct PairLayout {
+  uint32_t b1, b3, b4, b5, b6, total;
+  __host__ __device__ PairLayout(int H, int I) {
+    b1 = Layout(H, I).total + (uint32_t)kWG * 2u * Ws::kTraceLayers * Ws::kTraceEvents;
+    b3 = b1 + kNKV * 512;
+    b4 = b3 + kQ;
+    b5 = b4 + H;
+    b6 = b5 + I;
+    total = b6 + H;
+  }
+};
+
 // Records a timeout: error code, then frame and layer of the stage that gave up (diagnostic words of the workspace).
 struct Ctx;
 __device__ void fail(const Ctx& c, uint32_t code, int f, int l);
@@ -349,7 +377,7 @@ __device__ __forceinline__ void load_rows(uint4 (&w)[RW][C], uint16_t (&s)[RW], 
 #pragma unroll
       for (int c = 0; c < C; c++)
         w[r][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(W)),
-                                                                                  (uint32_t)lane * 16u + 1024u * c, so, kNT));
+                                                                                  (uint32_t)lane * 16u + 1024u * c, so, KEEP ? 0 : kNT));
       s[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), 0, __builtin_amdgcn_readfirstlane((uint32_t)row * 2u), 0);
       continue;
     }
@@ -388,6 +416,48 @@ __device__ __forceinline__ void dot_rows(const uint4 (&w)[RW][C], const float* x
   }
 #pragma unroll
   for (int r = 0; r < RW; r++) y[r] = wave_sum(acc[r]);
+}
+
+// Two GEMV inputs against the same rows (the code predictor's paired pass): each weight byte is converted once and
+// multiplied with both inputs, as dot_rows does for one. The inputs are read one quarter chunk ahead of their use,
+// with a scheduling barrier after each quarter: left free, the scheduler issues every LDS read of the dot first and
+// holds all of them in registers (96 for the down rows), and the pass spills.
+template <int RW, int C>
+__device__ __forceinline__ void dot_rows2(const uint4 (&w)[RW][C], const float* xa, const float* xb, int lane,
+                                          float (&ya)[RW], float (&yb)[RW]) {
+  float aa[RW], ab[RW];
+#pragma unroll
+  for (int r = 0; r < RW; r++) { aa[r] = 0.f; ab[r] = 0.f; }
+  const float2* xa2 = (const float2*)xa;
+  const float2* xb2 = (const float2*)xb;
+  float2 na0 = xa2[2 * lane], na1 = xa2[2 * lane + 1], nb0 = xb2[2 * lane], nb1 = xb2[2 * lane + 1];
+#pragma unroll
+  for (int t = 0; t < 4 * C; t++) {  // quarter t: chunk t / 4, bytes 4 (t % 4) .. + 3 of each row's chunk
+    const float2 a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
+    if (t + 1 < 4 * C) {
+      const int k = 2 * ((t + 1) * 64 + lane);
+      na0 = xa2[k]; na1 = xa2[k + 1]; nb0 = xb2[k]; nb1 = xb2[k + 1];
+    }
+    const int c = t >> 2, j = t & 3;
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+      const uint32_t q = j == 0 ? w[r][c].x : j == 1 ? w[r][c].y : j == 2 ? w[r][c].z : w[r][c].w;
+      const float w0 = (float)(int8_t)q, w1 = (float)(int8_t)(q >> 8), w2 = (float)(int8_t)(q >> 16),
+                  w3 = (float)(int8_t)(q >> 24);
+      float t0 = w0 * a0.x, u = w0 * b0.x;
+      t0 = __builtin_fmaf(w1, a0.y, t0);
+      u = __builtin_fmaf(w1, b0.y, u);
+      t0 = __builtin_fmaf(w2, a1.x, t0);
+      u = __builtin_fmaf(w2, b1.x, u);
+      t0 = __builtin_fmaf(w3, a1.y, t0);
+      u = __builtin_fmaf(w3, b1.y, u);
+      aa[r] += t0;
+      ab[r] += u;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; r++) { ya[r] = wave_sum(aa[r]); yb[r] = wave_sum(ab[r]); }
 }
 
 // i8g32 weights (the reference's format: one fp16 scale per 32 weights of a row, applied per 16-weight chunk,
@@ -489,6 +559,22 @@ __device__ __forceinline__ void publish(L& S, void* cells, uint32_t idx0, int n,
         if (2 * lane + 128 * k < n) put2l(cells, idx0 + 128u * k, lane, S.pub[2 * lane + 128 * k], S.pub[2 * lane + 128 * k + 1], e);
     } else {
       for (int i = 2 * lane; i < n; i += 128) put2(cells, idx0 + i, S.pub[i], S.pub[i + 1], e);
+    }
+    if (lane == 0) __hip_atomic_store(&S.pubseq, (old + 1) / W, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+}
+
+// publish for the paired pass: S.pub holds the first row's n values, then the second row's; the last wave to arrive
+// writes them to cells [idxA, idxA + n) and [idxB, idxB + n). One publication (one pubseq step) for both rows.
+template <int W, class L>
+__device__ __forceinline__ void publish_pair(L& S, void* cells, uint32_t idxA, uint32_t idxB, int n, uint32_t e, int lane) {
+  uint32_t old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(&S.pubcnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+  old = __builtin_amdgcn_readfirstlane(old);
+  if (old % W == W - 1) {
+    for (int i = 2 * lane; i < n; i += 128) {
+      put2(cells, idxA + i, S.pub[i], S.pub[i + 1], e);
+      put2(cells, idxB + i, S.pub[n + i], S.pub[n + i + 1], e);
     }
     if (lane == 0) __hip_atomic_store(&S.pubseq, (old + 1) / W, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
@@ -831,6 +917,7 @@ struct CpArgs {
   const void* const* head_w;  // [n_positions] int8 heads; [0] unused
   const void* const* head_s;  // [n_positions] bf16 row scales
   int emb0_rows;              // rows of emb[1] (the range code 0 must lie in)
+  int pair;                   // positions 0 and 1 in one pass (two rows per stage)
 };
 
 // Everything a role function needs about this workgroup and launch.
@@ -882,6 +969,78 @@ __device__ __forceinline__ int attn_barriers(const Ck& ck) { return 1 + (ck.n > 
 // ================================================================================================================
 // Control wave
 // ================================================================================================================
+// Control wave of the code predictor's paired first pass (positions 0 and 1 as two rows per stage, the
+// reference's cp_pair: qwen3/kernels.py:276-310, 600-617). The control wave polls and stages the first row's inputs
+// as in a regular frame; the compute waves poll the second row's from PairLayout's cells at the same time (two
+// polls in parallel instead of one after the other), and compute both rows' attention (two barriers). Returns
+// false when a poll of either row failed (P.bad, or the stage flags for the compute waves).
+template <int H, int I, int W, int V, bool CP>
+__device__ __forceinline__ bool ctl_pair_pass(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
+  constexpr int kNP = H / 128;
+  constexpr bool kLO = true;  // lane offsets, as the compute waves of the pass use them
+  static_assert(W == 4, "the paired pass stages its inputs from registers");
+  const Layout LY(H, I);
+  LdsPair<H, I>& P = *(LdsPair<H, I>*)((char*)&S + sizeof(Lds<H, I, W, V, CP>));
+  const float eps = c.d.eps;
+  const int f = 0;
+  for (int l = 0; l < c.L; l++) {
+    const sk_layer_desc& Ly = S.desc[l];
+    bool ok = true;
+    float ss;
+    {
+      // S1 input: position 0's vector (layer 0), else the residual, times the input norm
+      float2 w[kNP], v[kNP];
+      load_pairs<kNP>(Ly.in_norm, w, lane);
+      if (l == 0) {
+        load_pairs<kNP>(c.cp.x0, v, lane);
+      } else {
+        after_publish(S, (uint32_t)l * 4u, c.dl[Ws::kHopS1]);
+        u32x4 q[kNP];
+        ok = poll_regs<kNP, kLO>(c.cells, LY.e6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
+        cells_to_pairs<kNP>(q, v);
+      }
+      ss = stage_rms<kNP>(v, w, S.hin, S.xs[0], lane);
+    }
+    if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[0] = !ok; }
+    wg_sync();
+    if (!ok || P.bad) return false;
+    // S2 input: q|k|v of this workgroup's head
+    after_publish(S, (uint32_t)l * 4u + 1u, c.dl[Ws::kHopS2]);
+    ok = poll_cells<mb(512), false, kLO>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
+    if (lane == 0) S.flags[1] = !ok;
+    wg_sync();
+    if (!ok || P.bad) return false;
+    wg_sync();  // paired attention: vectors ready
+    wg_sync();  // paired attention: scores of the second row
+    // S4 input: the attention output, written whole by the workgroups themselves
+    sleep_units(c.dl[Ws::kHopS4]);
+    ok = poll_cells<mb(kQ), true, kLO>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
+    if (lane == 0) S.flags[2] = !ok;
+    wg_sync();
+    if (!ok || P.bad) return false;
+    {
+      // S5 input: the residual after o, times the post-attention norm
+      float2 w[kNP], v[kNP];
+      load_pairs<kNP>(Ly.post_norm, w, lane);
+      after_publish(S, (uint32_t)l * 4u + 2u, c.dl[Ws::kHopS5]);
+      u32x4 q[kNP];
+      ok = poll_regs<kNP, kLO>(c.cells, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
+      cells_to_pairs<kNP>(q, v);
+      ss = stage_rms<kNP>(v, w, S.hmid, S.xs[0], lane);
+    }
+    if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[3] = !ok; }
+    wg_sync();
+    if (!ok || P.bad) return false;
+    // S6 input: the SwiGLU activation
+    after_publish(S, (uint32_t)l * 4u + 3u, c.dl[Ws::kHopS6]);
+    ok = poll_cells<mbh(I, W), true, kLO>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+    if (lane == 0) S.flags[4] = !ok;
+    wg_sync();
+    if (!ok || P.bad) return false;
+  }
+  return true;
+}
+
 template <int H, int I, int W, int V, bool CP, bool SMP>
 __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
   // 4 compute waves (256 registers for the control wave): the RMSNorm inputs are polled into registers and staged
@@ -894,10 +1053,15 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
   const bf16_t* emb = (const bf16_t*)c.d.emb;
   int64_t tok = gload(c.d.id0);
   if (CP && c.g == 0 && lane == 0 && c.d.out) gstore(c.d.out, tok);  // code 0 passes through
-  for (int f = 0; f < c.n_frames; f++) {
+  // After the code predictor's paired pass (positions 0 and 1, a launch of its own: k_frames with PAIRK) frame 1
+  // runs only its head, from the pass's second row, and the stage publications of this launch start at frame 2
+  // (fq counts the frames with layers before this one).
+  const bool pr = CP && c.cp.pair;
+  for (int f = pr ? 1 : 0; f < c.n_frames; f++) {
     const int pos = c.pos0 + f;
     const auto ck = make_chunk<CP>(pos, c.r, Cfg<H, I, W, V, CP>::whole(pos));
-    for (int l = 0; l < c.L; l++) {
+    const int fq = pr ? f - 2 : f;
+    for (int l = 0; l < (pr && f == 1 ? 0 : c.L); l++) {
       const sk_layer_desc& Ly = S.desc[l];
       bool ok = true;
       float ss = 0.f;
@@ -939,7 +1103,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
             }
           }
         } else {
-          after_publish(S, (uint32_t)(f * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
+          after_publish(S, (uint32_t)(fq * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
           u32x4 q[kNP];
           ok = poll_regs<kNP, kLO>(c.cells, LY.e6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
           cells_to_pairs<kNP>(q, v);
@@ -978,7 +1142,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 #pragma unroll
         for (int k = 0; k < H / 64; k++) S.hin[lane + 64 * k] = ev[k];
       } else {
-        after_publish(S, (uint32_t)(f * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
+        after_publish(S, (uint32_t)(fq * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
         ok = poll_cells<mb(H), false, kLO>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
       }
       for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
@@ -990,7 +1154,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       wg_sync();
       if (!ok) return;
       // S2 input: this head's q/k/v
-      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 1u, c.dl[Ws::kHopS2]);
+      after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 1u, c.dl[Ws::kHopS2]);
       ok = poll_cells<mb(512), false, kLO>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
       if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
@@ -1115,7 +1279,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if constexpr (kRegRms) {
         float2 w[kNP], v[kNP];
         load_pairs<kNP>(Ly.post_norm, w, lane);
-        after_publish(S, (uint32_t)(f * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
+        after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
         u32x4 q[kNP];
         ok = poll_regs<kNP, kLO>(c.cells, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
         cells_to_pairs<kNP>(q, v);
@@ -1124,7 +1288,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       float npost[H / 64];
 #pragma unroll
       for (int k = 0; k < H / 64; k++) npost[k] = gload(Ly.post_norm + lane + 64 * k);
-      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
+      after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
       ok = poll_cells<mb(H), false, kLO>(c.cells, LY.e4, H, c.tick(f, l, 3), S.hmid, c.ws, lane, c, 15u, f, l);
       ss = 0.f;
       for (int i = lane; i < H; i += 64) { const float v = S.hmid[i]; ss += v * v; }
@@ -1136,7 +1300,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       wg_sync();
       if (!ok) return;
       // S6 input: the whole SwiGLU activation
-      after_publish(S, (uint32_t)(f * c.L + l) * 4u + 3u, c.dl[Ws::kHopS6]);
+      after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 3u, c.dl[Ws::kHopS6]);
       ok = poll_cells<mbh(I, W), true, kLO>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
       if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
       wg_sync();
@@ -1149,9 +1313,12 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     if constexpr (kRegRms) {
       float2 w[kNP], v[kNP];
       load_pairs<kNP>(c.d.norm, w, lane);
-      after_publish(S, (uint32_t)((f + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
+      after_publish(S, (uint32_t)((fq + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
       u32x4 q[kNP];
-      ok = poll_regs<kNP, kLO>(c.cells, LY.e6, c.tick(f, c.L - 1, 5), q, c.ws, lane, c, 17u, f, c.L);
+      // the head of frame 1 after a paired pass reads the pass's second row
+      const bool hb = pr && f == 1;
+      ok = poll_regs<kNP, kLO>(c.cells, hb ? PairLayout(H, I).b6 : LY.e6, c.tick(hb ? 0 : f, c.L - 1, 5), q, c.ws, lane, c,
+                               17u, f, c.L);
       cells_to_pairs<kNP>(q, v);
       ss = stage_rms<kNP>(v, w, S.hin, S.xs[0], lane);
       if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[5] = !ok; }
@@ -1168,8 +1335,10 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     float nfin[H / 64];
 #pragma unroll
     for (int k = 0; k < H / 64; k++) nfin[k] = gload(c.d.norm + lane + 64 * k);
-    after_publish(S, (uint32_t)((f + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
-    ok = poll_cells<mb(H), false, kLO>(c.cells, LY.e6, H, c.tick(f, c.L - 1, 5), S.hin, c.ws, lane, c, 17u, f, c.L);
+    after_publish(S, (uint32_t)((fq + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
+    const bool hb = pr && f == 1;
+    ok = poll_cells<mb(H), false, kLO>(c.cells, hb ? PairLayout(H, I).b6 : LY.e6, H, c.tick(hb ? 0 : f, c.L - 1, 5), S.hin,
+                                       c.ws, lane, c, 17u, f, c.L);
     for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
     ss = wave_sum(ss);
 #pragma unroll
@@ -1263,6 +1432,251 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 // ================================================================================================================
 // Compute waves
 // ================================================================================================================
+// Compute waves of the code predictor's paired first pass (positions 0 and 1 as two rows per stage;
+// ctl_pair_pass is the control wave's side), run before the frame loop and before run_compute sets up its own
+// state (weights, rows, RoPE): nothing of this pass stays live into the loop, whose registers are then allocated
+// as without it. The layer weights in registers serve both rows' dots, and the attention covers the two new
+// positions (the first row attends to position 0 alone, the second to both). The compute waves also poll and stage
+// the second row's inputs while the control wave polls the first row's: wave 3 the residuals (with their RMSNorm),
+// wave 2 the q|k|v, waves 0-1 the attention output and waves 0-2 the activation, 1024 cells each. Frame 1 then
+// runs only its head. Returns false when a poll failed.
+template <int H, int I, int W, int V, bool CP, int WD, bool KEEP>
+__device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
+  using C = Cfg<H, I, W, V, CP>;
+  // lane offsets for every cell and weight access: per-load vector addresses, hoisted out of the layer loop by the
+  // compiler, held ~100 registers through the pass and made it spill
+  constexpr bool kLO = true;
+  constexpr int kNP = H / 128;
+  static_assert(!C::kLate && !C::kSpread, "the paired pass prefetches a whole layer ahead");
+  static_assert(WD == SK_WD_I8ROW, "the code predictor reads i8row weights");
+  static_assert(2 * 16 <= 64 && 2 * C::R_O <= 64 && C::R_GU <= 64 && 2 * C::R_D <= 64, "both rows fit S.pub");
+  static_assert(kQ % 1024 == 0 && I % 1024 == 0 && kQ / 1024 <= W && I / 1024 <= W && W == 4,
+                "the second row's polls: 1024-cell blocks, one per compute wave");
+  const Layout LY(H, I);
+  const PairLayout PL(H, I);
+  LdsPair<H, I>& P = *(LdsPair<H, I>*)((char*)&S + sizeof(Lds<H, I, W, V, CP>));
+  const float eps = c.d.eps;
+  const int x = (int)c.x, r = c.r, g = c.g;
+  const int f = 0;
+  // this wave's rows in every stage, as run_compute assigns them
+  const int qkv_row0 = r < 16 ? 256 * x + 16 * r : r < 24 ? kQ + 128 * x + 16 * (r - 16) : kQ + kNKV * 128 + 128 * x + 16 * (r - 24);
+  const int q_w0 = qkv_row0 + C::RW_QKV * cw;
+  const int o_w0 = C::R_O * g + C::RW_O * cw, o_wn = max(0, min(C::RW_O, C::R_O - C::RW_O * cw));
+  const int gu_w0 = C::R_GU * g + C::RW_GU * cw;
+  const int d_w0 = C::R_D * g + C::RW_D * cw, d_wn = max(0, min(C::RW_D, C::R_D - C::RW_D * cw));
+  static_assert(C::RW_O * W == C::R_O && C::RW_D * W == C::R_D, "every wave has rows of o and down");
+  const int p = tid >> 7, dd = tid & 127;  // the attention's head and dim of this thread
+  uint4 wq[C::RW_QKV][C::CH], wo[C::RW_O][C::CQ], wg[C::RW_GU][C::CH], wd[C::RW_D][C::CI];
+  uint16_t sq[C::RW_QKV], so[C::RW_O], sg[C::RW_GU], sd[C::RW_D];
+  uint16_t gq[1][1], go[1][1], gg[1][1], gd[1][1];  // unused (no group scales)
+  float a_cs, a_sn, a_n0, a_n1;  // RoPE of position 0 and the q / k norm weights of this wave's vector
+  auto load_attn_vec = [&](const sk_layer_desc& Lx) {
+    const float* nw = (cw & 3) == 2 ? Lx.kn : Lx.qn;
+    a_cs = gload(c.d.rope + (size_t)c.pos0 * SK_HD + lane);
+    a_sn = gload(c.d.rope + (size_t)c.pos0 * SK_HD + 64 + lane);
+    a_n0 = gload(nw + lane);
+    a_n1 = gload(nw + 64 + lane);
+  };
+  if (cw == 0 && lane == 0) P.bad = 0;
+  // the second row's RMSNorm input from registers: P.hin / P.hmid, P.xs[0] and P.inv, as the control wave stages
+  // the first row's
+  auto stage_b = [&](const float2 (&v)[kNP], const float* nw, float* res) {
+    float2 w[kNP];
+    load_pairs<kNP>(nw, w, lane);
+    const float ss = stage_rms<kNP>(v, w, res, P.xs[0], lane);
+    if (lane == 0) P.inv = rsqrtf(ss / H + eps);
+  };
+  {
+    const sk_layer_desc& L0 = S.desc[0];
+    load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
+    load_attn_vec(L0);
+    load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  for (int l = 0; l < c.L; l++) {
+    const sk_layer_desc& Ly = S.desc[l];
+    // the next layer's weights are prefetched unconditionally (after the last layer the frame loop's prologue
+    // loads frame 2's)
+    const sk_layer_desc& Ln = S.desc[l == c.L - 1 ? 0 : l + 1];
+    if (cw == 3) {  // the second row's S1 input: the talker embedding row of code 0 (layer 0), else its residual
+      float2 v[kNP];
+      if (l == 0) {
+        const bf16_t* tab = (const bf16_t*)uniform(gload(c.cp.emb + 1));
+        const int64_t tok = gload(c.d.id0);
+#pragma unroll
+        for (int b = 0; b < kNP; b++) {
+          const uint32_t u = gload((const uint32_t*)(tab + (size_t)tok * H) + lane + 64 * b);
+          v[b] = make_float2(bf2f(u & 0xffffu), bf2f(u >> 16));
+        }
+      } else {
+        sleep_units(c.dl[Ws::kHopS1]);
+        u32x4 q[kNP];
+        const bool ok = poll_regs<kNP, kLO>(c.cells, PL.b6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
+        if (!ok && lane == 0) P.bad = 1;
+        cells_to_pairs<kNP>(q, v);
+      }
+      stage_b(v, Ly.in_norm, P.hin);
+    }
+    // ---- S1: qkv rows of both positions
+    wg_sync();
+    if (S.flags[0] || P.bad) return false;
+    {
+      float ya[C::RW_QKV], yb[C::RW_QKV];
+      dot_rows2<C::RW_QKV, C::CH>(wq, S.xs[0], P.xs[0], lane, ya, yb);
+      const float ia = S.inv, ib = P.inv;
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < C::RW_QKV; i++) {
+          S.pub[C::RW_QKV * cw + i] = ya[i] * row_scale_of<WD>(sq[i]) * ia;
+          S.pub[16 + C::RW_QKV * cw + i] = yb[i] * row_scale_of<WD>(sq[i]) * ib;
+        }
+      }
+      publish_pair<W>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, PL.b1 + (uint32_t)x * 512 + 16 * r, 16,
+                      c.tick(f, l, 0), lane);
+      if (cw == 2) {  // the second row's S2 input
+        sleep_units(c.dl[Ws::kHopS2]);
+        const bool ok = poll_cells<mb(512), false, kLO>(c.cells, PL.b1 + (uint32_t)x * 512, 512, c.tick(f, l, 0), P.qkv,
+                                                        c.ws, lane, c, 12u, f, l);
+        if (!ok && lane == 0) P.bad = 1;
+      }
+      load_w<WD, C::RW_GU, C::CH, kLO, KEEP>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+    }
+    // ---- S2: attention of both positions over positions 0 and 1
+    wg_sync();
+    if (S.flags[1] || P.bad) return false;
+    {
+      // (1) wave vw normalises and rotates vector vw (q0, q1, k, v) of both rows; workgroup 0 of the head
+      // appends both K/V rows
+      const int vw = cw & 3;
+      const float b_cs = gload(c.d.rope + (size_t)(c.pos0 + 1) * SK_HD + lane);
+      const float b_sn = gload(c.d.rope + (size_t)(c.pos0 + 1) * SK_HD + 64 + lane);
+#pragma unroll
+      for (int row = 0; row < 2; row++) {
+        const float* src = row ? P.qkv : S.qkv;
+        const float cs = row ? b_cs : a_cs, sn = row ? b_sn : a_sn;
+        const float x0 = src[vw * SK_HD + lane], x1 = src[vw * SK_HD + 64 + lane];
+        const float inv = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / SK_HD + eps);
+        const float n0 = x0 * inv * a_n0, n1 = x1 * inv * a_n1;
+        const float r0 = n0 * cs - n1 * sn, r1 = n1 * cs + n0 * sn;  // rotate-half RoPE
+        if (cw < 2) {
+          float* qd = row ? P.qs[cw] : S.qs[cw];
+          qd[lane] = r0 * kInvSqrtHd;
+          qd[lane + 64] = r1 * kInvSqrtHd;
+        } else if (cw < 4) {
+          const float y0 = bf2f(f2bf(cw == 2 ? r0 : x0)), y1 = bf2f(f2bf(cw == 2 ? r1 : x1));
+          float* dst = cw == 2 ? (row ? P.kn : S.kn) : (row ? P.vn : S.vn);
+          dst[lane] = y0;
+          dst[lane + 64] = y1;
+          if (r == 0) {
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(uniform(cw == 2 ? c.kh(Ly) : c.vh(Ly)));
+            const uint32_t off = (uint32_t)((c.pos0 + row) * SK_HD + lane) * 2u;
+            __builtin_amdgcn_raw_buffer_store_b16(f2bf(y0), rs, off, 0, kPolDev);
+            __builtin_amdgcn_raw_buffer_store_b16(f2bf(y1), rs, off + 128u, 0, kPolDev);
+          }
+        }
+      }
+      wg_sync();  // paired barrier 1
+      // (2) the second row's scores at positions 0 and 1: head p's q . k over the head's two waves
+      {
+        const float qb = P.qs[p][dd];
+        const float s0 = wave_sum(qb * S.kn[dd]), s1 = wave_sum(qb * P.kn[dd]);
+        if (lane == 0) { P.red[2 * cw] = s0; P.red[2 * cw + 1] = s1; }
+      }
+      wg_sync();  // paired barrier 2
+      {
+        // waves 2p and 2p + 1 hold head p; the first row's output is v at position 0 (weight 1)
+        const float s0 = P.red[4 * p] + P.red[4 * p + 2], s1 = P.red[4 * p + 1] + P.red[4 * p + 3];
+        const float m = fmaxf(s0, s1), e0 = expf(s0 - m), e1 = expf(s1 - m);
+        const float oa = S.vn[dd], ob = (e0 * S.vn[dd] + e1 * P.vn[dd]) / (e0 + e1);
+        // this workgroup's slice of the S4 inputs (q head 2x + r/16, dims 8 (r % 16) .. + 8), as the whole-cache
+        // attention writes it
+        if (p == (r >> 4) && (dd >> 3) == (r & 15)) {
+          put(c.cells, LY.e3 + (2 * x + p) * SK_HD + dd, oa, c.tick(f, l, 2));
+          put(c.cells, PL.b3 + (2 * x + p) * SK_HD + dd, ob, c.tick(f, l, 2));
+        }
+      }
+      if (cw < kQ / 1024) {  // the second row's S4 input, 1024 cells per wave (swizzle blocks are 1024 long)
+        sleep_units(c.dl[Ws::kHopS4]);
+        const bool ok = poll_cells<mb(1024), true, kLO>(c.cells, PL.b3 + 1024u * cw, 1024, c.tick(f, l, 2),
+                                                        P.xs[1] + 1024 * cw, c.ws, lane, c, 14u, f, l);
+        if (!ok && lane == 0) P.bad = 1;
+      }
+      load_attn_vec(Ln);
+    }
+    // ---- S4: o rows of both positions, added to their residuals
+    wg_sync();
+    if (S.flags[2] || P.bad) return false;
+    {
+      float ya[C::RW_O], yb[C::RW_O];
+      dot_rows2<C::RW_O, C::CQ>(wo, S.xs[1], P.xs[1], lane, ya, yb);
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < C::RW_O; i++)
+          if (i < o_wn) {
+            S.pub[C::RW_O * cw + i] = S.hin[o_w0 + i] + ya[i] * row_scale_of<WD>(so[i]);
+            S.pub[C::R_O + C::RW_O * cw + i] = P.hin[o_w0 + i] + yb[i] * row_scale_of<WD>(so[i]);
+          }
+      }
+      publish_pair<W>(S, c.cells, LY.e4 + C::R_O * g, PL.b4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
+      if (cw == 3) {  // the second row's S5 input: its residual after o, times the post-attention norm
+        sleep_units(c.dl[Ws::kHopS5]);
+        u32x4 q[kNP];
+        float2 v[kNP];
+        const bool ok = poll_regs<kNP, kLO>(c.cells, PL.b4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
+        if (!ok && lane == 0) P.bad = 1;
+        cells_to_pairs<kNP>(q, v);
+        stage_b(v, Ly.post_norm, P.hmid);
+      }
+      load_w<WD, C::RW_D, C::CI, kLO, KEEP>(wd, sd, gd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
+    }
+    // ---- S5: gate/up rows of both positions, SwiGLU
+    wg_sync();
+    if (S.flags[3] || P.bad) return false;
+    {
+      float ya[C::RW_GU], yb[C::RW_GU];
+      dot_rows2<C::RW_GU, C::CH>(wg, S.xs[0], P.xs[0], lane, ya, yb);
+      const float ia = S.inv, ib = P.inv;
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < C::RW_GU; i += 2) {
+          S.pub[(C::RW_GU * cw + i) / 2] = silu_mul(ya[i] * row_scale_of<WD>(sg[i]) * ia, ya[i + 1] * row_scale_of<WD>(sg[i + 1]) * ia);
+          S.pub[C::R_GU / 2 + (C::RW_GU * cw + i) / 2] =
+              silu_mul(yb[i] * row_scale_of<WD>(sg[i]) * ib, yb[i + 1] * row_scale_of<WD>(sg[i + 1]) * ib);
+        }
+      }
+      publish_pair<W>(S, c.cells, LY.e5 + C::R_GU / 2 * g, PL.b5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
+      if (cw < I / 1024) {  // the second row's S6 input, 1024 cells per wave
+        sleep_units(c.dl[Ws::kHopS6]);
+        const bool ok = poll_cells<mb(1024), true, kLO>(c.cells, PL.b5 + 1024u * cw, 1024, c.tick(f, l, 4),
+                                                        P.xs[1] + 1024 * cw, c.ws, lane, c, 16u, f, l);
+        if (!ok && lane == 0) P.bad = 1;
+      }
+      load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+    }
+    // ---- S6: down rows of both positions, added to their residuals after o
+    wg_sync();
+    if (S.flags[4] || P.bad) return false;
+    {
+      float ya[C::RW_D], yb[C::RW_D];
+      dot_rows2<C::RW_D, C::CI>(wd, S.xs[1], P.xs[1], lane, ya, yb);
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < C::RW_D; i++) {
+          if (i < d_wn) {
+            const float hb = P.hmid[d_w0 + i] + yb[i] * row_scale_of<WD>(sd[i]);
+            S.pub[C::RW_D * cw + i] = S.hmid[d_w0 + i] + ya[i] * row_scale_of<WD>(sd[i]);
+            S.pub[C::R_D + C::RW_D * cw + i] = hb;
+            if (c.d.layer_out && c.n_frames == 2) gstore(c.d.layer_out + (size_t)l * H + d_w0 + i, hb);
+          }
+        }
+      }
+      publish_pair<W>(S, c.cells, LY.e6 + C::R_D * g, PL.b6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
+      load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
+    }
+  }
+  return true;
+}
+
 template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP>
 __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
   using C = Cfg<H, I, W, V, CP>;
@@ -1307,11 +1721,14 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
     a_n0 = gload(nw + lane);
     a_n1 = gload(nw + 64 + lane);
   };
+  const int f0 = CP && c.cp.pair ? 1 : 0;  // the frame loop's first frame: 1 after the paired pass (its own launch)
+  // the first frame with layers: 0, or 2 after a paired pass (position 2 < max_len when there is a frame 2)
+  const int p0 = c.pos0 + (f0 && c.n_frames > 2 ? 2 : 0);
   {
     const sk_layer_desc& L0 = S.desc[0];
     load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
-    load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), make_chunk<CP>(c.pos0, r, C::whole(c.pos0)), cw, ag, asl);
-    load_attn_vec(L0, c.pos0);
+    load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), make_chunk<CP>(p0, r, C::whole(p0)), cw, ag, asl);
+    load_attn_vec(L0, p0);
     if constexpr (!C::kLate) {
       load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
       load_w<WD, C::RW_GU, C::CH, kLO, KEEP>(wg, sg, gg, (const int8_t*)L0.gu_w, L0.gu_s, gu_w0, C::RW_GU, H, lane);
@@ -1323,10 +1740,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   // Wait once for the first layer's loads. The compiler places one static wait count per use; without this it
   // would have to allow for the prologue's own load order on every layer, and waits would come out shallow.
   __builtin_amdgcn_s_waitcnt(0);
-  for (int f = 0; f < c.n_frames; f++) {
+  for (int f = f0; f < c.n_frames; f++) {
     const int pos = c.pos0 + f;
     const auto ck = make_chunk<CP>(pos, r, C::whole(pos));
-    for (int l = 0; l < c.L; l++) {
+    const bool pr = CP && c.cp.pair;
+    for (int l = 0; l < (pr && f == 1 ? 0 : c.L); l++) {
       const sk_layer_desc& Ly = S.desc[l];
       const bool last_layer = l == c.L - 1;
       const sk_layer_desc& Ln = S.desc[last_layer ? 0 : l + 1];
@@ -1606,7 +2024,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
 
 // SMP: sampled picks (do_sample != 0). The greedy instantiation carries none of the sampling code, whose call and
 // registers would otherwise weigh on the control loop of every greedy frame.
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP>
+// PAIRK: the code predictor's paired pass alone (positions 0 and 1, no head), launched before the frames of a
+// cp.pair launch (which then start at frame 1's head): a kernel of its own, so that its registers do not add to
+// the frame loop's (inlined into the same kernel, the pass made the loop's values spill).
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK = false>
 __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArgs cp, int n_frames) {
   extern __shared__ char smem_raw[];
   Lds<H, I, W, V, CP>& S = *(Lds<H, I, W, V, CP>*)smem_raw;
@@ -1656,8 +2077,9 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   c.x = x;
   c.r = r;
   c.g = (int)x * kPerXcd + r;
-  c.base = s_base;
   c.tpf = (uint32_t)d.n_layers * 8u + 8u;
+  // after a paired pass the frames' epochs continue from that launch's (frame 0 is the pass's)
+  c.base = s_base - (CP && !PAIRK && cp.pair ? c.tpf : 0u);
   c.pos0 = d.pos ? (int)gload(d.pos) : 0;
   // read before this workgroup publishes anything: workgroup 0 advances the counter once every pick is done
   c.seed = SMP ? gload(d.seed) : 0;
@@ -1683,11 +2105,16 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     }
   }
   c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
-  if (wave == W) run_control<H, I, W, V, CP, SMP>(c, S, lane);
-  else run_compute<H, I, W, V, CP, SMP, WD, KEEP>(c, S, wave, tid, lane);
+  if constexpr (PAIRK) {
+    if (wave == W) ctl_pair_pass<H, I, W, V, CP>(c, S, lane);
+    else compute_pair<H, I, W, V, CP, WD, KEEP>(c, S, wave, tid, lane);
+  } else {
+    if (wave == W) run_control<H, I, W, V, CP, SMP>(c, S, lane);
+    else run_compute<H, I, W, V, CP, SMP, WD, KEEP>(c, S, wave, tid, lane);
+  }
   // ---- end of launch: epoch base and launch count (workgroup 0; every workgroup finished its census) --------
   if (c.g == 0 && tid == 0) {
-    st_u32_dev(ws, Ws::kTick, c.base + (uint32_t)n_frames * c.tpf);
+    st_u32_dev(ws, Ws::kTick, c.base + (uint32_t)(PAIRK ? 1 : n_frames) * c.tpf);
     st_u32_dev(ws, Ws::kLaunch, ld_u32_dev(ws, Ws::kLaunch) + 1u);
   }
 }
@@ -1696,14 +2123,14 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
 // cannot hold a workgroup, would only surface as poll timeouts). Done once per device and instantiation; a failure
 // is reported every time and retried on the next call.
 constexpr int kMaxDevices = 64;
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK>
 int prepare_kernel(size_t lds) {
   static bool ready[kMaxDevices] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return sk_set_error(SK_EDEVICE, "sk_talker_frames: no current HIP device");
   if (ready[dev]) return SK_OK;
-  const void* fn = (const void*)k_frames<H, I, W, V, CP, SMP, WD, KEEP>;
+  const void* fn = (const void*)k_frames<H, I, W, V, CP, SMP, WD, KEEP, PAIRK>;
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return sk_check_launch(e, "sk_talker_frames: raising the LDS limit");
   int cus = 0, per_cu = 0;
@@ -1718,12 +2145,14 @@ int prepare_kernel(size_t lds) {
   ready[dev] = true;
   return SK_OK;
 }
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK = false>
 int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
-  const size_t lds = sizeof(Lds<H, I, W, V, CP>) < 96 * 1024 ? 96 * 1024 : sizeof(Lds<H, I, W, V, CP>);  // one workgroup per CU
-  const int rc = prepare_kernel<H, I, W, V, CP, SMP, WD, KEEP>(lds);
+  constexpr size_t need = sizeof(Lds<H, I, W, V, CP>) + (PAIRK ? sizeof(LdsPair<H, I>) : 0);
+  const size_t lds = need < 96 * 1024 ? 96 * 1024 : need;  // one workgroup per CU
+  const int rc = prepare_kernel<H, I, W, V, CP, SMP, WD, KEEP, PAIRK>(lds);
   if (rc != SK_OK) return rc;
-  hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP, WD, KEEP>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp, n_frames);
+  hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP, WD, KEEP, PAIRK>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp,
+                     n_frames);
   return sk_check_launch(hipGetLastError(), "sk_talker_frames");
 }
 // KEEP: the layer weights are loaded through the caches instead of as non-temporal streams (the code predictor
@@ -1731,6 +2160,12 @@ int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipSt
 template <int H, int I, int W, int V, bool CP, int WD = SK_WD_I8ROW, bool KEEP = false>
 int launch_frames(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
   if (d->max_len > Cfg<H, I, W, V, CP>::kMaxLen) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: max_len too long");
+  if constexpr (CP) {
+    if (cp.pair) {  // the paired pass first (no head: greedy and sampled launches share it)
+      const int rc = launch_kernel<H, I, W, V, CP, false, WD, KEEP, true>(d, cp, n_frames, st);
+      if (rc != SK_OK) return rc;
+    }
+  }
   return d->do_sample ? launch_kernel<H, I, W, V, CP, true, WD, KEEP>(d, cp, n_frames, st)
                       : launch_kernel<H, I, W, V, CP, false, WD, KEEP>(d, cp, n_frames, st);
 }

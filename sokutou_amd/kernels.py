@@ -210,11 +210,13 @@ class CodePredictor:
 
     def __init__(self, cp, temb: torch.Tensor, n_positions: int = 16, wd: str = "i8row", device=None,
                  x0: torch.Tensor | None = None, id0: torch.Tensor | None = None, codes: torch.Tensor | None = None,
-                 keep_layers: bool = True):
+                 keep_layers: bool = True, pair: bool = True):
         """``x0`` (fp32 [hidden]), ``id0`` (int64, one element) and ``codes`` (int64 [n_positions]) may be a caller's
         own contiguous device buffers: the kernel then reads and writes them in place (no copies per frame).
         ``keep_layers`` loads the layer weights through the caches (read once per position, they stay in L2 and
-        the Infinity Cache across the frame) instead of streaming them like the heads (``sk_cp_desc.keep_layers``)."""
+        the Infinity Cache across the frame) instead of streaming them like the heads (``sk_cp_desc.keep_layers``).
+        ``pair`` runs positions 0 and 1 as one pass with two rows per stage (the reference's cp_pair,
+        qwen3/kernels.py:600-617; ``sk_cp_desc.pair``)."""
         if wd != "i8row":
             raise ValueError("the code-predictor kernel reads i8row weights")
         proj = getattr(cp, "small_to_mtp_projection", None)
@@ -253,15 +255,17 @@ class CodePredictor:
         hs = [0] + [h.s.data_ptr() for h in self.heads]
         self._ptrs = torch.tensor([tabs, hw, hs], dtype=torch.int64, device=dev)
         self._layer_desc = _layer_descs(P, list(self.kc.unbind(0)), list(self.vc.unbind(0)), dev)
-        self.ws = torch.zeros(int(L.sk_talker_workspace_size(P.H, P.I)), dtype=torch.uint8, device=dev)
+        self.ws = torch.zeros(int(L.sk_cp_workspace_size(P.H, P.I, int(bool(pair)))), dtype=torch.uint8, device=dev)
         self._desc = _lib.SkCpDesc(
             n_layers=len(P.layers), hidden=P.H, inter=P.I, nq=P.nq, nkv=P.nkv, vocab=self.V, n_positions=self.n,
             wd=_lib.WD[wd], ct=_lib.CT["bf16"], eps=P.eps, layers=self._layer_desc.data_ptr(), norm=P.norm.data_ptr(),
             rope=P.rope.data_ptr(), x0=self.x0.data_ptr(), id0=self.id0.data_ptr(), emb0_rows=self.temb.shape[0],
             emb=self._ptrs[0].data_ptr(), head_w=self._ptrs[1].data_ptr(), head_s=self._ptrs[2].data_ptr(),
             codes=self.codes.data_ptr(), logits=self.logits.data_ptr(), layer_out=None,
-            workspace=self.ws.data_ptr(), workspace_bytes=self.ws.numel(), keep_layers=int(bool(keep_layers)))
+            workspace=self.ws.data_ptr(), workspace_bytes=self.ws.numel(), keep_layers=int(bool(keep_layers)),
+            pair=int(bool(pair)))
         self.keep_layers = bool(keep_layers)
+        self.pair = bool(pair)
         self.graph: torch.cuda.CUDAGraph | None = None
 
     def set_sampling(self, temperature: float, top_k: int, seed: torch.Tensor, counter: torch.Tensor) -> None:
@@ -327,8 +331,9 @@ class Qwen3Kernels(Qwen3Fast):
     for the code predictor's layers (qwen3/kernels.py:525-542): matrices within it, in layer order, are loaded
     cacheable (policy 0), the rest and every talker and head weight are streamed (policy 1); unset, it covers all
     of them (their 79 MB fit MI355X's 256 MB Infinity Cache). The one-launch code-predictor kernel applies one
-    policy to all its layers: cacheable only when the budget covers every layer. ``cp_pair`` is accepted for
-    interface parity (positions 0 and 1 run as two passes). ``suppress_tail`` (default 1024, as the reference) sets how many trailing ids the
+    policy to all its layers: cacheable only when the budget covers every layer. ``cp_pair`` (default on, as the
+    reference) runs the code predictor's positions 0 and 1 as one pass on the one-launch kernel; the per-kernel
+    path runs them one after the other. ``suppress_tail`` (default 1024, as the reference) sets how many trailing ids the
     processor suppresses; 0 disables suppression.
     """
 
@@ -444,7 +449,7 @@ class Qwen3Kernels(Qwen3Fast):
             # bound to the frame state: reads ph32 and code 0, writes all G codes, with no copy per frame
             keep = all(Ly[m].pol == 0 for Ly in P.layers for m in ("qkv", "o", "gu", "down"))
             self.cpk = CodePredictor(cp, self.temb, n_positions=self.G, wd=wd, device=dev, x0=self.ph32, id0=self.id0,
-                                     codes=self.codes, keep_layers=keep)
+                                     codes=self.codes, keep_layers=keep, pair=self.cp_pair)
             if self.s.sub_do_sample:  # the fused sampler's draws, in the same order as position by position
                 self.cpk.set_sampling(self.s.sub_temperature, self.s.sub_top_k, self.fs.seed, self.fs.counter)
 

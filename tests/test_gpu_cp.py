@@ -1,4 +1,5 @@
-"""The code predictor on the persistent kernel (sk_cp_frame), with its layer weights kept or streamed: greedy
+"""The code predictor on the persistent kernel (sk_cp_frame), with its layer weights kept or streamed and positions
+0 and 1 paired or not: greedy
 sub-codes of every position, per-layer residuals and logits at the last position, against the oracle fixture;
 graph replay; the error word."""
 
@@ -21,11 +22,14 @@ def rel_err(a, b) -> float:
     return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
 
 
-@pytest.fixture(scope="module", params=[True, False], ids=["keep", "stream"])
+@pytest.fixture(scope="module", params=[(True, True), (False, True), (True, False)],
+                ids=["keep-pair", "stream-pair", "keep-serial"])
 def cp_engine(gpu, request):
-    """Both instantiations of the kernel: layer weights loaded cacheable (the default) or streamed."""
-    print(f"cp06b: building the seeded code predictor (5 layers, 15 heads), keep_layers={request.param}", flush=True)
-    return syn.make_cp_engine("cp06b", 0, gpu, keep_layers=request.param)
+    """Both instantiations of the kernel, layer weights loaded cacheable (the default) or streamed, with positions 0
+    and 1 paired (the default) or run one after the other: the same codes either way."""
+    keep, pair = request.param
+    print(f"cp06b: building the seeded code predictor (5 layers, 15 heads), keep_layers={keep} pair={pair}", flush=True)
+    return syn.make_cp_engine("cp06b", 0, gpu, keep_layers=keep, pair=pair)
 
 
 def test_code_predictor_frames_against_oracle(cp_engine, gpu):

@@ -80,6 +80,16 @@ def test_cp_frame_rejects_bad_shapes_without_launching():
     assert L.sk_cp_frame(ctypes.byref(d), None) == _lib.SK_EUNSUPPORTED
 
 
+def test_cp_workspace_size_covers_the_paired_rows():
+    """Serial positions need the talker's workspace; pairing adds the second row's cells (q|k|v of 8 heads,
+    attention output, h after o, activation, h after down: 4096 + 2048 + 1024 + 3072 + 1024 cells of 8 bytes)."""
+    L = _lib.load()
+    base = L.sk_talker_workspace_size(1024, 3072)
+    assert L.sk_cp_workspace_size(1024, 3072, 0) == base
+    assert L.sk_cp_workspace_size(1024, 3072, 1) == base + 8 * (8 * 512 + 2048 + 1024 + 3072 + 1024)
+    assert L.sk_cp_workspace_size(0, 3072, 1) == 0
+
+
 def test_batched_entry_points_reject_bad_shapes_without_launching():
     import ctypes
 
