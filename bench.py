@@ -128,7 +128,8 @@ def cp_algorithmic_bytes(s, positions: int = 16) -> dict:
 
 
 def run_cp(args) -> None:
-    """Code-predictor frames: HIP events around every sk_cp_frame launch of the timed steps."""
+    """Code-predictor frames: HIP events around every sk_cp_frame call of the timed steps (two launches per frame:
+    the paired pass of positions 0 and 1, then positions 1 (head) to 15)."""
     import numpy as np
     import torch
 
@@ -184,14 +185,17 @@ def run_cp(args) -> None:
         "config": {"workload": f"{name}: {s.n_layers} layers, hidden {s.hidden}, {s.nq}q/{s.nkv}kv heads x 128, "
                                f"intermediate {s.inter}, 15 heads of {s.vocab}, i8row, {spec['positions']} positions "
                                f"(KV 1..16) per frame, {frames} frames per step", "weights": "i8row",
-                   "engine": "sk_cp_frame (one launch per frame)"},
-        "roofline": {"bound": "hbm", "kernel": "k_frames code-predictor mode (sk_cp_frame)",
+                   "engine": "sk_cp_frame (paired pass of positions 0 and 1, then one launch for the rest)"
+                   if eng.pair else "sk_cp_frame (one launch per frame)"},
+        "roofline": {"bound": "hbm", "kernel": "k_frames code-predictor mode (sk_cp_frame; both launches of a frame)",
                      "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "bytes_per_launch": ab["frame"],
-                     "avg_launch_us": round(launch_us, 2),
+                     "avg_launch_us": round(launch_us, 2), "launches_per_frame": 2 if eng.pair else 1,
                      "note": "the 79 MB stack + 31 MB of heads fit in the 256 MB Infinity Cache across passes; "
-                             "the kernel runs positions 0 and 1 as two passes (16 passes, "
-                             f"{ab['frame_16_passes']} bytes touched)"},
+                             + ("positions 0 and 1 share one pass over the layers (15 passes, as the algorithmic "
+                                "bytes count them); avg_launch_us spans both launches of a frame" if eng.pair else
+                                "the kernel runs positions 0 and 1 as two passes (16 passes, "
+                                f"{ab['frame_16_passes']} bytes touched)")},
         "frame": {"us_per_frame": round(launch_us, 2), "us_per_position": round(launch_us / spec["positions"], 2),
                   "us_per_layer_pass": round(launch_us / spec["positions"] / s.n_layers, 3)},
         "parity_codes_match_oracle": parity, "setup_s": round(setup_s, 1),
