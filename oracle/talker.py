@@ -28,6 +28,12 @@ How each function is pinned (independent checks, in ``tests/test_oracle.py``):
   * ``process_logits``/``argmax_first`` - crafted ties, NaN, all -inf; restated from qwen3/sampler.py:50-65, 129-149.
   * ``philox4x32_10``        - the Random123 known-answer vectors of philox4x32_10.
   * ``topk_threshold``       - brute force (count of strictly larger keys < k <= count of keys >= it).
+  * ``gumbel_uniform``       - PARITY UNPINNED for the draw sequence: its Philox counter layout (index, draw lo,
+                               draw hi, 0x51), key order and uniform mapping ((r0 >> 8) + 0.5) * 2^-24 are read
+                               from qwen3/sampler.py:118-125. The reference holds no vectors of its draws, and its
+                               CUDA kernel (compiled by CuPy NVRTC) cannot run here. The Philox function itself is
+                               pinned by the known-answer vectors, and ``sample_draw``'s law by a chi-square test;
+                               neither would catch a swapped counter word.
   * ``sample_draw``          - the empirical law of many draws against softmax over the top-k (chi-square), and
                                the keep rule by hand on crafted ties / -inf / NaN.
 """
