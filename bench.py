@@ -111,14 +111,14 @@ def time_kernels(eng, reps: int = 200) -> dict:
     return out
 
 
-def cp_algorithmic_bytes(s, positions: int = 16) -> dict:
+def cp_algorithmic_bytes(s, positions: int = 16, wd: str = "i8row") -> dict:
     """Bytes one code-predictor frame must move: the stack's weights and scales once per pass, positions 0 and 1
     counted as one pass as the reference pairs them (positions - 1 passes), plus the 15 heads once each and the
-    K/V reads and appends of every position."""
+    K/V reads and appends of every position. Scales: a bf16 per row (i8row) or an fp16 per 32 weights (i8g32)."""
     H, I, nq, nkv, hd = s.hidden, s.inter, s.nq, s.nkv, s.head_dim
 
     def mat(N, K):
-        return N * K + 2 * N
+        return N * K + (2 * N * (K // 32) if wd == "i8g32" else 2 * N)
 
     layer = mat((nq + 2 * nkv) * hd, H) + mat(H, nq * hd) + mat(2 * I, H) + mat(H, I)
     kv = sum(2 * nkv * (p + 1) * hd * 2 + 2 * nkv * hd * 2 for p in range(positions)) * s.n_layers
@@ -140,7 +140,7 @@ def run_cp(args) -> None:
     spec = syn.WORKLOADS[name]
     s = syn.workload_shape(name)
     t0 = time.perf_counter()
-    eng = syn.make_cp_engine(name, args.seed, dev)
+    eng = syn.make_cp_engine(name, args.seed, dev, wd=args.wd)
     x0, id0 = syn.cp_frame_inputs(args.seed, 0, s)
     eng.x0.copy_(torch.from_numpy(x0))
     eng.id0.fill_(id0)
@@ -169,13 +169,14 @@ def run_cp(args) -> None:
     dt = time.perf_counter() - t0
     if eng.error():
         raise RuntimeError(f"code-predictor kernel error {eng.error()}")
-    gold = ROOT / "tests" / "golden" / f"{name}_seed{args.seed}.json"
+    gold = ROOT / "tests" / "golden" / (f"{name}_seed{args.seed}.json" if args.wd == "i8row" else
+                                        f"{name}_{args.wd}_seed{args.seed}.json")
     parity = None
     if gold.exists():
         parity = eng.codes.cpu().tolist() == json.loads(gold.read_text())["codes"][0]
     fps = frames * args.steps / dt
     launch_us = sum(a.elapsed_time(b) for a, b in ev) * 1e3 / len(ev)
-    ab = cp_algorithmic_bytes(s, spec["positions"])
+    ab = cp_algorithmic_bytes(s, spec["positions"], args.wd)
     achieved = ab["frame"] / (launch_us * 1e-6) / 1e9
     res = {
         "metric": "code predictor frames/sec (5 layers of the 0.6B shape, 16 positions, 15 greedy sub-codes, int8)",
@@ -183,8 +184,8 @@ def run_cp(args) -> None:
         "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8 weights x fp32 accumulate (bf16 KV cache)", "data": "synthetic",
         "config": {"workload": f"{name}: {s.n_layers} layers, hidden {s.hidden}, {s.nq}q/{s.nkv}kv heads x 128, "
-                               f"intermediate {s.inter}, 15 heads of {s.vocab}, i8row, {spec['positions']} positions "
-                               f"(KV 1..16) per frame, {frames} frames per step", "weights": "i8row",
+                               f"intermediate {s.inter}, 15 heads of {s.vocab}, {args.wd}, {spec['positions']} positions "
+                               f"(KV 1..16) per frame, {frames} frames per step", "weights": args.wd,
                    "engine": "sk_cp_frame (paired pass of positions 0 and 1, then one launch for the rest)"
                    if eng.pair else "sk_cp_frame (one launch per frame)"},
         "roofline": {"bound": "hbm", "kernel": "k_frames code-predictor mode (sk_cp_frame; both launches of a frame)",
@@ -203,7 +204,7 @@ def run_cp(args) -> None:
     if not args.no_cpu:
         from oracle.workload import cp_oracle
 
-        orc, _ = cp_oracle(name, args.seed)
+        orc, _ = cp_oracle(name, args.seed, wd=args.wd)
         orc.frame(x0, id0)  # warm-up
         times = []
         t_start = time.perf_counter()

@@ -15,9 +15,9 @@ extern "C" int64_t sk_cp_workspace_size(int hidden, int inter, int pair) {
 extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
   if (!d) return sk_set_error(SK_EINVAL, "sk_cp_frame: bad arguments");
   if (d->nq != kNQ || d->nkv != kNKV || d->vocab != 2048 || d->hidden != 1024 || d->inter != 3072 ||
-      d->wd != SK_WD_I8ROW || d->ct != SK_CT_BF16)
-    return sk_set_error(SK_EUNSUPPORTED,
-                        "sk_cp_frame: needs hidden 1024, intermediate 3072, 16 q / 8 kv heads, vocab 2048, i8row, bf16 cache");
+      !(d->wd == SK_WD_I8ROW || d->wd == SK_WD_I8G32) || d->ct != SK_CT_BF16)
+    return sk_set_error(SK_EUNSUPPORTED, "sk_cp_frame: needs hidden 1024, intermediate 3072, 16 q / 8 kv heads, "
+                                         "vocab 2048, i8row or i8g32 weights, bf16 cache");
   if (d->n_positions < 2 || d->n_positions > 64 || d->n_layers <= 0 || d->n_layers > Ws::kTraceLayers)
     return sk_set_error(SK_EUNSUPPORTED, "sk_cp_frame: 2..64 positions and 1..32 layers");
   if (!d->layers || !d->norm || !d->rope || !d->x0 || !d->id0 || !d->emb || !d->head_w || !d->head_s || !d->codes ||
@@ -27,15 +27,10 @@ extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
     return sk_set_error(SK_EWORKSPACE, "sk_cp_frame: workspace too small");
   if (d->do_sample && (!d->seed || !d->counter || !(d->inv_temp > 0.f)))
     return sk_set_error(SK_EINVAL, "sk_cp_frame: sampling needs seed, counter and inv_temp > 0");
-  sk_talker_desc t{};
-  t.n_layers = d->n_layers; t.hidden = d->hidden; t.inter = d->inter; t.nq = d->nq; t.nkv = d->nkv;
-  t.vocab = d->vocab; t.max_len = d->n_positions; t.wd = d->wd; t.ct = d->ct; t.eps = d->eps;
-  t.layers = d->layers; t.norm = d->norm; t.rope = d->rope; t.id0 = const_cast<int64_t*>(d->id0);
-  t.out = d->codes; t.rep_pen = 1.f; t.eos = -1; t.talker_processor = 0;
-  t.logits = d->logits; t.layer_out = d->layer_out; t.workspace = d->workspace; t.workspace_bytes = d->workspace_bytes;
-  t.do_sample = d->do_sample; t.inv_temp = d->inv_temp; t.top_k = d->top_k; t.seed = d->seed; t.counter = d->counter;
-  // pairing needs a position 1 to pair with (n_positions >= 2, checked above)
-  const CpArgs cp{d->x0, d->emb, d->head_w, d->head_s, d->emb0_rows, d->pair ? 1 : 0};
+  if (d->wd == SK_WD_I8G32) return sk_cp_frame_g32(d, (hipStream_t)stream);
+  sk_talker_desc t;
+  CpArgs cp;
+  cp_launch_args(d, t, cp);
   if (d->keep_layers) return launch_frames<1024, 3072, 4, 2048, true, SK_WD_I8ROW, true>(&t, cp, d->n_positions, (hipStream_t)stream);
   return launch_frames<1024, 3072, 4, 2048, true>(&t, cp, d->n_positions, (hipStream_t)stream);
 }

@@ -462,8 +462,8 @@ __device__ __forceinline__ void dot_rows2(const uint4 (&w)[RW][C], const float* 
 
 // i8g32 weights (the reference's format: one fp16 scale per 32 weights of a row, applied per 16-weight chunk,
 // qwen3/kernels.py:104-110): a lane's chunk c of a row covers weights 16 (lane + 64 c) .. + 15, inside group
-// (lane + 64 c) / 2, whose scale comes with the chunk (raw fp16 bits until the dot).
-template <int RW, int C, bool LO = false>
+// (lane + 64 c) / 2, whose scale comes with the chunk (raw fp16 bits until the dot). KEEP as for load_rows.
+template <int RW, int C, bool LO = false, bool KEEP = false>
 __device__ __forceinline__ void load_rows_g32(uint4 (&w)[RW][C], uint16_t (&g)[RW][C], const int8_t* W, const uint16_t* S,
                                               int row0, int nvalid, int K, int lane) {
 #pragma unroll
@@ -475,7 +475,8 @@ __device__ __forceinline__ void load_rows_g32(uint4 (&w)[RW][C], uint16_t (&g)[R
 #pragma unroll
       for (int c = 0; c < C; c++) {
         w[r][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(W)),
-                                                                                  (uint32_t)lane * 16u + 1024u * c, so, kNT));
+                                                                                  (uint32_t)lane * 16u + 1024u * c, so,
+                                                                                  KEEP ? 0 : kNT));
         g[r][c] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)), ((uint32_t)lane & ~1u) + 64u * c, sg, 0);
       }
       continue;
@@ -483,7 +484,7 @@ __device__ __forceinline__ void load_rows_g32(uint4 (&w)[RW][C], uint16_t (&g)[R
     const uint4* p = (const uint4*)(W + (size_t)row * K);
 #pragma unroll
     for (int c = 0; c < C; c++) {
-      w[r][c] = ld_stream(p + lane + 64 * c);
+      w[r][c] = KEEP ? ld_keep(p + lane + 64 * c) : ld_stream(p + lane + 64 * c);
       g[r][c] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(uniform(S)),
                                                      ((uint32_t)row * (uint32_t)(K >> 5) + (uint32_t)((lane + 64 * c) >> 1)) * 2u,
                                                      0, 0);
@@ -529,7 +530,7 @@ __device__ __forceinline__ void dot_rows_g32(const uint4 (&w)[RW][C], const uint
 template <int WD, int RW, int C, bool LO = false, bool KEEP = false, int GR, int GC>
 __device__ __forceinline__ void load_w(uint4 (&w)[RW][C], uint16_t (&s)[RW], uint16_t (&g)[GR][GC], const int8_t* W,
                                        const uint16_t* S, int row0, int nvalid, int K, int lane) {
-  if constexpr (WD == SK_WD_I8G32) load_rows_g32<RW, C, LO>(w, g, W, S, row0, nvalid, K, lane);
+  if constexpr (WD == SK_WD_I8G32) load_rows_g32<RW, C, LO, KEEP>(w, g, W, S, row0, nvalid, K, lane);
   else load_rows<RW, C, LO, KEEP>(w, s, W, S, row0, nvalid, K, lane);
 }
 template <int WD, int RW, int C, int GR, int GC>
@@ -537,6 +538,58 @@ __device__ __forceinline__ void dot_w(const uint4 (&w)[RW][C], const uint16_t (&
                                       float (&y)[RW]) {
   if constexpr (WD == SK_WD_I8G32) dot_rows_g32<RW, C>(w, g, xs, lane, y);
   else dot_rows<RW, C>(w, xs, lane, y);
+}
+// dot_rows2 for i8g32 weights: each chunk's sums of both inputs are scaled by the chunk's group scale, as
+// dot_rows_g32 does for one input.
+template <int RW, int C>
+__device__ __forceinline__ void dot_rows2_g32(const uint4 (&w)[RW][C], const uint16_t (&g)[RW][C], const float* xa,
+                                              const float* xb, int lane, float (&ya)[RW], float (&yb)[RW]) {
+  float aa[RW], ab[RW], pa[RW], pb[RW];
+#pragma unroll
+  for (int r = 0; r < RW; r++) { aa[r] = 0.f; ab[r] = 0.f; pa[r] = 0.f; pb[r] = 0.f; }
+  const float2* xa2 = (const float2*)xa;
+  const float2* xb2 = (const float2*)xb;
+  float2 na0 = xa2[2 * lane], na1 = xa2[2 * lane + 1], nb0 = xb2[2 * lane], nb1 = xb2[2 * lane + 1];
+#pragma unroll
+  for (int t = 0; t < 4 * C; t++) {  // quarter t: chunk t / 4, bytes 4 (t % 4) .. + 3 of each row's chunk
+    const float2 a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
+    if (t + 1 < 4 * C) {
+      const int k = 2 * ((t + 1) * 64 + lane);
+      na0 = xa2[k]; na1 = xa2[k + 1]; nb0 = xb2[k]; nb1 = xb2[k + 1];
+    }
+    const int c = t >> 2, j = t & 3;
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+      const uint32_t q = j == 0 ? w[r][c].x : j == 1 ? w[r][c].y : j == 2 ? w[r][c].z : w[r][c].w;
+      const float w0 = (float)(int8_t)q, w1 = (float)(int8_t)(q >> 8), w2 = (float)(int8_t)(q >> 16),
+                  w3 = (float)(int8_t)(q >> 24);
+      float t0 = w0 * a0.x, u = w0 * b0.x;
+      t0 = __builtin_fmaf(w1, a0.y, t0);
+      u = __builtin_fmaf(w1, b0.y, u);
+      t0 = __builtin_fmaf(w2, a1.x, t0);
+      u = __builtin_fmaf(w2, b1.x, u);
+      t0 = __builtin_fmaf(w3, a1.y, t0);
+      u = __builtin_fmaf(w3, b1.y, u);
+      pa[r] += t0;
+      pb[r] += u;
+      if (j == 3) {
+        const float sc = h2f(g[r][c]);
+        aa[r] = __builtin_fmaf(sc, pa[r], aa[r]);
+        ab[r] = __builtin_fmaf(sc, pb[r], ab[r]);
+        pa[r] = 0.f;
+        pb[r] = 0.f;
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; r++) { ya[r] = wave_sum(aa[r]); yb[r] = wave_sum(ab[r]); }
+}
+template <int WD, int RW, int C, int GR, int GC>
+__device__ __forceinline__ void dot2_w(const uint4 (&w)[RW][C], const uint16_t (&g)[GR][GC], const float* xa,
+                                       const float* xb, int lane, float (&ya)[RW], float (&yb)[RW]) {
+  if constexpr (WD == SK_WD_I8G32) dot_rows2_g32<RW, C>(w, g, xa, xb, lane, ya, yb);
+  else dot_rows2<RW, C>(w, xa, xb, lane, ya, yb);
 }
 template <int WD>
 __device__ __forceinline__ float row_scale_of(uint16_t s) {
@@ -919,6 +972,20 @@ struct CpArgs {
   int emb0_rows;              // rows of emb[1] (the range code 0 must lie in)
   int pair;                   // positions 0 and 1 in one pass (two rows per stage)
 };
+
+// A code-predictor launch as the kernel takes it: the talker descriptor of the shared kernel (max_len = the positions,
+// no processor) and the code predictor's own arguments. Pairing needs a position 1 to pair with (n_positions >= 2,
+// checked by sk_cp_frame).
+inline void cp_launch_args(const sk_cp_desc* d, sk_talker_desc& t, CpArgs& cp) {
+  t = sk_talker_desc{};
+  t.n_layers = d->n_layers; t.hidden = d->hidden; t.inter = d->inter; t.nq = d->nq; t.nkv = d->nkv;
+  t.vocab = d->vocab; t.max_len = d->n_positions; t.wd = d->wd; t.ct = d->ct; t.eps = d->eps;
+  t.layers = d->layers; t.norm = d->norm; t.rope = d->rope; t.id0 = const_cast<int64_t*>(d->id0);
+  t.out = d->codes; t.rep_pen = 1.f; t.eos = -1; t.talker_processor = 0;
+  t.logits = d->logits; t.layer_out = d->layer_out; t.workspace = d->workspace; t.workspace_bytes = d->workspace_bytes;
+  t.do_sample = d->do_sample; t.inv_temp = d->inv_temp; t.top_k = d->top_k; t.seed = d->seed; t.counter = d->counter;
+  cp = CpArgs{d->x0, d->emb, d->head_w, d->head_s, d->emb0_rows, d->pair ? 1 : 0};
+}
 
 // Everything a role function needs about this workgroup and launch.
 struct Ctx {
@@ -1447,8 +1514,6 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
   // compiler, held ~100 registers through the pass and made it spill
   constexpr bool kLO = true;
   constexpr int kNP = H / 128;
-  static_assert(!C::kLate && !C::kSpread, "the paired pass prefetches a whole layer ahead");
-  static_assert(WD == SK_WD_I8ROW, "the code predictor reads i8row weights");
   static_assert(2 * 16 <= 64 && 2 * C::R_O <= 64 && C::R_GU <= 64 && 2 * C::R_D <= 64, "both rows fit S.pub");
   static_assert(kQ % 1024 == 0 && I % 1024 == 0 && kQ / 1024 <= W && I / 1024 <= W && W == 4,
                 "the second row's polls: 1024-cell blocks, one per compute wave");
@@ -1468,7 +1533,9 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
   const int p = tid >> 7, dd = tid & 127;  // the attention's head and dim of this thread
   uint4 wq[C::RW_QKV][C::CH], wo[C::RW_O][C::CQ], wg[C::RW_GU][C::CH], wd[C::RW_D][C::CI];
   uint16_t sq[C::RW_QKV], so[C::RW_O], sg[C::RW_GU], sd[C::RW_D];
-  uint16_t gq[1][1], go[1][1], gg[1][1], gd[1][1];  // unused (no group scales)
+  constexpr bool G32 = WD == SK_WD_I8G32;  // i8g32: raw fp16 group scales, one per row and chunk
+  uint16_t gq[G32 ? C::RW_QKV : 1][G32 ? C::CH : 1], go[G32 ? C::RW_O : 1][G32 ? C::CQ : 1];
+  uint16_t gg[G32 ? C::RW_GU : 1][G32 ? C::CH : 1], gd[G32 ? C::RW_D : 1][G32 ? C::CI : 1];
   float a_cs, a_sn, a_n0, a_n1;  // RoPE of position 0 and the q / k norm weights of this wave's vector
   auto load_attn_vec = [&](const sk_layer_desc& Lx) {
     const float* nw = (cw & 3) == 2 ? Lx.kn : Lx.qn;
@@ -1522,7 +1589,7 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
     if (S.flags[0] || P.bad) return false;
     {
       float ya[C::RW_QKV], yb[C::RW_QKV];
-      dot_rows2<C::RW_QKV, C::CH>(wq, S.xs[0], P.xs[0], lane, ya, yb);
+      dot2_w<WD, C::RW_QKV, C::CH>(wq, gq, S.xs[0], P.xs[0], lane, ya, yb);
       const float ia = S.inv, ib = P.inv;
       if (lane == 0) {
 #pragma unroll
@@ -1608,7 +1675,7 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
     if (S.flags[2] || P.bad) return false;
     {
       float ya[C::RW_O], yb[C::RW_O];
-      dot_rows2<C::RW_O, C::CQ>(wo, S.xs[1], P.xs[1], lane, ya, yb);
+      dot2_w<WD, C::RW_O, C::CQ>(wo, go, S.xs[1], P.xs[1], lane, ya, yb);
       if (lane == 0) {
 #pragma unroll
         for (int i = 0; i < C::RW_O; i++)
@@ -1634,7 +1701,7 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
     if (S.flags[3] || P.bad) return false;
     {
       float ya[C::RW_GU], yb[C::RW_GU];
-      dot_rows2<C::RW_GU, C::CH>(wg, S.xs[0], P.xs[0], lane, ya, yb);
+      dot2_w<WD, C::RW_GU, C::CH>(wg, gg, S.xs[0], P.xs[0], lane, ya, yb);
       const float ia = S.inv, ib = P.inv;
       if (lane == 0) {
 #pragma unroll
@@ -1658,7 +1725,7 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
     if (S.flags[4] || P.bad) return false;
     {
       float ya[C::RW_D], yb[C::RW_D];
-      dot_rows2<C::RW_D, C::CI>(wd, S.xs[1], P.xs[1], lane, ya, yb);
+      dot2_w<WD, C::RW_D, C::CI>(wd, gd, S.xs[1], P.xs[1], lane, ya, yb);
       if (lane == 0) {
 #pragma unroll
         for (int i = 0; i < C::RW_D; i++) {

@@ -217,8 +217,8 @@ class CodePredictor:
         the Infinity Cache across the frame) instead of streaming them like the heads (``sk_cp_desc.keep_layers``).
         ``pair`` runs positions 0 and 1 as one pass with two rows per stage (the reference's cp_pair,
         qwen3/kernels.py:600-617; ``sk_cp_desc.pair``)."""
-        if wd != "i8row":
-            raise ValueError("the code-predictor kernel reads i8row weights")
+        if wd not in ("i8row", "i8g32"):
+            raise ValueError("the code-predictor kernel reads i8row or i8g32 weights")
         proj = getattr(cp, "small_to_mtp_projection", None)
         if proj is not None and not isinstance(proj, torch.nn.Identity):
             raise NotImplementedError("a code predictor narrower than the talker (small_to_mtp_projection) is not "
@@ -266,6 +266,7 @@ class CodePredictor:
             pair=int(bool(pair)))
         self.keep_layers = bool(keep_layers)
         self.pair = bool(pair)
+        self.wd = wd
         self.graph: torch.cuda.CUDAGraph | None = None
 
     def set_sampling(self, temperature: float, top_k: int, seed: torch.Tensor, counter: torch.Tensor) -> None:
@@ -442,7 +443,7 @@ class Qwen3Kernels(Qwen3Fast):
         self.ck = torch.zeros((len(P.layers), P.nkv, self.G, HD), dtype=cdt, device=dev)
         self.cv = torch.zeros_like(self.ck)
         self.cpk: CodePredictor | None = None
-        fast = ((not self.s.sub_do_sample or self.fs is not None) and self.proj is None and wd == "i8row"
+        fast = ((not self.s.sub_do_sample or self.fs is not None) and self.proj is None and wd in ("i8row", "i8g32")
                 and self.ct == "bf16" and (P.H, P.I, P.nq, P.nkv, self.cp_heads[0].N) == (1024, 3072, 16, 8, 2048)
                 and 2 <= self.G <= 64)
         if fast:

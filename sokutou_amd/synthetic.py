@@ -446,16 +446,17 @@ def make_prefill_engine(name: str, seed: int = 0, L: int = 24, frames: int = 8, 
     return eng, kw
 
 
-def make_cp_engine(name: str = "cp06b", seed: int = 0, device="cuda", keep_layers: bool = True, pair: bool = True):
+def make_cp_engine(name: str = "cp06b", seed: int = 0, device="cuda", keep_layers: bool = True, pair: bool = True,
+                   wd: str = "i8row"):
     """A CodePredictor over the seeded synthetic code predictor of workload ``name`` (one frame per run);
-    ``keep_layers`` and ``pair`` as CodePredictor's (layer weights loaded cacheable, positions 0 and 1 paired:
-    the defaults)."""
+    ``keep_layers``, ``pair`` and ``wd`` as CodePredictor's (layer weights loaded cacheable, positions 0 and 1
+    paired, i8row: the defaults)."""
     from .kernels import CodePredictor
 
     spec = WORKLOADS[name]
     s = workload_shape(name)
     cp, temb = make_code_predictor(seed, s, device=device, n_positions=spec["positions"])
-    return CodePredictor(cp, temb, n_positions=spec["positions"], wd="i8row", device=device, keep_layers=keep_layers,
+    return CodePredictor(cp, temb, n_positions=spec["positions"], wd=wd, device=device, keep_layers=keep_layers,
                          pair=pair)
 
 

@@ -115,7 +115,7 @@ def talker(name: str, seed: int, wd: str = "i8row") -> None:
     print(stem, "codes", codes[:12], "... min margin", min(margins), meta["oracle_seconds"])
 
 
-def code_predictor(name: str = "cp06b", seed: int = 0) -> None:
+def code_predictor(name: str = "cp06b", seed: int = 0, wd: str = "i8row") -> None:
     """Code-predictor frames: codes of every position, top-1/top-2 margins, per-layer residuals at the last
     position and its logits, for frame 0 (inputs x0 and code 0 differ per frame)."""
     from oracle.workload import cp_oracle
@@ -123,7 +123,7 @@ def code_predictor(name: str = "cp06b", seed: int = 0) -> None:
     spec = syn.WORKLOADS[name]
     t0 = time.time()
     dig: dict = {}
-    orc, s = cp_oracle(name, seed, digests=dig)
+    orc, s = cp_oracle(name, seed, wd=wd, digests=dig)
     t1 = time.time()
     codes, margins, inputs = [], [], []
     layer_out: list = []
@@ -137,11 +137,12 @@ def code_predictor(name: str = "cp06b", seed: int = 0) -> None:
         if f == 0:
             last = lg[-1]
     t2 = time.time()
-    np.savez_compressed(HERE / f"{name}_seed{seed}.npz", layer_out_last0=np.stack(layer_out), logits_last0=last)
-    meta = {"workload": name, "seed": seed, "wd": "i8row", "positions": spec["positions"], "inputs": inputs,
+    stem = f"{name}_seed{seed}" if wd == "i8row" else f"{name}_{wd}_seed{seed}"
+    np.savez_compressed(HERE / f"{stem}.npz", layer_out_last0=np.stack(layer_out), logits_last0=last)
+    meta = {"workload": name, "seed": seed, "wd": wd, "positions": spec["positions"], "inputs": inputs,
             "codes": codes, "margins": margins, "min_margin": min(min(m) for m in margins), "digests": dig,
             "oracle_seconds": {"build": round(t1 - t0, 1), "frames": round(t2 - t1, 1)}}
-    (HERE / f"{name}_seed{seed}.json").write_text(json.dumps(meta, indent=1))
+    (HERE / f"{stem}.json").write_text(json.dumps(meta, indent=1))
     print(name, "codes[0]", codes[0], "min margin", meta["min_margin"], meta["oracle_seconds"])
 
 
@@ -190,6 +191,7 @@ if __name__ == "__main__":
             # difference of summation orders between the kernel and the oracle
             "talker17b_i8g32": lambda: talker("talker17b", 1, "i8g32"),
             "talker17b": lambda: talker("talker17b", 0), "cp06b": lambda: code_predictor("cp06b", 0),
+            "cp06b_i8g32": lambda: code_predictor("cp06b", 0, "i8g32"),
             "batch17b": lambda: batch("batch17b", 0)}
     for n, fn in jobs.items():
         if a.only in (None, n):

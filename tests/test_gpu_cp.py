@@ -1,5 +1,5 @@
-"""The code predictor on the persistent kernel (sk_cp_frame), with its layer weights kept or streamed and positions
-0 and 1 paired or not: greedy
+"""The code predictor on the persistent kernel (sk_cp_frame), with its layer weights kept or streamed, positions 0
+and 1 paired or not, and i8row or i8g32 weights: greedy
 sub-codes of every position, per-layer residuals and logits at the last position, against the oracle fixture;
 graph replay; the error word."""
 
@@ -22,19 +22,26 @@ def rel_err(a, b) -> float:
     return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
 
 
-@pytest.fixture(scope="module", params=[(True, True), (False, True), (True, False)],
-                ids=["keep-pair", "stream-pair", "keep-serial"])
+@pytest.fixture(scope="module",
+                params=[(True, True, "i8row"), (False, True, "i8row"), (True, False, "i8row"), (True, True, "i8g32"),
+                        (False, False, "i8g32")],
+                ids=["keep-pair", "stream-pair", "keep-serial", "i8g32-keep-pair", "i8g32-stream-serial"])
 def cp_engine(gpu, request):
-    """Both instantiations of the kernel, layer weights loaded cacheable (the default) or streamed, with positions 0
-    and 1 paired (the default) or run one after the other: the same codes either way."""
-    keep, pair = request.param
-    print(f"cp06b: building the seeded code predictor (5 layers, 15 heads), keep_layers={keep} pair={pair}", flush=True)
-    return syn.make_cp_engine("cp06b", 0, gpu, keep_layers=keep, pair=pair)
+    """The kernel's instantiations: layer weights loaded cacheable (the default) or streamed, positions 0 and 1
+    paired (the default) or run one after the other, i8row or i8g32 weights (the latter against its own fixture)."""
+    keep, pair, wd = request.param
+    print(f"cp06b: building the seeded code predictor (5 layers, 15 heads), keep_layers={keep} pair={pair} wd={wd}",
+          flush=True)
+    return syn.make_cp_engine("cp06b", 0, gpu, keep_layers=keep, pair=pair, wd=wd)
+
+
+def gold_stem(eng) -> str:
+    return "cp06b_seed0" if eng.wd == "i8row" else f"cp06b_{eng.wd}_seed0"
 
 
 def test_code_predictor_frames_against_oracle(cp_engine, gpu):
-    meta = json.loads((GOLD / "cp06b_seed0.json").read_text())
-    gold = np.load(GOLD / "cp06b_seed0.npz")
+    meta = json.loads((GOLD / f"{gold_stem(cp_engine)}.json").read_text())
+    gold = np.load(GOLD / f"{gold_stem(cp_engine)}.npz")
     eng = cp_engine
     s = syn.workload_shape("cp06b")
     eng.layer_out = torch.zeros((s.n_layers, s.hidden), device=gpu)
@@ -54,7 +61,7 @@ def test_code_predictor_frames_against_oracle(cp_engine, gpu):
 
 
 def test_code_predictor_graph_replay(cp_engine, gpu):
-    meta = json.loads((GOLD / "cp06b_seed0.json").read_text())
+    meta = json.loads((GOLD / f"{gold_stem(cp_engine)}.json").read_text())
     eng = cp_engine
     s = syn.workload_shape("cp06b")
     eng.capture()
