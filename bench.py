@@ -408,7 +408,7 @@ def run_frame(args) -> None:
     s, cs = syn.workload_shape(name), syn.workload_shape(spec["cp"])
     F, kv = spec["frames"], spec["kv"]
     t0 = time.perf_counter()
-    eng, tok, kw = syn.make_frame_engine(name, args.seed, dev, sampled=args.sampling)
+    eng, tok, kw = syn.make_frame_engine(name, args.seed, dev, sampled=args.sampling, wd=args.wd)
     if not eng.frame_kernel:
         raise RuntimeError("the whole-frame bench expects the persistent talker kernel")
     eng.capture()
@@ -445,8 +445,8 @@ def run_frame(args) -> None:
     cp_us = sum(a.elapsed_time(b) for a, b in ev_cp) * 1e3 / F
     t_us = sum(a.elapsed_time(b) for a, b in ev_t) * 1e3 / F
     fps = F * args.steps / dt
-    talker_b = sum(algorithmic_bytes(s, kv + 1 + f)["frame"] for f in range(F)) / F
-    cp_b = cp_algorithmic_bytes(cs, 16)["frame"]
+    talker_b = sum(algorithmic_bytes(s, kv + 1 + f, args.wd)["frame"] for f in range(F)) / F
+    cp_b = cp_algorithmic_bytes(cs, 16, args.wd)["frame"]
     frame_b = talker_b + cp_b
     res = {
         "metric": "whole Qwen3-TTS frame frames/sec (0.6B talker int8 KV 512 + 5-layer code predictor, 16 code groups)",
@@ -456,7 +456,8 @@ def run_frame(args) -> None:
         "config": {"workload": f"{name}: talker {s.n_layers} layers hidden {s.hidden} KV {kv}, code predictor "
                                f"{cs.n_layers} layers, 15 heads of {cs.vocab}, 16 code groups, {F} "
                                f"{'sampled' if args.sampling else 'greedy'} frames per step, "
-                               "talker_in of 16 codes + pad", "engine": "Qwen3Kernels graph: sk_cp_frame + sk_talker_frames"},
+                               "talker_in of 16 codes + pad", "weights": args.wd,
+                   "engine": "Qwen3Kernels graph: sk_cp_frame + sk_talker_frames"},
         "roofline": {"bound": "hbm", "kernel": "k_frames code-predictor mode (sk_cp_frame)",
                      "achieved": round(cp_b / (cp_us * 1e-6) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(cp_b / (cp_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
@@ -472,8 +473,8 @@ def run_frame(args) -> None:
         from oracle import talker as O
         from oracle.workload import cp_oracle, talker_oracle
 
-        torc, otok, _ = talker_oracle(name, args.seed, "i8row", max_len=kv + F + 1)
-        corc, _ = cp_oracle(spec["cp"], args.seed)
+        torc, otok, _ = talker_oracle(name, args.seed, args.wd, max_len=kv + F + 1)
+        corc, _ = cp_oracle(spec["cp"], args.seed, wd=args.wd)
         corc.w["temb"] = torc.w["emb"]
         w = syn.cp_weights(args.seed, cs, 16, talker_vocab=s.vocab)
         tabs = [torc.w["emb"]] + list(w["cemb"]) + [np.zeros((cs.vocab, s.hidden), np.float32)]

@@ -294,11 +294,12 @@ def batch_max_len(name: str, frames: int | None = None) -> int:
 
 
 def make_frame_engine(name: str = "frame06b", seed: int = 0, device="cuda", frame_kernel: bool | None = None,
-                      sampled: bool = False):
+                      sampled: bool = False, wd: str = "i8row"):
     """A Qwen3Kernels engine over the seeded synthetic talker with a code predictor (workload ``name``), prior cache
     loaded, state at position ``kv``. Greedy without the processor, or with ``sampled`` the reference's default
     settings (``Sampling()``: temperature 0.9, top_k 50, repetition penalty 1.05, 2 codes before EOS, sub-codes at
-    0.9 / 50, the last 1024 ids suppressed). Returns (engine, start token, kw) where kw holds the prefill results
+    0.9 / 50, the last 1024 ids suppressed); ``wd`` the weight format. Returns (engine, start token, kw) where kw
+    holds the prefill results
     ``generate_codes`` takes (``prefill_len``, ``first_token``, ``last_hidden``, ``tts_pad_embed``) and the
     sampling settings."""
     from .fast import Sampling
@@ -309,7 +310,7 @@ def make_frame_engine(name: str = "frame06b", seed: int = 0, device="cuda", fram
     cs = workload_shape(w["cp"])
     tts, pad = make_tts_with_cp(seed, s, cs, device=device)
     smp = Sampling(max_new_tokens=4096) if sampled else Sampling.greedy(processor=False, max_new_tokens=4096)
-    eng = Qwen3Kernels(tts, smp, max_cache=w["kv"] + w["frames"] + 1, wd="i8row", sampler="fused",
+    eng = Qwen3Kernels(tts, smp, max_cache=w["kv"] + w["frames"] + 1, wd=wd, sampler="fused",
                        suppress_tail=1024 if sampled else 0, frame_kernel=frame_kernel)
     eng.talker = None
     del tts

@@ -163,7 +163,7 @@ def test_sampled_generation_matches_oracle(gpu):
     assert len(set(codes)) > 3
 
 
-def _full_frame_oracle(seed, frames, sub_sample=None, sample=None, key=0):
+def _full_frame_oracle(seed, frames, sub_sample=None, sample=None, key=0, wd="i8row"):
     """Talker (2 layers of the 0.6B shape) + code predictor (5 layers, 2048-way heads) + talker_in, composed as the
     reference's frame (qwen3/kernels.py:666-693): code predictor from (ph32, code 0), then the talker on the sum of
     the 16 code embeddings plus the pad row. Picks greedy unless (temperature, top_k) are given for the sub-codes
@@ -171,8 +171,8 @@ def _full_frame_oracle(seed, frames, sub_sample=None, sample=None, key=0):
     from oracle import talker as O
     from oracle.workload import cp_oracle, talker_oracle
 
-    torc, tok, s = talker_oracle("small06b", seed, "i8row", max_len=80)
-    corc, cs = cp_oracle("cp06b", seed)
+    torc, tok, s = talker_oracle("small06b", seed, wd, max_len=80)
+    corc, cs = cp_oracle("cp06b", seed, wd=wd)
     temb = torc.w["emb"]
     corc.w["temb"] = temb
     w = syn.cp_weights(seed, cs, 16, talker_vocab=s.vocab)
@@ -214,12 +214,13 @@ def _full_frame_oracle(seed, frames, sub_sample=None, sample=None, key=0):
 
 
 @pytest.mark.parametrize("mode", ["greedy", "greedy_frame_kernel", "sampled_per_op", "sampled",
-                                  "sampled_frame_kernel"])
+                                  "sampled_frame_kernel", "greedy_frame_kernel_i8g32"])
 def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
     """The reference's whole frame: 15 sub-codes from the code predictor (one launch, greedy or with the fused
     sampler's draws inside it; ``sampled_per_op`` runs its positions on the per-op kernels and the fused sampler),
     then the talker on talker_in of all 16 codes (per-op kernels, or one launch of the persistent talker kernel fed
-    by talker_in, greedy or sampled). The one draw counter runs through sub-codes and code 0 in frame order."""
+    by talker_in, greedy or sampled). The one draw counter runs through sub-codes and code 0 in frame order.
+    ``greedy_frame_kernel_i8g32``: the reference's serving format, every kernel of the frame persistent."""
     from sokutou_amd.fast import Sampling
     from sokutou_amd.kernels import Qwen3Kernels
 
@@ -232,9 +233,11 @@ def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
     else:
         smp = Sampling(do_sample=True, temperature=0.9, top_k=50, repetition_penalty=1.0, min_new_tokens=0,
                        max_new_tokens=64, sub_do_sample=True, sub_temperature=0.8, sub_top_k=40)
-    eng = Qwen3Kernels(tts, smp, max_cache=80, wd="i8row", sampler="fused", suppress_tail=0,
-                       frame_kernel=mode.endswith("frame_kernel"))
+    wd = "i8g32" if mode.endswith("i8g32") else "i8row"
+    eng = Qwen3Kernels(tts, smp, max_cache=80, wd=wd, sampler="fused", suppress_tail=0,
+                       frame_kernel="frame_kernel" in mode)
     assert eng.cpk is not None
+    assert ("frame_kernel" in mode) == eng.frame_kernel
     if mode == "sampled_per_op":
         eng.cpk = None  # the code predictor's positions on the per-op kernels
     kv = syn.WORKLOADS["small06b"]["kv"]
@@ -257,7 +260,7 @@ def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
     key = int(torch.randint(0, 2**62, (1,)).item())
     print(f"full frame ({mode}): building the oracle", flush=True)
     if mode.startswith("greedy"):
-        ref, otok, _ = _full_frame_oracle(seed, F)
+        ref, otok, _ = _full_frame_oracle(seed, F, wd=wd)
     else:
         ref, otok, _ = _full_frame_oracle(seed, F, sub_sample=(0.8, 40), sample=(0.9, 50), key=key)
     assert otok == tok
