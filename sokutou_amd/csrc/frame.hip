@@ -25,10 +25,11 @@ extern "C" int64_t sk_talker_workspace_size(int hidden, int inter) {
 extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* stream) {
   if (!d || n_frames <= 0) return sk_set_error(SK_EINVAL, "sk_talker_frames: bad arguments");
   if (d->nq != kNQ || d->nkv != kNKV || d->vocab != kTalkerV || d->ct != SK_CT_BF16 ||
-      !(d->wd == SK_WD_I8ROW || d->wd == SK_WD_I8G32))
+      !(d->wd == SK_WD_I8ROW || d->wd == SK_WD_I8G32 || (d->wd == SK_WD_BF16 && d->hidden == 1024)))
     return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs 16 q / 8 kv heads, vocab 3072, bf16 cache and i8row "
-                                         "or i8g32 weights");
-  if (!d->layers || !d->norm || !d->head_w || !d->head_s || !d->emb || !d->rope || !d->id0 || !d->pos || !d->workspace)
+                                         "or i8g32 weights (or bf16 weights at hidden 1024)");
+  if (!d->layers || !d->norm || !d->head_w || (!d->head_s && d->wd != SK_WD_BF16) || !d->emb || !d->rope || !d->id0 ||
+      !d->pos || !d->workspace)
     return sk_set_error(SK_EINVAL, "sk_talker_frames: null pointer");
   if (d->n_layers <= 0 || d->n_layers > Ws::kTraceLayers)
     return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: 1..32 layers");
@@ -41,9 +42,11 @@ extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* str
     return sk_set_error(SK_EINVAL, "sk_talker_frames: sampling needs seed, counter and inv_temp > 0");
   hipStream_t st = (hipStream_t)stream;
   const CpArgs none{};
-  if (d->hidden == 1024 && d->inter == 3072)
+  if (d->hidden == 1024 && d->inter == 3072) {
+    if (d->wd == SK_WD_BF16) return sk_talker_frames_bf16(d, n_frames, st);
     return d->wd == SK_WD_I8G32 ? sk_talker_frames_g32(d, n_frames, st)
                                 : launch_frames<1024, 3072, 4, kTalkerV, false>(d, none, n_frames, st);
+  }
   if (d->hidden == 2048 && d->inter == 6144) {
     static const bool regs = [] {  // read once per process
       const char* poll = std::getenv("SOKUTOU_TALKER_POLL");

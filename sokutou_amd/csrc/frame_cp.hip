@@ -15,9 +15,9 @@ extern "C" int64_t sk_cp_workspace_size(int hidden, int inter, int pair) {
 extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
   if (!d) return sk_set_error(SK_EINVAL, "sk_cp_frame: bad arguments");
   if (d->nq != kNQ || d->nkv != kNKV || d->vocab != 2048 || d->hidden != 1024 || d->inter != 3072 ||
-      !(d->wd == SK_WD_I8ROW || d->wd == SK_WD_I8G32) || d->ct != SK_CT_BF16)
+      !(d->wd == SK_WD_I8ROW || d->wd == SK_WD_I8G32 || d->wd == SK_WD_BF16) || d->ct != SK_CT_BF16)
     return sk_set_error(SK_EUNSUPPORTED, "sk_cp_frame: needs hidden 1024, intermediate 3072, 16 q / 8 kv heads, "
-                                         "vocab 2048, i8row or i8g32 weights, bf16 cache");
+                                         "vocab 2048, i8row, i8g32 or bf16 weights, bf16 cache");
   if (d->n_positions < 2 || d->n_positions > 64 || d->n_layers <= 0 || d->n_layers > Ws::kTraceLayers)
     return sk_set_error(SK_EUNSUPPORTED, "sk_cp_frame: 2..64 positions and 1..32 layers");
   if (!d->layers || !d->norm || !d->rope || !d->x0 || !d->id0 || !d->emb || !d->head_w || !d->head_s || !d->codes ||
@@ -28,6 +28,7 @@ extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
   if (d->do_sample && (!d->seed || !d->counter || !(d->inv_temp > 0.f)))
     return sk_set_error(SK_EINVAL, "sk_cp_frame: sampling needs seed, counter and inv_temp > 0");
   if (d->wd == SK_WD_I8G32) return sk_cp_frame_g32(d, (hipStream_t)stream);
+  if (d->wd == SK_WD_BF16) return sk_cp_frame_bf16(d, (hipStream_t)stream);
   sk_talker_desc t;
   CpArgs cp;
   cp_launch_args(d, t, cp);

@@ -184,6 +184,17 @@ struct Cfg {
   static __device__ bool whole(int pos) { return CP && pos + 1 <= kMaxChunk; }
   static_assert(16 % W == 0 && R_GU % W == 0 && R_GU % 2 == 0, "row split");
 };
+// The compute waves' view of Cfg for weight format WD. bf16 weights take two 16-byte loads per 16-weight chunk
+// (CH, CQ, CI count loads per lane and row), twice the registers of int8; their stages are loaded one exchange
+// before their use (kLate, kSpread) instead of a whole layer ahead, whatever the shape does for int8.
+template <int H, int I, int W, int V, bool CP, int WD>
+struct CfgW : Cfg<H, I, W, V, CP> {
+  using B = Cfg<H, I, W, V, CP>;
+  static constexpr int WB = WD == SK_WD_BF16 ? 2 : 1;
+  static constexpr int CH = B::CH * WB, CQ = B::CQ * WB, CI = B::CI * WB;
+  static constexpr bool kLate = B::kLate || WD == SK_WD_BF16;
+  static constexpr bool kSpread = B::kSpread || WD == SK_WD_BF16;
+};
 
 // LDS of the frame kernel
 template <int H, int I, int W, int V, bool CP>
@@ -524,19 +535,117 @@ __device__ __forceinline__ void dot_rows_g32(const uint4 (&w)[RW][C], const uint
 #pragma unroll
   for (int r = 0; r < RW; r++) y[r] = wave_sum(acc[r]);
 }
+// bf16 weights (the reference's Qwen3Kernels default, qwen3/kernels.py:434-437; no scales): a lane's chunk c of a
+// row is still weights 16 (lane + 64 c) .. + 15, the same GEMV input layout as int8, held in two 16-byte loads
+// (w[r][2c], w[r][2c + 1]). KEEP as for load_rows.
+template <int RW, int C2, bool LO = false, bool KEEP = false>
+__device__ __forceinline__ void load_rows_bf16(uint4 (&w)[RW][C2], const void* W, int row0, int nvalid, int K, int lane) {
+  static_assert(C2 % 2 == 0, "two loads per chunk");
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const int row = r < nvalid ? row0 + r : row0;
+    if constexpr (LO) {  // row start in the scalar offset, lane bytes (+ chunk) in the shared vector offset
+      const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)row * (uint32_t)K * 2u);
+#pragma unroll
+      for (int c = 0; c < C2 / 2; c++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+          w[r][2 * c + h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          make_rsrc(uniform(W)), (uint32_t)lane * 32u + 2048u * c + 16u * h,
+                                                          so, KEEP ? 0 : kNT));
+      continue;
+    }
+    const uint4* p = (const uint4*)((const char*)W + (size_t)row * K * 2);
+#pragma unroll
+    for (int c = 0; c < C2 / 2; c++)
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+        w[r][2 * c + h] = KEEP ? ld_keep(p + 2 * (lane + 64 * c) + h) : ld_stream(p + 2 * (lane + 64 * c) + h);
+  }
+}
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+// y[r] = (row r) . xs for bf16 rows, reduced over the wave; xs swizzled (xsw) as for int8
+template <int RW, int C2>
+__device__ __forceinline__ void dot_rows_bf16(const uint4 (&w)[RW][C2], const float* xs, int lane, float (&y)[RW]) {
+  float acc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; r++) acc[r] = 0.f;
+  const float2* xs2 = (const float2*)xs;
+#pragma unroll
+  for (int c = 0; c < C2 / 2; c++) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {  // weights 4 j .. 4 j + 3 of the chunk
+      const float2 u0 = xs2[2 * ((4 * c + j) * 64 + lane)], u1 = xs2[2 * ((4 * c + j) * 64 + lane) + 1];
+#pragma unroll
+      for (int r = 0; r < RW; r++) {
+        const uint4 hq = w[r][2 * c + (j >> 1)];
+        const uint32_t q0 = (j & 1) ? hq.z : hq.x, q1 = (j & 1) ? hq.w : hq.y;
+        float t = bf_lo(q0) * u0.x;
+        t = __builtin_fmaf(bf_hi(q0), u0.y, t);
+        t = __builtin_fmaf(bf_lo(q1), u1.x, t);
+        t = __builtin_fmaf(bf_hi(q1), u1.y, t);
+        acc[r] += t;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; r++) y[r] = wave_sum(acc[r]);
+}
+// dot_rows2 for bf16 rows (the code predictor's paired pass)
+template <int RW, int C2>
+__device__ __forceinline__ void dot_rows2_bf16(const uint4 (&w)[RW][C2], const float* xa, const float* xb, int lane,
+                                               float (&ya)[RW], float (&yb)[RW]) {
+  float aa[RW], ab[RW];
+#pragma unroll
+  for (int r = 0; r < RW; r++) { aa[r] = 0.f; ab[r] = 0.f; }
+  const float2* xa2 = (const float2*)xa;
+  const float2* xb2 = (const float2*)xb;
+  constexpr int Q = 4 * (C2 / 2);  // quarter chunks
+  float2 na0 = xa2[2 * lane], na1 = xa2[2 * lane + 1], nb0 = xb2[2 * lane], nb1 = xb2[2 * lane + 1];
+#pragma unroll
+  for (int t = 0; t < Q; t++) {
+    const float2 a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
+    if (t + 1 < Q) {
+      const int k = 2 * ((t + 1) * 64 + lane);
+      na0 = xa2[k]; na1 = xa2[k + 1]; nb0 = xb2[k]; nb1 = xb2[k + 1];
+    }
+    const int c = t >> 2, j = t & 3;
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+      const uint4 hq = w[r][2 * c + (j >> 1)];
+      const uint32_t q0 = (j & 1) ? hq.z : hq.x, q1 = (j & 1) ? hq.w : hq.y;
+      const float w0 = bf_lo(q0), w1 = bf_hi(q0), w2 = bf_lo(q1), w3 = bf_hi(q1);
+      float t0 = w0 * a0.x, u = w0 * b0.x;
+      t0 = __builtin_fmaf(w1, a0.y, t0);
+      u = __builtin_fmaf(w1, b0.y, u);
+      t0 = __builtin_fmaf(w2, a1.x, t0);
+      u = __builtin_fmaf(w2, b1.x, u);
+      t0 = __builtin_fmaf(w3, a1.y, t0);
+      u = __builtin_fmaf(w3, b1.y, u);
+      aa[r] += t0;
+      ab[r] += u;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; r++) { ya[r] = wave_sum(aa[r]); yb[r] = wave_sum(ab[r]); }
+}
 // Weight-format dispatch of the compute waves: i8row keeps one bf16 scale per row (applied by the caller through
-// row_scale), i8g32 one fp16 scale per chunk (applied inside the dot; row_scale is then 1). The group-scale arrays
-// of the i8row kernels are [1][1] and unused.
+// row_scale), i8g32 one fp16 scale per chunk (applied inside the dot; row_scale is then 1), bf16 none (row_scale 1,
+// the chunk count C doubled by CfgW). The group-scale arrays of the i8row and bf16 kernels are [1][1] and unused.
 template <int WD, int RW, int C, bool LO = false, bool KEEP = false, int GR, int GC>
 __device__ __forceinline__ void load_w(uint4 (&w)[RW][C], uint16_t (&s)[RW], uint16_t (&g)[GR][GC], const int8_t* W,
                                        const uint16_t* S, int row0, int nvalid, int K, int lane) {
-  if constexpr (WD == SK_WD_I8G32) load_rows_g32<RW, C, LO, KEEP>(w, g, W, S, row0, nvalid, K, lane);
+  if constexpr (WD == SK_WD_BF16) load_rows_bf16<RW, C, LO, KEEP>(w, W, row0, nvalid, K, lane);
+  else if constexpr (WD == SK_WD_I8G32) load_rows_g32<RW, C, LO, KEEP>(w, g, W, S, row0, nvalid, K, lane);
   else load_rows<RW, C, LO, KEEP>(w, s, W, S, row0, nvalid, K, lane);
 }
 template <int WD, int RW, int C, int GR, int GC>
 __device__ __forceinline__ void dot_w(const uint4 (&w)[RW][C], const uint16_t (&g)[GR][GC], const float* xs, int lane,
                                       float (&y)[RW]) {
-  if constexpr (WD == SK_WD_I8G32) dot_rows_g32<RW, C>(w, g, xs, lane, y);
+  if constexpr (WD == SK_WD_BF16) dot_rows_bf16<RW, C>(w, xs, lane, y);
+  else if constexpr (WD == SK_WD_I8G32) dot_rows_g32<RW, C>(w, g, xs, lane, y);
   else dot_rows<RW, C>(w, xs, lane, y);
 }
 // dot_rows2 for i8g32 weights: each chunk's sums of both inputs are scaled by the chunk's group scale, as
@@ -588,12 +697,13 @@ __device__ __forceinline__ void dot_rows2_g32(const uint4 (&w)[RW][C], const uin
 template <int WD, int RW, int C, int GR, int GC>
 __device__ __forceinline__ void dot2_w(const uint4 (&w)[RW][C], const uint16_t (&g)[GR][GC], const float* xa,
                                        const float* xb, int lane, float (&ya)[RW], float (&yb)[RW]) {
-  if constexpr (WD == SK_WD_I8G32) dot_rows2_g32<RW, C>(w, g, xa, xb, lane, ya, yb);
+  if constexpr (WD == SK_WD_BF16) dot_rows2_bf16<RW, C>(w, xa, xb, lane, ya, yb);
+  else if constexpr (WD == SK_WD_I8G32) dot_rows2_g32<RW, C>(w, g, xa, xb, lane, ya, yb);
   else dot_rows2<RW, C>(w, xa, xb, lane, ya, yb);
 }
 template <int WD>
 __device__ __forceinline__ float row_scale_of(uint16_t s) {
-  if constexpr (WD == SK_WD_I8G32) return 1.f;
+  if constexpr (WD == SK_WD_I8G32 || WD == SK_WD_BF16) return 1.f;
   else return bf2f(s);
 }
 
@@ -1509,7 +1619,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 // runs only its head. Returns false when a poll failed.
 template <int H, int I, int W, int V, bool CP, int WD, bool KEEP>
 __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
-  using C = Cfg<H, I, W, V, CP>;
+  using C = CfgW<H, I, W, V, CP, WD>;
   // lane offsets for every cell and weight access: per-load vector addresses, hoisted out of the layer loop by the
   // compiler, held ~100 registers through the pass and made it spill
   constexpr bool kLO = true;
@@ -1746,7 +1856,7 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
 
 template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP>
 __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
-  using C = Cfg<H, I, W, V, CP>;
+  using C = CfgW<H, I, W, V, CP, WD>;
   constexpr bool kLO = LaneOffsetPolls<H>::value;
   const Layout LY(H, I);
   const float eps = c.d.eps;

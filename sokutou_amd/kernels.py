@@ -185,13 +185,18 @@ def _keep_policies(layers: list, l2_keep_mb: float | None) -> int:
     return kept
 
 
+def _sptr(lin: "_Lin") -> int:
+    """Device address of a matrix's scales, 0 for the formats without (bf16, f32)."""
+    return 0 if lin.s is None else lin.s.data_ptr()
+
+
 def _layer_descs(P: _Stack, kc: list, vc: list, device) -> torch.Tensor:
     """Device array of ``sk_layer_desc`` for the layers of ``P`` with caches ``kc[i]`` / ``vc[i]``."""
     arr = (_lib.SkLayerDesc * len(P.layers))()
     for i, Ly in enumerate(P.layers):
-        arr[i] = _lib.SkLayerDesc(Ly["qkv"].w.data_ptr(), Ly["qkv"].s.data_ptr(), Ly["o"].w.data_ptr(),
-                                  Ly["o"].s.data_ptr(), Ly["gu"].w.data_ptr(), Ly["gu"].s.data_ptr(),
-                                  Ly["down"].w.data_ptr(), Ly["down"].s.data_ptr(), Ly["in_norm"].data_ptr(),
+        arr[i] = _lib.SkLayerDesc(Ly["qkv"].w.data_ptr(), _sptr(Ly["qkv"]), Ly["o"].w.data_ptr(),
+                                  _sptr(Ly["o"]), Ly["gu"].w.data_ptr(), _sptr(Ly["gu"]),
+                                  Ly["down"].w.data_ptr(), _sptr(Ly["down"]), Ly["in_norm"].data_ptr(),
                                   Ly["post_norm"].data_ptr(), Ly["qn"].data_ptr(), Ly["kn"].data_ptr(),
                                   kc[i].data_ptr(), vc[i].data_ptr())
     return torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8).to(device)
@@ -217,8 +222,8 @@ class CodePredictor:
         the Infinity Cache across the frame) instead of streaming them like the heads (``sk_cp_desc.keep_layers``).
         ``pair`` runs positions 0 and 1 as one pass with two rows per stage (the reference's cp_pair,
         qwen3/kernels.py:600-617; ``sk_cp_desc.pair``)."""
-        if wd not in ("i8row", "i8g32"):
-            raise ValueError("the code-predictor kernel reads i8row or i8g32 weights")
+        if wd not in ("i8row", "i8g32", "bf16"):
+            raise ValueError("the code-predictor kernel reads i8row, i8g32 or bf16 weights")
         proj = getattr(cp, "small_to_mtp_projection", None)
         if proj is not None and not isinstance(proj, torch.nn.Identity):
             raise NotImplementedError("a code predictor narrower than the talker (small_to_mtp_projection) is not "
@@ -252,7 +257,7 @@ class CodePredictor:
         self.layer_out: torch.Tensor | None = None
         tabs = [0, self.temb.data_ptr()] + [t.data_ptr() for t in self.cemb]
         hw = [0] + [h.w.data_ptr() for h in self.heads]
-        hs = [0] + [h.s.data_ptr() for h in self.heads]
+        hs = [0] + [_sptr(h) for h in self.heads]
         self._ptrs = torch.tensor([tabs, hw, hs], dtype=torch.int64, device=dev)
         self._layer_desc = _layer_descs(P, list(self.kc.unbind(0)), list(self.vc.unbind(0)), dev)
         self.ws = torch.zeros(int(L.sk_cp_workspace_size(P.H, P.I, int(bool(pair)))), dtype=torch.uint8, device=dev)
@@ -443,7 +448,8 @@ class Qwen3Kernels(Qwen3Fast):
         self.ck = torch.zeros((len(P.layers), P.nkv, self.G, HD), dtype=cdt, device=dev)
         self.cv = torch.zeros_like(self.ck)
         self.cpk: CodePredictor | None = None
-        fast = ((not self.s.sub_do_sample or self.fs is not None) and self.proj is None and wd in ("i8row", "i8g32")
+        fast = ((not self.s.sub_do_sample or self.fs is not None) and self.proj is None
+                and wd in ("i8row", "i8g32", "bf16")
                 and self.ct == "bf16" and (P.H, P.I, P.nq, P.nkv, self.cp_heads[0].N) == (1024, 3072, 16, 8, 2048)
                 and 2 <= self.G <= 64)
         if fast:
@@ -497,10 +503,11 @@ class Qwen3Kernels(Qwen3Fast):
 
     # --- the persistent frame kernel ------------------------------------------------------------------------
     def frame_kernel_supported(self) -> bool:
-        """The persistent kernel covers the 0.6B and 1.7B talker shapes with i8row weights or the reference's i8g32."""
+        """The persistent kernel covers the 0.6B and 1.7B talker shapes with i8row weights or the reference's i8g32,
+        and the 0.6B shape with bf16 weights (the reference's default format)."""
         P = self.T
         shapes = {(1024, 3072): 1024, (2048, 6144): 2048}
-        wd_ok = self.wd in ("i8row", "i8g32")
+        wd_ok = self.wd in ("i8row", "i8g32") or (self.wd == "bf16" and P.H == 1024)
         return (wd_ok and self.ct == "bf16" and P.nq == 16 and P.nkv == 8 and self.V == 3072
                 and (P.H, P.I) in shapes and self.max_cache <= shapes[(P.H, P.I)])
 
@@ -516,7 +523,7 @@ class Qwen3Kernels(Qwen3Fast):
         self._desc = _lib.SkTalkerDesc(
             n_layers=len(P.layers), hidden=P.H, inter=P.I, nq=P.nq, nkv=P.nkv, vocab=self.V, max_len=P.max_len,
             wd=_lib.WD[self.wd], ct=_lib.CT[self.ct], eps=P.eps, layers=self._layer_desc.data_ptr(),
-            norm=P.norm.data_ptr(), head_w=self.codec_head.w.data_ptr(), head_s=self.codec_head.s.data_ptr(),
+            norm=P.norm.data_ptr(), head_w=self.codec_head.w.data_ptr(), head_s=_sptr(self.codec_head),
             emb=self.temb.data_ptr(), rope=P.rope.data_ptr(), id0=self.id0.data_ptr(), pos=self.pos.data_ptr(),
             next_id0=self.next_id0.data_ptr(), out=self.frame_ids.data_ptr(), seen=self.seen.data_ptr(),
             ngen=self.ngen.data_ptr(), suppress=self.suppress.data_ptr() if self.suppress_tail else None,

@@ -1,5 +1,5 @@
 """The code predictor on the persistent kernel (sk_cp_frame), with its layer weights kept or streamed, positions 0
-and 1 paired or not, and i8row or i8g32 weights: greedy
+and 1 paired or not, and i8row, i8g32 or bf16 weights: greedy
 sub-codes of every position, per-layer residuals and logits at the last position, against the oracle fixture;
 graph replay; the error word."""
 
@@ -24,11 +24,13 @@ def rel_err(a, b) -> float:
 
 @pytest.fixture(scope="module",
                 params=[(True, True, "i8row"), (False, True, "i8row"), (True, False, "i8row"), (True, True, "i8g32"),
-                        (False, False, "i8g32")],
-                ids=["keep-pair", "stream-pair", "keep-serial", "i8g32-keep-pair", "i8g32-stream-serial"])
+                        (False, False, "i8g32"), (True, True, "bf16"), (True, False, "bf16")],
+                ids=["keep-pair", "stream-pair", "keep-serial", "i8g32-keep-pair", "i8g32-stream-serial",
+                     "bf16-keep-pair", "bf16-keep-serial"])
 def cp_engine(gpu, request):
     """The kernel's instantiations: layer weights loaded cacheable (the default) or streamed, positions 0 and 1
-    paired (the default) or run one after the other, i8row or i8g32 weights (the latter against its own fixture)."""
+    paired (the default) or run one after the other, i8row, i8g32 or bf16 weights (each format against its own
+    fixture)."""
     keep, pair, wd = request.param
     print(f"cp06b: building the seeded code predictor (5 layers, 15 heads), keep_layers={keep} pair={pair} wd={wd}",
           flush=True)

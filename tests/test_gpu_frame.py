@@ -86,15 +86,16 @@ def test_talker06b_64_frames_one_launch(gpu):
     assert int(eng.pos.item()) == meta["start_pos"] + 64
 
 
-@pytest.mark.parametrize("name,seed", [("talker06b", 0), ("talker17b", 1)])
-def test_talker_i8g32_64_frames_one_launch(gpu, name, seed):
-    """The reference's i8g32 weights (fp16 scale per 32 weights, applied per 16-weight chunk) on the persistent
-    kernel: per-layer residuals and logits of frame 0, then 63 frames in one launch, against the i8g32 oracle.
-    The 1.7B fixture uses seed 1 (seed 0 has a top-2 logit margin of 2e-5 at one frame)."""
-    print(f"{name} i8g32 seed {seed}: frame 0 with residuals, then 63 frames in one launch", flush=True)
-    meta = json.loads((GOLD / f"{name}_i8g32_seed{seed}.json").read_text())
-    gold = np.load(GOLD / f"{name}_i8g32_seed{seed}.npz")
-    eng, tok = syn.make_engine(name, seed=seed, wd="i8g32", device=gpu, frame_kernel=True)
+@pytest.mark.parametrize("name,seed,wd", [("talker06b", 0, "i8g32"), ("talker17b", 1, "i8g32"), ("talker06b", 0, "bf16")])
+def test_talker_other_formats_64_frames_one_launch(gpu, name, seed, wd):
+    """The reference's i8g32 weights (fp16 scale per 32 weights, applied per 16-weight chunk) and its bf16 default
+    (0.6B shape) on the persistent kernel: per-layer residuals and logits of frame 0, then 63 frames in one launch,
+    against the oracle of the same format. The 1.7B i8g32 fixture uses seed 1 (seed 0 has a top-2 logit margin of
+    2e-5 at one frame)."""
+    print(f"{name} {wd} seed {seed}: frame 0 with residuals, then 63 frames in one launch", flush=True)
+    meta = json.loads((GOLD / f"{name}_{wd}_seed{seed}.json").read_text())
+    gold = np.load(GOLD / f"{name}_{wd}_seed{seed}.npz")
+    eng, tok = syn.make_engine(name, seed=seed, wd=wd, device=gpu, frame_kernel=True)
     assert eng.frame_kernel and tok == meta["start_token"]
     H = syn.workload_shape(name).hidden
     eng.layer_out = torch.zeros((28, H), device=gpu)

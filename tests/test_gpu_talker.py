@@ -214,13 +214,14 @@ def _full_frame_oracle(seed, frames, sub_sample=None, sample=None, key=0, wd="i8
 
 
 @pytest.mark.parametrize("mode", ["greedy", "greedy_frame_kernel", "sampled_per_op", "sampled",
-                                  "sampled_frame_kernel", "greedy_frame_kernel_i8g32"])
+                                  "sampled_frame_kernel", "greedy_frame_kernel_i8g32", "greedy_frame_kernel_bf16"])
 def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
     """The reference's whole frame: 15 sub-codes from the code predictor (one launch, greedy or with the fused
     sampler's draws inside it; ``sampled_per_op`` runs its positions on the per-op kernels and the fused sampler),
     then the talker on talker_in of all 16 codes (per-op kernels, or one launch of the persistent talker kernel fed
     by talker_in, greedy or sampled). The one draw counter runs through sub-codes and code 0 in frame order.
-    ``greedy_frame_kernel_i8g32``: the reference's serving format, every kernel of the frame persistent."""
+    ``greedy_frame_kernel_i8g32`` / ``_bf16``: the reference's serving format and its Qwen3Kernels default, every
+    kernel of the frame persistent."""
     from sokutou_amd.fast import Sampling
     from sokutou_amd.kernels import Qwen3Kernels
 
@@ -233,7 +234,7 @@ def test_full_frame_with_code_predictor_matches_oracle(gpu, mode):
     else:
         smp = Sampling(do_sample=True, temperature=0.9, top_k=50, repetition_penalty=1.0, min_new_tokens=0,
                        max_new_tokens=64, sub_do_sample=True, sub_temperature=0.8, sub_top_k=40)
-    wd = "i8g32" if mode.endswith("i8g32") else "i8row"
+    wd = mode.rsplit("_", 1)[1] if mode.endswith(("i8g32", "bf16")) else "i8row"
     eng = Qwen3Kernels(tts, smp, max_cache=80, wd=wd, sampler="fused", suppress_tail=0,
                        frame_kernel="frame_kernel" in mode)
     assert eng.cpk is not None
