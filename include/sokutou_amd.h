@@ -198,7 +198,8 @@ int64_t sk_talker_workspace_size(int hidden, int inter);
  * device exactly as the fused sampler advances it (id0, next_id0, seen, ngen, pos += 1 per frame).
  * 256 persistent workgroups (one per CU, grouped by XCD: kv head x on XCD x) exchange activations through the
  * workspace. Supports the 0.6B (H 1024, I 3072) and 1.7B (H 2048, I 6144) talkers: 16 q / 8 kv heads, vocab
- * 3072, i8row weights, bf16 cache, max_len <= 2048, a 256-CU device.
+ * 3072, i8row or i8g32 weights (and bf16 at H 1024; head_s may then be null), bf16 cache, max_len <= 2048, a
+ * 256-CU device.
  * Replaces, for greedy decoding, the talker half of Qwen3Kernels._frame (qwen3/kernels.py:676-685): talker_in /
  * embed, _layers (rms_gemv, attn, gemv, rms_gemv, gemv per layer, qwen3/kernels.py:619-627), rmsnorm, gemv
  * (codec_head) and sample (qwen3/sampler.py:37-159 with do_sample = 0). */
@@ -250,8 +251,8 @@ int64_t sk_cp_workspace_size(int hidden, int inter, int pair);
 /* All positions of the code predictor of one frame in ONE launch, or two with desc->pair (the paired pass of
  * positions 0 and 1, then the rest), of the persistent kernel of sk_talker_frames in its code-predictor mode:
  * greedy sub-codes 1..n_positions-1. Supports the Qwen3-TTS code predictor shape:
- * hidden 1024, intermediate 3072, 16 q / 8 kv heads, vocab 2048, i8row or i8g32 weights (layers and heads),
- * bf16 cache, a 256-CU device.
+ * hidden 1024, intermediate 3072, 16 q / 8 kv heads, vocab 2048, i8row, i8g32 or bf16 weights (layers and heads;
+ * head_s entries may be 0 for bf16), bf16 cache, a 256-CU device.
  * Replaces, for greedy sub-codes, the code-predictor loop of Qwen3Kernels._frame (qwen3/kernels.py:666-675) with
  * _cp_first / _cp_input (qwen3/kernels.py:629-655), _layers (619-627), rms_gemv over cp_heads[g - 1] and sample
  * (qwen3/sampler.py:37-159 with do_sample = 0, no processor). Positions 0 and 1 run one after the other, or as one
