@@ -3,7 +3,9 @@
 // Four compute waves leave the control wave 256 registers, enough to poll every exchange straight into registers
 // (the 0.6B kernels' polls); a full layer of 1.7B weights does not fit in the compute waves' registers beside the
 // rest, so each stage's weights are loaded one exchange before their use (SpreadLate; issuing o and gate/up
-// together after the attention measured 28.4 us per layer). Every cell, weight-row and cache access of this shape
+// together after the attention measured 28.4 us per layer), except the first half of the gate/up rows, which goes
+// out with o (SplitGateUp: 25 MB of gate/up weights per layer take longer than one exchange to stream; 24.2
+// against 25.2 us per layer). Every cell, weight-row and cache access of this shape
 // keeps its lane part in one shared vector offset and its uniform part in the scalar offset (LaneOffsetPolls):
 // with a vector address per access the waves spilled ~140 addresses and reloaded them from scratch on every
 // exchange; with the shared offsets nothing spills. Measured on the 64-frame 1.7B workload: 25.3 us per layer,
@@ -20,6 +22,10 @@ struct SpreadLate<kH, kI> {
 };
 template <>
 struct LaneOffsetPolls<kH> {
+  static constexpr bool value = true;
+};
+template <>
+struct SplitGateUp<kH, kI> {
   static constexpr bool value = true;
 };
 static_assert(Cfg<kH, kI, 4, kTalkerV, false>::kMaxLen >= 2048, "1.7B caches up to 2048 positions");

@@ -16,6 +16,10 @@ template <>
 struct LaneOffsetPolls<kH> {
   static constexpr bool value = true;
 };
+template <>
+struct SplitGateUp<kH, kI> {
+  static constexpr bool value = true;
+};
 
 }  // namespace
 

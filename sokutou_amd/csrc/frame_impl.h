@@ -161,6 +161,13 @@ template <int H>
 struct LaneOffsetPolls {
   static constexpr bool value = false;
 };
+// With kSpread: the first half of each wave's gate/up rows is loaded with o, after the attention (two exchanges
+// before their use), the second half one exchange before, as kSpread loads them all. The hidden-2048 gate/up
+// rows stream 25 MB per layer, more than one exchange can hide. Off unless a translation unit specialises it.
+template <int H, int I>
+struct SplitGateUp {
+  static constexpr bool value = false;
+};
 
 template <int H, int I, int W, int V, bool CP>
 struct Cfg {
@@ -1884,6 +1891,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   uint4 wq[C::RW_QKV][C::CH], wo[C::RW_O][C::CQ], wg[C::RW_GU][C::CH], wd[C::RW_D][C::CI];
   uint16_t sq[C::RW_QKV], so[C::RW_O], sg[C::RW_GU], sd[C::RW_D];  // raw bf16 row scales
   constexpr bool G32 = WD == SK_WD_I8G32;  // i8g32: raw fp16 group scales, one per row and chunk
+  constexpr bool kSplitGu = C::kSpread && SplitGateUp<H, I>::value && C::RW_GU % 2 == 0;
+  constexpr int kGuH = C::RW_GU / 2;
   uint16_t gq[G32 ? C::RW_QKV : 1][G32 ? C::CH : 1], go[G32 ? C::RW_O : 1][G32 ? C::CQ : 1];
   uint16_t gg[G32 ? C::RW_GU : 1][G32 ? C::CH : 1], gd[G32 ? C::RW_D : 1][G32 ? C::CI : 1];
   uint4 kr[C::KVL], vr[C::KVL];
@@ -2075,8 +2084,13 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         }
         if constexpr (C::kLate) {
           load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
-          if constexpr (!C::kSpread)
+          if constexpr (!C::kSpread) {
             load_w<WD, C::RW_GU, C::CH, kLO, KEEP>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+          } else if constexpr (kSplitGu) {  // the first half of the gate/up rows
+            load_w<WD, kGuH, C::CH, kLO, KEEP>(*(uint4(*)[kGuH][C::CH]) & wg[0], *(uint16_t(*)[kGuH]) & sg[0],
+                                               *(uint16_t(*)[G32 ? kGuH : 1][G32 ? C::CH : 1]) & gg[0],
+                                               (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, kGuH, H, lane);
+          }
         }
       }
       // ---- S4: o projection rows, added to the layer's input residual ------------------------------------
@@ -2097,8 +2111,13 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         publish<W, kLO>(S, c.cells, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
         if (tid == 0) c.tr(1, f, l, 5);
         if constexpr (!C::kLate) load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
-        if constexpr (C::kSpread)
+        if constexpr (C::kSpread && kSplitGu) {  // the second half of the gate/up rows
+          load_w<WD, kGuH, C::CH, kLO, KEEP>(*(uint4(*)[kGuH][C::CH]) & wg[kGuH], *(uint16_t(*)[kGuH]) & sg[kGuH],
+                                             *(uint16_t(*)[G32 ? kGuH : 1][G32 ? C::CH : 1]) & gg[G32 ? kGuH : 0],
+                                             (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0 + kGuH, kGuH, H, lane);
+        } else if constexpr (C::kSpread) {
           load_w<WD, C::RW_GU, C::CH, kLO, KEEP>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
+        }
       }
       // ---- S5: gate/up rows with the RMSNorm scale, SwiGLU ----------------------------------------------
       wg_sync();
