@@ -1,11 +1,12 @@
 """Per-stage timing of the persistent frame kernel from its own trace stamps.
 
-    python -m sokutou_amd.stage_trace [talker06b|talker17b] [--frames N]
+    python -m sokutou_amd.stage_trace [talker06b|talker17b|cp06b] [--frames N]
 
 The kernel keeps optional wall-clock stamps (100 MHz) of frame 0 of a launch for every workgroup and layer when
 the workspace's trace word is set: the compute waves stamp the start of each stage (after its barrier), the end of
 each dot and their publication; the control wave stamps when each stage's input has arrived and been staged. This
-tool runs one traced launch of the synthetic workload, then prints, as markdown:
+tool runs one traced launch of the synthetic workload (for the code predictor: one frame with positions 0 and 1
+unpaired, so that frame 0 of the launch is position 0's pass), then prints, as markdown:
 
 * the median time of each step of a layer (median over the 256 workgroups and the middle layers);
 * each exchange: from the last producer's publication to the median consumer's input being ready;
@@ -36,34 +37,47 @@ K_START, K_S1IN, K_QKV, K_ATTB, K_MRGPOLL, K_MRGDONE, K_ATT, K_HMID, K_ACT = 0, 
 
 
 def traced_launch(name: str, frames: int = 2):
-    """Builds the workload's engine, warms it up, then runs one launch of ``frames`` frames with tracing on.
-    Returns (stamps in us as float64 [256, 2, 32, 16], shape, us of the launch)."""
+    """Builds the workload's engine, warms it up, then runs one launch of ``frames`` frames (the code predictor:
+    one frame of all its positions) with tracing on. Returns (stamps in us as float64 [256, 2, 32, 16], shape, us
+    of the launch)."""
     dev = torch.device("cuda:0")
-    eng, tok = syn.make_engine(name, seed=0, wd="i8row", device=dev, frame_kernel=True)
     s = syn.workload_shape(name)
-    kv = syn.WORKLOADS[name]["kv"]
     L = _lib.load()
     total = int(L.sk_talker_workspace_size(s.hidden, s.inter))
     nbytes = _WG * 2 * _TRACE_LAYERS * _TRACE_EVENTS * 8
+    if name == "cp06b":
+        eng = syn.make_cp_engine(name, 0, dev, keep_layers=True, pair=False)
+        x0, id0 = syn.cp_frame_inputs(0, 0, s)
+        eng.x0.copy_(torch.from_numpy(x0))
+        eng.id0.fill_(id0)
+        ws, run, err = eng.ws, eng.run, eng.error
+    else:
+        eng, tok = syn.make_engine(name, seed=0, wd="i8row", device=dev, frame_kernel=True)
+        kv = syn.WORKLOADS[name]["kv"]
+        ws, err = eng.frame_ws, eng.frame_error
+
+        def run():
+            eng.reset(kv, tok)
+            eng.run_frames(frames)
     for _ in range(3):
-        eng.reset(kv, tok)
-        eng.run_frames(frames)
-    eng.frame_ws[32:36].view(torch.int32).fill_(1)
-    eng.reset(kv, tok)
+        run()
+    ws[32:36].view(torch.int32).fill_(1)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    eng.run_frames(frames)
+    run()
     e1.record()
     torch.cuda.synchronize()
-    if eng.frame_error():
-        raise RuntimeError(f"frame kernel error {eng.frame_diag()}")
-    raw = eng.frame_ws[total - nbytes:total].view(torch.int64).view(_WG, 2, _TRACE_LAYERS, _TRACE_EVENTS)
-    eng.frame_ws[32:36].zero_()
+    if err():
+        raise RuntimeError(f"frame kernel error {err()}")
+    raw = ws[total - nbytes:total].view(torch.int64).view(_WG, 2, _TRACE_LAYERS, _TRACE_EVENTS)
+    ws[32:36].zero_()
     return raw.cpu().numpy().astype(np.float64) * 0.01, s, e0.elapsed_time(e1) * 1e3
 
 
-def summarise(t: np.ndarray, n_layers: int) -> dict:
-    """Medians of the layer steps and exchanges over workgroups and the middle layers (1 .. n_layers - 2)."""
+def summarise(t: np.ndarray, n_layers: int, whole_attention: bool = False) -> dict:
+    """Medians of the layer steps and exchanges over workgroups and the middle layers (1 .. n_layers - 2).
+    ``whole_attention``: every workgroup attends over the whole cache (the code predictor), so there are no
+    partials to merge and the attention output is written by the workgroups themselves during S2."""
     ctl, cmp_ = t[:, 0], t[:, 1]
     layers = range(1, min(n_layers, _TRACE_LAYERS) - 1)
     xcd = np.arange(_WG) // 32  # the kernel's dense rank: workgroup g = 32 * XCD + rank
@@ -92,11 +106,17 @@ def summarise(t: np.ndarray, n_layers: int) -> dict:
         last = np.array([cmp_[xcd == x, l, ev].max() for x in range(8)])
         return last[xcd]
 
+    if whole_attention:
+        att = [("attention output (global, 256 producers, written during S2)",
+                lambda l: np.median(ctl[:, l, K_ATT]) - cmp_[:, l, C_S2END].max())]
+    else:
+        att = [("attention partials (XCD-local, 32 producers)", lambda l: np.median(ctl[:, l, K_MRGPOLL] - local_last(l, C_S2END))),
+               ("attention output (global, 256 producers; from the partials' arrival)",
+                lambda l: np.median(ctl[:, l, K_ATT] - ctl[:, l, K_MRGPOLL]))]
     exchanges = [
         ("residual h (global, 256 producers)", lambda l: np.median(ctl[:, l + 1, K_S1IN]) - cmp_[:, l, C_S6PUB].max()),
         ("q|k|v of the head (XCD-local, 32 producers)", lambda l: np.median(ctl[:, l, K_QKV] - local_last(l, C_S1PUB))),
-        ("attention partials (XCD-local, 32 producers)", lambda l: np.median(ctl[:, l, K_MRGPOLL] - local_last(l, C_S2END))),
-        ("attention output (global, 256 producers; from the partials' arrival)", lambda l: np.median(ctl[:, l, K_ATT] - ctl[:, l, K_MRGPOLL])),
+        *att,
         ("h after o (global, 256 producers)", lambda l: np.median(ctl[:, l, K_HMID]) - cmp_[:, l, C_S4PUB].max()),
         ("SwiGLU activation (global, 256 producers)", lambda l: np.median(ctl[:, l, K_ACT]) - cmp_[:, l, C_S5PUB].max()),
     ]
@@ -106,9 +126,10 @@ def summarise(t: np.ndarray, n_layers: int) -> dict:
 
 
 def to_markdown(name: str, s, summ: dict, launch_us: float, frames: int) -> str:
-    out = [f"Workload {name}: {s.n_layers} layers, hidden {s.hidden}, intermediate {s.inter}; one traced launch of "
-           f"{frames} frames ({launch_us:.1f} us, stamps of frame 0). Medians over the 256 workgroups and layers "
-           f"{summ['layers']}.", "", "| step of a layer | us |", "|---|---|"]
+    what = ("one traced launch of one frame, positions 0 and 1 unpaired ({:.1f} us, stamps of position 0)".format(launch_us)
+            if name == "cp06b" else f"one traced launch of {frames} frames ({launch_us:.1f} us, stamps of frame 0)")
+    out = [f"Workload {name}: {s.n_layers} layers, hidden {s.hidden}, intermediate {s.inter}; {what}. Medians over "
+           f"the 256 workgroups and layers {summ['layers']}.", "", "| step of a layer | us |", "|---|---|"]
     out += [f"| {n} | {v:.2f} |" for n, v in summ["steps"]]
     out += [f"| **layer (S1 start to next S1 start)** | **{summ['layer_us']:.2f}** |", "",
             "| exchange: last producer's publication -> median consumer's input ready | us |", "|---|---|"]
@@ -118,11 +139,11 @@ def to_markdown(name: str, s, summ: dict, launch_us: float, frames: int) -> str:
 
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", nargs="?", default="talker06b", choices=["talker06b", "talker17b"])
+    ap.add_argument("workload", nargs="?", default="talker06b", choices=["talker06b", "talker17b", "cp06b"])
     ap.add_argument("--frames", type=int, default=2)
     a = ap.parse_args(argv)
     t, s, us = traced_launch(a.workload, a.frames)
-    print(to_markdown(a.workload, s, summarise(t, s.n_layers), us, a.frames), flush=True)
+    print(to_markdown(a.workload, s, summarise(t, s.n_layers, a.workload == "cp06b"), us, a.frames), flush=True)
 
 
 if __name__ == "__main__":
