@@ -1073,6 +1073,20 @@ __device__ __forceinline__ void load_kv(uint4 (&kr)[KVL], uint4 (&vr)[KVL], cons
   }
 }
 
+// K/V of a code-predictor launch of at most 16 positions (F16), for one workgroup's attention slice: lane
+// 16 qq + j holds dims 32 qq .. 32 qq + 31 of K at position j (four 16-byte loads) and dims d0 + 2 qq, + 1 of V
+// (one 4-byte load). Positions beyond npos load position npos (< max_len): unconditional loads, as load_kv.
+__device__ __forceinline__ void load_kv16(uint4 (&kf)[4], uint32_t& vf, const bf16_t* Kh, const bf16_t* Vh, int npos,
+                                          int d0, int lane) {
+  const int j = lane & 15, qq = lane >> 4;
+  const int t = min(j, npos);
+  const uint32_t ko = (uint32_t)(t * SK_HD + 32 * qq) * 2u;
+#pragma unroll
+  for (int e = 0; e < 4; e++)
+    kf[e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Kh)), ko + 16u * e, 0, kPolDev));
+  vf = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(uniform(Vh)), (uint32_t)(t * SK_HD + d0 + 2 * qq) * 2u, 0, kPolDev);
+}
+
 __device__ __forceinline__ void unpack8(uint4 a, float* o) {
   o[0] = bf2f(a.x & 0xffffu); o[1] = bf2f(a.x >> 16); o[2] = bf2f(a.y & 0xffffu); o[3] = bf2f(a.y >> 16);
   o[4] = bf2f(a.z & 0xffffu); o[5] = bf2f(a.z >> 16); o[6] = bf2f(a.w & 0xffffu); o[7] = bf2f(a.w >> 16);
@@ -1225,7 +1239,7 @@ __device__ __forceinline__ bool ctl_pair_pass(const Ctx& c, Lds<H, I, W, V, CP>&
   return true;
 }
 
-template <int H, int I, int W, int V, bool CP, bool SMP>
+template <int H, int I, int W, int V, bool CP, bool SMP, bool F16 = false>
 __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
   // 4 compute waves (256 registers for the control wave): the RMSNorm inputs are polled into registers and staged
   // from there (kNP element pairs per lane); with 8 compute waves (168 registers) they are staged through LDS
@@ -1343,7 +1357,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
       if (!ok) return;
-      for (int b = 0; b < attn_barriers(ck); b++) wg_sync();
+      for (int b = 0; b < (CP && F16 ? 1 : attn_barriers(ck)); b++) wg_sync();
       if (lane == 0) c.tr(0, f, l, 3);
       // S3: merge of the 32 chunk partials for q head 2x + r/16, dims [8 (r % 16), 8 (r % 16) + 8)
       {
@@ -1861,7 +1875,7 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
   return true;
 }
 
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool F16 = false>
 __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int tid, int lane) {
   using C = CfgW<H, I, W, V, CP, WD>;
   constexpr bool kLO = LaneOffsetPolls<H>::value;
@@ -1896,6 +1910,12 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   uint16_t gq[G32 ? C::RW_QKV : 1][G32 ? C::CH : 1], go[G32 ? C::RW_O : 1][G32 ? C::CQ : 1];
   uint16_t gg[G32 ? C::RW_GU : 1][G32 ? C::CH : 1], gd[G32 ? C::RW_D : 1][G32 ? C::CI : 1];
   uint4 kr[C::KVL], vr[C::KVL];
+  // F16 (a code-predictor launch of at most 16 positions): wave 0 computes this workgroup's attention slice alone,
+  // from K / V loaded in load_kv16's layout
+  constexpr bool kF16 = CP && F16;
+  uint4 kf[kF16 ? 4 : 1];
+  uint32_t vf = 0;
+  const int sl_p = r >> 4, sl_d0 = 8 * (r & 15);  // the slice: q head 2x + sl_p, dims sl_d0 .. sl_d0 + 7
   // RoPE row (cos, sin of pair `lane`) and the norm weights of dims lane, lane + 64 for this wave's vector in
   // the next attention (q norm for waves 0, 1, k norm for wave 2; loaded by every compute wave: no select on
   // loaded values, only on the address)
@@ -1913,7 +1933,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   {
     const sk_layer_desc& L0 = S.desc[0];
     load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
-    load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), make_chunk<CP>(p0, r, C::whole(p0)), cw, ag, asl);
+    if constexpr (kF16) load_kv16(kf, vf, c.kh(L0), c.vh(L0), p0, sl_d0, lane);
+    else load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), make_chunk<CP>(p0, r, C::whole(p0)), cw, ag, asl);
     load_attn_vec(L0, p0);
     if constexpr (!C::kLate) {
       load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)L0.o_w, L0.o_s, o_w0, o_wn, kQ, lane);
@@ -1995,6 +2016,37 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           }
         }
         wg_sync();  // attention barrier 1
+        if constexpr (kF16) {
+          // (2') wave 0: this workgroup's slice over the whole cache (<= 16 positions), no further barrier. Lane
+          // 16 qq + j: q . k_j over dims 32 qq .. + 31, summed over the four quarters; softmax over j within
+          // each row; the slice's dims 2 qq, 2 qq + 1 summed over j within the row.
+          if (cw == 0) {
+            const int j = lane & 15, qq = lane >> 4;
+            float k32[32];
+            if (j == pos) {
+#pragma unroll
+              for (int e = 0; e < 32; e++) k32[e] = S.kn[32 * qq + e];
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; e++) unpack8(kf[e], k32 + 8 * e);
+            }
+            float sc = 0.f;
+#pragma unroll
+            for (int e = 0; e < 32; e++) sc = __builtin_fmaf(S.qs[sl_p][32 * qq + e], k32[e], sc);
+            sc += __shfl_xor(sc, 16);
+            sc += __shfl_xor(sc, 32);
+            const float sv = j <= pos ? sc : -INFINITY;
+            const float mx = row16_max(sv);
+            const float ew = j <= pos ? expf(sv - mx) : 0.f;
+            const float lw = row16_sum(ew);
+            const float v0 = j == pos ? S.vn[sl_d0 + 2 * qq] : bf2f(vf & 0xffffu);
+            const float v1 = j == pos ? S.vn[sl_d0 + 2 * qq + 1] : bf2f(vf >> 16);
+            const float o0 = row16_sum(ew * v0), o1 = row16_sum(ew * v1);
+            if (j == 0)
+              put2(c.cells, LY.e3 + (2 * x + sl_p) * SK_HD + sl_d0 + 2 * qq, lw > 0.f ? o0 / lw : 0.f,
+                   lw > 0.f ? o1 / lw : 0.f, c.tick(f, l, 2));
+          }
+        } else {
         float m = -INFINITY, lsum = 0.f, o = 0.f;
         if (ck.n > 0) {
           // (2) scores of this chunk's positions (kr from the prefetch; the new position from LDS)
@@ -2077,9 +2129,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
             put(c.cells, pb + 4 + p * SK_HD + dd, o, e);
           }
         }
+        }
         if (tid == 0) c.tr(1, f, l, 3);
         if constexpr (!C::kSpread) {
-          load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
+          if constexpr (kF16) load_kv16(kf, vf, c.kh(Ln), c.vh(Ln), npos, sl_d0, lane);
+          else load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
           load_attn_vec(Ln, npos);
         }
         if constexpr (C::kLate) {
@@ -2166,7 +2220,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         if constexpr (!C::kLate) load_w<WD, C::RW_D, C::CI, kLO, KEEP>(wd, sd, gd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
         if constexpr (C::kSpread) {
           load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
-          load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
+          if constexpr (kF16) load_kv16(kf, vf, c.kh(Ln), c.vh(Ln), npos, sl_d0, lane);
+          else load_kv<W, C::KVL>(kr, vr, c.kh(Ln), c.vh(Ln), make_chunk<CP>(npos, r, C::whole(npos)), cw, ag, asl);
           load_attn_vec(Ln, npos);
         }
       }
@@ -2223,7 +2278,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
 // PAIRK: the code predictor's paired pass alone (positions 0 and 1, no head), launched before the frames of a
 // cp.pair launch (which then start at frame 1's head): a kernel of its own, so that its registers do not add to
 // the frame loop's (inlined into the same kernel, the pass made the loop's values spill).
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK = false>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK = false, bool F16 = false>
 __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArgs cp, int n_frames) {
   extern __shared__ char smem_raw[];
   Lds<H, I, W, V, CP>& S = *(Lds<H, I, W, V, CP>*)smem_raw;
@@ -2288,10 +2343,11 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   {
     // default start delays per exchange, overridable through the workspace: tuned by coordinate descent on the
     // 0.6B talker, on the 1.7B talker for the spread prefetch (longer exchanges; the merge poll starts ~3 us
-    // after the attention) and on the code predictor (no merge; whole-cache attention)
+    // after the attention) and on the code predictor (no merge; the single-wave attention of F16 with the paired
+    // pass: 1008 -> 945 us per frame)
     constexpr uint8_t kDefault[Ws::kHops] = {17, 23, 31, 21, 17, 34, 34, 24};
     constexpr uint8_t kDefaultSpread[Ws::kHops] = {53, 3, 91, 55, 51, 36, 0, 46};
-    constexpr uint8_t kDefaultCp[Ws::kHops] = {20, 14, 35, 35, 29, 32, 17, 23};
+    constexpr uint8_t kDefaultCp[Ws::kHops] = {18, 14, 43, 25, 19, 30, 17, 25};
     const uint32_t w0 = ld_u32_dev(ws, Ws::kPollDelay), w1 = ld_u32_dev(ws, Ws::kPollDelay + 4);
 #pragma unroll
     for (int h = 0; h < Ws::kHops; h++) {
@@ -2305,8 +2361,8 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     if (wave == W) ctl_pair_pass<H, I, W, V, CP>(c, S, lane);
     else compute_pair<H, I, W, V, CP, WD, KEEP>(c, S, wave, tid, lane);
   } else {
-    if (wave == W) run_control<H, I, W, V, CP, SMP>(c, S, lane);
-    else run_compute<H, I, W, V, CP, SMP, WD, KEEP>(c, S, wave, tid, lane);
+    if (wave == W) run_control<H, I, W, V, CP, SMP, F16>(c, S, lane);
+    else run_compute<H, I, W, V, CP, SMP, WD, KEEP, F16>(c, S, wave, tid, lane);
   }
   // ---- end of launch: epoch base and launch count (workgroup 0; every workgroup finished its census) --------
   if (c.g == 0 && tid == 0) {
@@ -2319,14 +2375,14 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
 // cannot hold a workgroup, would only surface as poll timeouts). Done once per device and instantiation; a failure
 // is reported every time and retried on the next call.
 constexpr int kMaxDevices = 64;
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK, bool F16>
 int prepare_kernel(size_t lds) {
   static bool ready[kMaxDevices] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return sk_set_error(SK_EDEVICE, "sk_talker_frames: no current HIP device");
   if (ready[dev]) return SK_OK;
-  const void* fn = (const void*)k_frames<H, I, W, V, CP, SMP, WD, KEEP, PAIRK>;
+  const void* fn = (const void*)k_frames<H, I, W, V, CP, SMP, WD, KEEP, PAIRK, F16>;
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return sk_check_launch(e, "sk_talker_frames: raising the LDS limit");
   int cus = 0, per_cu = 0;
@@ -2341,13 +2397,13 @@ int prepare_kernel(size_t lds) {
   ready[dev] = true;
   return SK_OK;
 }
-template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK = false>
+template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK = false, bool F16 = false>
 int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
   constexpr size_t need = sizeof(Lds<H, I, W, V, CP>) + (PAIRK ? sizeof(LdsPair<H, I>) : 0);
   const size_t lds = need < 96 * 1024 ? 96 * 1024 : need;  // one workgroup per CU
-  const int rc = prepare_kernel<H, I, W, V, CP, SMP, WD, KEEP, PAIRK>(lds);
+  const int rc = prepare_kernel<H, I, W, V, CP, SMP, WD, KEEP, PAIRK, F16>(lds);
   if (rc != SK_OK) return rc;
-  hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP, WD, KEEP, PAIRK>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp,
+  hipLaunchKernelGGL((k_frames<H, I, W, V, CP, SMP, WD, KEEP, PAIRK, F16>), dim3(kWG), dim3((W + 1) * 64), lds, st, *d, cp,
                      n_frames);
   return sk_check_launch(hipGetLastError(), "sk_talker_frames");
 }
@@ -2361,6 +2417,11 @@ int launch_frames(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipSt
       const int rc = launch_kernel<H, I, W, V, CP, false, WD, KEEP, true>(d, cp, n_frames, st);
       if (rc != SK_OK) return rc;
     }
+  }
+  if constexpr (CP) {
+    if (d->max_len <= 16)  // the code predictor's 16 positions: the whole-cache attention of F16
+      return d->do_sample ? launch_kernel<H, I, W, V, CP, true, WD, KEEP, false, true>(d, cp, n_frames, st)
+                          : launch_kernel<H, I, W, V, CP, false, WD, KEEP, false, true>(d, cp, n_frames, st);
   }
   return d->do_sample ? launch_kernel<H, I, W, V, CP, true, WD, KEEP>(d, cp, n_frames, st)
                       : launch_kernel<H, I, W, V, CP, false, WD, KEEP>(d, cp, n_frames, st);
