@@ -62,11 +62,12 @@ def talker_oracle(name: str, seed: int = 0, wd: str = "i8row", max_len: int | No
 
 
 def cp_oracle(name: str = "cp06b", seed: int = 0, wd: str = "i8row", cache_bf16: bool = True,
-              digests: dict | None = None):
-    """Returns (CodePredictorOracle, shape) for a code-predictor workload, weights quantised by the oracle."""
+              digests: dict | None = None, positions: int | None = None):
+    """Returns (CodePredictorOracle, shape) for a code-predictor workload, weights quantised by the oracle;
+    ``positions`` overrides the workload's count of positions (and so of heads and code tables)."""
     spec = syn.WORKLOADS[name]
     s = syn.workload_shape(name)
-    n = spec["positions"]
+    n = positions or spec["positions"]
     w = syn.cp_weights(seed, s, n)
     if digests is not None:
         digests["layer0.q"] = syn.sha256(w["layers"][0]["q"])

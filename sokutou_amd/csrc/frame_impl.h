@@ -1057,9 +1057,29 @@ __device__ __forceinline__ ChunkOf<CP> make_chunk(int pos, int r, bool whole) {
   else return Chunk(pos, r);
 }
 
+// Reduce-scatter of 16 values over the 16 lanes of a row: lane i of the row returns the row's sum of v[i]. Four
+// exchanges between partner lanes (row_mirror i <-> 15 - i, row_half_mirror i <-> 7 - i within each half, then
+// xor 2 and xor 1), each partner keeping the half of its values selected by the lane bit that tells it from the
+// other (bits 3, 2, 1, 0 in turn) and adding the partner's copy of that half: 15 DPP adds instead of the 64 of 16
+// row sums.
+__device__ __forceinline__ float row16_reduce_scatter(const float (&v)[16], int lane) {
+  float a[8], b[4], c[2];
+  const bool h3 = lane & 8, h2 = lane & 4, h1 = lane & 2, h0 = lane & 1;
+#pragma unroll
+  for (int j = 0; j < 8; j++) a[j] = (h3 ? v[8 + j] : v[j]) + dpp<0x140>(h3 ? v[j] : v[8 + j]);  // row_mirror
+#pragma unroll
+  for (int j = 0; j < 4; j++) b[j] = (h2 ? a[4 + j] : a[j]) + dpp<0x141>(h2 ? a[j] : a[4 + j]);  // row_half_mirror
+#pragma unroll
+  for (int j = 0; j < 2; j++) c[j] = (h1 ? b[2 + j] : b[j]) + dpp<0x4E>(h1 ? b[j] : b[2 + j]);  // quad_perm [2,3,0,1]
+  return (h0 ? c[1] : c[0]) + dpp<0xB1>(h0 ? c[0] : c[1]);  // quad_perm [1,0,3,2]
+}
+
 template <int W, int KVL, class Ck>
 __device__ __forceinline__ void load_kv(uint4 (&kr)[KVL], uint4 (&vr)[KVL], const bf16_t* Kh, const bf16_t* Vh,
                                         const Ck& ck, int w, int g, int sl) {
+// K by position: lane (g, sl) of wave w holds dims 8 sl .. + 7 of position t0 + 4 W i + 4 w + g. With 4 compute
+// waves V goes by dimension slice: the same lane holds dims 32 w + 8 g .. + 7 of position t0 + sl + 16 i (each wave
+// multiplies its 32 dims with every position's weight, so no partial sum crosses waves); with 8, V as K.
 // Loads are unconditional, from a position clamped to ck.pos (< max_len): a load under a condition would need a
 // select on its result, and a select makes the wave wait for the load at once. Slots beyond the chunk and the
 // slot of `pos` itself (not written yet) are never read back: the attention code skips or replaces them.
@@ -1069,7 +1089,13 @@ __device__ __forceinline__ void load_kv(uint4 (&kr)[KVL], uint4 (&vr)[KVL], cons
     const int t = min(ck.t0 + jj, ck.pos);
     const uint32_t off = (uint32_t)(t * SK_HD + 8 * sl) * 2u;
     kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Kh)), off, 0, kPolDev));
-    vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Vh)), off, 0, kPolDev));
+    if constexpr (W == 4) {
+      const int tv = min(ck.t0 + sl + 16 * i, ck.pos);
+      const uint32_t ov = (uint32_t)(tv * SK_HD + 32 * w + 8 * g) * 2u;
+      vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Vh)), ov, 0, kPolDev));
+    } else {
+      vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Vh)), off, 0, kPolDev));
+    }
   }
 }
 
@@ -1161,8 +1187,8 @@ __device__ void fail(const Ctx& c, uint32_t code, int f, int l) {
 }
 
 // Barriers of the attention stage after its input has arrived (both roles execute the same count).
-template <class Ck>
-__device__ __forceinline__ int attn_barriers(const Ck& ck) { return 1 + (ck.n > 0 ? 2 : 0); }
+template <int W, class Ck>
+__device__ __forceinline__ int attn_barriers(const Ck& ck) { return 1 + (ck.n > 0 ? (W == 4 ? 1 : 2) : 0); }
 
 // ================================================================================================================
 // Control wave
@@ -1357,7 +1383,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
       if (!ok) return;
-      for (int b = 0; b < (CP && F16 ? 1 : attn_barriers(ck)); b++) wg_sync();
+      for (int b = 0; b < (CP && F16 ? 1 : attn_barriers<W>(ck)); b++) wg_sync();
       if (lane == 0) c.tr(0, f, l, 3);
       // S3: merge of the 32 chunk partials for q head 2x + r/16, dims [8 (r % 16), 8 (r % 16) + 8)
       {
@@ -2048,6 +2074,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           }
         } else {
         float m = -INFINITY, lsum = 0.f, o = 0.f;
+        // 4 compute waves: P V by dimension slice (load_kv's V layout), published straight from the registers (no
+        // third barrier); ov is this lane's output dim, m0v .. l1v the softmax statistics it is published with
+        constexpr bool kDimPV = W == 4;
+        float ov = 0.f;
+        float m0v = -INFINITY, m1v = -INFINITY, l0v = 0.f, l1v = 0.f;
         if (ck.n > 0) {
           // (2) scores of this chunk's positions (kr from the prefetch; the new position from LDS)
           {
@@ -2079,6 +2110,32 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           const float s0l = lane < ck.n ? S.sc[0][jl] : -INFINITY, s1l = lane < ck.n ? S.sc[1][jl] : -INFINITY;
           const float m0 = wave_max(s0l), m1 = wave_max(s1l);
           const float l0 = wave_sum(lane < ck.n ? expf(s0l - m0) : 0.f), l1 = wave_sum(lane < ck.n ? expf(s1l - m1) : 0.f);
+          if constexpr (kDimPV) {
+            // (4') P V of this wave's 32 dims over every position of the chunk: lane (ag, asl) takes positions
+            // asl + 16 i, dims 32 cw + 8 ag .. + 7; the row's sums then land one per lane, lane asl holding dim
+            // 32 cw + 8 ag + (asl % 8) of head asl / 8
+            float a[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) a[e] = 0.f;
+#pragma unroll
+            for (int i = 0; i < C::KVL; i++) {
+              const int jj = asl + 16 * i;
+              if (jj < ck.n) {
+                float v8[8];
+                if (ck.t0 + jj == pos) {
+#pragma unroll
+                  for (int e = 0; e < 8; e++) v8[e] = S.vn[32 * cw + 8 * ag + e];
+                } else {
+                  unpack8(vr[i], v8);
+                }
+                const float e0 = expf(S.sc[0][jj] - m0), e1 = expf(S.sc[1][jj] - m1);
+#pragma unroll
+                for (int e = 0; e < 8; e++) { a[e] = __builtin_fmaf(e0, v8[e], a[e]); a[8 + e] = __builtin_fmaf(e1, v8[e], a[8 + e]); }
+              }
+            }
+            ov = row16_reduce_scatter(a, lane);
+            m0v = m0; m1v = m1; l0v = l0; l1v = l1;
+          } else {
           // (4) P V over this thread's positions
           {
             float a0[8], a1[8];
@@ -2111,8 +2168,30 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
 #pragma unroll
               for (int gg = 0; gg < 4; gg++) o += S.opart[ww][gg][dd >> 3][p * 8 + (dd & 7)];
           }
+          }
         }
-        if (ck.whole) {
+        if constexpr (kDimPV) {
+          const int ph = asl >> 3, dsl = 32 * cw + 8 * ag + (asl & 7);
+          if (ck.whole) {
+            // the whole cache in this workgroup: its slice of the S4 input (q head 2x + r/16, dims 8 (r % 16) ..
+            // + 8), normalised, as the merge would write it
+            const float lw = ph ? l1v : l0v;
+            if (ph == (r >> 4) && (dsl >> 3) == (r & 15))
+              put(c.cells, LY.e3 + (2 * x + ph) * SK_HD + dsl, lw > 0.f ? ov / lw : 0.f, c.tick(f, l, 2));
+          } else {
+            // publish the partial: [m0 l0 m1 l1 | o0[128] | o1[128]]
+            const uint32_t pb = LY.e2 + ((uint32_t)x * kChunks + r) * kPartN;
+            const uint32_t e = c.tick(f, l, 1);
+            if constexpr (kLO) {
+              if (cw == 0 && lane < 4)
+                putl(c.cells, pb, (uint32_t)lane * 8u, lane == 0 ? m0v : lane == 1 ? l0v : lane == 2 ? m1v : l1v, e);
+              putl(c.cells, pb + 4, (uint32_t)(ph * SK_HD + dsl) * 8u, ov, e);
+            } else {
+              if (cw == 0 && lane < 4) put(c.cells, pb + lane, lane == 0 ? m0v : lane == 1 ? l0v : lane == 2 ? m1v : l1v, e);
+              put(c.cells, pb + 4 + ph * SK_HD + dsl, ov, e);
+            }
+          }
+        } else if (ck.whole) {
           // the whole cache in this workgroup: its slice of the S4 input (q head 2x + r/16, dims 8 (r % 16) ..
           // + 8), normalised, as the merge would write it
           if (att_thread && p == (r >> 4) && (dd >> 3) == (r & 15))
@@ -2342,18 +2421,24 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   __syncthreads();
   {
     // default start delays per exchange, overridable through the workspace: tuned by coordinate descent on the
-    // 0.6B talker, on the 1.7B talker for the spread prefetch (longer exchanges; the merge poll starts ~3 us
-    // after the attention) and on the code predictor (no merge; the single-wave attention of F16 with the paired
-    // pass: 1008 -> 945 us per frame)
-    constexpr uint8_t kDefault[Ws::kHops] = {17, 23, 31, 21, 17, 34, 34, 24};
-    constexpr uint8_t kDefaultSpread[Ws::kHops] = {53, 3, 91, 55, 51, 36, 0, 46};
+    // 0.6B talker, on the 1.7B talker for the spread prefetch (longer exchanges), on the bf16 0.6B talker (spread
+    // prefetch at hidden 1024) and on the code predictor (no merge; the single-wave attention of F16 with the
+    // paired pass: 1008 -> 945 us per frame). The merge poll (hop 2) starts after the second attention barrier,
+    // before the compute waves' P V; a poll that starts before the partials are there costs a whole extra round
+    // trip (0.6B: 410-430 against 374-383 us per frame at 30-36 against 40-44 units), so hop 2 keeps a margin
+    // of 4-8 units over the measured edge.
+    constexpr uint8_t kDefault[Ws::kHops] = {21, 23, 44, 25, 17, 34, 30, 28};
+    constexpr uint8_t kDefaultSpread[Ws::kHops] = {53, 11, 54, 39, 47, 48, 4, 38};
+    constexpr uint8_t kDefaultSpread06[Ws::kHops] = {49, 15, 60, 31, 59, 52, 4, 46};
     constexpr uint8_t kDefaultCp[Ws::kHops] = {18, 14, 43, 25, 19, 30, 17, 25};
     const uint32_t w0 = ld_u32_dev(ws, Ws::kPollDelay), w1 = ld_u32_dev(ws, Ws::kPollDelay + 4);
 #pragma unroll
     for (int h = 0; h < Ws::kHops; h++) {
       const uint32_t v = ((h < 4 ? w0 : w1) >> (8 * (h & 3))) & 0xffu;
       c.dl[h] = v ? (uint8_t)(v - 1)
-                  : CP ? kDefaultCp[h] : (Cfg<H, I, W, V, CP>::kSpread ? kDefaultSpread[h] : kDefault[h]);
+                  : CP ? kDefaultCp[h]
+                       : (CfgW<H, I, W, V, CP, WD>::kSpread ? (H == 1024 ? kDefaultSpread06[h] : kDefaultSpread[h])
+                                                            : kDefault[h]);
     }
   }
   c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;

@@ -448,17 +448,16 @@ def make_prefill_engine(name: str, seed: int = 0, L: int = 24, frames: int = 8, 
 
 
 def make_cp_engine(name: str = "cp06b", seed: int = 0, device="cuda", keep_layers: bool = True, pair: bool = True,
-                   wd: str = "i8row"):
+                   wd: str = "i8row", positions: int | None = None):
     """A CodePredictor over the seeded synthetic code predictor of workload ``name`` (one frame per run);
     ``keep_layers``, ``pair`` and ``wd`` as CodePredictor's (layer weights loaded cacheable, positions 0 and 1
-    paired, i8row: the defaults)."""
+    paired, i8row: the defaults); ``positions`` overrides the workload's count of positions."""
     from .kernels import CodePredictor
 
-    spec = WORKLOADS[name]
+    n = positions or WORKLOADS[name]["positions"]
     s = workload_shape(name)
-    cp, temb = make_code_predictor(seed, s, device=device, n_positions=spec["positions"])
-    return CodePredictor(cp, temb, n_positions=spec["positions"], wd=wd, device=device, keep_layers=keep_layers,
-                         pair=pair)
+    cp, temb = make_code_predictor(seed, s, device=device, n_positions=n)
+    return CodePredictor(cp, temb, n_positions=n, wd=wd, device=device, keep_layers=keep_layers, pair=pair)
 
 
 # ---------------------------------------------------------------------------------------------------------

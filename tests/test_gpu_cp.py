@@ -91,3 +91,26 @@ def test_code_zero_out_of_range_is_refused(cp_engine, gpu):
     x0, id0 = syn.cp_frame_inputs(0, 1, s)
     eng(torch.from_numpy(x0).to(gpu), id0)
     assert eng.error() == 0
+
+
+@pytest.mark.parametrize("pair", [True, False], ids=["pair", "serial"])
+def test_code_predictor_24_positions_against_oracle(gpu, pair):
+    """A code predictor of 24 positions: caches longer than 16 take the kernel's multi-wave attention (scores by
+    position, P V by dimension slice, each workgroup writing its slice of the attention output itself), where 16
+    positions take the single-wave one. Codes of two frames and the last position's logits against the oracle,
+    run here on the same seeded weights."""
+    from oracle.workload import cp_oracle
+
+    n = 24
+    print(f"cp06b with {n} positions, pair={pair}: oracle", flush=True)
+    orc, s = cp_oracle("cp06b", 0, positions=n)
+    eng = syn.make_cp_engine("cp06b", 0, gpu, pair=pair, positions=n)
+    for f in range(2):
+        x0, id0 = syn.cp_frame_inputs(0, f, s)
+        ref, lg = orc.frame(x0, id0)
+        print(f"frame {f}: one launch of {n} positions, min top-2 margin "
+              f"{min(float(np.diff(np.sort(v)[-2:])[0]) for v in lg):.2e}", flush=True)
+        codes = eng(torch.from_numpy(x0).to(gpu), id0).cpu().tolist()
+        assert eng.error() == 0
+        assert codes == ref, (f, codes, ref)
+        assert rel_err(eng.logits, lg[-1]) < TOL
