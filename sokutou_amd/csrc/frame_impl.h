@@ -1299,17 +1299,35 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
           if (CP && f == 0) {
             load_pairs<kNP>(c.cp.x0, v, lane);
           } else if (!CP && c.d.in_groups > 0) {
-            // talker_in: the embedding rows of the frame's codes summed in group order, then the pad row
+            // talker_in: the embedding rows of the frame's codes summed in group order, then the pad row. Lane g
+            // reads group g's table address and code, so the rows' loads of 4 groups at a time go out together
+            // (one group after the other cost two dependent memory round trips per group).
+            const int ng = c.d.in_groups;
+            const uint64_t tl = lane < ng ? gload(c.d.in_tabs + lane) : 0;
+            const int64_t cl = lane < ng ? gload(c.d.in_codes + lane) : 0;
 #pragma unroll
             for (int b = 0; b < kNP; b++) v[b] = make_float2(0.f, 0.f);
-            for (int gi = 0; gi < c.d.in_groups; gi++) {
-              const bf16_t* tab = (const bf16_t*)uniform((const void*)gload(c.d.in_tabs + gi));
-              const int64_t code = gload(c.d.in_codes + gi);
+            for (int g0 = 0; g0 < ng; g0 += 4) {
+              uint32_t u[4][kNP];
 #pragma unroll
-              for (int b = 0; b < kNP; b++) {
-                const uint32_t u = gload((const uint32_t*)(tab + (size_t)code * H) + lane + 64 * b);
-                v[b].x += bf2f(u & 0xffffu);
-                v[b].y += bf2f(u >> 16);
+              for (int j = 0; j < 4; j++) {
+                const int gi = min(g0 + j, ng - 1);
+                const bf16_t* tab = (const bf16_t*)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(tl >> 32), gi) << 32) |
+                                                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tl, gi));
+                const int64_t code = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)cl >> 32), gi) << 32) |
+                                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)cl, gi));
+#pragma unroll
+                for (int b = 0; b < kNP; b++) u[j][b] = gload((const uint32_t*)(tab + (size_t)code * H) + lane + 64 * b);
+              }
+#pragma unroll
+              for (int j = 0; j < 4; j++) {
+                if (g0 + j < ng) {
+#pragma unroll
+                  for (int b = 0; b < kNP; b++) {
+                    v[b].x += bf2f(u[j][b] & 0xffffu);
+                    v[b].y += bf2f(u[j][b] >> 16);
+                  }
+                }
               }
             }
 #pragma unroll
@@ -2367,7 +2385,13 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   __shared__ int s_rank;
   __shared__ uint32_t s_base;
   const uint32_t x = xcc_id();
-  if (tid == 0) {
+  if (wave == 0) {
+    // the loads of the launch checks are issued together: lane g < in_groups reads talker_in code g (a serial loop
+    // over the groups took one memory round trip per group before any workgroup could start)
+    const int64_t cg = (!CP && lane < d.in_groups) ? gload(d.in_codes + lane) : 0;
+    const int64_t pos0 = d.pos ? gload(d.pos) : 0, tok0 = gload(d.id0);
+    const bool bad_code = __any(!CP && lane < d.in_groups && (cg < 0 || cg >= (lane == 0 ? d.vocab : d.in_rows)));
+    if (lane == 0) {
     const uint32_t launch = ld_u32_dev(ws, Ws::kLaunch);
     const uint32_t old = __hip_atomic_fetch_add((uint32_t*)((char*)ws + Ws::kCensus + 4 * (x & 7)), 1u,
                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2379,13 +2403,8 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     // every position this launch writes must lie inside the cache, and the start token inside the vocabulary.
     // A refused launch leaves the launch count behind the census; the host's reset (the whole workspace zeroed)
     // brings them back together.
-    const int64_t pos0 = d.pos ? gload(d.pos) : 0, tok0 = gload(d.id0);
-    bool bad = pos0 < 0 || pos0 + n_frames > d.max_len || tok0 < 0 || tok0 >= (CP ? cp.emb0_rows : d.vocab);
-    if (!CP)
-      for (int gi = 0; gi < d.in_groups; gi++) {  // talker_in codes: code 0 in the talker vocabulary, the rest in in_rows
-        const int64_t cg = gload(d.in_codes + gi);
-        bad |= cg < 0 || cg >= (gi == 0 ? d.vocab : d.in_rows);
-      }
+    // talker_in codes: code 0 in the talker vocabulary, the rest in in_rows
+    const bool bad = pos0 < 0 || pos0 + n_frames > d.max_len || tok0 < 0 || tok0 >= (CP ? cp.emb0_rows : d.vocab) || bad_code;
     if (bad) {
       st_u32_dev(ws, Ws::kErr, 5u);
       r = -1;
@@ -2395,6 +2414,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     for (int i = 0; i < 8; i++) S.flags[i] = 0;
     S.pubcnt = 0;
     S.pubseq = 0;
+    }
   }
   __syncthreads();
   const int r = s_rank;
@@ -2423,7 +2443,8 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     // default start delays per exchange, overridable through the workspace: tuned by coordinate descent on the
     // 0.6B talker, on the 1.7B talker for the spread prefetch (longer exchanges), on the bf16 0.6B talker (spread
     // prefetch at hidden 1024) and on the code predictor (no merge; the single-wave attention of F16 with the
-    // paired pass: 1008 -> 945 us per frame). The merge poll (hop 2) starts after the second attention barrier,
+    // paired pass: 1008 -> 945 us per frame), with a set of its own for bf16 weights. The i8g32 kernels keep the
+    // i8row sets (their own descent gained under 1%). The merge poll (hop 2) starts after the second attention barrier,
     // before the compute waves' P V; a poll that starts before the partials are there costs a whole extra round
     // trip (0.6B: 410-430 against 374-383 us per frame at 30-36 against 40-44 units), so hop 2 keeps a margin
     // of 4-8 units over the measured edge.
@@ -2431,12 +2452,13 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     constexpr uint8_t kDefaultSpread[Ws::kHops] = {53, 11, 54, 39, 47, 48, 4, 38};
     constexpr uint8_t kDefaultSpread06[Ws::kHops] = {49, 15, 60, 31, 59, 52, 4, 46};
     constexpr uint8_t kDefaultCp[Ws::kHops] = {18, 14, 43, 25, 19, 30, 17, 25};
+    constexpr uint8_t kDefaultCpBf16[Ws::kHops] = {30, 10, 43, 21, 31, 30, 5, 29};  // 1105 -> 1071 us per frame
     const uint32_t w0 = ld_u32_dev(ws, Ws::kPollDelay), w1 = ld_u32_dev(ws, Ws::kPollDelay + 4);
 #pragma unroll
     for (int h = 0; h < Ws::kHops; h++) {
       const uint32_t v = ((h < 4 ? w0 : w1) >> (8 * (h & 3))) & 0xffu;
       c.dl[h] = v ? (uint8_t)(v - 1)
-                  : CP ? kDefaultCp[h]
+                  : CP ? (WD == SK_WD_BF16 ? kDefaultCpBf16[h] : kDefaultCp[h])
                        : (CfgW<H, I, W, V, CP, WD>::kSpread ? (H == 1024 ? kDefaultSpread06[h] : kDefaultSpread[h])
                                                             : kDefault[h]);
     }
