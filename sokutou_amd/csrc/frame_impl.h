@@ -53,6 +53,11 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11)) & 0xfu; }
+// lane i's 64-bit value, wave-uniform (i wave-uniform)
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int i) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), i) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, i);
+}
 
 // ---- exchange cells ------------------------------------------------------------------------------------------
 __device__ __forceinline__ void put(void* cells, uint32_t idx, float v, uint32_t e) {
@@ -1275,6 +1280,9 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
   const Layout LY(H, I);
   const float eps = c.d.eps;
   const bf16_t* emb = (const bf16_t*)c.d.emb;
+  // code predictor: lane f holds position f's embedding table (read once; per position it was a memory round trip
+  // ahead of the row's own)
+  const uint64_t emb_l = (CP && lane < c.d.max_len) ? (uint64_t)gload(c.cp.emb + lane) : 0;
   int64_t tok = gload(c.d.id0);
   if (CP && c.g == 0 && lane == 0 && c.d.out) gstore(c.d.out, tok);  // code 0 passes through
   // After the code predictor's paired pass (positions 0 and 1, a launch of its own: k_frames with PAIRK) frame 1
@@ -1312,10 +1320,8 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 #pragma unroll
               for (int j = 0; j < 4; j++) {
                 const int gi = min(g0 + j, ng - 1);
-                const bf16_t* tab = (const bf16_t*)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(tl >> 32), gi) << 32) |
-                                                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tl, gi));
-                const int64_t code = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)cl >> 32), gi) << 32) |
-                                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)cl, gi));
+                const bf16_t* tab = (const bf16_t*)lane_u64(tl, gi);
+                const int64_t code = (int64_t)lane_u64((uint64_t)cl, gi);
 #pragma unroll
                 for (int b = 0; b < kNP; b++) u[j][b] = gload((const uint32_t*)(tab + (size_t)code * H) + lane + 64 * b);
               }
@@ -1337,7 +1343,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
               v[b].y += bf2f(u >> 16);
             }
           } else {
-            const bf16_t* tab = CP ? (const bf16_t*)uniform(gload(c.cp.emb + f)) : emb;
+            const bf16_t* tab = CP ? (const bf16_t*)lane_u64(emb_l, f) : emb;
 #pragma unroll
             for (int b = 0; b < kNP; b++) {
               const uint32_t u = gload((const uint32_t*)(tab + (size_t)tok * H) + lane + 64 * b);
@@ -1377,7 +1383,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
 #pragma unroll
           for (int k = 0; k < H / 64; k++) ev[k] += bf2f(gload(pad + lane + 64 * k));
         } else {
-          const bf16_t* tab = CP ? (const bf16_t*)uniform(gload(c.cp.emb + f)) : emb;
+          const bf16_t* tab = CP ? (const bf16_t*)lane_u64(emb_l, f) : emb;
 #pragma unroll
           for (int k = 0; k < H / 64; k++) ev[k] = bf2f(gload(tab + (size_t)tok * H + lane + 64 * k));
         }
@@ -1946,6 +1952,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   const int p = tid >> 7, dd = tid & 127;
   const bool att_thread = tid < 256;
 
+  // code predictor: lane f holds position f's head weights and scales (read once, not per position)
+  const uint64_t head_w_l = (CP && lane < c.d.max_len) ? (uint64_t)gload(c.cp.head_w + lane) : 0;
+  const uint64_t head_s_l = (CP && lane < c.d.max_len) ? (uint64_t)gload(c.cp.head_s + lane) : 0;
   uint4 wq[C::RW_QKV][C::CH], wo[C::RW_O][C::CQ], wg[C::RW_GU][C::CH], wd[C::RW_D][C::CI];
   uint16_t sq[C::RW_QKV], so[C::RW_O], sg[C::RW_GU], sd[C::RW_D];  // raw bf16 row scales
   constexpr bool G32 = WD == SK_WD_I8G32;  // i8g32: raw fp16 group scales, one per row and chunk
@@ -2331,8 +2340,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
     uint4 wh[C::RW_HEAD][C::CH];
     uint16_t sh[C::RW_HEAD];
     uint16_t gh[G32 ? C::RW_HEAD : 1][G32 ? C::CH : 1];
-    const int8_t* hw = CP ? (const int8_t*)uniform(gload(c.cp.head_w + f)) : (const int8_t*)c.d.head_w;
-    const uint16_t* hsc = CP ? (const uint16_t*)uniform(gload(c.cp.head_s + f)) : c.d.head_s;
+    const int8_t* hw = CP ? (const int8_t*)lane_u64(head_w_l, f) : (const int8_t*)c.d.head_w;
+    const uint16_t* hsc = CP ? (const uint16_t*)lane_u64(head_s_l, f) : c.d.head_s;
     load_w<WD, C::RW_HEAD, C::CH, kLO>(wh, sh, gh, hw, hsc, h_w0, h_wn, H, lane);
     wg_sync();
     if (S.flags[5]) return;
