@@ -313,3 +313,41 @@ def test_sampled_frames_split_launches_and_graph_replay(gpu):
         codes.append(int(e2.next_id0.item()))
     assert e2.frame_error() == 0, e2.frame_diag()
     assert codes == ref
+
+
+@pytest.mark.parametrize("groups", [5, 7])
+def test_talker_in_group_counts_off_the_gather_batch(gpu, groups):
+    """One talker frame fed by talker_in of 5 or 7 groups (the kernel gathers the groups' rows 4 at a time, so
+    the last batch is partial): the input is the sum of the groups' rows in group order plus the pad row (the
+    reference's talker_in, qwen3/kernels.py:328-336), then the two layers, the final norm and the head, against
+    the oracle on the same input."""
+    from oracle.talker import argmax_first
+    from oracle.workload import talker_oracle
+
+    name, seed, rows = "small06b", 2, 40
+    eng, tok = _engine(name, seed, gpu)
+    orc, otok, s = talker_oracle(name, seed, "i8row")
+    assert otok == tok
+    rng = np.random.default_rng(groups)
+    extra = [syn.bf16_values((rng.standard_normal((rows, s.hidden)) * 0.05).astype(np.float32))
+             for _ in range(groups - 1)]
+    tabs = [eng.temb] + [torch.from_numpy(t).to(device=gpu, dtype=torch.bfloat16) for t in extra]
+    addr = torch.tensor([t.data_ptr() for t in tabs], dtype=torch.int64, device=gpu)
+    codes = [int(tok)] + [int(c) for c in rng.integers(0, rows, groups - 1)]
+    codes_g = torch.tensor(codes, dtype=torch.int64, device=gpu)
+    pad = syn.bf16_values((rng.standard_normal(s.hidden) * 0.02).astype(np.float32))
+    pad_g = torch.from_numpy(pad).to(device=gpu, dtype=torch.bfloat16)
+    d = eng._desc
+    d.in_tabs, d.in_codes, d.in_pad, d.in_groups, d.in_rows = (addr.data_ptr(), codes_g.data_ptr(),
+                                                              pad_g.data_ptr(), groups, rows)
+    print(f"talker_in of {groups} groups, codes {codes}", flush=True)
+    eng.run_frames(1)
+    torch.cuda.synchronize()
+    assert eng.frame_error() == 0, eng.frame_diag()
+    x = np.zeros(s.hidden, np.float32)
+    for g in range(groups):  # the kernel's order: group 0 .. groups - 1, then the pad row
+        x = x + (orc.w["emb"][codes[0]] if g == 0 else extra[g - 1][codes[g]]).astype(np.float32)
+    x = x + pad
+    lg = orc.logits(orc.forward(x, syn.WORKLOADS[name]["kv"]))
+    assert rel_err(eng.logit_t.view(-1), lg) < TOL
+    assert int(eng.frame_ids[0].item()) == argmax_first(lg)
