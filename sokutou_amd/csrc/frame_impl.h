@@ -2392,8 +2392,14 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   void* ws = d.workspace;
   // ---- placement: XCD from hardware, dense rank from an arrival counter ------------------------------------
   __shared__ int s_rank;
-  __shared__ uint32_t s_base;
+  __shared__ uint32_t s_base, s_dl[2], s_trace;
+  __shared__ int64_t s_pos0;
   const uint32_t x = xcc_id();
+  // Every load of the prologue goes out before the first barrier, so the launch pays one memory round trip for
+  // them instead of one per step: the layer descriptors (into LDS), the launch checks' inputs, the placement
+  // census, the epoch base, the poll delays and the trace flag.
+  for (int i = tid; i < d.n_layers * (int)(sizeof(sk_layer_desc) / 8); i += blockDim.x)
+    ((uint64_t*)S.desc)[i] = gload((const uint64_t*)d.layers + i);
   if (wave == 0) {
     // the loads of the launch checks are issued together: lane g < in_groups reads talker_in code g (a serial loop
     // over the groups took one memory round trip per group before any workgroup could start)
@@ -2420,6 +2426,10 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     }
     s_rank = r;
     s_base = ld_u32_dev(ws, Ws::kTick);
+    s_dl[0] = ld_u32_dev(ws, Ws::kPollDelay);
+    s_dl[1] = ld_u32_dev(ws, Ws::kPollDelay + 4);
+    s_trace = ld_u32_dev(ws, Ws::kTraceOn);
+    s_pos0 = pos0;
     for (int i = 0; i < 8; i++) S.flags[i] = 0;
     S.pubcnt = 0;
     S.pubseq = 0;
@@ -2439,15 +2449,12 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   c.tpf = (uint32_t)d.n_layers * 8u + 8u;
   // after a paired pass the frames' epochs continue from that launch's (frame 0 is the pass's)
   c.base = s_base - (CP && !PAIRK && cp.pair ? c.tpf : 0u);
-  c.pos0 = d.pos ? (int)gload(d.pos) : 0;
+  c.pos0 = (int)s_pos0;
   // read before this workgroup publishes anything: workgroup 0 advances the counter once every pick is done
   c.seed = SMP ? gload(d.seed) : 0;
   c.cnt0 = SMP ? gload(d.counter) : 0;
   c.n_frames = n_frames;
   c.L = d.n_layers;
-  for (int i = tid; i < d.n_layers * (int)(sizeof(sk_layer_desc) / 8); i += blockDim.x)
-    ((uint64_t*)S.desc)[i] = gload((const uint64_t*)d.layers + i);
-  __syncthreads();
   {
     // default start delays per exchange, overridable through the workspace: tuned by coordinate descent on the
     // 0.6B talker, on the 1.7B talker for the spread prefetch (longer exchanges), on the bf16 0.6B talker (spread
@@ -2462,7 +2469,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     constexpr uint8_t kDefaultSpread06[Ws::kHops] = {49, 15, 60, 31, 59, 52, 4, 46};
     constexpr uint8_t kDefaultCp[Ws::kHops] = {18, 14, 43, 25, 19, 30, 17, 25};
     constexpr uint8_t kDefaultCpBf16[Ws::kHops] = {30, 10, 43, 21, 31, 30, 5, 29};  // 1105 -> 1071 us per frame
-    const uint32_t w0 = ld_u32_dev(ws, Ws::kPollDelay), w1 = ld_u32_dev(ws, Ws::kPollDelay + 4);
+    const uint32_t w0 = s_dl[0], w1 = s_dl[1];
 #pragma unroll
     for (int h = 0; h < Ws::kHops; h++) {
       const uint32_t v = ((h < 4 ? w0 : w1) >> (8 * (h & 3))) & 0xffu;
@@ -2472,7 +2479,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
                                                             : kDefault[h]);
     }
   }
-  c.trace = ld_u32_dev(ws, Ws::kTraceOn) ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
+  c.trace = s_trace ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
   if constexpr (PAIRK) {
     if (wave == W) ctl_pair_pass<H, I, W, V, CP>(c, S, lane);
     else compute_pair<H, I, W, V, CP, WD, KEEP>(c, S, wave, tid, lane);
