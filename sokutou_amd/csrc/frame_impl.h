@@ -2028,6 +2028,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         publish<W, kLO>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, 16, c.tick(f, l, 0), lane);
         if (tid == 0) c.tr(1, f, l, 1);
         if constexpr (!C::kLate) load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
+        // With gate/up split over two exchanges (SplitGateUp) the o rows go out here, before the attention, rather
+        // than after it with the first gate/up half: the merge's poll then does not queue behind them (1.7B: 22.96
+        // against 23.25 us per layer; moving the first gate/up half here too measured 23.8)
+        if constexpr (C::kLate && kSplitGu) load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
       }
       // ---- S2: attention over this workgroup's chunk ----------------------------------------------------
       wg_sync();
@@ -2243,7 +2247,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           load_attn_vec(Ln, npos);
         }
         if constexpr (C::kLate) {
-          load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
+          if constexpr (!kSplitGu) load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)Ly.o_w, Ly.o_s, o_w0, o_wn, kQ, lane);
           if constexpr (!C::kSpread) {
             load_w<WD, C::RW_GU, C::CH, kLO, KEEP>(wg, sg, gg, (const int8_t*)Ly.gu_w, Ly.gu_s, gu_w0, C::RW_GU, H, lane);
           } else if constexpr (kSplitGu) {  // the first half of the gate/up rows
@@ -2465,7 +2469,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     // trip (0.6B: 410-430 against 374-383 us per frame at 30-36 against 40-44 units), so hop 2 keeps a margin
     // of 4-8 units over the measured edge.
     constexpr uint8_t kDefault[Ws::kHops] = {21, 23, 44, 25, 17, 34, 30, 28};
-    constexpr uint8_t kDefaultSpread[Ws::kHops] = {53, 11, 54, 39, 47, 48, 4, 38};
+    constexpr uint8_t kDefaultSpread[Ws::kHops] = {49, 19, 56, 35, 39, 56, 4, 34};
     constexpr uint8_t kDefaultSpread06[Ws::kHops] = {49, 15, 60, 31, 59, 52, 4, 46};
     constexpr uint8_t kDefaultCp[Ws::kHops] = {18, 14, 43, 25, 19, 30, 17, 25};
     constexpr uint8_t kDefaultCpBf16[Ws::kHops] = {30, 10, 43, 21, 31, 30, 5, 29};  // 1105 -> 1071 us per frame
