@@ -1191,7 +1191,9 @@ __device__ void fail(const Ctx& c, uint32_t code, int f, int l) {
   st_u32_dev(c.ws, Ws::kErr, code);
 }
 
-// Barriers of the attention stage after its input has arrived (both roles execute the same count).
+// Barriers of the attention stage after its input has arrived (both roles execute the same count): one after
+// the q / k / v preparation, then with a non-empty chunk one after the scores, and with 8 compute waves one more
+// after P V (4 compute waves publish P V by dimension slice from registers).
 template <int W, class Ck>
 __device__ __forceinline__ int attn_barriers(const Ck& ck) { return 1 + (ck.n > 0 ? (W == 4 ? 1 : 2) : 0); }
 
@@ -1414,7 +1416,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         const uint32_t e = c.tick(f, l, 1);
         const int mh = c.r >> 4, md0 = 8 * (c.r & 15);
         if (!ck.whole) {  // whole-cache attention publishes the S4 input itself
-          sleep_units(c.dl[Ws::kHopS3]);  // the compute waves publish their partial right after the last attention barrier
+          sleep_units(c.dl[Ws::kHopS3]);  // the compute waves publish their partial after the last attention barrier (and P V)
           if constexpr (kRegRms) {
             // lane = chunk + 32 * half: lane polls its chunk's (m, l) of head mh and the 4 dims md0 + 4 half .. + 3 of
             // its o slice straight into registers (both halves read the same (m, l)), so the merge needs no LDS
