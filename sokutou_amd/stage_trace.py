@@ -9,7 +9,8 @@ tool runs one traced launch of the synthetic workload (for the code predictor: o
 unpaired, so that frame 0 of the launch is position 0's pass), then prints, as markdown:
 
 * the median time of each step of a layer (median over the 256 workgroups and the middle layers);
-* each exchange: from the last producer's publication to the median consumer's input being ready;
+* each exchange: from the last producer's publication to a consumer's input being ready (the median, and the 90th
+  percentile over every consumer and layer);
 * the median layer time.
 
 This is the reference's per-frame profiling role (qwen3/prof_frame.py:41-87, which times the frame's kernels with
@@ -106,22 +107,29 @@ def summarise(t: np.ndarray, n_layers: int, whole_attention: bool = False) -> di
         last = np.array([cmp_[xcd == x, l, ev].max() for x in range(8)])
         return last[xcd]
 
+    # per consumer workgroup: its input ready, less the last producer's publication
     if whole_attention:
         att = [("attention output (global, 256 producers, written during S2)",
-                lambda l: np.median(ctl[:, l, K_ATT]) - cmp_[:, l, C_S2END].max())]
+                lambda l: ctl[:, l, K_ATT] - cmp_[:, l, C_S2END].max())]
     else:
-        att = [("attention partials (XCD-local, 32 producers)", lambda l: np.median(ctl[:, l, K_MRGPOLL] - local_last(l, C_S2END))),
+        att = [("attention partials (XCD-local, 32 producers)", lambda l: ctl[:, l, K_MRGPOLL] - local_last(l, C_S2END)),
                ("attention output (global, 256 producers; from the partials' arrival)",
-                lambda l: np.median(ctl[:, l, K_ATT] - ctl[:, l, K_MRGPOLL]))]
+                lambda l: ctl[:, l, K_ATT] - ctl[:, l, K_MRGPOLL])]
     exchanges = [
-        ("residual h (global, 256 producers)", lambda l: np.median(ctl[:, l + 1, K_S1IN]) - cmp_[:, l, C_S6PUB].max()),
-        ("q|k|v of the head (XCD-local, 32 producers)", lambda l: np.median(ctl[:, l, K_QKV] - local_last(l, C_S1PUB))),
+        ("residual h (global, 256 producers)", lambda l: ctl[:, l + 1, K_S1IN] - cmp_[:, l, C_S6PUB].max()),
+        ("q|k|v of the head (XCD-local, 32 producers)", lambda l: ctl[:, l, K_QKV] - local_last(l, C_S1PUB)),
         *att,
-        ("h after o (global, 256 producers)", lambda l: np.median(ctl[:, l, K_HMID]) - cmp_[:, l, C_S4PUB].max()),
-        ("SwiGLU activation (global, 256 producers)", lambda l: np.median(ctl[:, l, K_ACT]) - cmp_[:, l, C_S5PUB].max()),
+        ("h after o (global, 256 producers)", lambda l: ctl[:, l, K_HMID] - cmp_[:, l, C_S4PUB].max()),
+        ("SwiGLU activation (global, 256 producers)", lambda l: ctl[:, l, K_ACT] - cmp_[:, l, C_S5PUB].max()),
     ]
+
+    def p90(f):  # over every consumer and layer
+        return float(np.percentile(np.concatenate([f(l) for l in layers]), 90))
+
     layer = med(lambda l: np.median(cmp_[:, l + 1, C_S1] - cmp_[:, l, C_S1]))
-    return {"steps": [(n, med(f)) for n, f in steps], "exchanges": [(n, med(f)) for n, f in exchanges],
+    return {"steps": [(n, med(f)) for n, f in steps],
+            "exchanges": [(n, med(lambda l, f=f: np.median(f(l)))) for n, f in exchanges],
+            "exchanges_p90": [(n, p90(f)) for n, f in exchanges],
             "layer_us": layer, "layers": f"{layers.start}..{layers.stop - 1}"}
 
 
@@ -132,8 +140,8 @@ def to_markdown(name: str, s, summ: dict, launch_us: float, frames: int) -> str:
            f"the 256 workgroups and layers {summ['layers']}.", "", "| step of a layer | us |", "|---|---|"]
     out += [f"| {n} | {v:.2f} |" for n, v in summ["steps"]]
     out += [f"| **layer (S1 start to next S1 start)** | **{summ['layer_us']:.2f}** |", "",
-            "| exchange: last producer's publication -> median consumer's input ready | us |", "|---|---|"]
-    out += [f"| {n} | {v:.2f} |" for n, v in summ["exchanges"]]
+            "| exchange: last producer's publication -> consumer's input ready | median us | p90 us |", "|---|---|---|"]
+    out += [f"| {n} | {v:.2f} | {q:.2f} |" for (n, v), (_, q) in zip(summ["exchanges"], summ["exchanges_p90"])]
     return "\n".join(out)
 
 

@@ -3,6 +3,7 @@ a layer comes out as the difference the stamps were built with, for the talker (
 predictor (whole-cache attention) layouts."""
 
 import numpy as np
+import pytest
 
 from sokutou_amd import stage_trace as st
 
@@ -35,6 +36,19 @@ def test_talker_summary():
     assert ex["attention partials (XCD-local, 32 producers)"] == 0.5
     assert ex["attention output (global, 256 producers; from the partials' arrival)"] == 0.25
     assert ex["h after o (global, 256 producers)"] == 0.5
+    # every consumer is ready at the same time here, so the 90th percentile is the median
+    assert dict(s["exchanges_p90"]) == pytest.approx(ex)
+
+
+def test_exchange_percentile_sees_the_slow_consumers():
+    """One consumer in ten of the residual exchange 1 us late: the median stays, the 90th percentile moves."""
+    name = "residual h (global, 256 producers)"
+    base = dict(st.summarise(_stamps(), 5)["exchanges"])[name]
+    t = _stamps()
+    t[::10, 0, 1:5, st.K_S1IN] += 1.0  # 26 of the 256 consumers
+    s = st.summarise(t, 5)
+    assert dict(s["exchanges"])[name] == pytest.approx(base)
+    assert base < dict(s["exchanges_p90"])[name] <= base + 1.0
 
 
 def test_code_predictor_summary_has_no_merge():
