@@ -94,7 +94,7 @@ int sk_attn(const float* qkv, const float* qn, const float* kn, float eps, const
 /* sk_attn without a workspace, for callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. Same arguments and results as
  * sk_attn, except that the split-K scratch (arrival counters and partials) lives in a static device array of the
- * library, 520 KiB per device, held until the process ends: at most 16 kv heads (more is SK_EINVAL). err (nullable,
+ * library, 260 KiB per device, held until the process ends: at most 16 kv heads (more is SK_EINVAL). err (nullable,
  * device int32) receives 5 when the position lies outside [0, max_len) (the call then writes nothing else) and is
  * left alone otherwise. The call allocates nothing; its first call on a device looks up the array and launches a
  * small kernel that clears the counters. Every call on one device shares the array: calls that overlap on one

@@ -30,8 +30,11 @@ def test_version_string():
 
 def test_workspace_size():
     L = _lib.load()
-    assert L.sk_attn_workspace_size(16, 8, 1024) >= 8 * 2 * 32 * 130 * 4 + 8 * 4
-    assert L.sk_attn_workspace_size(16, 8, 16) > 0
+    # the error word, a counter per kv head and the partials (m, l, o[128]) of both q heads of every split: 8 splits
+    # at 1024 positions (one per 128, at least 8), 16 at 4096 (at most 16), one below 129
+    assert L.sk_attn_workspace_size(16, 8, 1024) >= 8 * 2 * 8 * 130 * 4 + 8 * 4 + 4
+    assert L.sk_attn_workspace_size(16, 8, 4096) >= 8 * 2 * 16 * 130 * 4 + 8 * 4 + 4
+    assert L.sk_attn_workspace_size(16, 8, 16) >= 8 * 2 * 130 * 4 + 8 * 4 + 4
     assert L.sk_attn_workspace_size(16, 0, 16) == 0
 
 
