@@ -32,7 +32,7 @@ constexpr float kInvSqrtHd = 0.08838834764831845f;
 
 // Splits of the cache: one block per head up to 128 positions (no merge), else one split per 128 positions, at least
 // 8 and at most 16. Every partial costs the merging block a load per thread, and a block covers its positions in
-// passes of 64. Measured per call with 8 kv heads at positions 64 / 255 / 512 / 1023 / 2047: 6.3 / 7.8 / 9.5 / 10.4 /
+// passes of 64: fewer, longer splits win until a block needs more than two or three passes. Measured per call with 8 kv heads at positions 64 / 255 / 512 / 1023 / 2047: 6.3 / 7.8 / 9.5 / 10.4 /
 // 12.2 us, against 8.1 / 10.9 / 13.7 / 14.0 / 14.3 us with up to 32 splits of 16 positions.
 int nsplit_for(int max_len) {
   if (max_len <= 128) return 1;
