@@ -188,7 +188,11 @@ hipError_t launch_wd(const float* x, const float* nw, float eps, const void* W, 
                      float* out, int N, int K, int mode, hipStream_t st) {
   // two rows per group once that still leaves at least 512 workgroups (two waves per CU). With one row per group
   // the few waves per CU keep more of each row in flight, 8 chunks per lane and pass, 16 from K = 3072: the 1.7B
-  // talker's bf16 down projection 15.3 -> 11.8 us per call, its o projection 5.4 -> 4.8 (4 chunks before).
+  // talker's bf16 down projection 15.3 -> 11.8 us per call, its o projection 5.4 -> 4.8 (4 chunks before). Two-row
+  // groups take 8 chunks only with long rows and few groups (the 1.7B qkv: 6.4 -> 5.5 us per call in bf16); with
+  // more groups (gate/up) the deeper pass was slower, 10.6 -> 11.3 us.
+  if (N >= 512 * kGroups * 2 && K >= 2048 && N <= 4096)
+    return launch_rg<WD, 2, POL, 8>(x, nw, eps, W, S, bias, out, N, K, mode, st);
   if (N >= 512 * kGroups * 2) return launch_rg<WD, 2, POL, 4>(x, nw, eps, W, S, bias, out, N, K, mode, st);
   if (K >= 3072) return launch_rg<WD, 1, POL, 16>(x, nw, eps, W, S, bias, out, N, K, mode, st);
   return launch_rg<WD, 1, POL, 8>(x, nw, eps, W, S, bias, out, N, K, mode, st);
