@@ -114,11 +114,14 @@ def time_kernels(eng, reps: int = 200) -> dict:
 def cp_algorithmic_bytes(s, positions: int = 16, wd: str = "i8row") -> dict:
     """Bytes one code-predictor frame must move: the stack's weights and scales once per pass, positions 0 and 1
     counted as one pass as the reference pairs them (positions - 1 passes), plus the 15 heads once each and the
-    K/V reads and appends of every position. Scales: a bf16 per row (i8row) or an fp16 per 32 weights (i8g32)."""
+    K/V reads and appends of every position. Weights 1 B (int8) or 2 B (bf16) each; scales a bf16 per row (i8row),
+    an fp16 per 32 weights (i8g32) or none (bf16)."""
     H, I, nq, nkv, hd = s.hidden, s.inter, s.nq, s.nkv, s.head_dim
+    wb = {"i8row": 1, "i8g32": 1, "bf16": 2}[wd]
 
     def mat(N, K):
-        return N * K + (2 * N * (K // 32) if wd == "i8g32" else 2 * N)
+        scales = {"i8row": 2 * N, "i8g32": 2 * N * (K // 32), "bf16": 0}[wd]
+        return N * K * wb + scales
 
     layer = mat((nq + 2 * nkv) * hd, H) + mat(H, nq * hd) + mat(2 * I, H) + mat(H, I)
     kv = sum(2 * nkv * (p + 1) * hd * 2 + 2 * nkv * hd * 2 for p in range(positions)) * s.n_layers

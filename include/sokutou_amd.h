@@ -97,8 +97,10 @@ int sk_attn(const float* qkv, const float* qn, const float* kn, float eps, const
  * library, 260 KiB per device, held until the process ends: at most 16 kv heads (more is SK_EINVAL). err (nullable,
  * device int32) receives 5 when the position lies outside [0, max_len) (the call then writes nothing else) and is
  * left alone otherwise. The call allocates nothing; its first call on a device looks up the array and launches a
- * small kernel that clears the counters. Every call on one device shares the array: calls that overlap on one
- * device (concurrent streams or threads) race and must be serialised by the caller. */
+ * small kernel that clears the counters, so make that first call outside graph capture (later calls may be
+ * captured: the merging block leaves the counters at zero for the next call or replay). Every call on one device
+ * shares the array: calls that overlap on one device (concurrent streams or threads) race and must be serialised by
+ * the caller. */
 int sk_attn_noalloc(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc, void* Vc,
                     const int64_t* pos_ptr, int pos_add, int max_len, int nq, int nkv, float* out, int* err, int ct,
                     void* stream);

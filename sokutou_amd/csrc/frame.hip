@@ -1,10 +1,6 @@
 // Entry points of the persistent kernel in talker mode (sk_talker_workspace_size, sk_talker_frames) and the 0.6B
 // talker's instantiations; the kernel itself is in frame_impl.h. The 1.7B talker runs the instantiations of
-// frame17.hip (4 compute waves, register polls); its instantiations here, with 8 compute waves and register polls,
-// are a comparison point (SOKUTOU_TALKER_POLL=regs). They also keep this module as the 0.6B kernels were tuned in:
-// their register allocation changes with what else the module holds, and measured 2.5% slower without them.
-#include <cstdlib>
-#include <cstring>
+// frame17.hip (4 compute waves, register polls).
 #include "frame_impl.h"
 
 namespace {
@@ -47,13 +43,6 @@ extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* str
     return d->wd == SK_WD_I8G32 ? sk_talker_frames_g32(d, n_frames, st)
                                 : launch_frames<1024, 3072, 4, kTalkerV, false>(d, none, n_frames, st);
   }
-  if (d->hidden == 2048 && d->inter == 6144) {
-    static const bool regs = [] {  // read once per process
-      const char* poll = std::getenv("SOKUTOU_TALKER_POLL");
-      return poll && !std::strcmp(poll, "regs");
-    }();
-    if (regs && d->wd == SK_WD_I8ROW) return launch_frames<2048, 6144, 8, kTalkerV, false>(d, none, n_frames, st);
-    return sk_talker_frames_2048(d, n_frames, st);
-  }
+  if (d->hidden == 2048 && d->inter == 6144) return sk_talker_frames_2048(d, n_frames, st);
   return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: shapes other than the 0.6B / 1.7B talker");
 }

@@ -23,7 +23,7 @@
 //  * Exchanges use 8-byte cells {value, epoch} written and read with device-coherent (sc1) accesses: a consumer
 //    polls the cells it needs until all carry the producer's epoch. A 64-bit aligned store is single-copy atomic,
 //    so data and readiness arrive together and no fence, flag or L2 writeback is needed.
-//  * Wave roles. Waves 0..W-1 compute; wave W (the control wave) does all polling and copies inputs into LDS.
+//  * Wave roles. Waves 0..3 compute; wave 4 (the control wave) does all polling and copies inputs into LDS.
 //    The compute waves issue only weight and K/V loads: as soon as a stage's registers are consumed, the same
 //    registers are reloaded with that stage's weights of the next layer, so the HBM stream runs a full layer
 //    ahead of the dependency chain. The hardware waits for loads in issue order per wave, which is why polling
@@ -148,8 +148,8 @@ __device__ __forceinline__ uint64_t pick_key(float v, int i) {
   return ((uint64_t)k << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
 }
 
-// Spread late prefetch (8 compute waves only): o after the attention, gate/up after o, down after gate/up, the
-// next layer's qkv and K/V after down. Each stage's weights are then in flight across exactly one exchange, and
+// Spread late prefetch: o after the attention, gate/up after o, down after gate/up, the next layer's qkv and K/V
+// after down. Each stage's weights are then in flight across exactly one exchange, and
 // the registers they occupy are live from one stage to the next only. Off unless a translation unit specialises
 // it for its shape before instantiating the kernel.
 template <int H, int I>
@@ -174,23 +174,27 @@ struct SplitGateUp {
   static constexpr bool value = false;
 };
 
+// W, the compute waves per workgroup, is 4: one per SIMD, with the control wave as the fifth wave of the CU. Each
+// wave then has 256 registers, which is what lets a whole layer of hidden-1024 weights sit in registers and the
+// control wave poll every exchange into registers.
 template <int H, int I, int W, int V, bool CP>
 struct Cfg {
+  static_assert(W == 4, "four compute waves");
   static constexpr int R_O = H / kWG, R_GU = 2 * I / kWG, R_D = H / kWG;
   static constexpr int RW_QKV = 16 / W;                       // rows per compute wave
   static constexpr int RW_O = (R_O + W - 1) / W, RW_GU = R_GU / W, RW_D = (R_D + W - 1) / W;
   static constexpr int kHeadRows = V / kWG;                   // head rows per workgroup: 12 (talker), 8 (code predictor)
   static constexpr int RW_HEAD = (kHeadRows + W - 1) / W;
   static constexpr int CH = H / 1024, CQ = kQ / 1024, CI = I / 1024;  // 16-byte chunks per lane per row
-  static constexpr int KVL = (W == 4 && H > 1024) ? 4 : 2;     // K (and V) loads per lane
+  static constexpr int KVL = H > 1024 ? 4 : 2;                 // K (and V) loads per lane
   static constexpr int kMaxChunk = 4 * W * KVL;                // positions per attention workgroup: 32 / 64
   static constexpr int kMaxLen = kMaxChunk * kChunks;          // 1024 / 2048
-  // Prefetch distances. At hidden 1024 with 4 compute waves every stage's weights for the next layer are held in
-  // registers (a full layer ahead). A full layer of 1.7B weights does not fit beside the rest (192 registers per
-  // wave with 4 compute waves; 96 of a 168-register budget with 8); each stage's weights are then loaded one to
-  // three exchanges before their use (kLate): o and gate/up after the attention of their layer, down and the next
-  // layer's qkv after gate/up. kSpread (SpreadLate) moves them later still, one exchange before their use.
-  static constexpr bool kLate = W == 8 || H > 1024;
+  // Prefetch distances. At hidden 1024 every stage's weights for the next layer are held in registers (a full
+  // layer ahead). A full layer of 1.7B weights does not fit beside the rest (192 registers per wave); each stage's
+  // weights are then loaded one to three exchanges before their use (kLate): o and gate/up after the attention of
+  // their layer, down and the next layer's qkv after gate/up. kSpread (SpreadLate) moves them later still, one
+  // exchange before their use.
+  static constexpr bool kLate = H > 1024;
   static constexpr bool kSpread = kLate && SpreadLate<H, I>::value;
   // code-predictor caches short enough for one workgroup to attend over all of them (see Chunk::whole)
   static __device__ bool whole(int pos) { return CP && pos + 1 <= kMaxChunk; }
@@ -220,8 +224,6 @@ struct Lds {
   float qs[2][SK_HD];  // normalised, rotated, scaled q
   float kn[SK_HD], vn[SK_HD];
   float sc[2][Cfg<H, I, W, V, CP>::kMaxChunk];
-  float opart[W][4][16][17];
-  float mrg[kChunks][10];  // S3 inputs per chunk: m, l, o[8] of one q head
   float pub[64];           // this workgroup's outputs of a stage, published by the last compute wave to finish
   uint32_t pubcnt;         // compute-wave arrivals at publish (counts up; the wave that makes it a multiple of W
                            // publishes)
@@ -276,9 +278,9 @@ __device__ __forceinline__ int xsw(int i) {
 
 // Loads per lane in one polling round: at most 16 (64 registers of the control wave).
 constexpr int mb(int n) { return n / 128 < 16 ? n / 128 : 16; }
-// With 4 compute waves (256 registers for the control wave) a round holds up to 24 loads (96 registers): the 3072-cell
+// The activation's poll holds up to 24 loads per round (96 of the control wave's 256 registers): the 3072-cell
 // activation of the hidden-1024 shape in one round (a second round trip costs about 0.5 us per exchange).
-constexpr int mbh(int n, int W) { return W == 4 ? (n / 128 < 24 ? n / 128 : 24) : mb(n); }
+constexpr int mbh(int n) { return n / 128 < 24 ? n / 128 : 24; }
 
 // ---- control wave: poll cells into LDS ---------------------------------------------------------------------
 // Waits until cells [idx0, idx0 + n) (n even, idx0 even) all carry epoch e, copying the values to dst.
@@ -1082,9 +1084,9 @@ __device__ __forceinline__ float row16_reduce_scatter(const float (&v)[16], int 
 template <int W, int KVL, class Ck>
 __device__ __forceinline__ void load_kv(uint4 (&kr)[KVL], uint4 (&vr)[KVL], const bf16_t* Kh, const bf16_t* Vh,
                                         const Ck& ck, int w, int g, int sl) {
-// K by position: lane (g, sl) of wave w holds dims 8 sl .. + 7 of position t0 + 4 W i + 4 w + g. With 4 compute
-// waves V goes by dimension slice: the same lane holds dims 32 w + 8 g .. + 7 of position t0 + sl + 16 i (each wave
-// multiplies its 32 dims with every position's weight, so no partial sum crosses waves); with 8, V as K.
+// K by position: lane (g, sl) of wave w holds dims 8 sl .. + 7 of position t0 + 4 W i + 4 w + g. V goes by
+// dimension slice: the same lane holds dims 32 w + 8 g .. + 7 of position t0 + sl + 16 i (each wave multiplies its
+// 32 dims with every position's weight, so no partial sum crosses waves).
 // Loads are unconditional, from a position clamped to ck.pos (< max_len): a load under a condition would need a
 // select on its result, and a select makes the wave wait for the load at once. Slots beyond the chunk and the
 // slot of `pos` itself (not written yet) are never read back: the attention code skips or replaces them.
@@ -1094,13 +1096,9 @@ __device__ __forceinline__ void load_kv(uint4 (&kr)[KVL], uint4 (&vr)[KVL], cons
     const int t = min(ck.t0 + jj, ck.pos);
     const uint32_t off = (uint32_t)(t * SK_HD + 8 * sl) * 2u;
     kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Kh)), off, 0, kPolDev));
-    if constexpr (W == 4) {
-      const int tv = min(ck.t0 + sl + 16 * i, ck.pos);
-      const uint32_t ov = (uint32_t)(tv * SK_HD + 32 * w + 8 * g) * 2u;
-      vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Vh)), ov, 0, kPolDev));
-    } else {
-      vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Vh)), off, 0, kPolDev));
-    }
+    const int tv = min(ck.t0 + sl + 16 * i, ck.pos);
+    const uint32_t ov = (uint32_t)(tv * SK_HD + 32 * w + 8 * g) * 2u;
+    vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(uniform(Vh)), ov, 0, kPolDev));
   }
 }
 
@@ -1192,10 +1190,10 @@ __device__ void fail(const Ctx& c, uint32_t code, int f, int l) {
 }
 
 // Barriers of the attention stage after its input has arrived (both roles execute the same count): one after
-// the q / k / v preparation, then with a non-empty chunk one after the scores, and with 8 compute waves one more
-// after P V (4 compute waves publish P V by dimension slice from registers).
-template <int W, class Ck>
-__device__ __forceinline__ int attn_barriers(const Ck& ck) { return 1 + (ck.n > 0 ? (W == 4 ? 1 : 2) : 0); }
+// the q / k / v preparation, then with a non-empty chunk one after the scores (P V is published by dimension slice
+// from registers, with no barrier after it).
+template <class Ck>
+__device__ __forceinline__ int attn_barriers(const Ck& ck) { return 1 + (ck.n > 0 ? 1 : 0); }
 
 // ================================================================================================================
 // Control wave
@@ -1264,7 +1262,7 @@ __device__ __forceinline__ bool ctl_pair_pass(const Ctx& c, Lds<H, I, W, V, CP>&
     if (!ok || P.bad) return false;
     // S6 input: the SwiGLU activation
     after_publish(S, (uint32_t)l * 4u + 3u, c.dl[Ws::kHopS6]);
-    ok = poll_cells<mbh(I, W), true, kLO>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+    ok = poll_cells<mbh(I), true, kLO>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
     if (lane == 0) S.flags[4] = !ok;
     wg_sync();
     if (!ok || P.bad) return false;
@@ -1274,9 +1272,7 @@ __device__ __forceinline__ bool ctl_pair_pass(const Ctx& c, Lds<H, I, W, V, CP>&
 
 template <int H, int I, int W, int V, bool CP, bool SMP, bool F16 = false>
 __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
-  // 4 compute waves (256 registers for the control wave): the RMSNorm inputs are polled into registers and staged
-  // from there (kNP element pairs per lane); with 8 compute waves (168 registers) they are staged through LDS
-  constexpr bool kRegRms = W == 4;
+  // The RMSNorm inputs are polled into registers and staged from there (kNP element pairs per lane)
   constexpr int kNP = H / 128;
   constexpr bool kLO = LaneOffsetPolls<H>::value;
   const Layout LY(H, I);
@@ -1299,7 +1295,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       const sk_layer_desc& Ly = S.desc[l];
       bool ok = true;
       float ss = 0.f;
-      if constexpr (kRegRms) {
+      {
         // S1 input from registers: embedding row (layer 0) or the previous layer's residual (polled), times the
         // input norm; lane holds elements 2 lane + 128 b, + 1
         float2 w[kNP], v[kNP];
@@ -1359,46 +1355,6 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
           cells_to_pairs<kNP>(q, v);
         }
         ss = stage_rms<kNP>(v, w, S.hin, S.xs[0], lane);
-      } else {
-      // the input norm weights, in registers before the poll (lane holds elements lane + 64 k)
-      float nin[H / 64];
-#pragma unroll
-      for (int k = 0; k < H / 64; k++) nin[k] = gload(Ly.in_norm + lane + 64 * k);
-      // S1 input: embedding row (layer 0) or the previous layer's residual, times the input norm
-      if (lane == 0) c.tr(0, f, l, 0);
-      if (l == 0) {
-        float ev[H / 64];
-        if (CP && f == 0) {
-#pragma unroll
-          for (int k = 0; k < H / 64; k++) ev[k] = gload(c.cp.x0 + lane + 64 * k);
-        } else if (!CP && c.d.in_groups > 0) {
-          // talker_in: the embedding rows of the frame's codes summed in group order, then the pad row
-#pragma unroll
-          for (int k = 0; k < H / 64; k++) ev[k] = 0.f;
-          for (int gi = 0; gi < c.d.in_groups; gi++) {
-            const bf16_t* tab = (const bf16_t*)uniform((const void*)gload(c.d.in_tabs + gi));
-            const int64_t code = gload(c.d.in_codes + gi);
-#pragma unroll
-            for (int k = 0; k < H / 64; k++) ev[k] += bf2f(gload(tab + (size_t)code * H + lane + 64 * k));
-          }
-          const bf16_t* pad = (const bf16_t*)c.d.in_pad;
-#pragma unroll
-          for (int k = 0; k < H / 64; k++) ev[k] += bf2f(gload(pad + lane + 64 * k));
-        } else {
-          const bf16_t* tab = CP ? (const bf16_t*)lane_u64(emb_l, f) : emb;
-#pragma unroll
-          for (int k = 0; k < H / 64; k++) ev[k] = bf2f(gload(tab + (size_t)tok * H + lane + 64 * k));
-        }
-#pragma unroll
-        for (int k = 0; k < H / 64; k++) S.hin[lane + 64 * k] = ev[k];
-      } else {
-        after_publish(S, (uint32_t)(fq * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
-        ok = poll_cells<mb(H), false, kLO>(c.cells, LY.e6, H, c.tick(f, l - 1, 5), S.hin, c.ws, lane, c, 11u, f, l);
-      }
-      for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
-      ss = wave_sum(ss);
-#pragma unroll
-      for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hin[lane + 64 * k] * nin[k];
       }
       if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[0] = !ok; c.tr(0, f, l, 1); }
       wg_sync();
@@ -1409,7 +1365,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
       if (!ok) return;
-      for (int b = 0; b < (CP && F16 ? 1 : attn_barriers<W>(ck)); b++) wg_sync();
+      for (int b = 0; b < (CP && F16 ? 1 : attn_barriers(ck)); b++) wg_sync();
       if (lane == 0) c.tr(0, f, l, 3);
       // S3: merge of the 32 chunk partials for q head 2x + r/16, dims [8 (r % 16), 8 (r % 16) + 8)
       {
@@ -1417,103 +1373,45 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         const int mh = c.r >> 4, md0 = 8 * (c.r & 15);
         if (!ck.whole) {  // whole-cache attention publishes the S4 input itself
           sleep_units(c.dl[Ws::kHopS3]);  // the compute waves publish their partial after the last attention barrier (and P V)
-          if constexpr (kRegRms) {
-            // lane = chunk + 32 * half: lane polls its chunk's (m, l) of head mh and the 4 dims md0 + 4 half .. + 3 of
-            // its o slice straight into registers (both halves read the same (m, l)), so the merge needs no LDS
-            static_assert(kChunks == 32, "merge lane mapping");
-            const int ch = lane & 31, hh = lane >> 5;
-            const uint32_t pb = LY.e2 + (c.x * kChunks + ch) * kPartN;
-            const uint32_t po = pb + 4 + mh * SK_HD + md0 + 4 * hh;
-            u32x4 ml, oa, ob;
-            for (uint32_t spin = 0;; spin++) {
-              ml = get2(c.cells, pb + 2 * mh);
-              oa = get2(c.cells, po);
-              ob = get2(c.cells, po + 2);
-              if (__all(ml.y == e && ml.w == e && oa.y == e && oa.w == e && ob.y == e && ob.w == e)) break;
-              if ((spin & 63) == 63) {
-                if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
-                if (spin > kSpinLimit) { if (lane == 0) fail(c, 13u, f, l); ok = false; break; }
-              }
-              __builtin_amdgcn_s_sleep(1);
+          // lane = chunk + 32 * half: lane polls its chunk's (m, l) of head mh and the 4 dims md0 + 4 half .. + 3 of
+          // its o slice straight into registers (both halves read the same (m, l)), so the merge needs no LDS
+          static_assert(kChunks == 32, "merge lane mapping");
+          const int ch = lane & 31, hh = lane >> 5;
+          const uint32_t pb = LY.e2 + (c.x * kChunks + ch) * kPartN;
+          const uint32_t po = pb + 4 + mh * SK_HD + md0 + 4 * hh;
+          u32x4 ml, oa, ob;
+          for (uint32_t spin = 0;; spin++) {
+            ml = get2(c.cells, pb + 2 * mh);
+            oa = get2(c.cells, po);
+            ob = get2(c.cells, po + 2);
+            if (__all(ml.y == e && ml.w == e && oa.y == e && oa.w == e && ob.y == e && ob.w == e)) break;
+            if ((spin & 63) == 63) {
+              if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
+              if (spin > kSpinLimit) { if (lane == 0) fail(c, 13u, f, l); ok = false; break; }
             }
-            if (lane == 0) c.tr(0, f, l, 8);
-            if (ok) {
-              // one exp per chunk; each half sums its 32 lanes (rows 0 + 1, rows 2 + 3), so lanes 16 and 48 end with
-              // the weight sum and the 4 merged dims of their half (empty chunks carry m = -inf and weigh nothing)
-              const float mc = __uint_as_float(ml.x);
-              const float rm = row16_max(mc);
-              const float M = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 0)),
-                                    __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 16)));
-              const float fct = mc == -INFINITY ? 0.f : expf(mc - M);
-              float v[5] = {fct * __uint_as_float(ml.z), fct * __uint_as_float(oa.x), fct * __uint_as_float(oa.z),
-                            fct * __uint_as_float(ob.x), fct * __uint_as_float(ob.z)};
+            __builtin_amdgcn_s_sleep(1);
+          }
+          if (lane == 0) c.tr(0, f, l, 8);
+          if (ok) {
+            // one exp per chunk; each half sums its 32 lanes (rows 0 + 1, rows 2 + 3), so lanes 16 and 48 end with
+            // the weight sum and the 4 merged dims of their half (empty chunks carry m = -inf and weigh nothing)
+            const float mc = __uint_as_float(ml.x);
+            const float rm = row16_max(mc);
+            const float M = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 0)),
+                                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 16)));
+            const float fct = mc == -INFINITY ? 0.f : expf(mc - M);
+            float v[5] = {fct * __uint_as_float(ml.z), fct * __uint_as_float(oa.x), fct * __uint_as_float(oa.z),
+                          fct * __uint_as_float(ob.x), fct * __uint_as_float(ob.z)};
 #pragma unroll
-              for (int d = 0; d < 5; d++) {
-                v[d] = row16_sum(v[d]);
-                v[d] += dpp<0x142, 0xA>(v[d]);  // row_bcast:15 into rows 1 and 3
-              }
-              if (ch == 16) {
-                const float Lw = v[0];
-                const uint32_t o0 = LY.e3 + (2 * c.x + mh) * SK_HD + md0 + 4 * hh, e3 = c.tick(f, l, 2);
-                put2(c.cells, o0, Lw > 0.f ? v[1] / Lw : 0.f, Lw > 0.f ? v[2] / Lw : 0.f, e3);
-                put2(c.cells, o0 + 2, Lw > 0.f ? v[3] / Lw : 0.f, Lw > 0.f ? v[4] / Lw : 0.f, e3);
-              }
+            for (int d = 0; d < 5; d++) {
+              v[d] = row16_sum(v[d]);
+              v[d] += dpp<0x142, 0xA>(v[d]);  // row_bcast:15 into rows 1 and 3
             }
-          } else {
-            for (uint32_t spin = 0;; spin++) {
-              bool good = true;
-              // per chunk 5 cell pairs: (m, l) of head mh, then 4 pairs of its o slice; all loads issued first
-              constexpr int kItems = kChunks * 5, kPer = (kItems + 63) / 64;
-              u32x4 q[kPer];
-#pragma unroll
-              for (int j = 0; j < kPer; j++) {
-                const int it = min(lane + 64 * j, kItems - 1);
-                const int ch = it / 5, k = it % 5;
-                const uint32_t pb = LY.e2 + (c.x * kChunks + ch) * kPartN;
-                q[j] = get2(c.cells, k == 0 ? pb + 2 * mh : pb + 4 + mh * SK_HD + md0 + 2 * (k - 1));
-              }
-#pragma unroll
-              for (int j = 0; j < kPer; j++) {
-                const int it = lane + 64 * j;
-                if (it < kItems) {
-                  const int ch = it / 5, k = it % 5;
-                  good &= q[j].y == e && q[j].w == e;
-                  S.mrg[ch][2 * k] = __uint_as_float(q[j].x);
-                  S.mrg[ch][2 * k + 1] = __uint_as_float(q[j].z);
-                }
-              }
-              if (__all(good)) break;
-              if ((spin & 63) == 63) {
-                if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
-                if (spin > kSpinLimit) { if (lane == 0) fail(c, 13u, f, l); ok = false; break; }
-              }
-              __builtin_amdgcn_s_sleep(1);
-            }
-            if (lane == 0) c.tr(0, f, l, 8);
-            if (ok) {
-              // lane = chunk + 32 * half: one exp per chunk, then wave reductions; half hh produces dims
-              // md0 + 4 hh .. md0 + 4 hh + 3 (empty chunks carry m = -inf and weigh nothing)
-              static_assert(kChunks == 32, "merge lane mapping");
-              const int ch = lane & 31, hh = lane >> 5;
-              const float mc = S.mrg[ch][0];
-              const float M = wave_max(mc);
-              const float fct = mc == -INFINITY ? 0.f : expf(mc - M);
-              const float Lw = wave_sum(hh == 0 ? fct * S.mrg[ch][1] : 0.f);
-              float od[4];
-#pragma unroll
-              for (int d = 0; d < 4; d++) {
-                const float v = row16_sum(fct * S.mrg[ch][2 + 4 * hh + d]);
-                const float h0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
-                                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-                const float h1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
-                                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-                od[d] = Lw > 0.f ? (hh ? h1 : h0) / Lw : 0.f;
-              }
-              if (ch == 0) {
-                const uint32_t o0 = LY.e3 + (2 * c.x + mh) * SK_HD + md0 + 4 * hh, e3 = c.tick(f, l, 2);
-                put2(c.cells, o0, od[0], od[1], e3);
-                put2(c.cells, o0 + 2, od[2], od[3], e3);
-              }
+            if (ch == 16) {
+              const float Lw = v[0];
+              const uint32_t o0 = LY.e3 + (2 * c.x + mh) * SK_HD + md0 + 4 * hh, e3 = c.tick(f, l, 2);
+              put2(c.cells, o0, Lw > 0.f ? v[1] / Lw : 0.f, Lw > 0.f ? v[2] / Lw : 0.f, e3);
+              put2(c.cells, o0 + 2, Lw > 0.f ? v[3] / Lw : 0.f, Lw > 0.f ? v[4] / Lw : 0.f, e3);
             }
           }
         }
@@ -1526,7 +1424,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       wg_sync();
       if (!ok) return;
       // S5 input: residual after o, times the post-attention norm (loaded while the exchange is under way)
-      if constexpr (kRegRms) {
+      {
         float2 w[kNP], v[kNP];
         load_pairs<kNP>(Ly.post_norm, w, lane);
         after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
@@ -1534,24 +1432,13 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         ok = poll_regs<kNP, kLO>(c.cells, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
         cells_to_pairs<kNP>(q, v);
         ss = stage_rms<kNP>(v, w, S.hmid, S.xs[0], lane);
-      } else {
-      float npost[H / 64];
-#pragma unroll
-      for (int k = 0; k < H / 64; k++) npost[k] = gload(Ly.post_norm + lane + 64 * k);
-      after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
-      ok = poll_cells<mb(H), false, kLO>(c.cells, LY.e4, H, c.tick(f, l, 3), S.hmid, c.ws, lane, c, 15u, f, l);
-      ss = 0.f;
-      for (int i = lane; i < H; i += 64) { const float v = S.hmid[i]; ss += v * v; }
-      ss = wave_sum(ss);
-#pragma unroll
-      for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hmid[lane + 64 * k] * npost[k];
       }
       if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[3] = !ok; c.tr(0, f, l, 6); }
       wg_sync();
       if (!ok) return;
       // S6 input: the whole SwiGLU activation
       after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 3u, c.dl[Ws::kHopS6]);
-      ok = poll_cells<mbh(I, W), true, kLO>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+      ok = poll_cells<mbh(I), true, kLO>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
       if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
       wg_sync();
       if (!ok) return;
@@ -1560,7 +1447,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     // head input: final residual times the final norm
     bool ok;
     float ss = 0.f;
-    if constexpr (kRegRms) {
+    {
       float2 w[kNP], v[kNP];
       load_pairs<kNP>(c.d.norm, w, lane);
       after_publish(S, (uint32_t)((fq + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
@@ -1581,24 +1468,6 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
           gstore(c.d.final_out + 2 * lane + 128 * b + 1, (v[b].y * inv) * w[b].y);
         }
       }
-    } else {
-    float nfin[H / 64];
-#pragma unroll
-    for (int k = 0; k < H / 64; k++) nfin[k] = gload(c.d.norm + lane + 64 * k);
-    after_publish(S, (uint32_t)((fq + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
-    const bool hb = pr && f == 1;
-    ok = poll_cells<mb(H), false, kLO>(c.cells, hb ? PairLayout(H, I).b6 : LY.e6, H, c.tick(hb ? 0 : f, c.L - 1, 5), S.hin,
-                                       c.ws, lane, c, 17u, f, c.L);
-    for (int i = lane; i < H; i += 64) { const float v = S.hin[i]; ss += v * v; }
-    ss = wave_sum(ss);
-#pragma unroll
-    for (int k = 0; k < H / 64; k++) S.xs[0][xsw(lane + 64 * k)] = S.hin[lane + 64 * k] * nfin[k];
-    if (lane == 0) { S.inv = rsqrtf(ss / H + eps); S.flags[5] = !ok; }
-    if (!CP && c.d.final_out && c.g == 0 && ok) {  // the final norm's output, h * inv * w (rmsnorm)
-      const float inv = rsqrtf(ss / H + eps);
-#pragma unroll
-      for (int k = 0; k < H / 64; k++) gstore(c.d.final_out + lane + 64 * k, (S.hin[lane + 64 * k] * inv) * nfin[k]);
-    }
     }
     wg_sync();
     if (!ok) return;
@@ -1950,9 +1819,6 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   const int d_w0 = C::R_D * g + (kClD ? min(C::RW_D * cw, C::R_D - 1) : C::RW_D * cw), d_wn = max(0, min(C::RW_D, C::R_D - C::RW_D * cw));
   const int h_w0 = C::kHeadRows * g + (kClH ? min(C::RW_HEAD * cw, C::kHeadRows - 1) : C::RW_HEAD * cw),
             h_wn = max(0, min(C::RW_HEAD, C::kHeadRows - C::RW_HEAD * cw));
-  // the attention thread mapping uses the first 256 compute threads: head p = t / 128, dim dd = t % 128
-  const int p = tid >> 7, dd = tid & 127;
-  const bool att_thread = tid < 256;
 
   // code predictor: lane f holds position f's head weights and scales (read once, not per position)
   const uint64_t head_w_l = (CP && lane < c.d.max_len) ? (uint64_t)gload(c.cp.head_w + lane) : 0;
@@ -2043,7 +1909,6 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         const bool has_pos = ck.has_pos();
         // (1) one wave per vector, two dims per lane (d and d + 64, the RoPE pair): wave 0 q of head 2x, wave 1 q
         // of head 2x + 1, wave 2 k, wave 3 v. RMSNorm over the head is a wave reduction, RoPE stays in the lane.
-        // Waves beyond 3 (8 compute waves) compute values that are never stored.
         {
           const int vw = cw & 3;
           const float x0 = S.qkv[vw * SK_HD + lane], x1 = S.qkv[vw * SK_HD + 64 + lane];
@@ -2106,10 +1971,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
                    lw > 0.f ? o1 / lw : 0.f, c.tick(f, l, 2));
           }
         } else {
-        float m = -INFINITY, lsum = 0.f, o = 0.f;
-        // 4 compute waves: P V by dimension slice (load_kv's V layout), published straight from the registers (no
-        // third barrier); ov is this lane's output dim, m0v .. l1v the softmax statistics it is published with
-        constexpr bool kDimPV = W == 4;
+        // P V by dimension slice (load_kv's V layout), published straight from the registers (no third barrier); ov
+        // is this lane's output dim, m0v .. l1v the softmax statistics it is published with
         float ov = 0.f;
         float m0v = -INFINITY, m1v = -INFINITY, l0v = 0.f, l1v = 0.f;
         if (ck.n > 0) {
@@ -2143,7 +2006,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           const float s0l = lane < ck.n ? S.sc[0][jl] : -INFINITY, s1l = lane < ck.n ? S.sc[1][jl] : -INFINITY;
           const float m0 = wave_max(s0l), m1 = wave_max(s1l);
           const float l0 = wave_sum(lane < ck.n ? expf(s0l - m0) : 0.f), l1 = wave_sum(lane < ck.n ? expf(s1l - m1) : 0.f);
-          if constexpr (kDimPV) {
+          {
             // (4') P V of this wave's 32 dims over every position of the chunk: lane (ag, asl) takes positions
             // asl + 16 i, dims 32 cw + 8 ag .. + 7; the row's sums then land one per lane, lane asl holding dim
             // 32 cw + 8 ag + (asl % 8) of head asl / 8
@@ -2168,42 +2031,9 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
             }
             ov = row16_reduce_scatter(a, lane);
             m0v = m0; m1v = m1; l0v = l0; l1v = l1;
-          } else {
-          // (4) P V over this thread's positions
-          {
-            float a0[8], a1[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) { a0[e] = 0.f; a1[e] = 0.f; }
-#pragma unroll
-            for (int i = 0; i < C::KVL; i++) {
-              const int jj = 4 * W * i + 4 * cw + ag;
-              if (jj < ck.n) {
-                float v8[8];
-                if (ck.t0 + jj == pos) {
-#pragma unroll
-                  for (int e = 0; e < 8; e++) v8[e] = S.vn[8 * asl + e];
-                } else {
-                  unpack8(vr[i], v8);
-                }
-                const float e0 = expf(S.sc[0][jj] - m0), e1 = expf(S.sc[1][jj] - m1);
-#pragma unroll
-                for (int e = 0; e < 8; e++) { a0[e] = __builtin_fmaf(e0, v8[e], a0[e]); a1[e] = __builtin_fmaf(e1, v8[e], a1[e]); }
-              }
-            }
-#pragma unroll
-            for (int e = 0; e < 8; e++) { S.opart[cw][ag][asl][e] = a0[e]; S.opart[cw][ag][asl][8 + e] = a1[e]; }
-          }
-          wg_sync();  // 3
-          if (att_thread) {
-            m = p ? m1 : m0;
-            lsum = p ? l1 : l0;
-            for (int ww = 0; ww < W; ww++)
-#pragma unroll
-              for (int gg = 0; gg < 4; gg++) o += S.opart[ww][gg][dd >> 3][p * 8 + (dd & 7)];
-          }
           }
         }
-        if constexpr (kDimPV) {
+        {
           const int ph = asl >> 3, dsl = 32 * cw + 8 * ag + (asl & 7);
           if (ck.whole) {
             // the whole cache in this workgroup: its slice of the S4 input (q head 2x + r/16, dims 8 (r % 16) ..
@@ -2223,22 +2053,6 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
               if (cw == 0 && lane < 4) put(c.cells, pb + lane, lane == 0 ? m0v : lane == 1 ? l0v : lane == 2 ? m1v : l1v, e);
               put(c.cells, pb + 4 + ph * SK_HD + dsl, ov, e);
             }
-          }
-        } else if (ck.whole) {
-          // the whole cache in this workgroup: its slice of the S4 input (q head 2x + r/16, dims 8 (r % 16) ..
-          // + 8), normalised, as the merge would write it
-          if (att_thread && p == (r >> 4) && (dd >> 3) == (r & 15))
-            put(c.cells, LY.e3 + (2 * x + p) * SK_HD + dd, lsum > 0.f ? o / lsum : 0.f, c.tick(f, l, 2));
-        } else if (att_thread) {
-          // publish the partial: [m0 l0 m1 l1 | o0[128] | o1[128]]
-          const uint32_t pb = LY.e2 + ((uint32_t)x * kChunks + r) * kPartN;
-          const uint32_t e = c.tick(f, l, 1);
-          if constexpr (kLO) {  // tid = p * 128 + dd
-            if (dd == 0) { putl(c.cells, pb, (uint32_t)p * 16u, m, e); putl(c.cells, pb, (uint32_t)p * 16u + 8u, lsum, e); }
-            putl(c.cells, pb + 4, (uint32_t)tid * 8u, o, e);
-          } else {
-            if (dd == 0) { put(c.cells, pb + 2 * p, m, e); put(c.cells, pb + 2 * p + 1, lsum, e); }
-            put(c.cells, pb + 4 + p * SK_HD + dd, o, e);
           }
         }
         }

@@ -234,9 +234,13 @@ def _sampled_engine(gpu, top_k, seed=2, name="small06b", frames=24):
     return eng, tok
 
 
-def _sampled_oracle(name, seed, tok, key, frames, top_k, eos, cnt0=0):
+def _sampled_oracle(name, seed, tok, key, frames, top_k, eos, cnt0=0, follow=None):
     """Codes of ``frames`` sampled frames: processor (repetition penalty 1.05 on the seen ids, the last 64 ids but
-    EOS suppressed, EOS blocked while fewer than 2 codes exist), temperature 0.9, top_k, draw cnt0 + f."""
+    EOS suppressed, EOS blocked while fewer than 2 codes exist), temperature 0.9, top_k, draw cnt0 + f.
+    With ``follow`` (the GPU's codes) the oracle takes the GPU's code as each frame's output instead of its own and
+    returns, per frame, its own pick and how far the GPU's pick was from winning: the larger of its distance below
+    the top_k-th largest value (the keep threshold) and below the winner in the perturbed values (0 when the two
+    picks are the same code)."""
     from oracle import talker as O
     from oracle.workload import talker_oracle
 
@@ -252,10 +256,38 @@ def _sampled_oracle(name, seed, tok, key, frames, top_k, eos, cnt0=0):
     for f in range(frames):
         lg = orc.logits(orc.forward(orc.w["emb"][t], pos + f))
         v = O.process_logits(lg, seen, 1.05, sup, 1 + f, 2, eos)
-        t, _ = O.sample_draw(v, float(np.float32(1.0 / 0.9)), top_k, key, cnt0 + f)
+        inv_t = float(np.float32(1.0 / 0.9))
+        mine, _ = O.sample_draw(v, inv_t, top_k, key, cnt0 + f)
+        if follow is None:
+            t = mine
+            out.append(t)
+        else:
+            t = follow[f]
+            gap = 0.0
+            if t != mine:
+                # how far the GPU's pick is from being the oracle's: below the top_k-th largest value (not kept), and
+                # below the winner in the perturbed values
+                x = np.asarray(v, np.float32) * np.float32(inv_t)
+                g = x - np.log(-np.log(O.gumbel_uniform(x.size, key, cnt0 + f))).astype(np.float32)
+                kth = np.sort(x)[::-1][min(top_k, x.size) - 1] if 0 < top_k < x.size else -np.inf
+                gap = max(float(kth - x[t]), float(g[mine] - g[t]))
+            out.append((mine, gap))
         seen[t] = True
-        out.append(t)
     return out
+
+
+def _check_sampled(codes, name, tok, key, top_k, eos, cnt0=0):
+    """Every GPU pick is the oracle's pick given the same history, except at near-ties: the GPU's logits differ from
+    the fp32 oracle's by up to about 3e-4 (1e-4 relative; the bf16 K/V cache rounds the two sides' keys and values
+    differently where their fp32 values straddle a rounding tie), so where the oracle's two best perturbed values
+    lie closer than 1e-3 either may win. At most two such frames in a run."""
+    chk = _sampled_oracle(name, 2, tok, key, len(codes), top_k, eos, cnt0=cnt0, follow=codes)
+    ties = [(f, c, m, gap) for f, (c, (m, gap)) in enumerate(zip(codes, chk)) if c != m]
+    for f, c, m, gap in ties:
+        assert gap < 1e-3, f"frame {f}: GPU {c} is {gap:.3e} below the oracle's pick {m}"
+    assert len(ties) <= 2, ties
+    if ties:
+        print(f"  near-ties resolved the other way: {ties}", flush=True)
 
 
 @pytest.mark.parametrize("top_k,name", [(50, "small06b"), (0, "small06b"), (1, "small06b"), (64, "small06b"),
@@ -276,12 +308,11 @@ def test_sampled_frames_one_launch_against_oracle(gpu, top_k, name):
     torch.cuda.synchronize()
     assert eng.frame_error() == 0, eng.frame_diag()
     codes = eng.frame_ids[:F].cpu().tolist()
-    ref = _sampled_oracle(name, 2, tok, key, F, top_k, eng.eos)
     print(f"  codes {codes[:8]}..., {len(set(codes))} distinct", flush=True)
-    assert codes == ref
+    _check_sampled(codes, name, tok, key, top_k, eng.eos)
     assert int(eng.fs.counter.item()) == F
     assert int(eng.ngen.item()) == 1 + F and int(eng.pos.item()) == syn.WORKLOADS[name]["kv"] + F
-    assert int(eng.next_id0.item()) == ref[-1]
+    assert int(eng.next_id0.item()) == codes[-1]
     if top_k != 1:
         assert len(set(codes)) > 3
 
@@ -290,8 +321,14 @@ def test_sampled_frames_split_launches_and_graph_replay(gpu):
     """The same sampled run as 1 + 7 + 16 frames over three launches, and as 24 replays of a captured one-frame
     launch: the counter carries the draws across launches, so the codes equal one launch of 24."""
     F, key = 24, 0x1234_5678_9ABC_DEF
+    e1, tok1 = _sampled_engine(gpu, 50, frames=F)
+    print("small06b: 24 sampled frames in one launch, against the oracle", flush=True)
+    e1.fs.set_seed(key)
+    e1.run_frames(F)
+    assert e1.frame_error() == 0, e1.frame_diag()
+    ref = e1.frame_ids[:F].cpu().tolist()
+    _check_sampled(ref, "small06b", tok1, key, 50, e1.eos)
     eng, tok = _sampled_engine(gpu, 50, frames=F)
-    ref = _sampled_oracle("small06b", 2, tok, key, F, 50, eng.eos)
     print("small06b: sampled frames over launches of 1, 7 and 16", flush=True)
     eng.fs.set_seed(key)
     got = []

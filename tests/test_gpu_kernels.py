@@ -113,8 +113,9 @@ def test_attention(gpu, ct, nkv, max_len, pos):
     mask[pos] = False
     np.testing.assert_array_equal(Kg[:, mask], Ko[:, mask])
     np.testing.assert_array_equal(Vg[:, mask], Vo[:, mask])
-    # arrival counters are back at zero (the head of the workspace)
-    assert int(ws[: nkv * 4].sum()) == 0
+    # the error word (bytes 0..3) is clear and every head's arrival counter (from byte 4) is back at zero
+    assert int(ws[:4].view(torch.int32).item()) == 0
+    assert int(ws[4 : 4 + 4 * nkv].view(torch.int32).abs().sum()) == 0
 
 
 def test_attention_invalid_position_sets_error_word(gpu):

@@ -1,5 +1,7 @@
 """sk_attn_noalloc (the allocation-free variant of sk_attn, scratch in a static device array) against sk_attn on the
-same inputs: two calls in a row, the second smaller, then a refused position and a valid call after it."""
+same inputs. Every cache here is longer than 128 positions, so each call splits the cache and merges the partials
+through the shared arrival counters of the static scratch: three calls in a row (the second smaller, the third the
+longest), then a refused position followed by a merged call, then replays of a captured call."""
 
 import numpy as np
 import pytest
@@ -47,12 +49,15 @@ def _no_alloc(c, gpu, err):
     return out, K, V
 
 
+CASES = ((8, 577, 512), (4, 300, 200), (8, 2048, 2047))
+
+
 def test_no_alloc_attention_matches_workspace_attention(gpu):
-    print("sk_attn_noalloc: two calls (nkv 8 / max_len 577 / pos 512, then nkv 4 / 64 / 20) against sk_attn",
-          flush=True)
+    print("sk_attn_noalloc: three merged calls in a row (nkv / max_len / pos " +
+          ", ".join("%d / %d / %d" % c for c in CASES) + ") against sk_attn", flush=True)
     rng = np.random.default_rng(11)
     err = torch.zeros(1, dtype=torch.int32, device=gpu)
-    for nkv, max_len, pos in ((8, 577, 512), (4, 64, 20)):
+    for nkv, max_len, pos in CASES:
         c = _case(gpu, rng, nkv, max_len, pos)
         want = _with_workspace(c, gpu)
         got = _no_alloc(c, gpu, err)
@@ -64,20 +69,49 @@ def test_no_alloc_attention_matches_workspace_attention(gpu):
 
 
 def test_no_alloc_attention_refuses_bad_position_then_runs(gpu):
-    print("sk_attn_noalloc: position past the cache refused (err 5, nothing written), then a valid call", flush=True)
+    print("sk_attn_noalloc: position past the cache refused (err 5, nothing written), then a merged valid call",
+          flush=True)
     rng = np.random.default_rng(12)
-    c = _case(gpu, rng, 8, 64, 64)
+    c = _case(gpu, rng, 8, 577, 577)
     err = torch.zeros(1, dtype=torch.int32, device=gpu)
     out, K, V = _no_alloc(c, gpu, err)
     assert int(err.item()) == 5
     assert bool((out == 7.0).all()) and torch.equal(K, c["K0"]) and torch.equal(V, c["V0"])
     err.zero_()
-    c["pos"].fill_(40)
+    c["pos"].fill_(540)  # 541 positions: split 8 ways and merged through the shared counters
     want = _with_workspace(c, gpu)
     got = _no_alloc(c, gpu, err)
     assert int(err.item()) == 0
     for a, b in zip(got, want):
         assert torch.equal(a, b)
+
+
+def test_no_alloc_attention_replays_in_a_graph(gpu):
+    """A call recorded into a graph (after the first call on the device, which sets the scratch up outside capture)
+    replays with the counters of the static scratch back at zero each time: each replay equals sk_attn."""
+    print("sk_attn_noalloc: a merged call captured in a graph, replayed three times against sk_attn", flush=True)
+    rng = np.random.default_rng(13)
+    c = _case(gpu, rng, 8, 577, 530)
+    want = _with_workspace(c, gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    _no_alloc(c, gpu, err)  # the device's scratch is set up (a no-op if an earlier call did it)
+    p = _lib.ptr
+    K, V = c["K0"].clone(), c["V0"].clone()
+    out = torch.full((c["nq"] * 128,), 7.0, device=gpu)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _lib.call("sk_attn_noalloc", p(c["qkv"]), p(c["qn"]), p(c["kn"]), 1e-6, p(c["rope"]), p(K), p(V),
+                  p(c["pos"]), 0, c["max_len"], c["nq"], c["nkv"], p(out), p(err), 0, _lib.stream())
+    for _ in range(3):
+        K.copy_(c["K0"])
+        V.copy_(c["V0"])
+        out.fill_(7.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        for a, b in zip((out, K, V), want):
+            assert torch.equal(a, b)
 
 
 def test_no_alloc_attention_rejects_too_many_heads_on_the_host(gpu):
