@@ -245,9 +245,20 @@ typedef struct sk_cp_desc {
    * the workspace is then sk_cp_workspace_size(hidden, inter, 1) bytes. 0: one position after the other, one
    * launch. Either gives the same codes up to fp32 summation order. */
   int pair;
+  /* Optional input projection, the code predictor's small_to_mtp_projection (qwen3/kernels.py:520-521, 629-637):
+   * with proj_in > 0 the position inputs are proj_in wide (x0 fp32 [proj_in], the emb tables bf16 [rows][proj_in])
+   * and each position's input to the stack is proj_w . input + proj_b, a gemv over proj_w ([hidden][proj_in] in the
+   * weight format wd, proj_s its scales as for the layers, null for bf16) with the fp32 bias proj_b ([hidden],
+   * nullable). proj_in 0: the inputs are hidden wide and enter the stack as they are. Supported: proj_in 2048 (the
+   * 1.7B talker's width) with pair = 0. */
+  int proj_in;
+  const void* proj_w;
+  const uint16_t* proj_s;
+  const float* proj_b;
 } sk_cp_desc;
 
-/* Bytes of workspace sk_cp_frame needs: sk_talker_workspace_size plus, for pair = 1, the second row's cells. */
+/* Bytes of workspace sk_cp_frame needs: sk_talker_workspace_size plus the cells of a projected input and, for
+ * pair = 1, the second row's cells. */
 int64_t sk_cp_workspace_size(int hidden, int inter, int pair);
 
 /* All positions of the code predictor of one frame in ONE launch, or two with desc->pair (the paired pass of

@@ -426,9 +426,11 @@ class CodePredictorOracle:
     """One frame of the code predictor over dequantised fp32 weights (the greedy sub-code loop of
     ``Qwen3Kernels._frame``, qwen3/kernels.py:666-675, with ``_cp_first`` 641-655 and ``_cp_input`` 629-639):
 
-      * position 0 takes the talker's last hidden state ``x0`` (``_cp_input(ph32)``; the projection is the
-        identity when both stacks are equally wide), position 1 the talker embedding row of code 0
-        (``embed(temb, id0)``), position g >= 2 row ``codes[g-1]`` of code table g - 2 (``cemb[g-2]``);
+      * position 0 takes the talker's last hidden state ``x0`` (``_cp_input(ph32)``), position 1 the talker
+        embedding row of code 0 (``embed(temb, id0)``), position g >= 2 row ``codes[g-1]`` of code table g - 2
+        (``cemb[g-2]``); each input goes through ``_cp_input`` (qwen3/kernels.py:629-637): the projection
+        ``small_to_mtp_projection`` as a gemv with its bias when the weights hold ``proj`` ([H, talker width])
+        and ``proj_b``, else the identity (both stacks equally wide);
       * each position runs the decoder stack at position g over a cache that starts empty for the frame;
       * position g >= 1 ends in ``rms_gemv(h, norm, eps, heads[g-1])`` and a greedy pick (lowest index on ties;
         the sub-codes get no processor, qwen3/kernels.py:671-674).
@@ -436,7 +438,7 @@ class CodePredictorOracle:
     Positions 0 and 1 may be computed as one pair in the reference (``_cp_layers_pair``, 600-617); the result is
     the same row by row, so they are computed one after the other here. ``weights``: ``layers`` (as in
     ``decoder_layer``), ``norm``, ``heads`` (list of [V, H] fp32), ``cemb`` (list of [V, H]), ``temb``,
-    ``rope``, ``eps``, ``nq``, ``nkv``."""
+    ``rope``, ``eps``, ``nq``, ``nkv``, optionally ``proj`` and ``proj_b``."""
 
     def __init__(self, weights: dict, n_positions: int = 16, cache_bf16: bool = True):
         self.w = weights
@@ -459,6 +461,8 @@ class CodePredictorOracle:
             else:
                 x = w["cemb"][g - 2][codes[g - 1]]
             h = np.asarray(x, F32)
+            if w.get("proj") is not None:
+                h = gemv(h, w["proj"], w.get("proj_b"))
             for i, L in enumerate(w["layers"]):
                 h = decoder_layer(h, L, w["eps"], w["rope"], K[i], V[i], g, w["nq"], w["nkv"], self.cache_bf16)
                 if layer_out is not None and g == self.n - 1:

@@ -68,7 +68,7 @@ def cp_oracle(name: str = "cp06b", seed: int = 0, wd: str = "i8row", cache_bf16:
     spec = syn.WORKLOADS[name]
     s = syn.workload_shape(name)
     n = positions or spec["positions"]
-    w = syn.cp_weights(seed, s, n)
+    w = syn.cp_weights(seed, s, n, in_hidden=spec.get("in_hidden"))
     if digests is not None:
         digests["layer0.q"] = syn.sha256(w["layers"][0]["q"])
         digests["head1"] = syn.sha256(w["heads"][0])
@@ -77,6 +77,11 @@ def cp_oracle(name: str = "cp06b", seed: int = 0, wd: str = "i8row", cache_bf16:
     weights = {"layers": [pack_layer(L, wd) for L in w["layers"]], "norm": w["norm"],
                "heads": [O.quantize(h, wd)[2] for h in w["heads"]], "cemb": w["cemb"], "temb": w["temb"],
                "rope": O.rope_table(syn.inv_freq(s), n), "eps": s.eps, "nq": s.nq, "nkv": s.nkv}
+    if "proj" in w:  # a projected code predictor: its input projection, quantised as the layers are
+        weights["proj"] = O.quantize(w["proj"], wd)[2]
+        weights["proj_b"] = w["proj_b"]
+        if digests is not None:
+            digests["proj"] = syn.sha256(w["proj"])
     return O.CodePredictorOracle(weights, n, cache_bf16), s
 
 
@@ -108,4 +113,41 @@ def batch_oracle(name: str, seed: int = 0, frames: int | None = None, cache_bf16
         Vs.append(V)
     orc = O.BatchTalkerOracle(weights, Ks, Vs, cache_bf16, act_terms)
     return orc, [T[b] for b in streams], [tok[b] for b in streams], s
+
+
+def frame_oracle(name: str, seed: int = 0, wd: str = "i8row", frames: int | None = None, detail: bool = False):
+    """Greedy whole Qwen3-TTS frames of a frame workload (the composition of the reference's ``_frame``,
+    qwen3/kernels.py:666-693): the code predictor from (ph32, code 0) gives sub-codes 1..15, then the talker runs on
+    talker_in, the sum of the 16 codes' embedding rows in group order (code 0 from the talker's table, code g from
+    code table g - 1) plus the pad row, and its final norm's output is the next frame's ph32. ph32 starts as the
+    synthetic last hidden state (``cp_frame_inputs`` at the talker's width), code 0 as the start token. Returns
+    (codes [frames][16], start token) or, with ``detail``, also the top-1/top-2 margins of every pick per frame
+    and the talker's logits per frame."""
+    spec = syn.WORKLOADS[name]
+    frames = spec["frames"] if frames is None else frames
+    cspec = syn.WORKLOADS[spec["cp"]]
+    torc, tok, s = talker_oracle(name, seed, wd, max_len=spec["kv"] + frames + 1)
+    corc, cs = cp_oracle(spec["cp"], seed, wd=wd)
+    G = cspec["positions"]
+    temb = torc.w["emb"]
+    corc.w["temb"] = temb
+    w = syn.cp_weights(seed, cs, G, talker_vocab=s.vocab, in_hidden=cspec.get("in_hidden"))
+    tabs = [temb] + [O.bf16_round(t) for t in w["cemb"]] + [np.zeros_like(temb)]
+    pad = syn.bf16_values(syn.normal(seed, syn.CP_FRAME0 - 1, "emb", (s.hidden,), 0.02))
+    ph32, _ = syn.cp_frame_inputs(seed, 0, s)
+    pos, t, out, margins, logits = spec["kv"], tok, [], [], []
+    for f in range(frames):
+        codes, clg = corc.frame(ph32, t)
+        out.append([int(c) for c in codes])
+        x = np.zeros(s.hidden, np.float32)
+        for g in range(G):
+            x = x + tabs[g][codes[g]]
+        x = x + pad
+        h = torc.forward(x, pos + f)
+        ph32 = O.rmsnorm(h, torc.w["norm"], s.eps)
+        lg = O.gemv(ph32, torc.w["head"])
+        t = O.argmax_first(lg)
+        margins.append([float(np.diff(np.sort(v)[-2:])[0]) for v in (*clg, lg)])
+        logits.append(lg)
+    return (out, tok, margins, logits) if detail else (out, tok)
 

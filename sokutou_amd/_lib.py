@@ -68,7 +68,8 @@ class SkCpDesc(ctypes.Structure):
                 ("emb0_rows", c_int), ("emb", c_void_p), ("head_w", c_void_p), ("head_s", c_void_p),
                 ("codes", c_void_p), ("logits", c_void_p), ("layer_out", c_void_p), ("workspace", c_void_p),
                 ("workspace_bytes", c_int64), ("do_sample", c_int), ("inv_temp", c_float), ("top_k", c_int),
-                ("seed", c_void_p), ("counter", c_void_p), ("keep_layers", c_int), ("pair", c_int)]
+                ("seed", c_void_p), ("counter", c_void_p), ("keep_layers", c_int), ("pair", c_int),
+                ("proj_in", c_int), ("proj_w", c_void_p), ("proj_s", c_void_p), ("proj_b", c_void_p)]
 
 
 class SkBatchDesc(ctypes.Structure):

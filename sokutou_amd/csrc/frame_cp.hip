@@ -7,9 +7,10 @@
 
 extern "C" int64_t sk_cp_workspace_size(int hidden, int inter, int pair) {
   if (hidden <= 0 || inter <= 0) return 0;
+  (void)pair;  // the paired pass's cells lie below the projected input's, which every code predictor may use
   const int64_t base = sk_talker_workspace_size(hidden, inter);
-  const int64_t paired = (int64_t)Ws::kCells + (int64_t)PairLayout(hidden, inter).total * 8;
-  return pair && paired > base ? paired : base;
+  const int64_t cells = (int64_t)Ws::kCells + ((int64_t)proj_cells(hidden, inter) + hidden) * 8;
+  return cells > base ? cells : base;
 }
 
 extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
@@ -27,6 +28,14 @@ extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {
     return sk_set_error(SK_EWORKSPACE, "sk_cp_frame: workspace too small");
   if (d->do_sample && (!d->seed || !d->counter || !(d->inv_temp > 0.f)))
     return sk_set_error(SK_EINVAL, "sk_cp_frame: sampling needs seed, counter and inv_temp > 0");
+  if (d->proj_in != 0) {
+    if (d->proj_in != 2048)
+      return sk_set_error(SK_EUNSUPPORTED, "sk_cp_frame: a projected input must be 2048 wide (the 1.7B talker)");
+    if (!d->proj_w || (!d->proj_s && d->wd != SK_WD_BF16))
+      return sk_set_error(SK_EINVAL, "sk_cp_frame: projection weights or scales missing");
+    if (d->pair) return sk_set_error(SK_EUNSUPPORTED, "sk_cp_frame: a projected code predictor runs unpaired");
+    return sk_cp_frame_proj(d, (hipStream_t)stream);
+  }
   if (d->wd == SK_WD_I8G32) return sk_cp_frame_g32(d, (hipStream_t)stream);
   if (d->wd == SK_WD_BF16) return sk_cp_frame_bf16(d, (hipStream_t)stream);
   sk_talker_desc t;

@@ -173,6 +173,14 @@ template <int H, int I>
 struct SplitGateUp {
   static constexpr bool value = false;
 };
+// Width of the code predictor's input before its projection (small_to_mtp_projection, qwen3/kernels.py:520-521,
+// 629-637): 0, no projection (the position inputs are H wide and enter the stack as they are). A translation unit
+// specialises it before instantiating the code-predictor kernels of a projected code predictor (the 1.7B
+// Qwen3-TTS: 2048-wide inputs into a 1024-wide stack); each position then starts with a projection stage.
+template <int H, int I>
+struct CpProjIn {
+  static constexpr int value = 0;
+};
 
 // W, the compute waves per workgroup, is 4: one per SIMD, with the control wave as the fifth wave of the CU. Each
 // wave then has 256 registers, which is what lets a whole layer of hidden-1024 weights sit in registers and the
@@ -263,6 +271,9 @@ struct PairLayout {
     total = b6 + H;
   }
 };
+
+// Cells of a projected code-predictor input [H], after the paired pass's cells.
+__host__ __device__ inline uint32_t proj_cells(int H, int I) { return PairLayout(H, I).total; }
 
 // Records a timeout: error code, then frame and layer of the stage that gave up (diagnostic words of the workspace).
 struct Ctx;
@@ -371,6 +382,12 @@ __device__ __forceinline__ float stage_rms(const float2 (&v)[NB], const float2 (
     ss += v[b].y * v[b].y;
   }
   return wave_sum(ss);
+}
+// A plain GEMV input from registers (lane holds elements 2 lane + 128 b, + 1 in v[b]) to xs, swizzled (xsw).
+template <int NB>
+__device__ __forceinline__ void stage_plain(const float2 (&v)[NB], float* xs, int lane) {
+#pragma unroll
+  for (int b = 0; b < NB; b++) *(float2*)(xs + xsw(2 * lane + 128 * b)) = v[b];
 }
 template <int NB>
 __device__ __forceinline__ void load_pairs(const float* p, float2 (&w)[NB], int lane) {
@@ -1131,6 +1148,9 @@ struct CpArgs {
   const void* const* head_s;  // [n_positions] bf16 row scales
   int emb0_rows;              // rows of emb[1] (the range code 0 must lie in)
   int pair;                   // positions 0 and 1 in one pass (two rows per stage)
+  const void* proj_w;         // projection [H][CpProjIn] (the kernels of a projected code predictor only)
+  const uint16_t* proj_s;     // its scales (i8row: per row; i8g32: per 32 weights)
+  const float* proj_b;        // its bias [H], nullable
 };
 
 // A code-predictor launch as the kernel takes it: the talker descriptor of the shared kernel (max_len = the positions,
@@ -1144,7 +1164,7 @@ inline void cp_launch_args(const sk_cp_desc* d, sk_talker_desc& t, CpArgs& cp) {
   t.out = d->codes; t.rep_pen = 1.f; t.eos = -1; t.talker_processor = 0;
   t.logits = d->logits; t.layer_out = d->layer_out; t.workspace = d->workspace; t.workspace_bytes = d->workspace_bytes;
   t.do_sample = d->do_sample; t.inv_temp = d->inv_temp; t.top_k = d->top_k; t.seed = d->seed; t.counter = d->counter;
-  cp = CpArgs{d->x0, d->emb, d->head_w, d->head_s, d->emb0_rows, d->pair ? 1 : 0};
+  cp = CpArgs{d->x0, d->emb, d->head_w, d->head_s, d->emb0_rows, d->pair ? 1 : 0, d->proj_w, d->proj_s, d->proj_b};
 }
 
 // Everything a role function needs about this workgroup and launch.
@@ -1176,6 +1196,7 @@ struct Ctx {
   __device__ uint32_t tick(int f, int l, int s) const {
     return base + 1u + (uint32_t)f * tpf + (uint32_t)l * 8u + (uint32_t)s;
   }
+
   __device__ const bf16_t* kh(const sk_layer_desc& Ly) const { return (const bf16_t*)Ly.kc + (size_t)x * d.max_len * SK_HD; }
   __device__ const bf16_t* vh(const sk_layer_desc& Ly) const { return (const bf16_t*)Ly.vc + (size_t)x * d.max_len * SK_HD; }
 };
@@ -1274,6 +1295,10 @@ template <int H, int I, int W, int V, bool CP, bool SMP, bool F16 = false>
 __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
   // The RMSNorm inputs are polled into registers and staged from there (kNP element pairs per lane)
   constexpr int kNP = H / 128;
+  constexpr int PK = CP ? CpProjIn<H, I>::value : 0;
+  // Stage publications per position: 4 per layer, and with a projection one more at the start of each position
+  // (the waits below count 4 (fq L + l) + k, plus kP0 (fq + 1))
+  constexpr uint32_t kP0 = PK > 0 ? 1u : 0u;
   constexpr bool kLO = LaneOffsetPolls<H>::value;
   const Layout LY(H, I);
   const float eps = c.d.eps;
@@ -1301,7 +1326,28 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         float2 w[kNP], v[kNP];
         load_pairs<kNP>(Ly.in_norm, w, lane);
         if (lane == 0) c.tr(0, f, l, 0);
-        if (l == 0) {
+        if (CP && PK > 0 && l == 0) {
+          // S0, the projection: its input (x0 at position 0, else the embedding row of the previous code; PK wide)
+          // staged plainly for the compute waves' dot, then the projected vector polled as the stack's input
+          constexpr int kNPP = PK > 0 ? PK / 128 : 1;
+          float2 x[kNPP];
+          if (f == 0) {
+            load_pairs<kNPP>(c.cp.x0, x, lane);
+          } else {
+            const bf16_t* tab = (const bf16_t*)lane_u64(emb_l, f);
+#pragma unroll
+            for (int b = 0; b < kNPP; b++) {
+              const uint32_t u = gload((const uint32_t*)(tab + (size_t)tok * PK) + lane + 64 * b);
+              x[b] = make_float2(bf2f(u & 0xffffu), bf2f(u >> 16));
+            }
+          }
+          stage_plain<kNPP>(x, S.xs[0], lane);
+          wg_sync();
+          after_publish(S, (uint32_t)(fq * c.L) * 4u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopS1]);
+          u32x4 q[kNP];
+          ok = poll_regs<kNP, kLO>(c.cells, proj_cells(H, I), c.tick(f, 0, 6), q, c.ws, lane, c, 10u, f, l);
+          cells_to_pairs<kNP>(q, v);
+        } else if (l == 0) {
           if (CP && f == 0) {
             load_pairs<kNP>(c.cp.x0, v, lane);
           } else if (!CP && c.d.in_groups > 0) {
@@ -1349,7 +1395,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
             }
           }
         } else {
-          after_publish(S, (uint32_t)(fq * c.L + l) * 4u, c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
+          after_publish(S, (uint32_t)(fq * c.L + l) * 4u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
           u32x4 q[kNP];
           ok = poll_regs<kNP, kLO>(c.cells, LY.e6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
           cells_to_pairs<kNP>(q, v);
@@ -1360,7 +1406,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       wg_sync();
       if (!ok) return;
       // S2 input: this head's q/k/v
-      after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 1u, c.dl[Ws::kHopS2]);
+      after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 1u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopS2]);
       ok = poll_cells<mb(512), false, kLO>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
       if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
@@ -1427,7 +1473,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       {
         float2 w[kNP], v[kNP];
         load_pairs<kNP>(Ly.post_norm, w, lane);
-        after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 2u, c.dl[Ws::kHopS5]);
+        after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 2u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopS5]);
         u32x4 q[kNP];
         ok = poll_regs<kNP, kLO>(c.cells, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
         cells_to_pairs<kNP>(q, v);
@@ -1437,7 +1483,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       wg_sync();
       if (!ok) return;
       // S6 input: the whole SwiGLU activation
-      after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 3u, c.dl[Ws::kHopS6]);
+      after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 3u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopS6]);
       ok = poll_cells<mbh(I), true, kLO>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
       if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
       wg_sync();
@@ -1450,7 +1496,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     {
       float2 w[kNP], v[kNP];
       load_pairs<kNP>(c.d.norm, w, lane);
-      after_publish(S, (uint32_t)((fq + 1) * c.L) * 4u, c.dl[Ws::kHopHead]);
+      after_publish(S, (uint32_t)((fq + 1) * c.L) * 4u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopHead]);
       u32x4 q[kNP];
       // the head of frame 1 after a paired pass reads the pass's second row
       const bool hb = pr && f == 1;
@@ -1831,6 +1877,19 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   uint16_t gq[G32 ? C::RW_QKV : 1][G32 ? C::CH : 1], go[G32 ? C::RW_O : 1][G32 ? C::CQ : 1];
   uint16_t gg[G32 ? C::RW_GU : 1][G32 ? C::CH : 1], gd[G32 ? C::RW_D : 1][G32 ? C::CI : 1];
   uint4 kr[C::KVL], vr[C::KVL];
+  // A projected code predictor (CpProjIn): each wave holds one row of the projection for the whole launch (rows
+  // 4 g .. 4 g + 3 of the workgroup; PK = 2048: 2 chunks per lane for int8, 4 for bf16) and its bias
+  constexpr int PK = CP ? CpProjIn<H, I>::value : 0;
+  constexpr int CPJ = PK > 0 ? PK / 1024 * C::WB : 1;
+  static_assert(PK == 0 || (H / kWG == W && PK % 1024 == 0), "one projection row per compute wave");
+  uint4 wpj[1][CPJ];
+  uint16_t spj[1];
+  uint16_t gpj[1][G32 && PK > 0 ? CPJ : 1];
+  float pbias = 0.f;
+  const int prow = (H / kWG) * g + cw;
+  auto load_proj = [&]() {
+    if constexpr (PK > 0) load_w<WD, 1, CPJ, kLO>(wpj, spj, gpj, (const int8_t*)c.cp.proj_w, c.cp.proj_s, prow, 1, PK, lane);
+  };
   // F16 (a code-predictor launch of at most 16 positions): wave 0 computes this workgroup's attention slice alone,
   // from K / V loaded in load_kv16's layout
   constexpr bool kF16 = CP && F16;
@@ -1853,6 +1912,10 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
   const int p0 = c.pos0 + (f0 && c.n_frames > 2 ? 2 : 0);
   {
     const sk_layer_desc& L0 = S.desc[0];
+    if constexpr (PK > 0) {
+      load_w<WD, 1, CPJ, kLO>(wpj, spj, gpj, (const int8_t*)c.cp.proj_w, c.cp.proj_s, prow, 1, PK, lane);
+      if (c.cp.proj_b) pbias = gload(c.cp.proj_b + prow);
+    }
     load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)L0.qkv_w, L0.qkv_s, q_w0, C::RW_QKV, H, lane);
     if constexpr (kF16) load_kv16(kf, vf, c.kh(L0), c.vh(L0), p0, sl_d0, lane);
     else load_kv<W, C::KVL>(kr, vr, c.kh(L0), c.vh(L0), make_chunk<CP>(p0, r, C::whole(p0)), cw, ag, asl);
@@ -1872,6 +1935,16 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
     const int pos = c.pos0 + f;
     const auto ck = make_chunk<CP>(pos, r, C::whole(pos));
     const bool pr = CP && c.cp.pair;
+    // ---- S0 (a projected code predictor): this wave's projection row, plus the bias, before the position's
+    // layers. The row was loaded after the previous position's head (its registers are the head's), or in the
+    // prologue for position 0; outside the layer loop it is live only from that load to this dot.
+    if constexpr (PK > 0) {
+      wg_sync();  // the projection's input is staged
+      float y[1];
+      dot_w<WD, 1, CPJ>(wpj, gpj, S.xs[0], lane, y);
+      if (lane == 0) S.pub[cw] = y[0] * row_scale_of<WD>(spj[0]) + pbias;
+      publish<W, kLO>(S, c.cells, proj_cells(H, I) + (uint32_t)(H / kWG) * g, H / kWG, c.tick(f, 0, 6), lane);
+    }
     for (int l = 0; l < (pr && f == 1 ? 0 : c.L); l++) {
       const sk_layer_desc& Ly = S.desc[l];
       const bool last_layer = l == c.L - 1;
@@ -2154,6 +2227,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
     }
     if (CP && f == 0) {  // the code predictor's position 0 has no head
       __builtin_amdgcn_s_waitcnt(0);  // same drain as after a head (see below)
+      load_proj();  // the next position's projection row
       continue;
     }
     // ---- head rows (loaded now; the final residual is a full layer away), processor, local argmax ----------
@@ -2190,6 +2264,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
         S.cand[cw] = best;
       }
     }
+    load_proj();  // the next position's projection row, in flight during the pick (the head's registers are free)
     wg_sync();  // candidates ready for the control wave
     wg_sync();  // pick done
     if (S.flags[6]) return;
@@ -2355,11 +2430,13 @@ int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipSt
 template <int H, int I, int W, int V, bool CP, int WD = SK_WD_I8ROW, bool KEEP = false>
 int launch_frames(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
   if (d->max_len > Cfg<H, I, W, V, CP>::kMaxLen) return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: max_len too long");
-  if constexpr (CP) {
+  if constexpr (CP && CpProjIn<H, I>::value == 0) {
     if (cp.pair) {  // the paired pass first (no head: greedy and sampled launches share it)
       const int rc = launch_kernel<H, I, W, V, CP, false, WD, KEEP, true>(d, cp, n_frames, st);
       if (rc != SK_OK) return rc;
     }
+  } else if constexpr (CP) {
+    if (cp.pair) return sk_set_error(SK_EUNSUPPORTED, "sk_cp_frame: a projected code predictor runs unpaired");
   }
   if constexpr (CP) {
     if (d->max_len <= 16)  // the code predictor's 16 positions: the whole-cache attention of F16

@@ -20,5 +20,7 @@ int sk_talker_frames_bf16(const sk_talker_desc* d, int n_frames, hipStream_t st)
 // sk_cp_frame).
 int sk_cp_frame_g32(const sk_cp_desc* d, hipStream_t st);
 int sk_cp_frame_bf16(const sk_cp_desc* d, hipStream_t st);
+// sk_cp_frame of a projected code predictor (proj_in 2048; frame_cp_proj.hip), any of the three weight formats.
+int sk_cp_frame_proj(const sk_cp_desc* d, hipStream_t st);
 
 #define SK_ALIGNED16(p) ((((uintptr_t)(p)) & 15u) == 0)

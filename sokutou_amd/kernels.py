@@ -211,23 +211,29 @@ class CodePredictor:
     (qwen3/kernels.py:666-675 with ``_cp_first`` 641-655): position 0 takes the talker's last hidden state,
     position 1 the talker embedding row of code 0, position g >= 2 the embedding of code g - 1; each position
     g >= 1 ends in the final RMSNorm, head g - 1 and a pick: greedy, or after ``set_sampling`` the fused
-    sampler's draw (temperature, top_k, Philox seed and counter in device memory; one draw per position g >= 1)."""
+    sampler's draw (temperature, top_k, Philox seed and counter in device memory; one draw per position g >= 1).
+    A code predictor narrower than the talker (``cp.small_to_mtp_projection`` not the identity, the 1.7B Qwen3-TTS)
+    projects every position's input, with the projection's bias, before its layers (``_cp_input``,
+    qwen3/kernels.py:629-637): ``x0`` and the tables are then the talker's width."""
 
     def __init__(self, cp, temb: torch.Tensor, n_positions: int = 16, wd: str = "i8row", device=None,
                  x0: torch.Tensor | None = None, id0: torch.Tensor | None = None, codes: torch.Tensor | None = None,
-                 keep_layers: bool = True, pair: bool = True):
+                 keep_layers: bool = True, pair: bool | None = None):
         """``x0`` (fp32 [hidden]), ``id0`` (int64, one element) and ``codes`` (int64 [n_positions]) may be a caller's
         own contiguous device buffers: the kernel then reads and writes them in place (no copies per frame).
         ``keep_layers`` loads the layer weights through the caches (read once per position, they stay in L2 and
         the Infinity Cache across the frame) instead of streaming them like the heads (``sk_cp_desc.keep_layers``).
         ``pair`` runs positions 0 and 1 as one pass with two rows per stage (the reference's cp_pair,
-        qwen3/kernels.py:600-617; ``sk_cp_desc.pair``)."""
+        qwen3/kernels.py:600-617; ``sk_cp_desc.pair``); by default on, and off for a projected code predictor,
+        which the kernel runs unpaired."""
         if wd not in ("i8row", "i8g32", "bf16"):
             raise ValueError("the code-predictor kernel reads i8row, i8g32 or bf16 weights")
         proj = getattr(cp, "small_to_mtp_projection", None)
-        if proj is not None and not isinstance(proj, torch.nn.Identity):
-            raise NotImplementedError("a code predictor narrower than the talker (small_to_mtp_projection) is not "
-                                      "supported by sk_cp_frame")
+        projected = proj is not None and not isinstance(proj, torch.nn.Identity)
+        if pair is None:
+            pair = not projected
+        if projected and pair:
+            raise NotImplementedError("a projected code predictor runs unpaired on sk_cp_frame (pair=False)")
         L = _lib.load()
         self.device = torch.device(device) if device is not None else temb.device
         self.n = int(n_positions)
@@ -236,6 +242,10 @@ class CodePredictor:
             self.heads = [_Lin(h.weight, wd) for h in cp.lm_head][: self.n - 1]
             self.cemb = [e.weight.to(torch.bfloat16).contiguous() for e in cp.get_input_embeddings()][: self.n - 2]
             self.temb = temb.to(torch.bfloat16).contiguous()
+            self.proj = None
+            if projected:
+                bias = getattr(proj, "bias", None)
+                self.proj = (_Lin(proj.weight, wd), None if bias is None else bias.float().contiguous().to(self.device))
         if len(self.heads) != self.n - 1 or len(self.cemb) != self.n - 2:
             raise ValueError(f"{self.n} positions need {self.n - 1} heads and {self.n - 2} code tables")
         P = self.C
@@ -250,7 +260,10 @@ class CodePredictor:
                 raise ValueError(f"a bound buffer must be a contiguous {dtype} tensor of {n} elements on {dev}")
             return t.view(n)
 
-        self.x0 = bind(x0, P.H, torch.float32)
+        self.in_width = self.proj[0].K if self.proj is not None else P.H  # the width of x0 and of the tables' rows
+        if self.temb.shape[1] != self.in_width or any(t.shape[1] != self.in_width for t in self.cemb):
+            raise ValueError(f"the input tables must be {self.in_width} wide")
+        self.x0 = bind(x0, self.in_width, torch.float32)
         self.id0 = bind(id0, 1, torch.int64)
         self.codes = bind(codes, self.n, torch.int64)
         self.logits = torch.zeros(self.V, dtype=torch.float32, device=dev)
@@ -269,6 +282,12 @@ class CodePredictor:
             codes=self.codes.data_ptr(), logits=self.logits.data_ptr(), layer_out=None,
             workspace=self.ws.data_ptr(), workspace_bytes=self.ws.numel(), keep_layers=int(bool(keep_layers)),
             pair=int(bool(pair)))
+        if self.proj is not None:
+            pw, pb = self.proj
+            self._desc.proj_in = pw.K
+            self._desc.proj_w = pw.w.data_ptr()
+            self._desc.proj_s = _sptr(pw)
+            self._desc.proj_b = None if pb is None else pb.data_ptr()
         self.keep_layers = bool(keep_layers)
         self.pair = bool(pair)
         self.wd = wd
@@ -327,7 +346,7 @@ class CodePredictor:
         self.ws.zero_()
 
     def weight_bytes(self) -> int:
-        return self.C.bytes() + sum(h.bytes() for h in self.heads)
+        return self.C.bytes() + sum(h.bytes() for h in self.heads) + (self.proj[0].bytes() if self.proj else 0)
 
 
 class Qwen3Kernels(Qwen3Fast):
@@ -405,7 +424,8 @@ class Qwen3Kernels(Qwen3Fast):
             raise ValueError("frame_kernel=True needs the fused sampler, i8row weights (or i8g32 at hidden 1024), "
                              "16 q / 8 kv heads, vocab 3072, "
                              "hidden 1024 or 2048, a cache of at most 1024 (0.6B) / 2048 (1.7B) positions and, with a "
-                             "code predictor, its one-launch kernel (no projection)")
+                             "code predictor, its one-launch kernel (the 1024-wide code predictor, unprojected or "
+                             "projected from 2048)")
         self.frame_kernel = supported if frame_kernel is None else bool(frame_kernel)
         if self.frame_kernel:
             self._setup_frame_kernel()
@@ -413,9 +433,10 @@ class Qwen3Kernels(Qwen3Fast):
     # --- the code predictor -----------------------------------------------------------------------------------
     def _setup_code_predictor(self, wd: str, cdt) -> None:
         """The code predictor's stack, heads, code tables and optional projection (qwen3/kernels.py:514-523), its
-        cache [layers, nkv, G, 128] and buffers. Greedy sub-codes on the 0.6B-shaped code predictor with no
-        projection run on the one-launch kernel (CodePredictor); anything else runs position by position on the
-        per-op kernels, as the reference does (qwen3/kernels.py:629-675)."""
+        cache [layers, nkv, G, 128] and buffers. Sub-codes of the 1024-wide code predictor (the 0.6B Qwen3-TTS's,
+        and the 1.7B's behind its projection from the talker's 2048-wide rows) run on the one-launch kernel
+        (CodePredictor); anything else runs position by position on the per-op kernels, as the reference does
+        (qwen3/kernels.py:629-675)."""
         cp, dev = self.cp, self.device
         with torch.no_grad():
             self.C = _Stack(cp.model, wd, self.G)
@@ -448,7 +469,10 @@ class Qwen3Kernels(Qwen3Fast):
         self.ck = torch.zeros((len(P.layers), P.nkv, self.G, HD), dtype=cdt, device=dev)
         self.cv = torch.zeros_like(self.ck)
         self.cpk: CodePredictor | None = None
-        fast = ((not self.s.sub_do_sample or self.fs is not None) and self.proj is None
+        # the one-launch kernel takes the 1024-wide code predictor, unprojected or behind a projection from the 1.7B
+        # talker's 2048-wide rows (then unpaired)
+        fast = ((not self.s.sub_do_sample or self.fs is not None)
+                and (self.proj is None or self.proj[0].K == 2048)
                 and wd in ("i8row", "i8g32", "bf16")
                 and self.ct == "bf16" and (P.H, P.I, P.nq, P.nkv, self.cp_heads[0].N) == (1024, 3072, 16, 8, 2048)
                 and 2 <= self.G <= 64)
@@ -456,7 +480,7 @@ class Qwen3Kernels(Qwen3Fast):
             # bound to the frame state: reads ph32 and code 0, writes all G codes, with no copy per frame
             keep = all(Ly[m].pol == 0 for Ly in P.layers for m in ("qkv", "o", "gu", "down"))
             self.cpk = CodePredictor(cp, self.temb, n_positions=self.G, wd=wd, device=dev, x0=self.ph32, id0=self.id0,
-                                     codes=self.codes, keep_layers=keep, pair=self.cp_pair)
+                                     codes=self.codes, keep_layers=keep, pair=self.cp_pair and self.proj is None)
             if self.s.sub_do_sample:  # the fused sampler's draws, in the same order as position by position
                 self.cpk.set_sampling(self.s.sub_temperature, self.s.sub_top_k, self.fs.seed, self.fs.counter)
 
@@ -557,9 +581,9 @@ class Qwen3Kernels(Qwen3Fast):
 
     def frame_error(self) -> int:
         """Error word of the frame kernel's workspace (0 when healthy; reads device memory, so it synchronises).
-        Codes: 2 placement, 5 position/token out of range, 11..18 a poll of stage S1, S2, S3, S4, S5, S6, head,
-        pick timed out, 19 the exchange of a sampled pick timed out (``frame_diag`` tells the frame, layer and
-        workgroup)."""
+        Codes: 2 placement, 5 position/token out of range, 10 the poll of a projected code predictor's input
+        timed out, 11..18 a poll of stage S1, S2, S3, S4, S5, S6, head, pick timed out, 19 the exchange of a
+        sampled pick timed out (``frame_diag`` tells the frame, layer and workgroup)."""
         return int(self.frame_ws[:4].view(torch.int32).item())
 
     def frame_diag(self) -> dict:

@@ -24,7 +24,7 @@ import torch
 
 _TAGS = {"q": 1, "k": 2, "v": 3, "o": 4, "gate": 5, "up": 6, "down": 7, "in_norm": 8, "post_norm": 9, "q_norm": 10,
          "k_norm": 11, "norm": 12, "head": 13, "emb": 14, "kcache": 15, "vcache": 16, "h": 17, "token": 18,
-         "kvlen": 19, "prompt": 20}
+         "kvlen": 19, "prompt": 20, "proj": 21, "bias": 22}
 
 
 @dataclass(frozen=True)
@@ -175,41 +175,62 @@ def make_tts(seed: int, s: TalkerShape, device="cpu", eos: int | None = None, **
 # code predictor (qwen3/kernels.py:516-523: cp.model, cp.lm_head[g], cp.get_input_embeddings()[g],
 # cp.small_to_mtp_projection)
 # ---------------------------------------------------------------------------------------------------------
-CP_LAYER0, CP_FINAL, CP_HEAD0, CP_EMB0, CP_TALKER_EMB, CP_FRAME0 = 100, 150, 200, 300, 400, 500
+CP_LAYER0, CP_FINAL, CP_HEAD0, CP_EMB0, CP_TALKER_EMB, CP_FRAME0, CP_PROJ = 100, 150, 200, 300, 400, 500, 600
 
 
-def cp_weights(seed: int, s: TalkerShape, n_positions: int = 16, talker_vocab: int = 3072) -> dict:
+def cp_weights(seed: int, s: TalkerShape, n_positions: int = 16, talker_vocab: int = 3072,
+               in_hidden: int | None = None) -> dict:
     """fp32 weights of a code predictor with ``s.n_layers`` layers: its layers, final norm, heads 1..n-1
-    ([vocab, hidden] each, head g produces code g), code-embedding tables 2..n-1 ([vocab, hidden] bf16; table g
-    embeds code g - 1) and the talker's own embedding table (which embeds code 0 at position 1)."""
-    return {
+    ([vocab, hidden] each, head g produces code g), code-embedding tables 2..n-1 ([vocab, in] bf16; table g
+    embeds code g - 1) and the talker's own embedding table ([talker_vocab, in]; it embeds code 0 at position 1).
+    ``in_hidden`` (the talker's width, when it differs from the code predictor's) adds the input projection
+    ``proj`` ([hidden, in] N(0, 0.02)) and its bias ``proj_b`` (N(0, 0.02)), the 1.7B Qwen3-TTS's
+    small_to_mtp_projection; the tables are then ``in_hidden`` wide."""
+    win = in_hidden or s.hidden
+    w = {
         "layers": [layer_weights(seed, CP_LAYER0 + i, s) for i in range(s.n_layers)],
         "norm": normal(seed, CP_FINAL, "norm", (s.hidden,), 0.1, 1.0),
         "heads": [normal(seed, CP_HEAD0 + g, "head", (s.vocab, s.hidden), 0.02) for g in range(1, n_positions)],
-        "cemb": [bf16_values(normal(seed, CP_EMB0 + g, "emb", (s.vocab, s.hidden), 0.02)) for g in range(2, n_positions)],
-        "temb": bf16_values(normal(seed, CP_TALKER_EMB, "emb", (talker_vocab, s.hidden), 0.02)),
+        "cemb": [bf16_values(normal(seed, CP_EMB0 + g, "emb", (s.vocab, win), 0.02)) for g in range(2, n_positions)],
+        "temb": bf16_values(normal(seed, CP_TALKER_EMB, "emb", (talker_vocab, win), 0.02)),
     }
+    if win != s.hidden:
+        w["proj"] = normal(seed, CP_PROJ, "proj", (s.hidden, win), 0.02)
+        w["proj_b"] = normal(seed, CP_PROJ, "bias", (s.hidden,), 0.02)
+    return w
 
 
-def cp_frame_inputs(seed: int, f: int, s: TalkerShape, talker_vocab: int = 3072) -> tuple[np.ndarray, int]:
-    """Inputs of code-predictor frame ``f``: the talker's last hidden state x0 ~ N(0, 1) (fp32) and code 0."""
-    x0 = normal(seed, CP_FRAME0 + f, "h", (s.hidden,))
+def cp_frame_inputs(seed: int, f: int, s: TalkerShape, talker_vocab: int = 3072,
+                    in_hidden: int | None = None) -> tuple[np.ndarray, int]:
+    """Inputs of code-predictor frame ``f``: the talker's last hidden state x0 ~ N(0, 1) (fp32; ``in_hidden``
+    wide when given, else the code predictor's width) and code 0."""
+    x0 = normal(seed, CP_FRAME0 + f, "h", (in_hidden or s.hidden,))
     return x0, int(_rng(seed, CP_FRAME0 + f, "token").integers(0, talker_vocab))
 
 
-def make_code_predictor(seed: int, s: TalkerShape, device="cpu", n_positions: int = 16, w: dict | None = None):
+def make_code_predictor(seed: int, s: TalkerShape, device="cpu", n_positions: int = 16, w: dict | None = None,
+                        in_hidden: int | None = None):
     """(cp, talker embedding) with the attributes the engine reads: ``cp.model`` (layers, norm, rotary_emb,
     config), ``cp.lm_head`` (n - 1 heads), ``cp.get_input_embeddings()`` (n - 1 tables: entry g - 1 embeds
-    code g; the last one is only used by the talker's input), ``cp.small_to_mtp_projection`` (identity: the
-    talker and the code predictor are both 1024 wide) and ``cp.config.vocab_size``."""
-    w = w if w is not None else cp_weights(seed, s, n_positions)
+    code g; the last one is only used by the talker's input), ``cp.small_to_mtp_projection`` (identity when the
+    talker and the code predictor are equally wide, else a ``torch.nn.Linear`` with bias, from the weights'
+    ``proj`` / ``proj_b``; ``in_hidden`` is the talker's width) and ``cp.config.vocab_size``."""
+    w = w if w is not None else cp_weights(seed, s, n_positions, in_hidden=in_hidden)
+    win = w["temb"].shape[1]
     base = make_talker(seed, s, device, layers=w["layers"],
                        final={"norm": w["norm"], "head": w["heads"][0], "emb": w["temb"]})
     cemb = [SimpleNamespace(weight=torch.from_numpy(t).to(device=device, dtype=torch.bfloat16)) for t in w["cemb"]]
     # the talker's input also embeds the last code: one more table, unused by the code predictor itself
-    cemb.append(SimpleNamespace(weight=torch.zeros((s.vocab, s.hidden), dtype=torch.bfloat16, device=device)))
+    cemb.append(SimpleNamespace(weight=torch.zeros((s.vocab, win), dtype=torch.bfloat16, device=device)))
+    proj = torch.nn.Identity()
+    if "proj" in w:
+        proj = torch.nn.Linear(win, s.hidden, bias=True)
+        with torch.no_grad():
+            proj.weight.copy_(torch.from_numpy(w["proj"]))
+            proj.bias.copy_(torch.from_numpy(w["proj_b"]))
+        proj = proj.to(device)
     cp = SimpleNamespace(model=base.model, lm_head=[_p(h, device) for h in w["heads"]],
-                         small_to_mtp_projection=torch.nn.Identity(), config=SimpleNamespace(vocab_size=s.vocab))
+                         small_to_mtp_projection=proj, config=SimpleNamespace(vocab_size=s.vocab))
     cp.get_input_embeddings = lambda: cemb
     temb = torch.from_numpy(w["temb"]).to(device=device, dtype=torch.bfloat16)
     return cp, temb
@@ -221,7 +242,8 @@ def make_tts_with_cp(seed: int, s: TalkerShape, cp_shape: TalkerShape, device="c
     (qwen3/kernels.py:514-523). Returns (tts, pad row): the pad row is the bf16 ``tts_pad_embed`` added to every
     talker input, N(0, 0.02)."""
     tts = make_tts(seed, s, device=device)
-    w = cp_weights(seed, cp_shape, n_groups, talker_vocab=s.vocab)
+    w = cp_weights(seed, cp_shape, n_groups, talker_vocab=s.vocab,
+                   in_hidden=s.hidden if s.hidden != cp_shape.hidden else None)
     w["temb"] = final_weights(seed, s)["emb"]
     cp, _ = make_code_predictor(seed, cp_shape, device=device, n_positions=n_groups, w=w)
     tts.model.talker.code_predictor = cp
@@ -249,9 +271,16 @@ WORKLOADS = {
     # code predictor: 5 layers of the 0.6B shape, 2048-way heads, 16 positions (KV 1 -> 16) per frame, greedy
     # sub-codes; a step is `frames` code-predictor frames with different (x0, code 0)
     "cp06b": dict(shape="0.6b", n_layers=5, vocab=2048, kv=0, positions=16, frames=8),
+    # the 1.7B Qwen3-TTS code predictor: the same 1024-wide stack behind a projection from the talker's 2048-wide
+    # hidden state and embedding rows (small_to_mtp_projection, with bias)
+    "cp17b": dict(shape="0.6b", n_layers=5, vocab=2048, kv=0, positions=16, frames=8, in_hidden=2048),
     # the whole Qwen3-TTS frame: the 0.6B talker (KV 512) fed by a 5-layer code predictor (16 code groups),
     # 64 greedy frames
     "frame06b": dict(shape="0.6b", n_layers=28, kv=512, frames=64, cp="cp06b"),
+    # the whole 1.7B Qwen3-TTS frame: the 1.7B talker (KV 1024) fed by the projected code predictor
+    "frame17b": dict(shape="1.7b", n_layers=28, kv=1024, frames=64, cp="cp17b"),
+    # the same with a two-layer talker, for quick checks
+    "frame17small": dict(shape="1.7b", n_layers=2, kv=40, frames=8, cp="cp17b"),
     # 16 concurrent 1.7B-shaped streams, prior KV lengths uniform in [64, 2048], 32 greedy frames
     "batch17b": dict(shape="1.7b", n_layers=28, kv=0, batch=16, kv_lo=64, kv_hi=2048, frames=32),
     # the same with two layers and five streams, for quick checks
@@ -447,16 +476,17 @@ def make_prefill_engine(name: str, seed: int = 0, L: int = 24, frames: int = 8, 
     return eng, kw
 
 
-def make_cp_engine(name: str = "cp06b", seed: int = 0, device="cuda", keep_layers: bool = True, pair: bool = True,
-                   wd: str = "i8row", positions: int | None = None):
+def make_cp_engine(name: str = "cp06b", seed: int = 0, device="cuda", keep_layers: bool = True,
+                   pair: bool | None = None, wd: str = "i8row", positions: int | None = None):
     """A CodePredictor over the seeded synthetic code predictor of workload ``name`` (one frame per run);
     ``keep_layers``, ``pair`` and ``wd`` as CodePredictor's (layer weights loaded cacheable, positions 0 and 1
-    paired, i8row: the defaults); ``positions`` overrides the workload's count of positions."""
+    paired unless the code predictor is projected, i8row: the defaults); ``positions`` overrides the workload's
+    count of positions."""
     from .kernels import CodePredictor
 
     n = positions or WORKLOADS[name]["positions"]
     s = workload_shape(name)
-    cp, temb = make_code_predictor(seed, s, device=device, n_positions=n)
+    cp, temb = make_code_predictor(seed, s, device=device, n_positions=n, in_hidden=WORKLOADS[name].get("in_hidden"))
     return CodePredictor(cp, temb, n_positions=n, wd=wd, device=device, keep_layers=keep_layers, pair=pair)
 
 

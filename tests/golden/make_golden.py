@@ -129,7 +129,7 @@ def code_predictor(name: str = "cp06b", seed: int = 0, wd: str = "i8row") -> Non
     layer_out: list = []
     last = None
     for f in range(spec["frames"]):
-        x0, id0 = syn.cp_frame_inputs(seed, f, s)
+        x0, id0 = syn.cp_frame_inputs(seed, f, s, in_hidden=spec.get("in_hidden"))
         inputs.append({"id0": id0, "x0_sha256": syn.sha256(x0)})
         c, lg = orc.frame(x0, id0, layer_out if f == 0 else None)
         codes.append(c)
@@ -144,6 +144,23 @@ def code_predictor(name: str = "cp06b", seed: int = 0, wd: str = "i8row") -> Non
             "oracle_seconds": {"build": round(t1 - t0, 1), "frames": round(t2 - t1, 1)}}
     (HERE / f"{stem}.json").write_text(json.dumps(meta, indent=1))
     print(name, "codes[0]", codes[0], "min margin", meta["min_margin"], meta["oracle_seconds"])
+
+
+def whole_frame(name: str = "frame17b", seed: int = 0, wd: str = "i8row", frames: int = 8) -> None:
+    """Whole Qwen3-TTS frames (the code predictor's 15 sub-codes, then the talker on talker_in of the 16 codes):
+    all 16 codes of ``frames`` greedy frames, the top-1/top-2 margins of every pick, and the talker's logits of the
+    first and last frame."""
+    from oracle.workload import frame_oracle
+
+    t0 = time.time()
+    codes, tok, margins, logits = frame_oracle(name, seed, wd, frames, detail=True)
+    t1 = time.time()
+    stem = f"{name}_seed{seed}" if wd == "i8row" else f"{name}_{wd}_seed{seed}"
+    np.savez_compressed(HERE / f"{stem}.npz", logits_first=logits[0], logits_last=logits[-1])
+    meta = {"workload": name, "seed": seed, "wd": wd, "start_token": tok, "frames": frames, "codes": codes,
+            "margins": margins, "min_margin": min(min(m) for m in margins), "oracle_seconds": round(t1 - t0, 1)}
+    (HERE / f"{stem}.json").write_text(json.dumps(meta, indent=1))
+    print(stem, "codes[0]", codes[0], "min margin", meta["min_margin"], meta["oracle_seconds"])
 
 
 def batch(name: str = "batch17b", seed: int = 0, rows=(0, 1)) -> None:
@@ -193,7 +210,10 @@ if __name__ == "__main__":
             "talker17b": lambda: talker("talker17b", 0), "cp06b": lambda: code_predictor("cp06b", 0),
             "cp06b_i8g32": lambda: code_predictor("cp06b", 0, "i8g32"),
             "talker06b_bf16": lambda: talker("talker06b", 0, "bf16"), "cp06b_bf16": lambda: code_predictor("cp06b", 0, "bf16"),
-            "batch17b": lambda: batch("batch17b", 0)}
+            "batch17b": lambda: batch("batch17b", 0),
+            "cp17b": lambda: code_predictor("cp17b", 0), "cp17b_i8g32": lambda: code_predictor("cp17b", 0, "i8g32"),
+            "cp17b_bf16": lambda: code_predictor("cp17b", 0, "bf16"),
+            "frame17b": lambda: whole_frame("frame17b", 0)}
     for n, fn in jobs.items():
         if a.only in (None, n):
             fn()

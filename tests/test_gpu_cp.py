@@ -114,3 +114,41 @@ def test_code_predictor_24_positions_against_oracle(gpu, pair):
         assert eng.error() == 0
         assert codes == ref, (f, codes, ref)
         assert rel_err(eng.logits, lg[-1]) < TOL
+
+
+@pytest.mark.parametrize("wd", ["i8row", "i8g32", "bf16"])
+def test_projected_code_predictor_against_oracle(gpu, wd):
+    """The 1.7B Qwen3-TTS code predictor: the 1024-wide stack behind small_to_mtp_projection (2048 -> 1024, with
+    bias, qwen3/kernels.py:520-521, 629-637), one launch per frame with a projection stage at the start of every
+    position (x0 and the embedding rows are the talker's 2048-wide ones). Codes of 8 frames, and per-layer
+    residuals and logits at the last position of frame 0, against the oracle fixture; then a graph replay."""
+    stem = "cp17b_seed0" if wd == "i8row" else f"cp17b_{wd}_seed0"
+    meta = json.loads((GOLD / f"{stem}.json").read_text())
+    gold = np.load(GOLD / f"{stem}.npz")
+    print(f"cp17b ({wd}): building the projected code predictor (5 layers, 15 heads, projection 2048 -> 1024)",
+          flush=True)
+    eng = syn.make_cp_engine("cp17b", 0, gpu, wd=wd)
+    assert eng.proj is not None and not eng.pair and eng.x0.numel() == 2048
+    s = syn.workload_shape("cp17b")
+    eng.layer_out = torch.zeros((s.n_layers, s.hidden), device=gpu)
+    for f, ref in enumerate(meta["codes"]):
+        x0, id0 = syn.cp_frame_inputs(0, f, s, in_hidden=2048)
+        assert id0 == meta["inputs"][f]["id0"]
+        print(f"frame {f}: one launch of {meta['positions']} positions", flush=True)
+        codes = eng(torch.from_numpy(x0).to(gpu), id0).cpu().tolist()
+        assert eng.error() == 0, eng.diag()
+        assert codes == ref, (f, codes, ref)
+        if f == 0:
+            errs = [rel_err(eng.layer_out[i], gold["layer_out_last0"][i]) for i in range(s.n_layers)]
+            print(f"per-layer max rel err {max(errs):.3e}", flush=True)
+            assert max(errs) < TOL
+            assert rel_err(eng.logits, gold["logits_last0"]) < TOL
+    eng.layer_out = None
+    eng.capture()
+    for f in (5, 2):
+        x0, id0 = syn.cp_frame_inputs(0, f, s, in_hidden=2048)
+        eng.x0.copy_(torch.from_numpy(x0))
+        eng.id0.fill_(id0)
+        eng.graph.replay()
+        assert eng.codes.cpu().tolist() == meta["codes"][f]
+    assert eng.error() == 0

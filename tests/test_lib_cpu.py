@@ -83,13 +83,31 @@ def test_cp_frame_rejects_bad_shapes_without_launching():
     assert L.sk_cp_frame(ctypes.byref(d), None) == _lib.SK_EUNSUPPORTED
 
 
-def test_cp_workspace_size_covers_the_paired_rows():
-    """Serial positions need the talker's workspace; pairing adds the second row's cells (q|k|v of 8 heads,
-    attention output, h after o, activation, h after down: 4096 + 2048 + 1024 + 3072 + 1024 cells of 8 bytes)."""
+def test_cp_frame_checks_the_projection_without_launching():
+    """A projected code predictor: 2048-wide inputs only, its weights (and scales, for int8) present, unpaired."""
+    L = _lib.load()
+    dv = ctypes.c_void_p(256)
+    c = _lib.SkCpDesc(n_layers=5, hidden=1024, inter=3072, nq=16, nkv=8, vocab=2048, n_positions=16,
+                      wd=_lib.WD["i8row"], ct=_lib.CT["bf16"], eps=1e-6, layers=dv, norm=dv, rope=dv, x0=dv, id0=dv,
+                      emb0_rows=3072, emb=dv, head_w=dv, head_s=dv, codes=dv, workspace=dv,
+                      workspace_bytes=int(L.sk_cp_workspace_size(1024, 3072, 0)), proj_in=1536, proj_w=dv, proj_s=dv)
+    assert L.sk_cp_frame(ctypes.byref(c), None) == _lib.SK_EUNSUPPORTED
+    c.proj_in, c.proj_s = 2048, None
+    assert L.sk_cp_frame(ctypes.byref(c), None) == _lib.SK_EINVAL  # int8 projection without its scales
+    c.proj_s, c.pair = dv, 1
+    assert L.sk_cp_frame(ctypes.byref(c), None) == _lib.SK_EUNSUPPORTED
+    assert b"unpaired" in L.sk_last_error()
+
+
+def test_cp_workspace_size_covers_the_paired_rows_and_the_projection():
+    """The talker's workspace, then the paired pass's second row (q|k|v of 8 heads, attention output, h after o,
+    activation, h after down: 4096 + 2048 + 1024 + 3072 + 1024 cells of 8 bytes), then a projected input's
+    1024 cells; one size serves paired, serial and projected code predictors."""
     L = _lib.load()
     base = L.sk_talker_workspace_size(1024, 3072)
-    assert L.sk_cp_workspace_size(1024, 3072, 0) == base
-    assert L.sk_cp_workspace_size(1024, 3072, 1) == base + 8 * (8 * 512 + 2048 + 1024 + 3072 + 1024)
+    want = base + 8 * (8 * 512 + 2048 + 1024 + 3072 + 1024) + 8 * 1024
+    assert L.sk_cp_workspace_size(1024, 3072, 0) == want
+    assert L.sk_cp_workspace_size(1024, 3072, 1) == want
     assert L.sk_cp_workspace_size(0, 3072, 1) == 0
 
 
@@ -138,8 +156,9 @@ def test_frame_kernels_reject_sampling_without_seed_or_temperature():
     assert L.sk_talker_frames(ctypes.byref(t), 1, None) == _lib.SK_EINVAL
     c = _lib.SkCpDesc(n_layers=5, hidden=1024, inter=3072, nq=16, nkv=8, vocab=2048, n_positions=16,
                       wd=_lib.WD["i8row"], ct=_lib.CT["bf16"], eps=1e-6, layers=d, norm=d, rope=d, x0=d, id0=d,
-                      emb0_rows=3072, emb=d, head_w=d, head_s=d, codes=d, workspace=d, workspace_bytes=ws,
-                      do_sample=1, inv_temp=1.25, top_k=40, seed=d, counter=None)
+                      emb0_rows=3072, emb=d, head_w=d, head_s=d, codes=d, workspace=d,
+                      workspace_bytes=int(L.sk_cp_workspace_size(1024, 3072, 0)), do_sample=1, inv_temp=1.25,
+                      top_k=40, seed=d, counter=None)
     assert L.sk_cp_frame(ctypes.byref(c), None) == _lib.SK_EINVAL
     assert b"sampling" in L.sk_last_error()
 

@@ -295,11 +295,13 @@ def test_process_logits_matches_torch_processor():
 
 
 # ---- code predictor composition -----------------------------------------------------------------------------
-def test_code_predictor_frame_matches_transformers_stack():
+@pytest.mark.parametrize("projected", [False, True])
+def test_code_predictor_frame_matches_transformers_stack(projected):
     """The code-predictor loop (inputs per position, growing cache, final norm + per-position head, greedy
     pick) against a stack of transformers' Qwen3DecoderLayer run position by position over one DynamicCache,
     Qwen3RMSNorm and a torch matmul head, f32 cache: the same codes at every position and logits to fp32
-    rounding. Tiny shape, 2 layers, 6 positions."""
+    rounding. Tiny shape, 2 layers, 6 positions. ``projected``: inputs twice as wide as the stack, each taken
+    through torch.nn.functional.linear with a bias first (small_to_mtp_projection, qwen3/kernels.py:629-637)."""
     from transformers import DynamicCache
     from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
 
@@ -310,14 +312,18 @@ def test_code_predictor_frame_matches_transformers_stack():
     norm = (1 + 0.1 * rng.standard_normal(s.hidden)).astype(F32)
     # large head weights so every position has a clear winner (the check is about composition, not ties)
     heads = [(0.5 * rng.standard_normal((s.vocab, s.hidden))).astype(F32) for _ in range(n - 1)]
-    cemb = [rng.standard_normal((s.vocab, s.hidden)).astype(F32) for _ in range(n - 2)]
-    temb = rng.standard_normal((96, s.hidden)).astype(F32)
-    x0 = rng.standard_normal(s.hidden).astype(F32)
+    win = 2 * s.hidden if projected else s.hidden
+    cemb = [rng.standard_normal((s.vocab, win)).astype(F32) for _ in range(n - 2)]
+    temb = rng.standard_normal((96, win)).astype(F32)
+    x0 = rng.standard_normal(win).astype(F32)
     id0 = 77
     rope = O.rope_table(syn.inv_freq(s), n)
-    orc = O.CodePredictorOracle({"layers": [_oracle_layer_weights(w) for w in layers], "norm": norm, "heads": heads,
-                                 "cemb": cemb, "temb": temb, "rope": rope, "eps": s.eps, "nq": s.nq, "nkv": s.nkv},
-                                n, cache_bf16=False)
+    wts = {"layers": [_oracle_layer_weights(w) for w in layers], "norm": norm, "heads": heads, "cemb": cemb,
+           "temb": temb, "rope": rope, "eps": s.eps, "nq": s.nq, "nkv": s.nkv}
+    if projected:
+        wts["proj"] = (0.05 * rng.standard_normal((s.hidden, win))).astype(F32)
+        wts["proj_b"] = (0.5 * rng.standard_normal(s.hidden)).astype(F32)
+    orc = O.CodePredictorOracle(wts, n, cache_bf16=False)
     codes, logits = orc.frame(x0, id0)
     hf = [_hf_layer(s, w) for w in layers]
     for i, (layer, _) in enumerate(hf):
@@ -330,6 +336,8 @@ def test_code_predictor_frame_matches_transformers_stack():
     for g in range(n):
         x = x0 if g == 0 else temb[id0] if g == 1 else cemb[g - 2][ref_codes[g - 1]]
         h = torch.from_numpy(np.asarray(x, F32))[None, None, :]
+        if projected:
+            h = torch.nn.functional.linear(h, torch.from_numpy(wts["proj"]), torch.from_numpy(wts["proj_b"]))
         pid = torch.tensor([[g]])
         with torch.no_grad():
             for layer, rot in hf:
