@@ -111,11 +111,12 @@ def time_kernels(eng, reps: int = 200) -> dict:
     return out
 
 
-def cp_algorithmic_bytes(s, positions: int = 16, wd: str = "i8row") -> dict:
+def cp_algorithmic_bytes(s, positions: int = 16, wd: str = "i8row", in_hidden: int | None = None) -> dict:
     """Bytes one code-predictor frame must move: the stack's weights and scales once per pass, positions 0 and 1
     counted as one pass as the reference pairs them (positions - 1 passes), plus the 15 heads once each and the
     K/V reads and appends of every position. Weights 1 B (int8) or 2 B (bf16) each; scales a bf16 per row (i8row),
-    an fp16 per 32 weights (i8g32) or none (bf16)."""
+    an fp16 per 32 weights (i8g32) or none (bf16). ``in_hidden``: the width of a projected input (the 1.7B code
+    predictor's small_to_mtp_projection), whose matrix every position reads once more, and its fp32 bias."""
     H, I, nq, nkv, hd = s.hidden, s.inter, s.nq, s.nkv, s.head_dim
     wb = {"i8row": 1, "i8g32": 1, "bf16": 2}[wd]
 
@@ -126,8 +127,9 @@ def cp_algorithmic_bytes(s, positions: int = 16, wd: str = "i8row") -> dict:
     layer = mat((nq + 2 * nkv) * hd, H) + mat(H, nq * hd) + mat(2 * I, H) + mat(H, I)
     kv = sum(2 * nkv * (p + 1) * hd * 2 + 2 * nkv * hd * 2 for p in range(positions)) * s.n_layers
     heads = (positions - 1) * mat(s.vocab, H)
-    return {"per_pass": layer * s.n_layers, "frame": (positions - 1) * layer * s.n_layers + heads + kv,
-            "frame_16_passes": positions * layer * s.n_layers + heads + kv}
+    proj = positions * (mat(H, in_hidden) + 4 * H) if in_hidden else 0
+    return {"per_pass": layer * s.n_layers, "frame": (positions - 1) * layer * s.n_layers + heads + kv + proj,
+            "frame_16_passes": positions * layer * s.n_layers + heads + kv + proj, "projection": proj}
 
 
 def run_cp(args) -> None:
@@ -139,12 +141,13 @@ def run_cp(args) -> None:
     from sokutou_amd import synthetic as syn
 
     dev = torch.device("cuda:0")
-    name = "cp06b"
+    name = args.workload
     spec = syn.WORKLOADS[name]
     s = syn.workload_shape(name)
+    win = spec.get("in_hidden")
     t0 = time.perf_counter()
     eng = syn.make_cp_engine(name, args.seed, dev, wd=args.wd)
-    x0, id0 = syn.cp_frame_inputs(args.seed, 0, s)
+    x0, id0 = syn.cp_frame_inputs(args.seed, 0, s, in_hidden=win)
     eng.x0.copy_(torch.from_numpy(x0))
     eng.id0.fill_(id0)
     setup_s = time.perf_counter() - t0
@@ -179,16 +182,20 @@ def run_cp(args) -> None:
         parity = eng.codes.cpu().tolist() == json.loads(gold.read_text())["codes"][0]
     fps = frames * args.steps / dt
     launch_us = sum(a.elapsed_time(b) for a, b in ev) * 1e3 / len(ev)
-    ab = cp_algorithmic_bytes(s, spec["positions"], args.wd)
+    ab = cp_algorithmic_bytes(s, spec["positions"], args.wd, win)
     achieved = ab["frame"] / (launch_us * 1e-6) / 1e9
     res = {
-        "metric": "code predictor frames/sec (5 layers of the 0.6B shape, 16 positions, 15 greedy sub-codes, int8)",
+        "metric": ("code predictor frames/sec (5 layers of the 0.6B shape, 16 positions, 15 greedy sub-codes, int8)"
+                   if not win else "code predictor frames/sec (the 1.7B model's: 5 layers of hidden 1024 behind a "
+                   f"{win} -> 1024 projection, 16 positions, 15 greedy sub-codes, int8)"),
         "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8 weights x fp32 accumulate (bf16 KV cache)", "data": "synthetic",
         "config": {"workload": f"{name}: {s.n_layers} layers, hidden {s.hidden}, {s.nq}q/{s.nkv}kv heads x 128, "
                                f"intermediate {s.inter}, 15 heads of {s.vocab}, {args.wd}, {spec['positions']} positions "
-                               f"(KV 1..16) per frame, {frames} frames per step", "weights": args.wd,
+                               f"(KV 1..16) per frame, "
+                               + (f"inputs {win} wide through the projection (with bias), " if win else "")
+                               + f"{frames} frames per step", "weights": args.wd,
                    "engine": "sk_cp_frame (paired pass of positions 0 and 1, then one launch for the rest)"
                    if eng.pair else "sk_cp_frame (one launch per frame)"},
         "roofline": {"bound": "hbm", "kernel": "k_frames code-predictor mode (sk_cp_frame; both launches of a frame)",
@@ -199,7 +206,9 @@ def run_cp(args) -> None:
                              + ("positions 0 and 1 share one pass over the layers (15 passes, as the algorithmic "
                                 "bytes count them); avg_launch_us spans both launches of a frame" if eng.pair else
                                 "the kernel runs positions 0 and 1 as two passes (16 passes, "
-                                f"{ab['frame_16_passes']} bytes touched)")},
+                                f"{ab['frame_16_passes']} bytes touched)")
+                             + (f"; every position reads the projection once ({ab['projection']} bytes per frame)"
+                                if win else "")},
         "frame": {"us_per_frame": round(launch_us, 2), "us_per_position": round(launch_us / spec["positions"], 2),
                   "us_per_layer_pass": round(launch_us / spec["positions"] / s.n_layers, 3)},
         "parity_codes_match_oracle": parity, "setup_s": round(setup_s, 1),
@@ -212,7 +221,7 @@ def run_cp(args) -> None:
         times = []
         t_start = time.perf_counter()
         while time.perf_counter() - t_start < 15.0 and len(times) < 64:
-            xf, i0 = syn.cp_frame_inputs(args.seed, len(times) % frames, s)
+            xf, i0 = syn.cp_frame_inputs(args.seed, len(times) % frames, s, in_hidden=win)
             t1 = time.perf_counter()
             orc.frame(xf, i0)
             times.append(time.perf_counter() - t1)
@@ -448,11 +457,25 @@ def run_frame(args) -> None:
     cp_us = sum(a.elapsed_time(b) for a, b in ev_cp) * 1e3 / F
     t_us = sum(a.elapsed_time(b) for a, b in ev_t) * 1e3 / F
     fps = F * args.steps / dt
+    win = syn.WORKLOADS[spec["cp"]].get("in_hidden")
     talker_b = sum(algorithmic_bytes(s, kv + 1 + f, args.wd)["frame"] for f in range(F)) / F
-    cp_b = cp_algorithmic_bytes(cs, 16, args.wd)["frame"]
+    cp_b = cp_algorithmic_bytes(cs, 16, args.wd, win)["frame"]
     frame_b = talker_b + cp_b
+    # greedy parity: the first frames of a step against the whole-frame oracle fixture, when there is one
+    parity = None
+    gold = ROOT / "tests" / "golden" / (f"{name}_seed{args.seed}.json" if args.wd == "i8row" else
+                                        f"{name}_{args.wd}_seed{args.seed}.json")
+    if not args.sampling and gold.exists():
+        ref = json.loads(gold.read_text())["codes"]
+        eng._start(kw)
+        got = []
+        for _ in range(len(ref)):
+            eng.graph.replay()
+            got.append(eng.codes.view(-1).cpu().tolist())
+        parity = got == ref
     res = {
-        "metric": "whole Qwen3-TTS frame frames/sec (0.6B talker int8 KV 512 + 5-layer code predictor, 16 code groups)",
+        "metric": (f"whole Qwen3-TTS frame frames/sec ({'0.6B' if s.hidden == 1024 else '1.7B'} talker int8 KV {kv} + "
+                   f"5-layer code predictor{' behind its projection' if win else ''}, 16 code groups)"),
         "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3 / args.steps, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8 weights x fp32 accumulate (bf16 KV cache)", "data": "synthetic",
@@ -468,8 +491,12 @@ def run_frame(args) -> None:
         "frame": {"us_per_frame": round(1e6 / fps, 2), "code_predictor_us": round(cp_us, 2), "talker_us": round(t_us, 2),
                   "algorithmic_bytes_per_frame": int(frame_b),
                   "effective_GBs": round(frame_b * fps / 1e9, 1)},
-        "reference_published": {"ms_per_frame": 2.84, "setup": "RTX 6000 Ada, real Qwen3-TTS 0.6B weights (i8g32), "
-                                "sampled decoding (docs/results.md:212, 226); a different workload, so vs_baseline is null"},
+        "reference_published": ({"ms_per_frame": 2.84, "setup": "RTX 6000 Ada, real Qwen3-TTS 0.6B weights (i8g32), "
+                                 "sampled decoding (docs/results.md:212, 226); a different workload, so vs_baseline is null"}
+                                if s.hidden == 1024 else
+                                {"ms_per_frame": 4.34, "setup": "RTX 6000 Ada, real Qwen3-TTS 1.7B weights (i8g32), "
+                                 "sampled decoding (docs/results.md:220); a different workload, so vs_baseline is null"}),
+        "parity_codes_match_oracle": parity,
         "setup_s": round(setup_s, 1),
     }
     if not args.no_cpu:
@@ -479,7 +506,7 @@ def run_frame(args) -> None:
         torc, otok, _ = talker_oracle(name, args.seed, args.wd, max_len=kv + F + 1)
         corc, _ = cp_oracle(spec["cp"], args.seed, wd=args.wd)
         corc.w["temb"] = torc.w["emb"]
-        w = syn.cp_weights(args.seed, cs, 16, talker_vocab=s.vocab)
+        w = syn.cp_weights(args.seed, cs, 16, talker_vocab=s.vocab, in_hidden=win)
         tabs = [torc.w["emb"]] + list(w["cemb"]) + [np.zeros((cs.vocab, s.hidden), np.float32)]
         pad = kw["tts_pad_embed"].numpy()
         ph, t, times = kw["last_hidden"].numpy(), otok, []
@@ -544,14 +571,15 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="talker06b", choices=["talker06b", "talker17b", "cp06b", "batch17b", "frame06b"])
+    ap.add_argument("--workload", default="talker06b",
+                    choices=["talker06b", "talker17b", "cp06b", "cp17b", "batch17b", "frame06b", "frame17b"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--engine", default="frames", choices=["frames", "graph", "multi"])
     ap.add_argument("--wd", default="i8row", choices=["i8row", "i8g32", "bf16"],
                     help="weight format of the talker (the reference's i8g32 and bf16 formats as well as i8row)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--sampling", action="store_true",
-                    help="talker06b / talker17b / frame06b with the reference's default sampled decoding (temperature "
+                    help="talker06b / talker17b / frame06b / frame17b with the reference's default sampled decoding (temperature "
                          "0.9, top_k 50, repetition penalty 1.05, the last 1024 ids suppressed) instead of greedy")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the run, copy this many MiB device-to-device twice (a plain copy of known size that "
@@ -562,7 +590,8 @@ def main() -> None:
               "(this build has no multi-GPU path); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
-    other = {"cp06b": run_cp, "batch17b": run_batch, "frame06b": run_frame}.get(args.workload)
+    other = {"cp06b": run_cp, "cp17b": run_cp, "batch17b": run_batch, "frame06b": run_frame,
+             "frame17b": run_frame}.get(args.workload)
     if other is not None:
         other(args)
         calibration_copy(args.calibration_copy_mib)
