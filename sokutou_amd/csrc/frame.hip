@@ -3,15 +3,6 @@
 // frame17.hip (4 compute waves, register polls).
 #include "frame_impl.h"
 
-namespace {
-// the sampled pick gathers 4 cell pairs per batch here as well (measured 0.6% faster on sampled 0.6B frames; the
-// greedy kernels' code is unchanged by it)
-template <>
-struct PickBatch<kTalkerV, kTalkerV / kWG> {
-  static constexpr int value = 4;
-};
-}  // namespace
-
 extern "C" int64_t sk_talker_workspace_size(int hidden, int inter) {
   if (hidden <= 0 || inter <= 0) return 0;
   const Layout LY(hidden, inter);

@@ -4,14 +4,6 @@
 // with the group scales applied per 16-weight chunk inside the dots.
 #include "frame_impl.h"
 
-namespace {
-// the sampled pick gathers 4 cell pairs per batch, as the i8row talker does
-template <>
-struct PickBatch<kTalkerV, kTalkerV / kWG> {
-  static constexpr int value = 4;
-};
-}  // namespace
-
 int sk_talker_frames_g32(const sk_talker_desc* d, int n_frames, hipStream_t st) {
   const CpArgs none{};
   return launch_frames<1024, 3072, 4, kTalkerV, false, SK_WD_I8G32>(d, none, n_frames, st);

@@ -258,6 +258,11 @@ struct LdsPair {
   float inv;
   int bad;  // a compute wave's poll of the second row failed (cleared at the start of the pass)
 };
+// Byte offset of the sampled pick's LDS copy of the value cells (V x 8 bytes, 16-byte aligned), after Lds; only the
+// sampling instantiations allocate it.
+template <int H, int I, int W, int V, bool CP>
+constexpr size_t kPickCopy = (sizeof(Lds<H, I, W, V, CP>) + 15) / 16 * 16;
+
 // Cells of the paired pass's second row, after the trace stamps of the workspace: q|k|v [8][512], attention output
 // [2048], h after o [H], activation [I], h after down [H] (the first row uses the regular regions).
 struct PairLayout {
@@ -851,9 +856,10 @@ __device__ __forceinline__ uint32_t bisect_keys(uint32_t lo, uint32_t hi, uint32
 //
 // The threshold without a histogram. Lane l holds the maxima of workgroups 2l, 2l+1, 128+2l, 129+2l; for
 // top_k <= 64 the top_k-th largest of the 64 lane maxima is a lower bound lb of the top_k-th largest value (they
-// are 64 of the values). lb is found while the first values are still in flight; as each batch of values arrives
-// the indices of those >= lb are compacted into LDS (ci; the values go to cv by index): a per-lane count, a scan
-// over the lanes, then every lane writes its own run (non-candidates to a trash slot, so no branch). A bisection
+// are 64 of the values). lb is found while the values are still in flight: all V cells are loaded straight into LDS
+// (cb, a copy of the cells) before the maxima are polled. Then the indices of the values >= lb are compacted into
+// LDS (ci), batch by batch: a per-lane count, a scan over the lanes, then every lane writes its own run
+// (non-candidates to a trash slot, so no branch). A bisection
 // of the keys then counts, per key t, the candidates >= t; below lb every count is at least top_k, as it is over
 // all values, so it ends on the same key. The kept candidates are compacted once more so each lane draws the
 // Philox noise of at most one of them when at most 64 are kept. Counts are ballots of one comparison each, with
@@ -863,8 +869,7 @@ __device__ __forceinline__ uint32_t bisect_keys(uint32_t lo, uint32_t hi, uint32
 // scalar. `tp` (null unless tracing) receives wall-clock stamps (tp[10..14]) and shader-clock stamps (tp[0..4])
 // after the bound, the gather with the compaction, the bisection, the kept compaction and the draw, and lb and
 // the counts of candidates and kept values (tp[5..7]).
-// Cell pairs per lane and batch of sampled_pick's value gather (two batches in flight). A translation unit may
-// specialise it before instantiating the kernel, for a smaller register footprint.
+// Cell pairs per lane and batch of sampled_pick's candidate compaction (one scan over the lanes per batch).
 template <int V, int ROWS>
 struct PickBatch {
   static constexpr int value = 8;
@@ -872,20 +877,24 @@ struct PickBatch {
 
 template <int V, int ROWS>
 __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t vals_, uint32_t maxs_, int g_,
-                                                          uint32_t e_, const float* hv_, float* cv_, uint32_t* ci_,
+                                                          uint32_t e_, const float* hv_, void* cb_, uint32_t* ci_,
                                                           int top_k_, uint64_t draw_, uint64_t seed_, void* ws_,
                                                           uint32_t delay_, int lane, uint64_t* tp_) {
   constexpr int NB = V / 128;  // value cell pairs per lane: lane holds indices 2 lane + 128 b and 2 lane + 128 b + 1
-  constexpr int kBatch = PickBatch<V, ROWS>::value;  // cell pairs per lane and batch (a small register footprint)
+  constexpr int kBatch = PickBatch<V, ROWS>::value;  // cell pairs per lane and batch
   static_assert(V % 128 == 0 && V == ROWS * kWG && ROWS % 2 == 0 && ROWS <= 16, "vocabulary of 256 x ROWS");
   static_assert(NB % kBatch == 0, "batches");
   typedef __attribute__((address_space(3))) float lds_f32;
   typedef __attribute__((address_space(3))) uint16_t lds_u16;
+  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+  typedef __attribute__((address_space(3))) void lds_void;
   char* cells = uniform(cells_);
   void* ws = uniform(ws_);
   uint64_t* tp = uniform(tp_);
   const float* hv = uniform(hv_);
-  lds_f32* cv = (lds_f32*)uniform(cv_);  // LDS arrays: ds_* accesses rather than flat
+  lds_u32x4* cb = (lds_u32x4*)uniform(cb_);  // LDS arrays: ds_* accesses rather than flat
+  const lds_f32* cbf = (const lds_f32*)cb;
+  auto cv = [&](uint32_t i) { return cbf[2 * i]; };  // value i: word 0 of its cell's LDS copy
   lds_u16* ci = (lds_u16*)uniform(ci_);  // candidate indices [V], then one trash slot per lane
   const uint32_t vals = __builtin_amdgcn_readfirstlane(vals_), maxs = __builtin_amdgcn_readfirstlane(maxs_);
   const uint32_t e = __builtin_amdgcn_readfirstlane(e_);
@@ -902,12 +911,17 @@ __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t
   if (lane < ROWS / 2) put2(cells, vals + (uint32_t)(ROWS * g + 2 * lane), hv[2 * lane], hv[2 * lane + 1], e);
   if (lane == 0) put(cells, maxs + (uint32_t)g, __uint_as_float(own_max), e);
   sleep_units(delay);
-  u32x4 qa[kBatch], qb[kBatch];  // double buffer: the next batch is in flight while one is waited for and processed
-  auto load_batch = [&](u32x4 (&q)[kBatch], int b0) {
+  // Every value cell at once, straight into LDS: cb mirrors cells [vals, vals + V) (cell i at byte 8 i). The direct
+  // loads hold no registers, so the whole vocabulary is one memory round trip (register batches of 4 or 8 cell
+  // pairs per lane, two in flight, took one round trip per batch pair); they go out before the maxima are polled.
+  auto gather = [&]() {
 #pragma unroll
-    for (int b = 0; b < kBatch; b++) q[b] = get2(cells, vals + (uint32_t)(2 * lane + 128 * (b0 + b)));
+    for (int b = 0; b < NB; b++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(cells), (lds_void*)(cb + 64 * b), 16, (uint32_t)lane * 16u,
+                                               __builtin_amdgcn_readfirstlane((vals + 128u * (uint32_t)b) * 8u), 0,
+                                               kPolDev);
   };
-  load_batch(qa, 0);  // in flight while the maxima are polled and the bound is found
+  gather();
   // the 256 maxima: lane l holds workgroups 2l, 2l+1, 128+2l, 129+2l
   u32x4 mq[2];
   for (uint32_t spin = 0;; spin++) {
@@ -930,35 +944,35 @@ __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t
     lb = bisect_keys(lmin, top_key, K, [&](uint32_t t) { return (uint32_t)__popcll(__ballot(lm >= t)); });
   }
   if (tp && lane == 0) { tp[10] = (uint64_t)wall_clock64(); tp[0] = (uint64_t)clock64(); }
-  // the values, batch by batch: staged into cv by index, the indices of those >= lb appended to ci
+  // the values' epochs, checked in LDS (lane holds cells 2 lane + 128 b, + 1); a stale cell re-fetches them all
+  for (uint32_t spin = 0;; spin++) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads have landed in LDS
+    bool ok = true;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      const u32x4 q = cb[64 * b + lane];
+      ok &= q.y == e && q.w == e;
+    }
+    if (__all(ok)) break;
+    if ((spin & 63) == 63) {
+      if (ld_u32_dev(ws, Ws::kErr) != 0) return -1;
+      if (spin > kSpinLimit) return -2;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    gather();
+  }
+  // the indices of the values >= lb, appended to ci batch by batch (a scan over the lanes per batch)
   uint32_t n = 0;
   const uint32_t trash = (uint32_t)(V + lane);
 #pragma unroll
   for (int b0 = 0; b0 < NB; b0 += kBatch) {
-    u32x4 (&q)[kBatch] = (b0 / kBatch) % 2 ? qb : qa;
-    // the next batch goes out before this one is waited for: two batches in flight
-    if (b0 + kBatch < NB) load_batch((b0 / kBatch) % 2 ? qa : qb, b0 + kBatch);
-    for (uint32_t spin = 0;; spin++) {
-      bool ok = true;
-#pragma unroll
-      for (int b = 0; b < kBatch; b++) ok &= q[b].y == e && q[b].w == e;
-      if (__all(ok)) break;
-      if ((spin & 63) == 63) {
-        if (ld_u32_dev(ws, Ws::kErr) != 0) return -1;
-        if (spin > kSpinLimit) return -2;
-      }
-      __builtin_amdgcn_s_sleep(1);
-      load_batch(q, b0);
-    }
     bool tk[2 * kBatch];
     uint32_t cnt = 0;
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
-      const int i = 2 * lane + 128 * (b0 + b);
-      cv[i] = __uint_as_float(q[b].x);
-      cv[i + 1] = __uint_as_float(q[b].z);
-      tk[2 * b] = order_key(__uint_as_float(q[b].x)) >= lb;
-      tk[2 * b + 1] = order_key(__uint_as_float(q[b].z)) >= lb;
+      const u32x4 q = cb[64 * (b0 + b) + lane];
+      tk[2 * b] = order_key(__uint_as_float(q.x)) >= lb;
+      tk[2 * b + 1] = order_key(__uint_as_float(q.z)) >= lb;
       cnt += (uint32_t)tk[2 * b] + (uint32_t)tk[2 * b + 1];
     }
     const uint32_t incl = wave_incl_scan_u32(cnt);
@@ -982,7 +996,7 @@ __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t
 #pragma unroll
     for (int m = 0; m < kReg; m++) {
       const uint32_t j = (uint32_t)(lane + 64 * m);
-      kk[m] = j < n ? order_key(cv[ci[j]]) : 0u;  // 0 never counts: every probed key t is at least 1
+      kk[m] = j < n ? order_key(cv(ci[j])) : 0u;  // 0 never counts: every probed key t is at least 1
     }
     if (nm <= 1) {
       thr = bisect_keys(lb, top_key, K, [&](uint32_t t) { return (uint32_t)__popcll(__ballot(kk[0] >= t)); });
@@ -1002,7 +1016,7 @@ __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t
         for (int m = 0; m < kReg; m++) c += (uint32_t)__popcll(__ballot(kk[m] >= t));
         for (int m = kReg; m < nm; m++) {
           const uint32_t j = (uint32_t)(lane + 64 * m);
-          c += (uint32_t)__popcll(__ballot(j < n && order_key(cv[ci[j]]) >= t));
+          c += (uint32_t)__popcll(__ballot(j < n && order_key(cv(ci[j])) >= t));
         }
         return c;
       });
@@ -1018,7 +1032,7 @@ __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t
     bool take = false;
     if (j < n) {
       i = ci[j];
-      const float x = cv[i];
+      const float x = cv(i);
       take = order_key(x) >= thr && x != -INFINITY;
     }
     const uint64_t msk = __ballot(take);
@@ -1031,7 +1045,7 @@ __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t
   int bi = 0x7fffffff;
   for (uint32_t j = (uint32_t)lane; j < nk; j += 64) {
     const int i = (int)ci[j];
-    const float gv = gumbel(cv[i], (uint32_t)i, draw, k0, k1);
+    const float gv = gumbel(cv(i), (uint32_t)i, draw, k0, k1);
     if (gv > best || (gv == best && i < bi)) { best = gv; bi = i; }
   }
   const float gmax = wave_max(best);
@@ -1520,10 +1534,11 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     wg_sync();  // candidates (greedy) or processed logits (sampled) of the compute waves are in S.cand / S.hv
     if (SMP && lane == 0) c.tr(0, f, c.L, 9);
     if constexpr (SMP) {
-      // every workgroup publishes its processed logits and every control wave draws the same pick from all of them
-      // S.xs[0] and S.xs[1] are free here: the head dot has consumed its input and the compute waves wait
-      const int64_t t = sampled_pick<V, V / kWG>(c.cells, LY.e8, LY.e7, c.g, c.tick(f, c.L, 1), S.hv, S.xs[1],
-                                                 (uint32_t*)S.xs[0], c.d.top_k, c.cnt0 + (uint64_t)(CP ? f - 1 : f),
+      // every workgroup publishes its processed logits and every control wave draws the same pick from all of them;
+      // S.xs[0] is free here (the head dot has consumed its input and the compute waves wait): the candidates
+      const int64_t t = sampled_pick<V, V / kWG>(c.cells, LY.e8, LY.e7, c.g, c.tick(f, c.L, 1), S.hv,
+                                                 (char*)&S + kPickCopy<H, I, W, V, CP>, (uint32_t*)S.xs[0],
+                                                 c.d.top_k, c.cnt0 + (uint64_t)(CP ? f - 1 : f),
                                                  c.seed, c.ws, c.dl[Ws::kHopPick], lane, c.tslot(0, f, c.L, 0));
       ok = t >= 0;
       if (ok) tok = t;
@@ -2417,7 +2432,8 @@ int prepare_kernel(size_t lds) {
 }
 template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK = false, bool F16 = false>
 int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
-  constexpr size_t need = sizeof(Lds<H, I, W, V, CP>) + (PAIRK ? sizeof(LdsPair<H, I>) : 0);
+  constexpr size_t need = SMP ? kPickCopy<H, I, W, V, CP> + (size_t)V * 8
+                              : sizeof(Lds<H, I, W, V, CP>) + (PAIRK ? sizeof(LdsPair<H, I>) : 0);
   const size_t lds = need < 96 * 1024 ? 96 * 1024 : need;  // one workgroup per CU
   const int rc = prepare_kernel<H, I, W, V, CP, SMP, WD, KEEP, PAIRK, F16>(lds);
   if (rc != SK_OK) return rc;
