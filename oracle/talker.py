@@ -445,9 +445,11 @@ class CodePredictorOracle:
         self.n = n_positions
         self.cache_bf16 = cache_bf16
 
-    def frame(self, x0: np.ndarray, id0: int, layer_out: list | None = None):
+    def frame(self, x0: np.ndarray, id0: int, layer_out: list | None = None, sample: tuple | None = None):
         """Returns (codes [n], logits of positions 1..n-1); ``layer_out`` receives the residual after every layer
-        at the last position."""
+        at the last position. ``sample`` = (temperature, top_k, key, counter) replaces the greedy pick of position
+        g >= 1 by the fused sampler's draw ``sample_draw`` with counter ``counter + g - 1`` (the sub-code draws of
+        ``subtalker_dosample``, qwen3/kernels.py:671-674, one draw counter for the frame)."""
         w = self.w
         nl = len(w["layers"])
         K = np.zeros((nl, w["nkv"], self.n, HD), F32)
@@ -470,7 +472,11 @@ class CodePredictorOracle:
             if g == 0:
                 continue
             lg = rms_gemv(h, w["norm"], w["eps"], w["heads"][g - 1])
-            codes.append(argmax_first(lg))
+            if sample is None:
+                codes.append(argmax_first(lg))
+            else:
+                temp, top_k, key, cnt = sample
+                codes.append(sample_draw(lg, float(np.float32(1.0 / temp)), top_k, key, cnt + g - 1)[0])
             logits.append(lg)
         return codes, logits
 

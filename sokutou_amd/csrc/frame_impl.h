@@ -847,56 +847,96 @@ __device__ __forceinline__ uint32_t bisect_keys(uint32_t lo, uint32_t hi, uint32
   return p;
 }
 
-// Publishes this workgroup's ROWS processed logits (cells vals + ROWS g ..) and their largest order key (cell
-// maxs + g), waits until all V values and the 256 maxima carry epoch e, then draws as the fused sampler does: the
-// key of the top_k-th largest value (ties kept; top_k <= 0 or >= V keeps everything), then the largest
-// v - log(-log u) over the kept values that are not -inf, u from Philox draw `draw` under key `seed`, lowest index
-// on ties, 0 if nothing is kept. Every workgroup computes the same pick from the same V values. Returns the pick,
-// -1 when the error word is set, -2 on timeout.
-//
-// The threshold without a histogram. Lane l holds the maxima of workgroups 2l, 2l+1, 128+2l, 129+2l; for
-// top_k <= 64 the top_k-th largest of the 64 lane maxima is a lower bound lb of the top_k-th largest value (they
-// are 64 of the values). lb is found while the values are still in flight: all V cells are loaded straight into LDS
-// (cb, a copy of the cells) before the maxima are polled. Then the indices of the values >= lb are compacted into
-// LDS (ci), batch by batch: a per-lane count, a scan over the lanes, then every lane writes its own run
-// (non-candidates to a trash slot, so no branch). A bisection
-// of the keys then counts, per key t, the candidates >= t; below lb every count is at least top_k, as it is over
-// all values, so it ends on the same key. The kept candidates are compacted once more so each lane draws the
-// Philox noise of at most one of them when at most 64 are kept. Counts are ballots of one comparison each, with
-// the number of comparisons per step fixed outside the bisection (a branch per step costs more than the ballot).
-// Kept out of line (one call per frame) and only in the sampling instantiation of the kernel. The arguments
-// arrive in vector registers under the call convention; they are made wave-uniform first so the control flow stays
-// scalar. `tp` (null unless tracing) receives wall-clock stamps (tp[10..14]) and shader-clock stamps (tp[0..4])
-// after the bound, the gather with the compaction, the bisection, the kept compaction and the draw, and lb and
-// the counts of candidates and kept values (tp[5..7]).
-// Cell pairs per lane and batch of sampled_pick's candidate compaction (one scan over the lanes per batch).
-template <int V, int ROWS>
-struct PickBatch {
-  static constexpr int value = 8;
+// LDS that a sampled pick's control wave and compute waves share, after the LDS copy of the value cells (sampling
+// instantiations only).
+struct PickShared {
+  uint32_t lm[64];  // the control wave's 64 lane maxima, for the bound's ranks
+  uint32_t lb;      // lower bound of the threshold key
+  uint32_t n;       // candidates compacted (LDS atomic; zeroed by the control wave before the compaction)
+  uint32_t bad;     // nonzero: a poll failed and there is no pick (zeroed at launch and after each pick)
+  uint32_t pad;
+  float gv[4];      // per compute wave: the largest perturbed value among its kept candidates (-inf: none)
+  uint32_t bi[4];   // the lowest index holding it (0x7fffffff: none)
+  uint32_t nk[4];   // kept candidates per compute wave
 };
+static_assert(offsetof(PickShared, gv) % 16 == 0 && offsetof(PickShared, bi) == offsetof(PickShared, gv) + 16 &&
+                  offsetof(PickShared, nk) == offsetof(PickShared, gv) + 32,
+              "the combine reads gv, bi and nk as three 16-byte vectors");
+template <int H, int I, int W, int V, bool CP>
+constexpr size_t kPickShared = kPickCopy<H, I, W, V, CP> + (size_t)V * 8;
+constexpr uint32_t kNegInfKey = 0x007fffffu;  // order_key(-inf)
+// The value whose order key is k (order_key is a bijection).
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? k ^ 0x80000000u : ~k);
+}
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) PickShared lds_pick;
+// The LDS address of p (a pointer into the workgroup's LDS) as a value the compiler cannot trace back to the
+// kernel's dynamic LDS array: an out-of-line function handed an address derived from that array looks the array's
+// base up in a per-kernel table in memory, again after every LDS store it cannot rule out as aliasing.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  uint32_t a = (uint32_t)(size_t)(const __attribute__((address_space(3))) char*)p;
+  __asm__ volatile("" : "+s"(a));
+  return a;
+}
+template <class T>
+__device__ __forceinline__ T* lds_at(uint32_t a) {  // an LDS pointer from an lds_addr value
+  return (T*)(size_t)__builtin_amdgcn_readfirstlane(a);
+}
 
+// A sampled pick draws as the fused sampler does: the key of the top_k-th largest of the V processed logits (ties
+// kept; top_k <= 0 or >= V keeps everything), then the largest v - log(-log u) over the kept values that are not
+// -inf, u from Philox draw `draw` under key `seed`, lowest index on ties, 0 if nothing is kept. Every workgroup
+// publishes its ROWS values (cells vals + ROWS g ..) and their largest order key (cell maxs + g), and every
+// workgroup computes the same pick from all of them, the control wave and the compute waves together:
+//
+//  1. control wave: publish, poll the 256 maxima (lane l holds workgroups 2l, 2l+1, 128+2l, 129+2l) and, for
+//     top_k <= 64, take the top_k-th largest of the 64 lane maxima as a lower bound lb of the threshold (they are
+//     64 of the values): the largest lane maximum that at least top_k lane maxima reach, one rank per lane.
+//     Compute waves, meanwhile: each loads a quarter of the V value cells straight into LDS (cb, a copy of the
+//     cells; direct loads hold no registers) and re-loads it until every epoch is the frame's.
+//  2. compute waves: the indices and keys of their values >= lb are appended to ci / ck (a scan over the lanes,
+//     one LDS atomic per wave for the wave's place; the order does not matter below).
+//  3. compute waves, when 0 < top_k <= 64 and at most 256 candidates: candidate j (lane j % 64 of wave j / 64) is
+//     kept iff fewer than top_k candidates have a larger key (every key above lb is a candidate, so this is the
+//     rank among all V values, and key >= threshold); kept candidates draw their Philox noise and each wave
+//     reduces its largest perturbed value and lowest index. The control wave combines the four.
+//     Otherwise the control wave finds the threshold by bisection of the keys over the candidates (ballot
+//     counts), compacts the kept ones and draws alone (keep-all, top_k > 64, or a bound that leaves more than
+//     256 candidates, as when many values tie).
+// Three workgroup barriers separate the steps; both roles pass all three whatever happens, and a failed poll
+// only sets `bad`. A single wave pays about 90 cycles for each comparison that feeds a ballot and issues one
+// instruction every few cycles, so the steps that scale with the candidates run on the four compute waves
+// (4 x 64 lanes) and the control wave keeps the parts that do not.
+
+// Control wave. Kept out of line (one call per frame) and only in the sampling instantiation of the kernel. The
+// arguments arrive in vector registers under the call convention; they are made wave-uniform first so the control
+// flow stays scalar. Returns the pick, -1 when the error word is set or a compute wave's poll failed, -2 when the
+// maxima poll timed out. `tp` (null unless tracing) receives wall-clock stamps (tp[10..14]) and shader-clock stamps
+// (tp[0..4]) after the bound, the compaction, the ranks and draws, the fallback's kept compaction and the pick, and
+// lb and the counts of candidates and kept values (tp[5..7]).
 template <int V, int ROWS>
 __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t vals_, uint32_t maxs_, int g_,
-                                                          uint32_t e_, const float* hv_, void* cb_, uint32_t* ci_,
-                                                          int top_k_, uint64_t draw_, uint64_t seed_, void* ws_,
-                                                          uint32_t delay_, int lane, uint64_t* tp_) {
-  constexpr int NB = V / 128;  // value cell pairs per lane: lane holds indices 2 lane + 128 b and 2 lane + 128 b + 1
-  constexpr int kBatch = PickBatch<V, ROWS>::value;  // cell pairs per lane and batch
-  static_assert(V % 128 == 0 && V == ROWS * kWG && ROWS % 2 == 0 && ROWS <= 16, "vocabulary of 256 x ROWS");
-  static_assert(NB % kBatch == 0, "batches");
-  typedef __attribute__((address_space(3))) float lds_f32;
-  typedef __attribute__((address_space(3))) uint16_t lds_u16;
-  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-  typedef __attribute__((address_space(3))) void lds_void;
+                                                          uint32_t e_, uint32_t hv_, uint32_t cb_, uint32_t ci_,
+                                                          uint32_t ck_, uint32_t ps_, int top_k_, uint64_t draw_,
+                                                          uint64_t seed_, void* ws_, uint32_t delay_, int lane,
+                                                          uint64_t* tp_) {
+  static_assert(V % 512 == 0 && V == ROWS * kWG && ROWS % 2 == 0 && ROWS <= 16, "vocabulary of 256 x ROWS");
   char* cells = uniform(cells_);
   void* ws = uniform(ws_);
-  uint64_t* tp = uniform(tp_);
-  const float* hv = uniform(hv_);
-  lds_u32x4* cb = (lds_u32x4*)uniform(cb_);  // LDS arrays: ds_* accesses rather than flat
-  const lds_f32* cbf = (const lds_f32*)cb;
+  gptr<uint64_t> tp = (gptr<uint64_t>)uniform(tp_);
+  const lds_f32* hv = lds_at<const lds_f32>(hv_);
+  const lds_f32* cbf = lds_at<const lds_f32>(cb_);  // LDS arrays: ds_* accesses rather than flat
   auto cv = [&](uint32_t i) { return cbf[2 * i]; };  // value i: word 0 of its cell's LDS copy
-  lds_u16* ci = (lds_u16*)uniform(ci_);  // candidate indices [V], then one trash slot per lane
-  const uint32_t vals = __builtin_amdgcn_readfirstlane(vals_), maxs = __builtin_amdgcn_readfirstlane(maxs_);
+  lds_u16* ci = lds_at<lds_u16>(ci_);                // candidate indices [V]
+  const lds_u32* ck = lds_at<const lds_u32>(ck_);    // their keys [V]
+  lds_pick* ps = lds_at<lds_pick>(ps_);
+  const uint32_t maxs = __builtin_amdgcn_readfirstlane(maxs_);
+  const uint32_t vals = __builtin_amdgcn_readfirstlane(vals_);
   const uint32_t e = __builtin_amdgcn_readfirstlane(e_);
   const int g = __builtin_amdgcn_readfirstlane(g_);
   const int top_k = __builtin_amdgcn_readfirstlane(top_k_);
@@ -904,153 +944,143 @@ __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t
   const uint32_t d0 = __builtin_amdgcn_readfirstlane((uint32_t)draw_), d1 = __builtin_amdgcn_readfirstlane((uint32_t)(draw_ >> 32));
   const uint32_t k0 = __builtin_amdgcn_readfirstlane((uint32_t)seed_), k1 = __builtin_amdgcn_readfirstlane((uint32_t)(seed_ >> 32));
   const uint64_t draw = ((uint64_t)d1 << 32) | d0;
+  const bool keep_all = top_k <= 0 || top_k >= V;
+  const uint32_t K = (uint32_t)top_k;
 
-  // publish: the values, then this workgroup's largest key
+  // (1) publish the values, then this workgroup's largest key; poll the maxima; the bound
   const float own = lane < ROWS ? hv[lane] : -INFINITY;
   const uint32_t own_max = wave_max_u32(lane < ROWS ? order_key(own) : 0u);
   if (lane < ROWS / 2) put2(cells, vals + (uint32_t)(ROWS * g + 2 * lane), hv[2 * lane], hv[2 * lane + 1], e);
   if (lane == 0) put(cells, maxs + (uint32_t)g, __uint_as_float(own_max), e);
+  if (lane == 0) ps->n = 0u;
   sleep_units(delay);
-  // Every value cell at once, straight into LDS: cb mirrors cells [vals, vals + V) (cell i at byte 8 i). The direct
-  // loads hold no registers, so the whole vocabulary is one memory round trip (register batches of 4 or 8 cell
-  // pairs per lane, two in flight, took one round trip per batch pair); they go out before the maxima are polled.
-  auto gather = [&]() {
-#pragma unroll
-    for (int b = 0; b < NB; b++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(cells), (lds_void*)(cb + 64 * b), 16, (uint32_t)lane * 16u,
-                                               __builtin_amdgcn_readfirstlane((vals + 128u * (uint32_t)b) * 8u), 0,
-                                               kPolDev);
-  };
-  gather();
-  // the 256 maxima: lane l holds workgroups 2l, 2l+1, 128+2l, 129+2l
+  int rc = 0;
   u32x4 mq[2];
   for (uint32_t spin = 0;; spin++) {
     mq[0] = get2(cells, maxs + (uint32_t)(2 * lane));
     mq[1] = get2(cells, maxs + (uint32_t)(128 + 2 * lane));
     if (__all(mq[0].y == e && mq[0].w == e && mq[1].y == e && mq[1].w == e)) break;
     if ((spin & 63) == 63) {
-      if (ld_u32_dev(ws, Ws::kErr) != 0) return -1;
-      if (spin > kSpinLimit) return -2;
+      if (ld_u32_dev(ws, Ws::kErr) != 0) { rc = -1; break; }
+      if (spin > kSpinLimit) { rc = -2; break; }
     }
     __builtin_amdgcn_s_sleep(1);
   }
   const uint32_t lm = max(max(mq[0].x, mq[0].z), max(mq[1].x, mq[1].z));  // the maxima are order keys already
   const uint32_t top_key = wave_max_u32(lm);                               // the largest key of all
-  const bool keep_all = top_k <= 0 || top_k >= V;
-  const uint32_t K = (uint32_t)top_k;
   uint32_t lb = 0;
-  if (!keep_all && top_k <= 64) {
-    const uint32_t lmin = ~wave_max_u32(~lm);  // 64 lane maxima reach the smallest of them, and 64 >= K
-    lb = bisect_keys(lmin, top_key, K, [&](uint32_t t) { return (uint32_t)__popcll(__ballot(lm >= t)); });
+  if (rc == 0 && !keep_all && top_k <= 64) {
+    ps->lm[lane] = lm;
+    const lds_u32x4* lm4 = (const lds_u32x4*)ps->lm;
+    uint32_t ge = 0;  // lane maxima >= this lane's
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+      const u32x4 m4 = lm4[q];
+      ge += (uint32_t)(m4.x >= lm) + (uint32_t)(m4.y >= lm) + (uint32_t)(m4.z >= lm) + (uint32_t)(m4.w >= lm);
+    }
+    lb = wave_max_u32(ge >= K ? lm : 0u);  // the top_k-th largest lane maximum
   }
-  if (tp && lane == 0) { tp[10] = (uint64_t)wall_clock64(); tp[0] = (uint64_t)clock64(); }
-  // the values' epochs, checked in LDS (lane holds cells 2 lane + 128 b, + 1); a stale cell re-fetches them all
-  for (uint32_t spin = 0;; spin++) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads have landed in LDS
-    bool ok = true;
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-      const u32x4 q = cb[64 * b + lane];
-      ok &= q.y == e && q.w == e;
-    }
-    if (__all(ok)) break;
-    if ((spin & 63) == 63) {
-      if (ld_u32_dev(ws, Ws::kErr) != 0) return -1;
-      if (spin > kSpinLimit) return -2;
-    }
-    __builtin_amdgcn_s_sleep(1);
-    gather();
+  if (lane == 0) {
+    ps->lb = lb;
+    if (rc != 0) __hip_atomic_fetch_or(&ps->bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  // the indices of the values >= lb, appended to ci batch by batch (a scan over the lanes per batch)
-  uint32_t n = 0;
-  const uint32_t trash = (uint32_t)(V + lane);
+  // stamps are kept in registers and stored at the end: a global store in flight would hold up the next wait
+  uint64_t st[16] = {};
+  const bool trc = tp != nullptr;
+  if (trc) { st[10] = (uint64_t)wall_clock64(); st[0] = (uint64_t)clock64(); }
+  wg_sync();  // (1) done: the values are in LDS, lb is set
+  wg_sync();  // (2) done: candidates compacted
+  const uint32_t n = __builtin_amdgcn_readfirstlane(ps->n);
+  const bool bad = __builtin_amdgcn_readfirstlane(ps->bad) != 0;
+  const bool fast = !bad && !keep_all && top_k <= 64 && n <= 256u;
+  if (trc) { st[11] = (uint64_t)wall_clock64(); st[1] = (uint64_t)clock64(); }
+  wg_sync();  // (3) done: ranks and draws of the compute waves
+  if (lane == 0) ps->bad = 0u;  // every wave has read it
+  if (bad) return rc == -2 ? -2 : -1;
+  if (trc) { st[12] = (uint64_t)wall_clock64(); st[2] = (uint64_t)clock64(); }
+  uint32_t nk = 0;
+  uint32_t pick;
+  if (fast) {
+    const lds_u32x4* r4 = (const lds_u32x4*)ps->gv;  // gv[4], bi[4], nk[4]: three 16-byte reads
+    const u32x4 gq = r4[0], bq = r4[1], nq = r4[2];
+    const float g0 = __uint_as_float(gq.x), g1 = __uint_as_float(gq.y), g2 = __uint_as_float(gq.z),
+                g3 = __uint_as_float(gq.w);
+    const float gmax = fmaxf(fmaxf(g0, g1), fmaxf(g2, g3));
+    pick = min(min(g0 == gmax ? bq.x : 0x7fffffffu, g1 == gmax ? bq.y : 0x7fffffffu),
+               min(g2 == gmax ? bq.z : 0x7fffffffu, g3 == gmax ? bq.w : 0x7fffffffu));
+    pick = __builtin_amdgcn_readfirstlane(pick);
+    nk = __builtin_amdgcn_readfirstlane((nq.x + nq.y) + (nq.z + nq.w));
+    if (trc) { st[13] = st[12]; st[3] = st[2]; }
+  } else {
+    // the threshold: a bisection of the keys over the candidates (counts are ballots of one comparison each, with
+    // the number of comparisons per step fixed outside the bisection: a branch per step costs more than a ballot)
+    const int nm = (int)((n + 63) / 64);
+    uint32_t thr = 0;
+    if (!keep_all) {
+      constexpr int kReg = 4;  // candidate keys held in registers; the rest are read from LDS
+      uint32_t kk[kReg];
 #pragma unroll
-  for (int b0 = 0; b0 < NB; b0 += kBatch) {
-    bool tk[2 * kBatch];
-    uint32_t cnt = 0;
+      for (int m = 0; m < kReg; m++) {
+        const uint32_t j = (uint32_t)(lane + 64 * m);
+        kk[m] = j < n ? ck[j] : 0u;  // 0 never counts: every probed key t is at least 1
+      }
+      if (nm <= 4) {
+        thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
+          return (uint32_t)__popcll(__ballot(kk[0] >= t)) + (uint32_t)__popcll(__ballot(kk[1] >= t)) +
+                 (uint32_t)__popcll(__ballot(kk[2] >= t)) + (uint32_t)__popcll(__ballot(kk[3] >= t));
+        });
+      } else {
+        thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
+          uint32_t c = 0;
 #pragma unroll
-    for (int b = 0; b < kBatch; b++) {
-      const u32x4 q = cb[64 * (b0 + b) + lane];
-      tk[2 * b] = order_key(__uint_as_float(q.x)) >= lb;
-      tk[2 * b + 1] = order_key(__uint_as_float(q.z)) >= lb;
-      cnt += (uint32_t)tk[2 * b] + (uint32_t)tk[2 * b + 1];
-    }
-    const uint32_t incl = wave_incl_scan_u32(cnt);
-    uint32_t at = n + incl - cnt;
-#pragma unroll
-    for (int b = 0; b < kBatch; b++) {
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        ci[tk[2 * b + h] ? at : trash] = (uint16_t)(2 * lane + 128 * (b0 + b) + h);
-        at += (uint32_t)tk[2 * b + h];
+          for (int m = 0; m < kReg; m++) c += (uint32_t)__popcll(__ballot(kk[m] >= t));
+          for (int m = kReg; m < nm; m++) {
+            const uint32_t j = (uint32_t)(lane + 64 * m);
+            c += (uint32_t)__popcll(__ballot(j < n && ck[j] >= t));
+          }
+          return c;
+        });
       }
     }
-    n += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-  }
-  const int nm = (int)((n + 63) / 64);
-  if (tp && lane == 0) { tp[11] = (uint64_t)wall_clock64(); tp[1] = (uint64_t)clock64(); }
-  uint32_t thr = 0;
-  if (!keep_all) {
-    constexpr int kReg = 4;  // candidate keys held in registers (n <= 256); the rest are read from LDS
-    uint32_t kk[kReg];
-#pragma unroll
-    for (int m = 0; m < kReg; m++) {
+    // the kept candidates (key >= thr, not -inf), compacted in place: a batch writes below its own start or over
+    // itself, after all its lanes have read their entries
+    for (int m = 0; m < nm; m++) {
       const uint32_t j = (uint32_t)(lane + 64 * m);
-      kk[m] = j < n ? order_key(cv(ci[j])) : 0u;  // 0 never counts: every probed key t is at least 1
+      uint32_t i = 0;
+      bool take = false;
+      if (j < n) {
+        i = ci[j];
+        const float x = cv(i);
+        take = order_key(x) >= thr && x != -INFINITY;
+      }
+      const uint64_t msk = __ballot(take);
+      if (take) ci[nk + __builtin_amdgcn_mbcnt_hi((uint32_t)(msk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)msk, 0u))] = (uint16_t)i;
+      nk += (uint32_t)__popcll(msk);
     }
-    if (nm <= 1) {
-      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) { return (uint32_t)__popcll(__ballot(kk[0] >= t)); });
-    } else if (nm <= 2) {
-      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
-        return (uint32_t)__popcll(__ballot(kk[0] >= t)) + (uint32_t)__popcll(__ballot(kk[1] >= t));
-      });
-    } else if (nm <= 4) {
-      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
-        return (uint32_t)__popcll(__ballot(kk[0] >= t)) + (uint32_t)__popcll(__ballot(kk[1] >= t)) +
-               (uint32_t)__popcll(__ballot(kk[2] >= t)) + (uint32_t)__popcll(__ballot(kk[3] >= t));
-      });
-    } else {
-      thr = bisect_keys(lb, top_key, K, [&](uint32_t t) {
-        uint32_t c = 0;
+    if (trc) { st[13] = (uint64_t)wall_clock64(); st[3] = (uint64_t)clock64(); }
+    // Gumbel-max: the largest perturbed value, then the lowest index among the lanes that hold it
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (uint32_t j = (uint32_t)lane; j < nk; j += 64) {
+      const int i = (int)ci[j];
+      const float gv = gumbel(cv(i), (uint32_t)i, draw, k0, k1);
+      if (gv > best || (gv == best && i < bi)) { best = gv; bi = i; }
+    }
+    const float gmax = wave_max(best);
+    pick = ~wave_max_u32(best == gmax ? ~(uint32_t)bi : 0u);
+  }
+  if (trc) {
+    st[14] = (uint64_t)wall_clock64();
+    st[4] = (uint64_t)clock64();
+    st[5] = lb;
+    st[6] = n;
+    st[7] = nk;
+    if (lane == 0) {
 #pragma unroll
-        for (int m = 0; m < kReg; m++) c += (uint32_t)__popcll(__ballot(kk[m] >= t));
-        for (int m = kReg; m < nm; m++) {
-          const uint32_t j = (uint32_t)(lane + 64 * m);
-          c += (uint32_t)__popcll(__ballot(j < n && order_key(cv(ci[j])) >= t));
-        }
-        return c;
-      });
+      for (int k = 0; k < 15; k++)
+        if (k != 8 && k != 9) tp[k] = st[k];
     }
   }
-  if (tp && lane == 0) { tp[12] = (uint64_t)wall_clock64(); tp[2] = (uint64_t)clock64(); }
-  // the kept candidates (key >= thr, not -inf), compacted in place: a batch writes below its own start or over
-  // itself, after all its lanes have read their entries
-  uint32_t nk = 0;
-  for (int m = 0; m < nm; m++) {
-    const uint32_t j = (uint32_t)(lane + 64 * m);
-    uint32_t i = 0;
-    bool take = false;
-    if (j < n) {
-      i = ci[j];
-      const float x = cv(i);
-      take = order_key(x) >= thr && x != -INFINITY;
-    }
-    const uint64_t msk = __ballot(take);
-    if (take) ci[nk + __builtin_amdgcn_mbcnt_hi((uint32_t)(msk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)msk, 0u))] = (uint16_t)i;
-    nk += (uint32_t)__popcll(msk);
-  }
-  if (tp && lane == 0) { tp[13] = (uint64_t)wall_clock64(); tp[3] = (uint64_t)clock64(); tp[5] = lb; tp[6] = n; tp[7] = nk; }
-  // Gumbel-max: the largest perturbed value, then the lowest index among the lanes that hold it
-  float best = -INFINITY;
-  int bi = 0x7fffffff;
-  for (uint32_t j = (uint32_t)lane; j < nk; j += 64) {
-    const int i = (int)ci[j];
-    const float gv = gumbel(cv(i), (uint32_t)i, draw, k0, k1);
-    if (gv > best || (gv == best && i < bi)) { best = gv; bi = i; }
-  }
-  const float gmax = wave_max(best);
-  const uint32_t pick = ~wave_max_u32(best == gmax ? ~(uint32_t)bi : 0u);
-  if (tp && lane == 0) { tp[14] = (uint64_t)wall_clock64(); tp[4] = (uint64_t)clock64(); }
   return pick == 0x7fffffffu || nk == 0 ? 0 : (int64_t)pick;
 }
 
@@ -1222,6 +1252,157 @@ __device__ void fail(const Ctx& c, uint32_t code, int f, int l) {
   st_u32_dev(c.ws, Ws::kDiag + 12, (uint32_t)c.g);
   __builtin_amdgcn_s_waitcnt(0);
   st_u32_dev(c.ws, Ws::kErr, code);
+}
+
+// Compute wave cw's part of a sampled pick (steps 1-3 above), between the barrier that hands the control wave the
+// processed logits and the one that ends the pick; it passes the same three barriers as the control wave. Out of
+// line for the same reason as the control wave's part: inlined, its registers pushed the compute waves' layer loop
+// into spills (38 against 1 spilled VGPRs on the 0.6B talker).
+template <int V, int W>
+__device__ __attribute__((noinline)) void pick_compute(uint32_t cb_, uint32_t ci_, uint32_t ck_, uint32_t ps_, char* cells_,
+                                                       void* ws_, uint32_t vals_, uint32_t e_, uint64_t draw_,
+                                                       uint64_t seed_, int top_k_, uint32_t delay_, int f_, int L_,
+                                                       int g_, int cw_, int lane, uint64_t* tp_) {
+  constexpr int NB = V / 128;  // value cell pairs per lane over the whole vocabulary
+  constexpr int NQ = NB / W;   // this wave's: pairs NQ cw .. NQ cw + NQ - 1, cells 2 lane + 128 b, + 1
+  static_assert(W == 4 && NB % W == 0, "a quarter of the values per compute wave");
+  lds_u32x4* cb = lds_at<lds_u32x4>(cb_);
+  lds_u16* ci = lds_at<lds_u16>(ci_);
+  lds_u32* ck = lds_at<lds_u32>(ck_);
+  lds_pick* ps = lds_at<lds_pick>(ps_);
+  char* cells = uniform(cells_);
+  void* ws = uniform(ws_);
+  const uint32_t vals = __builtin_amdgcn_readfirstlane(vals_), e = __builtin_amdgcn_readfirstlane(e_);
+  const uint32_t d0 = __builtin_amdgcn_readfirstlane((uint32_t)draw_), d1 = __builtin_amdgcn_readfirstlane((uint32_t)(draw_ >> 32));
+  const uint32_t k0 = __builtin_amdgcn_readfirstlane((uint32_t)seed_), k1 = __builtin_amdgcn_readfirstlane((uint32_t)(seed_ >> 32));
+  const uint64_t draw = ((uint64_t)d1 << 32) | d0;
+  const int top_k = __builtin_amdgcn_readfirstlane(top_k_);
+  const uint32_t delay = __builtin_amdgcn_readfirstlane(delay_);
+  const int f = __builtin_amdgcn_readfirstlane(f_), L = __builtin_amdgcn_readfirstlane(L_);
+  const int g = __builtin_amdgcn_readfirstlane(g_), cw = __builtin_amdgcn_readfirstlane(cw_);
+  gptr<uint64_t> tp = (gptr<uint64_t>)uniform(tp_);  // wave 0's wall-clock stamps when tracing (tp[0..7]), else null
+  const int b0 = NQ * cw;
+  auto gather = [&]() {
+#pragma unroll
+    for (int b = 0; b < NQ; b++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(cells), (lds_void*)(cb + 64 * (b0 + b)), 16,
+                                               (uint32_t)lane * 16u,
+                                               __builtin_amdgcn_readfirstlane((vals + 128u * (uint32_t)(b0 + b)) * 8u),
+                                               0, kPolDev);
+  };
+  sleep_units(delay);
+  gather();
+  uint64_t st[8] = {};  // stamps, stored at the end (a global store in flight would hold up the next wait)
+  const bool trc = tp != nullptr;
+  if (trc) st[0] = (uint64_t)wall_clock64();
+  bool good = false;
+  uint32_t spins = 0;
+  for (uint32_t spin = 0;; spin++) {
+    spins = spin;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads have landed in LDS
+    bool ok = true;
+#pragma unroll
+    for (int b = 0; b < NQ; b++) {
+      const u32x4 q = cb[64 * (b0 + b) + lane];
+      ok &= q.y == e && q.w == e;
+    }
+    if (__all(ok)) { good = true; break; }
+    if ((spin & 63) == 63) {
+      if (ld_u32_dev(ws, Ws::kErr) != 0) break;
+      if (spin > kSpinLimit) {  // the error word and the diagnostic words, as fail() writes them
+        if (lane == 0) {
+          st_u32_dev(ws, Ws::kDiag, 20u);
+          st_u32_dev(ws, Ws::kDiag + 4, (uint32_t)f);
+          st_u32_dev(ws, Ws::kDiag + 8, (uint32_t)L);
+          st_u32_dev(ws, Ws::kDiag + 12, (uint32_t)g);
+          __builtin_amdgcn_s_waitcnt(0);
+          st_u32_dev(ws, Ws::kErr, 20u);
+        }
+        break;
+      }
+    }
+    __builtin_amdgcn_s_sleep(1);
+    gather();
+  }
+  if (!good && lane == 0) __hip_atomic_fetch_or(&ps->bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (trc) { st[1] = (uint64_t)wall_clock64(); st[2] = spins; }
+  wg_sync();  // (1)
+  if (trc) st[3] = (uint64_t)wall_clock64();
+  const bool bad = __builtin_amdgcn_readfirstlane(ps->bad) != 0;
+  if (!bad) {
+    const uint32_t lb = __builtin_amdgcn_readfirstlane(ps->lb);
+    uint32_t key[2 * NQ];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int b = 0; b < NQ; b++) {
+      const u32x4 q = cb[64 * (b0 + b) + lane];
+      key[2 * b] = order_key(__uint_as_float(q.x));
+      key[2 * b + 1] = order_key(__uint_as_float(q.z));
+      cnt += (uint32_t)(key[2 * b] >= lb) + (uint32_t)(key[2 * b + 1] >= lb);
+    }
+    const uint32_t incl = wave_incl_scan_u32(cnt);
+    uint32_t base = 0;
+    if (lane == 63) base = __hip_atomic_fetch_add(&ps->n, incl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    uint32_t at = (uint32_t)__builtin_amdgcn_readlane((int)base, 63) + incl - cnt;
+#pragma unroll
+    for (int b = 0; b < NQ; b++) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        if (key[2 * b + h] >= lb) {
+          ci[at] = (uint16_t)(2 * lane + 128 * (b0 + b) + h);
+          ck[at] = key[2 * b + h];
+          at++;
+        }
+      }
+    }
+  }
+  if (trc) st[4] = (uint64_t)wall_clock64();
+  wg_sync();  // (2)
+  const uint32_t n = __builtin_amdgcn_readfirstlane(ps->n);
+  if (trc) st[5] = (uint64_t)wall_clock64();
+  if (!bad && top_k > 0 && top_k <= 64 && top_k < V && n <= 256u) {
+    // G lanes per candidate (consecutive lanes of a quad), each counting the larger keys in every G-th group of
+    // four; a lane that holds no candidate counts nothing
+    const uint32_t sh = n <= 64u ? 2u : n <= 128u ? 1u : 0u, G = 1u << sh;
+    const uint32_t t = (uint32_t)(64 * cw + lane), j = t >> sh, part = t & (G - 1u);
+    const bool has = j < n;
+    const uint32_t key = has ? ck[j] : 0xffffffffu;
+    const lds_u32x4* ck4 = (const lds_u32x4*)ck;
+    const bool wv = ((uint32_t)(64 * cw) >> sh) < n;  // this wave holds candidates
+    const uint32_t nf = wv ? n / 4 : 0u;                // full groups of four
+    uint32_t gt = 0;
+    const uint32_t nit = (nf + G - 1u) >> sh;  // a trip count common to the wave, so the reads overlap
+#pragma unroll 4
+    for (uint32_t it = 0; it < nit; it++) {
+      const uint32_t q = (it << sh) + part;
+      const u32x4 k4 = ck4[q < nf ? q : 0u];
+      const uint32_t c4 = (uint32_t)(k4.x > key) + (uint32_t)(k4.y > key) + (uint32_t)(k4.z > key) + (uint32_t)(k4.w > key);
+      gt += q < nf ? c4 : 0u;
+    }
+    if (wv && part == 0)
+      for (uint32_t i = n & ~3u; i < n; i++) gt += (uint32_t)(ck[i] > key);
+    if (sh >= 1) gt += dppu<0xB1>(gt);  // quad_perm [1,0,3,2]: the pair's sum
+    if (sh >= 2) gt += dppu<0x4E>(gt);  // quad_perm [2,3,0,1]: the quad's
+    if (trc) st[6] = (uint64_t)wall_clock64();
+    const bool kept = has && part == 0 && gt < (uint32_t)top_k && key != kNegInfKey;  // key >= threshold, not -inf
+    float best = -INFINITY;
+    uint32_t bi = 0x7fffffffu;
+    if (kept) {
+      const uint32_t i = ci[j];
+      const float gv = gumbel(key_value(key), i, draw, k0, k1);
+      if (gv == gv) { best = gv; bi = i; }  // a NaN never wins
+    }
+    const float gmax = wave_max(best);
+    const uint32_t pick = ~wave_max_u32(best == gmax ? ~bi : 0u);
+    const uint32_t nk = (uint32_t)__popcll(__ballot(kept));
+    if (lane == 0) { ps->gv[cw] = gmax; ps->bi[cw] = pick; ps->nk[cw] = nk; }
+    if (trc) st[7] = (uint64_t)wall_clock64();
+  }
+  wg_sync();  // (3)
+  if (trc && lane == 0) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) tp[k] = st[k];
+  }
 }
 
 // Barriers of the attention stage after its input has arrived (both roles execute the same count): one after
@@ -1534,10 +1715,14 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
     wg_sync();  // candidates (greedy) or processed logits (sampled) of the compute waves are in S.cand / S.hv
     if (SMP && lane == 0) c.tr(0, f, c.L, 9);
     if constexpr (SMP) {
-      // every workgroup publishes its processed logits and every control wave draws the same pick from all of them;
-      // S.xs[0] is free here (the head dot has consumed its input and the compute waves wait): the candidates
-      const int64_t t = sampled_pick<V, V / kWG>(c.cells, LY.e8, LY.e7, c.g, c.tick(f, c.L, 1), S.hv,
-                                                 (char*)&S + kPickCopy<H, I, W, V, CP>, (uint32_t*)S.xs[0],
+      // every workgroup publishes its processed logits and draws the same pick from all of them, the control wave
+      // with the compute waves (pick_compute)
+      // S.xs[0] and S.xs[1] are free here (the head dot has consumed its input and the next frame's inputs
+      // are staged after the pick): candidate indices and keys
+      static_assert(V <= Lds<H, I, W, V, CP>::XS, "candidate keys fit a staging buffer");
+      const int64_t t = sampled_pick<V, V / kWG>(c.cells, LY.e8, LY.e7, c.g, c.tick(f, c.L, 1), lds_addr(S.hv),
+                                                 lds_addr((char*)&S + kPickCopy<H, I, W, V, CP>), lds_addr(S.xs[0]),
+                                                 lds_addr(S.xs[1]), lds_addr((char*)&S + kPickShared<H, I, W, V, CP>),
                                                  c.d.top_k, c.cnt0 + (uint64_t)(CP ? f - 1 : f),
                                                  c.seed, c.ws, c.dl[Ws::kHopPick], lane, c.tslot(0, f, c.L, 0));
       ok = t >= 0;
@@ -2260,11 +2445,15 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
       const float inv = S.inv;
       const bool block_eos = block_eos0 && (ngen0 + f) < c.d.min_new;
       uint64_t best = 0;
+      // Sampling kernels: the rows' values (seen-byte masks and offsets) are recomputed each frame; hoisted out of
+      // the frame loop they stayed live across it and spilled, and their reloads sat in this serial lane-0 loop
+      int hr0 = h_w0;
+      if constexpr (SMP) __asm__ volatile("" : "+v"(hr0));
       if (lane == 0) {
 #pragma unroll
         for (int i = 0; i < C::RW_HEAD; i++) {
           if (i >= h_wn) break;
-          const int row = h_w0 + i;
+          const int row = hr0 + i;
           float v = y[i] * row_scale_of<WD>(sh[i]) * inv;
           if (c.d.logits && f == c.n_frames - 1) gstore(c.d.logits + row, v);
           if (c.d.talker_processor) {
@@ -2281,6 +2470,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
     }
     load_proj();  // the next position's projection row, in flight during the pick (the head's registers are free)
     wg_sync();  // candidates ready for the control wave
+    if constexpr (SMP)
+      pick_compute<V, W>(lds_addr((char*)&S + kPickCopy<H, I, W, V, CP>), lds_addr(S.xs[0]), lds_addr(S.xs[1]),
+                         lds_addr((char*)&S + kPickShared<H, I, W, V, CP>), c.cells, c.ws, LY.e8, c.tick(f, c.L, 1),
+                         c.cnt0 + (uint64_t)(CP ? f - 1 : f), c.seed, c.d.top_k, c.dl[Ws::kHopPick], f, c.L, c.g,
+                         cw, lane, cw == 0 ? c.tslot(1, f, c.L, 0) : nullptr);
     wg_sync();  // pick done
     if (S.flags[6]) return;
     // The head dot already waited for the youngest loads; draining here keeps the next frame's first layer from
@@ -2343,6 +2537,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     for (int i = 0; i < 8; i++) S.flags[i] = 0;
     S.pubcnt = 0;
     S.pubseq = 0;
+    if constexpr (SMP) ((PickShared*)((char*)&S + kPickShared<H, I, W, V, CP>))->bad = 0u;
     }
   }
   __syncthreads();
@@ -2432,7 +2627,7 @@ int prepare_kernel(size_t lds) {
 }
 template <int H, int I, int W, int V, bool CP, bool SMP, int WD, bool KEEP, bool PAIRK = false, bool F16 = false>
 int launch_kernel(const sk_talker_desc* d, const CpArgs& cp, int n_frames, hipStream_t st) {
-  constexpr size_t need = SMP ? kPickCopy<H, I, W, V, CP> + (size_t)V * 8
+  constexpr size_t need = SMP ? kPickShared<H, I, W, V, CP> + sizeof(PickShared)
                               : sizeof(Lds<H, I, W, V, CP>) + (PAIRK ? sizeof(LdsPair<H, I>) : 0);
   const size_t lds = need < 96 * 1024 ? 96 * 1024 : need;  // one workgroup per CU
   const int rc = prepare_kernel<H, I, W, V, CP, SMP, WD, KEEP, PAIRK, F16>(lds);

@@ -582,8 +582,8 @@ class Qwen3Kernels(Qwen3Fast):
     def frame_error(self) -> int:
         """Error word of the frame kernel's workspace (0 when healthy; reads device memory, so it synchronises).
         Codes: 2 placement, 5 position/token out of range, 10 the poll of a projected code predictor's input
-        timed out, 11..18 a poll of stage S1, S2, S3, S4, S5, S6, head, pick timed out, 19 the exchange of a
-        sampled pick timed out (``frame_diag`` tells the frame, layer and workgroup)."""
+        timed out, 11..18 a poll of stage S1, S2, S3, S4, S5, S6, head, pick timed out, 19 the maxima of a sampled
+        pick, 20 its values timed out (``frame_diag`` tells the frame, layer and workgroup)."""
         return int(self.frame_ws[:4].view(torch.int32).item())
 
     def frame_diag(self) -> dict:

@@ -223,20 +223,20 @@ def test_talker17b_64_frames_one_launch(gpu):
     assert rel_err(eng.logit_t.view(-1), gold["logits_last"]) < TOL
 
 
-def _sampled_engine(gpu, top_k, seed=2, name="small06b", frames=24):
+def _sampled_engine(gpu, top_k, seed=2, name="small06b", frames=24, sup=64):
     from sokutou_amd.fast import Sampling
 
     smp = Sampling(do_sample=True, temperature=0.9, top_k=top_k, repetition_penalty=1.05, min_new_tokens=2,
                    max_new_tokens=64)
     eng, tok = syn.make_engine(name, seed=seed, wd="i8row", device=gpu, frame_kernel=True, sampling=smp,
-                               suppress_tail=64, frames=frames)
+                               suppress_tail=sup, frames=frames)
     assert eng.frame_kernel
     return eng, tok
 
 
-def _sampled_oracle(name, seed, tok, key, frames, top_k, eos, cnt0=0, follow=None):
-    """Codes of ``frames`` sampled frames: processor (repetition penalty 1.05 on the seen ids, the last 64 ids but
-    EOS suppressed, EOS blocked while fewer than 2 codes exist), temperature 0.9, top_k, draw cnt0 + f.
+def _sampled_oracle(name, seed, tok, key, frames, top_k, eos, cnt0=0, follow=None, sup=64):
+    """Codes of ``frames`` sampled frames: processor (repetition penalty 1.05 on the seen ids, the last ``sup`` ids
+    but EOS suppressed, EOS blocked while fewer than 2 codes exist), temperature 0.9, top_k, draw cnt0 + f.
     With ``follow`` (the GPU's codes) the oracle takes the GPU's code as each frame's output instead of its own and
     returns, per frame, its own pick and how far the GPU's pick was from winning: the larger of its distance below
     the top_k-th largest value (the keep threshold) and below the winner in the perturbed values (0 when the two
@@ -247,15 +247,15 @@ def _sampled_oracle(name, seed, tok, key, frames, top_k, eos, cnt0=0, follow=Non
     orc, otok, s = talker_oracle(name, seed, "i8row", max_len=syn.WORKLOADS[name]["kv"] + frames + 1)
     assert otok == tok
     V = s.vocab
-    sup = np.zeros(V, bool)
-    sup[V - 64:] = True
-    sup[eos] = False
+    sup_m = np.zeros(V, bool)
+    sup_m[V - sup:] = True
+    sup_m[eos] = False
     seen = np.zeros(V, bool)
     seen[tok] = True
     pos, t, out = syn.WORKLOADS[name]["kv"], tok, []
     for f in range(frames):
         lg = orc.logits(orc.forward(orc.w["emb"][t], pos + f))
-        v = O.process_logits(lg, seen, 1.05, sup, 1 + f, 2, eos)
+        v = O.process_logits(lg, seen, 1.05, sup_m, 1 + f, 2, eos)
         inv_t = float(np.float32(1.0 / 0.9))
         mine, _ = O.sample_draw(v, inv_t, top_k, key, cnt0 + f)
         if follow is None:
@@ -276,12 +276,12 @@ def _sampled_oracle(name, seed, tok, key, frames, top_k, eos, cnt0=0, follow=Non
     return out
 
 
-def _check_sampled(codes, name, tok, key, top_k, eos, cnt0=0):
+def _check_sampled(codes, name, tok, key, top_k, eos, cnt0=0, sup=64):
     """Every GPU pick is the oracle's pick given the same history, except at near-ties: the GPU's logits differ from
     the fp32 oracle's by up to about 3e-4 (1e-4 relative; the bf16 K/V cache rounds the two sides' keys and values
     differently where their fp32 values straddle a rounding tie), so where the oracle's two best perturbed values
     lie closer than 1e-3 either may win. At most two such frames in a run."""
-    chk = _sampled_oracle(name, 2, tok, key, len(codes), top_k, eos, cnt0=cnt0, follow=codes)
+    chk = _sampled_oracle(name, 2, tok, key, len(codes), top_k, eos, cnt0=cnt0, follow=codes, sup=sup)
     ties = [(f, c, m, gap) for f, (c, (m, gap)) in enumerate(zip(codes, chk)) if c != m]
     for f, c, m, gap in ties:
         assert gap < 1e-3, f"frame {f}: GPU {c} is {gap:.3e} below the oracle's pick {m}"
@@ -290,17 +290,21 @@ def _check_sampled(codes, name, tok, key, top_k, eos, cnt0=0):
         print(f"  near-ties resolved the other way: {ties}", flush=True)
 
 
-@pytest.mark.parametrize("top_k,name", [(50, "small06b"), (0, "small06b"), (1, "small06b"), (64, "small06b"),
-                                         (100, "small06b"), (50, "small17b")])
-def test_sampled_frames_one_launch_against_oracle(gpu, top_k, name):
+@pytest.mark.parametrize("top_k,name,sup", [(50, "small06b", 64), (0, "small06b", 64), (1, "small06b", 64),
+                                             (64, "small06b", 64), (100, "small06b", 64), (50, "small06b", 3040),
+                                             (50, "small17b", 64)])
+def test_sampled_frames_one_launch_against_oracle(gpu, top_k, name, sup):
     """Sampled picks inside the persistent kernel: 24 frames in one launch with the talker processor, every code
     equal to the oracle's draw (Philox key from torch's generator, draw counter = frame index); top_k 0 keeps the
     whole vocabulary, top_k 1 reduces to the argmax of the processed logits, 64 is the largest top_k with the
-    lane-maxima bound and 100 takes the unbounded path (every value a candidate). The counter advances by the
+    lane-maxima bound and 100 takes the unbounded path (every value a candidate). With all but 32 ids (and EOS)
+    suppressed, fewer than top_k lane maxima are finite, so the bound is -inf, every value is a candidate and the
+    pick takes the bisection path with top_k 50; the kept set is the finite values. The counter advances by the
     frames."""
     F = 24
-    print(f"{name}: {F} sampled frames (top_k {top_k}) in one launch against the oracle", flush=True)
-    eng, tok = _sampled_engine(gpu, top_k, name=name, frames=F)
+    print(f"{name}: {F} sampled frames (top_k {top_k}, {sup} ids suppressed) in one launch against the oracle",
+          flush=True)
+    eng, tok = _sampled_engine(gpu, top_k, name=name, frames=F, sup=sup)
     torch.manual_seed(5 + top_k)
     key = int(torch.randint(0, 2**62, (1,)).item())
     eng.fs.set_seed(key)
@@ -309,7 +313,7 @@ def test_sampled_frames_one_launch_against_oracle(gpu, top_k, name):
     assert eng.frame_error() == 0, eng.frame_diag()
     codes = eng.frame_ids[:F].cpu().tolist()
     print(f"  codes {codes[:8]}..., {len(set(codes))} distinct", flush=True)
-    _check_sampled(codes, name, tok, key, top_k, eng.eos)
+    _check_sampled(codes, name, tok, key, top_k, eng.eos, sup=sup)
     assert int(eng.fs.counter.item()) == F
     assert int(eng.ngen.item()) == 1 + F and int(eng.pos.item()) == syn.WORKLOADS[name]["kv"] + F
     assert int(eng.next_id0.item()) == codes[-1]
