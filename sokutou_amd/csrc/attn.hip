@@ -8,9 +8,10 @@
 // one launch of nkv * nsplit blocks.
 //
 // Decode attention moves few bytes per block, so its time is the number of dependent memory round trips. The
-// kernel has four: the position, then every input it needs at once (q, the new k/v, the RoPE row, the norm
-// weights and the whole K/V chunk of the block, up to 64 positions held in registers), then publishing the
-// partial, then one batch of partial loads in the merging block.
+// kernel has three: the position together with the block's first 64 K/V rows (the split boundaries depend only on
+// the cache length, so these loads need no position), then every input that depends on the position (q, the new
+// k/v, the RoPE row, the norm weights), then publishing the partial, and one batch of partial loads in the merging
+// block.
 //
 // Layout inside a block (4 wave64s): lane (g = lane / 16, sl = lane % 16) of wave w holds dims [8 sl, 8 sl + 8)
 // of positions t0 + 16 i + 4 w + g (i = 0..3); one 16-byte load covers 8 bf16 values and a score is a 16-lane
@@ -30,15 +31,19 @@ constexpr int kPass = 64;         // positions one block holds in registers per 
 constexpr int kPart = SK_HD + 2;  // m, l, o[128]
 constexpr float kInvSqrtHd = 0.08838834764831845f;
 
-// Splits of the cache: one block per head up to 128 positions (no merge), else one split per 128 positions, at least
-// 8 and at most 16. Every partial costs the merging block a load per thread, and a block covers its positions in
-// passes of 64: fewer, longer splits win until a block needs more than two or three passes. Measured per call with 8 kv heads at positions 64 / 255 / 512 / 1023 / 2047: 6.3 / 7.8 / 9.5 / 10.4 /
-// 12.2 us, against 8.1 / 10.9 / 13.7 / 14.0 / 14.3 us with up to 32 splits of 16 positions.
-int nsplit_for(int max_len) {
-  if (max_len <= 128) return 1;
-  const int n = (max_len + 127) / 128;
-  return n < 8 ? 8 : (n > kSplitMax ? kSplitMax : n);
+// Splits of the cache: one block per head up to 128 positions (no merge), else chunks of a fixed number of positions,
+// a multiple of the 64-position pass: 64 up to 1024 positions, beyond that the fewest 64s that keep 16 splits or
+// fewer. Fixed chunks (rather than the cache so far divided evenly) let a block load its first pass before it knows
+// the position, and never leave a pass of one or two positions.
+struct SplitPlan {
+  int chunk, nsplit;
+};
+SplitPlan split_plan(int max_len) {
+  if (max_len <= 128) return {max_len, 1};
+  const int chunk = kPass * ((max_len + kPass * kSplitMax - 1) / (kPass * kSplitMax));
+  return {chunk, (max_len + chunk - 1) / chunk};
 }
+int nsplit_for(int max_len) { return split_plan(max_len).nsplit; }
 constexpr int64_t part_bytes(int nkv, int nsplit) { return ((int64_t)nkv * 2 * nsplit * kPart * 4 + 255) / 256 * 256; }
 // Workspace: the error word (byte 0) and the per-head arrival counters (from byte 4) first, at a fixed place for
 // any cache length, then the partials, so one workspace serves calls with different max_len (talker and code
@@ -74,18 +79,29 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ qkv
                                                    const int64_t* __restrict__ pos_ptr, int pos_add, int max_len, int nq,
                                                    int nkv, float* __restrict__ out, float* __restrict__ part,
                                                    unsigned* __restrict__ err, unsigned* __restrict__ counters,
-                                                   int nsplit) {
+                                                   int chunk, int nsplit) {
   using C = Cache<CT>;
   __shared__ float qsh[2][SK_HD];
   __shared__ float ksh[SK_HD];
   __shared__ float vsh[SK_HD];
   __shared__ float sc[2][kPass];
-  __shared__ float red[16];
   __shared__ float opart[4][4][16][17];  // [wave][row g][sl][head*8 + i], padded against bank conflicts
   __shared__ float mls[2][kSplitMax][2];
   __shared__ int is_last;
   const int kvh = blockIdx.x, split = blockIdx.y;
   const int t = threadIdx.x, p = t >> 7, d = t & (SK_HD - 1), w = t >> 6, lane = t & 63, g = lane >> 4, sl = lane & 15;
+  const int t0 = split * chunk;
+  typename C::T* Kh = Kc + (size_t)kvh * max_len * SK_HD;
+  typename C::T* Vh = Vc + (size_t)kvh * max_len * SK_HD;
+  // the first pass's K/V rows, before the position: rows past the cache's end read its last row instead and, like
+  // rows at or past the position, are never used (the row at the position comes from LDS)
+  Row8<CT> kr8[4], vr8[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int row = min(t0 + 16 * i + 4 * w + g, max_len - 1);
+    kr8[i].load(Kh + (size_t)row * SK_HD + 8 * sl);
+    vr8[i].load(Vh + (size_t)row * SK_HD + 8 * sl);
+  }
   const int64_t pos64 = (pos_ptr ? pos_ptr[0] : 0) + (int64_t)pos_add;
   if (pos64 < 0 || pos64 >= max_len) {
     // every block takes this exit (the position is uniform), so no counter moves and nothing is written
@@ -94,50 +110,56 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ qkv
   }
   const int pos = (int)pos64;
   const int T = pos + 1;
-  const int chunk = (T + nsplit - 1) / nsplit;
-  const int t0 = split * chunk, t1 = min(T, t0 + chunk);
+  const int t1 = min(T, t0 + chunk);
   const int n = t1 > t0 ? t1 - t0 : 0;
   const bool has_pos = t0 <= pos && pos < t1;
-  typename C::T* Kh = Kc + (size_t)kvh * max_len * SK_HD;
-  typename C::T* Vh = Vc + (size_t)kvh * max_len * SK_HD;
 
   float m = -INFINITY, l = 0.f, o = 0.f;  // running partial of head p, dim d
   for (int base = 0; base < n; base += kPass) {
-    // ---- every load of the pass at once: K/V rows, then (first pass) q / new k,v / rope / norm weights ------
-    Row8<CT> kr8[4], vr8[4];
+    // ---- every load of the pass at once: K/V rows (later passes), then (first pass) q / new k,v / rope / norm
+    if (base > 0) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int jj = base + 16 * i + 4 * w + g;
-      if (jj < n && t0 + jj != pos) {
-        kr8[i].load(Kh + (size_t)(t0 + jj) * SK_HD + 8 * sl);
-        vr8[i].load(Vh + (size_t)(t0 + jj) * SK_HD + 8 * sl);
-      } else {
-        kr8[i].zero();
-        vr8[i].zero();
+      for (int i = 0; i < 4; i++) {
+        const int jj = base + 16 * i + 4 * w + g;
+        if (jj < n && t0 + jj != pos) {
+          kr8[i].load(Kh + (size_t)(t0 + jj) * SK_HD + 8 * sl);
+          vr8[i].load(Vh + (size_t)(t0 + jj) * SK_HD + 8 * sl);
+        } else {
+          kr8[i].zero();
+          vr8[i].zero();
+        }
       }
     }
     if (base == 0) {
-      const float c = rope[(size_t)pos * SK_HD + (d & 63)], s = rope[(size_t)pos * SK_HD + 64 + (d & 63)];
-      const float qv = qkv[(2 * kvh + p) * SK_HD + d];
-      const float kv = has_pos ? qkv[nq * SK_HD + p * nkv * SK_HD + kvh * SK_HD + d] : 0.f;
-      const float qw = qn[d], kw = kn[d];
-      const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
-      if (lane == 0) { red[w] = sq; red[4 + w] = sk; }
-      __syncthreads();
-      qsh[p][d] = qv * rsqrtf((red[2 * p] + red[2 * p + 1]) / SK_HD + eps) * qw;
-      if (has_pos) {
-        if (p == 0) ksh[d] = kv * rsqrtf((red[4] + red[5]) / SK_HD + eps) * kw;
-        else vsh[d] = C::rnd(kv);
-      }
-      __syncthreads();
-      const float qr = (qsh[p][d] * c + (d < 64 ? -qsh[p][d + 64] : qsh[p][d - 64]) * s) * kInvSqrtHd;
-      float kr = 0.f;
-      if (has_pos && p == 0) kr = C::rnd(ksh[d] * c + (d < 64 ? -ksh[d + 64] : ksh[d - 64]) * s);
-      __syncthreads();
-      qsh[p][d] = qr;
-      if (has_pos) {
-        if (p == 0) { ksh[d] = kr; Kh[(size_t)pos * SK_HD + d] = C::st(kr); }
-        else Vh[(size_t)pos * SK_HD + d] = C::st(vsh[d]);
+      // q of both heads, and in the block holding the position this step's k and v: one wave per vector (wave 0 q of
+      // head 2 kvh, wave 1 q of head 2 kvh + 1, wave 2 k, wave 3 v), dims lane and lane + 64 per lane, so the per-head
+      // RMSNorm is a wave sum and the rotate-half RoPE pair stays in the lane: one barrier
+      if (w < 2 || has_pos) {
+        const float* src = w < 2 ? qkv + (2 * kvh + w) * SK_HD : qkv + nq * SK_HD + (w - 2) * nkv * SK_HD + kvh * SK_HD;
+        const float x0 = src[lane], x1 = src[lane + 64];
+        if (w < 3) {
+          const float* nw = w < 2 ? qn : kn;
+          const float c = rope[(size_t)pos * SK_HD + lane], sn = rope[(size_t)pos * SK_HD + 64 + lane];
+          const float inv = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / SK_HD + eps);
+          const float y0 = x0 * inv * nw[lane], y1 = x1 * inv * nw[lane + 64];
+          const float r0 = y0 * c + -y1 * sn, r1 = y1 * c + y0 * sn;
+          if (w < 2) {
+            qsh[w][lane] = r0 * kInvSqrtHd;
+            qsh[w][lane + 64] = r1 * kInvSqrtHd;
+          } else {
+            const float k0 = C::rnd(r0), k1 = C::rnd(r1);
+            ksh[lane] = k0;
+            ksh[lane + 64] = k1;
+            Kh[(size_t)pos * SK_HD + lane] = C::st(k0);
+            Kh[(size_t)pos * SK_HD + lane + 64] = C::st(k1);
+          }
+        } else {
+          const float v0 = C::rnd(x0), v1 = C::rnd(x1);
+          vsh[lane] = v0;
+          vsh[lane + 64] = v1;
+          Vh[(size_t)pos * SK_HD + lane] = C::st(v0);
+          Vh[(size_t)pos * SK_HD + lane + 64] = C::st(v1);
+        }
       }
       __syncthreads();
     }
@@ -164,18 +186,11 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ qkv
       if (sl == 0 && jj - base < np) { sc[0][jj - base] = s0; sc[1][jj - base] = s1; }
     }
     __syncthreads();
-    // ---- pass softmax statistics per head (threads 0-127: head 0, 128-255: head 1) ---------------------------
-    const float sv = d < np ? sc[p][d] : -INFINITY;
-    const float mx = wave_max(sv);
-    if (lane == 0) red[8 + w] = mx;
-    __syncthreads();
-    const float mp = fmaxf(red[8 + 2 * p], red[8 + 2 * p + 1]);
-    const float ev = d < np ? expf(sv - mp) : 0.f;
-    const float se = wave_sum(ev);
-    if (d < np) sc[p][d] = ev;
-    if (lane == 0) red[12 + w] = se;
-    __syncthreads();
-    const float lp = red[12 + 2 * p] + red[12 + 2 * p + 1];
+    // ---- pass softmax statistics of both heads, computed by every wave from the pass's scores (no barrier) -----
+    const float sv0 = lane < np ? sc[0][lane] : -INFINITY, sv1 = lane < np ? sc[1][lane] : -INFINITY;
+    const float mp0 = wave_max(sv0), mp1 = wave_max(sv1);
+    const float lp0 = wave_sum(lane < np ? expf(sv0 - mp0) : 0.f), lp1 = wave_sum(lane < np ? expf(sv1 - mp1) : 0.f);
+    const float mp = p ? mp1 : mp0, lp = p ? lp1 : lp0;
     // ---- o_pass = Σ p_j V_j for both heads -------------------------------------------------------------------
     float a0[8], a1[8];
 #pragma unroll
@@ -191,7 +206,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ qkv
         } else {
           vr8[i].get(v8);
         }
-        const float e0 = sc[0][jj - base], e1 = sc[1][jj - base];
+        const float e0 = expf(sc[0][jj - base] - mp0), e1 = expf(sc[1][jj - base] - mp1);
 #pragma unroll
         for (int e = 0; e < 8; e++) { a0[e] = __builtin_fmaf(e0, v8[e], a0[e]); a1[e] = __builtin_fmaf(e1, v8[e], a1[e]); }
       }
@@ -210,7 +225,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ qkv
     o = o * fo + op * fp;
     l = l * fo + lp * fp;
     m = mn;
-    __syncthreads();  // sc / opart are rewritten by the next pass
+    if (base + kPass < n) __syncthreads();  // sc / opart are rewritten by the next pass
   }
 
   if (nsplit == 1) {  // the whole cache in this block: no partial to merge
@@ -282,14 +297,15 @@ int check_attn(const float* qkv, const float* qn, const float* kn, const float* 
 int launch_attn(const float* qkv, const float* qn, const float* kn, float eps, const float* rope, void* Kc, void* Vc,
                 const int64_t* pos_ptr, int pos_add, int max_len, int nq, int nkv, float* out, float* part,
                 unsigned* err, unsigned* counters, int ct, hipStream_t st, const char* name) {
-  const int nsplit = nsplit_for(max_len);
+  const SplitPlan sp = split_plan(max_len);
+  const int nsplit = sp.nsplit;
   dim3 grid(nkv, nsplit);
   if (ct == SK_CT_BF16)
     hipLaunchKernelGGL((k_attn<SK_CT_BF16>), grid, dim3(kThreads), 0, st, qkv, qn, kn, eps, rope, (bf16_t*)Kc,
-                       (bf16_t*)Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, err, counters, nsplit);
+                       (bf16_t*)Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, err, counters, sp.chunk, nsplit);
   else
     hipLaunchKernelGGL((k_attn<SK_CT_F32>), grid, dim3(kThreads), 0, st, qkv, qn, kn, eps, rope, (float*)Kc,
-                       (float*)Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, err, counters, nsplit);
+                       (float*)Vc, pos_ptr, pos_add, max_len, nq, nkv, out, part, err, counters, sp.chunk, nsplit);
   return sk_check_launch(hipGetLastError(), name);
 }
 

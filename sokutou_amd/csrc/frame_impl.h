@@ -2445,10 +2445,11 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
       const float inv = S.inv;
       const bool block_eos = block_eos0 && (ngen0 + f) < c.d.min_new;
       uint64_t best = 0;
-      // Sampling kernels: the rows' values (seen-byte masks and offsets) are recomputed each frame; hoisted out of
-      // the frame loop they stayed live across it and spilled, and their reloads sat in this serial lane-0 loop
+      // The rows' values (seen-byte masks and offsets) are recomputed each frame: hoisted out of the frame loop they
+      // stayed live across it and spilled (spilled VGPRs 0.6B 1 -> 0, 1.7B 5 -> 2, 1.7B i8g32 15 -> 3), and in the
+      // sampling kernels their reloads sat in this serial lane-0 loop (0.5 us per frame)
       int hr0 = h_w0;
-      if constexpr (SMP) __asm__ volatile("" : "+v"(hr0));
+      __asm__ volatile("" : "+v"(hr0));
       if (lane == 0) {
 #pragma unroll
         for (int i = 0; i < C::RW_HEAD; i++) {
