@@ -36,6 +36,7 @@ constexpr int kM = 16;         // rows of every activation buffer (streams)
 constexpr int kTerms = SK_BATCH_TERMS;
 constexpr int kThreads = 256;
 constexpr int kOutF32 = 0, kOutSwiglu = 1, kOutAcc = 2;
+constexpr int kMaxSlices = 16;  // K slices of one GEMM (the plan keeps S = K / (64 CW) at or below this)
 
 // ---- conversions ----------------------------------------------------------------------------------------------
 // two floats whose low 16 bits are zero (small integers) -> packed bf16 pair, lo in the low half
@@ -82,128 +83,161 @@ struct GemmArgs {
   bf16_t* xn;           // ACC: planes [kTerms][16][N] of bf16(h ⊙ nw)
   const float* nw;      // ACC: next RMSNorm weight [N]
   float* ssp_out;       // ACC: [N/16][16] partial sums of squares of the updated residual
-  int S;                // K slices (workgroups per output tile)
-  float* part;          // S > 1: [S][tiles][R][256] partial sums
-  unsigned* counters;   // S > 1: [tiles] arrivals, zero between launches
+  int S;                // K slices (workgroups per row block)
+  float* part;          // S > 1: [S][N / 16][256] partial sums
+  unsigned* counters;   // S > 1: [row blocks] arrivals, zero between launches
 };
 
-// Workgroup (tile, slice) computes R 16-row groups of the output for all 16 rows over K slice `slice` (4 CW
-// chunks of 64); its 4 waves take CW chunks each and meet in LDS for a fixed-order sum. With S > 1 slices the
-// workgroups of a tile publish their sums (device-coherent stores) and the last to arrive adds them in slice
-// order and runs the epilogue, so the result does not depend on arrival order. Every weight load of a wave is
-// issued at the top (the weight stream is the kernel's HBM traffic); the activation planes (L2-resident) run DA
-// chunks ahead.
+// Workgroup (nb, slice) computes output row groups 4 R nb .. 4 R nb + 4 R - 1 (16 rows each; wave w owns R of them)
+// for all 16 streams over K slice `slice` (CW chunks of 64). The slice's activation planes are read from memory once
+// per workgroup into LDS and shared by the four waves, which split the rows: the planes' traffic is then one read
+// per 64 R output rows instead of one per 16 R (when the waves split K instead, each workgroup read its whole slice
+// for 16 R rows, and the planes of a step were read 2-3 times more often than the weights). Every load goes out at
+// the top: the activation slice first (it is needed first), then the wave's weights (its HBM traffic). With S > 1
+// slices the workgroups of a row block publish their sums (device-coherent stores) and the last to arrive adds them in
+// slice order and runs the epilogue, so the result does not depend on arrival order.
 template <int OUT, int R, int CW>
 __global__ __launch_bounds__(kThreads) void k_bgemm(GemmArgs p) {
-  constexpr int DA = CW < 4 ? CW : 4;
-  __shared__ float red[4][R][4][64];
+  constexpr int kSeg = kTerms * kM * CW * 8;            // 16-byte activation segments of the slice
+  constexpr int kAct = (kSeg + kThreads - 1) / kThreads;  // per thread
+  __shared__ uint4 xs[kTerms][CW][2][64];  // [term][chunk][half][lane m + 16 j]: bf16 x[m][64 c + 16 j + 8 h ..+8]
   __shared__ float ssq[16][kM];
   __shared__ float inv_s[kM];
   __shared__ int last_s;
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
   const int C = p.K / 64;                 // 64-wide chunks per row
-  const int tile = blockIdx.x, slice = blockIdx.y;
-  const int g0 = tile * R;
-  const int c0 = (slice * 4 + wv) * CW;
+  const int G = p.N / 16;                 // row groups
+  const int nb = blockIdx.x, slice = blockIdx.y;
+  const int c0 = slice * CW;
+  const int g0 = (nb * 4 + wv) * R;       // this wave's first row group
   const size_t plane = (size_t)kM * p.K;
-  const uint4* xp = (const uint4*)(p.x + (size_t)(lane & 15) * p.K + (size_t)c0 * 64 + 16 * (lane >> 4));
-  uint4 wq[CW][R], xa[DA][kTerms][2];
+  // the slice's activation segments: segment a = (t, m, q) holds bf16 x_t[m][64 c0 + 8 q .. + 8]
+  uint4 av[kAct];
+#pragma unroll
+  for (int i = 0; i < kAct; i++) {
+    const int a = tid + kThreads * i;
+    if (a < kSeg) {
+      const int t = a / (kM * CW * 8), m = (a / (CW * 8)) % kM, q = a % (CW * 8);
+      av[i] = gload4((const uint4*)(p.x + t * plane + (size_t)m * p.K + (size_t)c0 * 64 + 8 * q));
+    }
+  }
+  uint4 wq[CW][R];
 #pragma unroll
   for (int c = 0; c < CW; c++)
 #pragma unroll
-    for (int r = 0; r < R; r++)
-      wq[c][r] = ld_stream((const uint4*)p.w + ((size_t)(g0 + r) * C + c0 + c) * 64 + lane);
-  auto load_a = [&](int slot, int c) {
-#pragma unroll
-    for (int t = 0; t < kTerms; t++) {
-      const uint4* q = xp + (t * plane) / 8 + c * 8;
-      xa[slot][t][0] = gload4(q);
-      xa[slot][t][1] = gload4(q + 1);
+    for (int r = 0; r < R; r++) {
+      const int g = min(g0 + r, G - 1);  // a row group past the matrix loads the last one (never stored)
+      wq[c][r] = ld_stream((const uint4*)p.w + ((size_t)g * C + c0 + c) * 64 + lane);
     }
-  };
-#pragma unroll
-  for (int c = 0; c < DA; c++) load_a(c, c);
-  float ssv = 0.f;  // this thread's share of the RMSNorm partial sums (used by the epilogue workgroup)
+  float ssv = 0.f;  // this thread's share of the RMSNorm partial sums
   if (p.ssp)
     for (int q = tid >> 4; q < p.np; q += 16) ssv += gload(p.ssp + q * kM + (tid & 15));
-  __builtin_amdgcn_sched_barrier(0);
-  f32x4 acc[R], acc2[R];  // first term, later terms (kept apart: the small terms accumulate at their own scale)
 #pragma unroll
-  for (int r = 0; r < R; r++) { acc[r] = f32x4{0.f, 0.f, 0.f, 0.f}; acc2[r] = acc[r]; }
-#pragma unroll
-  for (int c = 0; c < CW; c++) {
-    const int slot = c % DA;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        const uint4 q = wq[c][r];
-        const bf16x8 b = h ? i8x8_bf16(q.z, q.w) : i8x8_bf16(q.x, q.y);
-        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[slot][0][h]), b, acc[r], 0, 0, 0);
-#pragma unroll
-        for (int t = 1; t < kTerms; t++)
-          acc2[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[slot][t][h]), b, acc2[r], 0, 0, 0);
-      }
+  for (int i = 0; i < kAct; i++) {
+    const int a = tid + kThreads * i;
+    if (a < kSeg) {
+      const int t = a / (kM * CW * 8), m = (a / (CW * 8)) % kM, q = a % (CW * 8);
+      xs[t][q >> 3][q & 1][m + 16 * ((q >> 1) & 3)] = av[i];
     }
-    if (c + DA < CW) load_a(slot, c + DA);
   }
-  // D[m][n] sits in lane n + 16 (m / 4), element m % 4
-#pragma unroll
-  for (int r = 0; r < R; r++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) red[wv][r][i][lane] = acc[r][i] + acc2[r][i];
   if (p.ssp) ssq[tid >> 4][tid & 15] = ssv;
   __syncthreads();
-  const int i = tid >> 6, L = tid & 63;
-  float v[R];
-#pragma unroll
-  for (int r = 0; r < R; r++) v[r] = (red[0][r][i][L] + red[1][r][i][L]) + (red[2][r][i][L] + red[3][r][i][L]);
-  if (p.S > 1) {
-    const uint32_t base = (uint32_t)(((size_t)slice * gridDim.x + tile) * R) * 256;
-#pragma unroll
-    for (int r = 0; r < R; r++) buf_stf(p.part, (base + r * 256 + tid) * 4, v[r]);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last_s = prev == (unsigned)(p.S - 1);
-    }
-    __syncthreads();
-    if (!last_s) return;
-#pragma unroll
-    for (int r = 0; r < R; r++) v[r] = 0.f;
-    for (int q = 0; q < p.S; q++) {
-      const uint32_t b2 = (uint32_t)(((size_t)q * gridDim.x + tile) * R) * 256;
-#pragma unroll
-      for (int r = 0; r < R; r++) v[r] += buf_ldf(p.part, (b2 + r * 256 + tid) * 4);
-    }
-    if (tid == 0) __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
   if (p.ssp && tid < kM) {
     float s = 0.f;
 #pragma unroll
     for (int q = 0; q < 16; q++) s += ssq[q][tid];
     inv_s[tid] = rsqrtf(s / p.K + p.eps);
   }
-  __syncthreads();
-  const int m = 4 * (L >> 4) + i, nl = L & 15;
-  const float iv = p.ssp ? inv_s[m] : 1.f;
+  f32x4 acc[R], acc2[R];  // first term, later terms (kept apart: the small terms accumulate at their own scale)
+#pragma unroll
+  for (int r = 0; r < R; r++) { acc[r] = f32x4{0.f, 0.f, 0.f, 0.f}; acc2[r] = acc[r]; }
+#pragma unroll
+  for (int c = 0; c < CW; c++) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      bf16x8 xa[kTerms];
+#pragma unroll
+      for (int t = 0; t < kTerms; t++) xa[t] = as_bf16x8(xs[t][c][h][lane]);
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const uint4 q = wq[c][r];
+        const bf16x8 b = h ? i8x8_bf16(q.z, q.w) : i8x8_bf16(q.x, q.y);
+        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[0], b, acc[r], 0, 0, 0);
+#pragma unroll
+        for (int t = 1; t < kTerms; t++) acc2[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[t], b, acc2[r], 0, 0, 0);
+      }
+    }
+  }
+  // D[m][n] sits in lane n + 16 (m / 4), element m % 4
+  float v[R][4];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[r][i] = acc[r][i] + acc2[r][i];
+  if (p.S > 1) {
+    // partial of (slice, row group g): 256 floats, element i of lane L at 64 i + L
+    const uint32_t stride = (uint32_t)G * 256u;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+      if (g0 + r < G)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          buf_stf(p.part, ((uint32_t)slice * stride + (uint32_t)(g0 + r) * 256u + 64u * i + lane) * 4u, v[r][i]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(&p.counters[nb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_s = prev == (unsigned)(p.S - 1);
+    }
+    __syncthreads();
+    if (!last_s) return;
+    // every slice's partial at once (one round trip), then the sum in slice order
+    float pv[kMaxSlices][R][4];
+#pragma unroll
+    for (int q = 0; q < kMaxSlices; q++)
+      if (q < p.S)
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            pv[q][r][i] = buf_ldf(p.part, ((uint32_t)q * stride + (uint32_t)min(g0 + r, G - 1) * 256u + 64u * i + lane) * 4u);
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float a = 0.f;
+#pragma unroll
+        for (int q = 0; q < kMaxSlices; q++)
+          if (q < p.S) a += pv[q][r][i];
+        v[r][i] = a;
+      }
+    if (tid == 0) __hip_atomic_store(&p.counters[nb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    __syncthreads();  // inv_s
+  }
+  const int nl = lane & 15;
 #pragma unroll
   for (int r = 0; r < R; r++) {
+    if (g0 + r >= G) break;
     const int n = (g0 + r) * 16 + nl;
-    const float y = v[r] * bf2f(p.s[n]) * iv;
-    if constexpr (OUT == kOutF32) {
-      p.out[(size_t)m * p.N + n] = y;
-    } else if constexpr (OUT == kOutSwiglu) {
-      const float u = dpp<0xB1>(y);  // lane L ^ 1: the up row next to this gate row
-      if (!(nl & 1)) store_terms(p.act, (size_t)kM * (p.N / 2), (size_t)m * (p.N / 2) + n / 2, silu_mul(y, u));
-    } else {
-      float* hp = p.out + (size_t)m * p.N + n;
-      const float hn = *hp + y;
-      *hp = hn;
-      store_terms(p.xn, (size_t)kM * p.N, (size_t)m * p.N + n, hn * p.nw[n]);
-      const float ss = row16_sum(hn * hn);
-      if (nl == 0) p.ssp_out[(g0 + r) * kM + m] = ss;
+    const float sc = bf2f(p.s[n]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int m = 4 * (lane >> 4) + i;
+      const float y = v[r][i] * sc * (p.ssp ? inv_s[m] : 1.f);
+      if constexpr (OUT == kOutF32) {
+        p.out[(size_t)m * p.N + n] = y;
+      } else if constexpr (OUT == kOutSwiglu) {
+        const float u = dpp<0xB1>(y);  // lane L ^ 1: the up row next to this gate row
+        if (!(nl & 1)) store_terms(p.act, (size_t)kM * (p.N / 2), (size_t)m * (p.N / 2) + n / 2, silu_mul(y, u));
+      } else {
+        float* hp = p.out + (size_t)m * p.N + n;
+        const float hn = *hp + y;
+        *hp = hn;
+        store_terms(p.xn, (size_t)kM * p.N, (size_t)m * p.N + n, hn * p.nw[n]);
+        const float ss = row16_sum(hn * hn);
+        if (nl == 0) p.ssp_out[(g0 + r) * kM + m] = ss;
+      }
     }
   }
 }
@@ -527,61 +561,46 @@ __global__ __launch_bounds__(kThreads) void k_bpick(PickArgs a) {
 }
 
 // ---- dispatch ------------------------------------------------------------------------------------------------
-template <int OUT, int R, int CW>
-hipError_t launch_one(const GemmArgs& p, hipStream_t st) {
-  if constexpr (R * CW > 32) {  // more weight registers than a wave holds: never planned
-    return hipErrorInvalidValue;
-  } else {
-    hipLaunchKernelGGL((k_bgemm<OUT, R, CW>), dim3(p.N / (16 * R), p.S), dim3(kThreads), 0, st, p);
-    return hipGetLastError();
-  }
-}
-template <int OUT, int R>
-hipError_t launch_cw(const GemmArgs& p, hipStream_t st) {
-  switch (p.K / (256 * p.S)) {
-    case 1: return launch_one<OUT, R, 1>(p, st);
-    case 2: return launch_one<OUT, R, 2>(p, st);
-    case 3: return launch_one<OUT, R, 3>(p, st);
-    case 4: return launch_one<OUT, R, 4>(p, st);
-    case 6: return launch_one<OUT, R, 6>(p, st);
-    case 8: return launch_one<OUT, R, 8>(p, st);
-  }
-  return hipErrorInvalidValue;
-}
-bool k_supported(int K) { return K == 512 || K == 1024 || K == 2048 || K == 3072 || K == 4096 || K == 6144; }
-
-// Launch plan: R 16-row groups per workgroup (4 for the wide gate/up projection, else 2: reuse of the activation
-// loads against enough workgroups) and the fewest K slices S that give at least kMinWg workgroups, each wave
-// keeping at most 8 chunks. Measured on MI355X for the 1.7B shapes: qkv R2 S2, o R2 S4, gate/up R4 S1, down R2 S4,
-// head R2 S2 were within 1% of the best of all (R, S).
+// Launch plan: R row groups per wave (2 from N = 8192 rows up, else 1), slices of CW 64-wide chunks (8, halved while
+// the grid has fewer than kMinWg workgroups), S = K / (64 CW) slices, NB row blocks of 4 R groups. Measured on the
+// 1.7B step (16 streams): slices of 16 chunks (96 KB of LDS, fewer slices) 7657 and a minimum of 96 workgroups 7958
+// against 7992 stream-frames/s.
 constexpr int kMinWg = 192;
-struct Plan { int R, S; };
+struct Plan { int R, CW, S, NB; };
 Plan plan(int N, int K) {
-  Plan pl{N % 64 == 0 && N >= 8192 ? 4 : N % 32 == 0 ? 2 : 1, 1};
-  const int tiles = N / (16 * pl.R);
-  auto cw_ok = [&](int S) {
-    if (K % (256 * S)) return false;
-    const int cw = K / (256 * S);
-    return (cw == 1 || cw == 2 || cw == 3 || cw == 4 || cw == 6 || cw == 8) && pl.R * cw <= 32;
-  };
-  auto splittable = [&](int S) { return K % (256 * S) == 0; };
-  while (pl.S < 64 && (!cw_ok(pl.S) || (tiles * pl.S < kMinWg && splittable(pl.S * 2) && cw_ok(pl.S * 2)))) pl.S *= 2;
+  Plan pl;
+  pl.R = N >= 8192 ? 2 : 1;
+  pl.NB = (N / 16 + 4 * pl.R - 1) / (4 * pl.R);
+  pl.CW = 8;
+  while (pl.CW > 2 && (K % (64 * pl.CW) != 0 ||
+                       (pl.NB * (K / (64 * pl.CW)) < kMinWg && K / (32 * pl.CW) <= kMaxSlices)))
+    pl.CW /= 2;
+  pl.S = K / (64 * pl.CW);
   return pl;
 }
 int64_t part_floats(int N, int K) {
   const Plan pl = plan(N, K);
   return pl.S > 1 ? (int64_t)pl.S * (N / 16) * 256 : 0;
 }
+template <int OUT, int R>
+hipError_t launch_cw(const GemmArgs& p, const Plan& pl, hipStream_t st) {
+  const dim3 grid(pl.NB, pl.S);
+  switch (pl.CW) {
+    case 2: hipLaunchKernelGGL((k_bgemm<OUT, R, 2>), grid, dim3(kThreads), 0, st, p); break;
+    case 4: hipLaunchKernelGGL((k_bgemm<OUT, R, 4>), grid, dim3(kThreads), 0, st, p); break;
+    case 8: hipLaunchKernelGGL((k_bgemm<OUT, R, 8>), grid, dim3(kThreads), 0, st, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+bool k_supported(int K) { return K == 512 || K == 1024 || K == 2048 || K == 3072 || K == 4096 || K == 6144; }
 
 hipError_t launch_gemm(GemmArgs p, int mode, hipStream_t st) {
   const Plan pl = plan(p.N, p.K);
   p.S = pl.S;
-  if (mode == kOutF32)
-    return pl.R == 4 ? launch_cw<kOutF32, 4>(p, st) : pl.R == 2 ? launch_cw<kOutF32, 2>(p, st) : launch_cw<kOutF32, 1>(p, st);
-  if (mode == kOutSwiglu)
-    return pl.R == 4 ? launch_cw<kOutSwiglu, 4>(p, st) : pl.R == 2 ? launch_cw<kOutSwiglu, 2>(p, st)
-                                                               : launch_cw<kOutSwiglu, 1>(p, st);
-  return pl.R == 4 ? launch_cw<kOutAcc, 4>(p, st) : pl.R == 2 ? launch_cw<kOutAcc, 2>(p, st) : launch_cw<kOutAcc, 1>(p, st);
+  if (mode == kOutF32) return pl.R == 2 ? launch_cw<kOutF32, 2>(p, pl, st) : launch_cw<kOutF32, 1>(p, pl, st);
+  if (mode == kOutSwiglu) return pl.R == 2 ? launch_cw<kOutSwiglu, 2>(p, pl, st) : launch_cw<kOutSwiglu, 1>(p, pl, st);
+  return pl.R == 2 ? launch_cw<kOutAcc, 2>(p, pl, st) : launch_cw<kOutAcc, 1>(p, pl, st);
 }
 
 int check_gemm(const GemmArgs& p, int mode) {
