@@ -200,7 +200,7 @@ int64_t sk_talker_workspace_size(int hidden, int inter);
  * device exactly as the fused sampler advances it (id0, next_id0, seen, ngen, pos += 1 per frame).
  * 256 persistent workgroups (one per CU, grouped by XCD: kv head x on XCD x) exchange activations through the
  * workspace. Supports the 0.6B (H 1024, I 3072) and 1.7B (H 2048, I 6144) talkers: 16 q / 8 kv heads, vocab
- * 3072, i8row or i8g32 weights (and bf16 at H 1024; head_s may then be null), bf16 cache, max_len <= 2048, a
+ * 3072, i8row, i8g32 or bf16 weights (head_s may be null for bf16), bf16 cache, max_len <= 2048, a
  * 256-CU device.
  * Replaces, for greedy decoding, the talker half of Qwen3Kernels._frame (qwen3/kernels.py:676-685): talker_in /
  * embed, _layers (rms_gemv, attn, gemv, rms_gemv, gemv per layer, qwen3/kernels.py:619-627), rmsnorm, gemv

@@ -12,9 +12,9 @@ extern "C" int64_t sk_talker_workspace_size(int hidden, int inter) {
 extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* stream) {
   if (!d || n_frames <= 0) return sk_set_error(SK_EINVAL, "sk_talker_frames: bad arguments");
   if (d->nq != kNQ || d->nkv != kNKV || d->vocab != kTalkerV || d->ct != SK_CT_BF16 ||
-      !(d->wd == SK_WD_I8ROW || d->wd == SK_WD_I8G32 || (d->wd == SK_WD_BF16 && d->hidden == 1024)))
-    return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs 16 q / 8 kv heads, vocab 3072, bf16 cache and i8row "
-                                         "or i8g32 weights (or bf16 weights at hidden 1024)");
+      !(d->wd == SK_WD_I8ROW || d->wd == SK_WD_I8G32 || d->wd == SK_WD_BF16))
+    return sk_set_error(SK_EUNSUPPORTED, "sk_talker_frames: needs 16 q / 8 kv heads, vocab 3072, bf16 cache and i8row, "
+                                         "i8g32 or bf16 weights");
   if (!d->layers || !d->norm || !d->head_w || (!d->head_s && d->wd != SK_WD_BF16) || !d->emb || !d->rope || !d->id0 ||
       !d->pos || !d->workspace)
     return sk_set_error(SK_EINVAL, "sk_talker_frames: null pointer");

@@ -10,7 +10,7 @@
 // with a vector address per access the waves spilled ~140 addresses and reloaded them from scratch on every
 // exchange; with the shared offsets nothing spills. Measured on the 64-frame 1.7B workload: 25.3 us per layer,
 // against 38.8 us for 8 compute waves with polls staged through LDS (the 168-register budget of 9 waves) and 69 us
-// for 8 compute waves with register polls (SOKUTOU_TALKER_POLL=regs, frame.hip).
+// for 8 compute waves with register polls (instantiations since deleted).
 #include "frame_impl.h"
 
 namespace {
@@ -35,5 +35,6 @@ static_assert(Cfg<kH, kI, 4, kTalkerV, false>::kMaxLen >= 2048, "1.7B caches up 
 int sk_talker_frames_2048(const sk_talker_desc* d, int n_frames, hipStream_t st) {
   const CpArgs none{};
   if (d->wd == SK_WD_I8G32) return sk_talker_frames_2048_g32(d, n_frames, st);
+  if (d->wd == SK_WD_BF16) return sk_talker_frames_2048_bf16(d, n_frames, st);
   return launch_frames<kH, kI, 4, kTalkerV, false>(d, none, n_frames, st);
 }

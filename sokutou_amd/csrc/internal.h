@@ -14,6 +14,8 @@ int sk_talker_frames_2048(const sk_talker_desc* d, int n_frames, hipStream_t st)
 int sk_talker_frames_g32(const sk_talker_desc* d, int n_frames, hipStream_t st);
 // The 1.7B shape's i8g32 kernel (frame17_g32.hip), called by sk_talker_frames_2048.
 int sk_talker_frames_2048_g32(const sk_talker_desc* d, int n_frames, hipStream_t st);
+// The 1.7B shape's bf16 kernel (frame17_bf16.hip), called by sk_talker_frames_2048.
+int sk_talker_frames_2048_bf16(const sk_talker_desc* d, int n_frames, hipStream_t st);
 // The 0.6B talker shape with bf16 weights (frame_bf16.hip), called by sk_talker_frames.
 int sk_talker_frames_bf16(const sk_talker_desc* d, int n_frames, hipStream_t st);
 // sk_cp_frame with i8g32 or bf16 weights (frame_cp_g32.hip, frame_cp_bf16.hip; the arguments already checked by

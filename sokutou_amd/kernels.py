@@ -421,7 +421,7 @@ class Qwen3Kernels(Qwen3Fast):
         supported = (self.frame_kernel_supported() and sampler == "fused"
                      and (self.cp is None or self.cpk is not None))
         if frame_kernel and not supported:
-            raise ValueError("frame_kernel=True needs the fused sampler, i8row weights (or i8g32 at hidden 1024), "
+            raise ValueError("frame_kernel=True needs the fused sampler, i8row, i8g32 or bf16 weights, "
                              "16 q / 8 kv heads, vocab 3072, "
                              "hidden 1024 or 2048, a cache of at most 1024 (0.6B) / 2048 (1.7B) positions and, with a "
                              "code predictor, its one-launch kernel (the 1024-wide code predictor, unprojected or "
@@ -527,11 +527,11 @@ class Qwen3Kernels(Qwen3Fast):
 
     # --- the persistent frame kernel ------------------------------------------------------------------------
     def frame_kernel_supported(self) -> bool:
-        """The persistent kernel covers the 0.6B and 1.7B talker shapes with i8row weights or the reference's i8g32,
-        and the 0.6B shape with bf16 weights (the reference's default format)."""
+        """The persistent kernel covers the 0.6B and 1.7B talker shapes with i8row weights, the reference's i8g32
+        or bf16 weights (the reference's default format)."""
         P = self.T
         shapes = {(1024, 3072): 1024, (2048, 6144): 2048}
-        wd_ok = self.wd in ("i8row", "i8g32") or (self.wd == "bf16" and P.H == 1024)
+        wd_ok = self.wd in ("i8row", "i8g32", "bf16")
         return (wd_ok and self.ct == "bf16" and P.nq == 16 and P.nkv == 8 and self.V == 3072
                 and (P.H, P.I) in shapes and self.max_cache <= shapes[(P.H, P.I)])
 

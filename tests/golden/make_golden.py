@@ -210,6 +210,7 @@ if __name__ == "__main__":
             "talker17b": lambda: talker("talker17b", 0), "cp06b": lambda: code_predictor("cp06b", 0),
             "cp06b_i8g32": lambda: code_predictor("cp06b", 0, "i8g32"),
             "talker06b_bf16": lambda: talker("talker06b", 0, "bf16"), "cp06b_bf16": lambda: code_predictor("cp06b", 0, "bf16"),
+            "talker17b_bf16": lambda: talker("talker17b", 0, "bf16"),
             "batch17b": lambda: batch("batch17b", 0),
             "cp17b": lambda: code_predictor("cp17b", 0), "cp17b_i8g32": lambda: code_predictor("cp17b", 0, "i8g32"),
             "cp17b_bf16": lambda: code_predictor("cp17b", 0, "bf16"),

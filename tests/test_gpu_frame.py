@@ -86,10 +86,11 @@ def test_talker06b_64_frames_one_launch(gpu):
     assert int(eng.pos.item()) == meta["start_pos"] + 64
 
 
-@pytest.mark.parametrize("name,seed,wd", [("talker06b", 0, "i8g32"), ("talker17b", 1, "i8g32"), ("talker06b", 0, "bf16")])
+@pytest.mark.parametrize("name,seed,wd", [("talker06b", 0, "i8g32"), ("talker17b", 1, "i8g32"), ("talker06b", 0, "bf16"),
+                                         ("talker17b", 0, "bf16")])
 def test_talker_other_formats_64_frames_one_launch(gpu, name, seed, wd):
     """The reference's i8g32 weights (fp16 scale per 32 weights, applied per 16-weight chunk) and its bf16 default
-    (0.6B shape) on the persistent kernel: per-layer residuals and logits of frame 0, then 63 frames in one launch,
+    (both shapes) on the persistent kernel: per-layer residuals and logits of frame 0, then 63 frames in one launch,
     against the oracle of the same format. The 1.7B i8g32 fixture uses seed 1 (seed 0 has a top-2 logit margin of
     2e-5 at one frame)."""
     print(f"{name} {wd} seed {seed}: frame 0 with residuals, then 63 frames in one launch", flush=True)
