@@ -2575,14 +2575,24 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     constexpr uint8_t kDefaultSpread06[Ws::kHops] = {49, 15, 60, 31, 59, 52, 4, 46};
     constexpr uint8_t kDefaultCp[Ws::kHops] = {18, 14, 43, 25, 19, 30, 17, 25};
     constexpr uint8_t kDefaultCpBf16[Ws::kHops] = {30, 10, 43, 21, 31, 30, 5, 29};  // 1105 -> 1071 us per frame
+    // the 1.7B talker with bf16 weights: 1010 -> 945 us per frame (the merge poll needs 70 units or more here)
+    constexpr uint8_t kDefaultSpread17Bf16[Ws::kHops] = {66, 44, 128, 56, 8, 0, 18, 64};
+    // the projected (1.7B) code predictor, unpaired: 991 -> 956 us per frame (i8g32 964 on the same set), and with
+    // bf16 weights 1137 -> 1091 on a set of its own
+    constexpr uint8_t kDefaultCpProj[Ws::kHops] = {14, 10, 22, 56, 20, 26, 20, 20};
+    constexpr uint8_t kDefaultCpProjBf16[Ws::kHops] = {14, 14, 22, 58, 28, 30, 16, 28};
+    constexpr bool kProj = CP && CpProjIn<H, I>::value > 0;
     const uint32_t w0 = s_dl[0], w1 = s_dl[1];
 #pragma unroll
     for (int h = 0; h < Ws::kHops; h++) {
       const uint32_t v = ((h < 4 ? w0 : w1) >> (8 * (h & 3))) & 0xffu;
       c.dl[h] = v ? (uint8_t)(v - 1)
-                  : CP ? (WD == SK_WD_BF16 ? kDefaultCpBf16[h] : kDefaultCp[h])
-                       : (CfgW<H, I, W, V, CP, WD>::kSpread ? (H == 1024 ? kDefaultSpread06[h] : kDefaultSpread[h])
-                                                            : kDefault[h]);
+                  : CP ? (kProj ? (WD == SK_WD_BF16 ? kDefaultCpProjBf16[h] : kDefaultCpProj[h])
+                                : (WD == SK_WD_BF16 ? kDefaultCpBf16[h] : kDefaultCp[h]))
+                       : (CfgW<H, I, W, V, CP, WD>::kSpread
+                              ? (H == 1024 ? kDefaultSpread06[h]
+                                           : (WD == SK_WD_BF16 ? kDefaultSpread17Bf16[h] : kDefaultSpread[h]))
+                              : kDefault[h]);
     }
   }
   c.trace = s_trace ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
