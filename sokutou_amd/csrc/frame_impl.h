@@ -220,13 +220,17 @@ struct CfgW : Cfg<H, I, W, V, CP> {
   static constexpr bool kSpread = B::kSpread || WD == SK_WD_BF16;
 };
 
+// floats of a GEMV staging buffer for n elements (n a multiple of 64): one 8-byte slot of padding after every 32
+// (xsw, below)
+constexpr int xs_floats(int n) { return n + n / 32; }
+
 // LDS of the frame kernel
 template <int H, int I, int W, int V, bool CP>
 struct Lds {
   static constexpr int XS = I > kQ ? I : kQ;
   float hin[H];        // residual entering the layer (S1; read back by S4), or the final residual (head)
   float hmid[H];       // residual after the o projection (S5; read back by S6)
-  float xs[2][XS];     // staged GEMV inputs, alternating so the control wave can fill the next stage's input
+  float xs[2][xs_floats(XS)];  // staged GEMV inputs (xsw), alternating so the control wave can fill the next stage's input
                        // while the compute waves still read the current one: [0] S1/S5/head, [1] S4/S6
   float qkv[512];      // S2: q0 | q1 | k | v of this workgroup's head
   float qs[2][SK_HD];  // normalised, rotated, scaled q
@@ -250,7 +254,7 @@ template <int H, int I>
 struct LdsPair {
   static constexpr int XS = I > kQ ? I : kQ;
   float hin[H], hmid[H];
-  float xs[2][XS];
+  float xs[2][xs_floats(XS)];
   float qkv[512];
   float qs[2][SK_HD];
   float kn[SK_HD], vn[SK_HD];
@@ -284,13 +288,23 @@ __host__ __device__ inline uint32_t proj_cells(int H, int I) { return PairLayout
 struct Ctx;
 __device__ void fail(const Ctx& c, uint32_t code, int f, int l);
 
-// GEMV inputs are staged in LDS swizzled: element i = 16 (L + 64 c) + 4 j + t, which lane L multiplies with byte
-// 4 j + t of its weight chunk c, sits at 16-byte slot (4 c + j) * 64 + L, word t (the natural order puts the lanes
-// of a read 64 bytes apart). The dot reads each slot as two 8-byte halves; measured on the frame kernel this is
-// faster than both 16-byte reads of the same slots and a layout of separate 8-byte slots.
-__device__ __forceinline__ int xsw(int i) {
-  return ((((i >> 10) << 2) | ((i >> 2) & 3)) << 8) | (((i >> 4) & 63) << 2) | (i & 3);
-}
+// GEMV inputs are staged in LDS in 8-byte slots, one per element pair. Lane L of a dot multiplies byte 4 j + t of
+// its weight chunk c with element 16 (L + 64 c) + 4 j + t, and reads those 4 elements as the pairs
+// P = 8 (L + 64 c) + 2 j + h (h = 0, 1) with two 8-byte reads; the control wave stages the pairs P = L + 64 b. Pair P
+// sits in slot P + P / 32 (one slot of padding after every 32): across the 32 lanes of a half-wave both patterns then
+// reach 32 different bank pairs (unpadded, the dot's reads fell 64 bytes apart, two lanes per bank pair, and the
+// staging writes four; SQ_LDS_BANK_CONFLICT on the 0.6B talker: 9.1e8 cycles per launch unpadded, 6.7e8 padded;
+// the frame rate is the same, the conflicts were off the critical path), and each lane's slot stays its own base
+// plus a compile-time offset (a XOR swizzle, also conflict-free, made the offsets per lane and spilled 9-35
+// registers). A vector staged at an
+// element offset that is a multiple of 64 starts at xsw(offset). 8-byte rather than 16-byte reads: 16-byte LDS
+// reads of the same data stall the LDS on gfx950 (SQ_LDS_UNALIGNED_STALL; 2250 against 820 cycles per stage).
+__device__ __forceinline__ int xslot(int P) { return P + (P >> 5); }
+// float index of element i (i even: i + 1 lands at xsw(i) + 1)
+__device__ __forceinline__ int xsw(int i) { return 2 * xslot(i >> 1) + (i & 1); }
+// 8-byte slot of the dot's read h of quarter q = 4 c + j (chunk c, bytes 4 j .. 4 j + 3) for lane L < 64: xslot of
+// pair 8 (L + 64 c) + 2 j + h, written as the lane's base and an offset (2 j + h < 8 keeps (8 L + 2 j + h) / 32 at L / 4)
+__device__ __forceinline__ int xq(int lane, int q, int h) { return 8 * lane + (lane >> 2) + 528 * (q >> 2) + 2 * (q & 3) + h; }
 
 // Loads per lane in one polling round: at most 16 (64 registers of the control wave).
 constexpr int mb(int n) { return n / 128 < 16 ? n / 128 : 16; }
@@ -448,7 +462,7 @@ __device__ __forceinline__ void dot_rows(const uint4 (&w)[RW][C], const float* x
     for (int j = 0; j < 4; j++) {  // one quarter of the chunk (4 bytes per row) at a time: 4 live x registers
       // two 8-byte LDS reads: 16-byte LDS reads stall the LDS on gfx950 (SQ_LDS_UNALIGNED_STALL; measured
       // 2250 against 820 cycles for the same 8 KB)
-      const float2 u0 = xs2[2 * ((4 * c + j) * 64 + lane)], u1 = xs2[2 * ((4 * c + j) * 64 + lane) + 1];
+      const float2 u0 = xs2[xq(lane, 4 * c + j, 0)], u1 = xs2[xq(lane, 4 * c + j, 1)];
       const float4 v = make_float4(u0.x, u0.y, u1.x, u1.y);
 #pragma unroll
       for (int r = 0; r < RW; r++) {
@@ -477,13 +491,13 @@ __device__ __forceinline__ void dot_rows2(const uint4 (&w)[RW][C], const float* 
   for (int r = 0; r < RW; r++) { aa[r] = 0.f; ab[r] = 0.f; }
   const float2* xa2 = (const float2*)xa;
   const float2* xb2 = (const float2*)xb;
-  float2 na0 = xa2[2 * lane], na1 = xa2[2 * lane + 1], nb0 = xb2[2 * lane], nb1 = xb2[2 * lane + 1];
+  float2 na0 = xa2[xq(lane, 0, 0)], na1 = xa2[xq(lane, 0, 1)], nb0 = xb2[xq(lane, 0, 0)], nb1 = xb2[xq(lane, 0, 1)];
 #pragma unroll
   for (int t = 0; t < 4 * C; t++) {  // quarter t: chunk t / 4, bytes 4 (t % 4) .. + 3 of each row's chunk
     const float2 a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
     if (t + 1 < 4 * C) {
-      const int k = 2 * ((t + 1) * 64 + lane);
-      na0 = xa2[k]; na1 = xa2[k + 1]; nb0 = xb2[k]; nb1 = xb2[k + 1];
+      const int k0 = xq(lane, t + 1, 0), k1 = xq(lane, t + 1, 1);
+      na0 = xa2[k0]; na1 = xa2[k1]; nb0 = xb2[k0]; nb1 = xb2[k1];
     }
     const int c = t >> 2, j = t & 3;
 #pragma unroll
@@ -553,7 +567,7 @@ __device__ __forceinline__ void dot_rows_g32(const uint4 (&w)[RW][C], const uint
     for (int r = 0; r < RW; r++) part[r] = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const float2 u0 = xs2[2 * ((4 * c + j) * 64 + lane)], u1 = xs2[2 * ((4 * c + j) * 64 + lane) + 1];
+      const float2 u0 = xs2[xq(lane, 4 * c + j, 0)], u1 = xs2[xq(lane, 4 * c + j, 1)];
       const float4 v = make_float4(u0.x, u0.y, u1.x, u1.y);
 #pragma unroll
       for (int r = 0; r < RW; r++) {
@@ -612,7 +626,7 @@ __device__ __forceinline__ void dot_rows_bf16(const uint4 (&w)[RW][C2], const fl
   for (int c = 0; c < C2 / 2; c++) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {  // weights 4 j .. 4 j + 3 of the chunk
-      const float2 u0 = xs2[2 * ((4 * c + j) * 64 + lane)], u1 = xs2[2 * ((4 * c + j) * 64 + lane) + 1];
+      const float2 u0 = xs2[xq(lane, 4 * c + j, 0)], u1 = xs2[xq(lane, 4 * c + j, 1)];
 #pragma unroll
       for (int r = 0; r < RW; r++) {
         const uint4 hq = w[r][2 * c + (j >> 1)];
@@ -638,13 +652,13 @@ __device__ __forceinline__ void dot_rows2_bf16(const uint4 (&w)[RW][C2], const f
   const float2* xa2 = (const float2*)xa;
   const float2* xb2 = (const float2*)xb;
   constexpr int Q = 4 * (C2 / 2);  // quarter chunks
-  float2 na0 = xa2[2 * lane], na1 = xa2[2 * lane + 1], nb0 = xb2[2 * lane], nb1 = xb2[2 * lane + 1];
+  float2 na0 = xa2[xq(lane, 0, 0)], na1 = xa2[xq(lane, 0, 1)], nb0 = xb2[xq(lane, 0, 0)], nb1 = xb2[xq(lane, 0, 1)];
 #pragma unroll
   for (int t = 0; t < Q; t++) {
     const float2 a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
     if (t + 1 < Q) {
-      const int k = 2 * ((t + 1) * 64 + lane);
-      na0 = xa2[k]; na1 = xa2[k + 1]; nb0 = xb2[k]; nb1 = xb2[k + 1];
+      const int k0 = xq(lane, t + 1, 0), k1 = xq(lane, t + 1, 1);
+      na0 = xa2[k0]; na1 = xa2[k1]; nb0 = xb2[k0]; nb1 = xb2[k1];
     }
     const int c = t >> 2, j = t & 3;
 #pragma unroll
@@ -694,13 +708,13 @@ __device__ __forceinline__ void dot_rows2_g32(const uint4 (&w)[RW][C], const uin
   for (int r = 0; r < RW; r++) { aa[r] = 0.f; ab[r] = 0.f; pa[r] = 0.f; pb[r] = 0.f; }
   const float2* xa2 = (const float2*)xa;
   const float2* xb2 = (const float2*)xb;
-  float2 na0 = xa2[2 * lane], na1 = xa2[2 * lane + 1], nb0 = xb2[2 * lane], nb1 = xb2[2 * lane + 1];
+  float2 na0 = xa2[xq(lane, 0, 0)], na1 = xa2[xq(lane, 0, 1)], nb0 = xb2[xq(lane, 0, 0)], nb1 = xb2[xq(lane, 0, 1)];
 #pragma unroll
   for (int t = 0; t < 4 * C; t++) {  // quarter t: chunk t / 4, bytes 4 (t % 4) .. + 3 of each row's chunk
     const float2 a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
     if (t + 1 < 4 * C) {
-      const int k = 2 * ((t + 1) * 64 + lane);
-      na0 = xa2[k]; na1 = xa2[k + 1]; nb0 = xb2[k]; nb1 = xb2[k + 1];
+      const int k0 = xq(lane, t + 1, 0), k1 = xq(lane, t + 1, 1);
+      na0 = xa2[k0]; na1 = xa2[k1]; nb0 = xb2[k0]; nb1 = xb2[k1];
     }
     const int c = t >> 2, j = t & 3;
 #pragma unroll
@@ -1960,10 +1974,10 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
           put(c.cells, PL.b3 + (2 * x + p) * SK_HD + dd, ob, c.tick(f, l, 2));
         }
       }
-      if (cw < kQ / 1024) {  // the second row's S4 input, 1024 cells per wave (swizzle blocks are 1024 long)
+      if (cw < kQ / 1024) {  // the second row's S4 input, 1024 cells per wave (staged from element 1024 cw)
         sleep_units(c.dl[Ws::kHopS4]);
         const bool ok = poll_cells<mb(1024), true, kLO>(c.cells, PL.b3 + 1024u * cw, 1024, c.tick(f, l, 2),
-                                                        P.xs[1] + 1024 * cw, c.ws, lane, c, 14u, f, l);
+                                                        P.xs[1] + xsw(1024 * cw), c.ws, lane, c, 14u, f, l);
         if (!ok && lane == 0) P.bad = 1;
       }
       load_attn_vec(Ln);
@@ -2013,7 +2027,7 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
       if (cw < I / 1024) {  // the second row's S6 input, 1024 cells per wave
         sleep_units(c.dl[Ws::kHopS6]);
         const bool ok = poll_cells<mb(1024), true, kLO>(c.cells, PL.b5 + 1024u * cw, 1024, c.tick(f, l, 4),
-                                                        P.xs[1] + 1024 * cw, c.ws, lane, c, 16u, f, l);
+                                                        P.xs[1] + xsw(1024 * cw), c.ws, lane, c, 16u, f, l);
         if (!ok && lane == 0) P.bad = 1;
       }
       load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
