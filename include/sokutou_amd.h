@@ -195,6 +195,16 @@ typedef struct sk_talker_desc {
  * after a call that reported an error (its first 4 bytes hold the error code, 0 when healthy). */
 int64_t sk_talker_workspace_size(int hidden, int inter);
 
+/* Places the exchange cells of a zeroed sk_talker_frames / sk_cp_frame workspace: measures which 4 KB page of each
+ * 32 KB period of the workspace's cell region is nearest each XCD (every XCD reads its own copy of the cells, on its
+ * nearest page) and records the result in the workspace, where every later launch reads it. One launch of 256
+ * one-wave workgroups, about 0.3 ms, stream-ordered; call it after each zeroing of the workspace, outside graph
+ * capture, with no frame launch on the same workspace in flight. Without it (or when the measurement is not
+ * consistent across the region) the launches use a fixed placement: the same results, slower exchanges. No
+ * counterpart in the reference, whose kernels exchange nothing between launches (its per-op launches,
+ * qwen3/kernels.py:619-627, pass activations through global memory at kernel boundaries). */
+int sk_frames_place(void* workspace, int64_t workspace_bytes, void* stream);
+
 /* n_frames greedy talker frames in ONE launch: for each frame, embedding row of id0 -> n_layers decoder layers
  * -> final RMSNorm -> codec head -> (processor) -> argmax -> next id, with the frame state advanced on the
  * device exactly as the fused sampler advances it (id0, next_id0, seen, ngen, pos += 1 per frame).
@@ -257,8 +267,8 @@ typedef struct sk_cp_desc {
   const float* proj_b;
 } sk_cp_desc;
 
-/* Bytes of workspace sk_cp_frame needs: sk_talker_workspace_size plus the cells of a projected input and, for
- * pair = 1, the second row's cells. */
+/* Bytes of workspace sk_cp_frame needs: sk_talker_workspace_size(hidden, inter), whose cell region also holds the
+ * cells of a projected input and, for pair = 1, the second row's. sk_frames_place serves it too. */
 int64_t sk_cp_workspace_size(int hidden, int inter, int pair);
 
 /* All positions of the code predictor of one frame in ONE launch, or two with desc->pair (the paired pass of

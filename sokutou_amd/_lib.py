@@ -95,6 +95,7 @@ _SIGS["sk_talker_workspace_size"] = (c_int64, [c_int, c_int])
 _SIGS["sk_talker_frames"] = (c_int, [ctypes.POINTER(SkTalkerDesc), c_int, _P])
 _SIGS["sk_cp_frame"] = (c_int, [ctypes.POINTER(SkCpDesc), _P])
 _SIGS["sk_cp_workspace_size"] = (c_int64, [c_int, c_int, c_int])
+_SIGS["sk_frames_place"] = (c_int, [_P, c_int64, _P])
 
 _lib = None
 

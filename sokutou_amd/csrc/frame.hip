@@ -5,8 +5,9 @@
 
 extern "C" int64_t sk_talker_workspace_size(int hidden, int inter) {
   if (hidden <= 0 || inter <= 0) return 0;
-  const Layout LY(hidden, inter);
-  return (int64_t)Ws::kCells + (int64_t)LY.total * 8 + (int64_t)kWG * 2 * Ws::kTraceLayers * Ws::kTraceEvents * 8;
+  // control words, trace stamps, then the 2 MB cell region at the first 2 MB boundary after them
+  if (Layout(hidden, inter).talker_end > kRegionCells) return 0;
+  return Ws::kBytes;
 }
 
 extern "C" int sk_talker_frames(const sk_talker_desc* d, int n_frames, void* stream) {

@@ -7,10 +7,9 @@
 
 extern "C" int64_t sk_cp_workspace_size(int hidden, int inter, int pair) {
   if (hidden <= 0 || inter <= 0) return 0;
-  (void)pair;  // the paired pass's cells lie below the projected input's, which every code predictor may use
-  const int64_t base = sk_talker_workspace_size(hidden, inter);
-  const int64_t cells = (int64_t)Ws::kCells + ((int64_t)proj_cells(hidden, inter) + hidden) * 8;
-  return cells > base ? cells : base;
+  (void)pair;  // the paired pass's and the projected input's cells are in the region whether used or not
+  if (Layout(hidden, inter).total > kRegionCells) return 0;
+  return Ws::kBytes;
 }
 
 extern "C" int sk_cp_frame(const sk_cp_desc* d, void* stream) {

@@ -42,7 +42,6 @@ namespace {
 
 constexpr int kXcd = 8, kPerXcd = 32, kWG = kXcd * kPerXcd;
 constexpr int kChunks = kPerXcd;           // attention split of the cache length per head
-constexpr int kPartN = 4 + 2 * SK_HD;      // m0 l0 m1 l1 o0[128] o1[128]
 constexpr int kNQ = 16, kNKV = 8, kQKV = (kNQ + 2 * kNKV) * SK_HD, kQ = kNQ * SK_HD;
 constexpr int kTalkerV = 3072;             // talker codec vocabulary
 constexpr uint32_t kSpinLimit = 1u << 19;
@@ -60,32 +59,95 @@ __device__ __forceinline__ uint64_t lane_u64(uint64_t v, int i) {
 }
 
 // ---- exchange cells ------------------------------------------------------------------------------------------
-__device__ __forceinline__ void put(void* cells, uint32_t idx, float v, uint32_t e) {
+// The cells live in a 2 MB region of the workspace, aligned to 2 MB. Cell i of the index space (Layout) lies in
+// block i / 512 (512 cells, one 4 KB page); block b owns period b of the region (32 KB, 8 pages), and each XCD has a
+// copy of the block in one page of the period. Each 4 KB page of HBM is served from one place on the chip, about
+// 0.42 us of device-coherent store-to-load latency away from the XCD nearest to it and up to 0.69 us from the
+// farthest, and within a 512 KB quarter of the region the same page of every period is nearest the same XCD;
+// sk_frames_place measures which. XCD x reads its copy from its nearest page of each quarter (`slots`: 3 bits per
+// quarter), the producer of a cell that every XCD reads stores all eight pages of the period (the *_all stores),
+// and the cells of an exchange inside one XCD (q|k|v and the attention partials of its head pair) exist in that
+// XCD's page only, so local index ranges serve all eight XCDs at once.
+constexpr uint32_t kRegionBytes = 2u << 20, kRegionCells = 64u * 512u;  // 64 periods of 8 pages
+constexpr int kQuarters = 4;                                             // 16 periods each
+__host__ __device__ constexpr uint32_t cell_off(uint32_t i) { return ((i >> 9) << 15) | ((i & 511u) << 3); }
+// byte offset of cell i in the copy of the XCD whose page slots are `slots`
+__host__ __device__ constexpr uint32_t own_off(uint32_t slots, uint32_t i) {
+  return cell_off(i) | (((slots >> (3u * (i >> 13))) & 7u) << 12);
+}
+// byte offset of cell i of a range every XCD reads, in the kernels that keep one copy of it (SINGLE: the hidden-2048
+// i8g32 and bf16 kernels): block b in page b % 8 of its period, so an exchange's consecutive blocks lie in different
+// pages, as a plain array's would
+__host__ __device__ constexpr uint32_t single_off(uint32_t i) { return cell_off(i) | (((i >> 9) & 7u) << 12); }
+template <bool SINGLE>
+__host__ __device__ constexpr uint32_t read_off(uint32_t slots, uint32_t i) { return SINGLE ? single_off(i) : own_off(slots, i); }
+// the placement of a workspace no sk_frames_place call has measured: XCD x's copy in page x of every period
+__host__ __device__ constexpr uint32_t slots_identity(uint32_t x) { return x | x << 3 | x << 6 | x << 9; }
+
+// Accesses of this XCD's copy (`region` the cell region, `slots` this XCD's page slots).
+__device__ __forceinline__ void put(void* region, uint32_t slots, uint32_t idx, float v, uint32_t e) {
   u32x2 x = {__float_as_uint(v), e};
-  __builtin_amdgcn_raw_buffer_store_b64(x, make_rsrc(cells), idx * 8u, 0, kPolDev);
+  __builtin_amdgcn_raw_buffer_store_b64(x, make_rsrc(region), own_off(slots, idx), 0, kPolDev);
 }
-__device__ __forceinline__ void put2(void* cells, uint32_t idx, float v0, float v1, uint32_t e) {  // idx even
-  u32x4 x = {__float_as_uint(v0), e, __float_as_uint(v1), e};
-  __builtin_amdgcn_raw_buffer_store_b128(x, make_rsrc(cells), idx * 8u, 0, kPolDev);
+template <bool SINGLE = false>
+__device__ __forceinline__ u32x4 get2(const void* region, uint32_t slots, uint32_t idx) {  // cells idx, idx+1
+  return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(region), read_off<SINGLE>(slots, idx), 0, kPolDev);
 }
-__device__ __forceinline__ u32x4 get2(const void* cells, uint32_t idx) {  // cells idx, idx+1
-  return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(cells), idx * 8u, 0, kPolDev);
+// cells idx + 2 lane, + 1 with idx wave-uniform and a multiple of 128 (so the 128 cells lie in one block): the lane
+// part goes in the one vector offset every such load shares (16 lane bytes), the uniform part in the scalar offset,
+// so a poll of many loads holds one address register.
+template <bool SINGLE = false>
+__device__ __forceinline__ u32x4 get2l(const void* region, uint32_t slots, uint32_t idx, int lane) {
+  return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(region), (uint32_t)lane * 16u,
+                                               __builtin_amdgcn_readfirstlane(read_off<SINGLE>(slots, idx)), kPolDev);
 }
-// cells idx + 2 lane, + 1 with idx wave-uniform: the lane part goes in the one vector offset every such load shares
-// (16 lane bytes), the uniform part in the scalar offset, so a poll of many loads holds one address register.
-__device__ __forceinline__ u32x4 get2l(const void* cells, uint32_t idx, int lane) {
-  return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(cells), (uint32_t)lane * 16u,
-                                               __builtin_amdgcn_readfirstlane(idx * 8u), kPolDev);
+// The same cells with a vector address per load (the hidden-1024 kernels' polls).
+template <bool SINGLE = false>
+__device__ __forceinline__ u32x4 get2v(const void* region, uint32_t slots, uint32_t idx, int lane) {
+  return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(region), read_off<SINGLE>(slots, idx) + (uint32_t)lane * 16u, 0,
+                                               kPolDev);
 }
-// The stores of the same addressing: cells idx + 2 lane, + 1 (put2l); cell idx + vbytes / 8 (putl, vbytes per lane)
-__device__ __forceinline__ void put2l(void* cells, uint32_t idx, int lane, float v0, float v1, uint32_t e) {
-  u32x4 x = {__float_as_uint(v0), e, __float_as_uint(v1), e};
-  __builtin_amdgcn_raw_buffer_store_b128(x, make_rsrc(cells), (uint32_t)lane * 16u,
-                                         __builtin_amdgcn_readfirstlane(idx * 8u), kPolDev);
-}
-__device__ __forceinline__ void putl(void* cells, uint32_t idx, uint32_t vbytes, float v, uint32_t e) {
+// cell idx + vbytes / 8 (vbytes per lane) of this XCD's copy, with the cells of the wave inside idx's block
+__device__ __forceinline__ void putl(void* region, uint32_t slots, uint32_t idx, uint32_t vbytes, float v, uint32_t e) {
   u32x2 x = {__float_as_uint(v), e};
-  __builtin_amdgcn_raw_buffer_store_b64(x, make_rsrc(cells), vbytes, __builtin_amdgcn_readfirstlane(idx * 8u), kPolDev);
+  __builtin_amdgcn_raw_buffer_store_b64(x, make_rsrc(region), vbytes, __builtin_amdgcn_readfirstlane(own_off(slots, idx)),
+                                        kPolDev);
+}
+// Stores of a cell every XCD reads, into all eight pages of its period at vector offset vo (the cell's place in the
+// first page): one address register stepped by a page after each store (eight scalar page offsets, or eight vector
+// addresses formed up front, made the kernels spill more).
+template <class T>
+__device__ __forceinline__ void store_pages(void* region, uint32_t vo, const T& x) {
+#pragma unroll
+  for (int pg = 0; pg < 8; pg++) {
+    if constexpr (sizeof(T) == 16) __builtin_amdgcn_raw_buffer_store_b128(x, make_rsrc(region), vo, 0, kPolDev);
+    else __builtin_amdgcn_raw_buffer_store_b64(x, make_rsrc(region), vo, 0, kPolDev);
+    vo += 4096u;
+    __asm__ volatile("" : "+v"(vo));
+  }
+}
+// (SINGLE: the one copy)
+template <bool SINGLE = false>
+__device__ __forceinline__ void put_all(void* region, uint32_t idx, float v, uint32_t e) {
+  const u32x2 x = {__float_as_uint(v), e};
+  if constexpr (SINGLE) __builtin_amdgcn_raw_buffer_store_b64(x, make_rsrc(region), single_off(idx), 0, kPolDev);
+  else store_pages(region, cell_off(idx), x);
+}
+template <bool SINGLE = false>
+__device__ __forceinline__ void put2_all(void* region, uint32_t idx, float v0, float v1, uint32_t e) {
+  const u32x4 x = {__float_as_uint(v0), e, __float_as_uint(v1), e};
+  if constexpr (SINGLE) __builtin_amdgcn_raw_buffer_store_b128(x, make_rsrc(region), single_off(idx), 0, kPolDev);
+  else store_pages(region, cell_off(idx), x);
+}
+// Cells idx, idx + 1 (values wave-uniform) into all eight pages, lane k < 8 storing page k (SINGLE: lane 0, the one
+// copy).
+template <bool SINGLE = false>
+__device__ __forceinline__ void put2_lanes(void* region, uint32_t idx, float v0, float v1, uint32_t e, int lane) {
+  if (lane < (SINGLE ? 1 : 8)) {
+    u32x4 x = {__float_as_uint(v0), e, __float_as_uint(v1), e};
+    __builtin_amdgcn_raw_buffer_store_b128(x, make_rsrc(region), SINGLE ? single_off(idx) : ((uint32_t)lane << 12) + cell_off(idx),
+                                           0, kPolDev);
+  }
 }
 __device__ __forceinline__ uint32_t ld_u32_dev(const void* base, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(base), off, 0, kPolDev);
@@ -107,7 +169,10 @@ __device__ __forceinline__ void wg_sync() {
 struct Ws {
   // control words
   static constexpr uint32_t kErr = 0, kTick = 4, kLaunch = 8, kDiag = 16, kTraceOn = 32, kPollDelay = 40,
-                            kCensus = 64;  // census: 8 counters
+                            kPlace = 48, kCensus = 64;  // place: 4 words; census: 8 counters
+  // kPlace: the cell placement sk_frames_place measured, one word per quarter of the cell region (bits 0-23: the
+  // page slot of each XCD's copy, 3 bits per XCD; bit 31: set by a measurement); a quarter without a measurement
+  // uses the fixed placement, XCD x's copy in page x.
   // Polling of a stage's input starts this many sleep units (s_sleep 1: 64 shader clocks, ~27 ns at 2.4 GHz)
   // after the workgroup published its own part of it. Reads that reach the cells before the producers' stores
   // are visible come back stale and make the whole exchange slower than one late, successful read. One delay
@@ -115,24 +180,59 @@ struct Ws {
   // the defaults (value - 1) when non-zero.
   static constexpr int kHopS1 = 0, kHopS2 = 1, kHopS3 = 2, kHopS4 = 3, kHopS5 = 4, kHopS6 = 5, kHopHead = 6,
                        kHopPick = 7, kHops = 8;
+  // sk_frames_place's own words: arrivals per XCD [8], arrivals, its end barrier, the start time (8 bytes), a sink
+  static constexpr uint32_t kPlaceArrive = 96, kPlaceAll = 128, kPlaceEnd = 132, kPlaceT0 = 136, kPlaceSink = 144;
   static constexpr int kTraceLayers = 32, kTraceEvents = 16;  // optional per-stage timestamps of frame 0
-  static constexpr uint32_t kCells = 256;
+  // trace stamps [256 workgroups][2 roles][32 layers][16 events] of 8 bytes (sk_frames_place's latency table while
+  // it runs), then the cell region: the first 2 MB boundary at or after kRegionMin
+  static constexpr uint32_t kTrace = 256, kTraceBytes = (uint32_t)kWG * 2u * kTraceLayers * kTraceEvents * 8u;
+  static constexpr uint32_t kRegionMin = kTrace + kTraceBytes;
+  static constexpr int64_t kBytes = (int64_t)kRegionMin + 2 * (int64_t)kRegionBytes;
 };
+// the cell region of workspace ws
+__host__ __device__ inline char* cell_region(void* ws) {
+  return (char*)(((uintptr_t)ws + Ws::kRegionMin + kRegionBytes - 1) & ~(uintptr_t)(kRegionBytes - 1));
+}
 
+// The index space of the cells (Layout). Local ranges first (each XCD's own copy; every range starts on a block):
+//   e1  q|k|v of the XCD's head pair [512]
+//   e2m the attention partials' softmax statistics [32 chunks][m0 l0 m1 l1]
+//   e2o the partials' outputs [32 chunks][2 heads][128]
+//   b1  the code predictor's paired pass: the second row's q|k|v [512]
+// then the ranges every XCD reads (all copies written):
+//   e3 attention output [2048], e4 h after o [H], e5 activation [I], e6 h after down [H], e7 pick candidates
+//   [256][2] (greedy) or maxima [256] (sampled), e8 processed logits of a sampled pick [vocab <= 3072], and for the
+//   code predictor the paired pass's second row (b3 attention output, b4 h after o, b5 activation, b6 h after down)
+//   and the projected input pj [H]. The talker's kernels use the cells up to e8's end.
 struct Layout {
-  uint32_t e1, e2, e3, e4, e5, e6, e7, e8, total;  // cell offsets (in cells) from the cell base
-  __host__ __device__ Layout(int H, int I) {
-    e1 = 0;                                    // qkv        [8][512]
-    e2 = e1 + kNKV * 512;                      // partials   [8][32][260]
-    e3 = e2 + kNKV * kChunks * kPartN;         // att        [2048]
-    e4 = e3 + kQ;                              // h after o  [H]
-    e5 = e4 + H;                               // act        [I]
-    e6 = e5 + I;                               // h after down [H]
-    e7 = e6 + H;                               // candidates [256][2] (greedy), maxima [256] (sampled)
-    e8 = e7 + kWG * 2;                         // processed logits of a sampled pick [vocab <= 3072]
-    total = e8 + kTalkerV;
+  uint32_t e1 = 0, e2m = 0, e2o = 0, b1 = 0, e3 = 0, e4 = 0, e5 = 0, e6 = 0, e7 = 0, e8 = 0, b3 = 0, b4 = 0, b5 = 0,
+           b6 = 0, pj = 0, talker_end = 0, total = 0;
+  __host__ __device__ constexpr Layout(int H, int I) {
+    e1 = 0;
+    e2m = 512;
+    e2o = 1024;
+    b1 = e2o + (uint32_t)kChunks * 2u * SK_HD;
+    e3 = b1 + 512;
+    e4 = e3 + kQ;
+    e5 = e4 + H;
+    e6 = e5 + I;
+    e7 = e6 + H;
+    e8 = e7 + 512;
+    talker_end = e8 + kTalkerV;
+    b3 = talker_end;
+    b4 = b3 + kQ;
+    b5 = b4 + H;
+    b6 = b5 + I;
+    pj = b6 + H;
+    total = pj + H;
   }
 };
+// Every range starts on a block at the shapes built (H and I multiples of 512), the talker's cells fit the region
+// at both shapes, and the code predictor's (hidden 1024) too.
+static_assert(Layout(1024, 3072).total <= kRegionCells && Layout(2048, 6144).talker_end <= kRegionCells, "cells fit");
+static_assert(Layout(2048, 6144).e5 % 512 == 0 && Layout(1024, 3072).b6 % 512 == 0 && Layout(1024, 3072).e2o % 512 == 0,
+              "ranges start on a block");
+static_assert((uint32_t)kChunks * 4u <= 512u && (2u * SK_HD) * 2u == 512u, "two chunks' outputs per block");
 
 }  // namespace
 
@@ -218,6 +318,11 @@ struct CfgW : Cfg<H, I, W, V, CP> {
   static constexpr int CH = B::CH * WB, CQ = B::CQ * WB, CI = B::CI * WB;
   static constexpr bool kLate = B::kLate || WD == SK_WD_BF16;
   static constexpr bool kSpread = B::kSpread || WD == SK_WD_BF16;
+  // One copy of every cell that all XCDs read (single_off) instead of one per XCD: the hidden-2048 i8g32 and bf16
+  // kernels, whose registers are full (bf16 weights one exchange ahead). Their copies cost more than their nearer
+  // reads gained: 1004 against 943 us per frame (bf16) and 672 against 659 (i8g32) with eight copies, while the
+  // i8row kernel at that shape broke even (637) and the hidden-1024 ones gained 4-7%.
+  static constexpr bool kSingle = H > 1024 && WD != SK_WD_I8ROW;
 };
 
 // floats of a GEMV staging buffer for n elements (n a multiple of 64): one 8-byte slot of padding after every 32
@@ -267,22 +372,6 @@ struct LdsPair {
 template <int H, int I, int W, int V, bool CP>
 constexpr size_t kPickCopy = (sizeof(Lds<H, I, W, V, CP>) + 15) / 16 * 16;
 
-// Cells of the paired pass's second row, after the trace stamps of the workspace: q|k|v [8][512], attention output
-// [2048], h after o [H], activation [I], h after down [H] (the first row uses the regular regions).
-struct PairLayout {
-  uint32_t b1, b3, b4, b5, b6, total;
-  __host__ __device__ PairLayout(int H, int I) {
-    b1 = Layout(H, I).total + (uint32_t)kWG * 2u * Ws::kTraceLayers * Ws::kTraceEvents;
-    b3 = b1 + kNKV * 512;
-    b4 = b3 + kQ;
-    b5 = b4 + H;
-    b6 = b5 + I;
-    total = b6 + H;
-  }
-};
-
-// Cells of a projected code-predictor input [H], after the paired pass's cells.
-__host__ __device__ inline uint32_t proj_cells(int H, int I) { return PairLayout(H, I).total; }
 
 // Records a timeout: error code, then frame and layer of the stage that gave up (diagnostic words of the workspace).
 struct Ctx;
@@ -313,23 +402,20 @@ constexpr int mb(int n) { return n / 128 < 16 ? n / 128 : 16; }
 constexpr int mbh(int n) { return n / 128 < 24 ? n / 128 : 24; }
 
 // ---- control wave: poll cells into LDS ---------------------------------------------------------------------
-// Waits until cells [idx0, idx0 + n) (n even, idx0 even) all carry epoch e, copying the values to dst.
+// Waits until cells [idx0, idx0 + n) (idx0 and n multiples of 128) all carry epoch e, copying the values to dst.
 // Returns false on timeout or when the global error word is set.
-template <int MAXB, bool SW = false, bool LO = false>
-__device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, float* dst, void* ws, int lane,
-                           const Ctx& c, uint32_t code, int f, int l) {
+template <int MAXB, bool SW = false, bool LO = false, bool SINGLE = false>
+__device__ bool poll_cells(const void* region, uint32_t slots, uint32_t idx0, int n, uint32_t e, float* dst, void* ws,
+                           int lane, const Ctx& c, uint32_t code, int f, int l) {
   for (uint32_t spin = 0;; spin++) {
     bool ok = true;
     for (int base = 0; base < n; base += 128 * MAXB) {
       u32x4 q[MAXB];
 #pragma unroll
       for (int b = 0; b < MAXB; b++) {
-        if constexpr (LO) {  // n is a multiple of 128: the condition is wave-uniform
-          if (base + 128 * b < n) q[b] = get2l(cells, idx0 + (uint32_t)(base + 128 * b), lane);
-        } else {
-          const int i = base + 128 * b + 2 * lane;
-          if (i < n) q[b] = get2(cells, idx0 + i);
-        }
+        if (base + 128 * b < n)  // n is a multiple of 128: the condition is wave-uniform
+          q[b] = LO ? get2l<SINGLE>(region, slots, idx0 + (uint32_t)(base + 128 * b), lane)
+                    : get2v<SINGLE>(region, slots, idx0 + (uint32_t)(base + 128 * b), lane);
       }
 #pragma unroll
       for (int b = 0; b < MAXB; b++) {
@@ -355,17 +441,18 @@ __device__ bool poll_cells(const void* cells, uint32_t idx0, int n, uint32_t e, 
 }
 
 // ---- control wave: a whole vector into registers -----------------------------------------------------------
-// Waits until cells [idx0, idx0 + 128 NB) all carry epoch e. Lane holds cells 2 lane + 128 b and 2 lane + 128 b + 1
+// Waits until cells [idx0, idx0 + 128 NB) (idx0 a multiple of 128) all carry epoch e. Lane holds cells 2 lane + 128 b and 2 lane + 128 b + 1
 // in q[b].x and q[b].z; nothing goes through LDS here, the caller uses the values from registers (reading them
 // back from LDS would cost one LDS round trip per dependent read). Returns false on timeout or when the global
 // error word is set.
-template <int NB, bool LO = false>
-__device__ bool poll_regs(const void* cells, uint32_t idx0, uint32_t e, u32x4 (&q)[NB], void* ws, int lane,
-                          const Ctx& c, uint32_t code, int f, int l) {
+template <int NB, bool LO = false, bool SINGLE = false>
+__device__ bool poll_regs(const void* region, uint32_t slots, uint32_t idx0, uint32_t e, u32x4 (&q)[NB], void* ws,
+                          int lane, const Ctx& c, uint32_t code, int f, int l) {
   for (uint32_t spin = 0;; spin++) {
 #pragma unroll
     for (int b = 0; b < NB; b++)
-      q[b] = LO ? get2l(cells, idx0 + (uint32_t)(128 * b), lane) : get2(cells, idx0 + (uint32_t)(2 * lane + 128 * b));
+      q[b] = LO ? get2l<SINGLE>(region, slots, idx0 + (uint32_t)(128 * b), lane)
+                : get2v<SINGLE>(region, slots, idx0 + (uint32_t)(128 * b), lane);
     bool ok = true;
 #pragma unroll
     for (int b = 0; b < NB; b++) ok &= q[b].y == e && q[b].w == e;
@@ -758,36 +845,56 @@ __device__ __forceinline__ float row_scale_of(uint16_t s) {
 }
 
 // Publishes a stage's outputs. Every compute wave has left its values in S.pub (lane 0, before the call); the last
-// wave to arrive writes the workgroup's n cells [idx0, idx0 + n) (idx0 and n even) with 16-byte stores, so each
-// line of cells is written by one wave at one time (lines written piecewise by several waves reach the pollers
-// later). There is no barrier: the control wave may be polling the next stage's input meanwhile.
-template <int W, bool LO = false, class L>
-__device__ __forceinline__ void publish(L& S, void* cells, uint32_t idx0, int n, uint32_t e, int lane) {
+// wave to arrive writes the workgroup's n cells [idx0, idx0 + n) (idx0 and n even, n <= 64) with 16-byte stores,
+// so each line of cells is written by one wave at one time (lines written piecewise by several waves reach the
+// pollers later). ALL: cells every XCD reads, stored into all eight pages of their period, lane k storing pair
+// j0 + k / 8 into page k % 8 (one store instruction per 8 pairs; eight stores per lane, or pages by lane with a
+// division by the pair count, made the kernels spill more and run slower), or with SINGLE into their one copy;
+// otherwise this XCD's copy. There is no barrier: the control wave may be polling the next stage's input meanwhile.
+template <int W, bool ALL, bool SINGLE = false, class L>
+__device__ __forceinline__ void publish(L& S, void* region, uint32_t slots, uint32_t idx0, int n, uint32_t e, int lane) {
   uint32_t old = 0;
   if (lane == 0) old = __hip_atomic_fetch_add(&S.pubcnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
   old = __builtin_amdgcn_readfirstlane(old);
   if (old % W == W - 1) {
-    if constexpr (LO) {
-      for (int k = 0; 128 * k < n; k++)
-        if (2 * lane + 128 * k < n) put2l(cells, idx0 + 128u * k, lane, S.pub[2 * lane + 128 * k], S.pub[2 * lane + 128 * k + 1], e);
-    } else {
-      for (int i = 2 * lane; i < n; i += 128) put2(cells, idx0 + i, S.pub[i], S.pub[i + 1], e);
+    const int pieces = n / 2;
+    if constexpr (ALL && !SINGLE) {
+#pragma unroll
+      for (int j0 = 0; j0 < 32; j0 += 8) {  // lane: page lane % 8 of pair j0 + lane / 8
+        const int j = j0 + (lane >> 3);
+        if (j0 < pieces && j < pieces) {
+          const u32x4 v = {__float_as_uint(S.pub[2 * j]), e, __float_as_uint(S.pub[2 * j + 1]), e};
+          __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(region),
+                                                 ((uint32_t)(lane & 7) << 12) + cell_off(idx0 + 2u * (uint32_t)j), 0, kPolDev);
+        }
+      }
+    } else if (lane < pieces) {
+      const u32x4 v = {__float_as_uint(S.pub[2 * lane]), e, __float_as_uint(S.pub[2 * lane + 1]), e};
+      const uint32_t i = idx0 + 2u * (uint32_t)lane;
+      __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(region), ALL ? single_off(i) : own_off(slots, i), 0, kPolDev);
     }
     if (lane == 0) __hip_atomic_store(&S.pubseq, (old + 1) / W, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
 
-// publish for the paired pass: S.pub holds the first row's n values, then the second row's; the last wave to arrive
-// writes them to cells [idxA, idxA + n) and [idxB, idxB + n). One publication (one pubseq step) for both rows.
-template <int W, class L>
-__device__ __forceinline__ void publish_pair(L& S, void* cells, uint32_t idxA, uint32_t idxB, int n, uint32_t e, int lane) {
+// publish for the paired pass (the hidden-1024 code predictor): S.pub holds the first row's n values, then the second
+// row's; the last wave to arrive writes them to cells [idxA, idxA + n) and [idxB, idxB + n) (ALL as for publish, the
+// pages by lane). One publication (one pubseq step) for both rows.
+template <int W, bool ALL, class L>
+__device__ __forceinline__ void publish_pair(L& S, void* region, uint32_t slots, uint32_t idxA, uint32_t idxB, int n,
+                                             uint32_t e, int lane) {
   uint32_t old = 0;
   if (lane == 0) old = __hip_atomic_fetch_add(&S.pubcnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
   old = __builtin_amdgcn_readfirstlane(old);
   if (old % W == W - 1) {
-    for (int i = 2 * lane; i < n; i += 128) {
-      put2(cells, idxA + i, S.pub[i], S.pub[i + 1], e);
-      put2(cells, idxB + i, S.pub[n + i], S.pub[n + i + 1], e);
+    const int pieces = n / 2, per_row = (ALL ? 8 : 1) * pieces;
+    for (int k = lane; k < 2 * per_row; k += 64) {
+      const int row = k >= per_row ? 1 : 0, kr = k - row * per_row;
+      const int pg = kr / pieces, j = kr - pg * pieces;
+      const u32x4 v = {__float_as_uint(S.pub[row * n + 2 * j]), e, __float_as_uint(S.pub[row * n + 2 * j + 1]), e};
+      const uint32_t i = (row ? idxB : idxA) + 2u * (uint32_t)j;
+      __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(region), ALL ? ((uint32_t)pg << 12) + cell_off(i) : own_off(slots, i),
+                                             0, kPolDev);
     }
     if (lane == 0) __hip_atomic_store(&S.pubseq, (old + 1) / W, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
@@ -933,14 +1040,15 @@ __device__ __forceinline__ T* lds_at(uint32_t a) {  // an LDS pointer from an ld
 // maxima poll timed out. `tp` (null unless tracing) receives wall-clock stamps (tp[10..14]) and shader-clock stamps
 // (tp[0..4]) after the bound, the compaction, the ranks and draws, the fallback's kept compaction and the pick, and
 // lb and the counts of candidates and kept values (tp[5..7]).
-template <int V, int ROWS>
-__device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t vals_, uint32_t maxs_, int g_,
-                                                          uint32_t e_, uint32_t hv_, uint32_t cb_, uint32_t ci_,
-                                                          uint32_t ck_, uint32_t ps_, int top_k_, uint64_t draw_,
-                                                          uint64_t seed_, void* ws_, uint32_t delay_, int lane,
-                                                          uint64_t* tp_) {
+template <int V, int ROWS, bool SINGLE = false>
+__device__ __attribute__((noinline)) int64_t sampled_pick(char* region_, uint32_t slots_, uint32_t vals_,
+                                                          uint32_t maxs_, int g_, uint32_t e_, uint32_t hv_,
+                                                          uint32_t cb_, uint32_t ci_, uint32_t ck_, uint32_t ps_,
+                                                          int top_k_, uint64_t draw_, uint64_t seed_, void* ws_,
+                                                          uint32_t delay_, int lane, uint64_t* tp_) {
   static_assert(V % 512 == 0 && V == ROWS * kWG && ROWS % 2 == 0 && ROWS <= 16, "vocabulary of 256 x ROWS");
-  char* cells = uniform(cells_);
+  char* region = uniform(region_);
+  const uint32_t slots = __builtin_amdgcn_readfirstlane(slots_);
   void* ws = uniform(ws_);
   gptr<uint64_t> tp = (gptr<uint64_t>)uniform(tp_);
   const lds_f32* hv = lds_at<const lds_f32>(hv_);
@@ -964,15 +1072,29 @@ __device__ __attribute__((noinline)) int64_t sampled_pick(char* cells_, uint32_t
   // (1) publish the values, then this workgroup's largest key; poll the maxima; the bound
   const float own = lane < ROWS ? hv[lane] : -INFINITY;
   const uint32_t own_max = wave_max_u32(lane < ROWS ? order_key(own) : 0u);
-  if (lane < ROWS / 2) put2(cells, vals + (uint32_t)(ROWS * g + 2 * lane), hv[2 * lane], hv[2 * lane + 1], e);
-  if (lane == 0) put(cells, maxs + (uint32_t)g, __uint_as_float(own_max), e);
+  // the values into all eight pages: lane k < 4 ROWS stores pair k % (ROWS / 2) into page k / (ROWS / 2); the
+  // maximum: lane k < 8 into page k (SINGLE: the one copy, lanes k < ROWS / 2 and lane 0)
+  constexpr int kPages = SINGLE ? 1 : 8;
+  if (lane < kPages * (ROWS / 2)) {
+    const int pg = lane / (ROWS / 2), j = lane - pg * (ROWS / 2);
+    const u32x4 v = {__float_as_uint(hv[2 * j]), e, __float_as_uint(hv[2 * j + 1]), e};
+    const uint32_t i = vals + (uint32_t)(ROWS * g + 2 * j);
+    __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(region), SINGLE ? single_off(i) : ((uint32_t)pg << 12) + cell_off(i), 0,
+                                           kPolDev);
+  }
+  if (lane < kPages) {
+    const u32x2 v = {own_max, e};
+    const uint32_t i = maxs + (uint32_t)g;
+    __builtin_amdgcn_raw_buffer_store_b64(v, make_rsrc(region), SINGLE ? single_off(i) : ((uint32_t)lane << 12) + cell_off(i), 0,
+                                          kPolDev);
+  }
   if (lane == 0) ps->n = 0u;
   sleep_units(delay);
   int rc = 0;
   u32x4 mq[2];
   for (uint32_t spin = 0;; spin++) {
-    mq[0] = get2(cells, maxs + (uint32_t)(2 * lane));
-    mq[1] = get2(cells, maxs + (uint32_t)(128 + 2 * lane));
+    mq[0] = get2<SINGLE>(region, slots, maxs + (uint32_t)(2 * lane));
+    mq[1] = get2<SINGLE>(region, slots, maxs + (uint32_t)(128 + 2 * lane));
     if (__all(mq[0].y == e && mq[0].w == e && mq[1].y == e && mq[1].w == e)) break;
     if ((spin & 63) == 63) {
       if (ld_u32_dev(ws, Ws::kErr) != 0) { rc = -1; break; }
@@ -1230,7 +1352,8 @@ struct Ctx {
   sk_talker_desc d;
   CpArgs cp;
   void* ws;
-  char* cells;
+  char* region;    // the cell region
+  uint32_t slots;  // this XCD's page slot in each quarter of the region (3 bits per quarter)
   uint32_t x;     // XCD = kv head
   int r, g;       // rank in the XCD, global workgroup index
   uint32_t base, tpf;
@@ -1272,8 +1395,9 @@ __device__ void fail(const Ctx& c, uint32_t code, int f, int l) {
 // processed logits and the one that ends the pick; it passes the same three barriers as the control wave. Out of
 // line for the same reason as the control wave's part: inlined, its registers pushed the compute waves' layer loop
 // into spills (38 against 1 spilled VGPRs on the 0.6B talker).
-template <int V, int W>
-__device__ __attribute__((noinline)) void pick_compute(uint32_t cb_, uint32_t ci_, uint32_t ck_, uint32_t ps_, char* cells_,
+template <int V, int W, bool SINGLE = false>
+__device__ __attribute__((noinline)) void pick_compute(uint32_t cb_, uint32_t ci_, uint32_t ck_, uint32_t ps_,
+                                                       char* region_, uint32_t slots_,
                                                        void* ws_, uint32_t vals_, uint32_t e_, uint64_t draw_,
                                                        uint64_t seed_, int top_k_, uint32_t delay_, int f_, int L_,
                                                        int g_, int cw_, int lane, uint64_t* tp_) {
@@ -1284,7 +1408,8 @@ __device__ __attribute__((noinline)) void pick_compute(uint32_t cb_, uint32_t ci
   lds_u16* ci = lds_at<lds_u16>(ci_);
   lds_u32* ck = lds_at<lds_u32>(ck_);
   lds_pick* ps = lds_at<lds_pick>(ps_);
-  char* cells = uniform(cells_);
+  char* region = uniform(region_);
+  const uint32_t slots = __builtin_amdgcn_readfirstlane(slots_);
   void* ws = uniform(ws_);
   const uint32_t vals = __builtin_amdgcn_readfirstlane(vals_), e = __builtin_amdgcn_readfirstlane(e_);
   const uint32_t d0 = __builtin_amdgcn_readfirstlane((uint32_t)draw_), d1 = __builtin_amdgcn_readfirstlane((uint32_t)(draw_ >> 32));
@@ -1298,11 +1423,11 @@ __device__ __attribute__((noinline)) void pick_compute(uint32_t cb_, uint32_t ci
   const int b0 = NQ * cw;
   auto gather = [&]() {
 #pragma unroll
-    for (int b = 0; b < NQ; b++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(cells), (lds_void*)(cb + 64 * (b0 + b)), 16,
-                                               (uint32_t)lane * 16u,
-                                               __builtin_amdgcn_readfirstlane((vals + 128u * (uint32_t)(b0 + b)) * 8u),
-                                               0, kPolDev);
+    for (int b = 0; b < NQ; b++) {
+      const uint32_t so = __builtin_amdgcn_readfirstlane(read_off<SINGLE>(slots, vals + 128u * (uint32_t)(b0 + b)));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(region), (lds_void*)(cb + 64 * (b0 + b)), 16,
+                                               (uint32_t)lane * 16u, so, 0, kPolDev);
+    }
   };
   sleep_units(delay);
   gather();
@@ -1430,7 +1555,7 @@ __device__ __forceinline__ int attn_barriers(const Ck& ck) { return 1 + (ck.n > 
 // ================================================================================================================
 // Control wave of the code predictor's paired first pass (positions 0 and 1 as two rows per stage, the
 // reference's cp_pair: qwen3/kernels.py:276-310, 600-617). The control wave polls and stages the first row's inputs
-// as in a regular frame; the compute waves poll the second row's from PairLayout's cells at the same time (two
+// as in a regular frame; the compute waves poll the second row's from its own cells (b1, b3..b6) at the same time (two
 // polls in parallel instead of one after the other), and compute both rows' attention (two barriers). Returns
 // false when a poll of either row failed (P.bad, or the stage flags for the compute waves).
 template <int H, int I, int W, int V, bool CP>
@@ -1455,7 +1580,7 @@ __device__ __forceinline__ bool ctl_pair_pass(const Ctx& c, Lds<H, I, W, V, CP>&
       } else {
         after_publish(S, (uint32_t)l * 4u, c.dl[Ws::kHopS1]);
         u32x4 q[kNP];
-        ok = poll_regs<kNP, kLO>(c.cells, LY.e6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
+        ok = poll_regs<kNP, kLO>(c.region, c.slots, LY.e6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
         cells_to_pairs<kNP>(q, v);
       }
       ss = stage_rms<kNP>(v, w, S.hin, S.xs[0], lane);
@@ -1465,7 +1590,7 @@ __device__ __forceinline__ bool ctl_pair_pass(const Ctx& c, Lds<H, I, W, V, CP>&
     if (!ok || P.bad) return false;
     // S2 input: q|k|v of this workgroup's head
     after_publish(S, (uint32_t)l * 4u + 1u, c.dl[Ws::kHopS2]);
-    ok = poll_cells<mb(512), false, kLO>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
+    ok = poll_cells<mb(512), false, kLO>(c.region, c.slots, LY.e1, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
     if (lane == 0) S.flags[1] = !ok;
     wg_sync();
     if (!ok || P.bad) return false;
@@ -1473,7 +1598,7 @@ __device__ __forceinline__ bool ctl_pair_pass(const Ctx& c, Lds<H, I, W, V, CP>&
     wg_sync();  // paired attention: scores of the second row
     // S4 input: the attention output, written whole by the workgroups themselves
     sleep_units(c.dl[Ws::kHopS4]);
-    ok = poll_cells<mb(kQ), true, kLO>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
+    ok = poll_cells<mb(kQ), true, kLO>(c.region, c.slots, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
     if (lane == 0) S.flags[2] = !ok;
     wg_sync();
     if (!ok || P.bad) return false;
@@ -1483,7 +1608,7 @@ __device__ __forceinline__ bool ctl_pair_pass(const Ctx& c, Lds<H, I, W, V, CP>&
       load_pairs<kNP>(Ly.post_norm, w, lane);
       after_publish(S, (uint32_t)l * 4u + 2u, c.dl[Ws::kHopS5]);
       u32x4 q[kNP];
-      ok = poll_regs<kNP, kLO>(c.cells, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
+      ok = poll_regs<kNP, kLO>(c.region, c.slots, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
       cells_to_pairs<kNP>(q, v);
       ss = stage_rms<kNP>(v, w, S.hmid, S.xs[0], lane);
     }
@@ -1492,7 +1617,7 @@ __device__ __forceinline__ bool ctl_pair_pass(const Ctx& c, Lds<H, I, W, V, CP>&
     if (!ok || P.bad) return false;
     // S6 input: the SwiGLU activation
     after_publish(S, (uint32_t)l * 4u + 3u, c.dl[Ws::kHopS6]);
-    ok = poll_cells<mbh(I), true, kLO>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+    ok = poll_cells<mbh(I), true, kLO>(c.region, c.slots, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
     if (lane == 0) S.flags[4] = !ok;
     wg_sync();
     if (!ok || P.bad) return false;
@@ -1500,7 +1625,7 @@ __device__ __forceinline__ bool ctl_pair_pass(const Ctx& c, Lds<H, I, W, V, CP>&
   return true;
 }
 
-template <int H, int I, int W, int V, bool CP, bool SMP, bool F16 = false>
+template <int H, int I, int W, int V, bool CP, bool SMP, bool F16 = false, bool SG = false>
 __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
   // The RMSNorm inputs are polled into registers and staged from there (kNP element pairs per lane)
   constexpr int kNP = H / 128;
@@ -1554,7 +1679,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
           wg_sync();
           after_publish(S, (uint32_t)(fq * c.L) * 4u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopS1]);
           u32x4 q[kNP];
-          ok = poll_regs<kNP, kLO>(c.cells, proj_cells(H, I), c.tick(f, 0, 6), q, c.ws, lane, c, 10u, f, l);
+          ok = poll_regs<kNP, kLO, SG>(c.region, c.slots, LY.pj, c.tick(f, 0, 6), q, c.ws, lane, c, 10u, f, l);
           cells_to_pairs<kNP>(q, v);
         } else if (l == 0) {
           if (CP && f == 0) {
@@ -1606,7 +1731,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         } else {
           after_publish(S, (uint32_t)(fq * c.L + l) * 4u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopS1]);  // own part of the previous layer's down output
           u32x4 q[kNP];
-          ok = poll_regs<kNP, kLO>(c.cells, LY.e6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
+          ok = poll_regs<kNP, kLO, SG>(c.region, c.slots, LY.e6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
           cells_to_pairs<kNP>(q, v);
         }
         ss = stage_rms<kNP>(v, w, S.hin, S.xs[0], lane);
@@ -1616,7 +1741,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if (!ok) return;
       // S2 input: this head's q/k/v
       after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 1u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopS2]);
-      ok = poll_cells<mb(512), false, kLO>(c.cells, LY.e1 + c.x * 512, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
+      ok = poll_cells<mb(512), false, kLO>(c.region, c.slots, LY.e1, 512, c.tick(f, l, 0), S.qkv, c.ws, lane, c, 12u, f, l);
       if (lane == 0) { S.flags[1] = !ok; c.tr(0, f, l, 2); }
       wg_sync();
       if (!ok) return;
@@ -1632,13 +1757,14 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
           // its o slice straight into registers (both halves read the same (m, l)), so the merge needs no LDS
           static_assert(kChunks == 32, "merge lane mapping");
           const int ch = lane & 31, hh = lane >> 5;
-          const uint32_t pb = LY.e2 + (c.x * kChunks + ch) * kPartN;
-          const uint32_t po = pb + 4 + mh * SK_HD + md0 + 4 * hh;
+          const uint32_t om = own_off(c.slots, LY.e2m + 4 * ch + 2 * mh);
+          const uint32_t oo = own_off(c.slots, LY.e2o + 2 * SK_HD * ch + mh * SK_HD + md0 + 4 * hh);
+          const __amdgpu_buffer_rsrc_t rc = make_rsrc(c.region);
           u32x4 ml, oa, ob;
           for (uint32_t spin = 0;; spin++) {
-            ml = get2(c.cells, pb + 2 * mh);
-            oa = get2(c.cells, po);
-            ob = get2(c.cells, po + 2);
+            ml = __builtin_amdgcn_raw_buffer_load_b128(rc, om, 0, kPolDev);
+            oa = __builtin_amdgcn_raw_buffer_load_b128(rc, oo, 0, kPolDev);
+            ob = __builtin_amdgcn_raw_buffer_load_b128(rc, oo + 16u, 0, kPolDev);
             if (__all(ml.y == e && ml.w == e && oa.y == e && oa.w == e && ob.y == e && ob.w == e)) break;
             if ((spin & 63) == 63) {
               if (ld_u32_dev(c.ws, Ws::kErr) != 0) { ok = false; break; }
@@ -1662,11 +1788,11 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
               v[d] = row16_sum(v[d]);
               v[d] += dpp<0x142, 0xA>(v[d]);  // row_bcast:15 into rows 1 and 3
             }
-            if (ch == 16) {
+            if (ch == 16) {  // lanes 16 and 48: the sums of their half, stored into every copy
               const float Lw = v[0];
               const uint32_t o0 = LY.e3 + (2 * c.x + mh) * SK_HD + md0 + 4 * hh, e3 = c.tick(f, l, 2);
-              put2(c.cells, o0, Lw > 0.f ? v[1] / Lw : 0.f, Lw > 0.f ? v[2] / Lw : 0.f, e3);
-              put2(c.cells, o0 + 2, Lw > 0.f ? v[3] / Lw : 0.f, Lw > 0.f ? v[4] / Lw : 0.f, e3);
+              put2_all<SG>(c.region, o0, Lw > 0.f ? v[1] / Lw : 0.f, Lw > 0.f ? v[2] / Lw : 0.f, e3);
+              put2_all<SG>(c.region, o0 + 2, Lw > 0.f ? v[3] / Lw : 0.f, Lw > 0.f ? v[4] / Lw : 0.f, e3);
             }
           }
         }
@@ -1674,7 +1800,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         if (lane == 0) c.tr(0, f, l, 4);
       }
       // S4 input: the whole attention output
-      ok = ok && poll_cells<mb(kQ), true, kLO>(c.cells, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
+      ok = ok && poll_cells<mb(kQ), true, kLO, SG>(c.region, c.slots, LY.e3, kQ, c.tick(f, l, 2), S.xs[1], c.ws, lane, c, 14u, f, l);
       if (lane == 0) { S.flags[2] = !ok; c.tr(0, f, l, 5); }
       wg_sync();
       if (!ok) return;
@@ -1684,7 +1810,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         load_pairs<kNP>(Ly.post_norm, w, lane);
         after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 2u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopS5]);
         u32x4 q[kNP];
-        ok = poll_regs<kNP, kLO>(c.cells, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
+        ok = poll_regs<kNP, kLO, SG>(c.region, c.slots, LY.e4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
         cells_to_pairs<kNP>(q, v);
         ss = stage_rms<kNP>(v, w, S.hmid, S.xs[0], lane);
       }
@@ -1693,7 +1819,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       if (!ok) return;
       // S6 input: the whole SwiGLU activation
       after_publish(S, (uint32_t)(fq * c.L + l) * 4u + 3u + kP0 * (uint32_t)(fq + 1), c.dl[Ws::kHopS6]);
-      ok = poll_cells<mbh(I), true, kLO>(c.cells, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
+      ok = poll_cells<mbh(I), true, kLO, SG>(c.region, c.slots, LY.e5, I, c.tick(f, l, 4), S.xs[1], c.ws, lane, c, 16u, f, l);
       if (lane == 0) { S.flags[4] = !ok; c.tr(0, f, l, 7); }
       wg_sync();
       if (!ok) return;
@@ -1709,7 +1835,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       u32x4 q[kNP];
       // the head of frame 1 after a paired pass reads the pass's second row
       const bool hb = pr && f == 1;
-      ok = poll_regs<kNP, kLO>(c.cells, hb ? PairLayout(H, I).b6 : LY.e6, c.tick(hb ? 0 : f, c.L - 1, 5), q, c.ws, lane, c,
+      ok = poll_regs<kNP, kLO, SG>(c.region, c.slots, hb ? LY.b6 : LY.e6, c.tick(hb ? 0 : f, c.L - 1, 5), q, c.ws, lane, c,
                                17u, f, c.L);
       cells_to_pairs<kNP>(q, v);
       ss = stage_rms<kNP>(v, w, S.hin, S.xs[0], lane);
@@ -1734,7 +1860,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       // S.xs[0] and S.xs[1] are free here (the head dot has consumed its input and the next frame's inputs
       // are staged after the pick): candidate indices and keys
       static_assert(V <= Lds<H, I, W, V, CP>::XS, "candidate keys fit a staging buffer");
-      const int64_t t = sampled_pick<V, V / kWG>(c.cells, LY.e8, LY.e7, c.g, c.tick(f, c.L, 1), lds_addr(S.hv),
+      const int64_t t = sampled_pick<V, V / kWG, SG>(c.region, c.slots, LY.e8, LY.e7, c.g, c.tick(f, c.L, 1), lds_addr(S.hv),
                                                  lds_addr((char*)&S + kPickCopy<H, I, W, V, CP>), lds_addr(S.xs[0]),
                                                  lds_addr(S.xs[1]), lds_addr((char*)&S + kPickShared<H, I, W, V, CP>),
                                                  c.d.top_k, c.cnt0 + (uint64_t)(CP ? f - 1 : f),
@@ -1744,11 +1870,12 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
       else if (t == -2 && lane == 0) fail(c, 19u, f, c.L);
       if (lane == 0) { S.tok = tok; S.flags[6] = !ok; }
     } else {
-    if (lane == 0) {
+    {
       uint64_t best = 0;
       for (int i = 0; i < W; i++) best = S.cand[i] > best ? S.cand[i] : best;
       const uint32_t e = c.tick(f, c.L, 0);
-      put2(c.cells, LY.e7 + 2 * c.g, __uint_as_float((uint32_t)(best >> 32)), __uint_as_float((uint32_t)best), e);
+      put2_lanes<SG>(c.region, LY.e7 + 2 * c.g, __uint_as_float((uint32_t)(best >> 32)), __uint_as_float((uint32_t)best),
+                 e, lane);
     }
     // pick: reduce the 256 candidates
     {
@@ -1760,7 +1887,7 @@ __device__ void run_control(const Ctx& c, Lds<H, I, W, V, CP>& S, int lane) {
         best = 0;
         u32x4 q[kWG / 64];
 #pragma unroll
-        for (int j = 0; j < kWG / 64; j++) q[j] = get2(c.cells, LY.e7 + 2 * (lane + 64 * j));
+        for (int j = 0; j < kWG / 64; j++) q[j] = get2<SG>(c.region, c.slots, LY.e7 + 2 * (lane + 64 * j));
 #pragma unroll
         for (int j = 0; j < kWG / 64; j++) {
           good &= q[j].y == e && q[j].w == e;
@@ -1830,7 +1957,6 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
   static_assert(kQ % 1024 == 0 && I % 1024 == 0 && kQ / 1024 <= W && I / 1024 <= W && W == 4,
                 "the second row's polls: 1024-cell blocks, one per compute wave");
   const Layout LY(H, I);
-  const PairLayout PL(H, I);
   LdsPair<H, I>& P = *(LdsPair<H, I>*)((char*)&S + sizeof(Lds<H, I, W, V, CP>));
   const float eps = c.d.eps;
   const int x = (int)c.x, r = c.r, g = c.g;
@@ -1890,7 +2016,7 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
       } else {
         sleep_units(c.dl[Ws::kHopS1]);
         u32x4 q[kNP];
-        const bool ok = poll_regs<kNP, kLO>(c.cells, PL.b6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
+        const bool ok = poll_regs<kNP, kLO>(c.region, c.slots, LY.b6, c.tick(f, l - 1, 5), q, c.ws, lane, c, 11u, f, l);
         if (!ok && lane == 0) P.bad = 1;
         cells_to_pairs<kNP>(q, v);
       }
@@ -1910,11 +2036,10 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
           S.pub[16 + C::RW_QKV * cw + i] = yb[i] * row_scale_of<WD>(sq[i]) * ib;
         }
       }
-      publish_pair<W>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, PL.b1 + (uint32_t)x * 512 + 16 * r, 16,
-                      c.tick(f, l, 0), lane);
+      publish_pair<W, false>(S, c.region, c.slots, LY.e1 + 16 * r, LY.b1 + 16 * r, 16, c.tick(f, l, 0), lane);
       if (cw == 2) {  // the second row's S2 input
         sleep_units(c.dl[Ws::kHopS2]);
-        const bool ok = poll_cells<mb(512), false, kLO>(c.cells, PL.b1 + (uint32_t)x * 512, 512, c.tick(f, l, 0), P.qkv,
+        const bool ok = poll_cells<mb(512), false, kLO>(c.region, c.slots, LY.b1, 512, c.tick(f, l, 0), P.qkv,
                                                         c.ws, lane, c, 12u, f, l);
         if (!ok && lane == 0) P.bad = 1;
       }
@@ -1970,13 +2095,13 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
         // this workgroup's slice of the S4 inputs (q head 2x + r/16, dims 8 (r % 16) .. + 8), as the whole-cache
         // attention writes it
         if (p == (r >> 4) && (dd >> 3) == (r & 15)) {
-          put(c.cells, LY.e3 + (2 * x + p) * SK_HD + dd, oa, c.tick(f, l, 2));
-          put(c.cells, PL.b3 + (2 * x + p) * SK_HD + dd, ob, c.tick(f, l, 2));
+          put_all(c.region, LY.e3 + (2 * x + p) * SK_HD + dd, oa, c.tick(f, l, 2));
+          put_all(c.region, LY.b3 + (2 * x + p) * SK_HD + dd, ob, c.tick(f, l, 2));
         }
       }
       if (cw < kQ / 1024) {  // the second row's S4 input, 1024 cells per wave (staged from element 1024 cw)
         sleep_units(c.dl[Ws::kHopS4]);
-        const bool ok = poll_cells<mb(1024), true, kLO>(c.cells, PL.b3 + 1024u * cw, 1024, c.tick(f, l, 2),
+        const bool ok = poll_cells<mb(1024), true, kLO>(c.region, c.slots, LY.b3 + 1024u * cw, 1024, c.tick(f, l, 2),
                                                         P.xs[1] + xsw(1024 * cw), c.ws, lane, c, 14u, f, l);
         if (!ok && lane == 0) P.bad = 1;
       }
@@ -1996,12 +2121,12 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
             S.pub[C::R_O + C::RW_O * cw + i] = P.hin[o_w0 + i] + yb[i] * row_scale_of<WD>(so[i]);
           }
       }
-      publish_pair<W>(S, c.cells, LY.e4 + C::R_O * g, PL.b4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
+      publish_pair<W, true>(S, c.region, c.slots, LY.e4 + C::R_O * g, LY.b4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
       if (cw == 3) {  // the second row's S5 input: its residual after o, times the post-attention norm
         sleep_units(c.dl[Ws::kHopS5]);
         u32x4 q[kNP];
         float2 v[kNP];
-        const bool ok = poll_regs<kNP, kLO>(c.cells, PL.b4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
+        const bool ok = poll_regs<kNP, kLO>(c.region, c.slots, LY.b4, c.tick(f, l, 3), q, c.ws, lane, c, 15u, f, l);
         if (!ok && lane == 0) P.bad = 1;
         cells_to_pairs<kNP>(q, v);
         stage_b(v, Ly.post_norm, P.hmid);
@@ -2023,10 +2148,11 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
               silu_mul(yb[i] * row_scale_of<WD>(sg[i]) * ib, yb[i + 1] * row_scale_of<WD>(sg[i + 1]) * ib);
         }
       }
-      publish_pair<W>(S, c.cells, LY.e5 + C::R_GU / 2 * g, PL.b5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
+      publish_pair<W, true>(S, c.region, c.slots, LY.e5 + C::R_GU / 2 * g, LY.b5 + C::R_GU / 2 * g, C::R_GU / 2,
+                            c.tick(f, l, 4), lane);
       if (cw < I / 1024) {  // the second row's S6 input, 1024 cells per wave
         sleep_units(c.dl[Ws::kHopS6]);
-        const bool ok = poll_cells<mb(1024), true, kLO>(c.cells, PL.b5 + 1024u * cw, 1024, c.tick(f, l, 4),
+        const bool ok = poll_cells<mb(1024), true, kLO>(c.region, c.slots, LY.b5 + 1024u * cw, 1024, c.tick(f, l, 4),
                                                         P.xs[1] + xsw(1024 * cw), c.ws, lane, c, 16u, f, l);
         if (!ok && lane == 0) P.bad = 1;
       }
@@ -2049,7 +2175,7 @@ __device__ __forceinline__ bool compute_pair(const Ctx& c, Lds<H, I, W, V, CP>& 
           }
         }
       }
-      publish_pair<W>(S, c.cells, LY.e6 + C::R_D * g, PL.b6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
+      publish_pair<W, true>(S, c.region, c.slots, LY.e6 + C::R_D * g, LY.b6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
       load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
     }
   }
@@ -2157,7 +2283,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
       float y[1];
       dot_w<WD, 1, CPJ>(wpj, gpj, S.xs[0], lane, y);
       if (lane == 0) S.pub[cw] = y[0] * row_scale_of<WD>(spj[0]) + pbias;
-      publish<W, kLO>(S, c.cells, proj_cells(H, I) + (uint32_t)(H / kWG) * g, H / kWG, c.tick(f, 0, 6), lane);
+      publish<W, true, C::kSingle>(S, c.region, c.slots, LY.pj + (uint32_t)(H / kWG) * g, H / kWG, c.tick(f, 0, 6), lane);
     }
     for (int l = 0; l < (pr && f == 1 ? 0 : c.L); l++) {
       const sk_layer_desc& Ly = S.desc[l];
@@ -2180,7 +2306,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
 #pragma unroll
           for (int i = 0; i < C::RW_QKV; i++) S.pub[C::RW_QKV * cw + i] = y[i] * row_scale_of<WD>(sq[i]) * inv;
         }
-        publish<W, kLO>(S, c.cells, LY.e1 + (uint32_t)x * 512 + 16 * r, 16, c.tick(f, l, 0), lane);
+        publish<W, false>(S, c.region, c.slots, LY.e1 + 16 * r, 16, c.tick(f, l, 0), lane);
         if (tid == 0) c.tr(1, f, l, 1);
         if constexpr (!C::kLate) load_w<WD, C::RW_QKV, C::CH, kLO, KEEP>(wq, sq, gq, (const int8_t*)Ln.qkv_w, Ln.qkv_s, q_w0, C::RW_QKV, H, lane);
         // With gate/up split over two exchanges (SplitGateUp) the o rows go out here, before the attention, rather
@@ -2253,9 +2379,15 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
             const float v0 = j == pos ? S.vn[sl_d0 + 2 * qq] : bf2f(vf & 0xffffu);
             const float v1 = j == pos ? S.vn[sl_d0 + 2 * qq + 1] : bf2f(vf >> 16);
             const float o0 = row16_sum(ew * v0), o1 = row16_sum(ew * v1);
-            if (j == 0)
-              put2(c.cells, LY.e3 + (2 * x + sl_p) * SK_HD + sl_d0 + 2 * qq, lw > 0.f ? o0 / lw : 0.f,
-                   lw > 0.f ? o1 / lw : 0.f, c.tick(f, l, 2));
+            // every lane of a row holds the row's sums: lane j < 8 stores copy j
+            if (j < kXcd) {
+              const uint32_t e = c.tick(f, l, 2);
+              const u32x4 y = {__float_as_uint(lw > 0.f ? o0 / lw : 0.f), e, __float_as_uint(lw > 0.f ? o1 / lw : 0.f), e};
+              __builtin_amdgcn_raw_buffer_store_b128(y, make_rsrc(c.region),
+                                                     ((uint32_t)j << 12) +
+                                                         cell_off(LY.e3 + (2 * x + sl_p) * SK_HD + sl_d0 + 2 * qq),
+                                                     0, kPolDev);
+            }
           }
         } else {
         // P V by dimension slice (load_kv's V layout), published straight from the registers (no third barrier); ov
@@ -2327,18 +2459,18 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
             // + 8), normalised, as the merge would write it
             const float lw = ph ? l1v : l0v;
             if (ph == (r >> 4) && (dsl >> 3) == (r & 15))
-              put(c.cells, LY.e3 + (2 * x + ph) * SK_HD + dsl, lw > 0.f ? ov / lw : 0.f, c.tick(f, l, 2));
+              put_all<C::kSingle>(c.region, LY.e3 + (2 * x + ph) * SK_HD + dsl, lw > 0.f ? ov / lw : 0.f, c.tick(f, l, 2));
           } else {
-            // publish the partial: [m0 l0 m1 l1 | o0[128] | o1[128]]
-            const uint32_t pb = LY.e2 + ((uint32_t)x * kChunks + r) * kPartN;
+            // publish the partial (this XCD's copy): m0 l0 m1 l1 at e2m + 4 r, o0[128] o1[128] at e2o + 256 r
+            const uint32_t pm = LY.e2m + 4u * (uint32_t)r, po = LY.e2o + 2u * SK_HD * (uint32_t)r;
             const uint32_t e = c.tick(f, l, 1);
             if constexpr (kLO) {
               if (cw == 0 && lane < 4)
-                putl(c.cells, pb, (uint32_t)lane * 8u, lane == 0 ? m0v : lane == 1 ? l0v : lane == 2 ? m1v : l1v, e);
-              putl(c.cells, pb + 4, (uint32_t)(ph * SK_HD + dsl) * 8u, ov, e);
+                putl(c.region, c.slots, pm, (uint32_t)lane * 8u, lane == 0 ? m0v : lane == 1 ? l0v : lane == 2 ? m1v : l1v, e);
+              putl(c.region, c.slots, po, (uint32_t)(ph * SK_HD + dsl) * 8u, ov, e);
             } else {
-              if (cw == 0 && lane < 4) put(c.cells, pb + lane, lane == 0 ? m0v : lane == 1 ? l0v : lane == 2 ? m1v : l1v, e);
-              put(c.cells, pb + 4 + ph * SK_HD + dsl, ov, e);
+              if (cw == 0 && lane < 4) put(c.region, c.slots, pm + lane, lane == 0 ? m0v : lane == 1 ? l0v : lane == 2 ? m1v : l1v, e);
+              put(c.region, c.slots, po + ph * SK_HD + dsl, ov, e);
             }
           }
         }
@@ -2375,7 +2507,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           for (int i = 0; i < C::RW_O; i++)
             if (i < o_wn) S.pub[C::RW_O * cw + i] = S.hin[o_w0 + i] + y[i] * row_scale_of<WD>(so[i]);
         }
-        publish<W, kLO>(S, c.cells, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
+        publish<W, true, C::kSingle>(S, c.region, c.slots, LY.e4 + C::R_O * g, C::R_O, c.tick(f, l, 3), lane);
         if (tid == 0) c.tr(1, f, l, 5);
         if constexpr (!C::kLate) load_w<WD, C::RW_O, C::CQ, kLO, KEEP>(wo, so, go, (const int8_t*)Ln.o_w, Ln.o_s, o_w0, o_wn, kQ, lane);
         if constexpr (C::kSpread && kSplitGu) {  // the second half of the gate/up rows
@@ -2400,7 +2532,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
           for (int i = 0; i < C::RW_GU; i += 2)
             S.pub[(C::RW_GU * cw + i) / 2] = silu_mul(y[i] * row_scale_of<WD>(sg[i]) * inv, y[i + 1] * row_scale_of<WD>(sg[i + 1]) * inv);
         }
-        publish<W, kLO>(S, c.cells, LY.e5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
+        publish<W, true, C::kSingle>(S, c.region, c.slots, LY.e5 + C::R_GU / 2 * g, C::R_GU / 2, c.tick(f, l, 4), lane);
         if (tid == 0) c.tr(1, f, l, 6);
         if constexpr (C::kLate) {
           load_w<WD, C::RW_D, C::CI, kLO, KEEP>(wd, sd, gd, (const int8_t*)Ly.down_w, Ly.down_s, d_w0, d_wn, I, lane);
@@ -2428,7 +2560,7 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
             }
           }
         }
-        publish<W, kLO>(S, c.cells, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
+        publish<W, true, C::kSingle>(S, c.region, c.slots, LY.e6 + C::R_D * g, C::R_D, c.tick(f, l, 5), lane);
         if (tid == 0) c.tr(1, f, l, 7);
         if constexpr (!C::kLate) load_w<WD, C::RW_D, C::CI, kLO, KEEP>(wd, sd, gd, (const int8_t*)Ln.down_w, Ln.down_s, d_w0, d_wn, I, lane);
         if constexpr (C::kSpread) {
@@ -2486,8 +2618,8 @@ __device__ void run_compute(const Ctx& c, Lds<H, I, W, V, CP>& S, int cw, int ti
     load_proj();  // the next position's projection row, in flight during the pick (the head's registers are free)
     wg_sync();  // candidates ready for the control wave
     if constexpr (SMP)
-      pick_compute<V, W>(lds_addr((char*)&S + kPickCopy<H, I, W, V, CP>), lds_addr(S.xs[0]), lds_addr(S.xs[1]),
-                         lds_addr((char*)&S + kPickShared<H, I, W, V, CP>), c.cells, c.ws, LY.e8, c.tick(f, c.L, 1),
+      pick_compute<V, W, C::kSingle>(lds_addr((char*)&S + kPickCopy<H, I, W, V, CP>), lds_addr(S.xs[0]), lds_addr(S.xs[1]),
+                         lds_addr((char*)&S + kPickShared<H, I, W, V, CP>), c.region, c.slots, c.ws, LY.e8, c.tick(f, c.L, 1),
                          c.cnt0 + (uint64_t)(CP ? f - 1 : f), c.seed, c.d.top_k, c.dl[Ws::kHopPick], f, c.L, c.g,
                          cw, lane, cw == 0 ? c.tslot(1, f, c.L, 0) : nullptr);
     wg_sync();  // pick done
@@ -2511,7 +2643,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   void* ws = d.workspace;
   // ---- placement: XCD from hardware, dense rank from an arrival counter ------------------------------------
   __shared__ int s_rank;
-  __shared__ uint32_t s_base, s_dl[2], s_trace;
+  __shared__ uint32_t s_base, s_dl[2], s_trace, s_place[kQuarters];
   __shared__ int64_t s_pos0;
   const uint32_t x = xcc_id();
   // Every load of the prologue goes out before the first barrier, so the launch pays one memory round trip for
@@ -2548,6 +2680,7 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     s_dl[0] = ld_u32_dev(ws, Ws::kPollDelay);
     s_dl[1] = ld_u32_dev(ws, Ws::kPollDelay + 4);
     s_trace = ld_u32_dev(ws, Ws::kTraceOn);
+    for (int q = 0; q < kQuarters; q++) s_place[q] = ld_u32_dev(ws, Ws::kPlace + 4 * q);
     s_pos0 = pos0;
     for (int i = 0; i < 8; i++) S.flags[i] = 0;
     S.pubcnt = 0;
@@ -2562,7 +2695,22 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   c.d = d;
   c.cp = cp;
   c.ws = ws;
-  c.cells = (char*)ws + Ws::kCells;
+  {
+    // this XCD's page slot in each quarter of the region: the placement sk_frames_place measured where a quarter's
+    // word carries one (bit 31) whose eight slots are distinct, else page x
+    uint32_t slots = 0;
+#pragma unroll
+    for (int q = 0; q < kQuarters; q++) {
+      const uint32_t w = __builtin_amdgcn_readfirstlane(s_place[q]);  // uniform: page offsets in scalar registers
+      uint32_t used = 0;
+#pragma unroll
+      for (uint32_t i = 0; i < kXcd; i++) used |= 1u << ((w >> (3u * i)) & 7u);
+      const uint32_t sl = ((w >> 31) && used == 0xffu) ? (w >> (3u * x)) & 7u : x;
+      slots |= sl << (3 * q);
+    }
+    c.slots = slots;
+    c.region = cell_region(ws);
+  }
   c.x = x;
   c.r = r;
   c.g = (int)x * kPerXcd + r;
@@ -2576,25 +2724,24 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
   c.n_frames = n_frames;
   c.L = d.n_layers;
   {
-    // default start delays per exchange, overridable through the workspace: tuned by coordinate descent on the
-    // 0.6B talker, on the 1.7B talker for the spread prefetch (longer exchanges), on the bf16 0.6B talker (spread
-    // prefetch at hidden 1024) and on the code predictor (no merge; the single-wave attention of F16 with the
-    // paired pass: 1008 -> 945 us per frame), with a set of its own for bf16 weights. The i8g32 kernels keep the
-    // i8row sets (their own descent gained under 1%). The merge poll (hop 2) starts after the second attention barrier,
-    // before the compute waves' P V; a poll that starts before the partials are there costs a whole extra round
-    // trip (0.6B: 410-430 against 374-383 us per frame at 30-36 against 40-44 units), so hop 2 keeps a margin
-    // of 4-8 units over the measured edge.
-    constexpr uint8_t kDefault[Ws::kHops] = {21, 23, 44, 25, 17, 34, 30, 28};
-    constexpr uint8_t kDefaultSpread[Ws::kHops] = {49, 19, 56, 35, 39, 56, 4, 34};
-    constexpr uint8_t kDefaultSpread06[Ws::kHops] = {49, 15, 60, 31, 59, 52, 4, 46};
-    constexpr uint8_t kDefaultCp[Ws::kHops] = {18, 14, 43, 25, 19, 30, 17, 25};
-    constexpr uint8_t kDefaultCpBf16[Ws::kHops] = {30, 10, 43, 21, 31, 30, 5, 29};  // 1105 -> 1071 us per frame
-    // the 1.7B talker with bf16 weights: 1010 -> 945 us per frame (the merge poll needs 70 units or more here)
-    constexpr uint8_t kDefaultSpread17Bf16[Ws::kHops] = {66, 44, 128, 56, 8, 0, 18, 64};
-    // the projected (1.7B) code predictor, unpaired: 991 -> 956 us per frame (i8g32 964 on the same set), and with
-    // bf16 weights 1137 -> 1091 on a set of its own
-    constexpr uint8_t kDefaultCpProj[Ws::kHops] = {14, 10, 22, 56, 20, 26, 20, 20};
-    constexpr uint8_t kDefaultCpProjBf16[Ws::kHops] = {14, 14, 22, 58, 28, 30, 16, 28};
+    // default start delays per exchange, overridable through the workspace: tuned by coordinate descent (a sweep of
+    // 0-100 units per hop, then steps of 4 and 8) with the cells placed by sk_frames_place, on the 0.6B talker
+    // (i8row; i8g32 keeps its set), on the 1.7B talker for the spread prefetch (i8row, and sets of its own for the
+    // single-copy i8g32 and bf16 kernels), on the bf16 0.6B talker (spread prefetch at hidden 1024) and on the code
+    // predictor (paired, and projected; sets of their own for bf16 weights). The merge poll (hop 2) starts after the
+    // second attention barrier, before the compute waves' P V; a poll that starts before the partials are there
+    // costs a whole extra round trip, so hop 2 keeps a margin over the measured edge. Per frame after tuning: 0.6B
+    // 354 us, 1.7B 635 / 675 / 967 (i8row / i8g32 / bf16), bf16 0.6B 469, code predictor 852 (paired) and 915
+    // (projected), bf16 961 and 1061.
+    constexpr uint8_t kDefault[Ws::kHops] = {16, 24, 50, 20, 14, 26, 28, 14};
+    constexpr uint8_t kDefaultSpread[Ws::kHops] = {36, 20, 70, 26, 54, 60, 46, 12};
+    constexpr uint8_t kDefaultSpread17G32[Ws::kHops] = {57, 19, 64, 39, 35, 64, 12, 42};
+    constexpr uint8_t kDefaultSpread06[Ws::kHops] = {36, 10, 56, 26, 46, 46, 12, 42};
+    constexpr uint8_t kDefaultCp[Ws::kHops] = {14, 14, 80, 56, 10, 20, 13, 17};
+    constexpr uint8_t kDefaultCpBf16[Ws::kHops] = {16, 10, 40, 58, 24, 22, 9, 21};
+    constexpr uint8_t kDefaultSpread17Bf16[Ws::kHops] = {74, 40, 136, 64, 8, 0, 26, 68};
+    constexpr uint8_t kDefaultCpProj[Ws::kHops] = {14, 16, 22, 56, 10, 20, 20, 12};
+    constexpr uint8_t kDefaultCpProjBf16[Ws::kHops] = {10, 14, 18, 60, 24, 26, 24, 20};
     constexpr bool kProj = CP && CpProjIn<H, I>::value > 0;
     const uint32_t w0 = s_dl[0], w1 = s_dl[1];
 #pragma unroll
@@ -2605,16 +2752,18 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
                                 : (WD == SK_WD_BF16 ? kDefaultCpBf16[h] : kDefaultCp[h]))
                        : (CfgW<H, I, W, V, CP, WD>::kSpread
                               ? (H == 1024 ? kDefaultSpread06[h]
-                                           : (WD == SK_WD_BF16 ? kDefaultSpread17Bf16[h] : kDefaultSpread[h]))
+                                           : (WD == SK_WD_BF16    ? kDefaultSpread17Bf16[h]
+                                              : WD == SK_WD_I8G32 ? kDefaultSpread17G32[h]
+                                                                  : kDefaultSpread[h]))
                               : kDefault[h]);
     }
   }
-  c.trace = s_trace ? (uint64_t*)((char*)ws + Ws::kCells + (size_t)Layout(H, I).total * 8) : nullptr;
+  c.trace = s_trace ? (uint64_t*)((char*)ws + Ws::kTrace) : nullptr;
   if constexpr (PAIRK) {
     if (wave == W) ctl_pair_pass<H, I, W, V, CP>(c, S, lane);
     else compute_pair<H, I, W, V, CP, WD, KEEP>(c, S, wave, tid, lane);
   } else {
-    if (wave == W) run_control<H, I, W, V, CP, SMP, F16>(c, S, lane);
+    if (wave == W) run_control<H, I, W, V, CP, SMP, F16, CfgW<H, I, W, V, CP, WD>::kSingle>(c, S, lane);
     else run_compute<H, I, W, V, CP, SMP, WD, KEEP, F16>(c, S, wave, tid, lane);
   }
   // ---- end of launch: epoch base and launch count (workgroup 0; every workgroup finished its census) --------

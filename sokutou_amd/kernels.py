@@ -190,6 +190,13 @@ def _sptr(lin: "_Lin") -> int:
     return 0 if lin.s is None else lin.s.data_ptr()
 
 
+def place_cells(ws: torch.Tensor) -> None:
+    """Measures where a zeroed frame-kernel workspace's exchange cells go (``sk_frames_place``: each XCD's copy on
+    the page nearest it), stream-ordered on the current stream. Called after every zeroing of the workspace; the
+    launches read the result from the workspace."""
+    _lib.check(_lib.load().sk_frames_place(ws.data_ptr(), ws.numel(), _lib.stream()), "sk_frames_place")
+
+
 def _layer_descs(P: _Stack, kc: list, vc: list, device) -> torch.Tensor:
     """Device array of ``sk_layer_desc`` for the layers of ``P`` with caches ``kc[i]`` / ``vc[i]``."""
     arr = (_lib.SkLayerDesc * len(P.layers))()
@@ -274,6 +281,7 @@ class CodePredictor:
         self._ptrs = torch.tensor([tabs, hw, hs], dtype=torch.int64, device=dev)
         self._layer_desc = _layer_descs(P, list(self.kc.unbind(0)), list(self.vc.unbind(0)), dev)
         self.ws = torch.zeros(int(L.sk_cp_workspace_size(P.H, P.I, int(bool(pair)))), dtype=torch.uint8, device=dev)
+        place_cells(self.ws)
         self._desc = _lib.SkCpDesc(
             n_layers=len(P.layers), hidden=P.H, inter=P.I, nq=P.nq, nkv=P.nkv, vocab=self.V, n_positions=self.n,
             wd=_lib.WD[wd], ct=_lib.CT["bf16"], eps=P.eps, layers=self._layer_desc.data_ptr(), norm=P.norm.data_ptr(),
@@ -344,6 +352,7 @@ class CodePredictor:
         next launch starts clean after a failed one. Stream-ordered on the current stream; not to be called while a
         launch of this code predictor may be in flight on another stream."""
         self.ws.zero_()
+        place_cells(self.ws)
 
     def weight_bytes(self) -> int:
         return self.C.bytes() + sum(h.bytes() for h in self.heads) + (self.proj[0].bytes() if self.proj else 0)
@@ -540,6 +549,7 @@ class Qwen3Kernels(Qwen3Fast):
         L = _lib.load()
         self._layer_desc = _layer_descs(P, self.tk, self.tv, self.device)
         self.frame_ws = torch.zeros(int(L.sk_talker_workspace_size(P.H, P.I)), dtype=torch.uint8, device=self.device)
+        place_cells(self.frame_ws)
         self.frame_ids = torch.zeros(4096, dtype=torch.int64, device=self.device)
         self.layer_out: torch.Tensor | None = None
         s = self.s
@@ -597,6 +607,7 @@ class Qwen3Kernels(Qwen3Fast):
         Stream-ordered on the current stream."""
         if self.frame_kernel:
             self.frame_ws.zero_()
+            place_cells(self.frame_ws)
         if self.cp is not None and self.cpk is not None:
             self.cpk.clear_error()
         self.attn_ws[:4].zero_()

@@ -25,11 +25,11 @@ import sys
 import numpy as np
 import torch
 
-from . import _lib
 from . import synthetic as syn
 
-# trace layout: [workgroup 256][role 2: control, compute][layer 32][event 16] of int64 stamps
-_TRACE_LAYERS, _TRACE_EVENTS, _WG = 32, 16, 256
+# trace layout: [workgroup 256][role 2: control, compute][layer 32][event 16] of int64 stamps, from byte 256 of the
+# workspace (after its control words)
+_TRACE_LAYERS, _TRACE_EVENTS, _WG, _TRACE_AT = 32, 16, 256, 256
 # compute-wave events
 C_S1, C_S1DOT, C_S1PUB, C_S2, C_S2END, C_S4, C_S4DOT, C_S4PUB = 0, 8, 1, 2, 3, 4, 9, 5
 C_S5, C_S5DOT, C_S5PUB, C_S6, C_S6DOT, C_S6PUB = 12, 10, 6, 13, 11, 7
@@ -43,8 +43,6 @@ def traced_launch(name: str, frames: int = 2):
     of the launch)."""
     dev = torch.device("cuda:0")
     s = syn.workload_shape(name)
-    L = _lib.load()
-    total = int(L.sk_talker_workspace_size(s.hidden, s.inter))
     nbytes = _WG * 2 * _TRACE_LAYERS * _TRACE_EVENTS * 8
     if name == "cp06b":
         eng = syn.make_cp_engine(name, 0, dev, keep_layers=True, pair=False)
@@ -70,7 +68,7 @@ def traced_launch(name: str, frames: int = 2):
     torch.cuda.synchronize()
     if err():
         raise RuntimeError(f"frame kernel error {err()}")
-    raw = ws[total - nbytes:total].view(torch.int64).view(_WG, 2, _TRACE_LAYERS, _TRACE_EVENTS)
+    raw = ws[_TRACE_AT:_TRACE_AT + nbytes].view(torch.int64).view(_WG, 2, _TRACE_LAYERS, _TRACE_EVENTS)
     ws[32:36].zero_()
     return raw.cpu().numpy().astype(np.float64) * 0.01, s, e0.elapsed_time(e1) * 1e3
 

@@ -26,15 +26,12 @@ def _engine(name, seed, gpu):
     return eng, tok
 
 
-@pytest.mark.parametrize("name,poll", [("small06b", None), ("small17b", None), ("small17b", "regs")])
-def test_small_model_against_oracle(gpu, name, poll, monkeypatch):
-    """Two 0.6B- or 1.7B-shaped layers: 8 frames in one launch against the oracle, then per-layer residuals. The
-    1.7B shape runs its default kernel (4 compute waves), and with SOKUTOU_TALKER_POLL=regs the 8-wave kernel."""
+@pytest.mark.parametrize("name", ["small06b", "small17b"])
+def test_small_model_against_oracle(gpu, name):
+    """Two 0.6B- or 1.7B-shaped layers: 8 frames in one launch against the oracle, then per-layer residuals."""
     from oracle.workload import talker_oracle
 
-    if poll:
-        monkeypatch.setenv("SOKUTOU_TALKER_POLL", poll)
-    print(f"{name}: persistent kernel ({poll or 'default'} kernel), 8 frames in one launch", flush=True)
+    print(f"{name}: persistent kernel, 8 frames in one launch", flush=True)
     spec = syn.WORKLOADS[name]
     eng, tok = _engine(name, 2, gpu)
     orc, otok, s = talker_oracle(name, 2, "i8row")
@@ -393,3 +390,31 @@ def test_talker_in_group_counts_off_the_gather_batch(gpu, groups):
     lg = orc.logits(orc.forward(x, syn.WORKLOADS[name]["kv"]))
     assert rel_err(eng.logit_t.view(-1), lg) < TOL
     assert int(eng.frame_ids[0].item()) == argmax_first(lg)
+
+
+def test_cell_placement_is_measured_and_changes_no_result(gpu):
+    """sk_frames_place (run by the engine on its zeroed workspace) finds, for each 512 KB quarter of the cell region,
+    a distinct nearest page for every XCD; 64 frames then give the fixture's codes with the measured placement,
+    with the fixed one (placement words zeroed) and with a word whose slots repeat (the kernel refuses it and uses
+    the fixed placement for that quarter): placement moves only where the cells live."""
+    meta = json.loads((GOLD / "talker06b_seed0.json").read_text())
+    eng, tok = _engine("talker06b", 0, gpu)
+    words = [int(v) & 0xffffffff for v in eng.frame_ws[48:64].view(torch.int32).tolist()]
+    print("placement words", [f"{w:08x}" for w in words], flush=True)
+    for w in words:
+        assert w >> 31 == 1, words
+        assert sorted((w >> (3 * x)) & 7 for x in range(8)) == list(range(8)), words
+    runs = {}
+    for mode in ("measured", "fixed", "repeated"):
+        if mode == "fixed":
+            eng.frame_ws[48:64].zero_()
+        elif mode == "repeated":  # quarter 1: every XCD in page 0 (refused), the others measured
+            eng.frame_ws[48:64].view(torch.int32).copy_(torch.tensor(words, dtype=torch.int64).to(torch.int32))
+            eng.frame_ws[52:56].view(torch.int32).fill_(-2147483648)
+        eng.reset(syn.WORKLOADS["talker06b"]["kv"], tok)
+        eng.run_frames(64)
+        torch.cuda.synchronize()
+        assert eng.frame_error() == 0, (mode, eng.frame_diag())
+        runs[mode] = eng.frame_ids[:64].cpu().tolist()
+        print(mode, "codes equal the fixture:", runs[mode] == meta["codes"], flush=True)
+    assert runs["measured"] == runs["fixed"] == runs["repeated"] == meta["codes"]

@@ -99,16 +99,28 @@ def test_cp_frame_checks_the_projection_without_launching():
     assert b"unpaired" in L.sk_last_error()
 
 
-def test_cp_workspace_size_covers_the_paired_rows_and_the_projection():
-    """The talker's workspace, then the paired pass's second row (q|k|v of 8 heads, attention output, h after o,
-    activation, h after down: 4096 + 2048 + 1024 + 3072 + 1024 cells of 8 bytes), then a projected input's
-    1024 cells; one size serves paired, serial and projected code predictors."""
+def test_frame_workspace_holds_trace_and_placed_cell_region():
+    """Control words (256 bytes), the trace stamps (256 workgroups x 2 roles x 32 layers x 16 events x 8 bytes),
+    then a 2 MB cell region at the first 2 MB boundary after them (2 MB of slack): one size for the talker at both
+    shapes and every code predictor (paired or projected), whose cells all fit the region's 64 x 512 cells; a shape
+    whose cells would not fit gets 0."""
     L = _lib.load()
-    base = L.sk_talker_workspace_size(1024, 3072)
-    want = base + 8 * (8 * 512 + 2048 + 1024 + 3072 + 1024) + 8 * 1024
+    want = 256 + 256 * 2 * 32 * 16 * 8 + 2 * (2 << 20)
+    assert L.sk_talker_workspace_size(1024, 3072) == want
+    assert L.sk_talker_workspace_size(2048, 6144) == want
     assert L.sk_cp_workspace_size(1024, 3072, 0) == want
     assert L.sk_cp_workspace_size(1024, 3072, 1) == want
     assert L.sk_cp_workspace_size(0, 3072, 1) == 0
+    assert L.sk_talker_workspace_size(4096, 12288) == 0  # 35840 cells > 32768
+
+
+def test_frames_place_checks_arguments_before_the_device():
+    """sk_frames_place refuses a null or short workspace before it queries the device."""
+    L = _lib.load()
+    assert L.sk_frames_place(None, 1 << 30, None) == _lib.SK_EINVAL
+    assert L.sk_frames_place(ctypes.c_void_p(256), int(L.sk_talker_workspace_size(1024, 3072)) - 1,
+                             None) == _lib.SK_EWORKSPACE
+    assert b"too small" in L.sk_last_error()
 
 
 def test_batched_entry_points_reject_bad_shapes_without_launching():
