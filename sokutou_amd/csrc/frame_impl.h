@@ -2730,17 +2730,17 @@ __global__ __launch_bounds__((W + 1) * 64) void k_frames(sk_talker_desc d, CpArg
     // single-copy i8g32 and bf16 kernels), on the bf16 0.6B talker (spread prefetch at hidden 1024) and on the code
     // predictor (paired, and projected; sets of their own for bf16 weights). The merge poll (hop 2) starts after the
     // second attention barrier, before the compute waves' P V; a poll that starts before the partials are there
-    // costs a whole extra round trip, so hop 2 keeps a margin over the measured edge. Per frame after tuning: 0.6B
-    // 354 us, 1.7B 635 / 675 / 967 (i8row / i8g32 / bf16), bf16 0.6B 469, code predictor 852 (paired) and 915
-    // (projected), bf16 961 and 1061.
-    constexpr uint8_t kDefault[Ws::kHops] = {16, 24, 50, 20, 14, 26, 28, 14};
-    constexpr uint8_t kDefaultSpread[Ws::kHops] = {36, 20, 70, 26, 54, 60, 46, 12};
+    // costs a whole extra round trip, so hop 2 keeps a margin over the measured edge. A second descent in steps of
+    // 1-4 units followed. Per frame after tuning: 0.6B 354 us, 1.7B 633 / 675 / 967 (i8row / i8g32 / bf16), bf16
+    // 0.6B 470, code predictor 846 (paired) and 911 (projected), bf16 957 and 1061.
+    constexpr uint8_t kDefault[Ws::kHops] = {19, 20, 50, 20, 16, 31, 28, 13};
+    constexpr uint8_t kDefaultSpread[Ws::kHops] = {38, 18, 74, 22, 50, 56, 46, 16};
     constexpr uint8_t kDefaultSpread17G32[Ws::kHops] = {57, 19, 64, 39, 35, 64, 12, 42};
-    constexpr uint8_t kDefaultSpread06[Ws::kHops] = {36, 10, 56, 26, 46, 46, 12, 42};
-    constexpr uint8_t kDefaultCp[Ws::kHops] = {14, 14, 80, 56, 10, 20, 13, 17};
-    constexpr uint8_t kDefaultCpBf16[Ws::kHops] = {16, 10, 40, 58, 24, 22, 9, 21};
+    constexpr uint8_t kDefaultSpread06[Ws::kHops] = {34, 6, 60, 26, 50, 50, 12, 46};
+    constexpr uint8_t kDefaultCp[Ws::kHops] = {14, 16, 84, 56, 10, 24, 15, 19};
+    constexpr uint8_t kDefaultCpBf16[Ws::kHops] = {16, 10, 38, 56, 24, 26, 13, 23};
     constexpr uint8_t kDefaultSpread17Bf16[Ws::kHops] = {74, 40, 136, 64, 8, 0, 26, 68};
-    constexpr uint8_t kDefaultCpProj[Ws::kHops] = {14, 16, 22, 56, 10, 20, 20, 12};
+    constexpr uint8_t kDefaultCpProj[Ws::kHops] = {14, 16, 20, 58, 12, 24, 24, 16};
     constexpr uint8_t kDefaultCpProjBf16[Ws::kHops] = {10, 14, 18, 60, 24, 26, 24, 20};
     constexpr bool kProj = CP && CpProjIn<H, I>::value > 0;
     const uint32_t w0 = s_dl[0], w1 = s_dl[1];
