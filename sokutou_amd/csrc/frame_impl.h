@@ -81,8 +81,6 @@ __host__ __device__ constexpr uint32_t own_off(uint32_t slots, uint32_t i) {
 __host__ __device__ constexpr uint32_t single_off(uint32_t i) { return cell_off(i) | (((i >> 9) & 7u) << 12); }
 template <bool SINGLE>
 __host__ __device__ constexpr uint32_t read_off(uint32_t slots, uint32_t i) { return SINGLE ? single_off(i) : own_off(slots, i); }
-// the placement of a workspace no sk_frames_place call has measured: XCD x's copy in page x of every period
-__host__ __device__ constexpr uint32_t slots_identity(uint32_t x) { return x | x << 3 | x << 6 | x << 9; }
 
 // Accesses of this XCD's copy (`region` the cell region, `slots` this XCD's page slots).
 __device__ __forceinline__ void put(void* region, uint32_t slots, uint32_t idx, float v, uint32_t e) {
@@ -258,7 +256,7 @@ struct SpreadLate {
 };
 // Global addressing of a shape's kernel: true = the lane part of every cell, weight-row and cache address in one
 // shared vector offset (lane bytes) and the wave-uniform part in the scalar offset of buffer instructions
-// (get2l, put2l, putl, weight rows by row start); false = a vector address per load or store. The hidden-2048
+// (get2l, putl, weight rows by row start); false = a vector address per load or store. The hidden-2048
 // kernel (frame17.hip) takes the shared offsets: with a vector address per load its waves spilled the addresses
 // (per-row weight pointers, poll and publish offsets) and reloaded them from scratch on every exchange. The
 // hidden-1024 kernels keep per-load addresses, the code they were tuned with (measured 4% slower with get2l polls).
