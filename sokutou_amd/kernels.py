@@ -190,11 +190,21 @@ def _sptr(lin: "_Lin") -> int:
     return 0 if lin.s is None else lin.s.data_ptr()
 
 
-def place_cells(ws: torch.Tensor) -> None:
+def place_cells(ws: torch.Tensor, attempts: int = 3) -> int:
     """Measures where a zeroed frame-kernel workspace's exchange cells go (``sk_frames_place``: each XCD's copy on
-    the page nearest it), stream-ordered on the current stream. Called after every zeroing of the workspace; the
-    launches read the result from the workspace."""
-    _lib.check(_lib.load().sk_frames_place(ws.data_ptr(), ws.numel(), _lib.stream()), "sk_frames_place")
+    the page nearest it) on the current stream, and returns how many of the cell region's four quarters got a
+    measured placement. A quarter whose measurement was not consistent keeps the fixed placement (same results,
+    slower exchanges); the measurement is repeated for it up to ``attempts`` times in all (each waits for the
+    stream). Called after every zeroing of the workspace; the launches read the result from the workspace."""
+    L = _lib.load()
+    placed = 0
+    for _ in range(max(1, attempts)):
+        _lib.check(L.sk_frames_place(ws.data_ptr(), ws.numel(), _lib.stream()), "sk_frames_place")
+        words = ws[48:64].view(torch.int32).tolist()
+        placed = sum(1 for w in words if w < 0)  # bit 31: a measured quarter
+        if placed == len(words):
+            break
+    return placed
 
 
 def _layer_descs(P: _Stack, kc: list, vc: list, device) -> torch.Tensor:
@@ -349,8 +359,9 @@ class CodePredictor:
 
     def clear_error(self) -> None:
         """Zeroes the kernel's whole workspace (error word, launch census, epoch base and exchange cells), so the
-        next launch starts clean after a failed one. Stream-ordered on the current stream; not to be called while a
-        launch of this code predictor may be in flight on another stream."""
+        next launch starts clean after a failed one, and places its cells again (``place_cells``, which waits for
+        the current stream); not to be called while a launch of this code predictor may be in flight on another
+        stream."""
         self.ws.zero_()
         place_cells(self.ws)
 
@@ -603,8 +614,8 @@ class Qwen3Kernels(Qwen3Fast):
     def clear_frame_error(self) -> None:
         """Clears every device error word of the engine so frames can run again after a failure: the frame kernel's
         and the one-launch code predictor's whole workspaces (error word, launch census, epoch base and exchange cells
-        all restart from zero, so no stale cell can match a new epoch) and the attention workspace's error word.
-        Stream-ordered on the current stream."""
+        all restart from zero, so no stale cell can match a new epoch, and the cells are placed again, which waits for
+        the current stream) and the attention workspace's error word."""
         if self.frame_kernel:
             self.frame_ws.zero_()
             place_cells(self.frame_ws)
