@@ -361,9 +361,10 @@ int64_t sk_batch_workspace_size(int hidden, int inter, int nq, int nkv, int voca
 /* Loads each stream's input for the next step: h = emb[ids[b]] and its normalised planes. */
 int sk_batch_embed(const sk_batch_desc* desc, void* stream);
 
-/* One decode step for every stream: n_layers x (qkv GEMM, ragged split-K attention with KV append at pos[b],
- * o GEMM, gate/up GEMM, down GEMM), final RMSNorm + head GEMM, greedy pick per stream (lowest index on ties), then
- * codes / ids / nstep / pos advance and the picked rows are embedded for the next step. 5 n_layers + 2 launches. */
+/* One decode step for every stream: n_layers x (qkv GEMM, ragged split-K attention with KV append at pos[b] and
+ * its merge, o GEMM, gate/up GEMM, down GEMM), final RMSNorm + head GEMM, greedy pick per stream (lowest index on
+ * ties), then codes / ids / nstep / pos advance and the picked rows are embedded for the next step.
+ * 6 n_layers + 2 launches. */
 int sk_batch_frame(const sk_batch_desc* desc, void* stream);
 
 #ifdef __cplusplus

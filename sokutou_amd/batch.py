@@ -117,7 +117,8 @@ class BatchedTalker:
 
     # --- steps -----------------------------------------------------------------------------------------------
     def step(self) -> None:
-        """One decode step of every stream on the current stream (5 launches per layer + 2)."""
+        """One decode step of every stream on the current stream (6 launches per layer: qkv, attention, its merge,
+        o, gate/up, down; then the head and the pick)."""
         self._desc.logits = None if self.logits is None else self.logits.data_ptr()
         self._desc.layer_out = None if self.layer_out is None else self.layer_out.data_ptr()
         _lib.check(_lib.load().sk_batch_frame(ctypes.byref(self._desc), _lib.stream()), "sk_batch_frame")
