@@ -95,7 +95,8 @@ def _attn_case(gpu, seed, nkv, max_len, pos, ct):
 @pytest.mark.parametrize("ct", ["bf16", "f32"])
 @pytest.mark.parametrize("nkv,max_len,pos", [(8, 1024, 0), (8, 1024, 1), (8, 1024, 16), (8, 1024, 256), (8, 1024, 512),
                                              (8, 1024, 575), (8, 1024, 1023), (8, 576, 575), (8, 16, 15), (8, 16, 3),
-                                             (2, 64, 40), (8, 2048, 2047)])
+                                             (2, 64, 40), (8, 2048, 2047), (8, 1024, 63), (8, 1024, 64), (8, 129, 128),
+                                             (8, 4096, 1000), (8, 4096, 4095)])
 def test_attention(gpu, ct, nkv, max_len, pos):
     print(f"attn ct={ct} nkv={nkv} max_len={max_len} pos={pos}", flush=True)
     out, ref, Kg, Vg, Ko, Vo, ws = _attn_case(gpu, pos + 31 * nkv, nkv, max_len, pos, ct)
