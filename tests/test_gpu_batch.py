@@ -45,6 +45,54 @@ def test_tile_layout(gpu):
     assert torch.equal(out.cpu(), ref)
 
 
+def test_batch_attention_at_block_boundaries(gpu):
+    """sk_batch_attn alone: eight streams at positions on either side of the 128-position blocks (one block, a
+    block plus one position, several blocks with a one-position tail) and the cache's last row, each against the fp32
+    oracle's attention over that stream's own cache; the appended K/V rows and nothing else of the caches change."""
+    nkv, nq, max_len = 8, 16, 1024
+    pos = [0, 63, 127, 128, 129, 255, 700, max_len - 1]
+    B = len(pos)
+    print(f"sk_batch_attn: {B} streams at positions {pos}", flush=True)
+    rng = np.random.default_rng(11)
+    width = (nq + 2 * nkv) * 128
+    qkv = np.zeros((16, width), np.float32)
+    qkv[:B] = rng.standard_normal((B, width)).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    Kc = O.bf16_round(rng.standard_normal((B, nkv, max_len, 128)).astype(np.float32))
+    Vc = O.bf16_round(rng.standard_normal((B, nkv, max_len, 128)).astype(np.float32))
+    rope = O.rope_table(syn.inv_freq(syn.shape("1.7b")), max_len)
+    L = _lib.load()
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    Kg, Vg = dev(Kc).to(torch.bfloat16), dev(Vc).to(torch.bfloat16)
+    nt = int(L.sk_batch_terms())
+    att = torch.zeros((nt, 16, nq * 128), dtype=torch.bfloat16, device=gpu)
+    ws = torch.zeros(int(L.sk_batch_attn_workspace_size(nkv)), dtype=torch.uint8, device=gpu)
+    posg = torch.tensor(pos, dtype=torch.int64, device=gpu)
+    p = _lib.ptr
+    qkvg, qng, kng, ropeg = dev(qkv), dev(qn), dev(kn), dev(rope)
+    _lib.call("sk_batch_attn", p(qkvg), p(qng), p(kng), 1e-6, p(ropeg), p(Kg), p(Vg), p(posg), B, max_len, nq, nkv,
+              p(att), p(ws), ws.numel(), _lib.stream())
+    torch.cuda.synchronize()
+    assert int(ws[:4].view(torch.int32).item()) == 0
+    got = att.float().sum(0).cpu().numpy()
+    Kn, Vn = Kg.float().cpu().numpy(), Vg.float().cpu().numpy()
+    for b in range(B):
+        Ko, Vo = Kc[b].copy(), Vc[b].copy()
+        ref = O.attention(qkv[b], qn, kn, 1e-6, rope, Ko, Vo, pos[b], nq, nkv, cache_bf16=True)
+        e = rel_err(got[b], ref)
+        assert e < 2e-5, (b, pos[b], e)
+        # the appended rows: V as given (bf16), K the same bf16 or one step away where fp32 rounding straddles a tie
+        np.testing.assert_array_equal(Vn[b][:, pos[b]], Vo[:, pos[b]])
+        dk = np.abs(Kn[b][:, pos[b]] - Ko[:, pos[b]])
+        assert np.all(dk <= np.abs(Ko[:, pos[b]]) * 2.0 ** -7 + 1e-30)
+        mask = np.ones(max_len, bool)
+        mask[pos[b]] = False
+        np.testing.assert_array_equal(Kn[b][:, mask], Kc[b][:, mask])
+        np.testing.assert_array_equal(Vn[b][:, mask], Vc[b][:, mask])
+    assert float(att[:, B:].float().abs().max()) == 0.0
+
+
 @pytest.mark.parametrize("N,K", [(4096, 2048), (2048, 6144), (12288, 2048), (96, 512), (3072, 1024)])
 def test_bgemm_modes_against_fp32(gpu, N, K):
     from sokutou_amd.batch import tile
