@@ -93,7 +93,8 @@ def test_batch_attention_at_block_boundaries(gpu):
     assert float(att[:, B:].float().abs().max()) == 0.0
 
 
-@pytest.mark.parametrize("N,K", [(4096, 2048), (2048, 6144), (12288, 2048), (96, 512), (3072, 1024)])
+@pytest.mark.parametrize("N,K", [(4096, 2048), (2048, 6144), (12288, 2048), (96, 512), (3072, 1024), (1024, 2048),
+                                 (1024, 3072), (6144, 1024)])
 def test_bgemm_modes_against_fp32(gpu, N, K):
     from sokutou_amd.batch import tile
     from sokutou_amd.kernels import _Lin
